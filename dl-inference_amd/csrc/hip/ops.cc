@@ -1,0 +1,332 @@
+// Kernel entry points of libdli_hip.so (declared in include/dli_hip.h): argument checks,
+// launch geometry, and the launch of the matching embedded gfx950 kernel.
+#include <cmath>
+#include <string>
+
+#include "runtime.h"
+
+namespace dli::hip {
+namespace {
+
+// The three float variants of one kernel in one code object.
+struct FloatKernels {
+  DeviceKernel f32, bf16, f16;
+  FloatKernels(const char* module, const char* base)
+      : f32(module, intern(base, "_f32")), bf16(module, intern(base, "_bf16")),
+        f16(module, intern(base, "_f16")) {}
+
+  DeviceKernel* pick(int dtype) {
+    switch (dtype) {
+      case DLI_F32: return &f32;
+      case DLI_BF16: return &bf16;
+      case DLI_F16: return &f16;
+      default: return nullptr;
+    }
+  }
+
+ private:
+  static const char* intern(const char* base, const char* suffix) {
+    return (new std::string(std::string(base) + suffix))->c_str();  // lives for the process
+  }
+};
+
+int badDtype(const char* op, int dtype) {
+  return fail(DLI_HIP_EINVAL, std::string(op) + ": unsupported dtype code " + std::to_string(dtype));
+}
+
+int badArg(const char* op, const char* what) {
+  return fail(DLI_HIP_EINVAL, std::string(op) + ": " + what);
+}
+
+bool validIndexDtype(int dtype) { return dtype == DLI_I64 || dtype == DLI_I32; }
+
+// Grid-stride launches: enough blocks to fill 256 CUs several times over, capped.
+unsigned strideBlocks(int64_t work) {
+  const int64_t blocks = (work + 255) / 256;
+  return static_cast<unsigned>(blocks < 4096 ? (blocks > 0 ? blocks : 1) : 4096);
+}
+
+FloatKernels k_add("elementwise", "add");
+FloatKernels k_mul("elementwise", "mul");
+FloatKernels k_silu("elementwise", "silu");
+FloatKernels k_relu("elementwise", "relu");
+FloatKernels k_bn("elementwise", "batch_norm2d");
+FloatKernels k_maxpool("elementwise", "max_pool2d");
+FloatKernels k_embedding("elementwise", "embedding");
+FloatKernels k_softmax("elementwise", "softmax");
+FloatKernels k_transpose("elementwise", "transpose2d");
+FloatKernels k_rotary("elementwise", "rotary");
+FloatKernels k_argmax("elementwise", "argmax");
+FloatKernels k_rms_norm("norm", "rms_norm");
+FloatKernels k_gemm("gemm", "gemm_tiled");
+DeviceKernel k_skinny1("gemm", "skinny_linear_m1");
+DeviceKernel k_skinny2("gemm", "skinny_linear_m2");
+DeviceKernel k_skinny4("gemm", "skinny_linear_m4");
+FloatKernels k_attention("attention", "attention");
+FloatKernels k_paged_attention("attention", "paged_attention");
+FloatKernels k_kv_append("attention", "kv_append");
+FloatKernels k_conv2d("conv", "conv2d");
+
+int binary(FloatKernels& kernels, const char* op, int dtype, const void* a, const void* b,
+           void* out, int64_t total, int64_t width, void* stream) {
+  DeviceKernel* k = kernels.pick(dtype);
+  if (k == nullptr) return badDtype(op, dtype);
+  if (total < 0 || width < 0) return badArg(op, "negative size");
+  if (total == 0) return 0;
+  if (width == 0) return badArg(op, "broadcast operand is empty");
+  if (a == nullptr || b == nullptr || out == nullptr) return badArg(op, "NULL pointer");
+  return launch(*k, {strideBlocks(total)}, {256}, 0, stream, a, b, out, total, width);
+}
+
+int unary(FloatKernels& kernels, const char* op, int dtype, const void* x, void* out,
+          int64_t total, void* stream) {
+  DeviceKernel* k = kernels.pick(dtype);
+  if (k == nullptr) return badDtype(op, dtype);
+  if (total < 0) return badArg(op, "negative size");
+  if (total == 0) return 0;
+  if (x == nullptr || out == nullptr) return badArg(op, "NULL pointer");
+  return launch(*k, {strideBlocks(total)}, {256}, 0, stream, x, out, total);
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace
+}  // namespace dli::hip
+
+using namespace dli::hip;
+
+extern "C" {
+
+int dli_hip_add(int dtype, const void* a, const void* b, void* out, int64_t total, int64_t width,
+                void* stream) {
+  return binary(k_add, "add", dtype, a, b, out, total, width, stream);
+}
+
+int dli_hip_mul(int dtype, const void* a, const void* b, void* out, int64_t total, int64_t width,
+                void* stream) {
+  return binary(k_mul, "mul", dtype, a, b, out, total, width, stream);
+}
+
+int dli_hip_silu(int dtype, const void* x, void* out, int64_t total, void* stream) {
+  return unary(k_silu, "silu", dtype, x, out, total, stream);
+}
+
+int dli_hip_relu(int dtype, const void* x, void* out, int64_t total, void* stream) {
+  return unary(k_relu, "relu", dtype, x, out, total, stream);
+}
+
+int dli_hip_rms_norm(int dtype, const void* x, const void* weight, void* out, int64_t rows,
+                     int64_t hidden, float eps, void* stream) {
+  DeviceKernel* k = k_rms_norm.pick(dtype);
+  if (k == nullptr) return badDtype("rms_norm", dtype);
+  if (rows < 0 || hidden <= 0) return badArg("rms_norm", "rows must be >= 0 and hidden > 0");
+  if (rows == 0) return 0;
+  const unsigned blocks = static_cast<unsigned>(rows < 65535 ? rows : 65535);
+  return launch(*k, {blocks}, {256}, 0, stream, x, weight, out, rows, hidden, eps);
+}
+
+int dli_hip_embedding(int dtype, int ids_dtype, const void* ids, const void* table, void* out,
+                      int64_t tokens, int64_t hidden, int64_t vocab, void* stream) {
+  DeviceKernel* k = k_embedding.pick(dtype);
+  if (k == nullptr) return badDtype("embedding", dtype);
+  if (!validIndexDtype(ids_dtype)) return badArg("embedding", "ids must be int64 or int32");
+  if (tokens < 0 || hidden < 0 || vocab < 0) return badArg("embedding", "negative size");
+  if (tokens == 0 || hidden == 0) return 0;
+  const int ids64 = ids_dtype == DLI_I64 ? 1 : 0;
+  const unsigned blocks = static_cast<unsigned>(tokens < 65535 ? tokens : 65535);
+  return launch(*k, {blocks}, {256}, 0, stream, ids, ids64, table, out, tokens, hidden, vocab);
+}
+
+int dli_hip_softmax(int dtype, const void* x, void* out, int64_t rows, int64_t width,
+                    void* stream) {
+  DeviceKernel* k = k_softmax.pick(dtype);
+  if (k == nullptr) return badDtype("softmax", dtype);
+  if (rows < 0 || width <= 0) return badArg("softmax", "rows must be >= 0 and width > 0");
+  if (rows == 0) return 0;
+  const unsigned blocks = static_cast<unsigned>(rows < 65535 ? rows : 65535);
+  return launch(*k, {blocks}, {256}, 0, stream, x, out, rows, width);
+}
+
+int dli_hip_transpose2d(int dtype, const void* x, void* out, int64_t rows, int64_t cols,
+                        void* stream) {
+  DeviceKernel* k = k_transpose.pick(dtype);
+  if (k == nullptr) return badDtype("transpose", dtype);
+  if (rows < 0 || cols < 0) return badArg("transpose", "negative size");
+  if (rows == 0 || cols == 0) return 0;
+  if ((rows + 31) / 32 > 65535) return badArg("transpose", "too many rows");
+  return launch(*k, {blocksFor(cols, 32), blocksFor(rows, 32)}, {256}, 0, stream, x, out, rows,
+                cols);
+}
+
+int dli_hip_batch_norm2d(int dtype, const void* x, const void* weight, const void* bias,
+                         const void* running_mean, const void* running_var, void* out,
+                         int64_t total, int64_t channels, int64_t spatial, float eps,
+                         void* stream) {
+  DeviceKernel* k = k_bn.pick(dtype);
+  if (k == nullptr) return badDtype("batch_norm2d", dtype);
+  if (total < 0 || channels <= 0 || spatial <= 0)
+    return badArg("batch_norm2d", "channels and spatial must be positive");
+  if (total == 0) return 0;
+  return launch(*k, {strideBlocks(total)}, {256}, 0, stream, x, weight, bias, running_mean,
+                running_var, out, total, channels, spatial, eps);
+}
+
+int dli_hip_max_pool2d(int dtype, const void* x, void* out, int64_t n, int64_t c, int64_t h,
+                       int64_t w, int64_t out_h, int64_t out_w, int64_t kernel_h,
+                       int64_t kernel_w, int64_t stride_h, int64_t stride_w, int64_t pad_h,
+                       int64_t pad_w, void* stream) {
+  DeviceKernel* k = k_maxpool.pick(dtype);
+  if (k == nullptr) return badDtype("max_pool2d", dtype);
+  if (kernel_h <= 0 || kernel_w <= 0 || stride_h <= 0 || stride_w <= 0 || pad_h < 0 || pad_w < 0)
+    return badArg("max_pool2d", "kernel and stride must be positive, padding non-negative");
+  const int64_t total = n * c * out_h * out_w;
+  if (n < 0 || c < 0 || out_h < 0 || out_w < 0) return badArg("max_pool2d", "negative size");
+  if (total == 0) return 0;
+  return launch(*k, {strideBlocks(total)}, {256}, 0, stream, x, out, n, c, h, w, out_h, out_w,
+                kernel_h, kernel_w, stride_h, stride_w, pad_h, pad_w);
+}
+
+int dli_hip_conv2d(int dtype, const void* x, const void* weight, const void* bias, void* out,
+                   int64_t n, int64_t in_c, int64_t h, int64_t w, int64_t out_c, int64_t kernel_h,
+                   int64_t kernel_w, int64_t out_h, int64_t out_w, int64_t stride_h,
+                   int64_t stride_w, int64_t pad_h, int64_t pad_w, void* stream) {
+  DeviceKernel* k = k_conv2d.pick(dtype);
+  if (k == nullptr) return badDtype("conv2d", dtype);
+  if (stride_h <= 0 || stride_w <= 0 || pad_h < 0 || pad_w < 0)
+    return badArg("conv2d", "stride must be positive, padding non-negative");
+  if (n < 0 || in_c < 0 || out_c < 0 || out_h < 0 || out_w < 0)
+    return badArg("conv2d", "negative size");
+  const int64_t total = n * out_c * out_h * out_w;
+  if (total == 0) return 0;
+  return launch(*k, {strideBlocks(total)}, {256}, 0, stream, x, weight, bias, out, n, in_c, h, w,
+                out_c, kernel_h, kernel_w, out_h, out_w, stride_h, stride_w, pad_h, pad_w);
+}
+
+int dli_hip_linear(int dtype, int out_dtype, const void* x, const void* w, const void* bias,
+                   void* out, int64_t m, int64_t n, int64_t k, void* stream) {
+  if (out_dtype != dtype && out_dtype != DLI_F32)
+    return badArg("linear", "out_dtype must equal dtype or be float32");
+  if (m < 0 || n < 0 || k < 0) return badArg("linear", "negative size");
+  if (m == 0 || n == 0) return 0;
+  if (x == nullptr || w == nullptr || out == nullptr) return badArg("linear", "NULL pointer");
+  const int out_f32 = out_dtype == DLI_F32 ? 1 : 0;
+  // bf16 weight streaming for decode-sized m: MFMA skinny kernel.
+  if (dtype == DLI_BF16 && m <= 64 && k % 64 == 0 && aligned16(x) && aligned16(w)) {
+    DeviceKernel* sk = m <= 16 ? &k_skinny1 : (m <= 32 ? &k_skinny2 : &k_skinny4);
+    return launch(*sk, {blocksFor(n, 32)}, {256}, 0, stream, x, w, bias, out, m, n, k, out_f32);
+  }
+  DeviceKernel* kt = k_gemm.pick(dtype);
+  if (kt == nullptr) return badDtype("linear", dtype);
+  if ((m + 63) / 64 > 65535) return badArg("linear", "m too large");
+  return launch(*kt, {blocksFor(n, 64), blocksFor(m, 64)}, {256}, 0, stream, x, w, bias, out, m,
+                n, k, 1, out_f32);
+}
+
+int dli_hip_matmul(int dtype, const void* a, const void* b, void* out, int64_t m, int64_t n,
+                   int64_t k, void* stream) {
+  DeviceKernel* kt = k_gemm.pick(dtype);
+  if (kt == nullptr) return badDtype("matmul", dtype);
+  if (m < 0 || n < 0 || k < 0) return badArg("matmul", "negative size");
+  if (m == 0 || n == 0) return 0;
+  if ((m + 63) / 64 > 65535) return badArg("matmul", "m too large");
+  const void* no_bias = nullptr;
+  return launch(*kt, {blocksFor(n, 64), blocksFor(m, 64)}, {256}, 0, stream, a, b, no_bias, out, m,
+                n, k, 0, 0);
+}
+
+int dli_hip_rotary(int dtype, const void* q, const void* k, const float* cos_table,
+                   const float* sin_table, void* out_q, void* out_k, int64_t batch,
+                   int64_t q_heads, int64_t k_heads, int64_t seq, int64_t head_dim, int64_t pairs,
+                   int64_t max_pos, int64_t start_pos, const void* positions,
+                   int positions_dtype, void* stream) {
+  DeviceKernel* kr = k_rotary.pick(dtype);
+  if (kr == nullptr) return badDtype("rotary_embedding", dtype);
+  if (head_dim <= 0 || head_dim % 2 != 0) return badArg("rotary_embedding", "head_dim must be even");
+  if (pairs < 0 || 2 * pairs > head_dim) return badArg("rotary_embedding", "pairs > head_dim / 2");
+  if (positions != nullptr && !validIndexDtype(positions_dtype))
+    return badArg("rotary_embedding", "positions must be int64 or int32");
+  if (batch < 0 || q_heads < 0 || k_heads < 0 || seq < 0) return badArg("rotary_embedding", "negative size");
+  const int64_t work = batch * (q_heads > k_heads ? q_heads : k_heads) * seq * (head_dim / 2);
+  if (work == 0) return 0;
+  const int pos64 = positions_dtype == DLI_I64 ? 1 : 0;
+  return launch(*kr, {strideBlocks(work)}, {256}, 0, stream, q, k, cos_table, sin_table, out_q,
+                out_k, batch, q_heads, k_heads, seq, head_dim, pairs, max_pos, start_pos, positions,
+                pos64);
+}
+
+int dli_hip_attention(int dtype, const void* q, const void* k, const void* v, void* out,
+                      int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t seq_q,
+                      int64_t seq_k, int64_t head_dim, int causal, float scale, void* stream) {
+  DeviceKernel* ka = k_attention.pick(dtype);
+  if (ka == nullptr) return badDtype("attention", dtype);
+  if (head_dim <= 0 || head_dim > 256) return badArg("attention", "head_dim must be in [1, 256]");
+  if (kv_heads <= 0 || q_heads % kv_heads != 0)
+    return badArg("attention", "q_heads must be a multiple of kv_heads");
+  if (batch < 0 || seq_q < 0 || seq_k < 0) return badArg("attention", "negative size");
+  const int64_t rows = batch * q_heads * seq_q;
+  if (rows == 0) return 0;
+  if (rows > 0x7fffffff) return badArg("attention", "too many query rows");
+  return launch(*ka, {static_cast<unsigned>(rows)}, {64}, 0, stream, q, k, v, out, batch, q_heads,
+                kv_heads, seq_q, seq_k, head_dim, causal, scale);
+}
+
+int dli_hip_kv_append(int dtype, const void* key, const void* value, void* key_pool,
+                      void* value_pool, const int32_t* block_table, int64_t batch, int64_t heads,
+                      int64_t seq, int64_t head_dim, int64_t block_size, int64_t max_blocks,
+                      int64_t start, const void* positions, int positions_dtype, void* stream) {
+  DeviceKernel* ka = k_kv_append.pick(dtype);
+  if (ka == nullptr) return badDtype("kv_append", dtype);
+  if (block_size <= 0 || max_blocks <= 0) return badArg("kv_append", "empty cache geometry");
+  if (positions != nullptr && !validIndexDtype(positions_dtype))
+    return badArg("kv_append", "positions must be int64 or int32");
+  if (batch < 0 || heads < 0 || seq < 0 || head_dim < 0) return badArg("kv_append", "negative size");
+  const int64_t total = batch * heads * seq * head_dim;
+  if (total == 0) return 0;
+  const int pos64 = positions_dtype == DLI_I64 ? 1 : 0;
+  return launch(*ka, {strideBlocks(total)}, {256}, 0, stream, key, value, key_pool, value_pool,
+                block_table, batch, heads, seq, head_dim, block_size, max_blocks, start, positions,
+                pos64);
+}
+
+size_t dli_hip_paged_attention_workspace(int64_t batch, int64_t q_heads, int64_t seq_q,
+                                         int64_t head_dim, int64_t max_tokens) {
+  (void)batch, (void)q_heads, (void)seq_q, (void)head_dim, (void)max_tokens;
+  return 0;
+}
+
+int dli_hip_paged_attention(int dtype, const void* q, const void* key_pool,
+                            const void* value_pool, const int32_t* block_table, void* out,
+                            int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t seq_q,
+                            int64_t head_dim, int64_t block_size, int64_t max_blocks, int64_t past,
+                            const void* positions, int positions_dtype, int causal, float scale,
+                            void* workspace, size_t workspace_bytes, void* stream) {
+  (void)workspace, (void)workspace_bytes;
+  DeviceKernel* ka = k_paged_attention.pick(dtype);
+  if (ka == nullptr) return badDtype("paged_attention", dtype);
+  if (head_dim <= 0 || head_dim > 256) return badArg("paged_attention", "head_dim must be in [1, 256]");
+  if (kv_heads <= 0 || q_heads % kv_heads != 0)
+    return badArg("paged_attention", "q_heads must be a multiple of kv_heads");
+  if (block_size <= 0 || max_blocks <= 0) return badArg("paged_attention", "empty cache geometry");
+  if (positions != nullptr && !validIndexDtype(positions_dtype))
+    return badArg("paged_attention", "positions must be int64 or int32");
+  if (batch < 0 || seq_q < 0) return badArg("paged_attention", "negative size");
+  const int64_t rows = batch * q_heads * seq_q;
+  if (rows == 0) return 0;
+  if (rows > 0x7fffffff) return badArg("paged_attention", "too many query rows");
+  const int pos64 = positions_dtype == DLI_I64 ? 1 : 0;
+  return launch(*ka, {static_cast<unsigned>(rows)}, {64}, 0, stream, q, key_pool, value_pool,
+                block_table, out, batch, q_heads, kv_heads, seq_q, head_dim, block_size, max_blocks,
+                past, positions, pos64, causal, scale);
+}
+
+int dli_hip_argmax(int dtype, const void* x, int64_t* ids, int64_t rows, int64_t width,
+                   void* stream) {
+  DeviceKernel* ka = k_argmax.pick(dtype);
+  if (ka == nullptr) return badDtype("argmax", dtype);
+  if (rows < 0 || width <= 0) return badArg("argmax", "rows must be >= 0 and width > 0");
+  if (rows == 0) return 0;
+  const unsigned blocks = static_cast<unsigned>(rows < 65535 ? rows : 65535);
+  return launch(*ka, {blocks}, {256}, 0, stream, x, ids, rows, width);
+}
+
+}  // extern "C"

@@ -1,0 +1,58 @@
+#pragma once
+
+// Internal C++ side of libdli_hip.so: the dlopen'd HIP runtime table, error reporting, and
+// lazily loaded per-device kernels from the embedded gfx950 code objects.
+
+#include <array>
+#include <atomic>
+#include <cstddef>
+#include <cstdint>
+#include <mutex>
+#include <string>
+
+#include "dli_hip.h"
+
+namespace dli::hip {
+
+struct Dim3 {
+  unsigned x = 1, y = 1, z = 1;
+};
+
+// Records `message` as this thread's last error and returns `code`.
+int fail(int code, const std::string& message);
+// Maps a hipError_t to 0 / a recorded error with context.
+int check(int hip_status, const char* what);
+int requireRuntime();
+
+// A kernel by name inside one embedded code object; resolved once per device.
+class DeviceKernel {
+ public:
+  DeviceKernel(const char* module, const char* name) : module_(module), name_(name) {}
+  // Returns 0 and the function handle for the current device, or an error code.
+  int resolve(void** function);
+  const char* name() const { return name_; }
+
+ private:
+  static constexpr int kMaxDevices = 64;
+  const char* module_;
+  const char* name_;
+  std::array<std::atomic<void*>, kMaxDevices> functions_{};
+  std::mutex mutex_;
+};
+
+int launchRaw(DeviceKernel& kernel, Dim3 grid, Dim3 block, unsigned lds_bytes, void* stream,
+              void** args);
+
+template <typename... Args>
+int launch(DeviceKernel& kernel, Dim3 grid, Dim3 block, unsigned lds_bytes, void* stream,
+           Args... args) {
+  if (grid.x == 0 || grid.y == 0 || grid.z == 0) return 0;
+  void* params[] = {static_cast<void*>(&args)..., nullptr};
+  return launchRaw(kernel, grid, block, lds_bytes, stream, params);
+}
+
+inline unsigned blocksFor(int64_t work, int64_t per_block) {
+  return static_cast<unsigned>((work + per_block - 1) / per_block);
+}
+
+}  // namespace dli::hip

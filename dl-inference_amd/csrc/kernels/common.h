@@ -1,0 +1,122 @@
+#pragma once
+
+// Shared device helpers for the gfx950 kernels of libdli_hip.so.
+// Storage types: float, bf16 (raw 16-bit, converted with round-to-nearest-even, NaN kept
+// quiet) and _Float16. All arithmetic is fp32.
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace dk {
+
+constexpr int kWave = 64;
+
+struct bf16 {
+  uint16_t bits;
+};
+using f16 = _Float16;
+
+__device__ __forceinline__ float bf16ToFloat(uint16_t bits) {
+  return __uint_as_float(static_cast<uint32_t>(bits) << 16);
+}
+
+// Round-to-nearest-even, the rule torch uses for float -> bfloat16.
+__device__ __forceinline__ uint16_t floatToBf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+template <typename T>
+struct Num;
+
+template <>
+struct Num<float> {
+  static __device__ __forceinline__ float load(const float* p) { return *p; }
+  static __device__ __forceinline__ void store(float* p, float v) { *p = v; }
+  static __device__ __forceinline__ float round(float v) { return v; }
+};
+
+template <>
+struct Num<bf16> {
+  static __device__ __forceinline__ float load(const bf16* p) { return bf16ToFloat(p->bits); }
+  static __device__ __forceinline__ void store(bf16* p, float v) { p->bits = floatToBf16(v); }
+  static __device__ __forceinline__ float round(float v) { return bf16ToFloat(floatToBf16(v)); }
+};
+
+template <>
+struct Num<f16> {
+  static __device__ __forceinline__ float load(const f16* p) { return static_cast<float>(*p); }
+  static __device__ __forceinline__ void store(f16* p, float v) { *p = static_cast<f16>(v); }
+  static __device__ __forceinline__ float round(float v) {
+    return static_cast<float>(static_cast<f16>(v));
+  }
+};
+
+template <typename T>
+__device__ __forceinline__ float ld(const T* p) {
+  return Num<T>::load(p);
+}
+template <typename T>
+__device__ __forceinline__ void st(T* p, float v) {
+  Num<T>::store(p, v);
+}
+
+__device__ __forceinline__ float waveSum(float v) {
+#pragma unroll
+  for (int offset = kWave / 2; offset > 0; offset >>= 1) v += __shfl_xor(v, offset, kWave);
+  return v;
+}
+
+__device__ __forceinline__ float waveMax(float v) {
+#pragma unroll
+  for (int offset = kWave / 2; offset > 0; offset >>= 1) v = fmaxf(v, __shfl_xor(v, offset, kWave));
+  return v;
+}
+
+// Sum over the whole block; `scratch` holds one float per wave. Every thread gets the result.
+__device__ __forceinline__ float blockSum(float v, float* scratch) {
+  const int lane = threadIdx.x % kWave;
+  const int wave = threadIdx.x / kWave;
+  const int waves = (blockDim.x + kWave - 1) / kWave;
+  v = waveSum(v);
+  __syncthreads();
+  if (lane == 0) scratch[wave] = v;
+  __syncthreads();
+  float total = 0.f;
+  for (int w = 0; w < waves; ++w) total += scratch[w];
+  return total;
+}
+
+__device__ __forceinline__ float blockMax(float v, float* scratch) {
+  const int lane = threadIdx.x % kWave;
+  const int wave = threadIdx.x / kWave;
+  const int waves = (blockDim.x + kWave - 1) / kWave;
+  v = waveMax(v);
+  __syncthreads();
+  if (lane == 0) scratch[wave] = v;
+  __syncthreads();
+  float m = -INFINITY;
+  for (int w = 0; w < waves; ++w) m = fmaxf(m, scratch[w]);
+  return m;
+}
+
+__device__ __forceinline__ int64_t loadIndex(const void* p, int is64, int64_t i) {
+  return is64 ? static_cast<const int64_t*>(p)[i] : static_cast<int64_t>(static_cast<const int32_t*>(p)[i]);
+}
+
+}  // namespace dk
+
+// Instantiates `extern "C"` kernels named <base>_f32 / _bf16 / _f16 from a template kernel body
+// `base##_impl<T>`; ARGS/CALL are the parameter list and the forwarding argument list.
+#define DK_FLOAT_KERNELS(base, bounds, ARGS, CALL)                                        \
+  extern "C" __global__ void __launch_bounds__(bounds) base##_f32 ARGS {                  \
+    base##_impl<float> CALL;                                                              \
+  }                                                                                       \
+  extern "C" __global__ void __launch_bounds__(bounds) base##_bf16 ARGS {                 \
+    base##_impl<dk::bf16> CALL;                                                           \
+  }                                                                                       \
+  extern "C" __global__ void __launch_bounds__(bounds) base##_f16 ARGS {                  \
+    base##_impl<dk::f16> CALL;                                                            \
+  }

@@ -1,0 +1,150 @@
+#pragma once
+
+// Weight-streaming MFMA core for skinny GEMMs on gfx950: out[m, n] = sum_k x[m, k] * w[n, k]
+// with few rows m (decode batch, M <= 16 * MB) and a large bf16 weight w [N, K] read once.
+//
+// Work split
+//   - A workgroup owns an N-tile of 16 * NF weight rows and a slice of K (grid.y splits K).
+//   - Its kWaves waves split that slice further, each walking 64-column steps: per step a lane
+//     loads two 16-byte runs of one weight row, so every wave-wide load pair covers 16 rows x
+//     128 contiguous bytes (whole cache lines, each byte fetched once).
+//   - x fragments are read straight from global memory (x is small and stays in L2).
+//   - MFMA v_mfma_f32_16x16x32_bf16: A = 16 weight rows x 32 k, B = 32 k x 16 batch rows.
+//     Lane l holds A[l % 16][(l / 16) * 8 + j] and B[(l / 16) * 8 + j][l % 16], j < 8, and
+//     receives D[(l / 16) * 4 + i][l % 16], i < 4. A and B use the same k order, so the
+//     assignment of k to lanes only has to agree between the two operands.
+//   - Partial tiles of the waves are summed in LDS in a fixed order, so results do not depend
+//     on timing. The reduced fp32 tile [16 * NF][16 * MB] is left in LDS for an epilogue.
+
+#include "common.h"
+
+namespace dk {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+struct alignas(16) U128 {
+  uint32_t w[4];
+};
+
+__device__ __forceinline__ bf16x8 asBf16x8(const U128& v) { return __builtin_bit_cast(bf16x8, v); }
+
+__device__ __forceinline__ U128 load16(const void* p) {
+  return *reinterpret_cast<const U128*>(p);
+}
+
+__device__ __forceinline__ U128 zero16() {
+  U128 z;
+  z.w[0] = z.w[1] = z.w[2] = z.w[3] = 0;
+  return z;
+}
+
+template <int NF, int MB, int kWaves>
+struct SkinnyCore {
+  static constexpr int kTileN = 16 * NF;
+  static constexpr int kTileM = 16 * MB;
+  // LDS floats needed by run(): one partial tile per wave.
+  static constexpr int kLdsFloats = kWaves * kTileN * kTileM;
+
+  // Accumulates this block's share of the tile and leaves the reduced tile in lds[0 .. tile).
+  //   w: [N, K] bf16 row-major, x: [M, K] bf16 row-major (rows >= M read as zero)
+  //   n0: first weight row of the tile; rows >= N contribute zero.
+  //   step_begin/step_end: range of 64-column steps owned by this block.
+  __device__ static void run(const uint16_t* __restrict__ w, const uint16_t* __restrict__ x,
+                             int64_t N, int64_t K, int M, int64_t n0, int step_begin, int step_end,
+                             float* lds) {
+    const int lane = threadIdx.x % kWave;
+    const int wave = threadIdx.x / kWave;
+    const int r = lane % 16;  // A row / B column within a fragment
+    const int g = lane / 16;  // 8-element k group
+
+    f32x4 acc[NF][MB];
+#pragma unroll
+    for (int f = 0; f < NF; ++f)
+#pragma unroll
+      for (int b = 0; b < MB; ++b) acc[f][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    const uint16_t* wrow[NF];
+    bool wvalid[NF];
+#pragma unroll
+    for (int f = 0; f < NF; ++f) {
+      const int64_t n = n0 + f * 16 + r;
+      wvalid[f] = n < N;
+      wrow[f] = w + (wvalid[f] ? n : 0) * K + g * 8;
+    }
+    const uint16_t* xrow[MB];
+    bool xvalid[MB];
+#pragma unroll
+    for (int b = 0; b < MB; ++b) {
+      const int m = b * 16 + r;
+      xvalid[b] = m < M;
+      xrow[b] = x + (xvalid[b] ? m : 0) * K + g * 8;
+    }
+
+    constexpr int kUnroll = 4;
+    int s = step_begin + wave;
+    for (; s + (kUnroll - 1) * kWaves < step_end; s += kUnroll * kWaves) {
+      U128 a[kUnroll][NF][2];
+      U128 bx[kUnroll][MB][2];
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        const int64_t k0 = static_cast<int64_t>(s + u * kWaves) * 64;
+#pragma unroll
+        for (int f = 0; f < NF; ++f) {
+          a[u][f][0] = wvalid[f] ? load16(wrow[f] + k0) : zero16();
+          a[u][f][1] = wvalid[f] ? load16(wrow[f] + k0 + 32) : zero16();
+        }
+#pragma unroll
+        for (int b = 0; b < MB; ++b) {
+          bx[u][b][0] = xvalid[b] ? load16(xrow[b] + k0) : zero16();
+          bx[u][b][1] = xvalid[b] ? load16(xrow[b] + k0 + 32) : zero16();
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int f = 0; f < NF; ++f)
+#pragma unroll
+            for (int b = 0; b < MB; ++b)
+              acc[f][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                  asBf16x8(a[u][f][h]), asBf16x8(bx[u][b][h]), acc[f][b], 0, 0, 0);
+    }
+    for (; s < step_end; s += kWaves) {
+      const int64_t k0 = static_cast<int64_t>(s) * 64;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        U128 a[NF], bx[MB];
+#pragma unroll
+        for (int f = 0; f < NF; ++f) a[f] = wvalid[f] ? load16(wrow[f] + k0 + h * 32) : zero16();
+#pragma unroll
+        for (int b = 0; b < MB; ++b) bx[b] = xvalid[b] ? load16(xrow[b] + k0 + h * 32) : zero16();
+#pragma unroll
+        for (int f = 0; f < NF; ++f)
+#pragma unroll
+          for (int b = 0; b < MB; ++b)
+            acc[f][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(asBf16x8(a[f]), asBf16x8(bx[b]),
+                                                                acc[f][b], 0, 0, 0);
+      }
+    }
+
+    // Partial tiles -> LDS [wave][n][m], then a fixed-order sum over waves into lds[0..tile).
+    float* mine = lds + wave * kTileN * kTileM;
+#pragma unroll
+    for (int f = 0; f < NF; ++f)
+#pragma unroll
+      for (int b = 0; b < MB; ++b)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) mine[(f * 16 + g * 4 + i) * kTileM + b * 16 + r] = acc[f][b][i];
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < kTileN * kTileM; idx += blockDim.x) {
+      float sum = lds[idx];
+      for (int v = 1; v < kWaves; ++v) sum += lds[v * kTileN * kTileM + idx];
+      lds[idx] = sum;
+    }
+    __syncthreads();
+  }
+};
+
+}  // namespace dk

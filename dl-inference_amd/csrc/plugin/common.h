@@ -1,0 +1,64 @@
+#pragma once
+
+// Shared helpers for the gfx950 operator plugin: dtype mapping to the device C ABI, error
+// translation (device status -> std::runtime_error, as the reference's CUDA wrappers throw),
+// and operator registration.
+
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "dli/operator.h"
+#include "dli/utils.h"
+#include "dli_hip.h"
+
+namespace dli::plugin {
+
+inline int hipDtype(DType dtype) {
+  switch (dtype) {
+    case DType::Float32: return DLI_F32;
+    case DType::Int64: return DLI_I64;
+    case DType::BFloat16: return DLI_BF16;
+    case DType::Float16: return DLI_F16;
+    case DType::Int32: return DLI_I32;
+  }
+  throw std::invalid_argument("unknown dtype");
+}
+
+inline void check(int rc, const std::string& op) {
+  if (rc == DLI_HIP_EINVAL) throw std::invalid_argument(op + ": " + dli_hip_last_error());
+  if (rc != 0) throw std::runtime_error(op + ": " + dli_hip_last_error());
+}
+
+inline void requireArity(const std::vector<const Tensor*>& inputs,
+                         const std::vector<Tensor*>& outputs, std::size_t min_in,
+                         std::size_t max_in, std::size_t n_out, const std::string& op) {
+  if (inputs.size() < min_in || inputs.size() > max_in || outputs.size() != n_out)
+    throw std::invalid_argument(op + " arity");
+  for (const Tensor* t : inputs)
+    if (t == nullptr) throw std::invalid_argument(op + " received a null input");
+  for (Tensor* t : outputs)
+    if (t == nullptr) throw std::invalid_argument(op + " received a null output");
+}
+
+inline void requireIndex(const Tensor& t, const std::string& op, const std::string& what) {
+  if (t.dtype() != DType::Int64 && t.dtype() != DType::Int32)
+    throw std::invalid_argument(op + " " + what + " must be int64 or int32");
+}
+
+inline std::vector<std::int64_t> withLast(std::vector<std::int64_t> shape, std::int64_t last) {
+  shape.back() = last;
+  return shape;
+}
+
+template <typename Op>
+void add(OperatorRegistry* registry) {
+  registry->registerFactory(Op().type(), [] { return std::make_unique<Op>(); });
+}
+
+// Registration hooks of the plugin's source files.
+void registerReferenceOps(OperatorRegistry* registry);
+void registerFusedOps(OperatorRegistry* registry);
+
+}  // namespace dli::plugin

@@ -1,0 +1,216 @@
+/*
+ * dli_hip.h — C ABI of libdli_hip.so, the MI355X (gfx950) device layer of dl-inference.
+ *
+ * Plain C: pointers, sizes and int status codes only (no torch or C++ types), so it can be
+ * bound from ctypes, cgo or any other FFI. Two groups of entry points:
+ *
+ *  1. Launch / allocator layer. Replaces the dlopen'd CUDA driver and runtime wrappers of
+ *     the reference: include/dli/cuda_driver.h:8-32 (CudaAotKernel: cuModuleLoadData,
+ *     cuModuleGetFunction, cuLaunchKernel) and include/dli/cuda_runtime.h:8-18
+ *     (cudaMallocBytes / cudaFreePointer / cudaMemcpyBytes). The HIP runtime is dlopen'd on
+ *     first use; without a GPU the calls fail with an error text instead of aborting.
+ *
+ *  2. Kernel entry points, one per operator of the reference plugin, plus fused decode
+ *     kernels. Each replaces the argument packing + cuLaunchKernel of one
+ *     python/dli_ops/aot/<op>/template.cc and follows the semantics of the matching
+ *     python/dli_ops/aot/<op>/kernel.py (cited per function). Kernels are hand-written HIP
+ *     for gfx950, compiled ahead of time to code objects embedded in the library.
+ *
+ * Conventions
+ *  - Return value: 0 on success; DLI_HIP_EINVAL (-1) for a rejected argument, DLI_HIP_ENODEV
+ *    (-2) when no HIP runtime/device is usable, otherwise the hipError_t code. The message of
+ *    the last failure on the calling thread is returned by dli_hip_last_error().
+ *  - stream: a hipStream_t passed as void*; NULL is the null stream. Every kernel entry point
+ *    is asynchronous on that stream, allocates nothing and never synchronizes, so a sequence
+ *    of them can be captured into a HIP graph.
+ *  - dtype codes follow dli::DType: DLI_F32=0, DLI_I64=1, DLI_BF16=2, DLI_F16=3, DLI_I32=4.
+ *    Floating kernels compute in fp32 and round the result to the output dtype once.
+ *  - Sizes are element counts unless named *_bytes. Zero-sized work is a successful no-op.
+ */
+#ifndef DLI_HIP_H_
+#define DLI_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  DLI_F32 = 0,
+  DLI_I64 = 1,
+  DLI_BF16 = 2,
+  DLI_F16 = 3,
+  DLI_I32 = 4,
+};
+
+enum {
+  DLI_HIP_OK = 0,
+  DLI_HIP_EINVAL = -1,
+  DLI_HIP_ENODEV = -2,
+};
+
+/* memcpy kinds, numbered as cudaMemcpyKind in include/dli/cuda_runtime.h:8-12. */
+enum {
+  DLI_MEMCPY_HOST_TO_DEVICE = 1,
+  DLI_MEMCPY_DEVICE_TO_HOST = 2,
+  DLI_MEMCPY_DEVICE_TO_DEVICE = 3,
+};
+
+/* ---------------------------------------------------------------------------------------
+ * 1. Launch / allocator layer
+ * ------------------------------------------------------------------------------------- */
+
+/* 1 when the HIP runtime loaded and reports at least one device (cuda_driver.h:8). */
+int dli_hip_available(void);
+/* Why the runtime is unavailable; "" when it is available (cuda_driver.h:9). */
+const char* dli_hip_load_error(void);
+/* Message of the last failed dli_hip_* call on this thread. */
+const char* dli_hip_last_error(void);
+/* Architecture the embedded code objects were built for, e.g. "gfx950". */
+const char* dli_hip_target_arch(void);
+
+int dli_hip_device_count(int* count);
+int dli_hip_get_device(int* device);
+int dli_hip_set_device(int device);
+
+/* Module load + launch (CudaAotKernel::load / launch, cuda_driver.cc:107-129). A launch with
+ * any grid dimension 0 returns 0 without touching the runtime (cuda_driver.cc:123). */
+int dli_hip_module_load(const void* image, size_t image_bytes, void** module);
+int dli_hip_module_get_function(void* module, const char* name, void** function);
+int dli_hip_module_unload(void* module);
+int dli_hip_launch(void* function, unsigned grid_x, unsigned grid_y, unsigned grid_z,
+                   unsigned block_x, unsigned block_y, unsigned block_z, unsigned lds_bytes,
+                   void* stream, void** args);
+
+/* Allocator / copies (cuda_runtime.cc:74-91). dli_hip_free(NULL) is a no-op. */
+int dli_hip_malloc(size_t bytes, void** ptr);
+int dli_hip_free(void* ptr);
+int dli_hip_memcpy(void* dst, const void* src, size_t bytes, int kind);
+int dli_hip_memcpy_async(void* dst, const void* src, size_t bytes, int kind, void* stream);
+int dli_hip_stream_synchronize(void* stream);
+int dli_hip_device_synchronize(void);
+
+/* Events for timing kernels on a given stream. */
+int dli_hip_event_create(void** event);
+int dli_hip_event_record(void* event, void* stream);
+int dli_hip_event_synchronize(void* event);
+int dli_hip_event_elapsed_ms(void* start, void* stop, float* ms);
+int dli_hip_event_destroy(void* event);
+
+/* ---------------------------------------------------------------------------------------
+ * 2. Kernel entry points
+ * ------------------------------------------------------------------------------------- */
+
+/* out[i] = a[i] + b[i % width] (add/kernel.py:6-11; add/template.cc:10-14). */
+int dli_hip_add(int dtype, const void* a, const void* b, void* out, int64_t total,
+                int64_t width, void* stream);
+/* out[i] = a[i] * b[i % width] (mul/kernel.py:6-11; mul/template.cc:10-14). */
+int dli_hip_mul(int dtype, const void* a, const void* b, void* out, int64_t total,
+                int64_t width, void* stream);
+/* out = x / (1 + exp(-x)) (silu/kernel.py:6-10). */
+int dli_hip_silu(int dtype, const void* x, void* out, int64_t total, void* stream);
+/* out = max(x, 0) (relu/kernel.py:6-10). */
+int dli_hip_relu(int dtype, const void* x, void* out, int64_t total, void* stream);
+
+/* y = x * rsqrt(mean(x^2) + eps) * w per row of `hidden` (rms_norm/kernel.py:6-14;
+ * rms_norm/template.cc:20-26). x, w, out share dtype. */
+int dli_hip_rms_norm(int dtype, const void* x, const void* weight, void* out, int64_t rows,
+                     int64_t hidden, float eps, void* stream);
+
+/* out[t, :] = table[ids[t], :] (embedding/kernel.py:6-23). ids_dtype is DLI_I64 or DLI_I32.
+ * An id outside [0, vocab) yields a zero row. */
+int dli_hip_embedding(int dtype, int ids_dtype, const void* ids, const void* table, void* out,
+                      int64_t tokens, int64_t hidden, int64_t vocab, void* stream);
+
+/* Row softmax over the last dim (softmax/kernel.py:6-14), any width. */
+int dli_hip_softmax(int dtype, const void* x, void* out, int64_t rows, int64_t width,
+                    void* stream);
+
+/* out[c, r] = x[r, c] (transpose/kernel.py:6-20). */
+int dli_hip_transpose2d(int dtype, const void* x, void* out, int64_t rows, int64_t cols,
+                        void* stream);
+
+/* Eval batch norm on NCHW (batch_norm2d/kernel.py:6-28). */
+int dli_hip_batch_norm2d(int dtype, const void* x, const void* weight, const void* bias,
+                         const void* running_mean, const void* running_var, void* out,
+                         int64_t total, int64_t channels, int64_t spatial, float eps,
+                         void* stream);
+
+/* Max pooling with -inf padding on NCHW (max_pool2d/kernel.py:6-41). */
+int dli_hip_max_pool2d(int dtype, const void* x, void* out, int64_t n, int64_t c, int64_t h,
+                       int64_t w, int64_t out_h, int64_t out_w, int64_t kernel_h,
+                       int64_t kernel_w, int64_t stride_h, int64_t stride_w, int64_t pad_h,
+                       int64_t pad_w, void* stream);
+
+/* Direct NCHW convolution with zero padding (conv2d/kernel.py:6-49); bias may be NULL. */
+int dli_hip_conv2d(int dtype, const void* x, const void* weight, const void* bias, void* out,
+                   int64_t n, int64_t in_c, int64_t h, int64_t w, int64_t out_c,
+                   int64_t kernel_h, int64_t kernel_w, int64_t out_h, int64_t out_w,
+                   int64_t stride_h, int64_t stride_w, int64_t pad_h, int64_t pad_w,
+                   void* stream);
+
+/* out[m, n] = sum_k x[m, k] * w[n, k] (+ bias[n]) (linear/kernel.py:6-44;
+ * linear/template.cc:23-32). x, w, bias share `dtype`; out_dtype is dtype or DLI_F32.
+ * bias may be NULL. fp32 accumulation; bf16/fp16 use MFMA. */
+int dli_hip_linear(int dtype, int out_dtype, const void* x, const void* w, const void* bias,
+                   void* out, int64_t m, int64_t n, int64_t k, void* stream);
+
+/* out[m, n] = sum_k a[m, k] * b[k, n] (matmul/kernel.py:6-40). */
+int dli_hip_matmul(int dtype, const void* a, const void* b, void* out, int64_t m, int64_t n,
+                   int64_t k, void* stream);
+
+/* Interleaved-pair rotary embedding (rotary/kernel.py:6-35): for pair p of head-vector v at
+ * token t, with c = cos[pos, p], s = sin[pos, p]:
+ *   out[2p] = x[2p]*c - x[2p+1]*s ;  out[2p+1] = x[2p]*s + x[2p+1]*c
+ * q is [batch, q_heads, seq, head_dim], k is [batch, k_heads, seq, head_dim]; cos/sin are fp32
+ * [max_pos, pairs]; pairs <= head_dim/2 (dims beyond 2*pairs are copied). Position:
+ * pos = start_pos + t, plus positions[b] when positions is non-NULL (int32/int64 [batch]).
+ * Positions outside [0, max_pos) leave the pair unrotated. */
+int dli_hip_rotary(int dtype, const void* q, const void* k, const float* cos_table,
+                   const float* sin_table, void* out_q, void* out_k, int64_t batch,
+                   int64_t q_heads, int64_t k_heads, int64_t seq, int64_t head_dim,
+                   int64_t pairs, int64_t max_pos, int64_t start_pos, const void* positions,
+                   int positions_dtype, void* stream);
+
+/* Softmax attention over contiguous [B, H, S, D] tensors (attention/kernel.py:6-62), with
+ * grouped KV heads (q head h reads kv head h / (q_heads / kv_heads)) and the causal rule
+ * key <= (seq_k - seq_q) + query. scale is usually 1/sqrt(head_dim). head_dim <= 256. */
+int dli_hip_attention(int dtype, const void* q, const void* k, const void* v, void* out,
+                      int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t seq_q,
+                      int64_t seq_k, int64_t head_dim, int causal, float scale, void* stream);
+
+/* Writes key/value [B, H, S, D] into the paged cache (layout in include/dli/kv_cache.h):
+ * token s of sequence b goes to position p = start + s, or positions[b] + s when positions is
+ * non-NULL. Tokens at p >= max_blocks * block_size are dropped. */
+int dli_hip_kv_append(int dtype, const void* key, const void* value, void* key_pool,
+                      void* value_pool, const int32_t* block_table, int64_t batch,
+                      int64_t heads, int64_t seq, int64_t head_dim, int64_t block_size,
+                      int64_t max_blocks, int64_t start, const void* positions,
+                      int positions_dtype, void* stream);
+
+/* Attention of q [B, Hq, Sq, D] over the paged cache. Sequence b holds
+ * L_b = past_len + Sq tokens (past_len = positions[b] when positions is non-NULL, else
+ * `past`); the query at index i sits at position past_len + i and, when causal, sees keys
+ * at positions <= past_len + i. Split along the keys across workgroups ("flash decoding");
+ * partial results go to `workspace` (size from dli_hip_paged_attention_workspace). */
+size_t dli_hip_paged_attention_workspace(int64_t batch, int64_t q_heads, int64_t seq_q,
+                                         int64_t head_dim, int64_t max_tokens);
+int dli_hip_paged_attention(int dtype, const void* q, const void* key_pool,
+                            const void* value_pool, const int32_t* block_table, void* out,
+                            int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t seq_q,
+                            int64_t head_dim, int64_t block_size, int64_t max_blocks,
+                            int64_t past, const void* positions, int positions_dtype,
+                            int causal, float scale, void* workspace, size_t workspace_bytes,
+                            void* stream);
+
+/* ids[r] = first index of the maximum of row r of x [rows, width] (torch.argmax rule). */
+int dli_hip_argmax(int dtype, const void* x, int64_t* ids, int64_t rows, int64_t width,
+                   void* stream);
+
+#ifdef __cplusplus
+}  /* extern "C" */
+#endif
+
+#endif  /* DLI_HIP_H_ */

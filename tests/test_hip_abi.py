@@ -1,0 +1,73 @@
+"""The C ABI of libdli_hip.so on a machine without a GPU: every symbol declared in
+include/dli_hip.h is exported, and calls fail with an error text instead of crashing
+(the reference's tests/cpp/test_cuda_aot_kernel.cc:4-12 and test_cuda_runtime.cc:4-11)."""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import subprocess
+
+import torch  # noqa: F401  (load torch's HIP runtime first)
+
+import dli
+from dli import hip
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include",
+                      "dli_hip.h")
+
+
+def declared_in_header():
+    text = open(HEADER, encoding="utf-8").read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(dli_hip_\w+)\s*\(", text)))
+
+
+def exported_symbols():
+    out = subprocess.run(["nm", "-D", "--defined-only", dli.hip_library_path()],
+                         capture_output=True, text=True, check=True).stdout
+    return sorted({line.split()[-1] for line in out.splitlines() if " T " in line})
+
+
+def test_every_declared_symbol_is_exported_and_bound():
+    declared = declared_in_header()
+    assert len(declared) > 30
+    assert declared == exported_symbols()
+    assert declared == hip.declared_symbols()
+
+
+def test_library_loads_and_reports_target():
+    lib = hip.load()
+    assert lib.dli_hip_target_arch() == b"gfx950"
+
+
+def test_no_device_behaviour():
+    lib = hip.load()
+    if torch.cuda.is_available():
+        assert lib.dli_hip_available() == 1
+        return
+    assert lib.dli_hip_available() == 0
+    assert lib.dli_hip_load_error()  # non-empty reason
+    assert lib.dli_hip_free(None) == 0  # cudaFreePointer(nullptr) is a no-op
+    p = ctypes.c_void_p()
+    assert lib.dli_hip_malloc(16, ctypes.byref(p)) == -2
+    assert b"unavailable" in lib.dli_hip_last_error()
+
+
+def test_grid_zero_launch_and_empty_work_are_noops():
+    lib = hip.load()
+    assert lib.dli_hip_launch(None, 0, 1, 1, 64, 1, 1, 0, None, None) == 0
+    assert lib.dli_hip_add(hip.BF16, None, None, None, 0, 1, None) == 0
+    assert lib.dli_hip_linear(hip.F32, hip.F32, None, None, None, None, 0, 5, 5, None) == 0
+    assert lib.dli_hip_attention(hip.F32, None, None, None, None, 0, 2, 2, 1, 1, 8, 1, 1.0, None) == 0
+
+
+def test_invalid_arguments_are_rejected_with_a_message():
+    lib = hip.load()
+    assert lib.dli_hip_add(hip.I64, None, None, None, 4, 1, None) == -1
+    assert b"unsupported dtype" in lib.dli_hip_last_error()
+    assert lib.dli_hip_attention(hip.F32, None, None, None, None, 1, 3, 2, 1, 1, 8, 1, 1.0, None) == -1
+    assert b"multiple of kv_heads" in lib.dli_hip_last_error()
+    assert lib.dli_hip_rotary(hip.F32, None, None, None, None, None, None, 1, 1, 1, 1, 3, 1, 4, 0,
+                              None, hip.I64, None) == -1
+    assert lib.dli_hip_linear(hip.BF16, hip.F16, None, None, None, None, 1, 1, 1, None) == -1
