@@ -1,0 +1,200 @@
+"""Decode throughput of the gfx950 operator plugin on one MI355X.
+
+Workload: Qwen2-0.5B-shape (24 layers, hidden 896, 14/2 heads, head_dim 64, MLP 4864, vocab
+151936, tied embeddings), random-init bf16, greedy decode at batch 32 with every sequence at
+context 4096 (a seeded synthetic KV context fills positions 0..4094; each step writes position
+4095 and attends over 4096 keys). One step = one replay of the captured dli.graph.v1 decode
+step (fused operator graph) through Engine + libdli_hip_ops.so; inputs already in HBM.
+
+Prints one JSON line: decode tok/s (whole job), ms/step, the step's HBM roofline fraction
+(algorithmic bytes = weights + KV read + KV write + bf16 logits), the dominant kernel's roofline
+(decode attention, timed live with HIP events on its stream) and a CPU baseline (the CPU oracle
+timed on a bounded sample of the same step on this host).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "dl-inference_amd", "python"))
+
+METRIC = "decode tok/s + % HBM roofline, Qwen2-0.5B-shape bf16 b=32 ctx4096"
+HBM_PEAK_GBS = 8000.0
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--batch", type=int, default=32)
+    ap.add_argument("--context", type=int, default=4096)
+    ap.add_argument("--layers", type=int, default=None, help="override (for quick local checks)")
+    ap.add_argument("--cpu-baseline-steps", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--splits", default="qkv=1,o=2,down=4")
+    ap.add_argument("--eager", action="store_true", help="run the step without graph capture")
+    return ap.parse_args()
+
+
+def step_bytes(cfg, batch, context):
+    weights = cfg.weight_bytes()
+    kv_read = batch * context * cfg.kv_bytes_per_token()
+    kv_write = batch * cfg.kv_bytes_per_token()
+    logits = batch * cfg.vocab * 2
+    return weights + kv_read + kv_write, weights, kv_read, kv_write, logits
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 "
+                                   "(multi-GPU decode is data-parallel by batch, see DESIGN.md)"}))
+        sys.exit(2)
+
+    import torch
+
+    import dli
+    from dli import hip
+    from dli_qwen2 import QWEN2_0_5B, DecodeSession, random_weights
+    from dataclasses import replace
+
+    cfg = QWEN2_0_5B if args.layers is None else replace(QWEN2_0_5B, layers=args.layers)
+    B, ctx = args.batch, args.context
+    splits = {k: int(v) for k, v in (item.split("=") for item in args.splits.split(","))}
+    dev = "cuda"
+    torch.manual_seed(0)
+    weights = random_weights(cfg, seed=0, device=dev)
+    session = DecodeSession(cfg, weights, batch=B, max_seq_len=ctx + 64, fused=True,
+                            splits=splits, logits_dtype="bfloat16")
+    g = torch.Generator(device=dev).manual_seed(1)
+    ids = torch.randint(0, cfg.vocab, (B,), generator=g, device=dev)
+    pos = torch.full((B,), ctx - 1, dtype=torch.int64, device=dev)
+    session.ids.copy_(ids)
+    session.positions.copy_(pos)
+    session.run_eager()  # reserves the paged caches
+    torch.cuda.synchronize()
+    # seeded synthetic context: positions [0, ctx-1) of every layer's K/V pools
+    for i in range(cfg.layers):
+        e = session.engine.kv_cache_entry(f"layer_{i}")
+        for pool in (e["key"], e["value"]):
+            pool.copy_(torch.randn(pool.shape, generator=g, device=dev, dtype=torch.float32)
+                       .to(pool.dtype))
+    torch.cuda.synchronize()
+    if not args.eager:
+        session.capture(chain_ids=True)  # each replay feeds its greedy tokens to the next
+
+    def one_step():
+        if args.eager:
+            out = session.run_eager()
+            session.ids.copy_(out["next_ids"])
+            return out
+        return session.replay()
+
+    for _ in range(args.warmup):
+        one_step()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    start_ev, stop_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start_ev.record(stream)
+    for _ in range(args.steps):
+        one_step()
+    stop_ev.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = start_ev.elapsed_time(stop_ev) / args.steps
+    tok_s = B * 1000.0 / ms_per_step
+    total, w_bytes, kv_read, kv_write, logit_bytes = step_bytes(cfg, B, ctx)
+    total += logit_bytes
+    step_gbs = total / (ms_per_step * 1e-3) / 1e9
+
+    # dominant kernel: decode attention of one layer (same cache, same q), timed with HIP
+    # events on the stream it is launched on
+    e = session.engine.kv_cache_entry("layer_0")
+    q = torch.randn(B, cfg.heads, 1, cfg.head_dim, generator=g, device=dev).to(torch.bfloat16)
+    out = torch.empty_like(q)
+    ws_bytes = hip.lib().dli_hip_paged_attention_workspace(B, cfg.heads, 1, cfg.head_dim,
+                                                            e["max_blocks"] * e["block_size"])
+    ws = torch.empty((ws_bytes + 3) // 4, dtype=torch.float32, device=dev)
+    s_ptr = stream.cuda_stream
+
+    def attn():
+        hip.call("dli_hip_paged_attention", hip.BF16, q.data_ptr(), e["key"].data_ptr(),
+                 e["value"].data_ptr(), e["block_table"].data_ptr(), out.data_ptr(), B, cfg.heads,
+                 cfg.kv_heads, 1, cfg.head_dim, e["block_size"], e["max_blocks"], 0,
+                 pos.data_ptr(), hip.I64, 1, cfg.head_dim ** -0.5, ws.data_ptr(), ws_bytes, s_ptr)
+
+    for _ in range(5):
+        attn()
+    reps = 200
+    a0, a1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a0.record(stream)
+    for _ in range(reps):
+        attn()
+    a1.record(stream)
+    torch.cuda.synchronize()
+    attn_us = a0.elapsed_time(a1) * 1000.0 / reps
+    attn_bytes = B * ctx * cfg.kv_heads * cfg.head_dim * 2 * 2 + 2 * B * cfg.heads * cfg.head_dim * 2
+    attn_gbs = attn_bytes / (attn_us * 1e-6) / 1e9
+
+    cpu = None
+    if not args.no_cpu_baseline and args.cpu_baseline_steps > 0:
+        sys.path.insert(0, ROOT)
+        from oracle.qwen2 import Qwen2Oracle
+
+        threads = torch.get_num_threads()
+        oracle = Qwen2Oracle(cfg, {k: v for k, v in weights.items()})
+        oracle.reset_static(B, ctx, seed=2, fill=ctx - 1)
+        cpu_ids = ids.cpu()
+        oracle.step_static(cpu_ids, ctx - 1)  # warm-up
+        t1 = time.perf_counter()
+        for _ in range(args.cpu_baseline_steps):
+            oracle.step_static(cpu_ids, ctx - 1)
+        cpu_s = (time.perf_counter() - t1) / args.cpu_baseline_steps
+        cpu = {"value": round(B / cpu_s, 2), "unit": "tok/s", "cores": threads, "kind": "port",
+               "sample": f"{args.cpu_baseline_steps} decode steps (after 1 warm-up) of the same "
+                         f"batch-{B}, context-{ctx} step; torch fp32 CPU oracle with bf16 "
+                         f"rounding points; {cpu_s * 1000:.1f} ms/step"}
+        del oracle
+
+    result = {
+        "metric": METRIC,
+        "value": round(tok_s, 1),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "Qwen2-0.5B-shape bf16 greedy decode, batch 32, context 4096",
+                   "model": "qwen2-0.5b-shape (random init)", "global_batch": B,
+                   "seq_len": ctx, "layers": cfg.layers, "parallelism": "none (1 GPU)",
+                   "graph": "fused dli.graph.v1 decode step, HIP-graph replay",
+                   "splits": splits},
+        "roofline": {"bound": "hbm", "kernel": "decode attention (decode_attention_d64 + combine)",
+                     "achieved": round(attn_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(attn_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "avg_us": round(attn_us, 2), "bytes_per_launch": attn_bytes},
+        "step_roofline": {"bound": "hbm", "bytes_per_step": total, "achieved": round(step_gbs, 1),
+                          "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                          "frac": round(step_gbs / HBM_PEAK_GBS, 4),
+                          "bytes": {"weights": w_bytes, "kv_read": kv_read, "kv_write": kv_write,
+                                    "logits_bf16": logit_bytes}},
+        "cpu_baseline": cpu,
+        "wall_s_timed": round(wall, 3),
+        "device": torch.cuda.get_device_name(0),
+    }
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -39,8 +39,11 @@ Tensor identityBlockTable(std::int64_t batch, std::int64_t max_blocks, int devic
 
 void allocatePools(KVCacheEntry& e, DType dtype, int device_id) {
   const std::int64_t blocks = e.batch * e.max_blocks;
-  e.key = Tensor::cuda(dtype, {blocks, e.heads, e.block_size, e.head_dim}, device_id);
-  e.value = Tensor::cuda(dtype, {blocks, e.heads, e.head_dim, e.block_size}, device_id);
+  // Zero-filled once, so that attention kernels reading a partially filled block see finite
+  // values in the slots they mask out.
+  const auto options = at::TensorOptions().dtype(toTorchDType(dtype)).device(at::kCUDA, device_id);
+  e.key = Tensor(at::zeros({blocks, e.heads, e.block_size, e.head_dim}, options));
+  e.value = Tensor(at::zeros({blocks, e.heads, e.head_dim, e.block_size}, options));
   e.block_table = identityBlockTable(e.batch, e.max_blocks, device_id);
 }
 

@@ -1,0 +1,236 @@
+// Entry points of the fused decode kernels (csrc/kernels/decode.hip) and the MFMA decode
+// attention (csrc/kernels/attention.hip). Declared in include/dli_hip.h.
+#include <cmath>
+#include <string>
+
+#include "runtime.h"
+
+namespace dli::hip {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kTileN = 32;           // weight rows per workgroup (NF = 2)
+constexpr size_t kMaxLds = 160 * 1024;  // gfx950 LDS per workgroup
+constexpr int kDecodeChunk = 256;    // keys per decode-attention workgroup
+
+struct MbKernels {
+  DeviceKernel m1, m2, m4;
+  MbKernels(const char* module, const char* base)
+      : m1(module, make(base, "_m1")), m2(module, make(base, "_m2")), m4(module, make(base, "_m4")) {}
+  DeviceKernel* pick(int64_t m) { return m <= 16 ? &m1 : (m <= 32 ? &m2 : (m <= 64 ? &m4 : nullptr)); }
+
+ private:
+  static const char* make(const char* base, const char* suffix) {
+    return (new std::string(std::string(base) + suffix))->c_str();
+  }
+};
+
+MbKernels k_qkv("decode", "qkv_rope_append");
+MbKernels k_linres("decode", "linear_residual");
+MbKernels k_gate_up("decode", "gate_up_silu");
+MbKernels k_lm_head("decode", "lm_head_argmax");
+DeviceKernel k_argmax_final("decode", "argmax_finalize");
+DeviceKernel k_dec_attn("attention", "decode_attention_d64");
+DeviceKernel k_dec_combine("attention", "decode_attention_combine_d64");
+
+int tileM(int64_t m) { return m <= 16 ? 16 : (m <= 32 ? 32 : 64); }
+
+int bad(const char* op, const std::string& what) {
+  return fail(DLI_HIP_EINVAL, std::string(op) + ": " + what);
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+size_t alignUp(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// Split-K workspace: [counters: tiles x u32, padded to 256 B][partials: tiles x splits x tile fp32]
+size_t splitWorkspace(int64_t n, int64_t m, int splits) {
+  if (splits <= 1) return 0;
+  const int64_t tiles = (n + kTileN - 1) / kTileN;
+  return alignUp(static_cast<size_t>(tiles) * 4, 256) +
+         static_cast<size_t>(tiles) * splits * kTileN * tileM(m) * sizeof(float);
+}
+
+size_t normLds(int64_t m, int64_t k) {
+  return static_cast<size_t>(tileM(m)) * (k + 8) * 2 + 4ull * kTileN * tileM(m) * sizeof(float);
+}
+
+int checkSkinny(const char* op, int64_t m, int64_t k) {
+  if (m <= 0 || m > 64) return bad(op, "batch rows must be in [1, 64]");
+  if (k <= 0 || k % 64 != 0) return bad(op, "reduction size must be a positive multiple of 64");
+  return 0;
+}
+
+int checkSplits(const char* op, int64_t n, int64_t m, int64_t k, int splits, void* workspace,
+                size_t workspace_bytes) {
+  if (splits < 1 || splits > k / 64) return bad(op, "splits must be in [1, k / 64]");
+  if (splits > 1 && (workspace == nullptr || workspace_bytes < splitWorkspace(n, m, splits)))
+    return bad(op, "workspace too small for split-K");
+  return 0;
+}
+
+}  // namespace
+}  // namespace dli::hip
+
+using namespace dli::hip;
+
+extern "C" {
+
+size_t dli_hip_splitk_workspace(int64_t n, int64_t m, int splits) {
+  return splitWorkspace(n, m, splits);
+}
+
+int dli_hip_qkv_rope_append(const void* hidden, const void* norm_weight, const void* w_qkv,
+                            const void* b_qkv, const float* cos_table, const float* sin_table,
+                            int64_t max_pos, const void* positions, int positions_dtype,
+                            void* q_out, void* key_pool, void* value_pool,
+                            const int32_t* block_table, int64_t block_size, int64_t max_blocks,
+                            int64_t batch, int64_t hidden_size, int64_t q_heads, int64_t kv_heads,
+                            int64_t head_dim, float eps, int splits, void* workspace,
+                            size_t workspace_bytes, void* stream) {
+  const char* op = "qkv_rope_append";
+  if (int rc = checkSkinny(op, batch, hidden_size)) return rc;
+  if (positions == nullptr || (positions_dtype != DLI_I64 && positions_dtype != DLI_I32))
+    return bad(op, "positions (int64/int32 [batch]) are required");
+  if (head_dim <= 0 || head_dim % 2 != 0) return bad(op, "head_dim must be even");
+  if (kv_heads <= 0 || q_heads <= 0) return bad(op, "head counts must be positive");
+  if ((q_heads * head_dim) % kTileN != 0 || (kv_heads * head_dim) % kTileN != 0)
+    return bad(op, "q and kv widths must be multiples of 32");
+  if (block_size <= 0 || max_blocks <= 0) return bad(op, "empty cache geometry");
+  const int64_t n = (q_heads + 2 * kv_heads) * head_dim;
+  if (int rc = checkSplits(op, n, batch, hidden_size, splits, workspace, workspace_bytes)) return rc;
+  if (!aligned16(hidden) || !aligned16(w_qkv) || !aligned16(norm_weight))
+    return bad(op, "hidden, norm_weight and w_qkv must be 16-byte aligned");
+  const size_t lds = normLds(batch, hidden_size);
+  if (lds > kMaxLds) return bad(op, "batch x hidden too large for the LDS prologue");
+  const int64_t tiles = (n + kTileN - 1) / kTileN;
+  uint32_t* counters = static_cast<uint32_t*>(workspace);
+  float* partials = splits > 1
+                        ? reinterpret_cast<float*>(static_cast<char*>(workspace) +
+                                                   alignUp(static_cast<size_t>(tiles) * 4, 256))
+                        : nullptr;
+  const int pos64 = positions_dtype == DLI_I64 ? 1 : 0;
+  return launch(*k_qkv.pick(batch), {static_cast<unsigned>(tiles), static_cast<unsigned>(splits)},
+                {kThreads}, static_cast<unsigned>(lds), stream, hidden, norm_weight, w_qkv, b_qkv,
+                cos_table, sin_table, max_pos, positions, pos64, q_out, key_pool, value_pool,
+                block_table, block_size, max_blocks, static_cast<int>(batch),
+                static_cast<int>(hidden_size), static_cast<int>(q_heads),
+                static_cast<int>(kv_heads), static_cast<int>(head_dim), eps, partials, counters,
+                splits);
+}
+
+int dli_hip_linear_residual(const void* x, const void* w, const void* bias, const void* residual,
+                            void* out, int64_t m, int64_t n, int64_t k, int splits,
+                            void* workspace, size_t workspace_bytes, void* stream) {
+  const char* op = "linear_residual";
+  if (int rc = checkSkinny(op, m, k)) return rc;
+  if (n <= 0) return bad(op, "n must be positive");
+  if (int rc = checkSplits(op, n, m, k, splits, workspace, workspace_bytes)) return rc;
+  if (!aligned16(x) || !aligned16(w)) return bad(op, "x and w must be 16-byte aligned");
+  const int64_t tiles = (n + kTileN - 1) / kTileN;
+  uint32_t* counters = static_cast<uint32_t*>(workspace);
+  float* partials = splits > 1
+                        ? reinterpret_cast<float*>(static_cast<char*>(workspace) +
+                                                   alignUp(static_cast<size_t>(tiles) * 4, 256))
+                        : nullptr;
+  return launch(*k_linres.pick(m), {static_cast<unsigned>(tiles), static_cast<unsigned>(splits)},
+                {kThreads}, 0, stream, x, w, bias, residual, out, static_cast<int>(m), n,
+                static_cast<int>(k), partials, counters, splits);
+}
+
+int dli_hip_gate_up_silu(const void* hidden, const void* norm_weight, const void* w_gate_up,
+                         void* out, int64_t m, int64_t ffn, int64_t hidden_size, float eps,
+                         void* stream) {
+  const char* op = "gate_up_silu";
+  if (int rc = checkSkinny(op, m, hidden_size)) return rc;
+  if (ffn <= 0 || ffn % 16 != 0) return bad(op, "ffn must be a positive multiple of 16");
+  if (!aligned16(hidden) || !aligned16(w_gate_up) || !aligned16(norm_weight))
+    return bad(op, "hidden, norm_weight and w_gate_up must be 16-byte aligned");
+  const size_t lds = normLds(m, hidden_size);
+  if (lds > kMaxLds) return bad(op, "batch x hidden too large for the LDS prologue");
+  return launch(*k_gate_up.pick(m), {static_cast<unsigned>(ffn / 16)}, {kThreads},
+                static_cast<unsigned>(lds), stream, hidden, norm_weight, w_gate_up, out,
+                static_cast<int>(m), ffn, static_cast<int>(hidden_size), eps);
+}
+
+size_t dli_hip_lm_head_argmax_workspace(int64_t m, int64_t vocab) {
+  const int64_t tiles = (vocab + kTileN - 1) / kTileN;
+  return static_cast<size_t>(tiles) * m * (sizeof(float) + sizeof(int32_t));
+}
+
+int dli_hip_lm_head_argmax(const void* hidden, const void* norm_weight, const void* w,
+                           void* logits, int logits_dtype, int64_t* ids, int64_t m, int64_t vocab,
+                           int64_t hidden_size, float eps, void* workspace,
+                           size_t workspace_bytes, void* stream) {
+  const char* op = "lm_head_argmax";
+  if (int rc = checkSkinny(op, m, hidden_size)) return rc;
+  if (vocab <= 0 || vocab >= (int64_t{1} << 31)) return bad(op, "vocab must be in [1, 2^31)");
+  if (logits != nullptr && logits_dtype != DLI_F32 && logits_dtype != DLI_BF16)
+    return bad(op, "logits dtype must be float32 or bfloat16");
+  if (ids == nullptr) return bad(op, "ids is NULL");
+  if (workspace == nullptr || workspace_bytes < dli_hip_lm_head_argmax_workspace(m, vocab))
+    return bad(op, "workspace too small");
+  if (!aligned16(hidden) || !aligned16(w) || !aligned16(norm_weight))
+    return bad(op, "hidden, norm_weight and w must be 16-byte aligned");
+  const size_t lds = normLds(m, hidden_size);
+  if (lds > kMaxLds) return bad(op, "batch x hidden too large for the LDS prologue");
+  const int64_t tiles = (vocab + kTileN - 1) / kTileN;
+  if (tiles > 0x7fffffff) return bad(op, "too many tiles");
+  float* part_val = static_cast<float*>(workspace);
+  int32_t* part_idx = reinterpret_cast<int32_t*>(part_val + tiles * m);
+  const int logits_f32 = logits_dtype == DLI_F32 ? 1 : 0;
+  if (int rc = launch(*k_lm_head.pick(m), {static_cast<unsigned>(tiles)}, {kThreads},
+                      static_cast<unsigned>(lds), stream, hidden, norm_weight, w, logits,
+                      logits_f32, part_val, part_idx, static_cast<int>(m), vocab,
+                      static_cast<int>(hidden_size), eps))
+    return rc;
+  return launch(k_argmax_final, {static_cast<unsigned>(m)}, {kThreads}, 0, stream,
+                static_cast<const float*>(part_val), static_cast<const int32_t*>(part_idx),
+                static_cast<int>(tiles), static_cast<int>(m), ids);
+}
+
+}  // extern "C"
+
+namespace dli::hip {
+
+// MFMA decode attention (one query per sequence, bf16, head_dim 64); used by
+// dli_hip_paged_attention when the case fits. Returns 1 when it does not apply.
+int decodeAttentionFast(int dtype, const void* q, const void* key_pool, const void* value_pool,
+                        const int32_t* block_table, void* out, int64_t batch, int64_t q_heads,
+                        int64_t kv_heads, int64_t seq_q, int64_t head_dim, int64_t block_size,
+                        int64_t max_blocks, int64_t past, const void* positions,
+                        int positions_dtype, float scale, void* workspace, size_t workspace_bytes,
+                        void* stream) {
+  if (dtype != DLI_BF16 || seq_q != 1 || head_dim != 64 || q_heads / kv_heads > 16 ||
+      block_size % 32 != 0 || !aligned16(q))
+    return 1;
+  const int64_t capacity = max_blocks * block_size;
+  const int max_splits = static_cast<int>((capacity + kDecodeChunk - 1) / kDecodeChunk);
+  const size_t need = static_cast<size_t>(batch * q_heads) * max_splits * (2 + 64) * sizeof(float);
+  if (workspace == nullptr || workspace_bytes < need) return 1;
+  if (batch * kv_heads > 65535) return 1;
+  float* ws_ml = static_cast<float*>(workspace);
+  float* ws_o = ws_ml + batch * q_heads * max_splits * 2;
+  const int pos64 = positions_dtype == DLI_I64 ? 1 : 0;
+  const float scale_log2 = scale * 1.4426950408889634f;
+  if (int rc = launch(k_dec_attn, {static_cast<unsigned>(max_splits), static_cast<unsigned>(batch * kv_heads)},
+                      {kThreads}, 0, stream, static_cast<const uint16_t*>(q),
+                      static_cast<const uint16_t*>(key_pool), static_cast<const uint16_t*>(value_pool),
+                      block_table, positions, pos64, past, ws_ml, ws_o, static_cast<int>(q_heads),
+                      static_cast<int>(kv_heads), block_size, max_blocks, kDecodeChunk, max_splits,
+                      scale_log2))
+    return rc;
+  return launch(k_dec_combine, {static_cast<unsigned>(batch * q_heads)}, {64}, 0, stream,
+                static_cast<const float*>(ws_ml), static_cast<const float*>(ws_o), positions, pos64,
+                past, static_cast<uint16_t*>(out), static_cast<int>(q_heads), capacity, kDecodeChunk,
+                max_splits);
+}
+
+size_t decodeAttentionWorkspace(int64_t batch, int64_t q_heads, int64_t seq_q, int64_t head_dim,
+                                int64_t max_tokens) {
+  if (seq_q != 1 || head_dim != 64) return 0;
+  const int64_t max_splits = (max_tokens + kDecodeChunk - 1) / kDecodeChunk;
+  return static_cast<size_t>(batch * q_heads * max_splits) * (2 + 64) * sizeof(float);
+}
+
+}  // namespace dli::hip

@@ -91,6 +91,15 @@ int unary(FloatKernels& kernels, const char* op, int dtype, const void* x, void*
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 }  // namespace
+
+int decodeAttentionFast(int dtype, const void* q, const void* key_pool, const void* value_pool,
+                        const int32_t* block_table, void* out, int64_t batch, int64_t q_heads,
+                        int64_t kv_heads, int64_t seq_q, int64_t head_dim, int64_t block_size,
+                        int64_t max_blocks, int64_t past, const void* positions,
+                        int positions_dtype, float scale, void* workspace, size_t workspace_bytes,
+                        void* stream);
+size_t decodeAttentionWorkspace(int64_t batch, int64_t q_heads, int64_t seq_q, int64_t head_dim,
+                                int64_t max_tokens);
 }  // namespace dli::hip
 
 using namespace dli::hip;
@@ -290,8 +299,7 @@ int dli_hip_kv_append(int dtype, const void* key, const void* value, void* key_p
 
 size_t dli_hip_paged_attention_workspace(int64_t batch, int64_t q_heads, int64_t seq_q,
                                          int64_t head_dim, int64_t max_tokens) {
-  (void)batch, (void)q_heads, (void)seq_q, (void)head_dim, (void)max_tokens;
-  return 0;
+  return decodeAttentionWorkspace(batch, q_heads, seq_q, head_dim, max_tokens);
 }
 
 int dli_hip_paged_attention(int dtype, const void* q, const void* key_pool,
@@ -300,7 +308,6 @@ int dli_hip_paged_attention(int dtype, const void* q, const void* key_pool,
                             int64_t head_dim, int64_t block_size, int64_t max_blocks, int64_t past,
                             const void* positions, int positions_dtype, int causal, float scale,
                             void* workspace, size_t workspace_bytes, void* stream) {
-  (void)workspace, (void)workspace_bytes;
   DeviceKernel* ka = k_paged_attention.pick(dtype);
   if (ka == nullptr) return badDtype("paged_attention", dtype);
   if (head_dim <= 0 || head_dim > 256) return badArg("paged_attention", "head_dim must be in [1, 256]");
@@ -313,6 +320,13 @@ int dli_hip_paged_attention(int dtype, const void* q, const void* key_pool,
   const int64_t rows = batch * q_heads * seq_q;
   if (rows == 0) return 0;
   if (rows > 0x7fffffff) return badArg("paged_attention", "too many query rows");
+  if (causal || seq_q == 1) {
+    const int rc = decodeAttentionFast(dtype, q, key_pool, value_pool, block_table, out, batch,
+                                       q_heads, kv_heads, seq_q, head_dim, block_size, max_blocks,
+                                       past, positions, positions_dtype, scale, workspace,
+                                       workspace_bytes, stream);
+    if (rc != 1) return rc;
+  }
   const int pos64 = positions_dtype == DLI_I64 ? 1 : 0;
   return launch(*ka, {static_cast<unsigned>(rows)}, {64}, 0, stream, q, key_pool, value_pool,
                 block_table, out, batch, q_heads, kv_heads, seq_q, head_dim, block_size, max_blocks,

@@ -186,3 +186,217 @@ DK_FLOAT_KERNELS(kv_append, 256,
                   int pos64),
                  (key, value, k_pool, v_pool, block_table, B, H, S, D, block_size, max_blocks,
                   start, positions, pos64))
+
+// ---------------------------------------------------------------------------------------------
+// Decode attention over the paged cache with MFMA (bf16, head_dim 64, one query per sequence,
+// up to 16 query heads per KV head). "Flash decoding": grid (splits, batch * kv_heads); a
+// workgroup owns `chunk` consecutive keys of one (sequence, kv head) and all query heads of that
+// group, so each K/V byte is read once per KV head rather than once per query head.
+//
+// Per wave and 32-key sub-tile (v_mfma_f32_16x16x32_bf16):
+//   S = K Q^T    A = 16 keys x 32 dims (two MFMAs per 64 dims), B = Q^T (16 heads).
+//                The A rows of half hf are keys t0 + 8*(r/4) + 4*hf + r%4, so the output lane
+//                (r, g) holds keys t0 + 8g + 4hf + i (i < 4) of head r: eight consecutive keys.
+//   online softmax per head column (max/sum over the 4 lane groups with xor-shuffles)
+//   O^T += V^T P^T  A = V^T (16 dims x 32 keys, dim-major cache blocks give 16-byte runs),
+//                B = P^T straight from the registers above (no LDS round trip).
+// The 4 waves of a workgroup merge (m, l, O) through LDS; the split's partial goes to workspace
+// and decode_attention_combine merges the splits.
+// ---------------------------------------------------------------------------------------------
+#include "skinny.h"
+
+namespace {
+
+constexpr int kDecD = 64;
+
+__device__ __forceinline__ uint32_t packBf16(float lo, float hi) {
+  return static_cast<uint32_t>(floatToBf16(lo)) | (static_cast<uint32_t>(floatToBf16(hi)) << 16);
+}
+
+__device__ void decode_attention_impl(const uint16_t* q, const uint16_t* k_pool,
+                                      const uint16_t* v_pool, const int32_t* block_table,
+                                      const void* positions, int pos64, int64_t past, float* ws_ml,
+                                      float* ws_o, int Hq, int Hkv, int64_t BS, int64_t max_blocks,
+                                      int chunk, int max_splits, float scale_log2) {
+  __shared__ float sm[4][16];
+  __shared__ float sl[4][16];
+  __shared__ float so[4][kDecD][17];
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int r = lane % 16, g = lane / 16;
+  const int bk = blockIdx.y;
+  const int b = bk / Hkv, kvh = bk % Hkv;
+  const int group = Hq / Hkv;
+  const int64_t past_b = positions != nullptr ? loadIndex(positions, pos64, b) : past;
+  int64_t L = past_b + 1;
+  if (L > max_blocks * BS) L = max_blocks * BS;
+  const int64_t start = static_cast<int64_t>(blockIdx.x) * chunk;
+  if (start >= L) return;  // uniform per workgroup
+  const int64_t end = start + chunk < L ? start + chunk : L;
+
+  U128 qf[2];
+  if (r < group) {
+    const uint16_t* qp = q + (static_cast<int64_t>(b) * Hq + kvh * group + r) * kDecD + g * 8;
+    qf[0] = load16(qp);
+    qf[1] = load16(qp + 32);
+  } else {
+    qf[0] = zero16();
+    qf[1] = zero16();
+  }
+  const int32_t* table = block_table + static_cast<int64_t>(b) * max_blocks;
+  const int64_t head_stride = BS * kDecD;  // elements per (block, kv head)
+
+  float m_run = -INFINITY, l_run = 0.f;
+  f32x4 o[4];
+#pragma unroll
+  for (int d = 0; d < 4; ++d) o[d] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int64_t t0 = start + wave * 32; t0 < end; t0 += 4 * 32) {
+    U128 kf[2][2];
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      const int64_t tok = t0 + 8 * (r / 4) + 4 * hf + (r % 4);
+      if (tok < end) {
+        const int64_t blk = table[tok / BS];
+        const uint16_t* kp = k_pool + (blk * Hkv + kvh) * head_stride + (tok % BS) * kDecD + g * 8;
+        kf[hf][0] = load16(kp);
+        kf[hf][1] = load16(kp + 32);
+      } else {
+        kf[hf][0] = zero16();
+        kf[hf][1] = zero16();
+      }
+    }
+    U128 vf[4];
+    const int64_t tv = t0 + 8 * g;
+    if (tv < end) {
+      const int64_t blk = table[tv / BS];
+      const uint16_t* vp = v_pool + (blk * Hkv + kvh) * head_stride + (tv % BS);
+#pragma unroll
+      for (int d = 0; d < 4; ++d) vf[d] = load16(vp + (d * 16 + r) * BS);
+    } else {
+#pragma unroll
+      for (int d = 0; d < 4; ++d) vf[d] = zero16();
+    }
+
+    f32x4 s[2];
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      s[hf] = f32x4{0.f, 0.f, 0.f, 0.f};
+      s[hf] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(asBf16x8(kf[hf][0]), asBf16x8(qf[0]), s[hf], 0, 0, 0);
+      s[hf] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(asBf16x8(kf[hf][1]), asBf16x8(qf[1]), s[hf], 0, 0, 0);
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t tok = t0 + 8 * g + 4 * hf + i;
+        const float v = tok < end ? s[hf][i] * scale_log2 : -INFINITY;
+        s[hf][i] = v;
+        mx = fmaxf(mx, v);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+    const float m_new = fmaxf(m_run, mx);
+    const float alpha = exp2f(m_run - m_new);
+    float p[2][4];
+    float sum = 0.f;
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        p[hf][i] = exp2f(s[hf][i] - m_new);
+        sum += p[hf][i];
+      }
+    sum += __shfl_xor(sum, 16, kWave);
+    sum += __shfl_xor(sum, 32, kWave);
+    l_run = l_run * alpha + sum;
+    m_run = m_new;
+    U128 pk;
+    pk.w[0] = packBf16(p[0][0], p[0][1]);
+    pk.w[1] = packBf16(p[0][2], p[0][3]);
+    pk.w[2] = packBf16(p[1][0], p[1][1]);
+    pk.w[3] = packBf16(p[1][2], p[1][3]);
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      o[d] *= alpha;
+      o[d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(asBf16x8(vf[d]), asBf16x8(pk), o[d], 0, 0, 0);
+    }
+  }
+
+  if (g == 0) {
+    sm[wave][r] = m_run;
+    sl[wave][r] = l_run;
+  }
+#pragma unroll
+  for (int d = 0; d < 4; ++d)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) so[wave][d * 16 + 4 * g + i][r] = o[d][i];
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < group * kDecD; idx += blockDim.x) {
+    const int hl = idx / kDecD, d = idx % kDecD;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) M = fmaxf(M, sm[w][hl]);
+    float l = 0.f, acc = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float e = sm[w][hl] == -INFINITY ? 0.f : exp2f(sm[w][hl] - M);
+      l += e * sl[w][hl];
+      acc += e * so[w][d][hl];
+    }
+    const int64_t row = static_cast<int64_t>(b) * Hq + kvh * group + hl;
+    const int64_t slot = row * max_splits + blockIdx.x;
+    if (d == 0) {
+      ws_ml[slot * 2] = M;
+      ws_ml[slot * 2 + 1] = l;
+    }
+    ws_o[slot * kDecD + d] = acc;
+  }
+}
+
+// One 64-thread block per (sequence, query head): merges the active splits in split order.
+__device__ void decode_attention_combine_impl(const float* ws_ml, const float* ws_o,
+                                              const void* positions, int pos64, int64_t past,
+                                              uint16_t* out, int Hq, int64_t capacity, int chunk,
+                                              int max_splits) {
+  const int64_t row = blockIdx.x;
+  const int b = static_cast<int>(row / Hq);
+  const int d = threadIdx.x;
+  const int64_t past_b = positions != nullptr ? loadIndex(positions, pos64, b) : past;
+  int64_t L = past_b + 1;
+  if (L > capacity) L = capacity;
+  if (L <= 0) {
+    out[row * kDecD + d] = 0;
+    return;
+  }
+  const int n = static_cast<int>((L + chunk - 1) / chunk);
+  float M = -INFINITY;
+  for (int s = 0; s < n; ++s) M = fmaxf(M, ws_ml[(row * max_splits + s) * 2]);
+  float l = 0.f, acc = 0.f;
+  for (int s = 0; s < n; ++s) {
+    const int64_t slot = row * max_splits + s;
+    const float e = exp2f(ws_ml[slot * 2] - M);
+    l += e * ws_ml[slot * 2 + 1];
+    acc += e * ws_o[slot * kDecD + d];
+  }
+  out[row * kDecD + d] = floatToBf16(acc / l);
+}
+
+}  // namespace
+
+extern "C" __global__ void __launch_bounds__(256)
+    decode_attention_d64(const uint16_t* q, const uint16_t* k_pool, const uint16_t* v_pool,
+                         const int32_t* block_table, const void* positions, int pos64, int64_t past,
+                         float* ws_ml, float* ws_o, int Hq, int Hkv, int64_t block_size,
+                         int64_t max_blocks, int chunk, int max_splits, float scale_log2) {
+  decode_attention_impl(q, k_pool, v_pool, block_table, positions, pos64, past, ws_ml, ws_o, Hq,
+                        Hkv, block_size, max_blocks, chunk, max_splits, scale_log2);
+}
+
+extern "C" __global__ void __launch_bounds__(64)
+    decode_attention_combine_d64(const float* ws_ml, const float* ws_o, const void* positions,
+                                 int pos64, int64_t past, uint16_t* out, int Hq, int64_t capacity,
+                                 int chunk, int max_splits) {
+  decode_attention_combine_impl(ws_ml, ws_o, positions, pos64, past, out, Hq, capacity, chunk,
+                                max_splits);
+}

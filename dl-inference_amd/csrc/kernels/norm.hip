@@ -34,7 +34,7 @@ __device__ void rms_norm_impl(const void* x, const void* weight, void* out, int6
         sq += e * e;
       }
     }
-    const float inv = rsqrtf(blockSum(sq, scratch) / static_cast<float>(hidden) + eps);
+    const float inv = 1.0f / sqrtf(blockSum(sq, scratch) / static_cast<float>(hidden) + eps);
     if (cached) {
 #pragma unroll
       for (int j = 0; j < kPer; ++j) {

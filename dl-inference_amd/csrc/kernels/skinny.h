@@ -8,7 +8,8 @@
 //   - Its kWaves waves split that slice further, each walking 64-column steps: per step a lane
 //     loads two 16-byte runs of one weight row, so every wave-wide load pair covers 16 rows x
 //     128 contiguous bytes (whole cache lines, each byte fetched once).
-//   - x fragments are read straight from global memory (x is small and stays in L2).
+//   - x fragments come from global memory (x is small and stays in L2) or from an LDS copy
+//     (used when a prologue has produced x inside the workgroup, e.g. RMSNorm).
 //   - MFMA v_mfma_f32_16x16x32_bf16: A = 16 weight rows x 32 k, B = 32 k x 16 batch rows.
 //     Lane l holds A[l % 16][(l / 16) * 8 + j] and B[(l / 16) * 8 + j][l % 16], j < 8, and
 //     receives D[(l / 16) * 4 + i][l % 16], i < 4. A and B use the same k order, so the
@@ -39,6 +40,16 @@ __device__ __forceinline__ U128 zero16() {
   return z;
 }
 
+// Where the B operand (the skinny activation x) is read from.
+struct XGlobal {
+  const uint16_t* x;  // [M, K] row-major
+  int64_t stride;     // elements between rows (K)
+};
+struct XLds {
+  const uint16_t* x;  // LDS copy [16 * MB rows][stride], rows >= M are zero
+  int stride;
+};
+
 template <int NF, int MB, int kWaves>
 struct SkinnyCore {
   static constexpr int kTileN = 16 * NF;
@@ -46,13 +57,23 @@ struct SkinnyCore {
   // LDS floats needed by run(): one partial tile per wave.
   static constexpr int kLdsFloats = kWaves * kTileN * kTileM;
 
+  template <typename XSrc>
+  __device__ static U128 loadX(const XSrc& xs, int b, int r, int g, int M, int64_t k) {
+    const int m = b * 16 + r;
+    if constexpr (__is_same(XSrc, XLds)) {
+      return load16(xs.x + m * xs.stride + k + g * 8);
+    } else {
+      return m < M ? load16(xs.x + m * xs.stride + k + g * 8) : zero16();
+    }
+  }
+
   // Accumulates this block's share of the tile and leaves the reduced tile in lds[0 .. tile).
-  //   w: [N, K] bf16 row-major, x: [M, K] bf16 row-major (rows >= M read as zero)
-  //   n0: first weight row of the tile; rows >= N contribute zero.
+  //   w: [N, K] bf16 row-major; rows >= N contribute zero.
+  //   n0: first weight row of the tile.
   //   step_begin/step_end: range of 64-column steps owned by this block.
-  __device__ static void run(const uint16_t* __restrict__ w, const uint16_t* __restrict__ x,
-                             int64_t N, int64_t K, int M, int64_t n0, int step_begin, int step_end,
-                             float* lds) {
+  template <typename XSrc>
+  __device__ static void run(const uint16_t* __restrict__ w, const XSrc& xs, int64_t N, int64_t K,
+                             int M, int64_t n0, int step_begin, int step_end, float* lds) {
     const int lane = threadIdx.x % kWave;
     const int wave = threadIdx.x / kWave;
     const int r = lane % 16;  // A row / B column within a fragment
@@ -72,20 +93,11 @@ struct SkinnyCore {
       wvalid[f] = n < N;
       wrow[f] = w + (wvalid[f] ? n : 0) * K + g * 8;
     }
-    const uint16_t* xrow[MB];
-    bool xvalid[MB];
-#pragma unroll
-    for (int b = 0; b < MB; ++b) {
-      const int m = b * 16 + r;
-      xvalid[b] = m < M;
-      xrow[b] = x + (xvalid[b] ? m : 0) * K + g * 8;
-    }
 
     constexpr int kUnroll = 4;
     int s = step_begin + wave;
     for (; s + (kUnroll - 1) * kWaves < step_end; s += kUnroll * kWaves) {
       U128 a[kUnroll][NF][2];
-      U128 bx[kUnroll][MB][2];
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) {
         const int64_t k0 = static_cast<int64_t>(s + u * kWaves) * 64;
@@ -94,22 +106,23 @@ struct SkinnyCore {
           a[u][f][0] = wvalid[f] ? load16(wrow[f] + k0) : zero16();
           a[u][f][1] = wvalid[f] ? load16(wrow[f] + k0 + 32) : zero16();
         }
-#pragma unroll
-        for (int b = 0; b < MB; ++b) {
-          bx[u][b][0] = xvalid[b] ? load16(xrow[b] + k0) : zero16();
-          bx[u][b][1] = xvalid[b] ? load16(xrow[b] + k0 + 32) : zero16();
-        }
       }
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u)
+      for (int u = 0; u < kUnroll; ++u) {
+        const int64_t k0 = static_cast<int64_t>(s + u * kWaves) * 64;
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
+        for (int h = 0; h < 2; ++h) {
+          U128 bx[MB];
+#pragma unroll
+          for (int b = 0; b < MB; ++b) bx[b] = loadX(xs, b, r, g, M, k0 + h * 32);
 #pragma unroll
           for (int f = 0; f < NF; ++f)
 #pragma unroll
             for (int b = 0; b < MB; ++b)
               acc[f][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                  asBf16x8(a[u][f][h]), asBf16x8(bx[u][b][h]), acc[f][b], 0, 0, 0);
+                  asBf16x8(a[u][f][h]), asBf16x8(bx[b]), acc[f][b], 0, 0, 0);
+        }
+      }
     }
     for (; s < step_end; s += kWaves) {
       const int64_t k0 = static_cast<int64_t>(s) * 64;
@@ -119,7 +132,7 @@ struct SkinnyCore {
 #pragma unroll
         for (int f = 0; f < NF; ++f) a[f] = wvalid[f] ? load16(wrow[f] + k0 + h * 32) : zero16();
 #pragma unroll
-        for (int b = 0; b < MB; ++b) bx[b] = xvalid[b] ? load16(xrow[b] + k0 + h * 32) : zero16();
+        for (int b = 0; b < MB; ++b) bx[b] = loadX(xs, b, r, g, M, k0 + h * 32);
 #pragma unroll
         for (int f = 0; f < NF; ++f)
 #pragma unroll
@@ -146,5 +159,77 @@ struct SkinnyCore {
     __syncthreads();
   }
 };
+
+// Split-K across workgroups. Every workgroup (tile, split) stores its partial tile to
+// workspace; the last one to arrive for a tile (atomic ticket) sums all partials in split order
+// — independent of arrival order — into lds and returns true; the others return false. The
+// ticket is reset by that last workgroup, so counters are zero again after every launch.
+//   partials: [tiles][splits][tile_elems] fp32, counters: [tiles] uint32 (zero before first use)
+template <int kTileElems>
+__device__ bool splitKReduce(float* lds, float* partials, uint32_t* counters, int tile, int split,
+                             int splits) {
+  if (splits <= 1) return true;
+  float* mine = partials + (static_cast<int64_t>(tile) * splits + split) * kTileElems;
+  for (int idx = threadIdx.x; idx < kTileElems; idx += blockDim.x) mine[idx] = lds[idx];
+  __threadfence();
+  __syncthreads();
+  __shared__ uint32_t ticket;
+  if (threadIdx.x == 0) ticket = atomicAdd(counters + tile, 1u);
+  __syncthreads();
+  if (ticket != static_cast<uint32_t>(splits - 1)) return false;
+  __threadfence();
+  const float* base = partials + static_cast<int64_t>(tile) * splits * kTileElems;
+  for (int idx = threadIdx.x; idx < kTileElems; idx += blockDim.x) {
+    float sum = 0.f;
+    for (int s = 0; s < splits; ++s) sum += base[s * kTileElems + idx];
+    lds[idx] = sum;
+  }
+  if (threadIdx.x == 0) counters[tile] = 0u;
+  __syncthreads();
+  return true;
+}
+
+// RMSNorm prologue: xs[m][0..K) = bf16(x[m] * rsqrt(mean(x[m]^2) + eps) * w) for m < M, zero rows
+// for M <= m < rows. One wave per row at a time; K % 8 == 0.
+__device__ inline void rmsNormRowsToLds(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
+                                        int M, int rows, int K, float eps, uint16_t* xs,
+                                        int stride) {
+  const int lane = threadIdx.x % kWave;
+  const int wave = threadIdx.x / kWave;
+  const int waves = blockDim.x / kWave;
+  const int vecs = K / 8;
+  for (int m = wave; m < rows; m += waves) {
+    uint16_t* dst = xs + m * stride;
+    if (m >= M) {
+      for (int v = lane; v < vecs; v += kWave) *reinterpret_cast<U128*>(dst + v * 8) = zero16();
+      continue;
+    }
+    const uint16_t* src = x + static_cast<int64_t>(m) * K;
+    float sq = 0.f;
+    for (int v = lane; v < vecs; v += kWave) {
+      const U128 raw = load16(src + v * 8);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float lo = bf16ToFloat(raw.w[j] & 0xffffu), hi = bf16ToFloat(raw.w[j] >> 16);
+        sq += lo * lo + hi * hi;
+      }
+    }
+    sq = waveSum(sq);
+    const float inv = 1.0f / sqrtf(sq / static_cast<float>(K) + eps);
+    for (int v = lane; v < vecs; v += kWave) {
+      const U128 raw = load16(src + v * 8);
+      const U128 wv = load16(w + v * 8);
+      U128 out;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float lo = bf16ToFloat(raw.w[j] & 0xffffu) * inv * bf16ToFloat(wv.w[j] & 0xffffu);
+        const float hi = bf16ToFloat(raw.w[j] >> 16) * inv * bf16ToFloat(wv.w[j] >> 16);
+        out.w[j] = static_cast<uint32_t>(floatToBf16(lo)) | (static_cast<uint32_t>(floatToBf16(hi)) << 16);
+      }
+      *reinterpret_cast<U128*>(dst + v * 8) = out;
+    }
+  }
+  __syncthreads();
+}
 
 }  // namespace dk

@@ -1,8 +1,238 @@
-// Fused decode operators (registered next to the reference operators).
+// Fused decode operators (extensions registered next to the reference operators). Each replaces
+// a run of nodes of the reference's exported Qwen2 decoder graph
+// (python/dli_export/export.py:272-446) and keeps that graph's bf16 rounding points:
+//
+//   qkv_rope_append   input_layernorm, q/k/v_proj, reshapes, rotary_embedding, KV append
+//   paged_attention   attention over the already appended paged KV cache (decode)
+//   linear_residual   o_proj + attention_residual, down_proj + mlp_residual
+//   gate_up_silu      post_attention_layernorm, gate_proj, up_proj, act_fn, mul
+//   lm_head_argmax    model.norm, lm_head, greedy argmax
+//   argmax            greedy argmax over the last dim (unfused graphs)
+#include <cmath>
+#include <mutex>
+
 #include "common.h"
 
 namespace dli::plugin {
+namespace {
 
-void registerFusedOps(OperatorRegistry*) {}
+void requireBf16(const Tensor& t, const std::string& op, const std::string& what) {
+  if (t.dtype() != DType::BFloat16) throw std::invalid_argument(op + " " + what + " must be bfloat16");
+}
+
+std::int64_t rowsOf(const Tensor& t) { return product(t.shape(), 0, t.rank() - 1); }
+
+// Zero-initialised device scratch kept across calls (split-K tile counters must start at 0 and
+// are left at 0 by every kernel, so one buffer serves all nodes of an operator type in stream
+// order). Grows when a node needs more.
+class PersistentWorkspace {
+ public:
+  void* get(std::size_t bytes, int device_id) {
+    if (bytes == 0) return nullptr;
+    std::lock_guard<std::mutex> lock(mutex_);
+    if (!buffer_.defined() || buffer_.nbytes() < bytes || buffer_.deviceId() != device_id) {
+      const auto words = static_cast<std::int64_t>((bytes + 3) / 4);
+      buffer_ = Tensor(at::zeros({words}, at::TensorOptions().dtype(at::kInt).device(at::kCUDA, device_id)));
+    }
+    return buffer_.deviceData();
+  }
+
+ private:
+  std::mutex mutex_;
+  Tensor buffer_;
+};
+
+class QkvRopeAppendOp final : public Operator {
+ public:
+  std::string type() const override { return "qkv_rope_append"; }
+  void compute(const std::vector<const Tensor*>& in, const std::vector<Tensor*>& out,
+               const Attributes& attrs, ExecutionContext& ctx) const override {
+    requireArity(in, out, 7, 7, 1, type());
+    requireCudaInputs(in, type());
+    const Tensor &x = *in[0], &nw = *in[1], &w = *in[2], &b = *in[3], &cos = *in[4], &sin = *in[5],
+                 &pos = *in[6];
+    for (const Tensor* t : {&x, &nw, &w, &b}) requireBf16(*t, type(), "hidden/weights");
+    requireFloat(cos, type());
+    requireFloat(sin, type());
+    requireIndex(pos, type(), "positions");
+    const auto hq = attrs.require<std::int64_t>("q_heads");
+    const auto hkv = attrs.require<std::int64_t>("kv_heads");
+    const auto d = attrs.require<std::int64_t>("head_dim");
+    const auto eps = static_cast<float>(attrDouble(attrs, "eps", 1e-6));
+    const auto splits = static_cast<int>(attrs.value_or<std::int64_t>("splits", 1));
+    const std::string& cache_name = attrs.require<std::string>("kv_cache");
+    const std::int64_t hidden = x.shape().back();
+    const std::int64_t m = rowsOf(x);
+    const std::int64_t n = (hq + 2 * hkv) * d;
+    if (w.rank() != 2 || w.dim(0) != n || w.dim(1) != hidden || static_cast<std::int64_t>(b.numel()) != n ||
+        static_cast<std::int64_t>(nw.numel()) != hidden)
+      throw std::invalid_argument("qkv_rope_append weight shapes do not match the attributes");
+    if (cos.rank() != 2 || cos.dim(1) != d / 2 || cos.shape() != sin.shape())
+      throw std::invalid_argument("qkv_rope_append cos/sin must be [max_pos, head_dim/2]");
+    if (static_cast<std::int64_t>(pos.numel()) != m)
+      throw std::invalid_argument("qkv_rope_append positions must have one entry per row");
+    if (ctx.kv_cache == nullptr) throw std::invalid_argument("qkv_rope_append missing KV cache");
+    KVCacheEntry& e = ctx.kv_cache->reserve(cache_name, DType::BFloat16, m, hkv, d, x.deviceId());
+    *out[0] = Tensor::cuda(DType::BFloat16, {m, hq, 1, d}, x.deviceId());
+    const std::size_t ws_bytes = dli_hip_splitk_workspace(n, m, splits);
+    check(dli_hip_qkv_rope_append(
+              ptr(x), ptr(nw), ptr(w), ptr(b), static_cast<const float*>(ptr(cos)),
+              static_cast<const float*>(ptr(sin)), cos.dim(0), ptr(pos), hipDtype(pos.dtype()),
+              ptr(*out[0]), ptr(e.key), ptr(e.value),
+              static_cast<const std::int32_t*>(ptr(e.block_table)), e.block_size, e.max_blocks, m,
+              hidden, hq, hkv, d, eps, splits, workspace_.get(ws_bytes, x.deviceId()), ws_bytes,
+              ctx.stream),
+          type());
+  }
+
+ private:
+  mutable PersistentWorkspace workspace_;
+};
+
+// Decode attention over a cache entry whose newest token (at positions[b]) is already written.
+class PagedAttentionOp final : public Operator {
+ public:
+  std::string type() const override { return "paged_attention"; }
+  void compute(const std::vector<const Tensor*>& in, const std::vector<Tensor*>& out,
+               const Attributes& attrs, ExecutionContext& ctx) const override {
+    requireArity(in, out, 2, 2, 1, type());
+    requireCudaInputs(in, type());
+    const Tensor& q = *in[0];
+    const Tensor& pos = *in[1];
+    requireFloating(q, type());
+    requireIndex(pos, type(), "positions");
+    if (q.rank() != 4 || q.dim(2) != 1) throw std::invalid_argument("paged_attention expects q [B, H, 1, D]");
+    if (ctx.kv_cache == nullptr) throw std::invalid_argument("paged_attention missing KV cache");
+    const KVCacheEntry* e = ctx.kv_cache->get(attrs.require<std::string>("kv_cache"));
+    if (e == nullptr) throw std::invalid_argument("paged_attention: unknown kv_cache entry");
+    if (e->batch != q.dim(0) || e->head_dim != q.dim(3) || e->key.dtype() != q.dtype())
+      throw std::invalid_argument("paged_attention: q does not match the cache entry");
+    const std::int64_t B = q.dim(0), Hq = q.dim(1), D = q.dim(3);
+    const float scale = static_cast<float>(attrDouble(attrs, "scale", 1.0 / std::sqrt(static_cast<double>(D))));
+    *out[0] = Tensor::cuda(q.dtype(), q.shape(), q.deviceId());
+    const std::size_t ws_bytes = dli_hip_paged_attention_workspace(B, Hq, 1, D, e->capacity());
+    Tensor ws;
+    if (ws_bytes > 0)
+      ws = Tensor::cuda(DType::Float32, {static_cast<std::int64_t>((ws_bytes + 3) / 4)}, q.deviceId());
+    check(dli_hip_paged_attention(hipDtype(q.dtype()), ptr(q), ptr(e->key), ptr(e->value),
+                                  static_cast<const std::int32_t*>(ptr(e->block_table)), ptr(*out[0]),
+                                  B, Hq, e->heads, 1, D, e->block_size, e->max_blocks, 0, ptr(pos),
+                                  hipDtype(pos.dtype()), 1, scale, ws_bytes ? ptr(ws) : nullptr,
+                                  ws_bytes, ctx.stream),
+          type());
+  }
+};
+
+// inputs: x [.., K], w [N, K], residual [.., N] (+ bias [N]); out = residual + bf16(x w^T + b)
+class LinearResidualOp final : public Operator {
+ public:
+  std::string type() const override { return "linear_residual"; }
+  void compute(const std::vector<const Tensor*>& in, const std::vector<Tensor*>& out,
+               const Attributes& attrs, ExecutionContext& ctx) const override {
+    requireArity(in, out, 3, 4, 1, type());
+    requireCudaInputs(in, type());
+    for (const Tensor* t : in) requireBf16(*t, type(), "inputs");
+    const Tensor &x = *in[0], &w = *in[1], &res = *in[2];
+    const std::int64_t k = x.shape().back(), m = rowsOf(x);
+    if (w.rank() != 2 || w.dim(1) != k) throw std::invalid_argument("linear_residual weight shape mismatch");
+    const std::int64_t n = w.dim(0);
+    if (rowsOf(res) != m || res.shape().back() != n)
+      throw std::invalid_argument("linear_residual residual shape mismatch");
+    if (in.size() == 4 && static_cast<std::int64_t>(in[3]->numel()) != n)
+      throw std::invalid_argument("linear_residual bias size mismatch");
+    const auto splits = static_cast<int>(attrs.value_or<std::int64_t>("splits", 1));
+    *out[0] = Tensor::cuda(DType::BFloat16, res.shape(), x.deviceId());
+    const std::size_t ws_bytes = dli_hip_splitk_workspace(n, m, splits);
+    check(dli_hip_linear_residual(ptr(x), ptr(w), in.size() == 4 ? ptr(*in[3]) : nullptr, ptr(res),
+                                  ptr(*out[0]), m, n, k, splits,
+                                  workspace_.get(ws_bytes, x.deviceId()), ws_bytes, ctx.stream),
+          type());
+  }
+
+ private:
+  mutable PersistentWorkspace workspace_;
+};
+
+// inputs: hidden [.., H], norm_weight [H], w_gate_up [2F, H] (16-row interleaved)
+class GateUpSiluOp final : public Operator {
+ public:
+  std::string type() const override { return "gate_up_silu"; }
+  void compute(const std::vector<const Tensor*>& in, const std::vector<Tensor*>& out,
+               const Attributes& attrs, ExecutionContext& ctx) const override {
+    requireArity(in, out, 3, 3, 1, type());
+    requireCudaInputs(in, type());
+    for (const Tensor* t : in) requireBf16(*t, type(), "inputs");
+    const Tensor &x = *in[0], &nw = *in[1], &w = *in[2];
+    const std::int64_t hidden = x.shape().back(), m = rowsOf(x);
+    if (w.rank() != 2 || w.dim(1) != hidden || w.dim(0) % 2 != 0 ||
+        static_cast<std::int64_t>(nw.numel()) != hidden)
+      throw std::invalid_argument("gate_up_silu weight shapes mismatch");
+    const std::int64_t f = w.dim(0) / 2;
+    const auto eps = static_cast<float>(attrDouble(attrs, "eps", 1e-6));
+    *out[0] = Tensor::cuda(DType::BFloat16, withLast(x.shape(), f), x.deviceId());
+    check(dli_hip_gate_up_silu(ptr(x), ptr(nw), ptr(w), ptr(*out[0]), m, f, hidden, eps, ctx.stream),
+          type());
+  }
+};
+
+// inputs: hidden [B, H], norm_weight [H], w [V, H]; outputs: (logits [B, V],) next_ids int64 [B]
+class LmHeadArgmaxOp final : public Operator {
+ public:
+  std::string type() const override { return "lm_head_argmax"; }
+  void compute(const std::vector<const Tensor*>& in, const std::vector<Tensor*>& out,
+               const Attributes& attrs, ExecutionContext& ctx) const override {
+    if (out.size() != 1 && out.size() != 2) throw std::invalid_argument("lm_head_argmax arity");
+    requireArity(in, out, 3, 3, out.size(), type());
+    requireCudaInputs(in, type());
+    for (const Tensor* t : in) requireBf16(*t, type(), "inputs");
+    const Tensor &x = *in[0], &nw = *in[1], &w = *in[2];
+    const std::int64_t hidden = x.shape().back(), m = rowsOf(x);
+    if (w.rank() != 2 || w.dim(1) != hidden || static_cast<std::int64_t>(nw.numel()) != hidden)
+      throw std::invalid_argument("lm_head_argmax weight shapes mismatch");
+    const std::int64_t vocab = w.dim(0);
+    const auto eps = static_cast<float>(attrDouble(attrs, "eps", 1e-6));
+    const DType logits_dtype = dtypeFromString(attrs.value_or<std::string>("logits_dtype", "float32"));
+    Tensor* logits = out.size() == 2 ? out[0] : nullptr;
+    Tensor* ids = out.back();
+    if (logits != nullptr) *logits = Tensor::cuda(logits_dtype, withLast(x.shape(), vocab), x.deviceId());
+    *ids = Tensor::cuda(DType::Int64, {m}, x.deviceId());
+    const std::size_t ws_bytes = dli_hip_lm_head_argmax_workspace(m, vocab);
+    Tensor ws = Tensor::cuda(DType::Float32, {static_cast<std::int64_t>((ws_bytes + 3) / 4)}, x.deviceId());
+    check(dli_hip_lm_head_argmax(ptr(x), ptr(nw), ptr(w), logits ? ptr(*logits) : nullptr,
+                                 hipDtype(logits_dtype), static_cast<std::int64_t*>(ptr(*ids)), m,
+                                 vocab, hidden, eps, ptr(ws), ws_bytes, ctx.stream),
+          type());
+  }
+};
+
+class ArgmaxOp final : public Operator {
+ public:
+  std::string type() const override { return "argmax"; }
+  void compute(const std::vector<const Tensor*>& in, const std::vector<Tensor*>& out,
+               const Attributes&, ExecutionContext& ctx) const override {
+    requireArity(in, out, 1, 1, 1, type());
+    requireCudaInputs(in, type());
+    requireFloating(*in[0], type());
+    const std::int64_t width = in[0]->shape().back();
+    const std::int64_t rows = width > 0 ? static_cast<std::int64_t>(in[0]->numel()) / width : 0;
+    std::vector<std::int64_t> shape(in[0]->shape().begin(), in[0]->shape().end() - 1);
+    *out[0] = Tensor::cuda(DType::Int64, shape.empty() ? std::vector<std::int64_t>{1} : shape,
+                           in[0]->deviceId());
+    check(dli_hip_argmax(hipDtype(in[0]->dtype()), ptr(*in[0]),
+                         static_cast<std::int64_t*>(ptr(*out[0])), rows, width, ctx.stream),
+          type());
+  }
+};
+
+}  // namespace
+
+void registerFusedOps(OperatorRegistry* registry) {
+  add<QkvRopeAppendOp>(registry);
+  add<PagedAttentionOp>(registry);
+  add<LinearResidualOp>(registry);
+  add<GateUpSiluOp>(registry);
+  add<LmHeadArgmaxOp>(registry);
+  add<ArgmaxOp>(registry);
+}
 
 }  // namespace dli::plugin

@@ -1,0 +1,151 @@
+"""dli.graph.v1 builders for one Qwen2 decode step (one new token per sequence).
+
+reference-style graph (fused=False): the node sequence of the reference exporter
+(python/dli_export/export.py:272-446; 19 nodes per layer) with the extensions a batched decode
+needs — a `positions` input feeding rotary_embedding (5th input) and attention (4th input),
+grouped KV heads, fp32 logits and an `argmax` node.
+
+fused graph (fused=True): 5 nodes per layer on the fused operators of the gfx950 plugin
+(qkv_rope_append, paged_attention, linear_residual, gate_up_silu, linear_residual) and one
+lm_head_argmax node; same rounding points, same tensor names for inputs and outputs.
+"""
+from __future__ import annotations
+
+import json
+
+import torch
+
+import dli
+
+from .config import Qwen2Config
+
+INPUTS = ["input_ids", "positions"]
+OUTPUTS = ["logits", "next_ids"]
+
+
+def _node(nodes, name, op, inputs, outputs, attrs=None):
+    nodes.append({"name": name, "op": op, "inputs": list(inputs), "outputs": list(outputs),
+                  "attrs": attrs or {}})
+
+
+def _reference_nodes(cfg: Qwen2Config, batch: int, nodes: list):
+    h = "hidden_states"
+    q_w = cfg.heads * cfg.head_dim
+    for i in range(cfg.layers):
+        p = f"model.layers.{i}"
+        t = f"layers_{i}"
+        _node(nodes, f"{p}.input_layernorm", "rms_norm", [h, f"{p}.input_layernorm.weight"],
+              [f"{t}_input_norm"], {"eps": cfg.eps})
+        for proj in ("q", "k", "v"):
+            _node(nodes, f"{p}.self_attn.{proj}_proj", "linear",
+                  [f"{t}_input_norm", f"{p}.self_attn.{proj}_proj.weight", f"{p}.self_attn.{proj}_proj.bias"],
+                  [f"{t}_{proj}"])
+        _node(nodes, f"{p}.self_attn.q_reshape", "reshape", [f"{t}_q"], [f"{t}_q_heads"],
+              {"shape": [batch, cfg.heads, 1, cfg.head_dim]})
+        _node(nodes, f"{p}.self_attn.k_reshape", "reshape", [f"{t}_k"], [f"{t}_k_heads"],
+              {"shape": [batch, cfg.kv_heads, 1, cfg.head_dim]})
+        _node(nodes, f"{p}.self_attn.v_reshape", "reshape", [f"{t}_v"], [f"{t}_v_heads"],
+              {"shape": [batch, cfg.kv_heads, 1, cfg.head_dim]})
+        _node(nodes, f"{p}.self_attn.rotary_embedding", "rotary_embedding",
+              [f"{t}_q_heads", f"{t}_k_heads", "rotary_cos", "rotary_sin", "positions"],
+              [f"{t}_q_rotary", f"{t}_k_rotary"])
+        _node(nodes, f"{p}.self_attn.attention", "attention",
+              [f"{t}_q_rotary", f"{t}_k_rotary", f"{t}_v_heads", "positions"], [f"{t}_attention"],
+              {"causal": True, "kv_cache": f"layer_{i}"})
+        _node(nodes, f"{p}.self_attn.merge", "reshape", [f"{t}_attention"], [f"{t}_attention_merged"],
+              {"shape": [batch, q_w]})
+        _node(nodes, f"{p}.self_attn.o_proj", "linear",
+              [f"{t}_attention_merged", f"{p}.self_attn.o_proj.weight"], [f"{t}_attention_proj"])
+        _node(nodes, f"{p}.attention_residual", "add", [h, f"{t}_attention_proj"], [f"{t}_after_attention"])
+        _node(nodes, f"{p}.post_attention_layernorm", "rms_norm",
+              [f"{t}_after_attention", f"{p}.post_attention_layernorm.weight"],
+              [f"{t}_post_attention_norm"], {"eps": cfg.eps})
+        _node(nodes, f"{p}.mlp.gate_proj", "linear",
+              [f"{t}_post_attention_norm", f"{p}.mlp.gate_proj.weight"], [f"{t}_gate"])
+        _node(nodes, f"{p}.mlp.up_proj", "linear",
+              [f"{t}_post_attention_norm", f"{p}.mlp.up_proj.weight"], [f"{t}_up"])
+        _node(nodes, f"{p}.mlp.act_fn", "silu", [f"{t}_gate"], [f"{t}_silu"])
+        _node(nodes, f"{p}.mlp.mul", "mul", [f"{t}_silu", f"{t}_up"], [f"{t}_gated"])
+        _node(nodes, f"{p}.mlp.down_proj", "linear", [f"{t}_gated", f"{p}.mlp.down_proj.weight"],
+              [f"{t}_mlp_down"])
+        _node(nodes, f"{p}.mlp_residual", "add", [f"{t}_after_attention", f"{t}_mlp_down"], [f"{t}_output"])
+        h = f"{t}_output"
+    _node(nodes, "model.norm", "rms_norm", [h, "model.norm.weight"], ["norm_hidden"], {"eps": cfg.eps})
+    _node(nodes, "lm_head", "linear", ["norm_hidden", "lm_head.weight"], ["logits"],
+          {"out_dtype": "float32"})
+    _node(nodes, "greedy", "argmax", ["logits"], ["next_ids"])
+
+
+def _fused_nodes(cfg: Qwen2Config, batch: int, nodes: list, splits: dict, logits_dtype: str):
+    h = "hidden_states"
+    for i in range(cfg.layers):
+        p = f"model.layers.{i}"
+        t = f"layers_{i}"
+        _node(nodes, f"{p}.self_attn.qkv_rope_append", "qkv_rope_append",
+              [h, f"{p}.input_layernorm.weight", f"{p}.self_attn.qkv_proj.weight",
+               f"{p}.self_attn.qkv_proj.bias", "rotary_cos", "rotary_sin", "positions"],
+              [f"{t}_q_rotary"],
+              {"kv_cache": f"layer_{i}", "q_heads": cfg.heads, "kv_heads": cfg.kv_heads,
+               "head_dim": cfg.head_dim, "eps": cfg.eps, "splits": splits.get("qkv", 1)})
+        _node(nodes, f"{p}.self_attn.attention", "paged_attention", [f"{t}_q_rotary", "positions"],
+              [f"{t}_attention"], {"kv_cache": f"layer_{i}"})
+        _node(nodes, f"{p}.self_attn.merge", "reshape", [f"{t}_attention"], [f"{t}_attention_merged"],
+              {"shape": [batch, cfg.heads * cfg.head_dim]})
+        _node(nodes, f"{p}.self_attn.o_proj", "linear_residual",
+              [f"{t}_attention_merged", f"{p}.self_attn.o_proj.weight", h], [f"{t}_after_attention"],
+              {"splits": splits.get("o", 1)})
+        _node(nodes, f"{p}.mlp.gate_up", "gate_up_silu",
+              [f"{t}_after_attention", f"{p}.post_attention_layernorm.weight", f"{p}.mlp.gate_up_proj.weight"],
+              [f"{t}_gated"], {"eps": cfg.eps})
+        _node(nodes, f"{p}.mlp.down_proj", "linear_residual",
+              [f"{t}_gated", f"{p}.mlp.down_proj.weight", f"{t}_after_attention"], [f"{t}_output"],
+              {"splits": splits.get("down", 1)})
+        h = f"{t}_output"
+    _node(nodes, "lm_head", "lm_head_argmax", [h, "model.norm.weight", "lm_head.weight"], OUTPUTS,
+          {"eps": cfg.eps, "logits_dtype": logits_dtype})
+
+
+DEFAULT_SPLITS = {"qkv": 1, "o": 2, "down": 4}
+
+
+def build_decode_graph(cfg: Qwen2Config, batch: int, fused: bool = True,
+                       splits: dict | None = None, logits_dtype: str = "float32") -> "dli.Graph":
+    nodes: list = []
+    _node(nodes, "model.embed_tokens", "embedding", ["input_ids", "model.embed_tokens.weight"],
+          ["hidden_states"])
+    if fused:
+        _fused_nodes(cfg, batch, nodes, splits or DEFAULT_SPLITS, logits_dtype)
+    else:
+        _reference_nodes(cfg, batch, nodes)
+    graph = {"format": "dli.graph.v1", "model_type": "qwen2_decode_fused" if fused else "qwen2_decode",
+             "inputs": INPUTS, "outputs": OUTPUTS, "nodes": nodes}
+    return dli.Graph.from_json(json.dumps(graph))
+
+
+def interleave_gate_up(gate: torch.Tensor, up: torch.Tensor, block: int = 16) -> torch.Tensor:
+    """[F, H] x 2 -> [2F, H]: rows [2*block*i, +block) gate block i, then up block i."""
+    f, hsz = gate.shape
+    g = gate.reshape(f // block, block, hsz)
+    u = up.reshape(f // block, block, hsz)
+    return torch.stack([g, u], dim=1).reshape(2 * f, hsz).contiguous()
+
+
+def pack_fused_weights(cfg: Qwen2Config, weights: dict, drop_unfused: bool = False) -> dict:
+    """Adds the packed tensors the fused graph reads: qkv_proj.{weight,bias} ([q|k|v] rows) and
+    mlp.gate_up_proj.weight (16-row interleave)."""
+    out = dict(weights)
+    for i in range(cfg.layers):
+        p = f"model.layers.{i}"
+        a = f"{p}.self_attn"
+        out[f"{a}.qkv_proj.weight"] = torch.cat(
+            [weights[f"{a}.{x}_proj.weight"] for x in "qkv"], 0).contiguous()
+        out[f"{a}.qkv_proj.bias"] = torch.cat([weights[f"{a}.{x}_proj.bias"] for x in "qkv"], 0).contiguous()
+        out[f"{p}.mlp.gate_up_proj.weight"] = interleave_gate_up(
+            weights[f"{p}.mlp.gate_proj.weight"], weights[f"{p}.mlp.up_proj.weight"])
+        if drop_unfused:
+            for x in "qkv":
+                out.pop(f"{a}.{x}_proj.weight")
+                out.pop(f"{a}.{x}_proj.bias")
+            out.pop(f"{p}.mlp.gate_proj.weight")
+            out.pop(f"{p}.mlp.up_proj.weight")
+    return out
