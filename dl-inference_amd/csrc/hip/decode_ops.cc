@@ -9,9 +9,14 @@ namespace dli::hip {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kTileN = 32;           // weight rows per workgroup (NF = 2)
+constexpr int kTileN = 32;           // weight rows per workgroup of gate_up / lm_head (NF = 2)
+constexpr int kQkvTile = 16;         // weight rows per workgroup of qkv_rope_append (kQkvNF = 1)
+constexpr int kResTile = 16;         // weight rows per workgroup of linear_residual (kResNF = 1)
+constexpr int kLmTilesPerBlock = 8;  // vocab tiles per lm_head workgroup
+constexpr int64_t kMaxNormHidden = 1024;
 constexpr size_t kMaxLds = 160 * 1024;  // gfx950 LDS per workgroup
-constexpr int kDecodeChunk = 256;    // keys per decode-attention workgroup
+constexpr int kDecodeChunk = 512;    // keys per decode-attention workgroup (kChunk)
+constexpr int kMaxDecodeSplits = 32; // kMaxSplits of the combine kernel
 
 struct MbKernels {
   DeviceKernel m1, m2, m4;
@@ -43,16 +48,17 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 size_t alignUp(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
-// Split-K workspace: [counters: tiles x u32, padded to 256 B][partials: tiles x splits x tile fp32]
+// Split-K workspace for 16-row tiles: [counters: tiles x u32, padded to 256 B]
+// [partials: tiles x splits x (16 x tileM) fp32]
 size_t splitWorkspace(int64_t n, int64_t m, int splits) {
   if (splits <= 1) return 0;
-  const int64_t tiles = (n + kTileN - 1) / kTileN;
+  const int64_t tiles = (n + 15) / 16;
   return alignUp(static_cast<size_t>(tiles) * 4, 256) +
-         static_cast<size_t>(tiles) * splits * kTileN * tileM(m) * sizeof(float);
+         static_cast<size_t>(tiles) * splits * 16 * tileM(m) * sizeof(float);
 }
 
-size_t normLds(int64_t m, int64_t k) {
-  return static_cast<size_t>(tileM(m)) * (k + 8) * 2 + 4ull * kTileN * tileM(m) * sizeof(float);
+size_t normLds(int64_t m, int64_t k, int tile_n) {
+  return static_cast<size_t>(tileM(m)) * (k + 8) * 2 + 4ull * tile_n * tileM(m) * sizeof(float);
 }
 
 int checkSkinny(const char* op, int64_t m, int64_t k) {
@@ -94,16 +100,17 @@ int dli_hip_qkv_rope_append(const void* hidden, const void* norm_weight, const v
     return bad(op, "positions (int64/int32 [batch]) are required");
   if (head_dim <= 0 || head_dim % 2 != 0) return bad(op, "head_dim must be even");
   if (kv_heads <= 0 || q_heads <= 0) return bad(op, "head counts must be positive");
-  if ((q_heads * head_dim) % kTileN != 0 || (kv_heads * head_dim) % kTileN != 0)
-    return bad(op, "q and kv widths must be multiples of 32");
+  if ((q_heads * head_dim) % kQkvTile != 0 || (kv_heads * head_dim) % kQkvTile != 0)
+    return bad(op, "q and kv widths must be multiples of 16");
+  if (hidden_size > kMaxNormHidden) return bad(op, "hidden_size above 1024 is not supported");
   if (block_size <= 0 || max_blocks <= 0) return bad(op, "empty cache geometry");
   const int64_t n = (q_heads + 2 * kv_heads) * head_dim;
   if (int rc = checkSplits(op, n, batch, hidden_size, splits, workspace, workspace_bytes)) return rc;
   if (!aligned16(hidden) || !aligned16(w_qkv) || !aligned16(norm_weight))
     return bad(op, "hidden, norm_weight and w_qkv must be 16-byte aligned");
-  const size_t lds = normLds(batch, hidden_size);
+  const size_t lds = normLds(batch, hidden_size, kQkvTile);
   if (lds > kMaxLds) return bad(op, "batch x hidden too large for the LDS prologue");
-  const int64_t tiles = (n + kTileN - 1) / kTileN;
+  const int64_t tiles = (n + kQkvTile - 1) / kQkvTile;
   uint32_t* counters = static_cast<uint32_t*>(workspace);
   float* partials = splits > 1
                         ? reinterpret_cast<float*>(static_cast<char*>(workspace) +
@@ -127,7 +134,7 @@ int dli_hip_linear_residual(const void* x, const void* w, const void* bias, cons
   if (n <= 0) return bad(op, "n must be positive");
   if (int rc = checkSplits(op, n, m, k, splits, workspace, workspace_bytes)) return rc;
   if (!aligned16(x) || !aligned16(w)) return bad(op, "x and w must be 16-byte aligned");
-  const int64_t tiles = (n + kTileN - 1) / kTileN;
+  const int64_t tiles = (n + kResTile - 1) / kResTile;
   uint32_t* counters = static_cast<uint32_t*>(workspace);
   float* partials = splits > 1
                         ? reinterpret_cast<float*>(static_cast<char*>(workspace) +
@@ -144,9 +151,10 @@ int dli_hip_gate_up_silu(const void* hidden, const void* norm_weight, const void
   const char* op = "gate_up_silu";
   if (int rc = checkSkinny(op, m, hidden_size)) return rc;
   if (ffn <= 0 || ffn % 16 != 0) return bad(op, "ffn must be a positive multiple of 16");
+  if (hidden_size > kMaxNormHidden) return bad(op, "hidden_size above 1024 is not supported");
   if (!aligned16(hidden) || !aligned16(w_gate_up) || !aligned16(norm_weight))
     return bad(op, "hidden, norm_weight and w_gate_up must be 16-byte aligned");
-  const size_t lds = normLds(m, hidden_size);
+  const size_t lds = normLds(m, hidden_size, kTileN);
   if (lds > kMaxLds) return bad(op, "batch x hidden too large for the LDS prologue");
   return launch(*k_gate_up.pick(m), {static_cast<unsigned>(ffn / 16)}, {kThreads},
                 static_cast<unsigned>(lds), stream, hidden, norm_weight, w_gate_up, out,
@@ -172,14 +180,16 @@ int dli_hip_lm_head_argmax(const void* hidden, const void* norm_weight, const vo
     return bad(op, "workspace too small");
   if (!aligned16(hidden) || !aligned16(w) || !aligned16(norm_weight))
     return bad(op, "hidden, norm_weight and w must be 16-byte aligned");
-  const size_t lds = normLds(m, hidden_size);
+  if (hidden_size > kMaxNormHidden) return bad(op, "hidden_size above 1024 is not supported");
+  const size_t lds = normLds(m, hidden_size, kTileN);
   if (lds > kMaxLds) return bad(op, "batch x hidden too large for the LDS prologue");
   const int64_t tiles = (vocab + kTileN - 1) / kTileN;
+  const int64_t blocks = (tiles + kLmTilesPerBlock - 1) / kLmTilesPerBlock;
   if (tiles > 0x7fffffff) return bad(op, "too many tiles");
   float* part_val = static_cast<float*>(workspace);
   int32_t* part_idx = reinterpret_cast<int32_t*>(part_val + tiles * m);
   const int logits_f32 = logits_dtype == DLI_F32 ? 1 : 0;
-  if (int rc = launch(*k_lm_head.pick(m), {static_cast<unsigned>(tiles)}, {kThreads},
+  if (int rc = launch(*k_lm_head.pick(m), {static_cast<unsigned>(blocks)}, {kThreads},
                       static_cast<unsigned>(lds), stream, hidden, norm_weight, w, logits,
                       logits_f32, part_val, part_idx, static_cast<int>(m), vocab,
                       static_cast<int>(hidden_size), eps))
@@ -206,6 +216,7 @@ int decodeAttentionFast(int dtype, const void* q, const void* key_pool, const vo
     return 1;
   const int64_t capacity = max_blocks * block_size;
   const int max_splits = static_cast<int>((capacity + kDecodeChunk - 1) / kDecodeChunk);
+  if (max_splits > kMaxDecodeSplits) return 1;
   const size_t need = static_cast<size_t>(batch * q_heads) * max_splits * (2 + 64) * sizeof(float);
   if (workspace == nullptr || workspace_bytes < need) return 1;
   if (batch * kv_heads > 65535) return 1;
@@ -217,13 +228,11 @@ int decodeAttentionFast(int dtype, const void* q, const void* key_pool, const vo
                       {kThreads}, 0, stream, static_cast<const uint16_t*>(q),
                       static_cast<const uint16_t*>(key_pool), static_cast<const uint16_t*>(value_pool),
                       block_table, positions, pos64, past, ws_ml, ws_o, static_cast<int>(q_heads),
-                      static_cast<int>(kv_heads), block_size, max_blocks, kDecodeChunk, max_splits,
-                      scale_log2))
+                      static_cast<int>(kv_heads), block_size, max_blocks, max_splits, scale_log2))
     return rc;
   return launch(k_dec_combine, {static_cast<unsigned>(batch * q_heads)}, {64}, 0, stream,
                 static_cast<const float*>(ws_ml), static_cast<const float*>(ws_o), positions, pos64,
-                past, static_cast<uint16_t*>(out), static_cast<int>(q_heads), capacity, kDecodeChunk,
-                max_splits);
+                past, static_cast<uint16_t*>(out), static_cast<int>(q_heads), capacity, max_splits);
 }
 
 size_t decodeAttentionWorkspace(int64_t batch, int64_t q_heads, int64_t seq_q, int64_t head_dim,

@@ -213,11 +213,16 @@ __device__ __forceinline__ uint32_t packBf16(float lo, float hi) {
   return static_cast<uint32_t>(floatToBf16(lo)) | (static_cast<uint32_t>(floatToBf16(hi)) << 16);
 }
 
+// Keys per workgroup = 4 waves x kSubTiles x 32. All K/V loads of a wave are issued before any
+// MFMA (one memory round trip per workgroup); block ids are wave-uniform loads.
+constexpr int kSubTiles = 4;
+constexpr int kChunk = 4 * kSubTiles * 32;
+
 __device__ void decode_attention_impl(const uint16_t* q, const uint16_t* k_pool,
                                       const uint16_t* v_pool, const int32_t* block_table,
                                       const void* positions, int pos64, int64_t past, float* ws_ml,
                                       float* ws_o, int Hq, int Hkv, int64_t BS, int64_t max_blocks,
-                                      int chunk, int max_splits, float scale_log2) {
+                                      int max_splits, float scale_log2) {
   __shared__ float sm[4][16];
   __shared__ float sl[4][16];
   __shared__ float so[4][kDecD][17];
@@ -229,9 +234,9 @@ __device__ void decode_attention_impl(const uint16_t* q, const uint16_t* k_pool,
   const int64_t past_b = positions != nullptr ? loadIndex(positions, pos64, b) : past;
   int64_t L = past_b + 1;
   if (L > max_blocks * BS) L = max_blocks * BS;
-  const int64_t start = static_cast<int64_t>(blockIdx.x) * chunk;
+  const int64_t start = static_cast<int64_t>(blockIdx.x) * kChunk;
   if (start >= L) return;  // uniform per workgroup
-  const int64_t end = start + chunk < L ? start + chunk : L;
+  const int64_t end = start + kChunk < L ? start + kChunk : L;
 
   U128 qf[2];
   if (r < group) {
@@ -245,53 +250,52 @@ __device__ void decode_attention_impl(const uint16_t* q, const uint16_t* k_pool,
   const int32_t* table = block_table + static_cast<int64_t>(b) * max_blocks;
   const int64_t head_stride = BS * kDecD;  // elements per (block, kv head)
 
+  // issue every load of this wave's sub-tiles
+  U128 kf[kSubTiles][2][2];
+  U128 vf[kSubTiles][4];
+#pragma unroll
+  for (int i = 0; i < kSubTiles; ++i) {
+    const int64_t t0 = start + 32 * (wave + 4 * i);
+    const bool live = t0 < end;
+    const int64_t blk = live ? table[t0 / BS] : 0;  // a 32-key sub-tile sits in one block
+    const uint16_t* kbase = k_pool + (blk * Hkv + kvh) * head_stride + (t0 % BS) * kDecD;
+    const uint16_t* vbase = v_pool + (blk * Hkv + kvh) * head_stride + (t0 % BS);
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      const int off = 8 * (r / 4) + 4 * hf + (r % 4);
+      const bool ok = live && t0 + off < end;
+      kf[i][hf][0] = ok ? load16(kbase + off * kDecD + g * 8) : zero16();
+      kf[i][hf][1] = ok ? load16(kbase + off * kDecD + 32 + g * 8) : zero16();
+    }
+    const bool vok = live && t0 + 8 * g < end;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) vf[i][d] = vok ? load16(vbase + (d * 16 + r) * BS + 8 * g) : zero16();
+  }
+
   float m_run = -INFINITY, l_run = 0.f;
   f32x4 o[4];
 #pragma unroll
   for (int d = 0; d < 4; ++d) o[d] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  for (int64_t t0 = start + wave * 32; t0 < end; t0 += 4 * 32) {
-    U128 kf[2][2];
+#pragma unroll
+  for (int i = 0; i < kSubTiles; ++i) {
+    const int64_t t0 = start + 32 * (wave + 4 * i);
+    if (t0 >= end) break;  // uniform per wave
+    f32x4 sc[2];
 #pragma unroll
     for (int hf = 0; hf < 2; ++hf) {
-      const int64_t tok = t0 + 8 * (r / 4) + 4 * hf + (r % 4);
-      if (tok < end) {
-        const int64_t blk = table[tok / BS];
-        const uint16_t* kp = k_pool + (blk * Hkv + kvh) * head_stride + (tok % BS) * kDecD + g * 8;
-        kf[hf][0] = load16(kp);
-        kf[hf][1] = load16(kp + 32);
-      } else {
-        kf[hf][0] = zero16();
-        kf[hf][1] = zero16();
-      }
-    }
-    U128 vf[4];
-    const int64_t tv = t0 + 8 * g;
-    if (tv < end) {
-      const int64_t blk = table[tv / BS];
-      const uint16_t* vp = v_pool + (blk * Hkv + kvh) * head_stride + (tv % BS);
-#pragma unroll
-      for (int d = 0; d < 4; ++d) vf[d] = load16(vp + (d * 16 + r) * BS);
-    } else {
-#pragma unroll
-      for (int d = 0; d < 4; ++d) vf[d] = zero16();
-    }
-
-    f32x4 s[2];
-#pragma unroll
-    for (int hf = 0; hf < 2; ++hf) {
-      s[hf] = f32x4{0.f, 0.f, 0.f, 0.f};
-      s[hf] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(asBf16x8(kf[hf][0]), asBf16x8(qf[0]), s[hf], 0, 0, 0);
-      s[hf] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(asBf16x8(kf[hf][1]), asBf16x8(qf[1]), s[hf], 0, 0, 0);
+      sc[hf] = f32x4{0.f, 0.f, 0.f, 0.f};
+      sc[hf] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(asBf16x8(kf[i][hf][0]), asBf16x8(qf[0]), sc[hf], 0, 0, 0);
+      sc[hf] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(asBf16x8(kf[i][hf][1]), asBf16x8(qf[1]), sc[hf], 0, 0, 0);
     }
     float mx = -INFINITY;
 #pragma unroll
     for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int64_t tok = t0 + 8 * g + 4 * hf + i;
-        const float v = tok < end ? s[hf][i] * scale_log2 : -INFINITY;
-        s[hf][i] = v;
+      for (int e = 0; e < 4; ++e) {
+        const int64_t tok = t0 + 8 * g + 4 * hf + e;
+        const float v = tok < end ? sc[hf][e] * scale_log2 : -INFINITY;
+        sc[hf][e] = v;
         mx = fmaxf(mx, v);
       }
     mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
@@ -303,23 +307,28 @@ __device__ void decode_attention_impl(const uint16_t* q, const uint16_t* k_pool,
 #pragma unroll
     for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        p[hf][i] = exp2f(s[hf][i] - m_new);
-        sum += p[hf][i];
+      for (int e = 0; e < 4; ++e) {
+        p[hf][e] = exp2f(sc[hf][e] - m_new);
+        sum += p[hf][e];
       }
     sum += __shfl_xor(sum, 16, kWave);
     sum += __shfl_xor(sum, 32, kWave);
     l_run = l_run * alpha + sum;
     m_run = m_new;
-    U128 pk;
-    pk.w[0] = packBf16(p[0][0], p[0][1]);
-    pk.w[1] = packBf16(p[0][2], p[0][3]);
-    pk.w[2] = packBf16(p[1][0], p[1][1]);
-    pk.w[3] = packBf16(p[1][2], p[1][3]);
+    // P in two bf16 terms (hi + lo) so the P*V products carry ~16 significant bits of P.
+    U128 phi, plo;
+#pragma unroll
+    for (int w2 = 0; w2 < 4; ++w2) {
+      const float a0 = p[w2 / 2][(w2 % 2) * 2], a1 = p[w2 / 2][(w2 % 2) * 2 + 1];
+      const uint16_t h0 = floatToBf16(a0), h1 = floatToBf16(a1);
+      phi.w[w2] = static_cast<uint32_t>(h0) | (static_cast<uint32_t>(h1) << 16);
+      plo.w[w2] = packBf16(a0 - bf16ToFloat(h0), a1 - bf16ToFloat(h1));
+    }
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
       o[d] *= alpha;
-      o[d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(asBf16x8(vf[d]), asBf16x8(pk), o[d], 0, 0, 0);
+      o[d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(asBf16x8(vf[i][d]), asBf16x8(phi), o[d], 0, 0, 0);
+      o[d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(asBf16x8(vf[i][d]), asBf16x8(plo), o[d], 0, 0, 0);
     }
   }
 
@@ -330,7 +339,7 @@ __device__ void decode_attention_impl(const uint16_t* q, const uint16_t* k_pool,
 #pragma unroll
   for (int d = 0; d < 4; ++d)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) so[wave][d * 16 + 4 * g + i][r] = o[d][i];
+    for (int e = 0; e < 4; ++e) so[wave][d * 16 + 4 * g + e][r] = o[d][e];
   __syncthreads();
   for (int idx = threadIdx.x; idx < group * kDecD; idx += blockDim.x) {
     const int hl = idx / kDecD, d = idx % kDecD;
@@ -355,9 +364,12 @@ __device__ void decode_attention_impl(const uint16_t* q, const uint16_t* k_pool,
 }
 
 // One 64-thread block per (sequence, query head): merges the active splits in split order.
+// Every load is issued before the reduction (kMaxSplits is a compile-time bound).
+constexpr int kMaxSplits = 32;
+
 __device__ void decode_attention_combine_impl(const float* ws_ml, const float* ws_o,
                                               const void* positions, int pos64, int64_t past,
-                                              uint16_t* out, int Hq, int64_t capacity, int chunk,
+                                              uint16_t* out, int Hq, int64_t capacity,
                                               int max_splits) {
   const int64_t row = blockIdx.x;
   const int b = static_cast<int>(row / Hq);
@@ -369,15 +381,24 @@ __device__ void decode_attention_combine_impl(const float* ws_ml, const float* w
     out[row * kDecD + d] = 0;
     return;
   }
-  const int n = static_cast<int>((L + chunk - 1) / chunk);
-  float M = -INFINITY;
-  for (int s = 0; s < n; ++s) M = fmaxf(M, ws_ml[(row * max_splits + s) * 2]);
-  float l = 0.f, acc = 0.f;
-  for (int s = 0; s < n; ++s) {
+  const int n = static_cast<int>((L + kChunk - 1) / kChunk);
+  float ms[kMaxSplits], ls[kMaxSplits], os[kMaxSplits];
+#pragma unroll
+  for (int s = 0; s < kMaxSplits; ++s) {
     const int64_t slot = row * max_splits + s;
-    const float e = exp2f(ws_ml[slot * 2] - M);
-    l += e * ws_ml[slot * 2 + 1];
-    acc += e * ws_o[slot * kDecD + d];
+    ms[s] = s < n ? ws_ml[slot * 2] : -INFINITY;
+    ls[s] = s < n ? ws_ml[slot * 2 + 1] : 0.f;
+    os[s] = s < n ? ws_o[slot * kDecD + d] : 0.f;
+  }
+  float M = -INFINITY;
+#pragma unroll
+  for (int s = 0; s < kMaxSplits; ++s) M = fmaxf(M, ms[s]);
+  float l = 0.f, acc = 0.f;
+#pragma unroll
+  for (int s = 0; s < kMaxSplits; ++s) {
+    const float e = s < n ? exp2f(ms[s] - M) : 0.f;
+    l += e * ls[s];
+    acc += e * os[s];
   }
   out[row * kDecD + d] = floatToBf16(acc / l);
 }
@@ -388,15 +409,14 @@ extern "C" __global__ void __launch_bounds__(256)
     decode_attention_d64(const uint16_t* q, const uint16_t* k_pool, const uint16_t* v_pool,
                          const int32_t* block_table, const void* positions, int pos64, int64_t past,
                          float* ws_ml, float* ws_o, int Hq, int Hkv, int64_t block_size,
-                         int64_t max_blocks, int chunk, int max_splits, float scale_log2) {
+                         int64_t max_blocks, int max_splits, float scale_log2) {
   decode_attention_impl(q, k_pool, v_pool, block_table, positions, pos64, past, ws_ml, ws_o, Hq,
-                        Hkv, block_size, max_blocks, chunk, max_splits, scale_log2);
+                        Hkv, block_size, max_blocks, max_splits, scale_log2);
 }
 
 extern "C" __global__ void __launch_bounds__(64)
     decode_attention_combine_d64(const float* ws_ml, const float* ws_o, const void* positions,
                                  int pos64, int64_t past, uint16_t* out, int Hq, int64_t capacity,
-                                 int chunk, int max_splits) {
-  decode_attention_combine_impl(ws_ml, ws_o, positions, pos64, past, out, Hq, capacity, chunk,
-                                max_splits);
+                                 int max_splits) {
+  decode_attention_combine_impl(ws_ml, ws_o, positions, pos64, past, out, Hq, capacity, max_splits);
 }

@@ -23,6 +23,10 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
+constexpr int kNormVec = 2;          // RMSNorm prologue: hidden <= 64 lanes * 8 * kNormVec = 1024
+constexpr int kQkvNF = 1;            // qkv_rope_append: 16 weight rows per workgroup
+constexpr int kResNF = 1;            // linear_residual: 16 weight rows per workgroup
+constexpr int kLmTilesPerBlock = 8;  // lm_head_argmax: 8 x 32 vocab rows per workgroup
 
 // Steps [begin, end) of split `split` out of `splits` over `steps` 64-column steps.
 __device__ __forceinline__ void splitRange(int steps, int split, int splits, int& begin, int& end) {
@@ -48,7 +52,7 @@ __device__ void qkv_rope_append_impl(const uint16_t* h, const uint16_t* norm_w, 
                                      uint16_t* q_out, KvCacheArgs kv, int M, int K, int Hq, int Hkv,
                                      int D, float eps, float* partials, uint32_t* counters,
                                      int splits) {
-  using Core = SkinnyCore<2, MB, kWaves>;
+  using Core = SkinnyCore<kQkvNF, MB, kWaves>;
   extern __shared__ __align__(16) unsigned char smem[];
   const int xstride = K + 8;
   uint16_t* xs = reinterpret_cast<uint16_t*>(smem);
@@ -56,7 +60,7 @@ __device__ void qkv_rope_append_impl(const uint16_t* h, const uint16_t* norm_w, 
 
   const int64_t N = static_cast<int64_t>(Hq + 2 * Hkv) * D;
   const int64_t n0 = static_cast<int64_t>(blockIdx.x) * Core::kTileN;
-  rmsNormRowsToLds(h, norm_w, M, Core::kTileM, K, eps, xs, xstride);
+  rmsNormRowsToLds<Core::kTileM / kWaves, kNormVec>(h, norm_w, M, Core::kTileM, K, eps, xs, xstride);
   int sb, se;
   splitRange(K / 64, blockIdx.y, splits, sb, se);
   Core::run(w, XLds{xs, xstride}, N, K, M, n0, sb, se, lds);
@@ -121,7 +125,7 @@ template <int MB>
 __device__ void linear_residual_impl(const uint16_t* x, const uint16_t* w, const uint16_t* bias,
                                      const uint16_t* residual, uint16_t* out, int M, int64_t N,
                                      int K, float* partials, uint32_t* counters, int splits) {
-  using Core = SkinnyCore<2, MB, kWaves>;
+  using Core = SkinnyCore<kResNF, MB, kWaves>;
   __shared__ float lds[Core::kLdsFloats];
   const int64_t n0 = static_cast<int64_t>(blockIdx.x) * Core::kTileN;
   int sb, se;
@@ -150,7 +154,7 @@ __device__ void gate_up_silu_impl(const uint16_t* h, const uint16_t* norm_w, con
   uint16_t* xs = reinterpret_cast<uint16_t*>(smem);
   float* lds = reinterpret_cast<float*>(smem + Core::kTileM * xstride * sizeof(uint16_t));
   const int64_t n0 = static_cast<int64_t>(blockIdx.x) * Core::kTileN;  // rows of w_gu
-  rmsNormRowsToLds(h, norm_w, M, Core::kTileM, K, eps, xs, xstride);
+  rmsNormRowsToLds<Core::kTileM / kWaves, kNormVec>(h, norm_w, M, Core::kTileM, K, eps, xs, xstride);
   Core::run(w_gu, XLds{xs, xstride}, 2 * F, K, M, n0, 0, K / 64, lds);
   const int64_t f0 = static_cast<int64_t>(blockIdx.x) * 16;
   for (int idx = threadIdx.x; idx < 16 * Core::kTileM; idx += blockDim.x) {
@@ -173,33 +177,40 @@ __device__ void lm_head_argmax_impl(const uint16_t* h, const uint16_t* norm_w, c
   const int xstride = K + 8;
   uint16_t* xs = reinterpret_cast<uint16_t*>(smem);
   float* lds = reinterpret_cast<float*>(smem + Core::kTileM * xstride * sizeof(uint16_t));
-  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * Core::kTileN;
-  rmsNormRowsToLds(h, norm_w, M, Core::kTileM, K, eps, xs, xstride);
-  Core::run(w, XLds{xs, xstride}, V, K, M, n0, 0, K / 64, lds);
-  if (logits != nullptr) {
-    for (int idx = threadIdx.x; idx < Core::kTileN * Core::kTileM; idx += blockDim.x) {
-      const int nl = idx / Core::kTileM, m = idx % Core::kTileM;
-      const int64_t n = n0 + nl;
-      if (m >= M || n >= V) continue;
-      if (logits_f32)
-        static_cast<float*>(logits)[m * V + n] = lds[idx];
-      else
-        static_cast<uint16_t*>(logits)[m * V + n] = floatToBf16(lds[idx]);
-    }
-  }
-  // per-row argmax of this tile's fp32 logits (first index among equal maxima)
-  for (int m = threadIdx.x; m < M; m += blockDim.x) {
-    float best = -INFINITY;
-    int32_t arg = static_cast<int32_t>(n0);
-    for (int nl = 0; nl < Core::kTileN && n0 + nl < V; ++nl) {
-      const float v = lds[nl * Core::kTileM + m];
-      if (v > best) {
-        best = v;
-        arg = static_cast<int32_t>(n0 + nl);
+  rmsNormRowsToLds<Core::kTileM / kWaves, kNormVec>(h, norm_w, M, Core::kTileM, K, eps, xs, xstride);
+  const int64_t tiles = (V + Core::kTileN - 1) / Core::kTileN;
+  // kLmTilesPerBlock consecutive vocab tiles per workgroup share one normalized copy of x
+  for (int t = 0; t < kLmTilesPerBlock; ++t) {
+    const int64_t tile = static_cast<int64_t>(blockIdx.x) * kLmTilesPerBlock + t;
+    if (tile >= tiles) break;  // uniform per workgroup
+    const int64_t n0 = tile * Core::kTileN;
+    Core::run(w, XLds{xs, xstride}, V, K, M, n0, 0, K / 64, lds);
+    if (logits != nullptr) {
+      for (int idx = threadIdx.x; idx < Core::kTileN * Core::kTileM; idx += blockDim.x) {
+        const int nl = idx / Core::kTileM, m = idx % Core::kTileM;
+        const int64_t n = n0 + nl;
+        if (m >= M || n >= V) continue;
+        if (logits_f32)
+          static_cast<float*>(logits)[m * V + n] = lds[idx];
+        else
+          static_cast<uint16_t*>(logits)[m * V + n] = floatToBf16(lds[idx]);
       }
     }
-    part_val[static_cast<int64_t>(blockIdx.x) * M + m] = best;
-    part_idx[static_cast<int64_t>(blockIdx.x) * M + m] = arg;
+    // per-row argmax of this tile's fp32 logits (first index among equal maxima)
+    for (int m = threadIdx.x; m < M; m += blockDim.x) {
+      float best = -INFINITY;
+      int32_t arg = static_cast<int32_t>(n0);
+      for (int nl = 0; nl < Core::kTileN && n0 + nl < V; ++nl) {
+        const float v = lds[nl * Core::kTileM + m];
+        if (v > best) {
+          best = v;
+          arg = static_cast<int32_t>(n0 + nl);
+        }
+      }
+      part_val[tile * M + m] = best;
+      part_idx[tile * M + m] = arg;
+    }
+    __syncthreads();  // lds is reused by the next tile
   }
 }
 

@@ -94,52 +94,38 @@ struct SkinnyCore {
       wrow[f] = w + (wvalid[f] ? n : 0) * K + g * 8;
     }
 
+    // Batches of kUnroll steps: every weight and x load of a batch is issued before its MFMAs,
+    // so one batch costs one memory round trip.
     constexpr int kUnroll = 4;
-    int s = step_begin + wave;
-    for (; s + (kUnroll - 1) * kWaves < step_end; s += kUnroll * kWaves) {
+    for (int s0 = step_begin + wave; s0 < step_end; s0 += kUnroll * kWaves) {
       U128 a[kUnroll][NF][2];
+      U128 bx[kUnroll][MB][2];
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) {
-        const int64_t k0 = static_cast<int64_t>(s + u * kWaves) * 64;
+        const int s = s0 + u * kWaves;
+        const bool live = s < step_end;
+        const int64_t k0 = static_cast<int64_t>(live ? s : step_begin) * 64;
 #pragma unroll
         for (int f = 0; f < NF; ++f) {
-          a[u][f][0] = wvalid[f] ? load16(wrow[f] + k0) : zero16();
-          a[u][f][1] = wvalid[f] ? load16(wrow[f] + k0 + 32) : zero16();
+          a[u][f][0] = (live && wvalid[f]) ? load16(wrow[f] + k0) : zero16();
+          a[u][f][1] = (live && wvalid[f]) ? load16(wrow[f] + k0 + 32) : zero16();
+        }
+#pragma unroll
+        for (int b = 0; b < MB; ++b) {
+          bx[u][b][0] = live ? loadX(xs, b, r, g, M, k0) : zero16();
+          bx[u][b][1] = live ? loadX(xs, b, r, g, M, k0 + 32) : zero16();
         }
       }
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        const int64_t k0 = static_cast<int64_t>(s + u * kWaves) * 64;
+      for (int u = 0; u < kUnroll; ++u)
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          U128 bx[MB];
-#pragma unroll
-          for (int b = 0; b < MB; ++b) bx[b] = loadX(xs, b, r, g, M, k0 + h * 32);
+        for (int h = 0; h < 2; ++h)
 #pragma unroll
           for (int f = 0; f < NF; ++f)
 #pragma unroll
             for (int b = 0; b < MB; ++b)
               acc[f][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                  asBf16x8(a[u][f][h]), asBf16x8(bx[b]), acc[f][b], 0, 0, 0);
-        }
-      }
-    }
-    for (; s < step_end; s += kWaves) {
-      const int64_t k0 = static_cast<int64_t>(s) * 64;
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        U128 a[NF], bx[MB];
-#pragma unroll
-        for (int f = 0; f < NF; ++f) a[f] = wvalid[f] ? load16(wrow[f] + k0 + h * 32) : zero16();
-#pragma unroll
-        for (int b = 0; b < MB; ++b) bx[b] = loadX(xs, b, r, g, M, k0 + h * 32);
-#pragma unroll
-        for (int f = 0; f < NF; ++f)
-#pragma unroll
-          for (int b = 0; b < MB; ++b)
-            acc[f][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(asBf16x8(a[f]), asBf16x8(bx[b]),
-                                                                acc[f][b], 0, 0, 0);
-      }
+                  asBf16x8(a[u][f][h]), asBf16x8(bx[u][b][h]), acc[f][b], 0, 0, 0);
     }
 
     // Partial tiles -> LDS [wave][n][m], then a fixed-order sum over waves into lds[0..tile).
@@ -190,7 +176,10 @@ __device__ bool splitKReduce(float* lds, float* partials, uint32_t* counters, in
 }
 
 // RMSNorm prologue: xs[m][0..K) = bf16(x[m] * rsqrt(mean(x[m]^2) + eps) * w) for m < M, zero rows
-// for M <= m < rows. One wave per row at a time; K % 8 == 0.
+// for M <= m < rows. Wave w owns rows w, w + waves, ...; each lane holds up to kVec 16-byte
+// pieces of every owned row in registers, so a row is read once and all rows of a wave are in
+// flight together. Requires K % 8 == 0 and K <= 64 * 8 * kVec.
+template <int kRowsPerWave, int kVec>
 __device__ inline void rmsNormRowsToLds(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
                                         int M, int rows, int K, float eps, uint16_t* xs,
                                         int stride) {
@@ -198,33 +187,47 @@ __device__ inline void rmsNormRowsToLds(const uint16_t* __restrict__ x, const ui
   const int wave = threadIdx.x / kWave;
   const int waves = blockDim.x / kWave;
   const int vecs = K / 8;
-  for (int m = wave; m < rows; m += waves) {
-    uint16_t* dst = xs + m * stride;
-    if (m >= M) {
-      for (int v = lane; v < vecs; v += kWave) *reinterpret_cast<U128*>(dst + v * 8) = zero16();
-      continue;
-    }
-    const uint16_t* src = x + static_cast<int64_t>(m) * K;
-    float sq = 0.f;
-    for (int v = lane; v < vecs; v += kWave) {
-      const U128 raw = load16(src + v * 8);
+  U128 raw[kRowsPerWave][kVec];
+  U128 wv[kVec];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float lo = bf16ToFloat(raw.w[j] & 0xffffu), hi = bf16ToFloat(raw.w[j] >> 16);
+  for (int j = 0; j < kVec; ++j) {
+    const int v = lane + j * kWave;
+    wv[j] = v < vecs ? load16(w + v * 8) : zero16();
+  }
+#pragma unroll
+  for (int i = 0; i < kRowsPerWave; ++i) {
+    const int m = wave + i * waves;
+#pragma unroll
+    for (int j = 0; j < kVec; ++j) {
+      const int v = lane + j * kWave;
+      raw[i][j] = (m < M && v < vecs) ? load16(x + static_cast<int64_t>(m) * K + v * 8) : zero16();
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < kRowsPerWave; ++i) {
+    const int m = wave + i * waves;
+    if (m >= rows) break;
+    float sq = 0.f;
+#pragma unroll
+    for (int j = 0; j < kVec; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float lo = bf16ToFloat(raw[i][j].w[e] & 0xffffu), hi = bf16ToFloat(raw[i][j].w[e] >> 16);
         sq += lo * lo + hi * hi;
       }
-    }
     sq = waveSum(sq);
-    const float inv = 1.0f / sqrtf(sq / static_cast<float>(K) + eps);
-    for (int v = lane; v < vecs; v += kWave) {
-      const U128 raw = load16(src + v * 8);
-      const U128 wv = load16(w + v * 8);
+    const float inv = m < M ? 1.0f / sqrtf(sq / static_cast<float>(K) + eps) : 0.f;
+    uint16_t* dst = xs + m * stride;
+#pragma unroll
+    for (int j = 0; j < kVec; ++j) {
+      const int v = lane + j * kWave;
+      if (v >= vecs) break;
       U128 out;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float lo = bf16ToFloat(raw.w[j] & 0xffffu) * inv * bf16ToFloat(wv.w[j] & 0xffffu);
-        const float hi = bf16ToFloat(raw.w[j] >> 16) * inv * bf16ToFloat(wv.w[j] >> 16);
-        out.w[j] = static_cast<uint32_t>(floatToBf16(lo)) | (static_cast<uint32_t>(floatToBf16(hi)) << 16);
+      for (int e = 0; e < 4; ++e) {
+        const float lo = bf16ToFloat(raw[i][j].w[e] & 0xffffu) * inv * bf16ToFloat(wv[j].w[e] & 0xffffu);
+        const float hi = bf16ToFloat(raw[i][j].w[e] >> 16) * inv * bf16ToFloat(wv[j].w[e] >> 16);
+        out.w[e] = static_cast<uint32_t>(floatToBf16(lo)) | (static_cast<uint32_t>(floatToBf16(hi)) << 16);
       }
       *reinterpret_cast<U128*>(dst + v * 8) = out;
     }
