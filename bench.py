@@ -36,7 +36,7 @@ def parse():
     ap.add_argument("--layers", type=int, default=None, help="override (for quick local checks)")
     ap.add_argument("--cpu-baseline-steps", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--splits", default="qkv=1,o=2,down=4")
+    ap.add_argument("--splits", default="qkv=1,o=1,down=1")
     ap.add_argument("--eager", action="store_true", help="run the step without graph capture")
     return ap.parse_args()
 

@@ -1,6 +1,7 @@
 // Entry points of the fused decode kernels (csrc/kernels/decode.hip) and the MFMA decode
 // attention (csrc/kernels/attention.hip). Declared in include/dli_hip.h.
 #include <cmath>
+#include <cstdlib>
 #include <string>
 
 #include "runtime.h"
@@ -12,6 +13,7 @@ constexpr int kThreads = 256;
 constexpr int kTileN = 32;           // weight rows per workgroup of gate_up / lm_head (NF = 2)
 constexpr int kQkvTile = 16;         // weight rows per workgroup of qkv_rope_append (kQkvNF = 1)
 constexpr int kResTile = 16;         // weight rows per workgroup of linear_residual (kResNF = 1)
+constexpr int kResWaves = 8;         // waves per linear_residual workgroup
 constexpr int kLmTilesPerBlock = 8;  // vocab tiles per lm_head workgroup
 constexpr int64_t kMaxNormHidden = 1024;
 constexpr size_t kMaxLds = 160 * 1024;  // gfx950 LDS per workgroup
@@ -141,7 +143,7 @@ int dli_hip_linear_residual(const void* x, const void* w, const void* bias, cons
                                                    alignUp(static_cast<size_t>(tiles) * 4, 256))
                         : nullptr;
   return launch(*k_linres.pick(m), {static_cast<unsigned>(tiles), static_cast<unsigned>(splits)},
-                {kThreads}, 0, stream, x, w, bias, residual, out, static_cast<int>(m), n,
+                {kResWaves * 64}, 0, stream, x, w, bias, residual, out, static_cast<int>(m), n,
                 static_cast<int>(k), partials, counters, splits);
 }
 
@@ -203,8 +205,29 @@ int dli_hip_lm_head_argmax(const void* hidden, const void* norm_weight, const vo
 
 namespace dli::hip {
 
-// MFMA decode attention (one query per sequence, bf16, head_dim 64); used by
-// dli_hip_paged_attention when the case fits. Returns 1 when it does not apply.
+// MFMA decode attention (one query per sequence, bf16, head_dim 64, 64-key cache blocks); used
+// by dli_hip_paged_attention when the case fits. Returns 1 when it does not apply.
+//
+// Splits along the keys: enough (sequence, kv head, split) workgroups to cover the 256 CUs, at
+// least kDecWaves cache blocks per split. One split writes the output directly; more splits
+// go through the combine kernel. DLI_ATTN_SPLITS=<n> overrides the choice (tuning).
+namespace {
+constexpr int kDecWaves = 8;
+constexpr int kDecBlock = 64;
+
+int chooseSplits(int64_t pairs, int64_t max_blocks) {
+  static const int forced = [] {
+    const char* v = std::getenv("DLI_ATTN_SPLITS");
+    return v ? std::atoi(v) : 0;
+  }();
+  int64_t splits = forced > 0 ? forced : (256 + pairs - 1) / pairs;
+  const int64_t max_by_blocks = (max_blocks + kDecWaves - 1) / kDecWaves;
+  if (splits > max_by_blocks) splits = max_by_blocks;
+  if (splits > kMaxDecodeSplits) splits = kMaxDecodeSplits;
+  return static_cast<int>(splits < 1 ? 1 : splits);
+}
+}  // namespace
+
 int decodeAttentionFast(int dtype, const void* q, const void* key_pool, const void* value_pool,
                         const int32_t* block_table, void* out, int64_t batch, int64_t q_heads,
                         int64_t kv_heads, int64_t seq_q, int64_t head_dim, int64_t block_size,
@@ -212,34 +235,35 @@ int decodeAttentionFast(int dtype, const void* q, const void* key_pool, const vo
                         int positions_dtype, float scale, void* workspace, size_t workspace_bytes,
                         void* stream) {
   if (dtype != DLI_BF16 || seq_q != 1 || head_dim != 64 || q_heads / kv_heads > 16 ||
-      block_size % 32 != 0 || !aligned16(q))
+      block_size != kDecBlock || !aligned16(q))
     return 1;
-  const int64_t capacity = max_blocks * block_size;
-  const int max_splits = static_cast<int>((capacity + kDecodeChunk - 1) / kDecodeChunk);
-  if (max_splits > kMaxDecodeSplits) return 1;
-  const size_t need = static_cast<size_t>(batch * q_heads) * max_splits * (2 + 64) * sizeof(float);
-  if (workspace == nullptr || workspace_bytes < need) return 1;
   if (batch * kv_heads > 65535) return 1;
+  const int splits = chooseSplits(batch * kv_heads, max_blocks);
+  const int blocks_per_split = static_cast<int>((max_blocks + splits - 1) / splits);
+  const size_t need = static_cast<size_t>(batch * q_heads) * splits * (2 + 64) * sizeof(float);
+  if (splits > 1 && (workspace == nullptr || workspace_bytes < need)) return 1;
   float* ws_ml = static_cast<float*>(workspace);
-  float* ws_o = ws_ml + batch * q_heads * max_splits * 2;
+  float* ws_o = splits > 1 ? ws_ml + batch * q_heads * splits * 2 : nullptr;
   const int pos64 = positions_dtype == DLI_I64 ? 1 : 0;
   const float scale_log2 = scale * 1.4426950408889634f;
-  if (int rc = launch(k_dec_attn, {static_cast<unsigned>(max_splits), static_cast<unsigned>(batch * kv_heads)},
-                      {kThreads}, 0, stream, static_cast<const uint16_t*>(q),
+  if (int rc = launch(k_dec_attn, {static_cast<unsigned>(splits), static_cast<unsigned>(batch * kv_heads)},
+                      {kDecWaves * 64}, 0, stream, static_cast<const uint16_t*>(q),
                       static_cast<const uint16_t*>(key_pool), static_cast<const uint16_t*>(value_pool),
-                      block_table, positions, pos64, past, ws_ml, ws_o, static_cast<int>(q_heads),
-                      static_cast<int>(kv_heads), block_size, max_blocks, max_splits, scale_log2))
+                      block_table, positions, pos64, past, ws_ml, ws_o, static_cast<uint16_t*>(out),
+                      static_cast<int>(q_heads), static_cast<int>(kv_heads), max_blocks,
+                      blocks_per_split, splits, scale_log2))
     return rc;
+  if (splits == 1) return 0;
   return launch(k_dec_combine, {static_cast<unsigned>(batch * q_heads)}, {64}, 0, stream,
                 static_cast<const float*>(ws_ml), static_cast<const float*>(ws_o), positions, pos64,
-                past, static_cast<uint16_t*>(out), static_cast<int>(q_heads), capacity, max_splits);
+                past, static_cast<uint16_t*>(out), static_cast<int>(q_heads),
+                max_blocks * block_size, blocks_per_split * kDecBlock, splits);
 }
 
 size_t decodeAttentionWorkspace(int64_t batch, int64_t q_heads, int64_t seq_q, int64_t head_dim,
                                 int64_t max_tokens) {
   if (seq_q != 1 || head_dim != 64) return 0;
-  const int64_t max_splits = (max_tokens + kDecodeChunk - 1) / kDecodeChunk;
-  return static_cast<size_t>(batch * q_heads * max_splits) * (2 + 64) * sizeof(float);
+  return static_cast<size_t>(batch * q_heads) * kMaxDecodeSplits * (2 + 64) * sizeof(float);
 }
 
 }  // namespace dli::hip

@@ -213,80 +213,62 @@ __device__ __forceinline__ uint32_t packBf16(float lo, float hi) {
   return static_cast<uint32_t>(floatToBf16(lo)) | (static_cast<uint32_t>(floatToBf16(hi)) << 16);
 }
 
-// Keys per workgroup = 4 waves x kSubTiles x 32. All K/V loads of a wave are issued before any
-// MFMA (one memory round trip per workgroup); block ids are wave-uniform loads.
-constexpr int kSubTiles = 4;
-constexpr int kChunk = 4 * kSubTiles * 32;
+// Workgroup = kDecWaves waves over the key range of one split; wave w takes cache blocks
+// w, w + kDecWaves, ... of that range (a whole block of 64 keys = two 32-key MFMA sub-tiles,
+// so every V row segment of a block is consumed by one wave). The next block's K/V loads are
+// issued before the current block is computed (two register buffers).
+constexpr int kDecWaves = 8;
+constexpr int kDecBlock = 64;  // keys per cache block handled by this kernel
 
-__device__ void decode_attention_impl(const uint16_t* q, const uint16_t* k_pool,
-                                      const uint16_t* v_pool, const int32_t* block_table,
-                                      const void* positions, int pos64, int64_t past, float* ws_ml,
-                                      float* ws_o, int Hq, int Hkv, int64_t BS, int64_t max_blocks,
-                                      int max_splits, float scale_log2) {
-  __shared__ float sm[4][16];
-  __shared__ float sl[4][16];
-  __shared__ float so[4][kDecD][17];
-  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
-  const int r = lane % 16, g = lane / 16;
-  const int bk = blockIdx.y;
-  const int b = bk / Hkv, kvh = bk % Hkv;
-  const int group = Hq / Hkv;
-  const int64_t past_b = positions != nullptr ? loadIndex(positions, pos64, b) : past;
-  int64_t L = past_b + 1;
-  if (L > max_blocks * BS) L = max_blocks * BS;
-  const int64_t start = static_cast<int64_t>(blockIdx.x) * kChunk;
-  if (start >= L) return;  // uniform per workgroup
-  const int64_t end = start + kChunk < L ? start + kChunk : L;
+struct KvBlockRegs {
+  U128 k[2][2][2];  // [sub-tile][half][dim half]
+  U128 v[2][4];     // [sub-tile][16-dim group]
+};
 
-  U128 qf[2];
-  if (r < group) {
-    const uint16_t* qp = q + (static_cast<int64_t>(b) * Hq + kvh * group + r) * kDecD + g * 8;
-    qf[0] = load16(qp);
-    qf[1] = load16(qp + 32);
-  } else {
-    qf[0] = zero16();
-    qf[1] = zero16();
-  }
-  const int32_t* table = block_table + static_cast<int64_t>(b) * max_blocks;
-  const int64_t head_stride = BS * kDecD;  // elements per (block, kv head)
-
-  // issue every load of this wave's sub-tiles
-  U128 kf[kSubTiles][2][2];
-  U128 vf[kSubTiles][4];
+__device__ __forceinline__ void loadKvBlock(KvBlockRegs& regs, const uint16_t* k_pool,
+                                            const uint16_t* v_pool, const int32_t* table,
+                                            int64_t blk_index, int64_t end, int Hkv, int kvh,
+                                            int r, int g) {
+  const int64_t t_block = blk_index * kDecBlock;
+  const int64_t blk = table[blk_index];
+  const int64_t head_stride = static_cast<int64_t>(kDecBlock) * kDecD;
+  const uint16_t* kbase = k_pool + (blk * Hkv + kvh) * head_stride;
+  const uint16_t* vbase = v_pool + (blk * Hkv + kvh) * head_stride;
 #pragma unroll
-  for (int i = 0; i < kSubTiles; ++i) {
-    const int64_t t0 = start + 32 * (wave + 4 * i);
-    const bool live = t0 < end;
-    const int64_t blk = live ? table[t0 / BS] : 0;  // a 32-key sub-tile sits in one block
-    const uint16_t* kbase = k_pool + (blk * Hkv + kvh) * head_stride + (t0 % BS) * kDecD;
-    const uint16_t* vbase = v_pool + (blk * Hkv + kvh) * head_stride + (t0 % BS);
+  for (int st = 0; st < 2; ++st) {
 #pragma unroll
     for (int hf = 0; hf < 2; ++hf) {
-      const int off = 8 * (r / 4) + 4 * hf + (r % 4);
-      const bool ok = live && t0 + off < end;
-      kf[i][hf][0] = ok ? load16(kbase + off * kDecD + g * 8) : zero16();
-      kf[i][hf][1] = ok ? load16(kbase + off * kDecD + 32 + g * 8) : zero16();
+      const int off = 32 * st + 8 * (r / 4) + 4 * hf + (r % 4);
+      const bool ok = t_block + off < end;
+      regs.k[st][hf][0] = ok ? load16(kbase + off * kDecD + g * 8) : zero16();
+      regs.k[st][hf][1] = ok ? load16(kbase + off * kDecD + 32 + g * 8) : zero16();
     }
-    const bool vok = live && t0 + 8 * g < end;
+    const bool vok = t_block + 32 * st + 8 * g < end;
 #pragma unroll
-    for (int d = 0; d < 4; ++d) vf[i][d] = vok ? load16(vbase + (d * 16 + r) * BS + 8 * g) : zero16();
+    for (int d = 0; d < 4; ++d)
+      regs.v[st][d] = vok ? load16(vbase + (d * 16 + r) * kDecBlock + 32 * st + 8 * g) : zero16();
   }
+}
 
-  float m_run = -INFINITY, l_run = 0.f;
+struct SoftmaxState {
+  float m = -INFINITY;
+  float l = 0.f;
   f32x4 o[4];
-#pragma unroll
-  for (int d = 0; d < 4; ++d) o[d] = f32x4{0.f, 0.f, 0.f, 0.f};
+};
 
+__device__ __forceinline__ void attendBlock(SoftmaxState& st8, const KvBlockRegs& regs,
+                                            const U128 (&qf)[2], int64_t t_block, int64_t end,
+                                            int g, float scale_log2) {
 #pragma unroll
-  for (int i = 0; i < kSubTiles; ++i) {
-    const int64_t t0 = start + 32 * (wave + 4 * i);
+  for (int st = 0; st < 2; ++st) {
+    const int64_t t0 = t_block + 32 * st;
     if (t0 >= end) break;  // uniform per wave
     f32x4 sc[2];
 #pragma unroll
     for (int hf = 0; hf < 2; ++hf) {
       sc[hf] = f32x4{0.f, 0.f, 0.f, 0.f};
-      sc[hf] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(asBf16x8(kf[i][hf][0]), asBf16x8(qf[0]), sc[hf], 0, 0, 0);
-      sc[hf] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(asBf16x8(kf[i][hf][1]), asBf16x8(qf[1]), sc[hf], 0, 0, 0);
+      sc[hf] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(asBf16x8(regs.k[st][hf][0]), asBf16x8(qf[0]), sc[hf], 0, 0, 0);
+      sc[hf] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(asBf16x8(regs.k[st][hf][1]), asBf16x8(qf[1]), sc[hf], 0, 0, 0);
     }
     float mx = -INFINITY;
 #pragma unroll
@@ -300,8 +282,8 @@ __device__ void decode_attention_impl(const uint16_t* q, const uint16_t* k_pool,
       }
     mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
     mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
-    const float m_new = fmaxf(m_run, mx);
-    const float alpha = exp2f(m_run - m_new);
+    const float m_new = fmaxf(st8.m, mx);
+    const float alpha = exp2f(st8.m - m_new);
     float p[2][4];
     float sum = 0.f;
 #pragma unroll
@@ -313,8 +295,8 @@ __device__ void decode_attention_impl(const uint16_t* q, const uint16_t* k_pool,
       }
     sum += __shfl_xor(sum, 16, kWave);
     sum += __shfl_xor(sum, 32, kWave);
-    l_run = l_run * alpha + sum;
-    m_run = m_new;
+    st8.l = st8.l * alpha + sum;
+    st8.m = m_new;
     // P in two bf16 terms (hi + lo) so the P*V products carry ~16 significant bits of P.
     U128 phi, plo;
 #pragma unroll
@@ -326,34 +308,91 @@ __device__ void decode_attention_impl(const uint16_t* q, const uint16_t* k_pool,
     }
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
-      o[d] *= alpha;
-      o[d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(asBf16x8(vf[i][d]), asBf16x8(phi), o[d], 0, 0, 0);
-      o[d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(asBf16x8(vf[i][d]), asBf16x8(plo), o[d], 0, 0, 0);
+      st8.o[d] *= alpha;
+      st8.o[d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(asBf16x8(regs.v[st][d]), asBf16x8(phi), st8.o[d], 0, 0, 0);
+      st8.o[d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(asBf16x8(regs.v[st][d]), asBf16x8(plo), st8.o[d], 0, 0, 0);
     }
+  }
+}
+
+// grid (splits, batch * kv_heads), kDecWaves * 64 threads. Split s covers cache blocks
+// [s * blocks_per_split, (s + 1) * blocks_per_split). With one split the normalized output
+// is written directly; otherwise (m, l, O) go to workspace for decode_attention_combine_d64.
+__device__ void decode_attention_impl(const uint16_t* q, const uint16_t* k_pool,
+                                      const uint16_t* v_pool, const int32_t* block_table,
+                                      const void* positions, int pos64, int64_t past, float* ws_ml,
+                                      float* ws_o, uint16_t* out, int Hq, int Hkv,
+                                      int64_t max_blocks, int blocks_per_split, int max_splits,
+                                      float scale_log2) {
+  __shared__ float sm[kDecWaves][16];
+  __shared__ float sl[kDecWaves][16];
+  __shared__ float so[kDecWaves][kDecD][17];
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int r = lane % 16, g = lane / 16;
+  const int bk = blockIdx.y;
+  const int b = bk / Hkv, kvh = bk % Hkv;
+  const int group = Hq / Hkv;
+  const int64_t past_b = positions != nullptr ? loadIndex(positions, pos64, b) : past;
+  int64_t L = past_b + 1;
+  if (L > max_blocks * kDecBlock) L = max_blocks * kDecBlock;
+  const int64_t first_blk = static_cast<int64_t>(blockIdx.x) * blocks_per_split;
+  if (first_blk * kDecBlock >= L) return;  // uniform per workgroup
+  const int64_t n_live = (L + kDecBlock - 1) / kDecBlock;
+  const int64_t last_blk = first_blk + blocks_per_split < n_live ? first_blk + blocks_per_split : n_live;
+
+  U128 qf[2];
+  if (r < group) {
+    const uint16_t* qp = q + (static_cast<int64_t>(b) * Hq + kvh * group + r) * kDecD + g * 8;
+    qf[0] = load16(qp);
+    qf[1] = load16(qp + 32);
+  } else {
+    qf[0] = zero16();
+    qf[1] = zero16();
+  }
+  const int32_t* table = block_table + static_cast<int64_t>(b) * max_blocks;
+
+  SoftmaxState st8;
+#pragma unroll
+  for (int d = 0; d < 4; ++d) st8.o[d] = f32x4{0.f, 0.f, 0.f, 0.f};
+  KvBlockRegs bufA, bufB;
+  int64_t i = first_blk + wave;
+  if (i < last_blk) loadKvBlock(bufA, k_pool, v_pool, table, i, L, Hkv, kvh, r, g);
+  for (; i < last_blk; i += 2 * kDecWaves) {
+    const int64_t j = i + kDecWaves;
+    if (j < last_blk) loadKvBlock(bufB, k_pool, v_pool, table, j, L, Hkv, kvh, r, g);
+    attendBlock(st8, bufA, qf, i * kDecBlock, L, g, scale_log2);
+    if (j >= last_blk) break;
+    const int64_t k2 = j + kDecWaves;
+    if (k2 < last_blk) loadKvBlock(bufA, k_pool, v_pool, table, k2, L, Hkv, kvh, r, g);
+    attendBlock(st8, bufB, qf, j * kDecBlock, L, g, scale_log2);
   }
 
   if (g == 0) {
-    sm[wave][r] = m_run;
-    sl[wave][r] = l_run;
+    sm[wave][r] = st8.m;
+    sl[wave][r] = st8.l;
   }
 #pragma unroll
   for (int d = 0; d < 4; ++d)
 #pragma unroll
-    for (int e = 0; e < 4; ++e) so[wave][d * 16 + 4 * g + e][r] = o[d][e];
+    for (int e = 0; e < 4; ++e) so[wave][d * 16 + 4 * g + e][r] = st8.o[d][e];
   __syncthreads();
   for (int idx = threadIdx.x; idx < group * kDecD; idx += blockDim.x) {
     const int hl = idx / kDecD, d = idx % kDecD;
     float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) M = fmaxf(M, sm[w][hl]);
+    for (int w = 0; w < kDecWaves; ++w) M = fmaxf(M, sm[w][hl]);
     float l = 0.f, acc = 0.f;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
+    for (int w = 0; w < kDecWaves; ++w) {
       const float e = sm[w][hl] == -INFINITY ? 0.f : exp2f(sm[w][hl] - M);
       l += e * sl[w][hl];
       acc += e * so[w][d][hl];
     }
     const int64_t row = static_cast<int64_t>(b) * Hq + kvh * group + hl;
+    if (max_splits == 1) {
+      out[row * kDecD + d] = floatToBf16(acc / l);
+      continue;
+    }
     const int64_t slot = row * max_splits + blockIdx.x;
     if (d == 0) {
       ws_ml[slot * 2] = M;
@@ -370,7 +409,7 @@ constexpr int kMaxSplits = 32;
 __device__ void decode_attention_combine_impl(const float* ws_ml, const float* ws_o,
                                               const void* positions, int pos64, int64_t past,
                                               uint16_t* out, int Hq, int64_t capacity,
-                                              int max_splits) {
+                                              int split_keys, int max_splits) {
   const int64_t row = blockIdx.x;
   const int b = static_cast<int>(row / Hq);
   const int d = threadIdx.x;
@@ -381,7 +420,7 @@ __device__ void decode_attention_combine_impl(const float* ws_ml, const float* w
     out[row * kDecD + d] = 0;
     return;
   }
-  const int n = static_cast<int>((L + kChunk - 1) / kChunk);
+  const int n = static_cast<int>((L + split_keys - 1) / split_keys);
   float ms[kMaxSplits], ls[kMaxSplits], os[kMaxSplits];
 #pragma unroll
   for (int s = 0; s < kMaxSplits; ++s) {
@@ -405,18 +444,20 @@ __device__ void decode_attention_combine_impl(const float* ws_ml, const float* w
 
 }  // namespace
 
-extern "C" __global__ void __launch_bounds__(256)
+extern "C" __global__ void __launch_bounds__(kDecWaves * 64)
     decode_attention_d64(const uint16_t* q, const uint16_t* k_pool, const uint16_t* v_pool,
                          const int32_t* block_table, const void* positions, int pos64, int64_t past,
-                         float* ws_ml, float* ws_o, int Hq, int Hkv, int64_t block_size,
-                         int64_t max_blocks, int max_splits, float scale_log2) {
-  decode_attention_impl(q, k_pool, v_pool, block_table, positions, pos64, past, ws_ml, ws_o, Hq,
-                        Hkv, block_size, max_blocks, max_splits, scale_log2);
+                         float* ws_ml, float* ws_o, uint16_t* out, int Hq, int Hkv,
+                         int64_t max_blocks, int blocks_per_split, int max_splits,
+                         float scale_log2) {
+  decode_attention_impl(q, k_pool, v_pool, block_table, positions, pos64, past, ws_ml, ws_o, out,
+                        Hq, Hkv, max_blocks, blocks_per_split, max_splits, scale_log2);
 }
 
 extern "C" __global__ void __launch_bounds__(64)
     decode_attention_combine_d64(const float* ws_ml, const float* ws_o, const void* positions,
                                  int pos64, int64_t past, uint16_t* out, int Hq, int64_t capacity,
-                                 int max_splits) {
-  decode_attention_combine_impl(ws_ml, ws_o, positions, pos64, past, out, Hq, capacity, max_splits);
+                                 int split_keys, int max_splits) {
+  decode_attention_combine_impl(ws_ml, ws_o, positions, pos64, past, out, Hq, capacity, split_keys,
+                                max_splits);
 }

@@ -26,6 +26,7 @@ constexpr int kWaves = kThreads / kWave;
 constexpr int kNormVec = 2;          // RMSNorm prologue: hidden <= 64 lanes * 8 * kNormVec = 1024
 constexpr int kQkvNF = 1;            // qkv_rope_append: 16 weight rows per workgroup
 constexpr int kResNF = 1;            // linear_residual: 16 weight rows per workgroup
+constexpr int kResWaves = 8;         // linear_residual: 8 waves split K inside a workgroup
 constexpr int kLmTilesPerBlock = 8;  // lm_head_argmax: 8 x 32 vocab rows per workgroup
 
 // Steps [begin, end) of split `split` out of `splits` over `steps` 64-column steps.
@@ -125,7 +126,7 @@ template <int MB>
 __device__ void linear_residual_impl(const uint16_t* x, const uint16_t* w, const uint16_t* bias,
                                      const uint16_t* residual, uint16_t* out, int M, int64_t N,
                                      int K, float* partials, uint32_t* counters, int splits) {
-  using Core = SkinnyCore<kResNF, MB, kWaves>;
+  using Core = SkinnyCore<kResNF, MB, kResWaves>;
   __shared__ float lds[Core::kLdsFloats];
   const int64_t n0 = static_cast<int64_t>(blockIdx.x) * Core::kTileN;
   int sb, se;
@@ -269,7 +270,7 @@ __device__ void argmax_finalize_impl(const float* part_val, const int32_t* part_
                              KvCacheArgs{k_pool, v_pool, block_table, block_size, max_blocks}, M, \
                              K, Hq, Hkv, D, eps, partials, counters, splits);                    \
   }                                                                                              \
-  extern "C" __global__ void __launch_bounds__(kThreads) linear_residual_m##MB(                  \
+  extern "C" __global__ void __launch_bounds__(kResWaves * 64) linear_residual_m##MB(                  \
       const uint16_t* x, const uint16_t* w, const uint16_t* bias, const uint16_t* residual,      \
       uint16_t* out, int M, int64_t N, int K, float* partials, uint32_t* counters, int splits) { \
     linear_residual_impl<MB>(x, w, bias, residual, out, M, N, K, partials, counters, splits);    \

@@ -105,7 +105,7 @@ def _fused_nodes(cfg: Qwen2Config, batch: int, nodes: list, splits: dict, logits
           {"eps": cfg.eps, "logits_dtype": logits_dtype})
 
 
-DEFAULT_SPLITS = {"qkv": 1, "o": 2, "down": 4}
+DEFAULT_SPLITS = {"qkv": 1, "o": 1, "down": 1}
 
 
 def build_decode_graph(cfg: Qwen2Config, batch: int, fused: bool = True,
