@@ -223,6 +223,9 @@ int chooseSplits(int64_t pairs, int64_t max_blocks) {
   int64_t splits = forced > 0 ? forced : (256 + pairs - 1) / pairs;
   const int64_t max_by_blocks = (max_blocks + kDecWaves - 1) / kDecWaves;
   if (splits > max_by_blocks) splits = max_by_blocks;
+  // each wave keeps the ids of its blocks in one register across the 64 lanes
+  const int64_t min_splits = (max_blocks + kDecWaves * 64 - 1) / (kDecWaves * 64);
+  if (splits < min_splits) splits = min_splits;
   if (splits > kMaxDecodeSplits) splits = kMaxDecodeSplits;
   return static_cast<int>(splits < 1 ? 1 : splits);
 }

@@ -226,11 +226,10 @@ struct KvBlockRegs {
 };
 
 __device__ __forceinline__ void loadKvBlock(KvBlockRegs& regs, const uint16_t* k_pool,
-                                            const uint16_t* v_pool, const int32_t* table,
+                                            const uint16_t* v_pool, int64_t blk,
                                             int64_t blk_index, int64_t end, int Hkv, int kvh,
                                             int r, int g) {
   const int64_t t_block = blk_index * kDecBlock;
-  const int64_t blk = table[blk_index];
   const int64_t head_stride = static_cast<int64_t>(kDecBlock) * kDecD;
   const uint16_t* kbase = k_pool + (blk * Hkv + kvh) * head_stride;
   const uint16_t* vbase = v_pool + (blk * Hkv + kvh) * head_stride;
@@ -332,13 +331,19 @@ __device__ void decode_attention_impl(const uint16_t* q, const uint16_t* k_pool,
   const int bk = blockIdx.y;
   const int b = bk / Hkv, kvh = bk % Hkv;
   const int group = Hq / Hkv;
+  // The sequence length and this wave's cache block ids are independent loads: issue both,
+  // one block id per lane (lane k holds the id of the wave's k-th block).
+  const int64_t first_blk = static_cast<int64_t>(blockIdx.x) * blocks_per_split;
+  const int64_t split_end = first_blk + blocks_per_split < max_blocks ? first_blk + blocks_per_split : max_blocks;
+  const int32_t* table = block_table + static_cast<int64_t>(b) * max_blocks;
+  const int64_t my_blk_index = first_blk + wave + static_cast<int64_t>(lane) * kDecWaves;
+  const int32_t my_blk = (lane < kWave && my_blk_index < split_end) ? table[my_blk_index] : 0;
   const int64_t past_b = positions != nullptr ? loadIndex(positions, pos64, b) : past;
   int64_t L = past_b + 1;
   if (L > max_blocks * kDecBlock) L = max_blocks * kDecBlock;
-  const int64_t first_blk = static_cast<int64_t>(blockIdx.x) * blocks_per_split;
   if (first_blk * kDecBlock >= L) return;  // uniform per workgroup
   const int64_t n_live = (L + kDecBlock - 1) / kDecBlock;
-  const int64_t last_blk = first_blk + blocks_per_split < n_live ? first_blk + blocks_per_split : n_live;
+  const int64_t last_blk = split_end < n_live ? split_end : n_live;
 
   U128 qf[2];
   if (r < group) {
@@ -349,21 +354,21 @@ __device__ void decode_attention_impl(const uint16_t* q, const uint16_t* k_pool,
     qf[0] = zero16();
     qf[1] = zero16();
   }
-  const int32_t* table = block_table + static_cast<int64_t>(b) * max_blocks;
 
   SoftmaxState st8;
 #pragma unroll
   for (int d = 0; d < 4; ++d) st8.o[d] = f32x4{0.f, 0.f, 0.f, 0.f};
   KvBlockRegs bufA, bufB;
+  int k = 0;  // ordinal of the wave's block
   int64_t i = first_blk + wave;
-  if (i < last_blk) loadKvBlock(bufA, k_pool, v_pool, table, i, L, Hkv, kvh, r, g);
-  for (; i < last_blk; i += 2 * kDecWaves) {
+  if (i < last_blk) loadKvBlock(bufA, k_pool, v_pool, __shfl(my_blk, 0, kWave), i, L, Hkv, kvh, r, g);
+  for (; i < last_blk; i += 2 * kDecWaves, k += 2) {
     const int64_t j = i + kDecWaves;
-    if (j < last_blk) loadKvBlock(bufB, k_pool, v_pool, table, j, L, Hkv, kvh, r, g);
+    if (j < last_blk) loadKvBlock(bufB, k_pool, v_pool, __shfl(my_blk, k + 1, kWave), j, L, Hkv, kvh, r, g);
     attendBlock(st8, bufA, qf, i * kDecBlock, L, g, scale_log2);
     if (j >= last_blk) break;
     const int64_t k2 = j + kDecWaves;
-    if (k2 < last_blk) loadKvBlock(bufA, k_pool, v_pool, table, k2, L, Hkv, kvh, r, g);
+    if (k2 < last_blk) loadKvBlock(bufA, k_pool, v_pool, __shfl(my_blk, k + 2, kWave), k2, L, Hkv, kvh, r, g);
     attendBlock(st8, bufB, qf, j * kDecBlock, L, g, scale_log2);
   }
 
@@ -420,14 +425,22 @@ __device__ void decode_attention_combine_impl(const float* ws_ml, const float* w
     out[row * kDecD + d] = 0;
     return;
   }
-  const int n = static_cast<int>((L + split_keys - 1) / split_keys);
   float ms[kMaxSplits], ls[kMaxSplits], os[kMaxSplits];
 #pragma unroll
-  for (int s = 0; s < kMaxSplits; ++s) {
+  for (int s = 0; s < kMaxSplits; ++s) {  // loads do not wait for the length
     const int64_t slot = row * max_splits + s;
-    ms[s] = s < n ? ws_ml[slot * 2] : -INFINITY;
-    ls[s] = s < n ? ws_ml[slot * 2 + 1] : 0.f;
-    os[s] = s < n ? ws_o[slot * kDecD + d] : 0.f;
+    ms[s] = s < max_splits ? ws_ml[slot * 2] : -INFINITY;
+    ls[s] = s < max_splits ? ws_ml[slot * 2 + 1] : 0.f;
+    os[s] = s < max_splits ? ws_o[slot * kDecD + d] : 0.f;
+  }
+  const int n = static_cast<int>((L + split_keys - 1) / split_keys);
+#pragma unroll
+  for (int s = 0; s < kMaxSplits; ++s) {
+    if (s >= n) {  // splits past the sequence wrote nothing this step
+      ms[s] = -INFINITY;
+      ls[s] = 0.f;
+      os[s] = 0.f;
+    }
   }
   float M = -INFINITY;
 #pragma unroll

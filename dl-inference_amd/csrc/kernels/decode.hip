@@ -61,42 +61,68 @@ __device__ void qkv_rope_append_impl(const uint16_t* h, const uint16_t* norm_w, 
 
   const int64_t N = static_cast<int64_t>(Hq + 2 * Hkv) * D;
   const int64_t n0 = static_cast<int64_t>(blockIdx.x) * Core::kTileN;
-  rmsNormRowsToLds<Core::kTileM / kWaves, kNormVec>(h, norm_w, M, Core::kTileM, K, eps, xs, xstride);
-  int sb, se;
-  splitRange(K / 64, blockIdx.y, splits, sb, se);
-  Core::run(w, XLds{xs, xstride}, N, K, M, n0, sb, se, lds);
-  if (!splitKReduce<Core::kTileN * Core::kTileM>(lds, partials, counters, blockIdx.x, blockIdx.y,
-                                                   splits))
-    return;
-
   const int64_t q_rows = static_cast<int64_t>(Hq) * D;
   const int64_t k_rows = static_cast<int64_t>(Hkv) * D;
   const int half = D / 2;
   const int64_t capacity = kv.max_blocks * kv.block_size;
-  for (int idx = threadIdx.x; idx < (Core::kTileN / 2) * Core::kTileM; idx += blockDim.x) {
+
+  // Epilogue operands do not depend on the GEMM: fetch them first (position, then the rotary
+  // coefficients, the bias pair and the cache block of this thread's (pair, row) items).
+  constexpr int kItems = ((Core::kTileN / 2) * Core::kTileM + kThreads - 1) / kThreads;
+  int64_t pos[kItems];
+  float cs[kItems][2], bs[kItems][2];
+  int64_t blk[kItems];
+#pragma unroll
+  for (int it = 0; it < kItems; ++it) {
+    const int idx = threadIdx.x + it * kThreads;
+    const int m = idx % Core::kTileM;
+    pos[it] = (idx < (Core::kTileN / 2) * Core::kTileM && m < M) ? loadIndex(positions, pos64, m) : -1;
+  }
+#pragma unroll
+  for (int it = 0; it < kItems; ++it) {
+    const int idx = threadIdx.x + it * kThreads;
+    const int pair = idx / Core::kTileM, m = idx % Core::kTileM;
+    const int64_t n = n0 + 2 * pair;
+    const bool live = pos[it] >= 0 && n < N;
+    const int64_t local = n < q_rows ? n : (n < q_rows + k_rows ? n - q_rows : n - q_rows - k_rows);
+    const int d = static_cast<int>(local % D);
+    const bool rot = live && n < q_rows + k_rows && pos[it] < max_pos;
+    cs[it][0] = rot ? cos_t[pos[it] * half + d / 2] : 1.f;
+    cs[it][1] = rot ? sin_t[pos[it] * half + d / 2] : 0.f;
+    bs[it][0] = (live && bias != nullptr) ? bf16ToFloat(bias[n]) : 0.f;
+    bs[it][1] = (live && bias != nullptr) ? bf16ToFloat(bias[n + 1]) : 0.f;
+    blk[it] = (live && n >= q_rows && pos[it] < capacity)
+                  ? kv.block_table[m * kv.max_blocks + pos[it] / kv.block_size]
+                  : -1;
+  }
+
+  int sb, se;
+  splitRange(K / 64, blockIdx.y, splits, sb, se);
+  Core::run(w, XLds{xs, xstride}, N, K, M, n0, sb, se, lds, [&] {
+    rmsNormRowsToLds<Core::kTileM / kWaves, kNormVec>(h, norm_w, M, Core::kTileM, K, eps, xs, xstride);
+  });
+  if (!splitKReduce<Core::kTileN * Core::kTileM>(lds, partials, counters, blockIdx.x, blockIdx.y,
+                                                   splits))
+    return;
+
+#pragma unroll
+  for (int it = 0; it < kItems; ++it) {
+    const int idx = threadIdx.x + it * kThreads;
     const int pair = idx / Core::kTileM;
     const int m = idx % Core::kTileM;
     const int64_t n = n0 + 2 * pair;
-    if (m >= M || n >= N) continue;
-    float v0 = lds[(2 * pair) * Core::kTileM + m];
-    float v1 = lds[(2 * pair + 1) * Core::kTileM + m];
-    if (bias != nullptr) {
-      v0 += bf16ToFloat(bias[n]);
-      v1 += bf16ToFloat(bias[n + 1]);
-    }
-    v0 = roundBf16(v0);  // linear output
-    v1 = roundBf16(v1);
-    const int64_t pos = loadIndex(positions, pos64, m);
+    if (pos[it] < 0 || n >= N) continue;
+    // linear output (bias added, rounded), then the rotation in fp32, rounded again
+    float v0 = roundBf16(lds[(2 * pair) * Core::kTileM + m] + bs[it][0]);
+    float v1 = roundBf16(lds[(2 * pair + 1) * Core::kTileM + m] + bs[it][1]);
     const bool is_q = n < q_rows;
     const bool is_k = !is_q && n < q_rows + k_rows;
     const int64_t local = is_q ? n : (is_k ? n - q_rows : n - q_rows - k_rows);
     const int head = static_cast<int>(local / D);
     const int d = static_cast<int>(local % D);
-    if ((is_q || is_k) && pos >= 0 && pos < max_pos) {
-      const float c = cos_t[pos * half + d / 2];
-      const float s = sin_t[pos * half + d / 2];
-      const float r0 = v0 * c - v1 * s;
-      const float r1 = v0 * s + v1 * c;
+    if (is_q || is_k) {
+      const float r0 = v0 * cs[it][0] - v1 * cs[it][1];
+      const float r1 = v0 * cs[it][1] + v1 * cs[it][0];
       v0 = r0;
       v1 = r1;
     }
@@ -107,15 +133,14 @@ __device__ void qkv_rope_append_impl(const uint16_t* h, const uint16_t* norm_w, 
       dst[1] = b1;
       continue;
     }
-    if (pos < 0 || pos >= capacity) continue;
-    const int64_t blk = kv.block_table[m * kv.max_blocks + pos / kv.block_size];
-    const int64_t off = pos % kv.block_size;
+    if (blk[it] < 0) continue;
+    const int64_t off = pos[it] % kv.block_size;
     if (is_k) {
-      uint16_t* dst = kv.k_pool + ((blk * Hkv + head) * kv.block_size + off) * D + d;
+      uint16_t* dst = kv.k_pool + ((blk[it] * Hkv + head) * kv.block_size + off) * D + d;
       dst[0] = b0;
       dst[1] = b1;
     } else {
-      uint16_t* dst = kv.v_pool + ((blk * Hkv + head) * D + d) * kv.block_size + off;
+      uint16_t* dst = kv.v_pool + ((blk[it] * Hkv + head) * D + d) * kv.block_size + off;
       dst[0] = b0;
       dst[kv.block_size] = b1;
     }
@@ -129,20 +154,33 @@ __device__ void linear_residual_impl(const uint16_t* x, const uint16_t* w, const
   using Core = SkinnyCore<kResNF, MB, kResWaves>;
   __shared__ float lds[Core::kLdsFloats];
   const int64_t n0 = static_cast<int64_t>(blockIdx.x) * Core::kTileN;
+  constexpr int kThreadsRes = kResWaves * kWave;
+  constexpr int kItems = (Core::kTileN * Core::kTileM + kThreadsRes - 1) / kThreadsRes;
+  float res[kItems];
+#pragma unroll
+  for (int it = 0; it < kItems; ++it) {  // residual (+ bias) fetched before the weights
+    const int idx = threadIdx.x + it * kThreadsRes;
+    const int nl = idx / Core::kTileM, m = idx % Core::kTileM;
+    const int64_t n = n0 + nl;
+    const bool live = idx < Core::kTileN * Core::kTileM && m < M && n < N;
+    res[it] = live ? bf16ToFloat(residual[m * N + n]) : 0.f;
+  }
   int sb, se;
   splitRange(K / 64, blockIdx.y, splits, sb, se);
   Core::run(w, XGlobal{x, K}, N, K, M, n0, sb, se, lds);
   if (!splitKReduce<Core::kTileN * Core::kTileM>(lds, partials, counters, blockIdx.x, blockIdx.y,
                                                    splits))
     return;
-  for (int idx = threadIdx.x; idx < Core::kTileN * Core::kTileM; idx += blockDim.x) {
+#pragma unroll
+  for (int it = 0; it < kItems; ++it) {
+    const int idx = threadIdx.x + it * kThreadsRes;
     const int nl = idx / Core::kTileM, m = idx % Core::kTileM;
     const int64_t n = n0 + nl;
-    if (m >= M || n >= N) continue;
+    if (idx >= Core::kTileN * Core::kTileM || m >= M || n >= N) continue;
     float y = lds[idx];
     if (bias != nullptr) y += bf16ToFloat(bias[n]);
     y = roundBf16(y);
-    out[m * N + n] = floatToBf16(bf16ToFloat(residual[m * N + n]) + y);
+    out[m * N + n] = floatToBf16(res[it] + y);
   }
 }
 
@@ -155,8 +193,9 @@ __device__ void gate_up_silu_impl(const uint16_t* h, const uint16_t* norm_w, con
   uint16_t* xs = reinterpret_cast<uint16_t*>(smem);
   float* lds = reinterpret_cast<float*>(smem + Core::kTileM * xstride * sizeof(uint16_t));
   const int64_t n0 = static_cast<int64_t>(blockIdx.x) * Core::kTileN;  // rows of w_gu
-  rmsNormRowsToLds<Core::kTileM / kWaves, kNormVec>(h, norm_w, M, Core::kTileM, K, eps, xs, xstride);
-  Core::run(w_gu, XLds{xs, xstride}, 2 * F, K, M, n0, 0, K / 64, lds);
+  Core::run(w_gu, XLds{xs, xstride}, 2 * F, K, M, n0, 0, K / 64, lds, [&] {
+    rmsNormRowsToLds<Core::kTileM / kWaves, kNormVec>(h, norm_w, M, Core::kTileM, K, eps, xs, xstride);
+  });
   const int64_t f0 = static_cast<int64_t>(blockIdx.x) * 16;
   for (int idx = threadIdx.x; idx < 16 * Core::kTileM; idx += blockDim.x) {
     const int j = idx / Core::kTileM, m = idx % Core::kTileM;
@@ -169,49 +208,81 @@ __device__ void gate_up_silu_impl(const uint16_t* h, const uint16_t* norm_w, con
   }
 }
 
+// Multiplies one vocab tile already loaded into `bt`, stores its logits and argmax partials.
+template <int MB, typename Batch>
+__device__ void lmHeadTile(Batch& bt, const XLds& xsrc, float* lds, void* logits, int logits_f32,
+                           float* part_val, int32_t* part_idx, int M, int64_t V, int64_t t,
+                           int steps, int r, int g, int wave) {
+  using Core = SkinnyCore<2, MB, kWaves>;
+  f32x4 acc[2][MB];
+#pragma unroll
+  for (int f = 0; f < 2; ++f)
+#pragma unroll
+    for (int b = 0; b < MB; ++b) acc[f][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+  Core::compute(acc, bt, xsrc, M, wave, steps, r, g);
+  Core::reduce(acc, lds, r, g, wave);
+  const int64_t n0 = t * Core::kTileN;
+  if (logits != nullptr) {
+    for (int idx = threadIdx.x; idx < Core::kTileN * Core::kTileM; idx += blockDim.x) {
+      const int nl = idx / Core::kTileM, m = idx % Core::kTileM;
+      const int64_t n = n0 + nl;
+      if (m >= M || n >= V) continue;
+      if (logits_f32)
+        static_cast<float*>(logits)[m * V + n] = lds[idx];
+      else
+        static_cast<uint16_t*>(logits)[m * V + n] = floatToBf16(lds[idx]);
+    }
+  }
+  // per-row argmax of this tile's fp32 logits (first index among equal maxima)
+  for (int m = threadIdx.x; m < M; m += blockDim.x) {
+    float best = -INFINITY;
+    int32_t arg = static_cast<int32_t>(n0);
+    for (int nl = 0; nl < Core::kTileN && n0 + nl < V; ++nl) {
+      const float v = lds[nl * Core::kTileM + m];
+      if (v > best) {
+        best = v;
+        arg = static_cast<int32_t>(n0 + nl);
+      }
+    }
+    part_val[t * M + m] = best;
+    part_idx[t * M + m] = arg;
+  }
+  __syncthreads();  // lds is reused by the next tile
+}
+
+// Vocab tiles of 32 rows; kLmTilesPerBlock consecutive tiles per workgroup share one normalized
+// copy of x, and tile t + 1's weights stream in while tile t is multiplied. Requires
+// K / 64 <= kUnroll * kWaves (one batch per tile).
 template <int MB>
 __device__ void lm_head_argmax_impl(const uint16_t* h, const uint16_t* norm_w, const uint16_t* w,
                                     void* logits, int logits_f32, float* part_val,
                                     int32_t* part_idx, int M, int64_t V, int K, float eps) {
   using Core = SkinnyCore<2, MB, kWaves>;
+  using Batch = typename Core::template Batch<XLds>;
   extern __shared__ __align__(16) unsigned char smem[];
   const int xstride = K + 8;
   uint16_t* xs = reinterpret_cast<uint16_t*>(smem);
   float* lds = reinterpret_cast<float*>(smem + Core::kTileM * xstride * sizeof(uint16_t));
-  rmsNormRowsToLds<Core::kTileM / kWaves, kNormVec>(h, norm_w, M, Core::kTileM, K, eps, xs, xstride);
+  const XLds xsrc{xs, xstride};
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int r = lane % 16, g = lane / 16;
+  const int steps = K / 64;
   const int64_t tiles = (V + Core::kTileN - 1) / Core::kTileN;
-  // kLmTilesPerBlock consecutive vocab tiles per workgroup share one normalized copy of x
-  for (int t = 0; t < kLmTilesPerBlock; ++t) {
-    const int64_t tile = static_cast<int64_t>(blockIdx.x) * kLmTilesPerBlock + t;
-    if (tile >= tiles) break;  // uniform per workgroup
-    const int64_t n0 = tile * Core::kTileN;
-    Core::run(w, XLds{xs, xstride}, V, K, M, n0, 0, K / 64, lds);
-    if (logits != nullptr) {
-      for (int idx = threadIdx.x; idx < Core::kTileN * Core::kTileM; idx += blockDim.x) {
-        const int nl = idx / Core::kTileM, m = idx % Core::kTileM;
-        const int64_t n = n0 + nl;
-        if (m >= M || n >= V) continue;
-        if (logits_f32)
-          static_cast<float*>(logits)[m * V + n] = lds[idx];
-        else
-          static_cast<uint16_t*>(logits)[m * V + n] = floatToBf16(lds[idx]);
-      }
-    }
-    // per-row argmax of this tile's fp32 logits (first index among equal maxima)
-    for (int m = threadIdx.x; m < M; m += blockDim.x) {
-      float best = -INFINITY;
-      int32_t arg = static_cast<int32_t>(n0);
-      for (int nl = 0; nl < Core::kTileN && n0 + nl < V; ++nl) {
-        const float v = lds[nl * Core::kTileM + m];
-        if (v > best) {
-          best = v;
-          arg = static_cast<int32_t>(n0 + nl);
-        }
-      }
-      part_val[tile * M + m] = best;
-      part_idx[tile * M + m] = arg;
-    }
-    __syncthreads();  // lds is reused by the next tile
+  const int64_t t_first = static_cast<int64_t>(blockIdx.x) * kLmTilesPerBlock;
+  const int64_t t_last = t_first + kLmTilesPerBlock < tiles ? t_first + kLmTilesPerBlock : tiles;
+
+  Batch bufA, bufB;
+  Core::issue(bufA, Core::rows(w, V, K, t_first * Core::kTileN, r, g), xsrc, M, wave, steps, r, g);
+  rmsNormRowsToLds<Core::kTileM / kWaves, kNormVec>(h, norm_w, M, Core::kTileM, K, eps, xs, xstride);
+  for (int64_t t = t_first; t < t_last; t += 2) {
+    if (t + 1 < t_last)
+      Core::issue(bufB, Core::rows(w, V, K, (t + 1) * Core::kTileN, r, g), xsrc, M, wave, steps, r, g);
+    lmHeadTile<MB>(bufA, xsrc, lds, logits, logits_f32, part_val, part_idx, M, V, t, steps, r, g, wave);
+    if (t + 1 >= t_last) break;
+    if (t + 2 < t_last)
+      Core::issue(bufA, Core::rows(w, V, K, (t + 2) * Core::kTileN, r, g), xsrc, M, wave, steps, r, g);
+    lmHeadTile<MB>(bufB, xsrc, lds, logits, logits_f32, part_val, part_idx, M, V, t + 1, steps, r, g,
+                   wave);
   }
 }
 

@@ -54,8 +54,16 @@ template <int NF, int MB, int kWaves>
 struct SkinnyCore {
   static constexpr int kTileN = 16 * NF;
   static constexpr int kTileM = 16 * MB;
-  // LDS floats needed by run(): one partial tile per wave.
+  // LDS floats needed by reduce(): one partial tile per wave.
   static constexpr int kLdsFloats = kWaves * kTileN * kTileM;
+  static constexpr int kUnroll = 4;  // 64-column steps per batch
+
+  // One batch of operands in registers: weights always, x only when it comes from global.
+  template <typename XSrc>
+  struct Batch {
+    U128 a[kUnroll][NF][2];
+    U128 x[kUnroll][MB][2];
+  };
 
   template <typename XSrc>
   __device__ static U128 loadX(const XSrc& xs, int b, int r, int g, int M, int64_t k) {
@@ -67,68 +75,117 @@ struct SkinnyCore {
     }
   }
 
-  // Accumulates this block's share of the tile and leaves the reduced tile in lds[0 .. tile).
-  //   w: [N, K] bf16 row-major; rows >= N contribute zero.
-  //   n0: first weight row of the tile.
-  //   step_begin/step_end: range of 64-column steps owned by this block.
+  struct Rows {
+    const uint16_t* w[NF];
+    bool valid[NF];
+  };
+
+  __device__ static Rows rows(const uint16_t* w, int64_t N, int64_t K, int64_t n0, int r, int g) {
+    Rows rw;
+#pragma unroll
+    for (int f = 0; f < NF; ++f) {
+      const int64_t n = n0 + f * 16 + r;
+      rw.valid[f] = n < N;
+      rw.w[f] = w + (rw.valid[f] ? n : 0) * K + g * 8;
+    }
+    return rw;
+  }
+
+  // Issues the weight loads (and global x loads) of the batch starting at step s0.
   template <typename XSrc>
+  __device__ static void issue(Batch<XSrc>& bt, const Rows& rw, const XSrc& xs, int M, int s0,
+                               int step_end, int r, int g) {
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int s = s0 + u * kWaves;
+      const bool live = s < step_end;
+      const int64_t k0 = static_cast<int64_t>(live ? s : 0) * 64;
+#pragma unroll
+      for (int f = 0; f < NF; ++f) {
+        bt.a[u][f][0] = (live && rw.valid[f]) ? load16(rw.w[f] + k0) : zero16();
+        bt.a[u][f][1] = (live && rw.valid[f]) ? load16(rw.w[f] + k0 + 32) : zero16();
+      }
+      if constexpr (!__is_same(XSrc, XLds)) {
+#pragma unroll
+        for (int b = 0; b < MB; ++b) {
+          bt.x[u][b][0] = live ? loadX(xs, b, r, g, M, k0) : zero16();
+          bt.x[u][b][1] = live ? loadX(xs, b, r, g, M, k0 + 32) : zero16();
+        }
+      }
+    }
+  }
+
+  template <typename XSrc>
+  __device__ static void compute(f32x4 (&acc)[NF][MB], Batch<XSrc>& bt, const XSrc& xs, int M,
+                                 int s0, int step_end, int r, int g) {
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int s = s0 + u * kWaves;
+      if (s >= step_end) break;  // uniform per wave
+      const int64_t k0 = static_cast<int64_t>(s) * 64;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        U128 bx[MB];
+#pragma unroll
+        for (int b = 0; b < MB; ++b) {
+          if constexpr (__is_same(XSrc, XLds))
+            bx[b] = loadX(xs, b, r, g, M, k0 + h * 32);
+          else
+            bx[b] = bt.x[u][b][h];
+        }
+#pragma unroll
+        for (int f = 0; f < NF; ++f)
+#pragma unroll
+          for (int b = 0; b < MB; ++b)
+            acc[f][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(asBf16x8(bt.a[u][f][h]),
+                                                                asBf16x8(bx[b]), acc[f][b], 0, 0, 0);
+      }
+    }
+  }
+
+  // Accumulates steps [step_begin, step_end) of the tile at weight row n0 and leaves the reduced
+  // fp32 tile [kTileN][kTileM] in lds[0 .. tile). Wave w takes steps step_begin + w, + kWaves,
+  // ...; batches are double-buffered (the next batch's loads are in flight while the current one
+  // is multiplied). `prologue` runs once after the first batch's loads are issued (it may fill
+  // the LDS copy of x and must end with __syncthreads()).
+  template <typename XSrc, typename Prologue>
   __device__ static void run(const uint16_t* __restrict__ w, const XSrc& xs, int64_t N, int64_t K,
-                             int M, int64_t n0, int step_begin, int step_end, float* lds) {
+                             int M, int64_t n0, int step_begin, int step_end, float* lds,
+                             Prologue&& prologue) {
     const int lane = threadIdx.x % kWave;
     const int wave = threadIdx.x / kWave;
-    const int r = lane % 16;  // A row / B column within a fragment
-    const int g = lane / 16;  // 8-element k group
-
+    const int r = lane % 16, g = lane / 16;
     f32x4 acc[NF][MB];
 #pragma unroll
     for (int f = 0; f < NF; ++f)
 #pragma unroll
       for (int b = 0; b < MB; ++b) acc[f][b] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    const uint16_t* wrow[NF];
-    bool wvalid[NF];
-#pragma unroll
-    for (int f = 0; f < NF; ++f) {
-      const int64_t n = n0 + f * 16 + r;
-      wvalid[f] = n < N;
-      wrow[f] = w + (wvalid[f] ? n : 0) * K + g * 8;
+    const Rows rw = rows(w, N, K, n0, r, g);
+    constexpr int kStride = kUnroll * kWaves;
+    Batch<XSrc> b0, b1;
+    int s0 = step_begin + wave;
+    issue(b0, rw, xs, M, s0, step_end, r, g);
+    prologue();
+    for (; s0 < step_end; s0 += 2 * kStride) {
+      const int s1 = s0 + kStride;
+      if (s1 < step_end) issue(b1, rw, xs, M, s1, step_end, r, g);
+      compute(acc, b0, xs, M, s0, step_end, r, g);
+      if (s1 >= step_end) break;
+      const int s2 = s1 + kStride;
+      if (s2 < step_end) issue(b0, rw, xs, M, s2, step_end, r, g);
+      compute(acc, b1, xs, M, s1, step_end, r, g);
     }
+    reduce(acc, lds, r, g, wave);
+  }
 
-    // Batches of kUnroll steps: every weight and x load of a batch is issued before its MFMAs,
-    // so one batch costs one memory round trip.
-    constexpr int kUnroll = 4;
-    for (int s0 = step_begin + wave; s0 < step_end; s0 += kUnroll * kWaves) {
-      U128 a[kUnroll][NF][2];
-      U128 bx[kUnroll][MB][2];
-#pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        const int s = s0 + u * kWaves;
-        const bool live = s < step_end;
-        const int64_t k0 = static_cast<int64_t>(live ? s : step_begin) * 64;
-#pragma unroll
-        for (int f = 0; f < NF; ++f) {
-          a[u][f][0] = (live && wvalid[f]) ? load16(wrow[f] + k0) : zero16();
-          a[u][f][1] = (live && wvalid[f]) ? load16(wrow[f] + k0 + 32) : zero16();
-        }
-#pragma unroll
-        for (int b = 0; b < MB; ++b) {
-          bx[u][b][0] = live ? loadX(xs, b, r, g, M, k0) : zero16();
-          bx[u][b][1] = live ? loadX(xs, b, r, g, M, k0 + 32) : zero16();
-        }
-      }
-#pragma unroll
-      for (int u = 0; u < kUnroll; ++u)
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-#pragma unroll
-          for (int f = 0; f < NF; ++f)
-#pragma unroll
-            for (int b = 0; b < MB; ++b)
-              acc[f][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                  asBf16x8(a[u][f][h]), asBf16x8(bx[u][b][h]), acc[f][b], 0, 0, 0);
-    }
+  template <typename XSrc>
+  __device__ static void run(const uint16_t* __restrict__ w, const XSrc& xs, int64_t N, int64_t K,
+                             int M, int64_t n0, int step_begin, int step_end, float* lds) {
+    run(w, xs, N, K, M, n0, step_begin, step_end, lds, [] {});
+  }
 
-    // Partial tiles -> LDS [wave][n][m], then a fixed-order sum over waves into lds[0..tile).
+  // Partial tiles -> LDS [wave][n][m], then a fixed-order sum over waves into lds[0..tile).
+  __device__ static void reduce(f32x4 (&acc)[NF][MB], float* lds, int r, int g, int wave) {
     float* mine = lds + wave * kTileN * kTileM;
 #pragma unroll
     for (int f = 0; f < NF; ++f)
