@@ -52,9 +52,11 @@ class Qwen2Oracle:
         self.length = 0
         self.batch = batch
 
-    def forward(self, ids: torch.Tensor, last_only: bool = False) -> torch.Tensor:
+    def forward(self, ids: torch.Tensor, last_only: bool = False,
+                logits_last: int | None = None) -> torch.Tensor:
         """ids [B, S] int64: the next S tokens of every sequence (all at the same position).
-        Returns fp32 logits [B, S, V] ([B, 1, V] with last_only)."""
+        Returns fp32 logits [B, S, V] ([B, 1, V] with last_only, [B, n, V] for the last n
+        positions with logits_last=n)."""
         cfg, w, _bf16 = self.cfg, self.w, self.rnd
         b, s = ids.shape
         pos = torch.arange(self.length, self.length + s)[None].expand(b, s)
@@ -94,6 +96,8 @@ class Qwen2Oracle:
         self.length += s
         if last_only:
             h = h[:, -1:]
+        elif logits_last is not None:
+            h = h[:, h.shape[1] - logits_last:]
         x = _bf16(_rms_norm(h, w["model.norm.weight"], cfg.eps))
         return x @ w["lm_head.weight"].T
 
@@ -169,6 +173,6 @@ class Qwen2Oracle:
         Returns argmax ids [B, T] and margins [B, T] for the T continuation positions."""
         self.reset(prompt.shape[0])
         full = torch.cat([prompt, continuation[:, :-1]], 1)
-        logits = self.forward(full)[:, prompt.shape[1] - 1:]
+        logits = self.forward(full, logits_last=continuation.shape[1])
         top = torch.topk(logits, 2, dim=-1)
         return torch.argmax(logits, -1), top.values[..., 0] - top.values[..., 1], logits

@@ -1,6 +1,7 @@
-"""Qwen2 decode on the GPU through Engine + the gfx950 plugin, against the CPU oracle
-(oracle/qwen2.py) and against each other (fused vs reference-style graph, HIP-graph replay vs
-eager). Greedy token ids must be identical; logits agree to bf16-level tolerance."""
+"""Qwen2 decode on the GPU through Engine + the gfx950 plugin. The fused graph and the
+reference-style graph, and HIP-graph replay and eager runs, must give identical greedy tokens;
+against the CPU oracle (oracle/qwen2.py) the bar is bf16 logit parity, teacher-forced on the
+GPU's own tokens."""
 from __future__ import annotations
 
 import pytest
@@ -62,32 +63,68 @@ def test_capture_replay_equals_eager():
         assert torch.equal(ia, ib)
 
 
-def _check_tokens(cfg, w, batch, prompt_len, steps, rows, seed):
+def _teacher_forced_parity(cfg, w, batch, prompt_len, steps, rows, seed, agree_min):
+    """Free-running greedy decode on the GPU, then the oracle teacher-forced on the GPU's own
+    tokens (one batched CPU pass over prompt + generated tokens), so both score the same
+    prefixes at every step.
+
+    Two bf16 implementations that sum in different orders cannot promise identical tokens or
+    logits: every node output is rounded to bf16, and where the two orders round a value
+    differently the difference propagates through the remaining layers. The size of that noise
+    is measured here rather than assumed: the oracle is run twice, with its bf16 rounding points
+    (the graph's arithmetic) and in plain fp32 (the same model without rounding). Criteria:
+      1. next_ids is exactly argmax(logits) (first index of the maximum) at every step;
+      2. the GPU's logits are no further from the bf16 oracle, and no further from the fp32
+         model, than bf16 rounding itself moves the oracle (relative L2 error per step, ratio
+         bounds below); a wrong index, sign or operand gives errors of order 1 and fails;
+      3. wherever the GPU token differs from the oracle's argmax, the oracle's own gap between
+         the two is within twice that step's max logit error (a near-tie), and the tokens agree
+         on at least `agree_min` of the steps.
+    """
     prompt = _prompt(cfg, batch, prompt_len, seed)
     session = DecodeSession(cfg, w, batch, max_seq_len=prompt_len + steps + 8).capture()
-    got = session.generate(prompt.cuda(), steps).cpu()
-    oracle = Qwen2Oracle(cfg, w)
-    expect, margins = oracle.generate(prompt[rows], steps)
-    for i, r in enumerate(rows):
-        same = got[r] == expect[i]
-        if not bool(same.all()):
-            first = int((~same).nonzero()[0])
-            pytest.fail(f"row {r}: tokens diverge at step {first}: gpu {got[r][first].item()} vs "
-                        f"oracle {expect[i][first].item()} (oracle top-2 margin "
-                        f"{margins[i][first].item():.5f}); min margin before: "
-                        f"{margins[i][:first + 1].min().item():.5f}")
+    got = _run_steps(session, prompt, steps - 1)  # logits after the prompt + steps-1 tokens
+    logits = torch.stack([lg[rows] for lg, _ in got], 1)  # [R, T, V]
+    ids = torch.stack([nx for _, nx in got], 1)  # [B, T]
+    assert torch.equal(ids[rows], torch.argmax(logits, -1)), "next_ids != argmax(logits)"
+    expect, _, ref = Qwen2Oracle(cfg, w).teacher_forced(prompt[rows], ids[rows])
+    _, _, exact = Qwen2Oracle(cfg, w, round_bf16=False).teacher_forced(prompt[rows], ids[rows])
+
+    def rel(a, b):  # [R, T]
+        return (a - b).norm(dim=-1) / b.norm(dim=-1)
+
+    err_bf16, err_fp32, noise = rel(logits, ref), rel(logits, exact), rel(ref, exact)
+    print(f"\nteacher-forced parity, rows {rows}, {logits.shape[1]} steps: relative logit error "
+          f"vs bf16 oracle mean {float(err_bf16.mean()):.3e} max {float(err_bf16.max()):.3e}; "
+          f"vs fp32 model mean {float(err_fp32.mean()):.3e} max {float(err_fp32.max()):.3e}; "
+          f"bf16 oracle vs fp32 model mean {float(noise.mean()):.3e} max {float(noise.max()):.3e}")
+    assert float(err_bf16.mean()) <= 1.25 * float(noise.mean())
+    assert float(err_fp32.mean()) <= 1.25 * float(noise.mean())
+    assert float(err_bf16.max()) <= 1.5 * float(noise.max())
+    assert float(err_fp32.max()) <= 1.5 * float(noise.max())
+    max_err = (logits - ref).abs().amax(-1)
+    agree = ids[rows] == expect
+    chosen = ref.gather(-1, ids[rows][..., None])[..., 0]
+    gap = ref.amax(-1) - chosen  # oracle's preference for its argmax over the GPU token
+    bad = (~agree) & (gap > 2 * max_err)
+    assert not bool(bad.any()), f"token flips outside the noise band at {bad.nonzero().tolist()}"
+    rate = float(agree.float().mean())
+    print(f"token agreement {rate:.3f}, max abs logit error {float(max_err.max()):.3e}")
+    assert rate >= agree_min, f"token agreement {rate:.3f} < {agree_min}"
 
 
-def test_tiny_decode_tokens_match_oracle():
+def test_tiny_decode_teacher_forced_parity():
     cfg = tiny_config()
     w = random_weights(cfg, seed=31, device="cuda")
-    _check_tokens(cfg, w, batch=6, prompt_len=12, steps=24, rows=[0, 3, 5], seed=32)
+    _teacher_forced_parity(cfg, w, batch=6, prompt_len=12, steps=24, rows=[0, 3, 5], seed=32,
+                           agree_min=0.9)
 
 
 @pytest.mark.slow
-def test_qwen2_0_5b_shape_greedy_64_steps_match_oracle():
+def test_qwen2_0_5b_shape_64_steps_teacher_forced_parity():
     """Full Qwen2-0.5B shape, batch 32, 512 random prompt tokens, 64 greedy steps; the oracle
-    replays rows 0, 17 and 31 on the CPU."""
+    scores rows 0, 17 and 31 on the CPU."""
     cfg = QWEN2_0_5B
     w = random_weights(cfg, seed=41, device="cuda")
-    _check_tokens(cfg, w, batch=32, prompt_len=512, steps=64, rows=[0, 17, 31], seed=42)
+    _teacher_forced_parity(cfg, w, batch=32, prompt_len=512, steps=64, rows=[0, 17, 31], seed=42,
+                           agree_min=0.9)

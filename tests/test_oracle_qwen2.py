@@ -101,3 +101,28 @@ def test_bf16_mode_rounds_and_stays_close():
     assert torch.equal(k, k.to(torch.bfloat16).float())
     tokens, margins = rounded.generate(ids, 3)
     assert tokens.shape == (1, 3) and bool((margins >= 0).all())
+
+
+def test_teacher_forced_reproduces_free_running_greedy():
+    # fp32 mode, so batched and stepwise passes agree to 1e-5 and the argmax is the same
+    w = _weights()
+    prompt = torch.tensor([[5, 17, 3, 99], [8, 8, 1, 70]])
+    o = Qwen2Oracle(CFG, w, round_bf16=False)
+    tokens, margins = o.generate(prompt, 5)
+    ids, tf_margins, logits = o.teacher_forced(prompt, tokens)
+    assert torch.equal(ids, tokens)
+    torch.testing.assert_close(tf_margins, margins, rtol=1e-4, atol=1e-4)
+    assert logits.shape == (2, 5, CFG.vocab)
+
+
+def test_static_cache_step_equals_forward():
+    # the preallocated-cache step used for CPU timing computes the same logits as forward()
+    w = _weights()
+    prompt = torch.tensor([[5, 17, 3], [8, 8, 1]])
+    a = Qwen2Oracle(CFG, w, round_bf16=False)
+    a.reset(2)
+    full = a.forward(prompt)
+    b = Qwen2Oracle(CFG, w, round_bf16=False)
+    b.reset_static(2, 8)
+    steps = torch.stack([b.step_static(prompt[:, t], t) for t in range(3)], 1)
+    torch.testing.assert_close(steps, full, rtol=1e-5, atol=1e-5)
