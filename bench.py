@@ -38,7 +38,25 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--splits", default="qkv=1,o=1,down=1")
     ap.add_argument("--eager", action="store_true", help="run the step without graph capture")
+    ap.add_argument("--calibration-copy-mib", type=int, default=0,
+                    help="after timing, copy this many MiB device-to-device 3 times (a plain copy "
+                         "of known size that scales rocprofv3's FETCH_SIZE / WRITE_SIZE)")
     return ap.parse_args()
+
+
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "decode_attention_pmc_qwen2-0.5b_b32_ctx4096.txt")
+
+
+def profiled_traffic():
+    """HBM bytes per decode-attention launch measured by two rocprofv3 --pmc runs (FETCH_SIZE,
+    WRITE_SIZE) scaled by a copy kernel of known size; recorded in the committed profile."""
+    try:
+        for line in open(TRAFFIC_PROFILE):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(float(line.split(":")[1].split()[0]))
+    except OSError:
+        pass
+    return None
 
 
 def step_bytes(cfg, batch, context):
@@ -142,6 +160,14 @@ def main():
     attn_bytes = B * ctx * cfg.kv_heads * cfg.head_dim * 2 * 2 + 2 * B * cfg.heads * cfg.head_dim * 2
     attn_gbs = attn_bytes / (attn_us * 1e-6) / 1e9
 
+    if args.calibration_copy_mib > 0:
+        src = torch.empty(args.calibration_copy_mib << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+
     cpu = None
     if not args.no_cpu_baseline and args.cpu_baseline_steps > 0:
         sys.path.insert(0, ROOT)
@@ -182,7 +208,7 @@ def main():
                    "splits": splits},
         "roofline": {"bound": "hbm", "kernel": "decode attention (decode_attention_d64 + combine)",
                      "achieved": round(attn_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(attn_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(attn_gbs / HBM_PEAK_GBS, 4), "traffic": profiled_traffic(),
                      "avg_us": round(attn_us, 2), "bytes_per_launch": attn_bytes},
         "step_roofline": {"bound": "hbm", "bytes_per_step": total, "achieved": round(step_gbs, 1),
                           "peak": HBM_PEAK_GBS, "unit": "GB/s",
