@@ -36,7 +36,7 @@ def parse():
     ap.add_argument("--layers", type=int, default=None, help="override (for quick local checks)")
     ap.add_argument("--cpu-baseline-steps", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--splits", default="qkv=1,o=1,down=1")
+    ap.add_argument("--splits", default=None, help="split-K per projection, e.g. o=2,down=4")
     ap.add_argument("--eager", action="store_true", help="run the step without graph capture")
     ap.add_argument("--calibration-copy-mib", type=int, default=0,
                     help="after timing, copy this many MiB device-to-device 3 times (a plain copy "
@@ -83,7 +83,11 @@ def main():
 
     cfg = QWEN2_0_5B if args.layers is None else replace(QWEN2_0_5B, layers=args.layers)
     B, ctx = args.batch, args.context
-    splits = {k: int(v) for k, v in (item.split("=") for item in args.splits.split(","))}
+    from dli_qwen2.graph import DEFAULT_SPLITS
+
+    splits = dict(DEFAULT_SPLITS)
+    if args.splits:
+        splits.update({k: int(v) for k, v in (item.split("=") for item in args.splits.split(","))})
     dev = "cuda"
     torch.manual_seed(0)
     weights = random_weights(cfg, seed=0, device=dev)

@@ -11,13 +11,11 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kTileN = 32;           // weight rows per workgroup of gate_up / lm_head (NF = 2)
-constexpr int kQkvTile = 16;         // weight rows per workgroup of qkv_rope_append (kQkvNF = 1)
-constexpr int kResTile = 16;         // weight rows per workgroup of linear_residual (kResNF = 1)
+constexpr int kRowTile = 16;         // weight rows per workgroup of qkv / linear_residual / partial
 constexpr int kResWaves = 8;         // waves per linear_residual workgroup
 constexpr int kLmTilesPerBlock = 8;  // vocab tiles per lm_head workgroup
-constexpr int64_t kMaxNormHidden = 1024;
-constexpr size_t kMaxLds = 160 * 1024;  // gfx950 LDS per workgroup
-constexpr int kDecodeChunk = 512;    // keys per decode-attention workgroup (kChunk)
+constexpr int64_t kMaxNormN = 1024;  // residual_rms_norm: 256 threads x 4 columns
+constexpr int64_t kMaxLmK = 1024;    // lm_head keeps x for K / 64 <= 16 steps in registers
 constexpr int kMaxDecodeSplits = 32; // kMaxSplits of the combine kernel
 
 struct MbKernels {
@@ -34,13 +32,13 @@ struct MbKernels {
 
 MbKernels k_qkv("decode", "qkv_rope_append");
 MbKernels k_linres("decode", "linear_residual");
+MbKernels k_partial("decode", "linear_partial");
 MbKernels k_gate_up("decode", "gate_up_silu");
 MbKernels k_lm_head("decode", "lm_head_argmax");
+DeviceKernel k_res_norm("decode", "residual_rms_norm");
 DeviceKernel k_argmax_final("decode", "argmax_finalize");
 DeviceKernel k_dec_attn("attention", "decode_attention_d64");
 DeviceKernel k_dec_combine("attention", "decode_attention_combine_d64");
-
-int tileM(int64_t m) { return m <= 16 ? 16 : (m <= 32 ? 32 : 64); }
 
 int bad(const char* op, const std::string& what) {
   return fail(DLI_HIP_EINVAL, std::string(op) + ": " + what);
@@ -48,33 +46,31 @@ int bad(const char* op, const std::string& what) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-size_t alignUp(size_t v, size_t a) { return (v + a - 1) / a * a; }
-
-// Split-K workspace for 16-row tiles: [counters: tiles x u32, padded to 256 B]
-// [partials: tiles x splits x (16 x tileM) fp32]
-size_t splitWorkspace(int64_t n, int64_t m, int splits) {
-  if (splits <= 1) return 0;
-  const int64_t tiles = (n + 15) / 16;
-  return alignUp(static_cast<size_t>(tiles) * 4, 256) +
-         static_cast<size_t>(tiles) * splits * 16 * tileM(m) * sizeof(float);
-}
-
-size_t normLds(int64_t m, int64_t k, int tile_n) {
-  return static_cast<size_t>(tileM(m)) * (k + 8) * 2 + 4ull * tile_n * tileM(m) * sizeof(float);
-}
-
 int checkSkinny(const char* op, int64_t m, int64_t k) {
   if (m <= 0 || m > 64) return bad(op, "batch rows must be in [1, 64]");
   if (k <= 0 || k % 64 != 0) return bad(op, "reduction size must be a positive multiple of 64");
   return 0;
 }
 
-int checkSplits(const char* op, int64_t n, int64_t m, int64_t k, int splits, void* workspace,
-                size_t workspace_bytes) {
+// Partial GEMM over `splits` K ranges into workspace [splits, m, n] fp32, then the residual
+// (+ RMSNorm) kernel. n <= kMaxNormN.
+int partialThenResidual(const char* op, const void* x, const void* w, const void* bias,
+                        const void* residual, const void* norm_weight, void* h_out, void* xn_out,
+                        int64_t m, int64_t n, int64_t k, float eps, int splits, void* workspace,
+                        size_t workspace_bytes, void* stream) {
+  if (n <= 0 || n > kMaxNormN) return bad(op, "n must be in [1, 1024]");
   if (splits < 1 || splits > k / 64) return bad(op, "splits must be in [1, k / 64]");
-  if (splits > 1 && (workspace == nullptr || workspace_bytes < splitWorkspace(n, m, splits)))
-    return bad(op, "workspace too small for split-K");
-  return 0;
+  if (workspace == nullptr || workspace_bytes < dli_hip_splitk_workspace(n, m, splits))
+    return bad(op, "workspace too small");
+  if (!aligned16(x) || !aligned16(w)) return bad(op, "x and w must be 16-byte aligned");
+  float* partials = static_cast<float*>(workspace);
+  const unsigned tiles = static_cast<unsigned>((n + kRowTile - 1) / kRowTile);
+  if (int rc = launch(*k_partial.pick(m), {tiles, static_cast<unsigned>(splits)}, {kThreads}, 0,
+                      stream, x, w, partials, static_cast<int>(m), n, static_cast<int>(k), splits))
+    return rc;
+  return launch(k_res_norm, {static_cast<unsigned>(m)}, {kThreads}, 0, stream,
+                static_cast<const float*>(partials), splits, bias, residual, norm_weight, h_out,
+                xn_out, static_cast<int>(m), static_cast<int>(n), eps);
 }
 
 }  // namespace
@@ -85,47 +81,35 @@ using namespace dli::hip;
 extern "C" {
 
 size_t dli_hip_splitk_workspace(int64_t n, int64_t m, int splits) {
-  return splitWorkspace(n, m, splits);
+  if (n <= 0 || m <= 0 || splits < 1) return 0;
+  return static_cast<size_t>(splits) * m * n * sizeof(float);
 }
 
-int dli_hip_qkv_rope_append(const void* hidden, const void* norm_weight, const void* w_qkv,
-                            const void* b_qkv, const float* cos_table, const float* sin_table,
-                            int64_t max_pos, const void* positions, int positions_dtype,
-                            void* q_out, void* key_pool, void* value_pool,
-                            const int32_t* block_table, int64_t block_size, int64_t max_blocks,
-                            int64_t batch, int64_t hidden_size, int64_t q_heads, int64_t kv_heads,
-                            int64_t head_dim, float eps, int splits, void* workspace,
-                            size_t workspace_bytes, void* stream) {
+int dli_hip_qkv_rope_append(const void* xn, const void* w_qkv, const void* b_qkv,
+                            const float* cos_table, const float* sin_table, int64_t max_pos,
+                            const void* positions, int positions_dtype, void* q_out,
+                            void* key_pool, void* value_pool, const int32_t* block_table,
+                            int64_t block_size, int64_t max_blocks, int64_t batch,
+                            int64_t hidden_size, int64_t q_heads, int64_t kv_heads,
+                            int64_t head_dim, void* stream) {
   const char* op = "qkv_rope_append";
   if (int rc = checkSkinny(op, batch, hidden_size)) return rc;
   if (positions == nullptr || (positions_dtype != DLI_I64 && positions_dtype != DLI_I32))
     return bad(op, "positions (int64/int32 [batch]) are required");
   if (head_dim <= 0 || head_dim % 2 != 0) return bad(op, "head_dim must be even");
   if (kv_heads <= 0 || q_heads <= 0) return bad(op, "head counts must be positive");
-  if ((q_heads * head_dim) % kQkvTile != 0 || (kv_heads * head_dim) % kQkvTile != 0)
+  if ((q_heads * head_dim) % kRowTile != 0 || (kv_heads * head_dim) % kRowTile != 0)
     return bad(op, "q and kv widths must be multiples of 16");
-  if (hidden_size > kMaxNormHidden) return bad(op, "hidden_size above 1024 is not supported");
   if (block_size <= 0 || max_blocks <= 0) return bad(op, "empty cache geometry");
+  if (!aligned16(xn) || !aligned16(w_qkv)) return bad(op, "xn and w_qkv must be 16-byte aligned");
   const int64_t n = (q_heads + 2 * kv_heads) * head_dim;
-  if (int rc = checkSplits(op, n, batch, hidden_size, splits, workspace, workspace_bytes)) return rc;
-  if (!aligned16(hidden) || !aligned16(w_qkv) || !aligned16(norm_weight))
-    return bad(op, "hidden, norm_weight and w_qkv must be 16-byte aligned");
-  const size_t lds = normLds(batch, hidden_size, kQkvTile);
-  if (lds > kMaxLds) return bad(op, "batch x hidden too large for the LDS prologue");
-  const int64_t tiles = (n + kQkvTile - 1) / kQkvTile;
-  uint32_t* counters = static_cast<uint32_t*>(workspace);
-  float* partials = splits > 1
-                        ? reinterpret_cast<float*>(static_cast<char*>(workspace) +
-                                                   alignUp(static_cast<size_t>(tiles) * 4, 256))
-                        : nullptr;
+  const int64_t tiles = (n + kRowTile - 1) / kRowTile;
   const int pos64 = positions_dtype == DLI_I64 ? 1 : 0;
-  return launch(*k_qkv.pick(batch), {static_cast<unsigned>(tiles), static_cast<unsigned>(splits)},
-                {kThreads}, static_cast<unsigned>(lds), stream, hidden, norm_weight, w_qkv, b_qkv,
-                cos_table, sin_table, max_pos, positions, pos64, q_out, key_pool, value_pool,
-                block_table, block_size, max_blocks, static_cast<int>(batch),
+  return launch(*k_qkv.pick(batch), {static_cast<unsigned>(tiles)}, {kThreads}, 0, stream, xn,
+                w_qkv, b_qkv, cos_table, sin_table, max_pos, positions, pos64, q_out, key_pool,
+                value_pool, block_table, block_size, max_blocks, static_cast<int>(batch),
                 static_cast<int>(hidden_size), static_cast<int>(q_heads),
-                static_cast<int>(kv_heads), static_cast<int>(head_dim), eps, partials, counters,
-                splits);
+                static_cast<int>(kv_heads), static_cast<int>(head_dim));
 }
 
 int dli_hip_linear_residual(const void* x, const void* w, const void* bias, const void* residual,
@@ -134,33 +118,36 @@ int dli_hip_linear_residual(const void* x, const void* w, const void* bias, cons
   const char* op = "linear_residual";
   if (int rc = checkSkinny(op, m, k)) return rc;
   if (n <= 0) return bad(op, "n must be positive");
-  if (int rc = checkSplits(op, n, m, k, splits, workspace, workspace_bytes)) return rc;
+  if (splits > 1)
+    return partialThenResidual(op, x, w, bias, residual, nullptr, out, nullptr, m, n, k, 0.f,
+                               splits, workspace, workspace_bytes, stream);
+  if (splits != 1) return bad(op, "splits must be >= 1");
   if (!aligned16(x) || !aligned16(w)) return bad(op, "x and w must be 16-byte aligned");
-  const int64_t tiles = (n + kResTile - 1) / kResTile;
-  uint32_t* counters = static_cast<uint32_t*>(workspace);
-  float* partials = splits > 1
-                        ? reinterpret_cast<float*>(static_cast<char*>(workspace) +
-                                                   alignUp(static_cast<size_t>(tiles) * 4, 256))
-                        : nullptr;
-  return launch(*k_linres.pick(m), {static_cast<unsigned>(tiles), static_cast<unsigned>(splits)},
-                {kResWaves * 64}, 0, stream, x, w, bias, residual, out, static_cast<int>(m), n,
-                static_cast<int>(k), partials, counters, splits);
+  const int64_t tiles = (n + kRowTile - 1) / kRowTile;
+  return launch(*k_linres.pick(m), {static_cast<unsigned>(tiles)}, {kResWaves * 64}, 0, stream, x,
+                w, bias, residual, out, static_cast<int>(m), n, static_cast<int>(k));
 }
 
-int dli_hip_gate_up_silu(const void* hidden, const void* norm_weight, const void* w_gate_up,
-                         void* out, int64_t m, int64_t ffn, int64_t hidden_size, float eps,
-                         void* stream) {
+int dli_hip_linear_residual_norm(const void* x, const void* w, const void* bias,
+                                 const void* residual, const void* norm_weight, void* h_out,
+                                 void* xn_out, int64_t m, int64_t n, int64_t k, float eps,
+                                 int splits, void* workspace, size_t workspace_bytes,
+                                 void* stream) {
+  const char* op = "linear_residual_norm";
+  if (int rc = checkSkinny(op, m, k)) return rc;
+  if (norm_weight == nullptr || xn_out == nullptr) return bad(op, "norm_weight and xn_out are required");
+  return partialThenResidual(op, x, w, bias, residual, norm_weight, h_out, xn_out, m, n, k, eps,
+                             splits, workspace, workspace_bytes, stream);
+}
+
+int dli_hip_gate_up_silu(const void* xn, const void* w_gate_up, void* out, int64_t m, int64_t ffn,
+                         int64_t hidden_size, void* stream) {
   const char* op = "gate_up_silu";
   if (int rc = checkSkinny(op, m, hidden_size)) return rc;
   if (ffn <= 0 || ffn % 16 != 0) return bad(op, "ffn must be a positive multiple of 16");
-  if (hidden_size > kMaxNormHidden) return bad(op, "hidden_size above 1024 is not supported");
-  if (!aligned16(hidden) || !aligned16(w_gate_up) || !aligned16(norm_weight))
-    return bad(op, "hidden, norm_weight and w_gate_up must be 16-byte aligned");
-  const size_t lds = normLds(m, hidden_size, kTileN);
-  if (lds > kMaxLds) return bad(op, "batch x hidden too large for the LDS prologue");
-  return launch(*k_gate_up.pick(m), {static_cast<unsigned>(ffn / 16)}, {kThreads},
-                static_cast<unsigned>(lds), stream, hidden, norm_weight, w_gate_up, out,
-                static_cast<int>(m), ffn, static_cast<int>(hidden_size), eps);
+  if (!aligned16(xn) || !aligned16(w_gate_up)) return bad(op, "xn and w_gate_up must be 16-byte aligned");
+  return launch(*k_gate_up.pick(m), {static_cast<unsigned>(ffn / 16)}, {kThreads}, 0, stream, xn,
+                w_gate_up, out, static_cast<int>(m), ffn, static_cast<int>(hidden_size));
 }
 
 size_t dli_hip_lm_head_argmax_workspace(int64_t m, int64_t vocab) {
@@ -168,37 +155,31 @@ size_t dli_hip_lm_head_argmax_workspace(int64_t m, int64_t vocab) {
   return static_cast<size_t>(tiles) * m * (sizeof(float) + sizeof(int32_t));
 }
 
-int dli_hip_lm_head_argmax(const void* hidden, const void* norm_weight, const void* w,
-                           void* logits, int logits_dtype, int64_t* ids, int64_t m, int64_t vocab,
-                           int64_t hidden_size, float eps, void* workspace,
-                           size_t workspace_bytes, void* stream) {
+int dli_hip_lm_head_argmax(const void* xn, const void* w, void* logits, int logits_dtype,
+                           int64_t* ids, int64_t m, int64_t vocab, int64_t hidden_size,
+                           void* workspace, size_t workspace_bytes, void* stream) {
   const char* op = "lm_head_argmax";
   if (int rc = checkSkinny(op, m, hidden_size)) return rc;
+  if (hidden_size > kMaxLmK) return bad(op, "hidden_size above 1024 is not supported");
   if (vocab <= 0 || vocab >= (int64_t{1} << 31)) return bad(op, "vocab must be in [1, 2^31)");
   if (logits != nullptr && logits_dtype != DLI_F32 && logits_dtype != DLI_BF16)
     return bad(op, "logits dtype must be float32 or bfloat16");
   if (ids == nullptr) return bad(op, "ids is NULL");
   if (workspace == nullptr || workspace_bytes < dli_hip_lm_head_argmax_workspace(m, vocab))
     return bad(op, "workspace too small");
-  if (!aligned16(hidden) || !aligned16(w) || !aligned16(norm_weight))
-    return bad(op, "hidden, norm_weight and w must be 16-byte aligned");
-  if (hidden_size > kMaxNormHidden) return bad(op, "hidden_size above 1024 is not supported");
-  const size_t lds = normLds(m, hidden_size, kTileN);
-  if (lds > kMaxLds) return bad(op, "batch x hidden too large for the LDS prologue");
+  if (!aligned16(xn) || !aligned16(w)) return bad(op, "xn and w must be 16-byte aligned");
   const int64_t tiles = (vocab + kTileN - 1) / kTileN;
   const int64_t blocks = (tiles + kLmTilesPerBlock - 1) / kLmTilesPerBlock;
-  if (tiles > 0x7fffffff) return bad(op, "too many tiles");
   float* part_val = static_cast<float*>(workspace);
   int32_t* part_idx = reinterpret_cast<int32_t*>(part_val + tiles * m);
   const int logits_f32 = logits_dtype == DLI_F32 ? 1 : 0;
-  if (int rc = launch(*k_lm_head.pick(m), {static_cast<unsigned>(blocks)}, {kThreads},
-                      static_cast<unsigned>(lds), stream, hidden, norm_weight, w, logits,
-                      logits_f32, part_val, part_idx, static_cast<int>(m), vocab,
-                      static_cast<int>(hidden_size), eps))
+  if (int rc = launch(*k_lm_head.pick(m), {static_cast<unsigned>(blocks)}, {kThreads}, 0, stream,
+                      xn, w, logits, logits_f32, part_val, part_idx, static_cast<int>(m), vocab,
+                      static_cast<int>(hidden_size)))
     return rc;
   return launch(k_argmax_final, {static_cast<unsigned>(m)}, {kThreads}, 0, stream,
                 static_cast<const float*>(part_val), static_cast<const int32_t*>(part_idx),
-                static_cast<int>(tiles), static_cast<int>(m), ids);
+                static_cast<int>(tiles), ids);
 }
 
 }  // extern "C"

@@ -1,19 +1,22 @@
-// Fused bf16 decode kernels for a Qwen2-style decoder layer on gfx950. Each one is a skinny
-// weight-streaming GEMM (skinny.h) with a fused prologue and/or epilogue. The rounding points
-// are those of the unfused dli.graph.v1 graph (every op rounds its output to bf16), so the
-// fused and unfused graphs compute the same values up to fp32 summation order:
+// Fused bf16 decode kernels for a Qwen2-style decoder layer on gfx950. The GEMMs are skinny
+// weight-streaming MFMA GEMMs (skinny.h) on activations that are already normalized, with
+// their epilogues fused; the RMSNorm itself runs once per residual update (residual_rms_norm),
+// not once per GEMM workgroup. Rounding points are those of the unfused dli.graph.v1 graph
+// (every op rounds its output to bf16), so fused and unfused graphs compute the same values up
+// to fp32 summation order.
 //
-//  qkv_rope_append   rms_norm -> [q|k|v] linear (+bias) -> interleaved RoPE on q, k
-//                    (rotary/kernel.py:6-35) -> k, v scattered into the paged KV cache, q out
-//  linear_residual   linear (+bias) -> add residual            (o_proj, down_proj)
-//  gate_up_silu      rms_norm -> gate/up linear -> silu(gate) * up  (weights interleaved in
-//                    16-row blocks: [gate 16 rows | up 16 rows] per output block of 16)
-//  lm_head_argmax    rms_norm -> logits linear (fp32 accumulate) -> logits out + per-tile
-//                    argmax partials; argmax_finalize reduces them (first index of the max)
-//
-// Launch: 256 threads, grid.x = N tiles of 32 weight rows, grid.y = K splits (split-K uses
-// the last-arriving-workgroup reduction of skinny.h). Kernels taking an RMSNorm prologue
-// keep the normalized activations in dynamic LDS ([16 * MB][K + 8] bf16).
+//  qkv_rope_append     [q|k|v] = xn W^T + b -> interleaved RoPE on q, k (rotary/kernel.py:6-35)
+//                      -> k, v written into the paged KV cache at each row's position, q out
+//  linear_residual     out = residual + bf16(x W^T + b)          (one workgroup per 16 rows)
+//  linear_partial      fp32 split-K partial tiles of x W^T: grid (N / 16, splits), no
+//                      cross-workgroup synchronization; residual_rms_norm sums the splits in
+//                      split order
+//  residual_rms_norm   h = bf16(residual + bf16(sum_s partial_s + b));
+//                      xn = bf16(h * rsqrt(mean(h^2) + eps) * w)   (rms_norm/kernel.py:6-14)
+//  gate_up_silu        gate/up = xn W^T -> bf16(bf16(silu(gate)) * up) (weights interleaved in
+//                      16-row blocks: [gate 16 rows | up 16 rows] per output block of 16)
+//  lm_head_argmax      logits = xn W^T (fp32) -> logits out + per-tile argmax partials;
+//                      argmax_finalize reduces them (first index of the maximum)
 #include "common.h"
 #include "skinny.h"
 
@@ -23,11 +26,9 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
-constexpr int kNormVec = 2;          // RMSNorm prologue: hidden <= 64 lanes * 8 * kNormVec = 1024
-constexpr int kQkvNF = 1;            // qkv_rope_append: 16 weight rows per workgroup
-constexpr int kResNF = 1;            // linear_residual: 16 weight rows per workgroup
 constexpr int kResWaves = 8;         // linear_residual: 8 waves split K inside a workgroup
 constexpr int kLmTilesPerBlock = 8;  // lm_head_argmax: 8 x 32 vocab rows per workgroup
+constexpr int kNormPer = 4;          // residual_rms_norm: N <= kThreads * kNormPer
 
 // Steps [begin, end) of split `split` out of `splits` over `steps` 64-column steps.
 __device__ __forceinline__ void splitRange(int steps, int split, int splits, int& begin, int& end) {
@@ -46,19 +47,14 @@ struct KvCacheArgs {
   int64_t max_blocks;
 };
 
+// 16 weight rows per workgroup (72 workgroups for Qwen2-0.5B's 1152 q|k|v rows).
 template <int MB>
-__device__ void qkv_rope_append_impl(const uint16_t* h, const uint16_t* norm_w, const uint16_t* w,
-                                     const uint16_t* bias, const float* cos_t, const float* sin_t,
-                                     int64_t max_pos, const void* positions, int pos64,
-                                     uint16_t* q_out, KvCacheArgs kv, int M, int K, int Hq, int Hkv,
-                                     int D, float eps, float* partials, uint32_t* counters,
-                                     int splits) {
-  using Core = SkinnyCore<kQkvNF, MB, kWaves>;
-  extern __shared__ __align__(16) unsigned char smem[];
-  const int xstride = K + 8;
-  uint16_t* xs = reinterpret_cast<uint16_t*>(smem);
-  float* lds = reinterpret_cast<float*>(smem + Core::kTileM * xstride * sizeof(uint16_t));
-
+__device__ void qkv_rope_append_impl(const uint16_t* xn, const uint16_t* w, const uint16_t* bias,
+                                     const float* cos_t, const float* sin_t, int64_t max_pos,
+                                     const void* positions, int pos64, uint16_t* q_out,
+                                     KvCacheArgs kv, int M, int K, int Hq, int Hkv, int D) {
+  using Core = SkinnyCore<1, MB, kWaves>;
+  __shared__ float lds[Core::kLdsFloats];
   const int64_t N = static_cast<int64_t>(Hq + 2 * Hkv) * D;
   const int64_t n0 = static_cast<int64_t>(blockIdx.x) * Core::kTileN;
   const int64_t q_rows = static_cast<int64_t>(Hq) * D;
@@ -68,7 +64,8 @@ __device__ void qkv_rope_append_impl(const uint16_t* h, const uint16_t* norm_w, 
 
   // Epilogue operands do not depend on the GEMM: fetch them first (position, then the rotary
   // coefficients, the bias pair and the cache block of this thread's (pair, row) items).
-  constexpr int kItems = ((Core::kTileN / 2) * Core::kTileM + kThreads - 1) / kThreads;
+  constexpr int kPairs = (Core::kTileN / 2) * Core::kTileM;
+  constexpr int kItems = (kPairs + kThreads - 1) / kThreads;
   int64_t pos[kItems];
   float cs[kItems][2], bs[kItems][2];
   int64_t blk[kItems];
@@ -76,7 +73,7 @@ __device__ void qkv_rope_append_impl(const uint16_t* h, const uint16_t* norm_w, 
   for (int it = 0; it < kItems; ++it) {
     const int idx = threadIdx.x + it * kThreads;
     const int m = idx % Core::kTileM;
-    pos[it] = (idx < (Core::kTileN / 2) * Core::kTileM && m < M) ? loadIndex(positions, pos64, m) : -1;
+    pos[it] = (idx < kPairs && m < M) ? loadIndex(positions, pos64, m) : -1;
   }
 #pragma unroll
   for (int it = 0; it < kItems; ++it) {
@@ -96,14 +93,7 @@ __device__ void qkv_rope_append_impl(const uint16_t* h, const uint16_t* norm_w, 
                   : -1;
   }
 
-  int sb, se;
-  splitRange(K / 64, blockIdx.y, splits, sb, se);
-  Core::run(w, XLds{xs, xstride}, N, K, M, n0, sb, se, lds, [&] {
-    rmsNormRowsToLds<Core::kTileM / kWaves, kNormVec>(h, norm_w, M, Core::kTileM, K, eps, xs, xstride);
-  });
-  if (!splitKReduce<Core::kTileN * Core::kTileM>(lds, partials, counters, blockIdx.x, blockIdx.y,
-                                                   splits))
-    return;
+  Core::run(w, XGlobal{xn, K}, N, K, M, n0, 0, K / 64, lds);
 
 #pragma unroll
   for (int it = 0; it < kItems; ++it) {
@@ -147,11 +137,12 @@ __device__ void qkv_rope_append_impl(const uint16_t* h, const uint16_t* norm_w, 
   }
 }
 
+// out = residual + bf16(x W^T + b); 16 weight rows per workgroup, 8 waves split K.
 template <int MB>
 __device__ void linear_residual_impl(const uint16_t* x, const uint16_t* w, const uint16_t* bias,
                                      const uint16_t* residual, uint16_t* out, int M, int64_t N,
-                                     int K, float* partials, uint32_t* counters, int splits) {
-  using Core = SkinnyCore<kResNF, MB, kResWaves>;
+                                     int K) {
+  using Core = SkinnyCore<1, MB, kResWaves, (MB >= 4 ? 2 : 4)>;  // 256 VGPRs at 512 threads
   __shared__ float lds[Core::kLdsFloats];
   const int64_t n0 = static_cast<int64_t>(blockIdx.x) * Core::kTileN;
   constexpr int kThreadsRes = kResWaves * kWave;
@@ -165,12 +156,7 @@ __device__ void linear_residual_impl(const uint16_t* x, const uint16_t* w, const
     const bool live = idx < Core::kTileN * Core::kTileM && m < M && n < N;
     res[it] = live ? bf16ToFloat(residual[m * N + n]) : 0.f;
   }
-  int sb, se;
-  splitRange(K / 64, blockIdx.y, splits, sb, se);
-  Core::run(w, XGlobal{x, K}, N, K, M, n0, sb, se, lds);
-  if (!splitKReduce<Core::kTileN * Core::kTileM>(lds, partials, counters, blockIdx.x, blockIdx.y,
-                                                   splits))
-    return;
+  Core::run(w, XGlobal{x, K}, N, K, M, n0, 0, K / 64, lds);
 #pragma unroll
   for (int it = 0; it < kItems; ++it) {
     const int idx = threadIdx.x + it * kThreadsRes;
@@ -179,26 +165,78 @@ __device__ void linear_residual_impl(const uint16_t* x, const uint16_t* w, const
     if (idx >= Core::kTileN * Core::kTileM || m >= M || n >= N) continue;
     float y = lds[idx];
     if (bias != nullptr) y += bf16ToFloat(bias[n]);
-    y = roundBf16(y);
-    out[m * N + n] = floatToBf16(res[it] + y);
+    out[m * N + n] = floatToBf16(res[it] + roundBf16(y));
+  }
+}
+
+// partials[split][m][n] = sum over the split's K steps of x[m, k] * w[n, k]; 16 rows per
+// workgroup.
+template <int MB>
+__device__ void linear_partial_impl(const uint16_t* x, const uint16_t* w, float* partials, int M,
+                                    int64_t N, int K, int splits) {
+  using Core = SkinnyCore<1, MB, kWaves>;
+  __shared__ float lds[Core::kLdsFloats];
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * Core::kTileN;
+  int sb, se;
+  splitRange(K / 64, blockIdx.y, splits, sb, se);
+  Core::run(w, XGlobal{x, K}, N, K, M, n0, sb, se, lds);
+  float* dst = partials + static_cast<int64_t>(blockIdx.y) * M * N;
+  for (int idx = threadIdx.x; idx < Core::kTileN * Core::kTileM; idx += blockDim.x) {
+    const int nl = idx % Core::kTileN, m = idx / Core::kTileN;  // n fastest: coalesced stores
+    const int64_t n = n0 + nl;
+    if (m < M && n < N) dst[m * N + n] = lds[nl * Core::kTileM + m];
+  }
+}
+
+// One workgroup per row m. With norm_w == nullptr only h is written.
+__device__ void residual_rms_norm_impl(const float* partials, int splits, const uint16_t* bias,
+                                       const uint16_t* residual, const uint16_t* norm_w,
+                                       uint16_t* h_out, uint16_t* xn_out, int M, int N, float eps) {
+  __shared__ float scratch[kWaves];
+  const int m = blockIdx.x;
+  float y[kNormPer], hv[kNormPer];
+#pragma unroll
+  for (int j = 0; j < kNormPer; ++j) {
+    const int n = threadIdx.x + j * kThreads;
+    y[j] = 0.f;
+    hv[j] = n < N ? bf16ToFloat(residual[static_cast<int64_t>(m) * N + n]) : 0.f;
+  }
+  for (int s = 0; s < splits; ++s) {  // fixed split order
+#pragma unroll
+    for (int j = 0; j < kNormPer; ++j) {
+      const int n = threadIdx.x + j * kThreads;
+      y[j] += n < N ? partials[(static_cast<int64_t>(s) * M + m) * N + n] : 0.f;
+    }
+  }
+  float sq = 0.f;
+#pragma unroll
+  for (int j = 0; j < kNormPer; ++j) {
+    const int n = threadIdx.x + j * kThreads;
+    if (n < N && bias != nullptr) y[j] += bf16ToFloat(bias[n]);
+    hv[j] = roundBf16(hv[j] + roundBf16(y[j]));
+    sq += hv[j] * hv[j];
+    if (n < N) h_out[static_cast<int64_t>(m) * N + n] = floatToBf16(hv[j]);
+  }
+  if (norm_w == nullptr) return;
+  const float inv = 1.0f / sqrtf(blockSum(sq, scratch) / static_cast<float>(N) + eps);
+#pragma unroll
+  for (int j = 0; j < kNormPer; ++j) {
+    const int n = threadIdx.x + j * kThreads;
+    if (n < N)
+      xn_out[static_cast<int64_t>(m) * N + n] = floatToBf16(hv[j] * inv * bf16ToFloat(norm_w[n]));
   }
 }
 
 template <int MB>
-__device__ void gate_up_silu_impl(const uint16_t* h, const uint16_t* norm_w, const uint16_t* w_gu,
-                                  uint16_t* out, int M, int64_t F, int K, float eps) {
+__device__ void gate_up_silu_impl(const uint16_t* xn, const uint16_t* w_gu, uint16_t* out, int M,
+                                  int64_t F, int K) {
   using Core = SkinnyCore<2, MB, kWaves>;
-  extern __shared__ __align__(16) unsigned char smem[];
-  const int xstride = K + 8;
-  uint16_t* xs = reinterpret_cast<uint16_t*>(smem);
-  float* lds = reinterpret_cast<float*>(smem + Core::kTileM * xstride * sizeof(uint16_t));
+  __shared__ float lds[Core::kLdsFloats];
   const int64_t n0 = static_cast<int64_t>(blockIdx.x) * Core::kTileN;  // rows of w_gu
-  Core::run(w_gu, XLds{xs, xstride}, 2 * F, K, M, n0, 0, K / 64, lds, [&] {
-    rmsNormRowsToLds<Core::kTileM / kWaves, kNormVec>(h, norm_w, M, Core::kTileM, K, eps, xs, xstride);
-  });
+  Core::run(w_gu, XGlobal{xn, K}, 2 * F, K, M, n0, 0, K / 64, lds);
   const int64_t f0 = static_cast<int64_t>(blockIdx.x) * 16;
   for (int idx = threadIdx.x; idx < 16 * Core::kTileM; idx += blockDim.x) {
-    const int j = idx / Core::kTileM, m = idx % Core::kTileM;
+    const int j = idx % 16, m = idx / 16;
     const int64_t f = f0 + j;
     if (m >= M || f >= F) continue;
     const float g = roundBf16(lds[j * Core::kTileM + m]);
@@ -208,62 +246,83 @@ __device__ void gate_up_silu_impl(const uint16_t* h, const uint16_t* norm_w, con
   }
 }
 
-// Multiplies one vocab tile already loaded into `bt`, stores its logits and argmax partials.
-template <int MB, typename Batch>
-__device__ void lmHeadTile(Batch& bt, const XLds& xsrc, float* lds, void* logits, int logits_f32,
-                           float* part_val, int32_t* part_idx, int M, int64_t V, int64_t t,
+constexpr int kLmTileN = 32;  // vocab rows per lm_head tile (NF = 2)
+constexpr int kLmQuarters = kLmTileN / 4;
+
+// Multiplies one vocab tile (weights in `wb`, x fragments in `xb`), stores its logits and the
+// tile's argmax partial per row: part_*[m * tiles + t].
+template <int MB>
+__device__ __forceinline__ void lmHeadTile(const typename SkinnyCore<2, MB, kWaves>::WBatch& wb,
+                           const typename SkinnyCore<2, MB, kWaves>::XBatch& xb, float* lds,
+                           int* lds_arg, void* logits, int logits_f32, float* part_val,
+                           int32_t* part_idx, int M, int64_t V, int64_t tiles, int64_t t,
                            int steps, int r, int g, int wave) {
   using Core = SkinnyCore<2, MB, kWaves>;
   f32x4 acc[2][MB];
-#pragma unroll
-  for (int f = 0; f < 2; ++f)
-#pragma unroll
-    for (int b = 0; b < MB; ++b) acc[f][b] = f32x4{0.f, 0.f, 0.f, 0.f};
-  Core::compute(acc, bt, xsrc, M, wave, steps, r, g);
+  Core::zero(acc);
+  Core::compute(acc, wb, xb, wave, steps);
   Core::reduce(acc, lds, r, g, wave);
   const int64_t n0 = t * Core::kTileN;
   if (logits != nullptr) {
     for (int idx = threadIdx.x; idx < Core::kTileN * Core::kTileM; idx += blockDim.x) {
-      const int nl = idx / Core::kTileM, m = idx % Core::kTileM;
+      const int nl = idx % Core::kTileN, m = idx / Core::kTileN;  // n fastest: coalesced stores
       const int64_t n = n0 + nl;
       if (m >= M || n >= V) continue;
+      const float v = lds[nl * Core::kTileM + m];
       if (logits_f32)
-        static_cast<float*>(logits)[m * V + n] = lds[idx];
+        static_cast<float*>(logits)[m * V + n] = v;
       else
-        static_cast<uint16_t*>(logits)[m * V + n] = floatToBf16(lds[idx]);
+        static_cast<uint16_t*>(logits)[m * V + n] = floatToBf16(v);
     }
   }
-  // per-row argmax of this tile's fp32 logits (first index among equal maxima)
-  for (int m = threadIdx.x; m < M; m += blockDim.x) {
+  // argmax: thread (m, q) scans rows 4q..4q+3 of the tile, then one thread per m merges the
+  // quarters in order (first index among equal maxima).
+  float* qv = lds + Core::kTileN * Core::kTileM;
+  for (int idx = threadIdx.x; idx < kLmQuarters * Core::kTileM; idx += blockDim.x) {
+    const int m = idx % Core::kTileM, q = idx / Core::kTileM;
     float best = -INFINITY;
-    int32_t arg = static_cast<int32_t>(n0);
-    for (int nl = 0; nl < Core::kTileN && n0 + nl < V; ++nl) {
+    int arg = -1;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int nl = q * 4 + j;
       const float v = lds[nl * Core::kTileM + m];
-      if (v > best) {
+      if (n0 + nl < V && (arg < 0 || v > best)) {
         best = v;
-        arg = static_cast<int32_t>(n0 + nl);
+        arg = nl;
       }
     }
-    part_val[t * M + m] = best;
-    part_idx[t * M + m] = arg;
+    qv[q * Core::kTileM + m] = best;
+    lds_arg[q * Core::kTileM + m] = arg;
+  }
+  __syncthreads();
+  for (int m = threadIdx.x; m < M; m += blockDim.x) {
+    float best = -INFINITY;
+    int arg = -1;
+    for (int q = 0; q < kLmQuarters; ++q) {
+      const float v = qv[q * Core::kTileM + m];
+      const int a = lds_arg[q * Core::kTileM + m];
+      if (a >= 0 && (arg < 0 || v > best)) {
+        best = v;
+        arg = a;
+      }
+    }
+    part_val[m * tiles + t] = best;
+    part_idx[m * tiles + t] = static_cast<int32_t>(n0 + (arg < 0 ? 0 : arg));
   }
   __syncthreads();  // lds is reused by the next tile
 }
 
-// Vocab tiles of 32 rows; kLmTilesPerBlock consecutive tiles per workgroup share one normalized
-// copy of x, and tile t + 1's weights stream in while tile t is multiplied. Requires
-// K / 64 <= kUnroll * kWaves (one batch per tile).
+// Vocab tiles of 32 rows; kLmTilesPerBlock consecutive tiles per workgroup. Wave w always owns
+// the same 64-column steps, so its x fragments are loaded once and stay in registers across
+// tiles, while tile t + 1's weights stream in during tile t. Requires K / 64 <= 4 * kWaves.
 template <int MB>
-__device__ void lm_head_argmax_impl(const uint16_t* h, const uint16_t* norm_w, const uint16_t* w,
-                                    void* logits, int logits_f32, float* part_val,
-                                    int32_t* part_idx, int M, int64_t V, int K, float eps) {
+__device__ void lm_head_argmax_impl(const uint16_t* xn, const uint16_t* w, void* logits,
+                                    int logits_f32, float* part_val, int32_t* part_idx, int M,
+                                    int64_t V, int K) {
   using Core = SkinnyCore<2, MB, kWaves>;
-  using Batch = typename Core::template Batch<XLds>;
-  extern __shared__ __align__(16) unsigned char smem[];
-  const int xstride = K + 8;
-  uint16_t* xs = reinterpret_cast<uint16_t*>(smem);
-  float* lds = reinterpret_cast<float*>(smem + Core::kTileM * xstride * sizeof(uint16_t));
-  const XLds xsrc{xs, xstride};
+  static_assert(Core::kTileN == kLmTileN, "lm_head tile");
+  __shared__ float lds[Core::kLdsFloats + kLmQuarters * Core::kTileM];
+  __shared__ int lds_arg[kLmQuarters * Core::kTileM];
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
   const int r = lane % 16, g = lane / 16;
   const int steps = K / 64;
@@ -271,32 +330,37 @@ __device__ void lm_head_argmax_impl(const uint16_t* h, const uint16_t* norm_w, c
   const int64_t t_first = static_cast<int64_t>(blockIdx.x) * kLmTilesPerBlock;
   const int64_t t_last = t_first + kLmTilesPerBlock < tiles ? t_first + kLmTilesPerBlock : tiles;
 
-  Batch bufA, bufB;
-  Core::issue(bufA, Core::rows(w, V, K, t_first * Core::kTileN, r, g), xsrc, M, wave, steps, r, g);
-  rmsNormRowsToLds<Core::kTileM / kWaves, kNormVec>(h, norm_w, M, Core::kTileM, K, eps, xs, xstride);
+  typename Core::WBatch bufA, bufB;
+  typename Core::XBatch xb;
+  Core::issueW(bufA, Core::rows(w, V, K, t_first * Core::kTileN, r, g), wave, steps);
+  Core::issueX(xb, XGlobal{xn, K}, M, wave, steps, r, g);
   for (int64_t t = t_first; t < t_last; t += 2) {
     if (t + 1 < t_last)
-      Core::issue(bufB, Core::rows(w, V, K, (t + 1) * Core::kTileN, r, g), xsrc, M, wave, steps, r, g);
-    lmHeadTile<MB>(bufA, xsrc, lds, logits, logits_f32, part_val, part_idx, M, V, t, steps, r, g, wave);
+      Core::issueW(bufB, Core::rows(w, V, K, (t + 1) * Core::kTileN, r, g), wave, steps);
+    lmHeadTile<MB>(bufA, xb, lds, lds_arg, logits, logits_f32, part_val, part_idx, M, V, tiles, t,
+                   steps, r, g, wave);
     if (t + 1 >= t_last) break;
     if (t + 2 < t_last)
-      Core::issue(bufA, Core::rows(w, V, K, (t + 2) * Core::kTileN, r, g), xsrc, M, wave, steps, r, g);
-    lmHeadTile<MB>(bufB, xsrc, lds, logits, logits_f32, part_val, part_idx, M, V, t + 1, steps, r, g,
-                   wave);
+      Core::issueW(bufA, Core::rows(w, V, K, (t + 2) * Core::kTileN, r, g), wave, steps);
+    lmHeadTile<MB>(bufB, xb, lds, lds_arg, logits, logits_f32, part_val, part_idx, M, V, tiles,
+                   t + 1, steps, r, g, wave);
   }
 }
 
-// One block per row: reduce tile partials in tile order (ties keep the lower index).
+// One workgroup per row: reduce that row's tile partials (contiguous) in tile order; ties keep
+// the lower index.
 __device__ void argmax_finalize_impl(const float* part_val, const int32_t* part_idx, int tiles,
-                                     int M, int64_t* ids) {
+                                     int64_t* ids) {
   __shared__ float sv[kWaves];
   __shared__ int32_t si[kWaves];
   const int m = blockIdx.x;
+  const float* vals = part_val + static_cast<int64_t>(m) * tiles;
+  const int32_t* idxs = part_idx + static_cast<int64_t>(m) * tiles;
   float best = -INFINITY;
   int32_t arg = 0x7fffffff;
   for (int t = threadIdx.x; t < tiles; t += blockDim.x) {
-    const float v = part_val[static_cast<int64_t>(t) * M + m];
-    const int32_t i = part_idx[static_cast<int64_t>(t) * M + m];
+    const float v = vals[t];
+    const int32_t i = idxs[t];
     if (v > best || (v == best && i < arg)) {
       best = v;
       arg = i;
@@ -330,31 +394,34 @@ __device__ void argmax_finalize_impl(const float* part_val, const int32_t* part_
 
 }  // namespace
 
-#define DK_DECODE_KERNELS(MB)                                                                    \
-  extern "C" __global__ void __launch_bounds__(kThreads) qkv_rope_append_m##MB(                  \
-      const uint16_t* h, const uint16_t* norm_w, const uint16_t* w, const uint16_t* bias,        \
-      const float* cos_t, const float* sin_t, int64_t max_pos, const void* positions, int pos64,  \
-      uint16_t* q_out, uint16_t* k_pool, uint16_t* v_pool, const int32_t* block_table,           \
-      int64_t block_size, int64_t max_blocks, int M, int K, int Hq, int Hkv, int D, float eps,   \
-      float* partials, uint32_t* counters, int splits) {                                         \
-    qkv_rope_append_impl<MB>(h, norm_w, w, bias, cos_t, sin_t, max_pos, positions, pos64, q_out, \
+#define DK_DECODE_KERNELS(MB)                                                                     \
+  extern "C" __global__ void __launch_bounds__(kThreads) qkv_rope_append_m##MB(                   \
+      const uint16_t* xn, const uint16_t* w, const uint16_t* bias, const float* cos_t,            \
+      const float* sin_t, int64_t max_pos, const void* positions, int pos64, uint16_t* q_out,     \
+      uint16_t* k_pool, uint16_t* v_pool, const int32_t* block_table, int64_t block_size,         \
+      int64_t max_blocks, int M, int K, int Hq, int Hkv, int D) {                                 \
+    qkv_rope_append_impl<MB>(xn, w, bias, cos_t, sin_t, max_pos, positions, pos64, q_out,         \
                              KvCacheArgs{k_pool, v_pool, block_table, block_size, max_blocks}, M, \
-                             K, Hq, Hkv, D, eps, partials, counters, splits);                    \
-  }                                                                                              \
-  extern "C" __global__ void __launch_bounds__(kResWaves * 64) linear_residual_m##MB(                  \
-      const uint16_t* x, const uint16_t* w, const uint16_t* bias, const uint16_t* residual,      \
-      uint16_t* out, int M, int64_t N, int K, float* partials, uint32_t* counters, int splits) { \
-    linear_residual_impl<MB>(x, w, bias, residual, out, M, N, K, partials, counters, splits);    \
-  }                                                                                              \
-  extern "C" __global__ void __launch_bounds__(kThreads) gate_up_silu_m##MB(                     \
-      const uint16_t* h, const uint16_t* norm_w, const uint16_t* w_gu, uint16_t* out, int M,     \
-      int64_t F, int K, float eps) {                                                             \
-    gate_up_silu_impl<MB>(h, norm_w, w_gu, out, M, F, K, eps);                                   \
-  }                                                                                              \
-  extern "C" __global__ void __launch_bounds__(kThreads) lm_head_argmax_m##MB(                   \
-      const uint16_t* h, const uint16_t* norm_w, const uint16_t* w, void* logits, int logits_f32, \
-      float* part_val, int32_t* part_idx, int M, int64_t V, int K, float eps) {                  \
-    lm_head_argmax_impl<MB>(h, norm_w, w, logits, logits_f32, part_val, part_idx, M, V, K, eps); \
+                             K, Hq, Hkv, D);                                                      \
+  }                                                                                               \
+  extern "C" __global__ void __launch_bounds__(kResWaves * 64) linear_residual_m##MB(             \
+      const uint16_t* x, const uint16_t* w, const uint16_t* bias, const uint16_t* residual,       \
+      uint16_t* out, int M, int64_t N, int K) {                                                   \
+    linear_residual_impl<MB>(x, w, bias, residual, out, M, N, K);                                 \
+  }                                                                                               \
+  extern "C" __global__ void __launch_bounds__(kThreads) linear_partial_m##MB(                    \
+      const uint16_t* x, const uint16_t* w, float* partials, int M, int64_t N, int K,             \
+      int splits) {                                                                               \
+    linear_partial_impl<MB>(x, w, partials, M, N, K, splits);                                     \
+  }                                                                                               \
+  extern "C" __global__ void __launch_bounds__(kThreads) gate_up_silu_m##MB(                      \
+      const uint16_t* xn, const uint16_t* w_gu, uint16_t* out, int M, int64_t F, int K) {         \
+    gate_up_silu_impl<MB>(xn, w_gu, out, M, F, K);                                                \
+  }                                                                                               \
+  extern "C" __global__ void __launch_bounds__(kThreads) lm_head_argmax_m##MB(                    \
+      const uint16_t* xn, const uint16_t* w, void* logits, int logits_f32, float* part_val,       \
+      int32_t* part_idx, int M, int64_t V, int K) {                                               \
+    lm_head_argmax_impl<MB>(xn, w, logits, logits_f32, part_val, part_idx, M, V, K);              \
   }
 
 DK_DECODE_KERNELS(1)
@@ -362,6 +429,13 @@ DK_DECODE_KERNELS(2)
 DK_DECODE_KERNELS(4)
 
 extern "C" __global__ void __launch_bounds__(kThreads)
-    argmax_finalize(const float* part_val, const int32_t* part_idx, int tiles, int M, int64_t* ids) {
-  argmax_finalize_impl(part_val, part_idx, tiles, M, ids);
+    residual_rms_norm(const float* partials, int splits, const uint16_t* bias,
+                      const uint16_t* residual, const uint16_t* norm_w, uint16_t* h_out,
+                      uint16_t* xn_out, int M, int N, float eps) {
+  residual_rms_norm_impl(partials, splits, bias, residual, norm_w, h_out, xn_out, M, N, eps);
+}
+
+extern "C" __global__ void __launch_bounds__(kThreads)
+    argmax_finalize(const float* part_val, const int32_t* part_idx, int tiles, int64_t* ids) {
+  argmax_finalize_impl(part_val, part_idx, tiles, ids);
 }

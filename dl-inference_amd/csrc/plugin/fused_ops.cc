@@ -2,12 +2,15 @@
 // a run of nodes of the reference's exported Qwen2 decoder graph
 // (python/dli_export/export.py:272-446) and keeps that graph's bf16 rounding points:
 //
-//   qkv_rope_append   input_layernorm, q/k/v_proj, reshapes, rotary_embedding, KV append
-//   paged_attention   attention over the already appended paged KV cache (decode)
-//   linear_residual   o_proj + attention_residual, down_proj + mlp_residual
-//   gate_up_silu      post_attention_layernorm, gate_proj, up_proj, act_fn, mul
-//   lm_head_argmax    model.norm, lm_head, greedy argmax
-//   argmax            greedy argmax over the last dim (unfused graphs)
+//   qkv_rope_append        q/k/v_proj, reshapes, rotary_embedding, KV append (input: the
+//                          input_layernorm output)
+//   paged_attention        attention over the already appended paged KV cache (decode)
+//   linear_residual        o_proj + attention_residual, down_proj + mlp_residual
+//   linear_residual_norm   the same plus the RMSNorm that follows the residual update
+//                          (post_attention_layernorm, the next input_layernorm, model.norm)
+//   gate_up_silu           gate_proj, up_proj, act_fn, mul
+//   lm_head_argmax         lm_head, greedy argmax
+//   argmax                 greedy argmax over the last dim (unfused graphs)
 #include <cmath>
 #include <mutex>
 
@@ -22,9 +25,9 @@ void requireBf16(const Tensor& t, const std::string& op, const std::string& what
 
 std::int64_t rowsOf(const Tensor& t) { return product(t.shape(), 0, t.rank() - 1); }
 
-// Zero-initialised device scratch kept across calls (split-K tile counters must start at 0 and
-// are left at 0 by every kernel, so one buffer serves all nodes of an operator type in stream
-// order). Grows when a node needs more.
+// Device scratch kept across calls (split-K partials; every call overwrites what it reads, and
+// nodes of one operator instance run in stream order). Allocated zeroed outside any captured
+// region on first use; grows when a node needs more.
 class PersistentWorkspace {
  public:
   void* get(std::size_t bytes, int device_id) {
@@ -47,25 +50,21 @@ class QkvRopeAppendOp final : public Operator {
   std::string type() const override { return "qkv_rope_append"; }
   void compute(const std::vector<const Tensor*>& in, const std::vector<Tensor*>& out,
                const Attributes& attrs, ExecutionContext& ctx) const override {
-    requireArity(in, out, 7, 7, 1, type());
+    requireArity(in, out, 6, 6, 1, type());
     requireCudaInputs(in, type());
-    const Tensor &x = *in[0], &nw = *in[1], &w = *in[2], &b = *in[3], &cos = *in[4], &sin = *in[5],
-                 &pos = *in[6];
-    for (const Tensor* t : {&x, &nw, &w, &b}) requireBf16(*t, type(), "hidden/weights");
+    const Tensor &x = *in[0], &w = *in[1], &b = *in[2], &cos = *in[3], &sin = *in[4], &pos = *in[5];
+    for (const Tensor* t : {&x, &w, &b}) requireBf16(*t, type(), "activations/weights");
     requireFloat(cos, type());
     requireFloat(sin, type());
     requireIndex(pos, type(), "positions");
     const auto hq = attrs.require<std::int64_t>("q_heads");
     const auto hkv = attrs.require<std::int64_t>("kv_heads");
     const auto d = attrs.require<std::int64_t>("head_dim");
-    const auto eps = static_cast<float>(attrDouble(attrs, "eps", 1e-6));
-    const auto splits = static_cast<int>(attrs.value_or<std::int64_t>("splits", 1));
     const std::string& cache_name = attrs.require<std::string>("kv_cache");
     const std::int64_t hidden = x.shape().back();
     const std::int64_t m = rowsOf(x);
     const std::int64_t n = (hq + 2 * hkv) * d;
-    if (w.rank() != 2 || w.dim(0) != n || w.dim(1) != hidden || static_cast<std::int64_t>(b.numel()) != n ||
-        static_cast<std::int64_t>(nw.numel()) != hidden)
+    if (w.rank() != 2 || w.dim(0) != n || w.dim(1) != hidden || static_cast<std::int64_t>(b.numel()) != n)
       throw std::invalid_argument("qkv_rope_append weight shapes do not match the attributes");
     if (cos.rank() != 2 || cos.dim(1) != d / 2 || cos.shape() != sin.shape())
       throw std::invalid_argument("qkv_rope_append cos/sin must be [max_pos, head_dim/2]");
@@ -74,19 +73,14 @@ class QkvRopeAppendOp final : public Operator {
     if (ctx.kv_cache == nullptr) throw std::invalid_argument("qkv_rope_append missing KV cache");
     KVCacheEntry& e = ctx.kv_cache->reserve(cache_name, DType::BFloat16, m, hkv, d, x.deviceId());
     *out[0] = Tensor::cuda(DType::BFloat16, {m, hq, 1, d}, x.deviceId());
-    const std::size_t ws_bytes = dli_hip_splitk_workspace(n, m, splits);
     check(dli_hip_qkv_rope_append(
-              ptr(x), ptr(nw), ptr(w), ptr(b), static_cast<const float*>(ptr(cos)),
+              ptr(x), ptr(w), ptr(b), static_cast<const float*>(ptr(cos)),
               static_cast<const float*>(ptr(sin)), cos.dim(0), ptr(pos), hipDtype(pos.dtype()),
               ptr(*out[0]), ptr(e.key), ptr(e.value),
               static_cast<const std::int32_t*>(ptr(e.block_table)), e.block_size, e.max_blocks, m,
-              hidden, hq, hkv, d, eps, splits, workspace_.get(ws_bytes, x.deviceId()), ws_bytes,
-              ctx.stream),
+              hidden, hq, hkv, d, ctx.stream),
           type());
   }
-
- private:
-  mutable PersistentWorkspace workspace_;
 };
 
 // Decode attention over a cache entry whose newest token (at positions[b]) is already written.
@@ -153,44 +147,76 @@ class LinearResidualOp final : public Operator {
   mutable PersistentWorkspace workspace_;
 };
 
-// inputs: hidden [.., H], norm_weight [H], w_gate_up [2F, H] (16-row interleaved)
+// inputs: x [.., K], w [N, K], residual [.., N], norm_weight [N] (+ bias [N]);
+// outputs: h = residual + bf16(x w^T + b), xn = rms_norm(h) * norm_weight
+class LinearResidualNormOp final : public Operator {
+ public:
+  std::string type() const override { return "linear_residual_norm"; }
+  void compute(const std::vector<const Tensor*>& in, const std::vector<Tensor*>& out,
+               const Attributes& attrs, ExecutionContext& ctx) const override {
+    requireArity(in, out, 4, 5, 2, type());
+    requireCudaInputs(in, type());
+    for (const Tensor* t : in) requireBf16(*t, type(), "inputs");
+    const Tensor &x = *in[0], &w = *in[1], &res = *in[2], &nw = *in[3];
+    const std::int64_t k = x.shape().back(), m = rowsOf(x);
+    if (w.rank() != 2 || w.dim(1) != k) throw std::invalid_argument("linear_residual_norm weight shape mismatch");
+    const std::int64_t n = w.dim(0);
+    if (rowsOf(res) != m || res.shape().back() != n)
+      throw std::invalid_argument("linear_residual_norm residual shape mismatch");
+    if (static_cast<std::int64_t>(nw.numel()) != n)
+      throw std::invalid_argument("linear_residual_norm norm weight size mismatch");
+    if (in.size() == 5 && static_cast<std::int64_t>(in[4]->numel()) != n)
+      throw std::invalid_argument("linear_residual_norm bias size mismatch");
+    const auto splits = static_cast<int>(attrs.value_or<std::int64_t>("splits", 1));
+    const auto eps = static_cast<float>(attrDouble(attrs, "eps", 1e-6));
+    *out[0] = Tensor::cuda(DType::BFloat16, res.shape(), x.deviceId());
+    *out[1] = Tensor::cuda(DType::BFloat16, res.shape(), x.deviceId());
+    const std::size_t ws_bytes = dli_hip_splitk_workspace(n, m, splits);
+    check(dli_hip_linear_residual_norm(ptr(x), ptr(w), in.size() == 5 ? ptr(*in[4]) : nullptr,
+                                       ptr(res), ptr(nw), ptr(*out[0]), ptr(*out[1]), m, n, k, eps,
+                                       splits, workspace_.get(ws_bytes, x.deviceId()), ws_bytes,
+                                       ctx.stream),
+          type());
+  }
+
+ private:
+  mutable PersistentWorkspace workspace_;
+};
+
+// inputs: xn [.., H], w_gate_up [2F, H] (16-row interleaved)
 class GateUpSiluOp final : public Operator {
  public:
   std::string type() const override { return "gate_up_silu"; }
   void compute(const std::vector<const Tensor*>& in, const std::vector<Tensor*>& out,
-               const Attributes& attrs, ExecutionContext& ctx) const override {
-    requireArity(in, out, 3, 3, 1, type());
+               const Attributes&, ExecutionContext& ctx) const override {
+    requireArity(in, out, 2, 2, 1, type());
     requireCudaInputs(in, type());
     for (const Tensor* t : in) requireBf16(*t, type(), "inputs");
-    const Tensor &x = *in[0], &nw = *in[1], &w = *in[2];
+    const Tensor &x = *in[0], &w = *in[1];
     const std::int64_t hidden = x.shape().back(), m = rowsOf(x);
-    if (w.rank() != 2 || w.dim(1) != hidden || w.dim(0) % 2 != 0 ||
-        static_cast<std::int64_t>(nw.numel()) != hidden)
-      throw std::invalid_argument("gate_up_silu weight shapes mismatch");
+    if (w.rank() != 2 || w.dim(1) != hidden || w.dim(0) % 2 != 0)
+      throw std::invalid_argument("gate_up_silu weight shape mismatch");
     const std::int64_t f = w.dim(0) / 2;
-    const auto eps = static_cast<float>(attrDouble(attrs, "eps", 1e-6));
     *out[0] = Tensor::cuda(DType::BFloat16, withLast(x.shape(), f), x.deviceId());
-    check(dli_hip_gate_up_silu(ptr(x), ptr(nw), ptr(w), ptr(*out[0]), m, f, hidden, eps, ctx.stream),
-          type());
+    check(dli_hip_gate_up_silu(ptr(x), ptr(w), ptr(*out[0]), m, f, hidden, ctx.stream), type());
   }
 };
 
-// inputs: hidden [B, H], norm_weight [H], w [V, H]; outputs: (logits [B, V],) next_ids int64 [B]
+// inputs: xn [B, H], w [V, H]; outputs: (logits [B, V],) next_ids int64 [B]
 class LmHeadArgmaxOp final : public Operator {
  public:
   std::string type() const override { return "lm_head_argmax"; }
   void compute(const std::vector<const Tensor*>& in, const std::vector<Tensor*>& out,
                const Attributes& attrs, ExecutionContext& ctx) const override {
     if (out.size() != 1 && out.size() != 2) throw std::invalid_argument("lm_head_argmax arity");
-    requireArity(in, out, 3, 3, out.size(), type());
+    requireArity(in, out, 2, 2, out.size(), type());
     requireCudaInputs(in, type());
     for (const Tensor* t : in) requireBf16(*t, type(), "inputs");
-    const Tensor &x = *in[0], &nw = *in[1], &w = *in[2];
+    const Tensor &x = *in[0], &w = *in[1];
     const std::int64_t hidden = x.shape().back(), m = rowsOf(x);
-    if (w.rank() != 2 || w.dim(1) != hidden || static_cast<std::int64_t>(nw.numel()) != hidden)
-      throw std::invalid_argument("lm_head_argmax weight shapes mismatch");
+    if (w.rank() != 2 || w.dim(1) != hidden)
+      throw std::invalid_argument("lm_head_argmax weight shape mismatch");
     const std::int64_t vocab = w.dim(0);
-    const auto eps = static_cast<float>(attrDouble(attrs, "eps", 1e-6));
     const DType logits_dtype = dtypeFromString(attrs.value_or<std::string>("logits_dtype", "float32"));
     Tensor* logits = out.size() == 2 ? out[0] : nullptr;
     Tensor* ids = out.back();
@@ -198,9 +224,9 @@ class LmHeadArgmaxOp final : public Operator {
     *ids = Tensor::cuda(DType::Int64, {m}, x.deviceId());
     const std::size_t ws_bytes = dli_hip_lm_head_argmax_workspace(m, vocab);
     Tensor ws = Tensor::cuda(DType::Float32, {static_cast<std::int64_t>((ws_bytes + 3) / 4)}, x.deviceId());
-    check(dli_hip_lm_head_argmax(ptr(x), ptr(nw), ptr(w), logits ? ptr(*logits) : nullptr,
+    check(dli_hip_lm_head_argmax(ptr(x), ptr(w), logits ? ptr(*logits) : nullptr,
                                  hipDtype(logits_dtype), static_cast<std::int64_t*>(ptr(*ids)), m,
-                                 vocab, hidden, eps, ptr(ws), ws_bytes, ctx.stream),
+                                 vocab, hidden, ptr(ws), ws_bytes, ctx.stream),
           type());
   }
 };
@@ -230,6 +256,7 @@ void registerFusedOps(OperatorRegistry* registry) {
   add<QkvRopeAppendOp>(registry);
   add<PagedAttentionOp>(registry);
   add<LinearResidualOp>(registry);
+  add<LinearResidualNormOp>(registry);
   add<GateUpSiluOp>(registry);
   add<LmHeadArgmaxOp>(registry);
   add<ArgmaxOp>(registry);

@@ -1,0 +1,170 @@
+"""Per-operator parity of the fused decode operators (plugin ops qkv_rope_append,
+linear_residual, linear_residual_norm, gate_up_silu, lm_head_argmax) against the CPU oracle.
+
+Each fused op stands for a run of nodes of the reference's decoder graph
+(python/dli_export/export.py:272-446) with every node's bf16 rounding point; the oracle applies
+oracle/ops.py's restatements of those nodes in float64 and rounds at the same points
+(round_bf16). Tolerance: bf16 2e-2. Argmax results are exact: the lm_head test builds integer
+logits (exact in fp32 in any summation order) with ties inside one tile and across workgroups.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import dli
+from dli_qwen2.graph import interleave_gate_up
+from oracle import ops
+from support import assert_close, run_op, to_np
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+R = ops.round_bf16
+
+
+def rand(shape, seed, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(shape, generator=g) * scale).to(torch.bfloat16).to(DEV)
+
+
+def rope_tables(max_pos, d, theta=10000.0):
+    inv = 1.0 / theta ** (torch.arange(0, d, 2, dtype=torch.float64) / d)
+    f = torch.outer(torch.arange(max_pos, dtype=torch.float64), inv)
+    return f.cos().float().to(DEV), f.sin().float().to(DEV)
+
+
+@pytest.mark.parametrize("B,H,hq,hkv,positions", [
+    (1, 128, 2, 1, [0]),
+    (5, 256, 4, 2, [0, 63, 64, 130, 5]),
+    (32, 896, 14, 2, None),   # Qwen2-0.5B shape, positions spread over 4 cache blocks
+    (40, 256, 4, 2, None),    # 33..64 rows
+])
+def test_qkv_rope_append(B, H, hq, hkv, positions):
+    d = 64
+    n = (hq + 2 * hkv) * d
+    if positions is None:
+        positions = [(7 * b + 3) % 250 for b in range(B)]
+    x, w, b = rand((B, H), 1), rand((n, H), 2, 0.05), rand((n,), 3, 0.1)
+    cos, sin = rope_tables(256, d)
+    pos = torch.tensor(positions, dtype=torch.int64, device=DEV)
+    e = dli.Engine().load_plugin()
+    e.configure_kv_cache(block_size=64, max_seq_len=256)
+    out = run_op("qkv_rope_append", {"x": x, "w": w, "b": b, "cos": cos, "sin": sin, "pos": pos},
+                 attrs={"kv_cache": "L", "q_heads": hq, "kv_heads": hkv, "head_dim": d},
+                 engine=e)["output"]
+    y = R(ops.linear(to_np(x), to_np(w), to_np(b)))  # [B, n]
+    q = y[:, :hq * d].reshape(B, hq, 1, d)
+    k = y[:, hq * d:(hq + hkv) * d].reshape(B, hkv, 1, d)
+    v = y[:, (hq + hkv) * d:].reshape(B, hkv, 1, d)
+    pnp = np.asarray(positions)
+    q = R(ops.rotary(q, to_np(cos), to_np(sin), positions=pnp))
+    k = R(ops.rotary(k, to_np(cos), to_np(sin), positions=pnp))
+    assert_close(out, q, "bfloat16")
+    entry = e.kv_cache_entry("L")
+    kp, vp, table = to_np(entry["key"]), to_np(entry["value"]), entry["block_table"].cpu().numpy()
+    bs = entry["block_size"]
+    for i, p in enumerate(positions):
+        blk = table[i, p // bs]
+        assert_close(kp[blk, :, p % bs, :], k[i, :, 0, :], "bfloat16")
+        assert_close(vp[blk, :, :, p % bs], v[i, :, 0, :], "bfloat16")
+    # nothing else was written: every other slot of the zero-initialised pools is still zero
+    written = np.zeros(kp.shape[0] * bs, bool)
+    for i, p in enumerate(positions):
+        written[table[i, p // bs] * bs + p % bs] = True
+    k_slots = np.abs(kp).sum(axis=(1, 3)).reshape(-1)
+    v_slots = np.abs(vp).sum(axis=(1, 2)).reshape(-1)
+    assert not k_slots[~written].any() and not v_slots[~written].any()
+
+
+def _residual_oracle(x, w, res, bias):
+    y = ops.linear(to_np(x), to_np(w), None if bias is None else to_np(bias))
+    return R(to_np(res) + R(y))
+
+
+CASES = [  # B, N, K, splits, bias
+    (1, 128, 256, 1, False),
+    (5, 896, 896, 2, True),
+    (32, 896, 896, 4, False),
+    (32, 896, 4864, 8, False),
+    (33, 896, 4864, 4, False),
+    (64, 256, 512, 8, True),
+]
+
+
+@pytest.mark.parametrize("B,N,K,splits,bias", CASES)
+def test_linear_residual_norm(B, N, K, splits, bias):
+    x, w, res = rand((B, K), 10), rand((N, K), 11, 0.03), rand((B, N), 12)
+    nw = (1 + rand((N,), 13, 0.1).float()).to(torch.bfloat16)
+    inputs = {"x": x, "w": w, "res": res, "nw": nw}
+    if bias:
+        inputs["b"] = rand((N,), 14, 0.1)
+    out = run_op("linear_residual_norm", inputs, outputs=("h", "xn"),
+                 attrs={"splits": splits, "eps": 1e-6})
+    h = _residual_oracle(x, w, res, inputs.get("b"))
+    assert_close(out["h"], h, "bfloat16")
+    assert_close(out["xn"], R(ops.rms_norm(h, to_np(nw), 1e-6)), "bfloat16")
+
+
+@pytest.mark.parametrize("B,N,K,splits,bias", CASES[:3] + [(16, 4096, 1024, 1, True)])
+def test_linear_residual(B, N, K, splits, bias):
+    if N > 1024 and splits > 1:
+        pytest.skip("split-K path is limited to n <= 1024")
+    x, w, res = rand((B, K), 20), rand((N, K), 21, 0.03), rand((B, N), 22)
+    inputs = {"x": x, "w": w, "res": res}
+    if bias:
+        inputs["b"] = rand((N,), 23, 0.1)
+    out = run_op("linear_residual", inputs, attrs={"splits": splits})["output"]
+    assert_close(out, _residual_oracle(x, w, res, inputs.get("b")), "bfloat16")
+
+
+@pytest.mark.parametrize("B,H,F", [(1, 128, 64), (7, 896, 4864), (32, 896, 4864), (64, 256, 512)])
+def test_gate_up_silu(B, H, F):
+    x, wg, wu = rand((B, H), 30), rand((F, H), 31, 0.05), rand((F, H), 32, 0.05)
+    out = run_op("gate_up_silu", {"x": x, "w": interleave_gate_up(wg, wu)})["output"]
+    g = R(ops.linear(to_np(x), to_np(wg)))
+    u = R(ops.linear(to_np(x), to_np(wu)))
+    assert_close(out, R(R(ops.silu(g)) * u), "bfloat16")
+
+
+@pytest.mark.parametrize("B,H,V", [(1, 128, 1000), (5, 896, 4099), (32, 896, 151936 // 8),
+                                   (48, 256, 777)])
+@pytest.mark.parametrize("logits_dtype", ["float32", "bfloat16"])
+def test_lm_head_argmax(B, H, V, logits_dtype):
+    g = torch.Generator().manual_seed(40 + B)
+    # small integers: every partial sum is exact in fp32, so logits are exact and ties are real
+    x = torch.randint(-2, 3, (B, H), generator=g).to(torch.bfloat16)
+    w = torch.randint(-1, 2, (V, H), generator=g).to(torch.bfloat16)
+    best = torch.sign(x.float()).to(torch.bfloat16)  # maximises row's logit: sum |x|
+    if V > 700:
+        w[3], w[700] = best[0], best[0]        # tie across workgroups (256 rows each)
+    if B > 1:
+        w[9], w[5] = best[1], best[1]          # tie inside one 32-row tile, lower index second
+    x, w = x.to(DEV), w.to(DEV)
+    out = run_op("lm_head_argmax", {"x": x, "w": w}, outputs=("logits", "ids"),
+                 attrs={"logits_dtype": logits_dtype})
+    exact = to_np(x) @ to_np(w).T
+    ids = out["ids"].cpu().numpy()
+    np.testing.assert_array_equal(ids, np.argmax(exact, axis=-1))
+    if V > 700:
+        assert ids[0] == 3
+    if B > 1:
+        assert ids[1] == 5
+    expect = exact if logits_dtype == "float32" else R(exact)
+    np.testing.assert_array_equal(to_np(out["logits"]), expect)
+
+
+def test_lm_head_argmax_random_logits_match_oracle():
+    B, H, V = 32, 896, 20000
+    x, w = rand((B, H), 50), rand((V, H), 51, 0.05)
+    out = run_op("lm_head_argmax", {"x": x, "w": w}, outputs=("logits", "ids"))
+    ref = ops.linear(to_np(x), to_np(w))
+    assert_close(out["logits"], ref, "float32", rtol=1e-4, atol=1e-4)
+    ids = out["ids"].cpu().numpy()
+    np.testing.assert_array_equal(ids, np.argmax(to_np(out["logits"]), axis=-1))
+    top2 = np.sort(ref, axis=-1)[:, -2:]
+    clear = (top2[:, 1] - top2[:, 0]) > 1e-3  # rows whose winner the fp32 sums cannot flip
+    np.testing.assert_array_equal(ids[clear], np.argmax(ref, axis=-1)[clear])

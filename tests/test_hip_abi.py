@@ -71,3 +71,29 @@ def test_invalid_arguments_are_rejected_with_a_message():
     assert lib.dli_hip_rotary(hip.F32, None, None, None, None, None, None, 1, 1, 1, 1, 3, 1, 4, 0,
                               None, hip.I64, None) == -1
     assert lib.dli_hip_linear(hip.BF16, hip.F16, None, None, None, None, 1, 1, 1, None) == -1
+
+
+def test_fused_decode_entry_points_reject_invalid_arguments():
+    lib = hip.load()
+    # residual + RMSNorm kernel holds a row of at most 1024 columns
+    assert lib.dli_hip_linear_residual_norm(None, None, None, None, None, None, None, 2, 64, 64,
+                                            1e-6, 1, None, 0, None) == -1
+    assert b"norm_weight and xn_out are required" in lib.dli_hip_last_error()
+    fake = ctypes.c_void_p(256)  # never dereferenced: the size check comes first
+    assert lib.dli_hip_linear_residual_norm(None, None, None, None, fake, None, fake, 2, 2048, 64,
+                                            1e-6, 1, None, 0, None) == -1
+    assert b"n must be in [1, 1024]" in lib.dli_hip_last_error()
+    assert lib.dli_hip_linear_residual_norm(None, None, None, None, fake, None, fake, 2, 64, 128,
+                                            1e-6, 3, None, 0, None) == -1  # 3 > k / 64
+    assert b"splits must be in" in lib.dli_hip_last_error()
+    assert lib.dli_hip_linear_residual(None, None, None, None, None, 2, 64, 128, 0, None, 0,
+                                       None) == -1
+    assert lib.dli_hip_lm_head_argmax(None, None, None, hip.F32, None, 2, 100, 2048, None, 0,
+                                      None) == -1
+    assert b"hidden_size above 1024" in lib.dli_hip_last_error()
+    assert lib.dli_hip_gate_up_silu(None, None, None, 65, 32, 64, None) == -1
+    assert b"batch rows" in lib.dli_hip_last_error()
+    assert lib.dli_hip_qkv_rope_append(None, None, None, None, None, 8, None, hip.I64, None, None,
+                                       None, None, 64, 1, 2, 64, 2, 1, 16, None) == -1
+    assert b"positions" in lib.dli_hip_last_error()
+    assert lib.dli_hip_splitk_workspace(896, 32, 4) == 4 * 32 * 896 * 4
