@@ -142,7 +142,7 @@ def main():
     out = torch.empty_like(q)
     ws_bytes = hip.lib().dli_hip_paged_attention_workspace(B, cfg.heads, 1, cfg.head_dim,
                                                             e["max_blocks"] * e["block_size"])
-    ws = torch.empty((ws_bytes + 3) // 4, dtype=torch.float32, device=dev)
+    ws = torch.zeros((ws_bytes + 3) // 4, dtype=torch.float32, device=dev)  # counters start at 0
     s_ptr = stream.cuda_stream
 
     def attn():

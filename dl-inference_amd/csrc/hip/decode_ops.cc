@@ -13,10 +13,9 @@ constexpr int kThreads = 256;
 constexpr int kTileN = 32;           // weight rows per workgroup of gate_up / lm_head (NF = 2)
 constexpr int kRowTile = 16;         // weight rows per workgroup of qkv / linear_residual / partial
 constexpr int kResWaves = 8;         // waves per linear_residual workgroup
-constexpr int kLmTilesPerBlock = 8;  // vocab tiles per lm_head workgroup
 constexpr int64_t kMaxNormN = 1024;  // residual_rms_norm: 256 threads x 4 columns
-constexpr int64_t kMaxLmK = 1024;    // lm_head keeps x for K / 64 <= 16 steps in registers
-constexpr int kMaxDecodeSplits = 32; // kMaxSplits of the combine kernel
+constexpr int64_t kMaxLmK = 1024;    // tile loops keep x for K / 64 <= 16 steps in registers
+constexpr int kMaxDecodeSplits = 32; // splits a decode-attention call may use
 
 struct MbKernels {
   DeviceKernel m1, m2, m4;
@@ -38,13 +37,22 @@ MbKernels k_lm_head("decode", "lm_head_argmax");
 DeviceKernel k_res_norm("decode", "residual_rms_norm");
 DeviceKernel k_argmax_final("decode", "argmax_finalize");
 DeviceKernel k_dec_attn("attention", "decode_attention_d64");
-DeviceKernel k_dec_combine("attention", "decode_attention_combine_d64");
 
 int bad(const char* op, const std::string& what) {
   return fail(DLI_HIP_EINVAL, std::string(op) + ": " + what);
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Workgroups of a grid-strided tile loop: one per tile, at most as many as are resident at once
+// (two 256-thread workgroups per CU fit below 256 VGPRs; the 64-row variants use more).
+int tileGrid(int64_t tiles, int64_t m, unsigned* grid) {
+  int cus = 0;
+  if (int rc = computeUnits(&cus)) return rc;
+  const int64_t resident = static_cast<int64_t>(cus) * (m <= 32 ? 2 : 1);
+  *grid = static_cast<unsigned>(tiles < resident ? tiles : resident);
+  return 0;
+}
 
 int checkSkinny(const char* op, int64_t m, int64_t k) {
   if (m <= 0 || m > 64) return bad(op, "batch rows must be in [1, 64]");
@@ -145,9 +153,12 @@ int dli_hip_gate_up_silu(const void* xn, const void* w_gate_up, void* out, int64
   const char* op = "gate_up_silu";
   if (int rc = checkSkinny(op, m, hidden_size)) return rc;
   if (ffn <= 0 || ffn % 16 != 0) return bad(op, "ffn must be a positive multiple of 16");
+  if (hidden_size > kMaxLmK) return bad(op, "hidden_size above 1024 is not supported");
   if (!aligned16(xn) || !aligned16(w_gate_up)) return bad(op, "xn and w_gate_up must be 16-byte aligned");
-  return launch(*k_gate_up.pick(m), {static_cast<unsigned>(ffn / 16)}, {kThreads}, 0, stream, xn,
-                w_gate_up, out, static_cast<int>(m), ffn, static_cast<int>(hidden_size));
+  unsigned grid = 0;
+  if (int rc = tileGrid(ffn / 16, m, &grid)) return rc;
+  return launch(*k_gate_up.pick(m), {grid}, {kThreads}, 0, stream, xn, w_gate_up, out,
+                static_cast<int>(m), ffn, static_cast<int>(hidden_size));
 }
 
 size_t dli_hip_lm_head_argmax_workspace(int64_t m, int64_t vocab) {
@@ -169,11 +180,12 @@ int dli_hip_lm_head_argmax(const void* xn, const void* w, void* logits, int logi
     return bad(op, "workspace too small");
   if (!aligned16(xn) || !aligned16(w)) return bad(op, "xn and w must be 16-byte aligned");
   const int64_t tiles = (vocab + kTileN - 1) / kTileN;
-  const int64_t blocks = (tiles + kLmTilesPerBlock - 1) / kLmTilesPerBlock;
+  unsigned blocks = 0;
+  if (int rc = tileGrid(tiles, m, &blocks)) return rc;
   float* part_val = static_cast<float*>(workspace);
   int32_t* part_idx = reinterpret_cast<int32_t*>(part_val + tiles * m);
   const int logits_f32 = logits_dtype == DLI_F32 ? 1 : 0;
-  if (int rc = launch(*k_lm_head.pick(m), {static_cast<unsigned>(blocks)}, {kThreads}, 0, stream,
+  if (int rc = launch(*k_lm_head.pick(m), {blocks}, {kThreads}, 0, stream,
                       xn, w, logits, logits_f32, part_val, part_idx, static_cast<int>(m), vocab,
                       static_cast<int>(hidden_size)))
     return rc;
@@ -189,26 +201,38 @@ namespace dli::hip {
 // MFMA decode attention (one query per sequence, bf16, head_dim 64, 64-key cache blocks); used
 // by dli_hip_paged_attention when the case fits. Returns 1 when it does not apply.
 //
-// Splits along the keys: enough (sequence, kv head, split) workgroups to cover the 256 CUs, at
-// least kDecWaves cache blocks per split. One split writes the output directly; more splits
-// go through the combine kernel. DLI_ATTN_SPLITS=<n> overrides the choice (tuning).
+// Splits along the keys: at most one (sequence, kv head, split) workgroup per CU, so the whole
+// grid runs in one round (the kernel fits one 8-wave workgroup per CU); the blocks of a
+// sequence are dealt round-robin over all waves of its splits. The last split of a (sequence,
+// kv head) to finish merges the partials (agent-scope stores and loads plus a per-(sequence,
+// kv head) counter in the workspace, which it leaves at zero). DLI_ATTN_SPLITS=<n> overrides
+// the split count (tuning).
 namespace {
 constexpr int kDecWaves = 8;
 constexpr int kDecBlock = 64;
 
-int chooseSplits(int64_t pairs, int64_t max_blocks) {
+size_t alignUp(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// Workspace: partials [ml: rows x splits x 2][o: rows x splits x 64] fp32 inside a region sized
+// for kMaxDecodeSplits, then per-(sequence, kv head) arrival counters (rows of them, which is
+// at least batch * kv_heads), 256-B aligned.
+size_t partialBytes(int64_t rows) {
+  return alignUp(static_cast<size_t>(rows) * kMaxDecodeSplits * (2 + 64) * sizeof(float), 256);
+}
+
+int chooseSplits(int64_t pairs, int64_t max_blocks, int cus) {
   static const int forced = [] {
     const char* v = std::getenv("DLI_ATTN_SPLITS");
     return v ? std::atoi(v) : 0;
   }();
-  int64_t splits = forced > 0 ? forced : (256 + pairs - 1) / pairs;
-  const int64_t max_by_blocks = (max_blocks + kDecWaves - 1) / kDecWaves;
-  if (splits > max_by_blocks) splits = max_by_blocks;
-  // each wave keeps the ids of its blocks in one register across the 64 lanes
-  const int64_t min_splits = (max_blocks + kDecWaves * 64 - 1) / (kDecWaves * 64);
-  if (splits < min_splits) splits = min_splits;
-  if (splits > kMaxDecodeSplits) splits = kMaxDecodeSplits;
-  return static_cast<int>(splits < 1 ? 1 : splits);
+  int64_t splits = forced > 0 ? forced : cus / pairs;
+  // no more splits than wave groups of blocks, never fewer than the block ids allow
+  const int64_t useful = (max_blocks + kDecWaves - 1) / kDecWaves;
+  if (splits > useful) splits = useful;
+  const int64_t needed = (max_blocks + kDecWaves * 64 - 1) / (kDecWaves * 64);
+  if (splits < needed) splits = needed;
+  if (splits < 1) splits = 1;
+  return static_cast<int>(splits);
 }
 }  // namespace
 
@@ -222,32 +246,33 @@ int decodeAttentionFast(int dtype, const void* q, const void* key_pool, const vo
       block_size != kDecBlock || !aligned16(q))
     return 1;
   if (batch * kv_heads > 65535) return 1;
-  const int splits = chooseSplits(batch * kv_heads, max_blocks);
-  const int blocks_per_split = static_cast<int>((max_blocks + splits - 1) / splits);
-  const size_t need = static_cast<size_t>(batch * q_heads) * splits * (2 + 64) * sizeof(float);
+  int cus = 0;
+  if (int rc = computeUnits(&cus)) return rc;
+  const int splits = chooseSplits(batch * kv_heads, max_blocks, cus);
+  if (splits > kMaxDecodeSplits) return 1;
+  const int64_t rows = batch * q_heads;
+  const size_t need = partialBytes(rows) + static_cast<size_t>(rows) * sizeof(unsigned);
   if (splits > 1 && (workspace == nullptr || workspace_bytes < need)) return 1;
   float* ws_ml = static_cast<float*>(workspace);
-  float* ws_o = splits > 1 ? ws_ml + batch * q_heads * splits * 2 : nullptr;
+  float* ws_o = splits > 1 ? ws_ml + rows * splits * 2 : nullptr;
+  unsigned* counters =
+      splits > 1 ? reinterpret_cast<unsigned*>(static_cast<char*>(workspace) + partialBytes(rows))
+                 : nullptr;
   const int pos64 = positions_dtype == DLI_I64 ? 1 : 0;
   const float scale_log2 = scale * 1.4426950408889634f;
-  if (int rc = launch(k_dec_attn, {static_cast<unsigned>(splits), static_cast<unsigned>(batch * kv_heads)},
-                      {kDecWaves * 64}, 0, stream, static_cast<const uint16_t*>(q),
-                      static_cast<const uint16_t*>(key_pool), static_cast<const uint16_t*>(value_pool),
-                      block_table, positions, pos64, past, ws_ml, ws_o, static_cast<uint16_t*>(out),
-                      static_cast<int>(q_heads), static_cast<int>(kv_heads), max_blocks,
-                      blocks_per_split, splits, scale_log2))
-    return rc;
-  if (splits == 1) return 0;
-  return launch(k_dec_combine, {static_cast<unsigned>(batch * q_heads)}, {64}, 0, stream,
-                static_cast<const float*>(ws_ml), static_cast<const float*>(ws_o), positions, pos64,
-                past, static_cast<uint16_t*>(out), static_cast<int>(q_heads),
-                max_blocks * block_size, blocks_per_split * kDecBlock, splits);
+  return launch(k_dec_attn, {static_cast<unsigned>(splits), static_cast<unsigned>(batch * kv_heads)},
+                {kDecWaves * 64}, 0, stream, static_cast<const uint16_t*>(q),
+                static_cast<const uint16_t*>(key_pool), static_cast<const uint16_t*>(value_pool),
+                block_table, positions, pos64, past, ws_ml, ws_o, counters,
+                static_cast<uint16_t*>(out), static_cast<int>(q_heads), static_cast<int>(kv_heads),
+                max_blocks, splits, scale_log2);
 }
 
 size_t decodeAttentionWorkspace(int64_t batch, int64_t q_heads, int64_t seq_q, int64_t head_dim,
                                 int64_t max_tokens) {
   if (seq_q != 1 || head_dim != 64) return 0;
-  return static_cast<size_t>(batch * q_heads) * kMaxDecodeSplits * (2 + 64) * sizeof(float);
+  const int64_t rows = batch * q_heads;
+  return partialBytes(rows) + static_cast<size_t>(rows) * sizeof(unsigned);
 }
 
 }  // namespace dli::hip

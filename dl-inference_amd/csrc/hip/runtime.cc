@@ -48,6 +48,7 @@ struct Runtime {
   Status (*eventSynchronize)(EventT) = nullptr;
   Status (*eventElapsedTime)(float*, EventT, EventT) = nullptr;
   Status (*eventDestroy)(EventT) = nullptr;
+  Status (*deviceGetAttribute)(int*, int, int) = nullptr;
 
   template <typename F>
   bool bind(F& slot, const char* symbol) {
@@ -81,7 +82,8 @@ struct Runtime {
                     bind(eventCreate, "hipEventCreate") && bind(eventRecord, "hipEventRecord") &&
                     bind(eventSynchronize, "hipEventSynchronize") &&
                     bind(eventElapsedTime, "hipEventElapsedTime") &&
-                    bind(eventDestroy, "hipEventDestroy");
+                    bind(eventDestroy, "hipEventDestroy") &&
+                    bind(deviceGetAttribute, "hipDeviceGetAttribute");
     if (!ok) {
       dlclose(handle);
       handle = nullptr;
@@ -171,6 +173,24 @@ int requireRuntime() {
   return 0;
 }
 
+int computeUnits(int* count) {
+  constexpr int kMultiprocessorCount = 63;  // hipDeviceAttributeMultiprocessorCount
+  static std::array<std::atomic<int>, 64> cached{};
+  if (int rc = requireRuntime()) return rc;
+  int device = 0;
+  if (int rc = check(runtime().getDevice(&device), "hipGetDevice")) return rc;
+  if (device < 0 || device >= 64) return fail(DLI_HIP_EINVAL, "device index out of range");
+  int value = cached[device].load(std::memory_order_relaxed);
+  if (value <= 0) {
+    if (int rc = check(runtime().deviceGetAttribute(&value, kMultiprocessorCount, device),
+                       "hipDeviceGetAttribute"))
+      return rc;
+    cached[device].store(value, std::memory_order_relaxed);
+  }
+  *count = value;
+  return 0;
+}
+
 int DeviceKernel::resolve(void** function) {
   if (int rc = requireRuntime()) return rc;
   int device = 0;
@@ -231,6 +251,11 @@ int dli_hip_get_device(int* device) {
   if (device == nullptr) return fail(DLI_HIP_EINVAL, "device is NULL");
   if (int rc = requireRuntime()) return rc;
   return check(runtime().getDevice(device), "hipGetDevice");
+}
+
+int dli_hip_compute_units(int* count) {
+  if (count == nullptr) return fail(DLI_HIP_EINVAL, "count is NULL");
+  return dli::hip::computeUnits(count);
 }
 
 int dli_hip_set_device(int device) {

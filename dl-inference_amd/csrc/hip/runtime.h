@@ -23,6 +23,8 @@ int fail(int code, const std::string& message);
 // Maps a hipError_t to 0 / a recorded error with context.
 int check(int hip_status, const char* what);
 int requireRuntime();
+// Compute units of the current device (cached per device).
+int computeUnits(int* count);
 
 // A kernel by name inside one embedded code object; resolved once per device.
 class DeviceKernel {

@@ -17,6 +17,9 @@
 //                      16-row blocks: [gate 16 rows | up 16 rows] per output block of 16)
 //  lm_head_argmax      logits = xn W^T (fp32) -> logits out + per-tile argmax partials;
 //                      argmax_finalize reduces them (first index of the maximum)
+// gate_up_silu and lm_head_argmax walk their weight tiles grid-strided (tileLoop), sized by the
+// host to the workgroups that are resident at once, so the weight stream never waits on a
+// second dispatch round.
 #include "common.h"
 #include "skinny.h"
 
@@ -27,7 +30,6 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
 constexpr int kResWaves = 8;         // linear_residual: 8 waves split K inside a workgroup
-constexpr int kLmTilesPerBlock = 8;  // lm_head_argmax: 8 x 32 vocab rows per workgroup
 constexpr int kNormPer = 4;          // residual_rms_norm: N <= kThreads * kNormPer
 
 // Steps [begin, end) of split `split` out of `splits` over `steps` 64-column steps.
@@ -227,94 +229,68 @@ __device__ void residual_rms_norm_impl(const float* partials, int splits, const 
   }
 }
 
+// Weight tiles t = blockIdx.x, + gridDim.x, ... (16 * NF rows each) against one x whose
+// fragments are loaded once and stay in registers; the next tile's weights stream in while the
+// current one is multiplied. epi(t) reads the reduced tile [16 NF][16 MB] from lds (its row n,
+// column m at lds[n * 16 MB + m]). Requires K / 64 <= 4 * kWaves.
+template <int NF, int MB, typename Epi>
+__device__ __forceinline__ void tileLoop(const uint16_t* w, const XGlobal& xs, int64_t N, int K,
+                                         int M, float* lds, Epi&& epi) {
+  using Core = SkinnyCore<NF, MB, kWaves>;
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int r = lane % 16, g = lane / 16;
+  const int steps = K / 64;
+  const int64_t tiles = (N + Core::kTileN - 1) / Core::kTileN;
+  const int64_t stride = gridDim.x;
+  int64_t t = blockIdx.x;
+  if (t >= tiles) return;
+  typename Core::WBatch bufA, bufB;
+  typename Core::XBatch xb;
+  Core::issueW(bufA, Core::rows(w, N, K, t * Core::kTileN, r, g), wave, steps);
+  Core::issueX(xb, xs, M, wave, steps, r, g);
+  auto tile = [&](const typename Core::WBatch& wb, int64_t tt) {
+    f32x4 acc[NF][MB];
+    Core::zero(acc);
+    Core::compute(acc, wb, xb, wave, steps);
+    Core::reduce(acc, lds, r, g, wave);
+    epi(tt);
+    __syncthreads();  // lds is reused by the next tile
+  };
+  for (; t < tiles; t += 2 * stride) {
+    if (t + stride < tiles)
+      Core::issueW(bufB, Core::rows(w, N, K, (t + stride) * Core::kTileN, r, g), wave, steps);
+    tile(bufA, t);
+    if (t + stride >= tiles) break;
+    if (t + 2 * stride < tiles)
+      Core::issueW(bufA, Core::rows(w, N, K, (t + 2 * stride) * Core::kTileN, r, g), wave, steps);
+    tile(bufB, t + stride);
+  }
+}
+
 template <int MB>
 __device__ void gate_up_silu_impl(const uint16_t* xn, const uint16_t* w_gu, uint16_t* out, int M,
                                   int64_t F, int K) {
   using Core = SkinnyCore<2, MB, kWaves>;
   __shared__ float lds[Core::kLdsFloats];
-  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * Core::kTileN;  // rows of w_gu
-  Core::run(w_gu, XGlobal{xn, K}, 2 * F, K, M, n0, 0, K / 64, lds);
-  const int64_t f0 = static_cast<int64_t>(blockIdx.x) * 16;
-  for (int idx = threadIdx.x; idx < 16 * Core::kTileM; idx += blockDim.x) {
-    const int j = idx % 16, m = idx / 16;
-    const int64_t f = f0 + j;
-    if (m >= M || f >= F) continue;
-    const float g = roundBf16(lds[j * Core::kTileM + m]);
-    const float u = roundBf16(lds[(16 + j) * Core::kTileM + m]);
-    const float s = roundBf16(g / (1.0f + expf(-g)));
-    out[m * F + f] = floatToBf16(s * u);
-  }
+  tileLoop<2, MB>(w_gu, XGlobal{xn, K}, 2 * F, K, M, lds, [&](int64_t t) {
+    const int64_t f0 = t * 16;  // tile t = gate rows [16t, 16t+16) then up rows [16t, 16t+16)
+    for (int idx = threadIdx.x; idx < 16 * Core::kTileM; idx += blockDim.x) {
+      const int j = idx % 16, m = idx / 16;
+      const int64_t f = f0 + j;
+      if (m >= M || f >= F) continue;
+      const float g = roundBf16(lds[j * Core::kTileM + m]);
+      const float u = roundBf16(lds[(16 + j) * Core::kTileM + m]);
+      const float s = roundBf16(g / (1.0f + expf(-g)));
+      out[m * F + f] = floatToBf16(s * u);
+    }
+  });
 }
 
 constexpr int kLmTileN = 32;  // vocab rows per lm_head tile (NF = 2)
 constexpr int kLmQuarters = kLmTileN / 4;
 
-// Multiplies one vocab tile (weights in `wb`, x fragments in `xb`), stores its logits and the
-// tile's argmax partial per row: part_*[m * tiles + t].
-template <int MB>
-__device__ __forceinline__ void lmHeadTile(const typename SkinnyCore<2, MB, kWaves>::WBatch& wb,
-                           const typename SkinnyCore<2, MB, kWaves>::XBatch& xb, float* lds,
-                           int* lds_arg, void* logits, int logits_f32, float* part_val,
-                           int32_t* part_idx, int M, int64_t V, int64_t tiles, int64_t t,
-                           int steps, int r, int g, int wave) {
-  using Core = SkinnyCore<2, MB, kWaves>;
-  f32x4 acc[2][MB];
-  Core::zero(acc);
-  Core::compute(acc, wb, xb, wave, steps);
-  Core::reduce(acc, lds, r, g, wave);
-  const int64_t n0 = t * Core::kTileN;
-  if (logits != nullptr) {
-    for (int idx = threadIdx.x; idx < Core::kTileN * Core::kTileM; idx += blockDim.x) {
-      const int nl = idx % Core::kTileN, m = idx / Core::kTileN;  // n fastest: coalesced stores
-      const int64_t n = n0 + nl;
-      if (m >= M || n >= V) continue;
-      const float v = lds[nl * Core::kTileM + m];
-      if (logits_f32)
-        static_cast<float*>(logits)[m * V + n] = v;
-      else
-        static_cast<uint16_t*>(logits)[m * V + n] = floatToBf16(v);
-    }
-  }
-  // argmax: thread (m, q) scans rows 4q..4q+3 of the tile, then one thread per m merges the
-  // quarters in order (first index among equal maxima).
-  float* qv = lds + Core::kTileN * Core::kTileM;
-  for (int idx = threadIdx.x; idx < kLmQuarters * Core::kTileM; idx += blockDim.x) {
-    const int m = idx % Core::kTileM, q = idx / Core::kTileM;
-    float best = -INFINITY;
-    int arg = -1;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int nl = q * 4 + j;
-      const float v = lds[nl * Core::kTileM + m];
-      if (n0 + nl < V && (arg < 0 || v > best)) {
-        best = v;
-        arg = nl;
-      }
-    }
-    qv[q * Core::kTileM + m] = best;
-    lds_arg[q * Core::kTileM + m] = arg;
-  }
-  __syncthreads();
-  for (int m = threadIdx.x; m < M; m += blockDim.x) {
-    float best = -INFINITY;
-    int arg = -1;
-    for (int q = 0; q < kLmQuarters; ++q) {
-      const float v = qv[q * Core::kTileM + m];
-      const int a = lds_arg[q * Core::kTileM + m];
-      if (a >= 0 && (arg < 0 || v > best)) {
-        best = v;
-        arg = a;
-      }
-    }
-    part_val[m * tiles + t] = best;
-    part_idx[m * tiles + t] = static_cast<int32_t>(n0 + (arg < 0 ? 0 : arg));
-  }
-  __syncthreads();  // lds is reused by the next tile
-}
-
-// Vocab tiles of 32 rows; kLmTilesPerBlock consecutive tiles per workgroup. Wave w always owns
-// the same 64-column steps, so its x fragments are loaded once and stay in registers across
-// tiles, while tile t + 1's weights stream in during tile t. Requires K / 64 <= 4 * kWaves.
+// Logits of vocab tiles of 32 rows (grid-strided over the workgroups) plus each tile's argmax
+// partial per row: part_*[m * tiles + t]. Requires K / 64 <= 4 * kWaves.
 template <int MB>
 __device__ void lm_head_argmax_impl(const uint16_t* xn, const uint16_t* w, void* logits,
                                     int logits_f32, float* part_val, int32_t* part_idx, int M,
@@ -323,28 +299,56 @@ __device__ void lm_head_argmax_impl(const uint16_t* xn, const uint16_t* w, void*
   static_assert(Core::kTileN == kLmTileN, "lm_head tile");
   __shared__ float lds[Core::kLdsFloats + kLmQuarters * Core::kTileM];
   __shared__ int lds_arg[kLmQuarters * Core::kTileM];
-  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
-  const int r = lane % 16, g = lane / 16;
-  const int steps = K / 64;
   const int64_t tiles = (V + Core::kTileN - 1) / Core::kTileN;
-  const int64_t t_first = static_cast<int64_t>(blockIdx.x) * kLmTilesPerBlock;
-  const int64_t t_last = t_first + kLmTilesPerBlock < tiles ? t_first + kLmTilesPerBlock : tiles;
-
-  typename Core::WBatch bufA, bufB;
-  typename Core::XBatch xb;
-  Core::issueW(bufA, Core::rows(w, V, K, t_first * Core::kTileN, r, g), wave, steps);
-  Core::issueX(xb, XGlobal{xn, K}, M, wave, steps, r, g);
-  for (int64_t t = t_first; t < t_last; t += 2) {
-    if (t + 1 < t_last)
-      Core::issueW(bufB, Core::rows(w, V, K, (t + 1) * Core::kTileN, r, g), wave, steps);
-    lmHeadTile<MB>(bufA, xb, lds, lds_arg, logits, logits_f32, part_val, part_idx, M, V, tiles, t,
-                   steps, r, g, wave);
-    if (t + 1 >= t_last) break;
-    if (t + 2 < t_last)
-      Core::issueW(bufA, Core::rows(w, V, K, (t + 2) * Core::kTileN, r, g), wave, steps);
-    lmHeadTile<MB>(bufB, xb, lds, lds_arg, logits, logits_f32, part_val, part_idx, M, V, tiles,
-                   t + 1, steps, r, g, wave);
-  }
+  tileLoop<2, MB>(w, XGlobal{xn, K}, V, K, M, lds, [&](int64_t t) {
+    const int64_t n0 = t * Core::kTileN;
+    if (logits != nullptr) {
+      for (int idx = threadIdx.x; idx < Core::kTileN * Core::kTileM; idx += blockDim.x) {
+        const int nl = idx % Core::kTileN, m = idx / Core::kTileN;  // n fastest: coalesced stores
+        const int64_t n = n0 + nl;
+        if (m >= M || n >= V) continue;
+        const float v = lds[nl * Core::kTileM + m];
+        if (logits_f32)
+          static_cast<float*>(logits)[m * V + n] = v;
+        else
+          static_cast<uint16_t*>(logits)[m * V + n] = floatToBf16(v);
+      }
+    }
+    // argmax: thread (m, q) scans rows 4q..4q+3 of the tile, then one thread per m merges the
+    // quarters in order (first index among equal maxima).
+    float* qv = lds + Core::kTileN * Core::kTileM;
+    for (int idx = threadIdx.x; idx < kLmQuarters * Core::kTileM; idx += blockDim.x) {
+      const int m = idx % Core::kTileM, q = idx / Core::kTileM;
+      float best = -INFINITY;
+      int arg = -1;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int nl = q * 4 + j;
+        const float v = lds[nl * Core::kTileM + m];
+        if (n0 + nl < V && (arg < 0 || v > best)) {
+          best = v;
+          arg = nl;
+        }
+      }
+      qv[q * Core::kTileM + m] = best;
+      lds_arg[q * Core::kTileM + m] = arg;
+    }
+    __syncthreads();
+    for (int m = threadIdx.x; m < M; m += blockDim.x) {
+      float best = -INFINITY;
+      int arg = -1;
+      for (int q = 0; q < kLmQuarters; ++q) {
+        const float v = qv[q * Core::kTileM + m];
+        const int a = lds_arg[q * Core::kTileM + m];
+        if (a >= 0 && (arg < 0 || v > best)) {
+          best = v;
+          arg = a;
+        }
+      }
+      part_val[m * tiles + t] = best;
+      part_idx[m * tiles + t] = static_cast<int32_t>(n0 + (arg < 0 ? 0 : arg));
+    }
+  });
 }
 
 // One workgroup per row: reduce that row's tile partials (contiguous) in tile order; ties keep

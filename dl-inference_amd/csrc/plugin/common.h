@@ -5,6 +5,7 @@
 // and operator registration.
 
 #include <memory>
+#include <mutex>
 #include <stdexcept>
 #include <string>
 #include <vector>
@@ -51,6 +52,27 @@ inline std::vector<std::int64_t> withLast(std::vector<std::int64_t> shape, std::
   shape.back() = last;
   return shape;
 }
+
+// Zero-initialised device scratch kept across calls of one operator instance (split-K partials,
+// attention partials and the arrival counters that kernels leave at zero; the nodes of one
+// operator instance run in stream order). Allocated on first use, outside any captured region
+// in a decode session, and replaced by a larger zeroed buffer when a node needs more.
+class PersistentWorkspace {
+ public:
+  void* get(std::size_t bytes, int device_id) {
+    if (bytes == 0) return nullptr;
+    std::lock_guard<std::mutex> lock(mutex_);
+    if (!buffer_.defined() || buffer_.nbytes() < bytes || buffer_.deviceId() != device_id) {
+      const auto words = static_cast<std::int64_t>((bytes + 3) / 4);
+      buffer_ = Tensor(at::zeros({words}, at::TensorOptions().dtype(at::kInt).device(at::kCUDA, device_id)));
+    }
+    return buffer_.deviceData();
+  }
+
+ private:
+  std::mutex mutex_;
+  Tensor buffer_;
+};
 
 template <typename Op>
 void add(OperatorRegistry* registry) {

@@ -12,7 +12,6 @@
 //   lm_head_argmax         lm_head, greedy argmax
 //   argmax                 greedy argmax over the last dim (unfused graphs)
 #include <cmath>
-#include <mutex>
 
 #include "common.h"
 
@@ -24,26 +23,6 @@ void requireBf16(const Tensor& t, const std::string& op, const std::string& what
 }
 
 std::int64_t rowsOf(const Tensor& t) { return product(t.shape(), 0, t.rank() - 1); }
-
-// Device scratch kept across calls (split-K partials; every call overwrites what it reads, and
-// nodes of one operator instance run in stream order). Allocated zeroed outside any captured
-// region on first use; grows when a node needs more.
-class PersistentWorkspace {
- public:
-  void* get(std::size_t bytes, int device_id) {
-    if (bytes == 0) return nullptr;
-    std::lock_guard<std::mutex> lock(mutex_);
-    if (!buffer_.defined() || buffer_.nbytes() < bytes || buffer_.deviceId() != device_id) {
-      const auto words = static_cast<std::int64_t>((bytes + 3) / 4);
-      buffer_ = Tensor(at::zeros({words}, at::TensorOptions().dtype(at::kInt).device(at::kCUDA, device_id)));
-    }
-    return buffer_.deviceData();
-  }
-
- private:
-  std::mutex mutex_;
-  Tensor buffer_;
-};
 
 class QkvRopeAppendOp final : public Operator {
  public:
@@ -105,16 +84,16 @@ class PagedAttentionOp final : public Operator {
     const float scale = static_cast<float>(attrDouble(attrs, "scale", 1.0 / std::sqrt(static_cast<double>(D))));
     *out[0] = Tensor::cuda(q.dtype(), q.shape(), q.deviceId());
     const std::size_t ws_bytes = dli_hip_paged_attention_workspace(B, Hq, 1, D, e->capacity());
-    Tensor ws;
-    if (ws_bytes > 0)
-      ws = Tensor::cuda(DType::Float32, {static_cast<std::int64_t>((ws_bytes + 3) / 4)}, q.deviceId());
     check(dli_hip_paged_attention(hipDtype(q.dtype()), ptr(q), ptr(e->key), ptr(e->value),
                                   static_cast<const std::int32_t*>(ptr(e->block_table)), ptr(*out[0]),
                                   B, Hq, e->heads, 1, D, e->block_size, e->max_blocks, 0, ptr(pos),
-                                  hipDtype(pos.dtype()), 1, scale, ws_bytes ? ptr(ws) : nullptr,
-                                  ws_bytes, ctx.stream),
+                                  hipDtype(pos.dtype()), 1, scale,
+                                  workspace_.get(ws_bytes, q.deviceId()), ws_bytes, ctx.stream),
           type());
   }
+
+ private:
+  mutable PersistentWorkspace workspace_;
 };
 
 // inputs: x [.., K], w [N, K], residual [.., N] (+ bias [N]); out = residual + bf16(x w^T + b)

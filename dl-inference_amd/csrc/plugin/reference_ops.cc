@@ -246,18 +246,17 @@ class AttentionOp final : public Operator {
     }
     const KVCacheEntry& e = *cache.get(cache_name);
     const std::size_t ws_bytes = dli_hip_paged_attention_workspace(B, Hq, Sq, D, e.capacity());
-    Tensor workspace;
-    if (ws_bytes > 0)
-      workspace = Tensor::cuda(DType::Float32, {static_cast<std::int64_t>((ws_bytes + 3) / 4)},
-                               q.deviceId());
     check(dli_hip_paged_attention(
               dt, ptr(q), ptr(e.key), ptr(e.value),
               static_cast<const std::int32_t*>(ptr(e.block_table)), ptr(*out[0]), B, Hq, Hkv, Sq,
               D, e.block_size, e.max_blocks, past, positions ? ptr(*positions) : nullptr,
               positions ? hipDtype(positions->dtype()) : DLI_I64, causal ? 1 : 0, scale,
-              ws_bytes > 0 ? ptr(workspace) : nullptr, ws_bytes, ctx.stream),
+              workspace_.get(ws_bytes, q.deviceId()), ws_bytes, ctx.stream),
           type());
   }
+
+ private:
+  mutable PersistentWorkspace workspace_;
 };
 
 // reshape/template.cc:7-9 — a view; one dim may be -1.

@@ -32,6 +32,7 @@ _SIGNATURES = {
     "dli_hip_device_count": [ctypes.POINTER(_int)],
     "dli_hip_get_device": [ctypes.POINTER(_int)],
     "dli_hip_set_device": [_int],
+    "dli_hip_compute_units": [ctypes.POINTER(_int)],
     "dli_hip_module_load": [_c_void_p, _size, ctypes.POINTER(_c_void_p)],
     "dli_hip_module_get_function": [_c_void_p, ctypes.c_char_p, ctypes.POINTER(_c_void_p)],
     "dli_hip_module_unload": [_c_void_p],

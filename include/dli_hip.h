@@ -73,6 +73,9 @@ const char* dli_hip_target_arch(void);
 
 int dli_hip_device_count(int* count);
 int dli_hip_get_device(int* device);
+/* Compute units of the current device (hipDeviceAttributeMultiprocessorCount; the reference
+ * has no counterpart: its launch grids do not depend on the device). */
+int dli_hip_compute_units(int* count);
 int dli_hip_set_device(int device);
 
 /* Module load + launch (CudaAotKernel::load / launch, cuda_driver.cc:107-129). A launch with
@@ -194,7 +197,10 @@ int dli_hip_kv_append(int dtype, const void* key, const void* value, void* key_p
  * L_b = past_len + Sq tokens (past_len = positions[b] when positions is non-NULL, else
  * `past`); the query at index i sits at position past_len + i and, when causal, sees keys
  * at positions <= past_len + i. Split along the keys across workgroups ("flash decoding");
- * partial results go to `workspace` (size from dli_hip_paged_attention_workspace). */
+ * partial results and per-(sequence, kv head) arrival counters go to `workspace` (size from
+ * dli_hip_paged_attention_workspace). The workspace must be zero-filled before its first use;
+ * every call leaves the counters at zero again. Calls sharing a workspace must be ordered
+ * (same stream). */
 size_t dli_hip_paged_attention_workspace(int64_t batch, int64_t q_heads, int64_t seq_q,
                                          int64_t head_dim, int64_t max_tokens);
 int dli_hip_paged_attention(int dtype, const void* q, const void* key_pool,
@@ -252,7 +258,7 @@ int dli_hip_linear_residual_norm(const void* x, const void* w, const void* bias,
                                  int splits, void* workspace, size_t workspace_bytes,
                                  void* stream);
 
-/* gate/up projections of xn -> silu(gate) * up, out [m, ffn]. w_gate_up interleaves the two
+/* gate/up projections of xn -> silu(gate) * up, out [m, ffn]; hidden <= 1024. w_gate_up interleaves the two
  * weights in blocks of 16 rows: rows [32i, 32i+16) = gate rows [16i, 16i+16), rows
  * [32i+16, 32i+32) = up rows [16i, 16i+16). Replaces gate_proj, up_proj, act_fn and mul
  * (export.py:378-414). */

@@ -168,3 +168,42 @@ def test_lm_head_argmax_random_logits_match_oracle():
     top2 = np.sort(ref, axis=-1)[:, -2:]
     clear = (top2[:, 1] - top2[:, 0]) > 1e-3  # rows whose winner the fp32 sums cannot flip
     np.testing.assert_array_equal(ids[clear], np.argmax(ref, axis=-1)[clear])
+
+
+@pytest.mark.parametrize("B,positions,max_seq", [
+    (8, [0, 1, 63, 64, 65, 1000, 2047, 4095], 4160),  # ragged lengths, partial last blocks
+    (32, None, 4160),                                  # the decode workload: every row at 4095
+    (3, [5, 130, 517], 600),                           # short cache: one split per sequence
+    (2, [-1, 10], 256),                                # an empty sequence yields zeros
+])
+def test_paged_attention_decode(B, positions, max_seq):
+    """paged_attention (decode, 64-key blocks): every (sequence, kv head) is split over
+    workgroups whose partials the last one merges; compared with the oracle's attention over the
+    cache contents of each sequence (attention/kernel.py:6-62 with past = position)."""
+    hq, hkv, d = 14, 2, 64
+    if positions is None:
+        positions = [4095] * B
+    e = dli.Engine().load_plugin()
+    e.configure_kv_cache(block_size=64, max_seq_len=max_seq)
+    e.reserve_kv_cache("L", "bfloat16", B, hkv, d)
+    entry = e.kv_cache_entry("L")
+    g = torch.Generator(device=DEV).manual_seed(60)
+    for pool in (entry["key"], entry["value"]):
+        pool.copy_(torch.randn(pool.shape, generator=g, device=DEV).to(pool.dtype))
+    q = rand((B, hq, 1, d), 61)
+    pos = torch.tensor(positions, dtype=torch.int64, device=DEV)
+    for _ in range(2):  # the second call reuses the workspace counters the first left at zero
+        out = run_op("paged_attention", {"q": q, "pos": pos}, attrs={"kv_cache": "L"},
+                     engine=e)["output"]
+    kp, vp = to_np(entry["key"]), to_np(entry["value"])
+    table, bs = entry["block_table"].cpu().numpy(), entry["block_size"]
+    for i, p in enumerate(positions):
+        n = p + 1
+        if n <= 0:
+            assert not to_np(out[i]).any()
+            continue
+        blocks = [table[i, j] for j in range((n + bs - 1) // bs)]
+        k = np.concatenate([kp[blk] for blk in blocks], axis=1)[:, :n]                      # [Hkv, n, D]
+        v = np.concatenate([vp[blk].transpose(0, 2, 1) for blk in blocks], axis=1)[:, :n]  # [Hkv, n, D]
+        ref = ops.attention(to_np(q[i:i + 1]), k[None], v[None], causal=True)
+        assert_close(out[i:i + 1], ref, "bfloat16")
