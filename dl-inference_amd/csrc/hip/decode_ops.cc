@@ -14,6 +14,7 @@ constexpr int kTileN = 32;           // weight rows per workgroup of gate_up / l
 constexpr int kRowTile = 16;         // weight rows per workgroup of qkv / linear_residual / partial
 constexpr int kResWaves = 8;         // waves per linear_residual workgroup
 constexpr int64_t kMaxNormN = 1024;  // residual_rms_norm: 256 threads x 4 columns
+constexpr int kMaxNormSplits = 8;    // residual_rms_norm sums at most 8 split-K partials
 constexpr int64_t kMaxLmK = 1024;    // tile loops keep x for K / 64 <= 16 steps in registers
 constexpr int kMaxDecodeSplits = 32; // splits a decode-attention call may use
 
@@ -31,6 +32,7 @@ struct MbKernels {
 
 MbKernels k_qkv("decode", "qkv_rope_append");
 MbKernels k_linres("decode", "linear_residual");
+MbKernels k_linres_splitk("decode", "linear_residual_splitk");
 MbKernels k_partial("decode", "linear_partial");
 MbKernels k_gate_up("decode", "gate_up_silu");
 MbKernels k_lm_head("decode", "lm_head_argmax");
@@ -44,12 +46,26 @@ int bad(const char* op, const std::string& what) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+size_t alignUp(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+int tileRows(int64_t m) { return m <= 16 ? 16 : (m <= 32 ? 32 : 64); }
+
+// Split-K partials: [splits, m, n] (linear_residual_norm) or [tiles][splits][16 x tileRows(m)]
+// (linear_residual), whichever is larger; arrival counters (one per 16-row tile) follow.
+size_t splitPartialBytes(int64_t n, int64_t m, int splits) {
+  const int64_t tiles = (n + kRowTile - 1) / kRowTile;
+  const int64_t a = static_cast<int64_t>(splits) * m * n;
+  const int64_t b = tiles * splits * kRowTile * tileRows(m);
+  return alignUp(static_cast<size_t>(a > b ? a : b) * sizeof(float), 256);
+}
+
 // Workgroups of a grid-strided tile loop: one per tile, at most as many as are resident at once
-// (two 256-thread workgroups per CU fit below 256 VGPRs; the 64-row variants use more).
-int tileGrid(int64_t tiles, int64_t m, unsigned* grid) {
+// (two 256-thread workgroups per CU fit below 256 VGPRs; the 64-row variants use more). With an
+// RMSNorm prologue (VALU work per workgroup) at most one per CU, so no SIMD normalizes twice.
+int tileGrid(int64_t tiles, int64_t m, unsigned* grid, bool prologue = false) {
   int cus = 0;
   if (int rc = computeUnits(&cus)) return rc;
-  const int64_t resident = static_cast<int64_t>(cus) * (m <= 32 ? 2 : 1);
+  const int64_t resident = static_cast<int64_t>(cus) * (m <= 32 && !prologue ? 2 : 1);
   *grid = static_cast<unsigned>(tiles < resident ? tiles : resident);
   return 0;
 }
@@ -67,11 +83,12 @@ int partialThenResidual(const char* op, const void* x, const void* w, const void
                         int64_t m, int64_t n, int64_t k, float eps, int splits, void* workspace,
                         size_t workspace_bytes, void* stream) {
   if (n <= 0 || n > kMaxNormN) return bad(op, "n must be in [1, 1024]");
-  if (splits < 1 || splits > k / 64) return bad(op, "splits must be in [1, k / 64]");
+  if (splits < 1 || splits > k / 64 || splits > kMaxNormSplits)
+    return bad(op, "splits must be in [1, min(8, k / 64)]");
   if (workspace == nullptr || workspace_bytes < dli_hip_splitk_workspace(n, m, splits))
     return bad(op, "workspace too small");
   if (!aligned16(x) || !aligned16(w)) return bad(op, "x and w must be 16-byte aligned");
-  float* partials = static_cast<float*>(workspace);
+  float* partials = static_cast<float*>(workspace);  // [splits, m, n]
   const unsigned tiles = static_cast<unsigned>((n + kRowTile - 1) / kRowTile);
   if (int rc = launch(*k_partial.pick(m), {tiles, static_cast<unsigned>(splits)}, {kThreads}, 0,
                       stream, x, w, partials, static_cast<int>(m), n, static_cast<int>(k), splits))
@@ -90,18 +107,20 @@ extern "C" {
 
 size_t dli_hip_splitk_workspace(int64_t n, int64_t m, int splits) {
   if (n <= 0 || m <= 0 || splits < 1) return 0;
-  return static_cast<size_t>(splits) * m * n * sizeof(float);
+  return splitPartialBytes(n, m, splits) +
+         alignUp(static_cast<size_t>((n + kRowTile - 1) / kRowTile) * sizeof(unsigned), 256);
 }
 
-int dli_hip_qkv_rope_append(const void* xn, const void* w_qkv, const void* b_qkv,
-                            const float* cos_table, const float* sin_table, int64_t max_pos,
-                            const void* positions, int positions_dtype, void* q_out,
-                            void* key_pool, void* value_pool, const int32_t* block_table,
-                            int64_t block_size, int64_t max_blocks, int64_t batch,
-                            int64_t hidden_size, int64_t q_heads, int64_t kv_heads,
-                            int64_t head_dim, void* stream) {
+int dli_hip_qkv_rope_append(const void* hidden, const void* norm_weight, const void* w_qkv,
+                            const void* b_qkv, const float* cos_table, const float* sin_table,
+                            int64_t max_pos, const void* positions, int positions_dtype,
+                            void* q_out, void* key_pool, void* value_pool,
+                            const int32_t* block_table, int64_t block_size, int64_t max_blocks,
+                            int64_t batch, int64_t hidden_size, int64_t q_heads, int64_t kv_heads,
+                            int64_t head_dim, float eps, void* stream) {
   const char* op = "qkv_rope_append";
   if (int rc = checkSkinny(op, batch, hidden_size)) return rc;
+  if (hidden_size > kMaxLmK) return bad(op, "hidden_size above 1024 is not supported");
   if (positions == nullptr || (positions_dtype != DLI_I64 && positions_dtype != DLI_I32))
     return bad(op, "positions (int64/int32 [batch]) are required");
   if (head_dim <= 0 || head_dim % 2 != 0) return bad(op, "head_dim must be even");
@@ -109,15 +128,19 @@ int dli_hip_qkv_rope_append(const void* xn, const void* w_qkv, const void* b_qkv
   if ((q_heads * head_dim) % kRowTile != 0 || (kv_heads * head_dim) % kRowTile != 0)
     return bad(op, "q and kv widths must be multiples of 16");
   if (block_size <= 0 || max_blocks <= 0) return bad(op, "empty cache geometry");
-  if (!aligned16(xn) || !aligned16(w_qkv)) return bad(op, "xn and w_qkv must be 16-byte aligned");
+  if (!aligned16(hidden) || !aligned16(w_qkv) || (norm_weight != nullptr && !aligned16(norm_weight)))
+    return bad(op, "hidden, norm_weight and w_qkv must be 16-byte aligned");
   const int64_t n = (q_heads + 2 * kv_heads) * head_dim;
   const int64_t tiles = (n + kRowTile - 1) / kRowTile;
+  if (tiles > 65535) return bad(op, "too many q|k|v rows");
   const int pos64 = positions_dtype == DLI_I64 ? 1 : 0;
-  return launch(*k_qkv.pick(batch), {static_cast<unsigned>(tiles)}, {kThreads}, 0, stream, xn,
-                w_qkv, b_qkv, cos_table, sin_table, max_pos, positions, pos64, q_out, key_pool,
-                value_pool, block_table, block_size, max_blocks, static_cast<int>(batch),
-                static_cast<int>(hidden_size), static_cast<int>(q_heads),
-                static_cast<int>(kv_heads), static_cast<int>(head_dim));
+  // one tile per workgroup: the kernel prefetches the epilogue operands of tile blockIdx.x
+  return launch(*k_qkv.pick(batch), {static_cast<unsigned>(tiles)}, {kThreads}, 0, stream, hidden,
+                norm_weight, eps, w_qkv, b_qkv, cos_table, sin_table, max_pos, positions, pos64,
+                q_out, key_pool, value_pool, block_table, block_size, max_blocks,
+                static_cast<int>(batch), static_cast<int>(hidden_size),
+                static_cast<int>(q_heads), static_cast<int>(kv_heads),
+                static_cast<int>(head_dim));
 }
 
 int dli_hip_linear_residual(const void* x, const void* w, const void* bias, const void* residual,
@@ -126,14 +149,22 @@ int dli_hip_linear_residual(const void* x, const void* w, const void* bias, cons
   const char* op = "linear_residual";
   if (int rc = checkSkinny(op, m, k)) return rc;
   if (n <= 0) return bad(op, "n must be positive");
-  if (splits > 1)
-    return partialThenResidual(op, x, w, bias, residual, nullptr, out, nullptr, m, n, k, 0.f,
-                               splits, workspace, workspace_bytes, stream);
-  if (splits != 1) return bad(op, "splits must be >= 1");
+  if (splits < 1 || splits > k / 64 || splits > kMaxNormSplits)
+    return bad(op, "splits must be in [1, min(8, k / 64)]");
   if (!aligned16(x) || !aligned16(w)) return bad(op, "x and w must be 16-byte aligned");
   const int64_t tiles = (n + kRowTile - 1) / kRowTile;
-  return launch(*k_linres.pick(m), {static_cast<unsigned>(tiles)}, {kResWaves * 64}, 0, stream, x,
-                w, bias, residual, out, static_cast<int>(m), n, static_cast<int>(k));
+  if (splits == 1)
+    return launch(*k_linres.pick(m), {static_cast<unsigned>(tiles)}, {kResWaves * 64}, 0, stream,
+                  x, w, bias, residual, out, static_cast<int>(m), n, static_cast<int>(k));
+  if (workspace == nullptr || workspace_bytes < dli_hip_splitk_workspace(n, m, splits))
+    return bad(op, "workspace too small");
+  float* partials = static_cast<float*>(workspace);
+  unsigned* counters = reinterpret_cast<unsigned*>(static_cast<char*>(workspace) +
+                                                   splitPartialBytes(n, m, splits));
+  return launch(*k_linres_splitk.pick(m),
+                {static_cast<unsigned>(tiles), static_cast<unsigned>(splits)}, {kThreads}, 0,
+                stream, x, w, bias, residual, out, static_cast<int>(m), n, static_cast<int>(k),
+                splits, partials, counters);
 }
 
 int dli_hip_linear_residual_norm(const void* x, const void* w, const void* bias,
@@ -148,17 +179,20 @@ int dli_hip_linear_residual_norm(const void* x, const void* w, const void* bias,
                              splits, workspace, workspace_bytes, stream);
 }
 
-int dli_hip_gate_up_silu(const void* xn, const void* w_gate_up, void* out, int64_t m, int64_t ffn,
-                         int64_t hidden_size, void* stream) {
+int dli_hip_gate_up_silu(const void* hidden, const void* norm_weight, const void* w_gate_up,
+                         void* out, int64_t m, int64_t ffn, int64_t hidden_size, float eps,
+                         void* stream) {
   const char* op = "gate_up_silu";
   if (int rc = checkSkinny(op, m, hidden_size)) return rc;
   if (ffn <= 0 || ffn % 16 != 0) return bad(op, "ffn must be a positive multiple of 16");
   if (hidden_size > kMaxLmK) return bad(op, "hidden_size above 1024 is not supported");
-  if (!aligned16(xn) || !aligned16(w_gate_up)) return bad(op, "xn and w_gate_up must be 16-byte aligned");
+  if (!aligned16(hidden) || !aligned16(w_gate_up) ||
+      (norm_weight != nullptr && !aligned16(norm_weight)))
+    return bad(op, "hidden, norm_weight and w_gate_up must be 16-byte aligned");
   unsigned grid = 0;
-  if (int rc = tileGrid(ffn / 16, m, &grid)) return rc;
-  return launch(*k_gate_up.pick(m), {grid}, {kThreads}, 0, stream, xn, w_gate_up, out,
-                static_cast<int>(m), ffn, static_cast<int>(hidden_size));
+  if (int rc = tileGrid(ffn / 16, m, &grid, norm_weight != nullptr)) return rc;
+  return launch(*k_gate_up.pick(m), {grid}, {kThreads}, 0, stream, hidden, norm_weight, eps,
+                w_gate_up, out, static_cast<int>(m), ffn, static_cast<int>(hidden_size));
 }
 
 size_t dli_hip_lm_head_argmax_workspace(int64_t m, int64_t vocab) {
@@ -210,8 +244,6 @@ namespace dli::hip {
 namespace {
 constexpr int kDecWaves = 8;
 constexpr int kDecBlock = 64;
-
-size_t alignUp(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 // Workspace: partials [ml: rows x splits x 2][o: rows x splits x 64] fp32 inside a region sized
 // for kMaxDecodeSplits, then per-(sequence, kv head) arrival counters (rows of them, which is

@@ -209,10 +209,6 @@ namespace {
 
 constexpr int kDecD = 64;
 
-__device__ __forceinline__ uint32_t packBf16(float lo, float hi) {
-  return static_cast<uint32_t>(floatToBf16(lo)) | (static_cast<uint32_t>(floatToBf16(hi)) << 16);
-}
-
 // Workgroup = kDecWaves waves over the key range of one split; wave w takes cache blocks
 // w, w + kDecWaves, ... of that range (a whole block of 64 keys = two 32-key MFMA sub-tiles,
 // so every V row segment of a block is consumed by one wave). The next block's K/V loads are
@@ -301,9 +297,9 @@ __device__ __forceinline__ void attendBlock(SoftmaxState& st8, const KvBlockRegs
 #pragma unroll
     for (int w2 = 0; w2 < 4; ++w2) {
       const float a0 = p[w2 / 2][(w2 % 2) * 2], a1 = p[w2 / 2][(w2 % 2) * 2 + 1];
-      const uint16_t h0 = floatToBf16(a0), h1 = floatToBf16(a1);
-      phi.w[w2] = static_cast<uint32_t>(h0) | (static_cast<uint32_t>(h1) << 16);
-      plo.w[w2] = packBf16(a0 - bf16ToFloat(h0), a1 - bf16ToFloat(h1));
+      phi.w[w2] = packBf16x2(a0, a1);
+      plo.w[w2] = packBf16x2(a0 - bf16ToFloat(static_cast<uint16_t>(phi.w[w2])),
+                             a1 - bf16ToFloat(static_cast<uint16_t>(phi.w[w2] >> 16)));
     }
 #pragma unroll
     for (int d = 0; d < 4; ++d) {

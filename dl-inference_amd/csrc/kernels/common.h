@@ -20,12 +20,18 @@ __device__ __forceinline__ float bf16ToFloat(uint16_t bits) {
   return __uint_as_float(static_cast<uint32_t>(bits) << 16);
 }
 
-// Round-to-nearest-even, the rule torch uses for float -> bfloat16.
+// Round-to-nearest-even, the rule torch uses for float -> bfloat16 (gfx950 converts in hardware:
+// v_cvt_pk_bf16_f32; NaN stays NaN).
 __device__ __forceinline__ uint16_t floatToBf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return static_cast<uint16_t>(u >> 16);
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
+}
+
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// Two floats -> two bfloat16 (RNE) packed as lo | hi << 16, one conversion instruction.
+__device__ __forceinline__ uint32_t packBf16x2(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_t));
 }
 
 template <typename T>

@@ -2,13 +2,13 @@
 // a run of nodes of the reference's exported Qwen2 decoder graph
 // (python/dli_export/export.py:272-446) and keeps that graph's bf16 rounding points:
 //
-//   qkv_rope_append        q/k/v_proj, reshapes, rotary_embedding, KV append (input: the
-//                          input_layernorm output)
+//   qkv_rope_append        (input_layernorm,) q/k/v_proj, reshapes, rotary_embedding, KV
+//                          append
 //   paged_attention        attention over the already appended paged KV cache (decode)
 //   linear_residual        o_proj + attention_residual, down_proj + mlp_residual
 //   linear_residual_norm   the same plus the RMSNorm that follows the residual update
 //                          (post_attention_layernorm, the next input_layernorm, model.norm)
-//   gate_up_silu           gate_proj, up_proj, act_fn, mul
+//   gate_up_silu           (post_attention_layernorm,) gate_proj, up_proj, act_fn, mul
 //   lm_head_argmax         lm_head, greedy argmax
 //   argmax                 greedy argmax over the last dim (unfused graphs)
 #include <cmath>
@@ -24,14 +24,20 @@ void requireBf16(const Tensor& t, const std::string& op, const std::string& what
 
 std::int64_t rowsOf(const Tensor& t) { return product(t.shape(), 0, t.rank() - 1); }
 
+// inputs: hidden [B, H], (norm_weight [H],) w_qkv [N, H], b_qkv [N], cos, sin, positions [B].
+// With norm_weight the RMSNorm (input_layernorm) runs inside the kernel; without it hidden is
+// the normalized activation.
 class QkvRopeAppendOp final : public Operator {
  public:
   std::string type() const override { return "qkv_rope_append"; }
   void compute(const std::vector<const Tensor*>& in, const std::vector<Tensor*>& out,
                const Attributes& attrs, ExecutionContext& ctx) const override {
-    requireArity(in, out, 6, 6, 1, type());
+    requireArity(in, out, 6, 7, 1, type());
     requireCudaInputs(in, type());
-    const Tensor &x = *in[0], &w = *in[1], &b = *in[2], &cos = *in[3], &sin = *in[4], &pos = *in[5];
+    const std::size_t o = in.size() == 7 ? 1 : 0;
+    const Tensor* nw = o ? in[1] : nullptr;
+    const Tensor &x = *in[0], &w = *in[1 + o], &b = *in[2 + o], &cos = *in[3 + o],
+                 &sin = *in[4 + o], &pos = *in[5 + o];
     for (const Tensor* t : {&x, &w, &b}) requireBf16(*t, type(), "activations/weights");
     requireFloat(cos, type());
     requireFloat(sin, type());
@@ -39,12 +45,15 @@ class QkvRopeAppendOp final : public Operator {
     const auto hq = attrs.require<std::int64_t>("q_heads");
     const auto hkv = attrs.require<std::int64_t>("kv_heads");
     const auto d = attrs.require<std::int64_t>("head_dim");
+    const auto eps = static_cast<float>(attrDouble(attrs, "eps", 1e-6));
     const std::string& cache_name = attrs.require<std::string>("kv_cache");
     const std::int64_t hidden = x.shape().back();
     const std::int64_t m = rowsOf(x);
     const std::int64_t n = (hq + 2 * hkv) * d;
     if (w.rank() != 2 || w.dim(0) != n || w.dim(1) != hidden || static_cast<std::int64_t>(b.numel()) != n)
       throw std::invalid_argument("qkv_rope_append weight shapes do not match the attributes");
+    if (nw != nullptr && (nw->dtype() != DType::BFloat16 || static_cast<std::int64_t>(nw->numel()) != hidden))
+      throw std::invalid_argument("qkv_rope_append norm weight must be bfloat16 [hidden]");
     if (cos.rank() != 2 || cos.dim(1) != d / 2 || cos.shape() != sin.shape())
       throw std::invalid_argument("qkv_rope_append cos/sin must be [max_pos, head_dim/2]");
     if (static_cast<std::int64_t>(pos.numel()) != m)
@@ -53,11 +62,11 @@ class QkvRopeAppendOp final : public Operator {
     KVCacheEntry& e = ctx.kv_cache->reserve(cache_name, DType::BFloat16, m, hkv, d, x.deviceId());
     *out[0] = Tensor::cuda(DType::BFloat16, {m, hq, 1, d}, x.deviceId());
     check(dli_hip_qkv_rope_append(
-              ptr(x), ptr(w), ptr(b), static_cast<const float*>(ptr(cos)),
+              ptr(x), nw ? ptr(*nw) : nullptr, ptr(w), ptr(b), static_cast<const float*>(ptr(cos)),
               static_cast<const float*>(ptr(sin)), cos.dim(0), ptr(pos), hipDtype(pos.dtype()),
               ptr(*out[0]), ptr(e.key), ptr(e.value),
               static_cast<const std::int32_t*>(ptr(e.block_table)), e.block_size, e.max_blocks, m,
-              hidden, hq, hkv, d, ctx.stream),
+              hidden, hq, hkv, d, eps, ctx.stream),
           type());
   }
 };
@@ -162,22 +171,30 @@ class LinearResidualNormOp final : public Operator {
   mutable PersistentWorkspace workspace_;
 };
 
-// inputs: xn [.., H], w_gate_up [2F, H] (16-row interleaved)
+// inputs: hidden [.., H], (norm_weight [H],) w_gate_up [2F, H] (16-row interleaved). With
+// norm_weight the RMSNorm (post_attention_layernorm) runs inside the kernel.
 class GateUpSiluOp final : public Operator {
  public:
   std::string type() const override { return "gate_up_silu"; }
   void compute(const std::vector<const Tensor*>& in, const std::vector<Tensor*>& out,
-               const Attributes&, ExecutionContext& ctx) const override {
-    requireArity(in, out, 2, 2, 1, type());
+               const Attributes& attrs, ExecutionContext& ctx) const override {
+    requireArity(in, out, 2, 3, 1, type());
     requireCudaInputs(in, type());
     for (const Tensor* t : in) requireBf16(*t, type(), "inputs");
-    const Tensor &x = *in[0], &w = *in[1];
+    const Tensor& x = *in[0];
+    const Tensor* nw = in.size() == 3 ? in[1] : nullptr;
+    const Tensor& w = *in.back();
     const std::int64_t hidden = x.shape().back(), m = rowsOf(x);
     if (w.rank() != 2 || w.dim(1) != hidden || w.dim(0) % 2 != 0)
       throw std::invalid_argument("gate_up_silu weight shape mismatch");
+    if (nw != nullptr && static_cast<std::int64_t>(nw->numel()) != hidden)
+      throw std::invalid_argument("gate_up_silu norm weight size mismatch");
     const std::int64_t f = w.dim(0) / 2;
+    const auto eps = static_cast<float>(attrDouble(attrs, "eps", 1e-6));
     *out[0] = Tensor::cuda(DType::BFloat16, withLast(x.shape(), f), x.deviceId());
-    check(dli_hip_gate_up_silu(ptr(x), ptr(w), ptr(*out[0]), m, f, hidden, ctx.stream), type());
+    check(dli_hip_gate_up_silu(ptr(x), nw ? ptr(*nw) : nullptr, ptr(w), ptr(*out[0]), m, f, hidden,
+                               eps, ctx.stream),
+          type());
   }
 };
 

@@ -5,10 +5,9 @@ reference-style graph (fused=False): the node sequence of the reference exporter
 needs — a `positions` input feeding rotary_embedding (5th input) and attention (4th input),
 grouped KV heads, fp32 logits and an `argmax` node.
 
-fused graph (fused=True): 5 nodes per layer on the fused operators of the gfx950 plugin
-(qkv_rope_append, paged_attention, linear_residual_norm, gate_up_silu, linear_residual_norm), an
-rms_norm after the embedding and one lm_head_argmax node. Each RMSNorm is computed once, by the
-node that produces the residual it normalizes (the last layer's produces model.norm's output).
+fused graph (fused=True): 5 launches per layer on the fused operators of the gfx950 plugin
+(qkv_rope_append and gate_up_silu with their RMSNorm inside, paged_attention, and
+linear_residual for o_proj and for down_proj), then model.norm and one lm_head_argmax node.
 Same rounding points, same tensor names for inputs and outputs.
 """
 from __future__ import annotations
@@ -80,42 +79,36 @@ def _reference_nodes(cfg: Qwen2Config, batch: int, nodes: list):
 
 def _fused_nodes(cfg: Qwen2Config, batch: int, nodes: list, splits: dict, logits_dtype: str):
     h = "hidden_states"
-    xn = "input_norm_0"
-    _node(nodes, "model.layers.0.input_layernorm", "rms_norm",
-          [h, "model.layers.0.input_layernorm.weight"], [xn], {"eps": cfg.eps})
     for i in range(cfg.layers):
         p = f"model.layers.{i}"
         t = f"layers_{i}"
-        last = i + 1 == cfg.layers
-        next_norm = "model.norm.weight" if last else f"model.layers.{i + 1}.input_layernorm.weight"
-        next_xn = "norm_hidden" if last else f"input_norm_{i + 1}"
         _node(nodes, f"{p}.self_attn.qkv_rope_append", "qkv_rope_append",
-              [xn, f"{p}.self_attn.qkv_proj.weight", f"{p}.self_attn.qkv_proj.bias", "rotary_cos",
-               "rotary_sin", "positions"],
+              [h, f"{p}.input_layernorm.weight", f"{p}.self_attn.qkv_proj.weight",
+               f"{p}.self_attn.qkv_proj.bias", "rotary_cos", "rotary_sin", "positions"],
               [f"{t}_q_rotary"],
               {"kv_cache": f"layer_{i}", "q_heads": cfg.heads, "kv_heads": cfg.kv_heads,
-               "head_dim": cfg.head_dim})
+               "head_dim": cfg.head_dim, "eps": cfg.eps})
         _node(nodes, f"{p}.self_attn.attention", "paged_attention", [f"{t}_q_rotary", "positions"],
               [f"{t}_attention"], {"kv_cache": f"layer_{i}"})
         _node(nodes, f"{p}.self_attn.merge", "reshape", [f"{t}_attention"], [f"{t}_attention_merged"],
               {"shape": [batch, cfg.heads * cfg.head_dim]})
-        _node(nodes, f"{p}.self_attn.o_proj", "linear_residual_norm",
-              [f"{t}_attention_merged", f"{p}.self_attn.o_proj.weight", h,
-               f"{p}.post_attention_layernorm.weight"],
-              [f"{t}_after_attention", f"{t}_post_attention_norm"],
-              {"splits": splits.get("o", 1), "eps": cfg.eps})
+        _node(nodes, f"{p}.self_attn.o_proj", "linear_residual",
+              [f"{t}_attention_merged", f"{p}.self_attn.o_proj.weight", h],
+              [f"{t}_after_attention"], {"splits": splits.get("o", 1)})
         _node(nodes, f"{p}.mlp.gate_up", "gate_up_silu",
-              [f"{t}_post_attention_norm", f"{p}.mlp.gate_up_proj.weight"], [f"{t}_gated"])
-        _node(nodes, f"{p}.mlp.down_proj", "linear_residual_norm",
-              [f"{t}_gated", f"{p}.mlp.down_proj.weight", f"{t}_after_attention", next_norm],
-              [f"{t}_output", next_xn], {"splits": splits.get("down", 1), "eps": cfg.eps})
+              [f"{t}_after_attention", f"{p}.post_attention_layernorm.weight",
+               f"{p}.mlp.gate_up_proj.weight"], [f"{t}_gated"], {"eps": cfg.eps})
+        _node(nodes, f"{p}.mlp.down_proj", "linear_residual",
+              [f"{t}_gated", f"{p}.mlp.down_proj.weight", f"{t}_after_attention"],
+              [f"{t}_output"], {"splits": splits.get("down", 1)})
         h = f"{t}_output"
-        xn = next_xn
-    _node(nodes, "lm_head", "lm_head_argmax", [xn, "lm_head.weight"], OUTPUTS,
+    _node(nodes, "model.norm", "rms_norm", [h, "model.norm.weight"], ["norm_hidden"],
+          {"eps": cfg.eps})
+    _node(nodes, "lm_head", "lm_head_argmax", ["norm_hidden", "lm_head.weight"], OUTPUTS,
           {"logits_dtype": logits_dtype})
 
 
-DEFAULT_SPLITS = {"o": 2, "down": 4}
+DEFAULT_SPLITS = {"o": 1, "down": 4}
 
 
 def build_decode_graph(cfg: Qwen2Config, batch: int, fused: bool = True,

@@ -219,31 +219,35 @@ int dli_hip_argmax(int dtype, const void* x, int64_t* ids, int64_t rows, int64_t
  * 3. Fused bf16 decode kernels (batch rows m in [1, 64], reduction sizes multiple of 64,
  *    16-byte aligned x and weights). They replace runs of nodes of the reference's exported
  *    decoder graph (python/dli_export/export.py:272-446), keeping every node's bf16 rounding
- *    point. The GEMM kernels take activations that are already RMS-normalized: the norm runs
- *    once per residual update, in dli_hip_linear_residual_norm (or rms_norm for the first
- *    layer). Split-K variants write fp32 partials [splits, m, n] to a caller workspace of
- *    dli_hip_splitk_workspace() bytes (no zeroing needed) and sum them in split order in a
- *    second kernel; calls that share one workspace must be ordered (same stream).
+ *    point. The RMSNorm in front of qkv and gate/up runs inside those kernels, on the
+ *    activation fragments each workgroup loads (or, with dli_hip_linear_residual_norm, once
+ *    after the residual update). Split-K variants use a caller workspace of
+ *    dli_hip_splitk_workspace() bytes; calls that share one workspace must be ordered (same
+ *    stream).
  * ------------------------------------------------------------------------------------- */
 
 size_t dli_hip_splitk_workspace(int64_t n, int64_t m, int splits);
 
-/* [q | k | v] = xn W_qkv^T + b -> interleaved RoPE on q and k at positions[b] -> k, v written
- * into the paged cache at positions[b] -> q_out [m, q_heads, head_dim]. xn is the output of
- * input_layernorm. W_qkv is [(q_heads + 2 kv_heads) * head_dim, hidden]; cos/sin are fp32
- * [max_pos, head_dim / 2]. Replaces q/k/v_proj, 3 reshapes, rotary_embedding and the KV append
- * inside attention (export.py:280-349; rotary/kernel.py:6-35). */
-int dli_hip_qkv_rope_append(const void* xn, const void* w_qkv, const void* b_qkv,
-                            const float* cos_table, const float* sin_table, int64_t max_pos,
-                            const void* positions, int positions_dtype, void* q_out,
-                            void* key_pool, void* value_pool, const int32_t* block_table,
-                            int64_t block_size, int64_t max_blocks, int64_t batch,
-                            int64_t hidden_size, int64_t q_heads, int64_t kv_heads,
-                            int64_t head_dim, void* stream);
+/* [xn = rms_norm(hidden) * norm_weight when norm_weight is non-NULL, else xn = hidden] ->
+ * [q | k | v] = xn W_qkv^T + b -> interleaved RoPE on q and k at positions[b] -> k, v written
+ * into the paged cache at positions[b] -> q_out [m, q_heads, head_dim]; hidden <= 1024.
+ * W_qkv is [(q_heads + 2 kv_heads) * head_dim, hidden]; cos/sin are fp32 [max_pos,
+ * head_dim / 2]. Replaces input_layernorm, q/k/v_proj, 3 reshapes, rotary_embedding and the
+ * KV append inside attention (export.py:280-349; rotary/kernel.py:6-35). */
+int dli_hip_qkv_rope_append(const void* hidden, const void* norm_weight, const void* w_qkv,
+                            const void* b_qkv, const float* cos_table, const float* sin_table,
+                            int64_t max_pos, const void* positions, int positions_dtype,
+                            void* q_out, void* key_pool, void* value_pool,
+                            const int32_t* block_table, int64_t block_size, int64_t max_blocks,
+                            int64_t batch, int64_t hidden_size, int64_t q_heads, int64_t kv_heads,
+                            int64_t head_dim, float eps, void* stream);
 
 /* out = residual + (x W^T + b), the linear output rounded before the add. Replaces o_proj +
- * attention_residual and down_proj + mlp_residual (export.py:366-376, 416-424). splits > 1
- * (n <= 1024) splits K over workgroups through the workspace. */
+ * attention_residual and down_proj + mlp_residual (export.py:366-376, 416-424). splits in
+ * [2, min(8, k / 64)] splits K over workgroups: each stores a partial tile in the workspace and
+ * the last to finish a tile sums them in split order and writes it. The workspace
+ * (dli_hip_splitk_workspace bytes) must be zero-filled before its first use; every call leaves
+ * its arrival counters at zero again. */
 int dli_hip_linear_residual(const void* x, const void* w, const void* bias, const void* residual,
                             void* out, int64_t m, int64_t n, int64_t k, int splits,
                             void* workspace, size_t workspace_bytes, void* stream);
@@ -251,19 +255,22 @@ int dli_hip_linear_residual(const void* x, const void* w, const void* bias, cons
 /* h_out = residual + (x W^T + b) as above, and xn_out = rms_norm(h_out) * norm_weight, both
  * [m, n] (n <= 1024). Replaces o_proj + attention_residual + post_attention_layernorm, and
  * down_proj + mlp_residual + the next layer's input_layernorm (or model.norm after the last
- * layer) (export.py:366-424; rms_norm/kernel.py:6-14). Always uses the workspace (splits >= 1). */
+ * layer) (export.py:366-424; rms_norm/kernel.py:6-14). Always uses the workspace; splits in
+ * [1, min(8, k / 64)]. */
 int dli_hip_linear_residual_norm(const void* x, const void* w, const void* bias,
                                  const void* residual, const void* norm_weight, void* h_out,
                                  void* xn_out, int64_t m, int64_t n, int64_t k, float eps,
                                  int splits, void* workspace, size_t workspace_bytes,
                                  void* stream);
 
-/* gate/up projections of xn -> silu(gate) * up, out [m, ffn]; hidden <= 1024. w_gate_up interleaves the two
- * weights in blocks of 16 rows: rows [32i, 32i+16) = gate rows [16i, 16i+16), rows
- * [32i+16, 32i+32) = up rows [16i, 16i+16). Replaces gate_proj, up_proj, act_fn and mul
- * (export.py:378-414). */
-int dli_hip_gate_up_silu(const void* xn, const void* w_gate_up, void* out, int64_t m, int64_t ffn,
-                         int64_t hidden_size, void* stream);
+/* [xn = rms_norm(hidden) * norm_weight when norm_weight is non-NULL, else xn = hidden] ->
+ * gate/up projections of xn -> silu(gate) * up, out [m, ffn]; hidden <= 1024. w_gate_up
+ * interleaves the two weights in blocks of 16 rows: rows [32i, 32i+16) = gate rows
+ * [16i, 16i+16), rows [32i+16, 32i+32) = up rows [16i, 16i+16). Replaces
+ * post_attention_layernorm, gate_proj, up_proj, act_fn and mul (export.py:378-414). */
+int dli_hip_gate_up_silu(const void* hidden, const void* norm_weight, const void* w_gate_up,
+                         void* out, int64_t m, int64_t ffn, int64_t hidden_size, float eps,
+                         void* stream);
 
 /* logits = xn W^T (fp32 accumulation) -> ids[m] = argmax (first maximum); hidden <= 1024.
  * logits may be NULL (only ids) or float32 / bfloat16 [m, vocab]. Replaces lm_head

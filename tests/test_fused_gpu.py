@@ -37,26 +37,31 @@ def rope_tables(max_pos, d, theta=10000.0):
     return f.cos().float().to(DEV), f.sin().float().to(DEV)
 
 
+@pytest.mark.parametrize("norm", [False, True])
 @pytest.mark.parametrize("B,H,hq,hkv,positions", [
     (1, 128, 2, 1, [0]),
     (5, 256, 4, 2, [0, 63, 64, 130, 5]),
     (32, 896, 14, 2, None),   # Qwen2-0.5B shape, positions spread over 4 cache blocks
     (40, 256, 4, 2, None),    # 33..64 rows
 ])
-def test_qkv_rope_append(B, H, hq, hkv, positions):
+def test_qkv_rope_append(B, H, hq, hkv, positions, norm):
     d = 64
     n = (hq + 2 * hkv) * d
     if positions is None:
         positions = [(7 * b + 3) % 250 for b in range(B)]
     x, w, b = rand((B, H), 1), rand((n, H), 2, 0.05), rand((n,), 3, 0.1)
+    nw = (1 + rand((H,), 4, 0.1).float()).to(torch.bfloat16)
     cos, sin = rope_tables(256, d)
     pos = torch.tensor(positions, dtype=torch.int64, device=DEV)
     e = dli.Engine().load_plugin()
     e.configure_kv_cache(block_size=64, max_seq_len=256)
-    out = run_op("qkv_rope_append", {"x": x, "w": w, "b": b, "cos": cos, "sin": sin, "pos": pos},
-                 attrs={"kv_cache": "L", "q_heads": hq, "kv_heads": hkv, "head_dim": d},
+    inputs = {"x": x, "nw": nw} if norm else {"x": x}
+    inputs.update({"w": w, "b": b, "cos": cos, "sin": sin, "pos": pos})
+    out = run_op("qkv_rope_append", inputs,
+                 attrs={"kv_cache": "L", "q_heads": hq, "kv_heads": hkv, "head_dim": d, "eps": 1e-6},
                  engine=e)["output"]
-    y = R(ops.linear(to_np(x), to_np(w), to_np(b)))  # [B, n]
+    xn = R(ops.rms_norm(to_np(x), to_np(nw), 1e-6)) if norm else to_np(x)
+    y = R(ops.linear(xn, to_np(w), to_np(b)))  # [B, n]
     q = y[:, :hq * d].reshape(B, hq, 1, d)
     k = y[:, hq * d:(hq + hkv) * d].reshape(B, hkv, 1, d)
     v = y[:, (hq + hkv) * d:].reshape(B, hkv, 1, d)
@@ -109,24 +114,33 @@ def test_linear_residual_norm(B, N, K, splits, bias):
     assert_close(out["xn"], R(ops.rms_norm(h, to_np(nw), 1e-6)), "bfloat16")
 
 
-@pytest.mark.parametrize("B,N,K,splits,bias", CASES[:3] + [(16, 4096, 1024, 1, True)])
+@pytest.mark.parametrize("B,N,K,splits,bias", CASES + [(16, 4096, 1024, 1, True),
+                                                      (16, 4096, 1024, 2, True)])
 def test_linear_residual(B, N, K, splits, bias):
-    if N > 1024 and splits > 1:
-        pytest.skip("split-K path is limited to n <= 1024")
+    """splits > 1: the last split to finish a tile sums the partials; the second call checks that
+    the first left every arrival counter at zero."""
     x, w, res = rand((B, K), 20), rand((N, K), 21, 0.03), rand((B, N), 22)
     inputs = {"x": x, "w": w, "res": res}
     if bias:
         inputs["b"] = rand((N,), 23, 0.1)
-    out = run_op("linear_residual", inputs, attrs={"splits": splits})["output"]
-    assert_close(out, _residual_oracle(x, w, res, inputs.get("b")), "bfloat16")
+    e = dli.Engine().load_plugin()
+    expect = _residual_oracle(x, w, res, inputs.get("b"))
+    for _ in range(2):
+        out = run_op("linear_residual", inputs, attrs={"splits": splits}, engine=e)["output"]
+        assert_close(out, expect, "bfloat16")
 
 
+@pytest.mark.parametrize("norm", [False, True])
 @pytest.mark.parametrize("B,H,F", [(1, 128, 64), (7, 896, 4864), (32, 896, 4864), (64, 256, 512)])
-def test_gate_up_silu(B, H, F):
+def test_gate_up_silu(B, H, F, norm):
     x, wg, wu = rand((B, H), 30), rand((F, H), 31, 0.05), rand((F, H), 32, 0.05)
-    out = run_op("gate_up_silu", {"x": x, "w": interleave_gate_up(wg, wu)})["output"]
-    g = R(ops.linear(to_np(x), to_np(wg)))
-    u = R(ops.linear(to_np(x), to_np(wu)))
+    nw = (1 + rand((H,), 33, 0.1).float()).to(torch.bfloat16)
+    inputs = {"x": x, "nw": nw} if norm else {"x": x}
+    inputs["w"] = interleave_gate_up(wg, wu)
+    out = run_op("gate_up_silu", inputs, attrs={"eps": 1e-6})["output"]
+    xn = R(ops.rms_norm(to_np(x), to_np(nw), 1e-6)) if norm else to_np(x)
+    g = R(ops.linear(xn, to_np(wg)))
+    u = R(ops.linear(xn, to_np(wu)))
     assert_close(out, R(R(ops.silu(g)) * u), "bfloat16")
 
 
