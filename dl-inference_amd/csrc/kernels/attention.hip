@@ -297,9 +297,9 @@ __device__ __forceinline__ void attendBlock(SoftmaxState& st8, const KvBlockRegs
 #pragma unroll
     for (int w2 = 0; w2 < 4; ++w2) {
       const float a0 = p[w2 / 2][(w2 % 2) * 2], a1 = p[w2 / 2][(w2 % 2) * 2 + 1];
-      phi.w[w2] = packBf16x2(a0, a1);
-      plo.w[w2] = packBf16x2(a0 - bf16ToFloat(static_cast<uint16_t>(phi.w[w2])),
-                             a1 - bf16ToFloat(static_cast<uint16_t>(phi.w[w2] >> 16)));
+      phi[w2] = packBf16x2(a0, a1);
+      plo[w2] = packBf16x2(a0 - bf16ToFloat(static_cast<uint16_t>(phi[w2])),
+                             a1 - bf16ToFloat(static_cast<uint16_t>(phi[w2] >> 16)));
     }
 #pragma unroll
     for (int d = 0; d < 4; ++d) {

@@ -65,25 +65,27 @@ __device__ __forceinline__ void normalizeFragments(typename SkinnyCore<NF, MB, k
 #pragma unroll
   for (int u = 0; u < kU; ++u) {
     const int s = wave + u * kWaves;
-    const bool live = s < steps;
-    const int64_t k0 = static_cast<int64_t>(live ? s : 0) * 64 + g * 8;
-    wv[u][0] = live ? load16(norm_w + k0) : zero16();
-    wv[u][1] = live ? load16(norm_w + k0 + 32) : zero16();
+    if (s >= steps) break;  // uniform: wave comes from readfirstlane
+    const int64_t k0 = static_cast<int64_t>(s) * 64 + g * 8;
+    wv[u][0] = load16(norm_w + k0);
+    wv[u][1] = load16(norm_w + k0 + 32);
   }
   float sq[MB];
 #pragma unroll
   for (int b = 0; b < MB; ++b) {
     sq[b] = 0.f;
 #pragma unroll
-    for (int u = 0; u < kU; ++u)
+    for (int u = 0; u < kU; ++u) {
+      if (wave + u * kWaves >= steps) break;
 #pragma unroll
       for (int h = 0; h < 2; ++h)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const float lo = bf16ToFloat(static_cast<uint16_t>(xb.x[u][b][h].w[e]));
-          const float hi = bf16ToFloat(static_cast<uint16_t>(xb.x[u][b][h].w[e] >> 16));
+          const float lo = bf16ToFloat(static_cast<uint16_t>(xb.x[u][b][h][e]));
+          const float hi = bf16ToFloat(static_cast<uint16_t>(xb.x[u][b][h][e] >> 16));
           sq[b] += lo * lo + hi * hi;
         }
+    }
     sq[b] += __shfl_xor(sq[b], 16, kWave);
     sq[b] += __shfl_xor(sq[b], 32, kWave);
     if (g == 0) lds[wave * Core::kTileM + b * 16 + r] = sq[b];
@@ -99,20 +101,22 @@ __device__ __forceinline__ void normalizeFragments(typename SkinnyCore<NF, MB, k
   }
   __syncthreads();  // lds is reused by the tile reductions
 #pragma unroll
-  for (int u = 0; u < kU; ++u)
+  for (int u = 0; u < kU; ++u) {
+    if (wave + u * kWaves >= steps) break;
 #pragma unroll
     for (int b = 0; b < MB; ++b)
 #pragma unroll
       for (int h = 0; h < 2; ++h)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const uint32_t xw = xb.x[u][b][h].w[e], ww = wv[u][h].w[e];
+          const uint32_t xw = xb.x[u][b][h][e], ww = wv[u][h][e];
           const float lo = bf16ToFloat(static_cast<uint16_t>(xw)) * inv[b] *
                            bf16ToFloat(static_cast<uint16_t>(ww));
           const float hi = bf16ToFloat(static_cast<uint16_t>(xw >> 16)) * inv[b] *
                            bf16ToFloat(static_cast<uint16_t>(ww >> 16));
-          xb.x[u][b][h].w[e] = packBf16x2(lo, hi);
+          xb.x[u][b][h][e] = packBf16x2(lo, hi);
         }
+  }
 }
 
 // Weight tiles t = blockIdx.x, + gridDim.x, ... (16 * NF rows each) against one x whose
@@ -125,7 +129,8 @@ __device__ __forceinline__ void tileLoop(const uint16_t* w, const XGlobal& xs, i
                                          int M, float* lds, const uint16_t* norm_w, float eps,
                                          Epi&& epi) {
   using Core = SkinnyCore<NF, MB, kWaves>;
-  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int lane = threadIdx.x % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int r = lane % 16, g = lane / 16;
   const int steps = K / 64;
   const int64_t tiles = (N + Core::kTileN - 1) / Core::kTileN;
@@ -134,8 +139,10 @@ __device__ __forceinline__ void tileLoop(const uint16_t* w, const XGlobal& xs, i
   if (t >= tiles) return;
   typename Core::WBatch bufA, bufB;
   typename Core::XBatch xb;
+  // x first: loads complete in issue order, so the RMSNorm of x (VALU) overlaps the weight
+  // stream instead of waiting behind it.
+  Core::issueX(xb, Core::xrows(xs, M, r, g), wave, steps);
   Core::issueW(bufA, Core::rows(w, N, K, t * Core::kTileN, r, g), wave, steps);
-  Core::issueX(xb, xs, M, wave, steps, r, g);
   if (norm_w != nullptr) normalizeFragments<NF, MB>(xb, norm_w, K, eps, lds, wave, steps, r, g);
   auto tile = [&](const typename Core::WBatch& wb, int64_t tt) {
     f32x4 acc[NF][MB];

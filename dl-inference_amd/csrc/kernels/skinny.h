@@ -24,9 +24,9 @@ namespace dk {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-struct alignas(16) U128 {
-  uint32_t w[4];
-};
+// 16 bytes as a native 4 x u32 vector: kept in 4 consecutive VGPRs, which is the register
+// layout an MFMA operand needs, so no moves are required to feed it.
+typedef uint32_t U128 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ bf16x8 asBf16x8(const U128& v) { return __builtin_bit_cast(bf16x8, v); }
 
@@ -34,11 +34,7 @@ __device__ __forceinline__ U128 load16(const void* p) {
   return *reinterpret_cast<const U128*>(p);
 }
 
-__device__ __forceinline__ U128 zero16() {
-  U128 z;
-  z.w[0] = z.w[1] = z.w[2] = z.w[3] = 0;
-  return z;
-}
+__device__ __forceinline__ U128 zero16() { return U128{0u, 0u, 0u, 0u}; }
 
 // The B operand (the skinny activation x): [M, K] row-major with `stride` elements per row.
 struct XGlobal {
@@ -61,9 +57,12 @@ struct SkinnyCore {
     U128 x[kUnroll][MB][2];
   };
 
+  // Row pointers of this lane (row r of each 16-row block, columns from g * 8). Rows past N
+  // (weights) or M (x) are clamped to the last valid row: their loads stay in bounds and the
+  // products land only in output rows and columns the epilogues discard, so the loads need no
+  // per-lane predicate.
   struct Rows {
     const uint16_t* w[NF];
-    bool valid[NF];
   };
 
   __device__ __forceinline__ static Rows rows(const uint16_t* w, int64_t N, int64_t K, int64_t n0,
@@ -72,41 +71,53 @@ struct SkinnyCore {
 #pragma unroll
     for (int f = 0; f < NF; ++f) {
       const int64_t n = n0 + f * 16 + r;
-      rw.valid[f] = n < N;
-      rw.w[f] = w + (rw.valid[f] ? n : 0) * K + g * 8;
+      rw.w[f] = w + (n < N ? n : N - 1) * K + g * 8;
     }
     return rw;
   }
 
-  // Weight loads of the batch whose first step is s0 (steps s0 + u * kWaves).
+  struct XRows {
+    const uint16_t* x[MB];
+  };
+
+  __device__ __forceinline__ static XRows xrows(const XGlobal& xs, int M, int r, int g) {
+    XRows xr;
+#pragma unroll
+    for (int b = 0; b < MB; ++b) {
+      const int m = b * 16 + r;
+      xr.x[b] = xs.x + static_cast<int64_t>(m < M ? m : M - 1) * xs.stride + g * 8;
+    }
+    return xr;
+  }
+
+  // Weight loads of the batch whose first step is s0 (steps s0 + u * kWaves). s0 is uniform
+  // over the wave, so steps past step_end are skipped with a scalar branch; their registers are
+  // never read (compute stops at step_end).
   __device__ __forceinline__ static void issueW(WBatch& bt, const Rows& rw, int s0, int step_end) {
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       const int s = s0 + u * kWaves;
-      const bool live = s < step_end;
-      const int64_t k0 = static_cast<int64_t>(live ? s : 0) * 64;
+      if (s >= step_end) break;
+      const int64_t k0 = static_cast<int64_t>(s) * 64;
 #pragma unroll
       for (int f = 0; f < NF; ++f) {
-        bt.a[u][f][0] = (live && rw.valid[f]) ? load16(rw.w[f] + k0) : zero16();
-        bt.a[u][f][1] = (live && rw.valid[f]) ? load16(rw.w[f] + k0 + 32) : zero16();
+        bt.a[u][f][0] = load16(rw.w[f] + k0);
+        bt.a[u][f][1] = load16(rw.w[f] + k0 + 32);
       }
     }
   }
 
-  // x loads of the same batch; rows m >= M read as zero.
-  __device__ __forceinline__ static void issueX(XBatch& bt, const XGlobal& xs, int M, int s0,
-                                                int step_end, int r, int g) {
+  // x loads of the same batch.
+  __device__ __forceinline__ static void issueX(XBatch& bt, const XRows& xr, int s0, int step_end) {
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       const int s = s0 + u * kWaves;
-      const bool live = s < step_end;
-      const int64_t k0 = static_cast<int64_t>(live ? s : 0) * 64 + g * 8;
+      if (s >= step_end) break;
+      const int64_t k0 = static_cast<int64_t>(s) * 64;
 #pragma unroll
       for (int b = 0; b < MB; ++b) {
-        const int m = b * 16 + r;
-        const bool ok = live && m < M;
-        bt.x[u][b][0] = ok ? load16(xs.x + m * xs.stride + k0) : zero16();
-        bt.x[u][b][1] = ok ? load16(xs.x + m * xs.stride + k0 + 32) : zero16();
+        bt.x[u][b][0] = load16(xr.x[b] + k0);
+        bt.x[u][b][1] = load16(xr.x[b] + k0 + 32);
       }
     }
   }
@@ -138,33 +149,37 @@ struct SkinnyCore {
   // Accumulates steps [step_begin, step_end) of the tile at weight row n0 and leaves the reduced
   // fp32 tile [kTileN][kTileM] in lds[0 .. tile). Batches are double-buffered: the next batch's
   // loads are in flight while the current one is multiplied.
+  // Accumulates steps [step_begin, step_end) of the tile at weight row n0 and leaves the reduced
+  // fp32 tile [kTileN][kTileM] in lds[0 .. tile). Batches are double-buffered: the next batch's
+  // loads are in flight while the current one is multiplied.
   __device__ __forceinline__ static void run(const uint16_t* __restrict__ w, const XGlobal& xs,
                                              int64_t N, int64_t K, int M, int64_t n0,
                                              int step_begin, int step_end, float* lds) {
     const int lane = threadIdx.x % kWave;
-    const int wave = threadIdx.x / kWave;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int r = lane % 16, g = lane / 16;
     f32x4 acc[NF][MB];
     zero(acc);
     const Rows rw = rows(w, N, K, n0, r, g);
+    const XRows xr = xrows(xs, M, r, g);
     constexpr int kStride = kUnroll * kWaves;
     WBatch w0, w1;
     XBatch x0, x1;
     int s0 = step_begin + wave;
     issueW(w0, rw, s0, step_end);
-    issueX(x0, xs, M, s0, step_end, r, g);
+    issueX(x0, xr, s0, step_end);
     for (; s0 < step_end; s0 += 2 * kStride) {
       const int s1 = s0 + kStride;
       if (s1 < step_end) {
         issueW(w1, rw, s1, step_end);
-        issueX(x1, xs, M, s1, step_end, r, g);
+        issueX(x1, xr, s1, step_end);
       }
       compute(acc, w0, x0, s0, step_end);
       if (s1 >= step_end) break;
       const int s2 = s1 + kStride;
       if (s2 < step_end) {
         issueW(w0, rw, s2, step_end);
-        issueX(x0, xs, M, s2, step_end, r, g);
+        issueX(x0, xr, s2, step_end);
       }
       compute(acc, w1, x1, s1, step_end);
     }
