@@ -10,6 +10,7 @@ namespace dli::hip {
 namespace {
 
 constexpr int kThreads = 256;
+constexpr int kNormThreads = 512;    // qkv_rope_append and gate_up_silu workgroups
 constexpr int kTileN = 32;           // weight rows per workgroup of gate_up / lm_head (NF = 2)
 constexpr int kRowTile = 16;         // weight rows per workgroup of qkv / linear_residual / partial
 constexpr int kResWaves = 8;         // waves per linear_residual workgroup
@@ -60,8 +61,8 @@ size_t splitPartialBytes(int64_t n, int64_t m, int splits) {
 }
 
 // Workgroups of a grid-strided tile loop: one per tile, at most as many as are resident at once
-// (two 256-thread workgroups per CU fit below 256 VGPRs; the 64-row variants use more). With an
-// RMSNorm prologue (VALU work per workgroup) at most one per CU, so no SIMD normalizes twice.
+// (two 256-thread workgroups per CU fit below 256 VGPRs; the 64-row variants use more). The
+// 512-thread RMSNorm-prologue kernels fit one per CU.
 int tileGrid(int64_t tiles, int64_t m, unsigned* grid, bool prologue = false) {
   int cus = 0;
   if (int rc = computeUnits(&cus)) return rc;
@@ -135,7 +136,8 @@ int dli_hip_qkv_rope_append(const void* hidden, const void* norm_weight, const v
   if (tiles > 65535) return bad(op, "too many q|k|v rows");
   const int pos64 = positions_dtype == DLI_I64 ? 1 : 0;
   // one tile per workgroup: the kernel prefetches the epilogue operands of tile blockIdx.x
-  return launch(*k_qkv.pick(batch), {static_cast<unsigned>(tiles)}, {kThreads}, 0, stream, hidden,
+  return launch(*k_qkv.pick(batch), {static_cast<unsigned>(tiles)}, {kNormThreads}, 0, stream,
+                hidden,
                 norm_weight, eps, w_qkv, b_qkv, cos_table, sin_table, max_pos, positions, pos64,
                 q_out, key_pool, value_pool, block_table, block_size, max_blocks,
                 static_cast<int>(batch), static_cast<int>(hidden_size),
@@ -191,7 +193,7 @@ int dli_hip_gate_up_silu(const void* hidden, const void* norm_weight, const void
     return bad(op, "hidden, norm_weight and w_gate_up must be 16-byte aligned");
   unsigned grid = 0;
   if (int rc = tileGrid(ffn / 16, m, &grid, norm_weight != nullptr)) return rc;
-  return launch(*k_gate_up.pick(m), {grid}, {kThreads}, 0, stream, hidden, norm_weight, eps,
+  return launch(*k_gate_up.pick(m), {grid}, {kNormThreads}, 0, stream, hidden, norm_weight, eps,
                 w_gate_up, out, static_cast<int>(m), ffn, static_cast<int>(hidden_size));
 }
 

@@ -30,6 +30,11 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
+// qkv_rope_append and gate_up_silu (RMSNorm prologue): 8 waves, two per SIMD, so one wave's
+// normalize VALU runs while the other is held issuing its weight loads.
+constexpr int kNormWaves = 8;
+constexpr int kNormThreads = kNormWaves * kWave;
+constexpr int kNormUnroll = 2;  // 8 waves x 2 steps x 64 columns: hidden <= 1024
 constexpr int kResWaves = 8;         // linear_residual: 8 waves split K inside a workgroup
 constexpr int kNormPer = 4;          // residual_rms_norm: N <= kThreads * kNormPer
 constexpr int kMaxNormSplits = 8;    // residual_rms_norm: split-K partials summed
@@ -52,19 +57,18 @@ struct KvCacheArgs {
 };
 
 // RMSNorm of x fragments held in registers, every 64-column step of K being in `xb` (lanes of
-// wave w hold steps w, w + kWaves, ...): x[m, k] <- bf16(x[m, k] * rsqrt(mean_k x[m, k]^2 + eps)
+// wave w hold steps w, w + kW, ...): x[m, k] <- bf16(x[m, k] * rsqrt(mean_k x[m, k]^2 + eps)
 // * w[k]) (rms_norm/kernel.py:6-14). Row sums of squares are reduced over the 4 lanes of a row
-// and then over the waves through lds (kWaves * 16 * MB floats) in a fixed order.
-template <int NF, int MB>
-__device__ __forceinline__ void normalizeFragments(typename SkinnyCore<NF, MB, kWaves>::XBatch& xb,
-                                                   const uint16_t* norm_w, int K, float eps,
-                                                   float* lds, int wave, int steps, int r, int g) {
-  using Core = SkinnyCore<NF, MB, kWaves>;
-  constexpr int kU = sizeof(xb.x) / sizeof(xb.x[0]);  // kUnroll
+// and then over the waves through lds (kW * 16 * MB floats) in a fixed order.
+template <int NF, int MB, int kW, int kU>
+__device__ __forceinline__ void normalizeFragments(
+    typename SkinnyCore<NF, MB, kW, kU>::XBatch& xb, const uint16_t* norm_w, int K, float eps,
+    float* lds, int wave, int steps, int r, int g) {
+  using Core = SkinnyCore<NF, MB, kW, kU>;
   U128 wv[kU][2];
 #pragma unroll
   for (int u = 0; u < kU; ++u) {
-    const int s = wave + u * kWaves;
+    const int s = wave + u * kW;
     if (s >= steps) break;  // uniform: wave comes from readfirstlane
     const int64_t k0 = static_cast<int64_t>(s) * 64 + g * 8;
     wv[u][0] = load16(norm_w + k0);
@@ -76,7 +80,7 @@ __device__ __forceinline__ void normalizeFragments(typename SkinnyCore<NF, MB, k
     sq[b] = 0.f;
 #pragma unroll
     for (int u = 0; u < kU; ++u) {
-      if (wave + u * kWaves >= steps) break;
+      if (wave + u * kW >= steps) break;
 #pragma unroll
       for (int h = 0; h < 2; ++h)
 #pragma unroll
@@ -96,13 +100,13 @@ __device__ __forceinline__ void normalizeFragments(typename SkinnyCore<NF, MB, k
   for (int b = 0; b < MB; ++b) {
     float total = 0.f;
 #pragma unroll
-    for (int v = 0; v < kWaves; ++v) total += lds[v * Core::kTileM + b * 16 + r];
+    for (int v = 0; v < kW; ++v) total += lds[v * Core::kTileM + b * 16 + r];
     inv[b] = 1.0f / sqrtf(total / static_cast<float>(K) + eps);
   }
   __syncthreads();  // lds is reused by the tile reductions
 #pragma unroll
   for (int u = 0; u < kU; ++u) {
-    if (wave + u * kWaves >= steps) break;
+    if (wave + u * kW >= steps) break;
 #pragma unroll
     for (int b = 0; b < MB; ++b)
 #pragma unroll
@@ -123,12 +127,12 @@ __device__ __forceinline__ void normalizeFragments(typename SkinnyCore<NF, MB, k
 // fragments are loaded once (and RMS-normalized with norm_w when it is non-NULL) and stay in
 // registers; the next tile's weights stream in while the current one is multiplied. epi(t)
 // reads the reduced tile [16 NF][16 MB] from lds (row n, column m at lds[n * 16 MB + m]).
-// Requires K / 64 <= 4 * kWaves.
-template <int NF, int MB, typename Epi>
+// Requires K / 64 <= kU * kW.
+template <int NF, int MB, int kW, int kU, typename Epi>
 __device__ __forceinline__ void tileLoop(const uint16_t* w, const XGlobal& xs, int64_t N, int K,
                                          int M, float* lds, const uint16_t* norm_w, float eps,
                                          Epi&& epi) {
-  using Core = SkinnyCore<NF, MB, kWaves>;
+  using Core = SkinnyCore<NF, MB, kW, kU>;
   const int lane = threadIdx.x % kWave;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int r = lane % 16, g = lane / 16;
@@ -140,10 +144,14 @@ __device__ __forceinline__ void tileLoop(const uint16_t* w, const XGlobal& xs, i
   typename Core::WBatch bufA, bufB;
   typename Core::XBatch xb;
   // x first: loads complete in issue order, so the RMSNorm of x (VALU) overlaps the weight
-  // stream instead of waiting behind it.
+  // stream instead of waiting behind it. The second tile's weights are requested before the
+  // prologue too.
   Core::issueX(xb, Core::xrows(xs, M, r, g), wave, steps);
   Core::issueW(bufA, Core::rows(w, N, K, t * Core::kTileN, r, g), wave, steps);
-  if (norm_w != nullptr) normalizeFragments<NF, MB>(xb, norm_w, K, eps, lds, wave, steps, r, g);
+  if (t + stride < tiles)
+    Core::issueW(bufB, Core::rows(w, N, K, (t + stride) * Core::kTileN, r, g), wave, steps);
+  if (norm_w != nullptr)
+    normalizeFragments<NF, MB, kW, kU>(xb, norm_w, K, eps, lds, wave, steps, r, g);
   auto tile = [&](const typename Core::WBatch& wb, int64_t tt) {
     f32x4 acc[NF][MB];
     Core::zero(acc);
@@ -152,8 +160,8 @@ __device__ __forceinline__ void tileLoop(const uint16_t* w, const XGlobal& xs, i
     epi(tt);
     __syncthreads();  // lds is reused by the next tile
   };
-  for (; t < tiles; t += 2 * stride) {
-    if (t + stride < tiles)
+  for (bool first = true; t < tiles; t += 2 * stride, first = false) {
+    if (!first && t + stride < tiles)
       Core::issueW(bufB, Core::rows(w, N, K, (t + stride) * Core::kTileN, r, g), wave, steps);
     tile(bufA, t);
     if (t + stride >= tiles) break;
@@ -172,7 +180,7 @@ __device__ void qkv_rope_append_impl(const uint16_t* x, const uint16_t* norm_w, 
                                      const float* sin_t, int64_t max_pos, const void* positions,
                                      int pos64, uint16_t* q_out, KvCacheArgs kv, int M, int K,
                                      int Hq, int Hkv, int D) {
-  using Core = SkinnyCore<1, MB, kWaves>;
+  using Core = SkinnyCore<1, MB, kNormWaves, kNormUnroll>;
   __shared__ float lds[Core::kLdsFloats];
   const int64_t N = static_cast<int64_t>(Hq + 2 * Hkv) * D;
   const int64_t n0 = static_cast<int64_t>(blockIdx.x) * Core::kTileN;
@@ -184,19 +192,19 @@ __device__ void qkv_rope_append_impl(const uint16_t* x, const uint16_t* norm_w, 
   // Epilogue operands do not depend on the GEMM: fetch them first (position, then the rotary
   // coefficients, the bias pair and the cache block of this thread's (pair, row) items).
   constexpr int kPairs = (Core::kTileN / 2) * Core::kTileM;
-  constexpr int kItems = (kPairs + kThreads - 1) / kThreads;
+  constexpr int kItems = (kPairs + kNormThreads - 1) / kNormThreads;
   int64_t pos[kItems];
   float cs[kItems][2], bs[kItems][2];
   int64_t blk[kItems];
 #pragma unroll
   for (int it = 0; it < kItems; ++it) {
-    const int idx = threadIdx.x + it * kThreads;
+    const int idx = threadIdx.x + it * kNormThreads;
     const int m = idx % Core::kTileM;
     pos[it] = (idx < kPairs && m < M) ? loadIndex(positions, pos64, m) : -1;
   }
 #pragma unroll
   for (int it = 0; it < kItems; ++it) {
-    const int idx = threadIdx.x + it * kThreads;
+    const int idx = threadIdx.x + it * kNormThreads;
     const int pair = idx / Core::kTileM, m = idx % Core::kTileM;
     const int64_t n = n0 + 2 * pair;
     const bool live = pos[it] >= 0 && n < N;
@@ -212,10 +220,10 @@ __device__ void qkv_rope_append_impl(const uint16_t* x, const uint16_t* norm_w, 
                   : -1;
   }
 
-  tileLoop<1, MB>(w, XGlobal{x, K}, N, K, M, lds, norm_w, eps, [&](int64_t) {
+  tileLoop<1, MB, kNormWaves, kNormUnroll>(w, XGlobal{x, K}, N, K, M, lds, norm_w, eps, [&](int64_t) {
 #pragma unroll
   for (int it = 0; it < kItems; ++it) {
-    const int idx = threadIdx.x + it * kThreads;
+    const int idx = threadIdx.x + it * kNormThreads;
     const int pair = idx / Core::kTileM;
     const int m = idx % Core::kTileM;
     const int64_t n = n0 + 2 * pair;
@@ -417,9 +425,10 @@ __device__ void residual_rms_norm_impl(const float* partials, int splits, const 
 template <int MB>
 __device__ void gate_up_silu_impl(const uint16_t* x, const uint16_t* norm_w, float eps,
                                   const uint16_t* w_gu, uint16_t* out, int M, int64_t F, int K) {
-  using Core = SkinnyCore<2, MB, kWaves>;
+  using Core = SkinnyCore<2, MB, kNormWaves, kNormUnroll>;
   __shared__ float lds[Core::kLdsFloats];
-  tileLoop<2, MB>(w_gu, XGlobal{x, K}, 2 * F, K, M, lds, norm_w, eps, [&](int64_t t) {
+  tileLoop<2, MB, kNormWaves, kNormUnroll>(w_gu, XGlobal{x, K}, 2 * F, K, M, lds, norm_w, eps,
+                                           [&](int64_t t) {
     const int64_t f0 = t * 16;  // tile t = gate rows [16t, 16t+16) then up rows [16t, 16t+16)
     for (int idx = threadIdx.x; idx < 16 * Core::kTileM; idx += blockDim.x) {
       const int j = idx % 16, m = idx / 16;
@@ -447,7 +456,7 @@ __device__ void lm_head_argmax_impl(const uint16_t* xn, const uint16_t* w, void*
   __shared__ float lds[Core::kLdsFloats + kLmQuarters * Core::kTileM];
   __shared__ int lds_arg[kLmQuarters * Core::kTileM];
   const int64_t tiles = (V + Core::kTileN - 1) / Core::kTileN;
-  tileLoop<2, MB>(w, XGlobal{xn, K}, V, K, M, lds, nullptr, 0.f, [&](int64_t t) {
+  tileLoop<2, MB, kWaves, 4>(w, XGlobal{xn, K}, V, K, M, lds, nullptr, 0.f, [&](int64_t t) {
     const int64_t n0 = t * Core::kTileN;
     if (logits != nullptr) {
       for (int idx = threadIdx.x; idx < Core::kTileN * Core::kTileM; idx += blockDim.x) {
@@ -556,7 +565,7 @@ __device__ void argmax_finalize_impl(const float* part_val, const int32_t* part_
 }  // namespace
 
 #define DK_DECODE_KERNELS(MB)                                                                     \
-  extern "C" __global__ void __launch_bounds__(kThreads) qkv_rope_append_m##MB(                   \
+  extern "C" __global__ void __launch_bounds__(kNormThreads) qkv_rope_append_m##MB(               \
       const uint16_t* x, const uint16_t* norm_w, float eps, const uint16_t* w,                    \
       const uint16_t* bias, const float* cos_t, const float* sin_t, int64_t max_pos,              \
       const void* positions, int pos64, uint16_t* q_out, uint16_t* k_pool, uint16_t* v_pool,      \
@@ -583,7 +592,7 @@ __device__ void argmax_finalize_impl(const float* part_val, const int32_t* part_
       int splits) {                                                                               \
     linear_partial_impl<MB>(x, w, partials, M, N, K, splits);                                     \
   }                                                                                               \
-  extern "C" __global__ void __launch_bounds__(kThreads) gate_up_silu_m##MB(                      \
+  extern "C" __global__ void __launch_bounds__(kNormThreads) gate_up_silu_m##MB(                  \
       const uint16_t* x, const uint16_t* norm_w, float eps, const uint16_t* w_gu, uint16_t* out,  \
       int M, int64_t F, int K) {                                                                  \
     gate_up_silu_impl<MB>(x, norm_w, eps, w_gu, out, M, F, K);                                    \
