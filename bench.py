@@ -4,12 +4,15 @@ Workload: Qwen2-0.5B-shape (24 layers, hidden 896, 14/2 heads, head_dim 64, MLP 
 151936, tied embeddings), random-init bf16, greedy decode at batch 32 with every sequence at
 context 4096 (a seeded synthetic KV context fills positions 0..4094; each step writes position
 4095 and attends over 4096 keys). One step = one replay of the captured dli.graph.v1 decode
-step (fused operator graph) through Engine + libdli_hip_ops.so; inputs already in HBM.
+step through Engine + libdli_hip_ops.so; inputs already in HBM. --graph stack (default): every
+decoder layer in one persistent decoder_stack launch, then model.norm and lm_head + argmax;
+--graph fused: five launches per layer.
 
 Prints one JSON line: decode tok/s (whole job), ms/step, the step's HBM roofline fraction
 (algorithmic bytes = weights + KV read + KV write + bf16 logits), the dominant kernel's roofline
-(decode attention, timed live with HIP events on its stream) and a CPU baseline (the CPU oracle
-timed on a bounded sample of the same step on this host).
+(the decoder stack, or decode attention for the fused graph, timed live with HIP events on its
+stream) and a CPU baseline (the CPU oracle timed on a bounded sample of the same step on this
+host).
 """
 from __future__ import annotations
 
@@ -38,20 +41,27 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--splits", default=None, help="split-K per projection, e.g. o=2,down=4")
     ap.add_argument("--eager", action="store_true", help="run the step without graph capture")
+    ap.add_argument("--graph", choices=("stack", "fused"), default="stack",
+                    help="stack: all decoder layers in one persistent launch; fused: five "
+                         "launches per layer")
     ap.add_argument("--calibration-copy-mib", type=int, default=0,
                     help="after timing, copy this many MiB device-to-device 3 times (a plain copy "
                          "of known size that scales rocprofv3's FETCH_SIZE / WRITE_SIZE)")
     return ap.parse_args()
 
 
-TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "decode_attention_pmc_qwen2-0.5b_b32_ctx4096.txt")
+TRAFFIC_PROFILES = {
+    "stack": os.path.join(ROOT, "profiles", "decoder_stack_pmc_qwen2-0.5b_b32_ctx4096.txt"),
+    "fused": os.path.join(ROOT, "profiles", "decode_attention_pmc_qwen2-0.5b_b32_ctx4096.txt"),
+}
 
 
-def profiled_traffic():
-    """HBM bytes per decode-attention launch measured by two rocprofv3 --pmc runs (FETCH_SIZE,
-    WRITE_SIZE) scaled by a copy kernel of known size; recorded in the committed profile."""
+def profiled_traffic(graph):
+    """HBM bytes per launch of the dominant kernel measured by two rocprofv3 --pmc runs
+    (FETCH_SIZE, WRITE_SIZE) scaled by a copy kernel of known size; recorded in the committed
+    profile."""
     try:
-        for line in open(TRAFFIC_PROFILE):
+        for line in open(TRAFFIC_PROFILES[graph]):
             if line.startswith("traffic_bytes_per_launch:"):
                 return int(float(line.split(":")[1].split()[0]))
     except OSError:
@@ -65,6 +75,92 @@ def step_bytes(cfg, batch, context):
     kv_write = batch * cfg.kv_bytes_per_token()
     logits = batch * cfg.vocab * 2
     return weights + kv_read + kv_write, weights, kv_read, kv_write, logits
+
+
+def time_decode_attention(session, cfg, B, ctx, pos, g, stream, hip, reps=200):
+    """Decode attention of one layer (same cache, fresh q) alone, timed with HIP events on the
+    stream it is launched on. Returns (kernel, average us, algorithmic bytes per launch)."""
+    import torch
+
+    e = session.engine.kv_cache_entry("layer_0")
+    q = torch.randn(B, cfg.heads, 1, cfg.head_dim, generator=g, device="cuda").to(torch.bfloat16)
+    out = torch.empty_like(q)
+    ws_bytes = hip.lib().dli_hip_paged_attention_workspace(B, cfg.heads, 1, cfg.head_dim,
+                                                            e["max_blocks"] * e["block_size"])
+    ws = torch.zeros((ws_bytes + 3) // 4, dtype=torch.float32, device="cuda")  # counters at 0
+    s_ptr = stream.cuda_stream
+
+    def attn():
+        hip.call("dli_hip_paged_attention", hip.BF16, q.data_ptr(), e["key"].data_ptr(),
+                 e["value"].data_ptr(), e["block_table"].data_ptr(), out.data_ptr(), B, cfg.heads,
+                 cfg.kv_heads, 1, cfg.head_dim, e["block_size"], e["max_blocks"], 0,
+                 pos.data_ptr(), hip.I64, 1, cfg.head_dim ** -0.5, ws.data_ptr(), ws_bytes, s_ptr)
+
+    us = _time_launches(attn, stream, reps)
+    nbytes = B * ctx * cfg.kv_heads * cfg.head_dim * 2 * 2 + 2 * B * cfg.heads * cfg.head_dim * 2
+    return "decode attention (decode_attention_d64)", us, nbytes
+
+
+def time_decoder_stack(session, cfg, B, ctx, pos, g, stream, hip, reps=20):
+    """The persistent decoder stack (every layer in one launch) alone, on the session's weights
+    and caches, timed with HIP events on the stream it is launched on. Algorithmic bytes per
+    launch: every layer's weights once, the K/V context read once, the new K/V written."""
+    import ctypes
+
+    import torch
+
+    L = cfg.layers
+    layers = (hip.DecoderLayer * L)()
+    layer_bytes = 0
+    for i in range(L):
+        p = f"model.layers.{i}"
+        names = [f"{p}.input_layernorm.weight", f"{p}.self_attn.qkv_proj.weight",
+                 f"{p}.self_attn.qkv_proj.bias", f"{p}.self_attn.o_proj.weight",
+                 f"{p}.post_attention_layernorm.weight", f"{p}.mlp.gate_up_proj.weight",
+                 f"{p}.mlp.down_proj.weight"]
+        t = [session.inputs[n] for n in names]
+        layer_bytes += sum(x.numel() * x.element_size() for x in t)
+        e = session.engine.kv_cache_entry(f"layer_{i}")
+        layers[i] = hip.DecoderLayer(*[x.data_ptr() for x in t], e["key"].data_ptr(),
+                                     e["value"].data_ptr(), e["block_table"].data_ptr())
+    e0 = session.engine.kv_cache_entry("layer_0")
+    ws_bytes = hip.lib().dli_hip_decoder_stack_workspace(L, B, cfg.hidden, cfg.heads,
+                                                          cfg.kv_heads, cfg.head_dim, cfg.ffn,
+                                                          e0["max_blocks"], 4)
+    ws = torch.zeros((ws_bytes + 3) // 4, dtype=torch.int32, device="cuda")
+    x = (torch.randn(B, cfg.hidden, generator=g, device="cuda") * 0.5).to(torch.bfloat16)
+    out = torch.empty_like(x)
+    cos, sin = session.inputs["rotary_cos"], session.inputs["rotary_sin"]
+    s_ptr = stream.cuda_stream
+
+    def stack():
+        hip.call("dli_hip_decoder_stack", layers, L, x.data_ptr(), out.data_ptr(),
+                 pos.data_ptr(), hip.I64, cos.data_ptr(), sin.data_ptr(), cos.shape[0],
+                 e0["block_size"], e0["max_blocks"], B, cfg.hidden, cfg.heads, cfg.kv_heads,
+                 cfg.head_dim, cfg.ffn, cfg.eps, 4, ws.data_ptr(), ws_bytes, s_ptr)
+
+    us = _time_launches(stack, stream, reps)
+    aborted = ctypes.c_int()
+    hip.call("dli_hip_decoder_stack_status", ws.data_ptr(), ctypes.byref(aborted), s_ptr)
+    if aborted.value:
+        raise RuntimeError("decoder_stack: a workgroup gave up waiting")
+    kv = cfg.kv_bytes_per_token()
+    nbytes = layer_bytes + B * ctx * kv + B * kv
+    return "decoder stack (decoder_stack_m2, all layers in one launch)", us, nbytes
+
+
+def _time_launches(fn, stream, reps):
+    import torch
+
+    for _ in range(5):
+        fn()
+    a0, a1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a0.record(stream)
+    for _ in range(reps):
+        fn()
+    a1.record(stream)
+    torch.cuda.synchronize()
+    return a0.elapsed_time(a1) * 1000.0 / reps
 
 
 def main():
@@ -92,7 +188,7 @@ def main():
     torch.manual_seed(0)
     weights = random_weights(cfg, seed=0, device=dev)
     session = DecodeSession(cfg, weights, batch=B, max_seq_len=ctx + 64, fused=True,
-                            splits=splits, logits_dtype="bfloat16")
+                            splits=splits, logits_dtype="bfloat16", stack=args.graph == "stack")
     g = torch.Generator(device=dev).manual_seed(1)
     ids = torch.randint(0, cfg.vocab, (B,), generator=g, device=dev)
     pos = torch.full((B,), ctx - 1, dtype=torch.int64, device=dev)
@@ -135,34 +231,11 @@ def main():
     total += logit_bytes
     step_gbs = total / (ms_per_step * 1e-3) / 1e9
 
-    # dominant kernel: decode attention of one layer (same cache, same q), timed with HIP
-    # events on the stream it is launched on
-    e = session.engine.kv_cache_entry("layer_0")
-    q = torch.randn(B, cfg.heads, 1, cfg.head_dim, generator=g, device=dev).to(torch.bfloat16)
-    out = torch.empty_like(q)
-    ws_bytes = hip.lib().dli_hip_paged_attention_workspace(B, cfg.heads, 1, cfg.head_dim,
-                                                            e["max_blocks"] * e["block_size"])
-    ws = torch.zeros((ws_bytes + 3) // 4, dtype=torch.float32, device=dev)  # counters start at 0
-    s_ptr = stream.cuda_stream
-
-    def attn():
-        hip.call("dli_hip_paged_attention", hip.BF16, q.data_ptr(), e["key"].data_ptr(),
-                 e["value"].data_ptr(), e["block_table"].data_ptr(), out.data_ptr(), B, cfg.heads,
-                 cfg.kv_heads, 1, cfg.head_dim, e["block_size"], e["max_blocks"], 0,
-                 pos.data_ptr(), hip.I64, 1, cfg.head_dim ** -0.5, ws.data_ptr(), ws_bytes, s_ptr)
-
-    for _ in range(5):
-        attn()
-    reps = 200
-    a0, a1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    a0.record(stream)
-    for _ in range(reps):
-        attn()
-    a1.record(stream)
-    torch.cuda.synchronize()
-    attn_us = a0.elapsed_time(a1) * 1000.0 / reps
-    attn_bytes = B * ctx * cfg.kv_heads * cfg.head_dim * 2 * 2 + 2 * B * cfg.heads * cfg.head_dim * 2
-    attn_gbs = attn_bytes / (attn_us * 1e-6) / 1e9
+    if args.graph == "stack":
+        kernel, dom_us, dom_bytes = time_decoder_stack(session, cfg, B, ctx, pos, g, stream, hip)
+    else:
+        kernel, dom_us, dom_bytes = time_decode_attention(session, cfg, B, ctx, pos, g, stream, hip)
+    dom_gbs = dom_bytes / (dom_us * 1e-6) / 1e9
 
     if args.calibration_copy_mib > 0:
         src = torch.empty(args.calibration_copy_mib << 20, dtype=torch.uint8, device=dev)
@@ -208,12 +281,15 @@ def main():
         "config": {"workload": "Qwen2-0.5B-shape bf16 greedy decode, batch 32, context 4096",
                    "model": "qwen2-0.5b-shape (random init)", "global_batch": B,
                    "seq_len": ctx, "layers": cfg.layers, "parallelism": "none (1 GPU)",
-                   "graph": "fused dli.graph.v1 decode step, HIP-graph replay",
+                   "graph": ("decoder_stack (one persistent launch for all layers)"
+                             if args.graph == "stack" else "fused (five launches per layer)")
+                   + " dli.graph.v1 decode step, HIP-graph replay",
                    "splits": splits},
-        "roofline": {"bound": "hbm", "kernel": "decode attention (decode_attention_d64 + combine)",
-                     "achieved": round(attn_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(attn_gbs / HBM_PEAK_GBS, 4), "traffic": profiled_traffic(),
-                     "avg_us": round(attn_us, 2), "bytes_per_launch": attn_bytes},
+        "roofline": {"bound": "hbm", "kernel": kernel,
+                     "achieved": round(dom_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(dom_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": profiled_traffic(args.graph),
+                     "avg_us": round(dom_us, 2), "bytes_per_launch": dom_bytes},
         "step_roofline": {"bound": "hbm", "bytes_per_step": total, "achieved": round(step_gbs, 1),
                           "peak": HBM_PEAK_GBS, "unit": "GB/s",
                           "frac": round(step_gbs / HBM_PEAK_GBS, 4),

@@ -1,5 +1,6 @@
 // Entry points of the fused decode kernels (csrc/kernels/decode.hip) and the MFMA decode
 // attention (csrc/kernels/attention.hip). Declared in include/dli_hip.h.
+#include <atomic>
 #include <cmath>
 #include <cstdlib>
 #include <string>
@@ -164,9 +165,9 @@ int dli_hip_linear_residual(const void* x, const void* w, const void* bias, cons
   unsigned* counters = reinterpret_cast<unsigned*>(static_cast<char*>(workspace) +
                                                    splitPartialBytes(n, m, splits));
   return launch(*k_linres_splitk.pick(m),
-                {static_cast<unsigned>(tiles), static_cast<unsigned>(splits)}, {kThreads}, 0,
-                stream, x, w, bias, residual, out, static_cast<int>(m), n, static_cast<int>(k),
-                splits, partials, counters);
+                {static_cast<unsigned>(tiles), static_cast<unsigned>(splits)}, {kResWaves * 64},
+                0, stream, x, w, bias, residual, out, static_cast<int>(m), n,
+                static_cast<int>(k), splits, partials, counters);
 }
 
 int dli_hip_linear_residual_norm(const void* x, const void* w, const void* bias,
@@ -254,12 +255,19 @@ size_t partialBytes(int64_t rows) {
   return alignUp(static_cast<size_t>(rows) * kMaxDecodeSplits * (2 + 64) * sizeof(float), 256);
 }
 
-int chooseSplits(int64_t pairs, int64_t max_blocks, int cus) {
-  static const int forced = [] {
-    const char* v = std::getenv("DLI_ATTN_SPLITS");
-    return v ? std::atoi(v) : 0;
-  }();
-  int64_t splits = forced > 0 ? forced : cus / pairs;
+}  // namespace
+
+namespace {
+// 0 = choose per call; set by dli_hip_set_decode_attention_splits or DLI_ATTN_SPLITS=<n>.
+std::atomic<int> forced_splits{[] {
+  const char* v = std::getenv("DLI_ATTN_SPLITS");
+  return v ? std::atoi(v) : 0;
+}()};
+}  // namespace
+
+int decodeAttentionSplits(int64_t pairs, int64_t max_blocks, int cus) {
+  const int forced = forced_splits.load(std::memory_order_relaxed);
+  int64_t splits = forced > 0 ? forced : (pairs > 0 ? cus / pairs : 1);
   // no more splits than wave groups of blocks, never fewer than the block ids allow
   const int64_t useful = (max_blocks + kDecWaves - 1) / kDecWaves;
   if (splits > useful) splits = useful;
@@ -268,7 +276,6 @@ int chooseSplits(int64_t pairs, int64_t max_blocks, int cus) {
   if (splits < 1) splits = 1;
   return static_cast<int>(splits);
 }
-}  // namespace
 
 int decodeAttentionFast(int dtype, const void* q, const void* key_pool, const void* value_pool,
                         const int32_t* block_table, void* out, int64_t batch, int64_t q_heads,
@@ -282,7 +289,7 @@ int decodeAttentionFast(int dtype, const void* q, const void* key_pool, const vo
   if (batch * kv_heads > 65535) return 1;
   int cus = 0;
   if (int rc = computeUnits(&cus)) return rc;
-  const int splits = chooseSplits(batch * kv_heads, max_blocks, cus);
+  const int splits = decodeAttentionSplits(batch * kv_heads, max_blocks, cus);
   if (splits > kMaxDecodeSplits) return 1;
   const int64_t rows = batch * q_heads;
   const size_t need = partialBytes(rows) + static_cast<size_t>(rows) * sizeof(unsigned);
@@ -310,3 +317,10 @@ size_t decodeAttentionWorkspace(int64_t batch, int64_t q_heads, int64_t seq_q, i
 }
 
 }  // namespace dli::hip
+
+extern "C" int dli_hip_set_decode_attention_splits(int splits) {
+  if (splits < 0 || splits > dli::hip::kMaxDecodeSplits)
+    return dli::hip::fail(DLI_HIP_EINVAL, "decode attention splits must be in [0, 32]");
+  dli::hip::forced_splits.store(splits, std::memory_order_relaxed);
+  return 0;
+}

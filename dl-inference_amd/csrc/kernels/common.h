@@ -11,6 +11,25 @@ namespace dk {
 
 constexpr int kWave = 64;
 
+// First statement of a function whose floating-point results must not depend on where it is
+// inlined: no multiply-add contraction, so every kernel that shares the function rounds
+// identically (the fused and the persistent decode paths are compared bit for bit).
+#define FP_EXACT _Pragma("clang fp contract(off)")
+
+// A wait that is not needed (data produced by an earlier launch).
+struct NoWait {
+  __device__ __forceinline__ void operator()() const {}
+};
+
+// threadIdx.x passed through an empty asm statement. Per-lane offsets computed from it are then
+// recomputed where a long kernel uses them, instead of being computed once at the start and
+// held in registers (or spilled to scratch) across everything in between.
+__device__ __forceinline__ int freshThreadIdx() {
+  int t = static_cast<int>(threadIdx.x);
+  asm volatile("" : "+v"(t));
+  return t;
+}
+
 struct bf16 {
   uint16_t bits;
 };

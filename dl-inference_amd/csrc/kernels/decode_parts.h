@@ -1,0 +1,402 @@
+#pragma once
+
+// Stage building blocks of a Qwen2-style decoder layer in bf16, shared by the one-stage kernels
+// (decode.hip) and the persistent decoder-stack kernel (stack.hip), so that both compute every
+// tile with the same instructions in the same order and give bit-identical results:
+//
+//   normalizeFragments  RMSNorm of x fragments held in registers (rms_norm/kernel.py:6-14)
+//   tileLoop            grid-strided weight tiles against one x kept in registers
+//   QkvEpilogue         bias, interleaved RoPE (rotary/kernel.py:6-35), q out, k/v into the
+//                       paged KV cache at each row's position
+//   gateUpEpilogue      bf16(bf16(silu(gate)) * up) of one 16-output block
+//   ResidualTile        out = residual + bf16(y + b) of one 16-row tile
+//   splitKArrive        split-K partial tile store + last-arriver merge into out
+//
+// Every node of the unfused graph rounds its output to bf16; these helpers keep those rounding
+// points. Mem (skinny.h) selects plain or agent-scope accesses for data another workgroup of
+// the same launch produces or consumes.
+#include "common.h"
+#include "skinny.h"
+
+namespace dk {
+
+// RMSNorm-prologue GEMMs (qkv, gate_up): 8 waves, two per SIMD, so one wave's normalize VALU
+// runs while the other is held issuing its weight loads; 8 waves x 2 steps x 64 columns covers
+// hidden <= 1024.
+constexpr int kNormWaves = 8;
+constexpr int kNormThreads = kNormWaves * kWave;
+constexpr int kNormUnroll = 2;
+// linear_residual (o_proj, down_proj): 8 waves split K inside a workgroup.
+constexpr int kResWaves = 8;
+constexpr int kResThreads = kResWaves * kWave;
+constexpr int kMaxSplits = 8;  // split-K partials summed by the last arriver
+
+__device__ __forceinline__ float roundBf16(float v) { return bf16ToFloat(floatToBf16(v)); }
+
+// Steps [begin, end) of split `split` out of `splits` over `steps` 64-column steps.
+__device__ __forceinline__ void splitRange(int steps, int split, int splits, int& begin, int& end) {
+  const int per = (steps + splits - 1) / splits;
+  begin = split * per;
+  end = begin + per < steps ? begin + per : steps;
+}
+
+struct KvCacheArgs {
+  uint16_t* k_pool;
+  uint16_t* v_pool;
+  const int32_t* block_table;
+  int64_t block_size;
+  int64_t max_blocks;
+};
+
+// RMSNorm of x fragments held in registers, every 64-column step of K being in `xb` (lanes of
+// wave w hold steps w, w + kW, ...): x[m, k] <- bf16(x[m, k] * rsqrt(mean_k x[m, k]^2 + eps)
+// * w[k]) (rms_norm/kernel.py:6-14). Row sums of squares are reduced over the 4 lanes of a row
+// and then over the waves through lds (kW * 16 * MB floats) in a fixed order.
+template <int NF, int MB, int kW, int kU>
+__device__ __forceinline__ void normalizeFragments(
+    typename SkinnyCore<NF, MB, kW, kU>::XBatch& xb, const uint16_t* norm_w, int K, float eps,
+    float* lds, int wave, int steps, int r, int g) {
+  FP_EXACT;
+  using Core = SkinnyCore<NF, MB, kW, kU>;
+  U128 wv[kU][2];
+#pragma unroll
+  for (int u = 0; u < kU; ++u) {
+    const int s = wave + u * kW;
+    if (s >= steps) break;  // uniform: wave comes from readfirstlane
+    const int64_t k0 = static_cast<int64_t>(s) * 64 + g * 8;
+    wv[u][0] = load16(norm_w + k0);
+    wv[u][1] = load16(norm_w + k0 + 32);
+  }
+  float sq[MB];
+#pragma unroll
+  for (int b = 0; b < MB; ++b) {
+    sq[b] = 0.f;
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      if (wave + u * kW >= steps) break;
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float lo = bf16ToFloat(static_cast<uint16_t>(xb.x[u][b][h][e]));
+          const float hi = bf16ToFloat(static_cast<uint16_t>(xb.x[u][b][h][e] >> 16));
+          sq[b] += lo * lo + hi * hi;
+        }
+    }
+    sq[b] += __shfl_xor(sq[b], 16, kWave);
+    sq[b] += __shfl_xor(sq[b], 32, kWave);
+    if (g == 0) lds[wave * Core::kTileM + b * 16 + r] = sq[b];
+  }
+  __syncthreads();
+  float inv[MB];
+#pragma unroll
+  for (int b = 0; b < MB; ++b) {
+    float total = 0.f;
+#pragma unroll
+    for (int v = 0; v < kW; ++v) total += lds[v * Core::kTileM + b * 16 + r];
+    inv[b] = 1.0f / sqrtf(total / static_cast<float>(K) + eps);
+  }
+  __syncthreads();  // lds is reused by the tile reductions
+#pragma unroll
+  for (int u = 0; u < kU; ++u) {
+    if (wave + u * kW >= steps) break;
+#pragma unroll
+    for (int b = 0; b < MB; ++b)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t xw = xb.x[u][b][h][e], ww = wv[u][h][e];
+          const float lo = bf16ToFloat(static_cast<uint16_t>(xw)) * inv[b] *
+                           bf16ToFloat(static_cast<uint16_t>(ww));
+          const float hi = bf16ToFloat(static_cast<uint16_t>(xw >> 16)) * inv[b] *
+                           bf16ToFloat(static_cast<uint16_t>(ww >> 16));
+          xb.x[u][b][h][e] = packBf16x2(lo, hi);
+        }
+  }
+}
+
+// Weight tiles t = t_first, t_first + t_stride, ... (16 * NF rows each) against one x whose
+// fragments are loaded once (and RMS-normalized with norm_w when it is non-NULL) and stay in
+// registers; the next tile's weights stream in while the current one is multiplied. epi(t)
+// reads the reduced tile [16 NF][16 MB] from lds (row n, column m at lds[n * 16 MB + m]).
+// Requires K / 64 <= kU * kW.
+//
+// Load order. With an ungated x (kGated false) x is requested first: loads complete in issue
+// order, so the RMSNorm of x (VALU) overlaps the weight stream instead of waiting behind it.
+// With kGated the first two tiles' weights are requested, then gate() waits until another
+// workgroup has produced x, and x is loaded with Mem. The arithmetic is the same either way.
+template <int NF, int MB, int kW, int kU, class Mem = PlainMem, bool kGated = false,
+          class Gate = NoWait, typename Epi>
+__device__ __forceinline__ void tileLoop(const uint16_t* w, const XGlobal& xs, int64_t N, int K,
+                                         int M, float* lds, const uint16_t* norm_w, float eps,
+                                         int64_t t_first, int64_t t_stride, Gate&& gate,
+                                         Epi&& epi) {
+  using Core = SkinnyCore<NF, MB, kW, kU>;
+  const int lane = freshThreadIdx() % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int r = lane % 16, g = lane / 16;
+  const int steps = K / 64;
+  const int64_t tiles = (N + Core::kTileN - 1) / Core::kTileN;
+  const int64_t stride = t_stride;
+  int64_t t = t_first;
+  if (t >= tiles) return;
+  typename Core::WBatch bufA, bufB;
+  typename Core::XBatch xb;
+  if (!kGated) Core::template issueX<Mem>(xb, Core::xrows(xs, M, r, g), wave, steps);
+  Core::issueW(bufA, Core::rows(w, N, K, t * Core::kTileN, r, g), wave, steps);
+  if (t + stride < tiles)
+    Core::issueW(bufB, Core::rows(w, N, K, (t + stride) * Core::kTileN, r, g), wave, steps);
+  if (kGated) {
+    gate();
+    Core::template issueX<Mem>(xb, Core::xrows(xs, M, r, g), wave, steps);
+  }
+  if (norm_w != nullptr)
+    normalizeFragments<NF, MB, kW, kU>(xb, norm_w, K, eps, lds, wave, steps, r, g);
+  auto tile = [&](const typename Core::WBatch& wb, int64_t tt) {
+    f32x4 acc[NF][MB];
+    Core::zero(acc);
+    Core::compute(acc, wb, xb, wave, steps);
+    Core::reduce(acc, lds, r, g, wave);
+    epi(tt);
+    __syncthreads();  // lds is reused by the next tile
+  };
+  for (bool first = true; t < tiles; t += 2 * stride, first = false) {
+    if (!first && t + stride < tiles)
+      Core::issueW(bufB, Core::rows(w, N, K, (t + stride) * Core::kTileN, r, g), wave, steps);
+    tile(bufA, t);
+    if (t + stride >= tiles) break;
+    if (t + 2 * stride < tiles)
+      Core::issueW(bufA, Core::rows(w, N, K, (t + 2 * stride) * Core::kTileN, r, g), wave, steps);
+    tile(bufB, t + stride);
+  }
+}
+
+// ---- qkv: bias, RoPE, q out, k/v into the paged cache -------------------------------------
+
+struct QkvParams {
+  const uint16_t* bias;  // [(Hq + 2 Hkv) D] or NULL
+  const float* cos_t;    // [max_pos, D / 2]
+  const float* sin_t;
+  int64_t max_pos;
+  const void* positions;  // [M] int32/int64: the slot each row's new token is written to
+  int pos64;
+  uint16_t* q_out;  // [M, Hq, D]
+  KvCacheArgs kv;
+  int M, Hq, Hkv, D;
+};
+
+enum : int { kQkvAll = 0, kQkvQ = 1, kQkvCache = 2 };
+
+// Epilogue of one 16-row tile of the [q | k | v] projection (kNormThreads threads). Thread item
+// (pair, m) owns output columns n0 + 2 pair, n0 + 2 pair + 1 of row m: a RoPE pair
+// (rotary/kernel.py:6-35 rotates interleaved pairs). The operands that do not depend on the GEMM
+// (position, rotary coefficients, bias, cache block) are fetched by prefetch() before it.
+template <int MB, class Mem>
+struct QkvEpilogue {
+  static constexpr int kTileN = 16;
+  static constexpr int kTileM = 16 * MB;
+  static constexpr int kPairs = (kTileN / 2) * kTileM;
+  static constexpr int kItems = (kPairs + kNormThreads - 1) / kNormThreads;
+  int64_t pos[kItems];
+  float cs[kItems][2], bs[kItems][2];
+  int64_t blk[kItems];
+
+  __device__ __forceinline__ void prefetch(const QkvParams& p, int64_t n0) {
+    FP_EXACT;
+    const int64_t N = static_cast<int64_t>(p.Hq + 2 * p.Hkv) * p.D;
+    const int64_t q_rows = static_cast<int64_t>(p.Hq) * p.D;
+    const int64_t k_rows = static_cast<int64_t>(p.Hkv) * p.D;
+    const int half = p.D / 2;
+    const int64_t capacity = p.kv.max_blocks * p.kv.block_size;
+#pragma unroll
+    for (int it = 0; it < kItems; ++it) {
+      const int idx = threadIdx.x + it * kNormThreads;
+      const int m = idx % kTileM;
+      pos[it] = (idx < kPairs && m < p.M) ? loadIndex(p.positions, p.pos64, m) : -1;
+    }
+#pragma unroll
+    for (int it = 0; it < kItems; ++it) {
+      const int idx = threadIdx.x + it * kNormThreads;
+      const int pair = idx / kTileM, m = idx % kTileM;
+      const int64_t n = n0 + 2 * pair;
+      const bool live = pos[it] >= 0 && n < N;
+      const int64_t local =
+          n < q_rows ? n : (n < q_rows + k_rows ? n - q_rows : n - q_rows - k_rows);
+      const int d = static_cast<int>(local % p.D);
+      const bool rot = live && n < q_rows + k_rows && pos[it] < p.max_pos;
+      cs[it][0] = rot ? p.cos_t[pos[it] * half + d / 2] : 1.f;
+      cs[it][1] = rot ? p.sin_t[pos[it] * half + d / 2] : 0.f;
+      bs[it][0] = (live && p.bias != nullptr) ? bf16ToFloat(p.bias[n]) : 0.f;
+      bs[it][1] = (live && p.bias != nullptr) ? bf16ToFloat(p.bias[n + 1]) : 0.f;
+      blk[it] = (live && n >= q_rows && pos[it] < capacity)
+                    ? p.kv.block_table[m * p.kv.max_blocks + pos[it] / p.kv.block_size]
+                    : -1;
+    }
+  }
+
+  // kOutputs selects what is written: kQkvAll, kQkvQ (q only) or kQkvCache (k/v into the cache
+  // only); values are computed identically in every case.
+  template <int kOutputs = 0>
+  __device__ __forceinline__ void apply(const QkvParams& p, int64_t n0, const float* lds) const {
+    FP_EXACT;
+    const int64_t N = static_cast<int64_t>(p.Hq + 2 * p.Hkv) * p.D;
+    const int64_t q_rows = static_cast<int64_t>(p.Hq) * p.D;
+    const int64_t k_rows = static_cast<int64_t>(p.Hkv) * p.D;
+#pragma unroll
+    for (int it = 0; it < kItems; ++it) {
+      const int idx = threadIdx.x + it * kNormThreads;
+      const int pair = idx / kTileM;
+      const int m = idx % kTileM;
+      const int64_t n = n0 + 2 * pair;
+      if (pos[it] < 0 || n >= N) continue;
+      // linear output (bias added, rounded), then the rotation in fp32, rounded again
+      float v0 = roundBf16(lds[(2 * pair) * kTileM + m] + bs[it][0]);
+      float v1 = roundBf16(lds[(2 * pair + 1) * kTileM + m] + bs[it][1]);
+      const bool is_q = n < q_rows;
+      const bool is_k = !is_q && n < q_rows + k_rows;
+      if ((kOutputs == kQkvQ && !is_q) || (kOutputs == kQkvCache && is_q)) continue;
+      const int64_t local = is_q ? n : (is_k ? n - q_rows : n - q_rows - k_rows);
+      const int head = static_cast<int>(local / p.D);
+      const int d = static_cast<int>(local % p.D);
+      if (is_q || is_k) {
+        const float r0 = v0 * cs[it][0] - v1 * cs[it][1];
+        const float r1 = v0 * cs[it][1] + v1 * cs[it][0];
+        v0 = r0;
+        v1 = r1;
+      }
+      const uint32_t packed = packBf16x2(v0, v1);
+      if (is_q) {
+        uint16_t* dst = p.q_out + (static_cast<int64_t>(m) * p.Hq + head) * p.D + d;
+        Mem::storeU32(reinterpret_cast<uint32_t*>(dst), packed);
+        continue;
+      }
+      if (blk[it] < 0) continue;
+      const int64_t off = pos[it] % p.kv.block_size;
+      if (is_k) {
+        uint16_t* dst =
+            p.kv.k_pool + ((blk[it] * p.Hkv + head) * p.kv.block_size + off) * p.D + d;
+        Mem::storeU32(reinterpret_cast<uint32_t*>(dst), packed);
+      } else {
+        uint16_t* dst =
+            p.kv.v_pool + ((blk[it] * p.Hkv + head) * p.D + d) * p.kv.block_size + off;
+        Mem::storeU16(dst, static_cast<uint16_t>(packed));
+        Mem::storeU16(dst + p.kv.block_size, static_cast<uint16_t>(packed >> 16));
+      }
+    }
+  }
+};
+
+// ---- gate_up: SwiGLU of one 16-output block ----------------------------------------------
+
+// Tile t of the interleaved gate/up weight = gate rows [16t, 16t+16) then up rows [16t, 16t+16);
+// lds holds the reduced [32][16 MB] tile. out[m, f] = bf16(bf16(silu(bf16 gate)) * bf16 up).
+template <int MB, class Mem>
+__device__ __forceinline__ void gateUpEpilogue(const float* lds, uint16_t* out, int M, int64_t F,
+                                               int64_t t) {
+  FP_EXACT;
+  constexpr int kTileM = 16 * MB;
+  const int64_t f0 = t * 16;
+  for (int idx = threadIdx.x; idx < 16 * kTileM; idx += blockDim.x) {
+    const int j = idx % 16, m = idx / 16;
+    const int64_t f = f0 + j;
+    if (m >= M || f >= F) continue;
+    const float g = roundBf16(lds[j * kTileM + m]);
+    const float u = roundBf16(lds[(16 + j) * kTileM + m]);
+    const float s = roundBf16(g / (1.0f + expf(-g)));
+    Mem::storeU16(out + m * F + f, floatToBf16(s * u));
+  }
+}
+
+// ---- residual update of one 16-row tile ---------------------------------------------------
+
+// out[m, n] = bf16(residual[m, n] + bf16(y[n][m] + b[n])) for the tile at weight row n0, with
+// kThreadsT threads; load() fetches the residual (and bias) so they can be requested early.
+template <int MB, int kThreadsT, class Mem>
+struct ResidualTile {
+  static constexpr int kTileN = 16;
+  static constexpr int kTileM = 16 * MB;
+  static constexpr int kElems = kTileN * kTileM;
+  static constexpr int kItems = (kElems + kThreadsT - 1) / kThreadsT;
+  float res[kItems], bv[kItems];
+
+  __device__ __forceinline__ void load(const uint16_t* residual, const uint16_t* bias, int64_t n0,
+                                       int M, int64_t N) {
+#pragma unroll
+    for (int it = 0; it < kItems; ++it) {
+      const int idx = threadIdx.x + it * kThreadsT;
+      const int nl = idx / kTileM, m = idx % kTileM;
+      const int64_t n = n0 + nl;
+      const bool live = idx < kElems && m < M && n < N;
+      res[it] = live ? bf16ToFloat(Mem::loadU16(residual + m * N + n)) : 0.f;
+      bv[it] = live && bias != nullptr ? bf16ToFloat(bias[n]) : 0.f;
+    }
+  }
+
+  // y(idx) returns the fp32 GEMM result of item idx (row nl = idx / kTileM, column m).
+  template <class Y>
+  __device__ __forceinline__ void store(uint16_t* out, int64_t n0, int M, int64_t N, Y&& y) const {
+    FP_EXACT;
+#pragma unroll
+    for (int it = 0; it < kItems; ++it) {
+      const int idx = threadIdx.x + it * kThreadsT;
+      const int nl = idx / kTileM, m = idx % kTileM;
+      const int64_t n = n0 + nl;
+      if (idx >= kElems || m >= M || n >= N) continue;
+      Mem::storeU16(out + m * N + n, floatToBf16(res[it] + roundBf16(y(it, idx) + bv[it])));
+    }
+  }
+};
+
+// Split-K tail of one 16-row tile whose reduced partial is in lds: the partial is stored with
+// agent-scope stores to partials[split] (layout [splits][16 x 16 MB]) and the workgroup arrives
+// at *counter. The workgroup that brings the counter to `arrivals` is the last one: it reads
+// every split's partial with agent-scope loads (all issued before any is used), sums them in
+// split order, writes out = residual + bf16(sum + b) through rt, resets the counter to zero when
+// `reset` is set, and returns true. No cross-workgroup fence is needed: agent-scope stores and
+// loads bypass the non-coherent L2, and s_waitcnt vmcnt(0) orders the partial stores before the
+// counter update.
+template <int MB, int kThreadsT, class Mem>
+__device__ __forceinline__ bool splitKArrive(const float* lds, float* partials, int split,
+                                             int splits, unsigned* counter, unsigned arrivals,
+                                             bool reset, const ResidualTile<MB, kThreadsT, Mem>& rt,
+                                             uint16_t* out, int64_t n0, int M, int64_t N,
+                                             int* is_last) {
+  FP_EXACT;
+  constexpr int kElems = 16 * 16 * MB;
+  for (int idx = threadIdx.x; idx < kElems; idx += blockDim.x)
+    __hip_atomic_store(partials + static_cast<int64_t>(split) * kElems + idx, lds[idx],
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const unsigned old =
+        __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *is_last = old + 1 == arrivals;
+    if (*is_last && reset)
+      __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (!*is_last) return false;
+  constexpr int kItems = ResidualTile<MB, kThreadsT, Mem>::kItems;
+  float sum[kItems];
+#pragma unroll
+  for (int it = 0; it < kItems; ++it) {
+    const int idx = threadIdx.x + it * kThreadsT;
+    float part[kMaxSplits];
+#pragma unroll
+    for (int sp = 0; sp < kMaxSplits; ++sp)
+      part[sp] = (idx < kElems && sp < splits)
+                     ? __hip_atomic_load(partials + sp * kElems + idx, __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT)
+                     : 0.f;
+    float y = part[0];
+#pragma unroll
+    for (int sp = 1; sp < kMaxSplits; ++sp) y += part[sp];  // split order; absent = +0
+    sum[it] = y;
+  }
+  rt.store(out, n0, M, N, [&](int it, int) { return sum[it]; });
+  return true;
+}
+
+}  // namespace dk

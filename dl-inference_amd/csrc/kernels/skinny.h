@@ -36,6 +36,40 @@ __device__ __forceinline__ U128 load16(const void* p) {
 
 __device__ __forceinline__ U128 zero16() { return U128{0u, 0u, 0u, 0u}; }
 
+// Memory-access policies for activations.
+//   PlainMem         ordinary loads and stores: the data crosses a kernel boundary (which makes
+//                    writes visible to every XCD) before it is read.
+//   WriteThroughMem  for data that other workgroups of the same launch read: stores are
+//                    agent-scope (global_store ... sc1), written through to the coherent memory
+//                    side instead of staying in this XCD's L2 (the L2s of the 8 XCDs are not
+//                    coherent with each other); loads are plain. Plain loads are correct only
+//                    for lines that no CU of the reading XCD has read earlier in the launch (a
+//                    stale copy could hit), which the persistent decoder stack guarantees by
+//                    giving every layer its own activation buffers. Plain loads let the XCD's
+//                    L2 serve repeated reads of a line, where agent-scope loads would send every
+//                    workgroup's request to the same memory channel.
+struct PlainMem {
+  __device__ __forceinline__ static U128 load16(const void* p) {
+    return *reinterpret_cast<const U128*>(p);
+  }
+  __device__ __forceinline__ static uint16_t loadU16(const uint16_t* p) { return *p; }
+  __device__ __forceinline__ static void storeU16(uint16_t* p, uint16_t v) { *p = v; }
+  __device__ __forceinline__ static void storeU32(uint32_t* p, uint32_t v) { *p = v; }
+};
+
+struct WriteThroughMem {
+  __device__ __forceinline__ static U128 load16(const void* p) {
+    return *reinterpret_cast<const U128*>(p);
+  }
+  __device__ __forceinline__ static uint16_t loadU16(const uint16_t* p) { return *p; }
+  __device__ __forceinline__ static void storeU16(uint16_t* p, uint16_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __device__ __forceinline__ static void storeU32(uint32_t* p, uint32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+};
+
 // The B operand (the skinny activation x): [M, K] row-major with `stride` elements per row.
 struct XGlobal {
   const uint16_t* x;
@@ -108,6 +142,7 @@ struct SkinnyCore {
   }
 
   // x loads of the same batch.
+  template <class Mem = PlainMem>
   __device__ __forceinline__ static void issueX(XBatch& bt, const XRows& xr, int s0, int step_end) {
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
@@ -116,8 +151,8 @@ struct SkinnyCore {
       const int64_t k0 = static_cast<int64_t>(s) * 64;
 #pragma unroll
       for (int b = 0; b < MB; ++b) {
-        bt.x[u][b][0] = load16(xr.x[b] + k0);
-        bt.x[u][b][1] = load16(xr.x[b] + k0 + 32);
+        bt.x[u][b][0] = Mem::load16(xr.x[b] + k0);
+        bt.x[u][b][1] = Mem::load16(xr.x[b] + k0 + 32);
       }
     }
   }
@@ -149,13 +184,10 @@ struct SkinnyCore {
   // Accumulates steps [step_begin, step_end) of the tile at weight row n0 and leaves the reduced
   // fp32 tile [kTileN][kTileM] in lds[0 .. tile). Batches are double-buffered: the next batch's
   // loads are in flight while the current one is multiplied.
-  // Accumulates steps [step_begin, step_end) of the tile at weight row n0 and leaves the reduced
-  // fp32 tile [kTileN][kTileM] in lds[0 .. tile). Batches are double-buffered: the next batch's
-  // loads are in flight while the current one is multiplied.
   __device__ __forceinline__ static void run(const uint16_t* __restrict__ w, const XGlobal& xs,
                                              int64_t N, int64_t K, int M, int64_t n0,
                                              int step_begin, int step_end, float* lds) {
-    const int lane = threadIdx.x % kWave;
+    const int lane = freshThreadIdx() % kWave;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int r = lane % 16, g = lane / 16;
     f32x4 acc[NF][MB];
@@ -182,6 +214,50 @@ struct SkinnyCore {
         issueX(x0, xr, s2, step_end);
       }
       compute(acc, w1, x1, s1, step_end);
+    }
+    reduce(acc, lds, r, g, wave);
+  }
+
+  // run() for an x that another workgroup of the same launch produces: the first two weight
+  // batches are requested, then gate() (called by every thread) waits until x is ready, and only
+  // then are the x batches loaded (with Mem). The batches are accumulated in the order run()
+  // uses, so both give bit-identical tiles.
+  template <class Mem, class Gate>
+  __device__ __forceinline__ static void runGated(const uint16_t* __restrict__ w, const XGlobal& xs,
+                                                  int64_t N, int64_t K, int M, int64_t n0,
+                                                  int step_begin, int step_end, float* lds,
+                                                  Gate&& gate) {
+    const int lane = freshThreadIdx() % kWave;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int r = lane % 16, g = lane / 16;
+    f32x4 acc[NF][MB];
+    zero(acc);
+    const Rows rw = rows(w, N, K, n0, r, g);
+    const XRows xr = xrows(xs, M, r, g);
+    constexpr int kStride = kUnroll * kWaves;
+    WBatch w0, w1;
+    XBatch x0, x1;
+    int s0 = step_begin + wave;
+    issueW(w0, rw, s0, step_end);
+    if (s0 + kStride < step_end) issueW(w1, rw, s0 + kStride, step_end);
+    gate();
+    issueX<Mem>(x0, xr, s0, step_end);
+    if (s0 + kStride < step_end) issueX<Mem>(x1, xr, s0 + kStride, step_end);
+    for (; s0 < step_end; s0 += 2 * kStride) {
+      const int s1 = s0 + kStride;
+      compute(acc, w0, x0, s0, step_end);
+      if (s1 >= step_end) break;
+      const int s2 = s1 + kStride;
+      if (s2 < step_end) {
+        issueW(w0, rw, s2, step_end);
+        issueX<Mem>(x0, xr, s2, step_end);
+      }
+      compute(acc, w1, x1, s1, step_end);
+      const int s3 = s2 + kStride;
+      if (s3 < step_end) {
+        issueW(w1, rw, s3, step_end);
+        issueX<Mem>(x1, xr, s3, step_end);
+      }
     }
     reduce(acc, lds, r, g, wave);
   }

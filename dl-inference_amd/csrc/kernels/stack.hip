@@ -1,0 +1,319 @@
+// Persistent decoder stack for batched decode on gfx950: every decoder layer of a Qwen2-style
+// model in ONE launch. The reference runs a decoder layer as 19 graph nodes
+// (python/dli_export/export.py:272-446); the five-launch fused path (decode.hip, attention.hip)
+// runs it as five kernels. Here one 8-wave workgroup per CU walks the layers and, per layer,
+// five stages:
+//
+//   S1 qkv     RMSNorm(h) W_qkv^T + b, RoPE, k/v into the paged cache, q     (16-row tiles)
+//   S2 attn    decode attention units (pair = (sequence, kv head), split)    (decode_attention.h)
+//   S3 o       h_mid = h + attn W_o^T                                         (16-row tiles)
+//   S4 gate_up act = bf16(silu(gate)) * up of RMSNorm(h_mid)                  (32-row tiles)
+//   S5 down    h = h_mid + act W_down^T, split-K, last arriver merges        (16-row tiles)
+//
+// Every tile is computed with the same code and order as the one-stage kernels, so the stack
+// and the five-launch path give bit-identical results.
+//
+// Synchronisation. A stage's consumers wait on an arrival counter instead of a kernel boundary:
+// each producing workgroup stores its outputs with agent-scope stores (written through to the
+// coherent memory side; the L2 caches of the 8 XCDs are not coherent with each other), waits
+// for them (s_waitcnt vmcnt(0)) and adds to its shard of the stage counter; a consumer polls the
+// shards until they sum to (layer + 1) x the producers of that stage. Consumers then read with
+// plain loads, so each XCD's L2 serves the repeated reads of an activation row. That is correct
+// because every layer has its own activation buffers (slabs): no line a consumer reads can have
+// been read, and cached stale, earlier in the launch. Before waiting, a workgroup requests the
+// weights of its next tile (attention units: their first cache blocks), which do not depend on
+// the previous stage, so that stream overlaps the wait.
+//
+// Work placement. q|k|v tiles go two per workgroup to the last workgroups of the grid, which
+// have no down_proj unit and reach the stage first; attention units go to the other
+// workgroups; o_proj tiles to the first ones; gate_up tile t to workgroup (t + o_tiles) % G, so
+// workgroups with a second gate_up tile are not busy with o_proj. The q|k|v stage publishes q
+// first and then writes k/v into the cache, signalled on a second counter: attention needs the
+// new k/v only for the block holding the newest token, which its waves reach last.
+//
+// Progress. The grid is at most one workgroup per CU and a workgroup fits a CU on its own, so
+// every workgroup is resident at once, and a stage only waits on earlier stages, which every
+// workgroup passes in the same order. Every wait is still bounded: after kSpinLimit polls the
+// workgroup raises the abort word, every later wait returns at once, and the launch ends with
+// the abort word set for the host to read (the outputs are then invalid).
+//
+// The counters only grow during a launch; the last workgroup to finish resets them all to zero
+// (except the abort word), so the next launch starts from zero without a memset.
+#include "decode_attention.h"
+#include "decode_parts.h"
+#include "stack_args.h"
+
+using namespace dk;
+using dli_stack::Args;
+using dli_stack::Layer;
+
+namespace {
+
+constexpr int kStackThreads = 512;
+constexpr int kSpinLimit = 1 << 20;
+constexpr int kAbortPollEvery = 64;
+
+__device__ __forceinline__ unsigned loadAgent(const unsigned* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Adds n to this workgroup's shard of a stage counter once every thread's stores have
+// completed.
+__device__ __forceinline__ void arrive(unsigned* stage, unsigned n) {
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (threadIdx.x == 0)
+    __hip_atomic_fetch_add(stage + (blockIdx.x % dli_stack::kShards) * dli_stack::kLineWords, n,
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Polls a stage counter from one wave (lane i < kShards loads shard i) until the shards sum to
+// at least target, the abort word is set, or kSpinLimit polls have passed (which sets the abort
+// word). The loop condition is uniform over the wave.
+__device__ __forceinline__ void pollStage(const unsigned* stage, unsigned target,
+                                          unsigned* abort_word) {
+  const int lane = freshThreadIdx() % kWave;
+  for (int spins = 0;; ++spins) {
+    unsigned v = lane < dli_stack::kShards ? loadAgent(stage + lane * dli_stack::kLineWords) : 0u;
+    v += __shfl_xor(v, 1, kWave);
+    v += __shfl_xor(v, 2, kWave);
+    v += __shfl_xor(v, 4, kWave);
+    if (__builtin_amdgcn_readfirstlane(v) >= target) break;
+    if (spins % kAbortPollEvery == 0 &&
+        __builtin_amdgcn_readfirstlane(loadAgent(abort_word)) != 0u)
+      break;
+    if (spins >= kSpinLimit) {
+      __hip_atomic_store(abort_word, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+
+// Returns in every thread of the workgroup once the stage counter reaches target (wave 0 polls).
+__device__ __forceinline__ void waitAtLeast(const unsigned* stage, unsigned target,
+                                            unsigned* abort_word) {
+  if (threadIdx.x < kWave) pollStage(stage, target, abort_word);
+  __syncthreads();
+}
+
+// Returns v unchanged through an empty asm statement, so the compiler cannot hoist what is
+// computed from it out of the layer loop: per-stage addresses are then recomputed in each
+// stage instead of being held in registers (or spilled) across all five stages.
+template <typename T>
+__device__ __forceinline__ T fresh(T v) {
+  asm volatile("" : "+s"(v));
+  return v;
+}
+
+template <int MB>
+struct StackLds {
+  using GuCore = SkinnyCore<2, MB, kNormWaves, kNormUnroll>;
+  float gemm[GuCore::kLdsFloats];  // the largest stage tile reduction (gate_up)
+  DecodeAttnLds attn;
+  int is_last;
+};
+
+template <int MB>
+__device__ void decoderStack(const Args& a) {
+  using OCore = SkinnyCore<1, MB, kResWaves, (MB >= 4 ? 2 : 4)>;
+  using DownCore = SkinnyCore<1, MB, kResWaves, 2>;
+  using Mem = WriteThroughMem;
+  constexpr int kTileElems = 16 * 16 * MB;
+  static_assert(SkinnyCore<1, MB, kNormWaves, kNormUnroll>::kLdsFloats <=
+                    StackLds<MB>::GuCore::kLdsFloats,
+                "lds");
+  static_assert(OCore::kLdsFloats <= StackLds<MB>::GuCore::kLdsFloats, "lds");
+  __shared__ StackLds<MB> smem;
+  float* lds = smem.gemm;
+
+  const int G = gridDim.x, bid = blockIdx.x;
+  const int qkv_tiles = (a.Hq + 2 * a.Hkv) * a.D / 16, o_tiles = a.H / 16;
+  const int gu_tiles = a.F / 16, down_tiles = a.H / 16;
+  const int pairs = a.M * a.Hkv, splits = a.attn_splits, down_splits = a.down_splits;
+  const int attn_units = pairs * splits, down_units = down_tiles * down_splits;
+  const int qkv_wgs = (qkv_tiles + 1) / 2 < G ? (qkv_tiles + 1) / 2 : G;  // S1 workgroups
+
+  for (int l = 0; l < a.layers; ++l) {
+    const Layer& L = a.layer[l];
+    const unsigned gen = static_cast<unsigned>(l + 1);
+    // This layer's activation slab and the residual stream entering it. Every pointer and size
+    // below passes through fresh() so that no address is computed once for all layers.
+    uint16_t* const slab = fresh(a.slabs) + l * fresh(a.slab_elems);
+    uint16_t* const q = slab;
+    uint16_t* const attn = slab + a.off_attn;
+    uint16_t* const h_mid = slab + a.off_h_mid;
+    uint16_t* const act = slab + a.off_act;
+    uint16_t* const h = l == a.layers - 1 ? fresh(a.h_out) : slab + a.off_h;
+    const uint16_t* const h_prev =
+        l == 0 ? fresh(a.x_in) : static_cast<const uint16_t*>(slab - a.slab_elems + a.off_h);
+    unsigned* const sync = fresh(a.sync);
+    unsigned* const abort_word = sync + dli_stack::kAbortWord;
+
+    // S1: q|k|v tiles of the residual stream the previous layer finished, two per workgroup on
+    // the last workgroups of the grid (the ones without down_proj work, which reach this stage
+    // first), so that few workgroups start their attention unit late.
+    if (bid >= G - qkv_wgs) {
+      const int H = fresh(a.H), M = fresh(a.M);
+      const QkvParams qp{L.b_qkv,
+                         fresh(a.cos_t),
+                         fresh(a.sin_t),
+                         a.max_pos,
+                         fresh(a.positions),
+                         a.pos64,
+                         q,
+                         KvCacheArgs{L.k_pool, L.v_pool, L.block_table, a.block_size,
+                                     a.max_blocks},
+                         M,
+                         a.Hq,
+                         a.Hkv,
+                         a.D};
+      const int n_qkv = fresh((a.Hq + 2 * a.Hkv) * a.D);
+      const int t0 = bid - (G - qkv_wgs);
+      QkvEpilogue<MB, Mem> epi0, epi1;  // operands of this workgroup's (at most) two tiles
+      epi0.prefetch(qp, static_cast<int64_t>(t0) * 16);
+      if (t0 + qkv_wgs < qkv_tiles) epi1.prefetch(qp, static_cast<int64_t>(t0 + qkv_wgs) * 16);
+      int done = 0;
+      auto finish = [&](const QkvEpilogue<MB, Mem>& e, int64_t t) {
+        // q first: attention needs it at once. The cache writes (scattered, slower to complete)
+        // follow and are signalled separately; attention needs them only for the block
+        // holding the newest token, which its waves reach last.
+        e.template apply<kQkvQ>(qp, t * 16, lds);
+        arrive(sync + dli_stack::stageWord(dli_stack::kQkvDone), 1);
+        e.template apply<kQkvCache>(qp, t * 16, lds);
+        ++done;
+      };
+      tileLoop<1, MB, kNormWaves, kNormUnroll, Mem, true>(
+          L.w_qkv, XGlobal{h_prev, H}, n_qkv, H, M, lds, L.input_norm, a.eps, t0, qkv_wgs,
+          [&] {
+            if (l > 0)
+              waitAtLeast(sync + dli_stack::stageWord(dli_stack::kDownDone), l * down_tiles,
+                          abort_word);
+          },
+          [&](int64_t t) {
+            if (t == t0)
+              finish(epi0, t);
+            else
+              finish(epi1, t);
+          });
+      arrive(sync + dli_stack::stageWord(dli_stack::kKvDone), static_cast<unsigned>(done));
+    }
+
+    // S2: attention units.
+    if (bid < attn_units) {
+      const DecodeAttnArgs da{q,
+                              L.k_pool,
+                              L.v_pool,
+                              L.block_table,
+                              fresh(a.positions),
+                              a.pos64,
+                              0,
+                              fresh(a.attn_ml),
+                              fresh(a.attn_o),
+                              sync + dli_stack::kPairCountersAt,
+                              attn,
+                              a.Hq,
+                              a.Hkv,
+                              a.max_blocks,
+                              splits,
+                              a.scale_log2};
+      for (int u = bid; u < attn_units; u += G) {
+        const bool merged = decodeAttentionUnit<Mem, true>(
+            da, u % splits, u / splits, gen * splits, false, smem.attn,
+            [&] {
+              waitAtLeast(sync + dli_stack::stageWord(dli_stack::kQkvDone), gen * qkv_tiles,
+                          abort_word);
+            },
+            [&] {
+              pollStage(sync + dli_stack::stageWord(dli_stack::kKvDone), gen * qkv_tiles,
+                        abort_word);
+            });
+        if (merged) arrive(sync + dli_stack::stageWord(dli_stack::kAttnDone), 1);
+      }
+    }
+
+    // S3: o_proj + attention residual.
+    for (int t = bid; t < o_tiles; t += G) {
+      const int H = fresh(a.H), M = fresh(a.M), qd = fresh(a.Hq * a.D);
+      const int64_t n0 = static_cast<int64_t>(t) * 16;
+      ResidualTile<MB, kResThreads, Mem> rt;
+      OCore::template runGated<Mem>(L.w_o, XGlobal{attn, qd}, H, qd, M, n0, 0, qd / 64, lds, [&] {
+        waitAtLeast(sync + dli_stack::stageWord(dli_stack::kAttnDone), gen * pairs, abort_word);
+        rt.load(h_prev, nullptr, n0, M, H);
+      });
+      rt.store(h_mid, n0, M, H, [&](int, int idx) { return lds[idx]; });
+      arrive(sync + dli_stack::stageWord(dli_stack::kODone), 1);
+    }
+
+    // S4: gate_up + SwiGLU, RMSNorm of h_mid in registers. Tile t runs on workgroup
+    // (t + o_tiles) % G: when there are more tiles than workgroups, the ones with a second tile
+    // are not the o_proj workgroups, so they request both tiles' weights during o_proj.
+    const int gu_first = (bid + G - o_tiles % G) % G;
+    if (gu_first < gu_tiles) {
+      const int H = fresh(a.H), M = fresh(a.M), F = fresh(a.F);
+      tileLoop<2, MB, kNormWaves, kNormUnroll, Mem, true>(
+          L.w_gate_up, XGlobal{h_mid, H}, 2 * static_cast<int64_t>(F), H, M, lds, L.post_norm,
+          a.eps, gu_first, G,
+          [&] {
+            waitAtLeast(sync + dli_stack::stageWord(dli_stack::kODone), gen * o_tiles,
+                        abort_word);
+          },
+          [&](int64_t t) { gateUpEpilogue<MB, Mem>(lds, act, M, F, t); });
+      arrive(sync + dli_stack::stageWord(dli_stack::kGateUpDone),
+             static_cast<unsigned>((gu_tiles - 1 - gu_first) / G + 1));
+    }
+
+    // S5: down_proj split-K + MLP residual; the last split of a tile writes h.
+    for (int u = bid; u < down_units; u += G) {
+      const int H = fresh(a.H), M = fresh(a.M), F = fresh(a.F);
+      const int tile = u % down_tiles, split = u / down_tiles;
+      const int64_t n0 = static_cast<int64_t>(tile) * 16;
+      int sb, se;
+      splitRange(F / 64, split, down_splits, sb, se);
+      ResidualTile<MB, kResThreads, Mem> rt;
+      DownCore::template runGated<Mem>(L.w_down, XGlobal{act, F}, H, F, M, n0, sb, se, lds, [&] {
+        waitAtLeast(sync + dli_stack::stageWord(dli_stack::kGateUpDone), gen * gu_tiles,
+                    abort_word);
+        rt.load(h_mid, nullptr, n0, M, H);
+      });
+      unsigned* const tile_counters = sync + dli_stack::kPairCountersAt + pairs;
+      if (splitKArrive<MB, kResThreads, Mem>(
+              lds, fresh(a.down_part) + static_cast<int64_t>(tile) * down_splits * kTileElems,
+              split, down_splits, tile_counters + tile, gen * down_splits, false, rt, h, n0, M, H,
+              &smem.is_last))
+        arrive(sync + dli_stack::stageWord(dli_stack::kDownDone), 1);
+    }
+  }
+
+  // Leave: the last workgroup out resets every counter but the abort word.
+  unsigned* const sync = a.sync;
+  unsigned* const pair_counters = sync + dli_stack::kPairCountersAt;
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const unsigned old = __hip_atomic_fetch_add(sync + dli_stack::kExitWord, 1u, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT);
+    smem.is_last = old + 1 == static_cast<unsigned>(G);
+  }
+  __syncthreads();
+  if (!smem.is_last) return;
+  for (int i = threadIdx.x; i < dli_stack::kStages * dli_stack::kShards; i += blockDim.x)
+    __hip_atomic_store(sync + i * dli_stack::kLineWords, 0u, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+  if (threadIdx.x == 0)
+    __hip_atomic_store(sync + dli_stack::kExitWord, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  for (int i = threadIdx.x; i < pairs + down_tiles; i += blockDim.x)
+    __hip_atomic_store(pair_counters + i, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+}  // namespace
+
+#define DK_STACK_KERNEL(MB)                                                                \
+  extern "C" __global__ void __launch_bounds__(kStackThreads, 1)                           \
+      decoder_stack_m##MB(const Args a) {                                                  \
+    decoderStack<MB>(a);                                                                   \
+  }
+
+DK_STACK_KERNEL(1)
+DK_STACK_KERNEL(2)
+DK_STACK_KERNEL(4)

@@ -1,0 +1,73 @@
+#pragma once
+
+// Kernel argument block of the persistent decoder-stack kernel (stack.hip), shared by the HIP
+// kernel and the host launcher (csrc/hip/stack_ops.cc) so both see one layout. Plain C types
+// only: it is passed by value as the kernel's single argument.
+#include <stdint.h>
+
+namespace dli_stack {
+
+constexpr int kMaxLayers = 32;  // layers per launch (more are run as several launches)
+
+// Device pointers of one decoder layer (bf16 unless noted).
+struct Layer {
+  const uint16_t* input_norm;  // [H]
+  const uint16_t* w_qkv;       // [(Hq + 2 Hkv) D, H]  rows q | k | v
+  const uint16_t* b_qkv;       // [(Hq + 2 Hkv) D] or NULL
+  const uint16_t* w_o;         // [H, Hq D]
+  const uint16_t* post_norm;   // [H]
+  const uint16_t* w_gate_up;   // [2 F, H]  16-row blocks: gate 16i.., then up 16i..
+  const uint16_t* w_down;      // [H, F]
+  uint16_t* k_pool;            // [blocks, Hkv, block_size, D]
+  uint16_t* v_pool;            // [blocks, Hkv, D, block_size]
+  const int32_t* block_table;  // int32 [M, max_blocks]
+};
+
+struct Args {
+  Layer layer[kMaxLayers];
+  const uint16_t* x_in;  // [M, H] residual stream entering the first layer
+  uint16_t* h_out;       // [M, H] residual stream after the last layer
+  // Activations of layer l live in their own slab at slabs + l * slab_elems (never reused within
+  // a launch): q [M, Hq, D] at offset 0, attn [M, Hq, D] at off_attn, h_mid [M, H] (residual
+  // stream after attention) at off_h_mid, act [M, F] at off_act, h [M, H] (after the layer) at
+  // off_h; the last layer writes h_out instead.
+  uint16_t* slabs;
+  int64_t slab_elems, off_attn, off_h_mid, off_act, off_h;
+  const float* cos_t;  // [max_pos, D / 2]
+  const float* sin_t;
+  const void* positions;  // [M] int32/int64: slot of each row's new token
+  float* attn_ml;         // attention unit partials (m, l)
+  float* attn_o;          // attention unit partials O
+  float* down_part;       // down_proj split-K partial tiles
+  unsigned* sync;         // arrival counters (zero before the first launch; left at zero)
+  int64_t max_pos, block_size, max_blocks;
+  int layers, M, H, Hq, Hkv, D, F, pos64, attn_splits, down_splits;
+  float eps, scale_log2;
+};
+
+// Layout of `sync` in 32-bit words. A stage counter is split into kShards sub-counters, each on
+// its own 256-byte line: a workgroup adds to sub-counter blockIdx.x % kShards (about one per
+// XCD), so arrivals do not all serialize on one address, and a waiting workgroup sums the
+// shards. Then the exit counter and the abort word (own lines), then one arrival counter per
+// attention pair (b, kv head) and per down_proj output tile.
+enum : int {
+  kQkvDone = 0,  // q of every q|k|v tile written
+  kKvDone,       // k/v of every q|k|v tile written into the cache
+  kAttnDone,     // attention output of every pair written
+  kODone,        // every o_proj tile (h_mid) written
+  kGateUpDone,   // every gate_up tile (act) written
+  kDownDone,     // every down_proj tile (h) written
+  kStages
+};
+constexpr int kShards = 8;
+constexpr int kLineWords = 64;
+constexpr int stageWord(int stage) { return stage * kShards * kLineWords; }
+constexpr int kExitWord = kStages * kShards * kLineWords;
+constexpr int kAbortWord = kExitWord + kLineWords;
+constexpr int kPairCountersAt = kAbortWord + kLineWords;
+
+inline int64_t syncWords(int64_t pairs, int64_t down_tiles) {
+  return kPairCountersAt + pairs + down_tiles;
+}
+
+}  // namespace dli_stack

@@ -10,6 +10,7 @@
 //                          (post_attention_layernorm, the next input_layernorm, model.norm)
 //   gate_up_silu           (post_attention_layernorm,) gate_proj, up_proj, act_fn, mul
 //   lm_head_argmax         lm_head, greedy argmax
+//   decoder_stack          every decoder layer above in one persistent launch
 //   argmax                 greedy argmax over the last dim (unfused graphs)
 #include <cmath>
 
@@ -227,6 +228,96 @@ class LmHeadArgmaxOp final : public Operator {
   }
 };
 
+// All decoder layers in one launch (dli_hip_decoder_stack). inputs: hidden [B, H], positions
+// [B], cos, sin, then per layer: input_layernorm.weight, qkv_proj.weight, qkv_proj.bias,
+// o_proj.weight, post_attention_layernorm.weight, gate_up_proj.weight, down_proj.weight.
+// Layer i appends to and attends over cache entry kv_cache_prefix + i. Computes what the
+// five-launch layer (qkv_rope_append, paged_attention, linear_residual, gate_up_silu,
+// linear_residual with down_splits) computes, bit for bit.
+class DecoderStackOp final : public Operator {
+ public:
+  std::string type() const override { return "decoder_stack"; }
+  void compute(const std::vector<const Tensor*>& in, const std::vector<Tensor*>& out,
+               const Attributes& attrs, ExecutionContext& ctx) const override {
+    constexpr std::size_t kPerLayer = 7, kHead = 4;
+    const auto layers = attrs.require<std::int64_t>("layers");
+    if (layers < 1 || in.size() != kHead + kPerLayer * static_cast<std::size_t>(layers))
+      throw std::invalid_argument("decoder_stack expects 4 + 7 * layers inputs");
+    requireArity(in, out, in.size(), in.size(), 1, type());
+    requireCudaInputs(in, type());
+    const Tensor &x = *in[0], &pos = *in[1], &cos = *in[2], &sin = *in[3];
+    requireBf16(x, type(), "hidden");
+    requireIndex(pos, type(), "positions");
+    requireFloat(cos, type());
+    requireFloat(sin, type());
+    const auto hq = attrs.require<std::int64_t>("q_heads");
+    const auto hkv = attrs.require<std::int64_t>("kv_heads");
+    const auto d = attrs.require<std::int64_t>("head_dim");
+    const auto eps = static_cast<float>(attrDouble(attrs, "eps", 1e-6));
+    const auto down_splits = attrs.value_or<std::int64_t>("down_splits", 4);
+    const std::string prefix = attrs.value_or<std::string>("kv_cache_prefix", "layer_");
+    const std::int64_t hidden = x.shape().back(), m = rowsOf(x);
+    const std::int64_t n_qkv = (hq + 2 * hkv) * d;
+    if (static_cast<std::int64_t>(pos.numel()) != m)
+      throw std::invalid_argument("decoder_stack positions must have one entry per row");
+    if (cos.rank() != 2 || cos.dim(1) != d / 2 || cos.shape() != sin.shape())
+      throw std::invalid_argument("decoder_stack cos/sin must be [max_pos, head_dim/2]");
+    if (ctx.kv_cache == nullptr) throw std::invalid_argument("decoder_stack missing KV cache");
+    std::vector<DliDecoderLayer> table(static_cast<std::size_t>(layers));
+    std::int64_t ffn = 0, block_size = 0, max_blocks = 0;
+    for (std::int64_t i = 0; i < layers; ++i) {
+      const Tensor* const* t = &in[kHead + kPerLayer * static_cast<std::size_t>(i)];
+      for (std::size_t j = 0; j < kPerLayer; ++j) requireBf16(*t[j], type(), "weights");
+      const Tensor &ln1 = *t[0], &wqkv = *t[1], &bqkv = *t[2], &wo = *t[3], &ln2 = *t[4],
+                   &wgu = *t[5], &wd = *t[6];
+      if (static_cast<std::int64_t>(ln1.numel()) != hidden ||
+          static_cast<std::int64_t>(ln2.numel()) != hidden || wqkv.rank() != 2 ||
+          wqkv.dim(0) != n_qkv || wqkv.dim(1) != hidden ||
+          static_cast<std::int64_t>(bqkv.numel()) != n_qkv || wo.rank() != 2 ||
+          wo.dim(0) != hidden || wo.dim(1) != hq * d || wgu.rank() != 2 || wgu.dim(1) != hidden ||
+          wd.rank() != 2 || wd.dim(0) != hidden || 2 * wd.dim(1) != wgu.dim(0))
+        throw std::invalid_argument("decoder_stack layer " + std::to_string(i) +
+                                    " weight shapes do not match the attributes");
+      ffn = wd.dim(1);
+      KVCacheEntry& e = ctx.kv_cache->reserve(prefix + std::to_string(i), DType::BFloat16, m, hkv,
+                                              d, x.deviceId());
+      if (i == 0) {
+        block_size = e.block_size;
+        max_blocks = e.max_blocks;
+      } else if (e.block_size != block_size || e.max_blocks != max_blocks) {
+        throw std::invalid_argument("decoder_stack cache entries differ in geometry");
+      }
+      table[static_cast<std::size_t>(i)] =
+          DliDecoderLayer{ptr(ln1), ptr(wqkv), ptr(bqkv), ptr(wo), ptr(ln2), ptr(wgu), ptr(wd),
+                          ptr(e.key), ptr(e.value),
+                          static_cast<const std::int32_t*>(ptr(e.block_table))};
+    }
+    *out[0] = Tensor::cuda(DType::BFloat16, x.shape(), x.deviceId());
+    const std::size_t ws_bytes = dli_hip_decoder_stack_workspace(
+        static_cast<int>(layers), m, hidden, hq, hkv, d, ffn, max_blocks,
+        static_cast<int>(down_splits));
+    check(dli_hip_decoder_stack(table.data(), static_cast<int>(layers), ptr(x), ptr(*out[0]),
+                                ptr(pos), hipDtype(pos.dtype()),
+                                static_cast<const float*>(ptr(cos)),
+                                static_cast<const float*>(ptr(sin)), cos.dim(0), block_size,
+                                max_blocks, m, hidden, hq, hkv, d, ffn, eps,
+                                static_cast<int>(down_splits),
+                                workspace_.get(ws_bytes, x.deviceId()), ws_bytes, ctx.stream),
+          type());
+    // check_status (tests): wait for the launch and fail if a wait in it gave up
+    if (attrs.value_or<std::int64_t>("check_status", 0) != 0) {
+      int aborted = 0;
+      check(dli_hip_decoder_stack_status(workspace_.get(ws_bytes, x.deviceId()), &aborted,
+                                         ctx.stream),
+            type());
+      if (aborted) throw std::runtime_error("decoder_stack: a workgroup gave up waiting");
+    }
+  }
+
+ private:
+  mutable PersistentWorkspace workspace_;
+};
+
 class ArgmaxOp final : public Operator {
  public:
   std::string type() const override { return "argmax"; }
@@ -255,6 +346,7 @@ void registerFusedOps(OperatorRegistry* registry) {
   add<LinearResidualNormOp>(registry);
   add<GateUpSiluOp>(registry);
   add<LmHeadArgmaxOp>(registry);
+  add<DecoderStackOp>(registry);
   add<ArgmaxOp>(registry);
 }
 

@@ -87,6 +87,12 @@ _SIGNATURES = {
     "dli_hip_lm_head_argmax_workspace": [_i64, _i64],
     "dli_hip_lm_head_argmax": [_c_void_p] * 3 + [_int, _c_void_p] + [_i64] * 3
     + [_c_void_p, _size, _c_void_p],
+    "dli_hip_decoder_stack_workspace": [_int] + [_i64] * 7 + [_int],
+    "dli_hip_decoder_stack": [_c_void_p, _int, _c_void_p, _c_void_p, _c_void_p, _int, _c_void_p,
+                              _c_void_p] + [_i64] * 9 + [_float, _int, _c_void_p, _size,
+                                                         _c_void_p],
+    "dli_hip_decoder_stack_status": [_c_void_p, ctypes.POINTER(_int), _c_void_p],
+    "dli_hip_set_decode_attention_splits": [_int],
 }
 _RESTYPES = {
     "dli_hip_load_error": ctypes.c_char_p,
@@ -95,7 +101,15 @@ _RESTYPES = {
     "dli_hip_paged_attention_workspace": _size,
     "dli_hip_splitk_workspace": _size,
     "dli_hip_lm_head_argmax_workspace": _size,
+    "dli_hip_decoder_stack_workspace": _size,
 }
+
+
+class DecoderLayer(ctypes.Structure):
+    """DliDecoderLayer: device pointers of one decoder layer (include/dli_hip.h)."""
+    _fields_ = [(name, _c_void_p) for name in (
+        "input_norm", "w_qkv", "b_qkv", "w_o", "post_norm", "w_gate_up", "w_down", "key_pool",
+        "value_pool", "block_table")]
 
 
 class HipError(RuntimeError):

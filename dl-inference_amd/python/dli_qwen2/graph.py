@@ -9,6 +9,9 @@ fused graph (fused=True): 5 launches per layer on the fused operators of the gfx
 (qkv_rope_append and gate_up_silu with their RMSNorm inside, paged_attention, and
 linear_residual for o_proj and for down_proj), then model.norm and one lm_head_argmax node.
 Same rounding points, same tensor names for inputs and outputs.
+
+stack graph (fused=True, stack=True): the decoder layers of the fused graph as one
+decoder_stack node (one persistent launch for all layers), bit-identical to the fused graph.
 """
 from __future__ import annotations
 
@@ -108,19 +111,48 @@ def _fused_nodes(cfg: Qwen2Config, batch: int, nodes: list, splits: dict, logits
           {"logits_dtype": logits_dtype})
 
 
+def _stack_nodes(cfg: Qwen2Config, nodes: list, splits: dict, logits_dtype: str,
+                 check_status: bool = False):
+    """Every decoder layer in one decoder_stack node (one persistent launch), then model.norm
+    and lm_head_argmax as in the fused graph. Same rounding points and values as the fused
+    graph with o split 1."""
+    inputs = ["hidden_states", "positions", "rotary_cos", "rotary_sin"]
+    for i in range(cfg.layers):
+        p = f"model.layers.{i}"
+        inputs += [f"{p}.input_layernorm.weight", f"{p}.self_attn.qkv_proj.weight",
+                   f"{p}.self_attn.qkv_proj.bias", f"{p}.self_attn.o_proj.weight",
+                   f"{p}.post_attention_layernorm.weight", f"{p}.mlp.gate_up_proj.weight",
+                   f"{p}.mlp.down_proj.weight"]
+    _node(nodes, "model.layers", "decoder_stack", inputs, ["layers_output"],
+          {"layers": cfg.layers, "q_heads": cfg.heads, "kv_heads": cfg.kv_heads,
+           "head_dim": cfg.head_dim, "eps": cfg.eps, "down_splits": splits.get("down", 4),
+           "kv_cache_prefix": "layer_", "check_status": int(check_status)})
+    _node(nodes, "model.norm", "rms_norm", ["layers_output", "model.norm.weight"], ["norm_hidden"],
+          {"eps": cfg.eps})
+    _node(nodes, "lm_head", "lm_head_argmax", ["norm_hidden", "lm_head.weight"], OUTPUTS,
+          {"logits_dtype": logits_dtype})
+
+
 DEFAULT_SPLITS = {"o": 1, "down": 4}
 
 
 def build_decode_graph(cfg: Qwen2Config, batch: int, fused: bool = True,
-                       splits: dict | None = None, logits_dtype: str = "float32") -> "dli.Graph":
+                       splits: dict | None = None, logits_dtype: str = "float32",
+                       stack: bool = False, check_status: bool = False) -> "dli.Graph":
+    """fused=False: the reference's node sequence; fused=True: five launches per layer;
+    stack=True (with fused): all layers in one decoder_stack node (check_status: the node waits
+    for its launch and fails if a workgroup gave up waiting; for tests, not for capture)."""
     nodes: list = []
     _node(nodes, "model.embed_tokens", "embedding", ["input_ids", "model.embed_tokens.weight"],
           ["hidden_states"])
-    if fused:
+    if fused and stack:
+        _stack_nodes(cfg, nodes, splits or DEFAULT_SPLITS, logits_dtype, check_status)
+    elif fused:
         _fused_nodes(cfg, batch, nodes, splits or DEFAULT_SPLITS, logits_dtype)
     else:
         _reference_nodes(cfg, batch, nodes)
-    graph = {"format": "dli.graph.v1", "model_type": "qwen2_decode_fused" if fused else "qwen2_decode",
+    model_type = "qwen2_decode" if not fused else ("qwen2_decode_stack" if stack else "qwen2_decode_fused")
+    graph = {"format": "dli.graph.v1", "model_type": model_type,
              "inputs": INPUTS, "outputs": OUTPUTS, "nodes": nodes}
     return dli.Graph.from_json(json.dumps(graph))
 

@@ -18,14 +18,17 @@ from .graph import build_decode_graph, pack_fused_weights
 class DecodeSession:
     def __init__(self, cfg: Qwen2Config, weights: dict, batch: int, max_seq_len: int,
                  fused: bool = True, engine: "dli.Engine | None" = None, splits: dict | None = None,
-                 block_size: int = 64, logits_dtype: str = "float32", device: str = "cuda"):
+                 block_size: int = 64, logits_dtype: str = "float32", device: str = "cuda",
+                 stack: bool = False, check_status: bool = False):
         self.cfg = cfg
         self.batch = batch
         self.fused = fused
+        self.stack = fused and stack
         self.engine = engine or dli.Engine().load_plugin()
         self.engine.configure_kv_cache(block_size=block_size, max_seq_len=max_seq_len)
         self.graph = build_decode_graph(cfg, batch, fused=fused, splits=splits,
-                                        logits_dtype=logits_dtype)
+                                        logits_dtype=logits_dtype, stack=stack,
+                                        check_status=check_status)
         tensors = pack_fused_weights(cfg, weights, drop_unfused=True) if fused else dict(weights)
         self.ids = torch.zeros(batch, dtype=torch.int64, device=device)
         self.positions = torch.zeros(batch, dtype=torch.int64, device=device)

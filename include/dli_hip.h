@@ -280,6 +280,64 @@ int dli_hip_lm_head_argmax(const void* xn, const void* w, void* logits, int logi
                            int64_t* ids, int64_t m, int64_t vocab, int64_t hidden_size,
                            void* workspace, size_t workspace_bytes, void* stream);
 
+/* ---------------------------------------------------------------------------------------
+ * 4. Persistent decoder stack: all decoder layers of one batched decode step in one launch
+ *    (one 8-wave workgroup per CU). Per layer it computes exactly what the five fused calls
+ *    above compute (dli_hip_qkv_rope_append with the input norm, dli_hip_paged_attention,
+ *    dli_hip_linear_residual for o_proj with one split, dli_hip_gate_up_silu with the
+ *    post-attention norm, dli_hip_linear_residual for down_proj with down_splits), bit for bit,
+ *    and replaces the same reference nodes: export.py:272-424 for every layer. Workgroups hand
+ *    stages to each other through arrival counters in the workspace instead of kernel
+ *    boundaries. Supported: bf16, head_dim 64, block_size 64, q_heads / kv_heads <= 16,
+ *    hidden <= 1024 and a multiple of 64, ffn a multiple of 64, batch <= 64, no o_proj or
+ *    down_proj bias.
+ * ------------------------------------------------------------------------------------- */
+
+/* Device pointers of one decoder layer. */
+typedef struct DliDecoderLayer {
+  const void* input_norm;      /* [hidden] */
+  const void* w_qkv;           /* [(q_heads + 2 kv_heads) head_dim, hidden], rows q | k | v */
+  const void* b_qkv;           /* [(q_heads + 2 kv_heads) head_dim] or NULL */
+  const void* w_o;             /* [hidden, q_heads head_dim] */
+  const void* post_norm;       /* [hidden] */
+  const void* w_gate_up;       /* [2 ffn, hidden], 16-row interleave as dli_hip_gate_up_silu */
+  const void* w_down;          /* [hidden, ffn] */
+  void* key_pool;              /* paged cache of this layer (include/dli/kv_cache.h) */
+  void* value_pool;
+  const int32_t* block_table;  /* [batch, max_blocks] */
+} DliDecoderLayer;
+
+/* Workspace bytes for dli_hip_decoder_stack with num_layers layers (arrival counters, partials
+ * and one activation slab per layer of a launch, so no activation buffer is reused within a
+ * launch). */
+size_t dli_hip_decoder_stack_workspace(int num_layers, int64_t batch, int64_t hidden_size,
+                                       int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+                                       int64_t ffn, int64_t max_blocks, int down_splits);
+
+/* hidden_out = the residual stream after `num_layers` layers applied to hidden_in [batch,
+ * hidden_size] (hidden_out may equal hidden_in). Each layer appends its new k/v at
+ * positions[b] and attends over keys [0, positions[b]]. The workspace must be zero-filled
+ * before its first use; every call leaves it ready for the next one on the same stream. Calls
+ * that share a workspace must not overlap. */
+int dli_hip_decoder_stack(const DliDecoderLayer* layers, int num_layers, const void* hidden_in,
+                          void* hidden_out, const void* positions, int positions_dtype,
+                          const float* cos_table, const float* sin_table, int64_t max_pos,
+                          int64_t block_size, int64_t max_blocks, int64_t batch,
+                          int64_t hidden_size, int64_t q_heads, int64_t kv_heads,
+                          int64_t head_dim, int64_t ffn, float eps, int down_splits,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
+/* Sets the key-range split count of MFMA decode attention for every later call of
+ * dli_hip_paged_attention and dli_hip_decoder_stack in the process (0 = choose per call: the
+ * stand-alone kernel spreads over all CUs, the decoder stack over the CUs its q|k|v stage leaves
+ * free). Equal counts make the two paths bit-identical. splits in [0, 32]. */
+int dli_hip_set_decode_attention_splits(int splits);
+
+/* Synchronizes `stream`, then *aborted = 1 when a launch since the last query gave up waiting
+ * for another workgroup (its outputs are invalid; this can only happen when the workgroups
+ * were not all resident at once), else 0. Clears the flag. */
+int dli_hip_decoder_stack_status(void* workspace, int* aborted, void* stream);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 #endif

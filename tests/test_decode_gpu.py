@@ -63,7 +63,7 @@ def test_capture_replay_equals_eager():
         assert torch.equal(ia, ib)
 
 
-def _teacher_forced_parity(cfg, w, batch, prompt_len, steps, rows, seed, agree_min):
+def _teacher_forced_parity(cfg, w, batch, prompt_len, steps, rows, seed, agree_min, stack=False):
     """Free-running greedy decode on the GPU, then the oracle teacher-forced on the GPU's own
     tokens (one batched CPU pass over prompt + generated tokens), so both score the same
     prefixes at every step.
@@ -82,7 +82,7 @@ def _teacher_forced_parity(cfg, w, batch, prompt_len, steps, rows, seed, agree_m
          on at least `agree_min` of the steps.
     """
     prompt = _prompt(cfg, batch, prompt_len, seed)
-    session = DecodeSession(cfg, w, batch, max_seq_len=prompt_len + steps + 8).capture()
+    session = DecodeSession(cfg, w, batch, max_seq_len=prompt_len + steps + 8, stack=stack).capture()
     got = _run_steps(session, prompt, steps - 1)  # logits after the prompt + steps-1 tokens
     logits = torch.stack([lg[rows] for lg, _ in got], 1)  # [R, T, V]
     ids = torch.stack([nx for _, nx in got], 1)  # [B, T]
@@ -113,18 +113,21 @@ def _teacher_forced_parity(cfg, w, batch, prompt_len, steps, rows, seed, agree_m
     assert rate >= agree_min, f"token agreement {rate:.3f} < {agree_min}"
 
 
-def test_tiny_decode_teacher_forced_parity():
+@pytest.mark.parametrize("stack", [False, True], ids=["fused", "stack"])
+def test_tiny_decode_teacher_forced_parity(stack):
     cfg = tiny_config()
     w = random_weights(cfg, seed=31, device="cuda")
     _teacher_forced_parity(cfg, w, batch=6, prompt_len=12, steps=24, rows=[0, 3, 5], seed=32,
-                           agree_min=0.9)
+                           agree_min=0.9, stack=stack)
 
 
 @pytest.mark.slow
-def test_qwen2_0_5b_shape_64_steps_teacher_forced_parity():
-    """Full Qwen2-0.5B shape, batch 32, 512 random prompt tokens, 64 greedy steps; the oracle
-    scores rows 0, 17 and 31 on the CPU."""
+@pytest.mark.parametrize("stack", [False, True], ids=["fused", "stack"])
+def test_qwen2_0_5b_shape_64_steps_teacher_forced_parity(stack):
+    """Full Qwen2-0.5B shape, batch 32, 512 random prompt tokens, 64 greedy steps (fused graph,
+    or every layer in the persistent decoder stack); the oracle scores rows 0, 17 and 31 on the
+    CPU."""
     cfg = QWEN2_0_5B
     w = random_weights(cfg, seed=41, device="cuda")
     _teacher_forced_parity(cfg, w, batch=32, prompt_len=512, steps=64, rows=[0, 17, 31], seed=42,
-                           agree_min=0.9)
+                           agree_min=0.9, stack=stack)

@@ -98,3 +98,38 @@ def test_fused_decode_entry_points_reject_invalid_arguments():
     assert b"positions" in lib.dli_hip_last_error()
     # partials [splits, m, n] fp32 (256-byte aligned) + one arrival counter per 16-row tile
     assert lib.dli_hip_splitk_workspace(896, 32, 4) == 4 * 32 * 896 * 4 + 256
+
+
+def test_decoder_stack_rejects_invalid_arguments():
+    """dli_hip_decoder_stack checks every argument before it touches the device."""
+    lib = hip.load()
+    layer = hip.DecoderLayer(*([256] * 10))  # fake, never dereferenced
+    fake = ctypes.c_void_p(256)
+
+    def call(layers=ctypes.byref(layer), n=1, positions=fake, pos_dtype=hip.I64, block_size=64,
+             batch=32, hidden=896, hq=14, hkv=2, d=64, ffn=4864, splits=4):
+        return lib.dli_hip_decoder_stack(layers, n, fake, fake, positions, pos_dtype, fake, fake,
+                                         1024, block_size, 64, batch, hidden, hq, hkv, d, ffn,
+                                         1e-6, splits, fake, 1 << 20, None)
+
+    assert call(n=0) == 0  # no layers: nothing to do
+    assert call(layers=None) == -1
+    assert call(batch=65) == -1
+    assert b"batch must be in [1, 64]" in lib.dli_hip_last_error()
+    assert call(hidden=2048) == -1
+    assert b"hidden_size" in lib.dli_hip_last_error()
+    assert call(d=128) == -1
+    assert b"head_dim must be 64" in lib.dli_hip_last_error()
+    assert call(block_size=16) == -1
+    assert call(hq=14, hkv=4) == -1
+    assert b"multiple of kv_heads" in lib.dli_hip_last_error()
+    assert call(ffn=100) == -1
+    assert call(splits=9) == -1
+    assert b"down_splits" in lib.dli_hip_last_error()
+    assert call(positions=None) == -1
+    assert call(pos_dtype=hip.F32) == -1
+    assert b"positions" in lib.dli_hip_last_error()
+    missing = hip.DecoderLayer(*([256] * 9 + [0]))  # no block table
+    assert call(layers=ctypes.byref(missing)) == -1
+    assert b"layer 0 has a NULL pointer" in lib.dli_hip_last_error()
+    assert lib.dli_hip_decoder_stack_status(None, None, None) == -1

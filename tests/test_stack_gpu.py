@@ -1,0 +1,166 @@
+"""The persistent decoder stack (plugin op decoder_stack -> C ABI dli_hip_decoder_stack: every
+decoder layer in one launch) against the five-launch fused graph.
+
+Per tile, the stack runs the same code in the same order as the one-stage kernels, so the two
+graphs must agree bit for bit: logits, greedy ids and every layer's KV cache, step after step.
+Repeated steps also check that each launch leaves its arrival counters at zero, and
+check_status makes every launch report whether a workgroup gave up waiting (it must not).
+The fused graph itself is checked against the CPU oracle in test_decode_gpu.py."""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from dli import hip
+from dli_qwen2 import QWEN2_0_5B, DecodeSession, random_weights, tiny_config
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(autouse=True)
+def same_attention_splits():
+    """Both paths split each attention pair's keys the same way (by default the stack spreads
+    attention over the CUs its q|k|v stage leaves free, the stand-alone kernel over all CUs)."""
+    hip.call("dli_hip_set_decode_attention_splits", 3)
+    yield
+    hip.call("dli_hip_set_decode_attention_splits", 0)
+
+
+def _prompt(cfg, batch, length, seed):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randint(0, cfg.vocab, (batch, length), generator=g)
+
+
+def _run_steps(session, prompt, steps, start=0):
+    b, s = prompt.shape
+    pos = torch.full((b,), start, dtype=torch.int64, device="cuda")
+    out = []
+    nxt = None
+    for t in range(s + steps):
+        ids = prompt[:, t].cuda() if t < s else nxt
+        logits, nxt = session.step(ids, pos)
+        nxt = nxt.clone()
+        out.append((logits.float().cpu().clone(), nxt.cpu()))
+        pos += 1
+    return out
+
+
+def _assert_same(fused, stack, a, b, layers):
+    for step, ((la, ia), (lb, ib)) in enumerate(zip(a, b)):
+        assert torch.equal(la, lb), f"logits differ at step {step}"
+        assert torch.equal(ia, ib), f"ids differ at step {step}"
+    for i in range(layers):
+        ea = fused.engine.kv_cache_entry(f"layer_{i}")
+        eb = stack.engine.kv_cache_entry(f"layer_{i}")
+        assert torch.equal(ea["key"], eb["key"]), f"key cache of layer {i} differs"
+        assert torch.equal(ea["value"], eb["value"]), f"value cache of layer {i} differs"
+
+
+@pytest.mark.parametrize("batch", [1, 5, 16, 32, 40])
+def test_stack_matches_fused_graph_bitwise(batch):
+    cfg = tiny_config(layers=3)
+    w = random_weights(cfg, seed=31, device="cuda")
+    prompt = _prompt(cfg, batch, 6, 32)
+    fused = DecodeSession(cfg, w, batch, max_seq_len=256, fused=True)
+    stack = DecodeSession(cfg, w, batch, max_seq_len=256, fused=True, stack=True,
+                          check_status=True)
+    print(f"stack vs fused: batch {batch}", flush=True)
+    _assert_same(fused, stack, _run_steps(fused, prompt, 4), _run_steps(stack, prompt, 4),
+                 cfg.layers)
+
+
+def test_stack_ragged_positions_cross_cache_blocks():
+    """Sequences at different positions, some crossing 64-token cache blocks during the run."""
+    cfg = tiny_config(layers=2)
+    w = random_weights(cfg, seed=41, device="cuda")
+    batch = 6
+    fused = DecodeSession(cfg, w, batch, max_seq_len=512, fused=True)
+    stack = DecodeSession(cfg, w, batch, max_seq_len=512, fused=True, stack=True,
+                          check_status=True)
+    start = torch.tensor([0, 61, 62, 127, 200, 300], device="cuda")
+    g = torch.Generator().manual_seed(42)
+    outs = []
+    for sess in (fused, stack):
+        pos = start.clone()
+        res = []
+        for t in range(5):
+            ids = torch.randint(0, cfg.vocab, (batch,), generator=g).cuda() if t == 0 else nxt
+            logits, nxt = sess.step(ids, pos)
+            nxt = nxt.clone()
+            res.append((logits.float().cpu().clone(), nxt.cpu()))
+            pos += 1
+        outs.append(res)
+        g.manual_seed(42)
+    _assert_same(fused, stack, outs[0], outs[1], cfg.layers)
+
+
+def test_stack_graph_replay_equals_fused_eager():
+    cfg = tiny_config(layers=2)
+    w = random_weights(cfg, seed=51, device="cuda")
+    prompt = _prompt(cfg, 8, 4, 52)
+    fused = DecodeSession(cfg, w, 8, max_seq_len=64)
+    stack = DecodeSession(cfg, w, 8, max_seq_len=64, stack=True).capture()
+    _assert_same(fused, stack, _run_steps(fused, prompt, 5), _run_steps(stack, prompt, 5),
+                 cfg.layers)
+
+
+def test_stack_qwen2_0_5b_shape_batch32_bitwise():
+    """All 24 layers of the Qwen2-0.5B shape at batch 32 (one launch)."""
+    cfg = QWEN2_0_5B
+    w = random_weights(cfg, seed=61, device="cuda")
+    prompt = _prompt(cfg, 32, 3, 62)
+    fused = DecodeSession(cfg, w, 32, max_seq_len=128, fused=True)
+    stack = DecodeSession(cfg, w, 32, max_seq_len=128, fused=True, stack=True, check_status=True)
+    _assert_same(fused, stack, _run_steps(fused, prompt, 3, start=60),
+                 _run_steps(stack, prompt, 3, start=60), cfg.layers)
+
+
+def test_stack_more_layers_than_one_launch():
+    """40 layers run as two launches (32 + 8) that continue from the same output buffer."""
+    cfg = tiny_config(layers=40)
+    w = random_weights(cfg, seed=71, device="cuda")
+    prompt = _prompt(cfg, 4, 3, 72)
+    fused = DecodeSession(cfg, w, 4, max_seq_len=64, fused=True)
+    stack = DecodeSession(cfg, w, 4, max_seq_len=64, fused=True, stack=True, check_status=True)
+    _assert_same(fused, stack, _run_steps(fused, prompt, 2), _run_steps(stack, prompt, 2),
+                 cfg.layers)
+
+
+def _fill_caches(sessions, cfg, seed):
+    """The same seeded context in every layer's cache of each session."""
+    for i in range(cfg.layers):
+        g = torch.Generator(device="cuda").manual_seed(seed + i)
+        pools = [sess.engine.kv_cache_entry(f"layer_{i}") for sess in sessions]
+        for name in ("key", "value"):
+            val = torch.randn(pools[0][name].shape, generator=g, device="cuda").to(torch.bfloat16)
+            for p in pools:
+                p[name].copy_(val)
+
+
+@pytest.mark.parametrize("splits", [3, 4])
+def test_stack_long_context_split_merge_bitwise(splits):
+    """Context up to 4096 keys: every pair's keys are split over several workgroups and merged
+    by the last to finish, in both paths."""
+    hip.call("dli_hip_set_decode_attention_splits", splits)
+    cfg = tiny_config(layers=2)
+    w = random_weights(cfg, seed=81, device="cuda")
+    batch = 32
+    fused = DecodeSession(cfg, w, batch, max_seq_len=4096 + 64, fused=True)
+    stack = DecodeSession(cfg, w, batch, max_seq_len=4096 + 64, fused=True, stack=True,
+                          check_status=True)
+    start = torch.tensor([4000 - 37 * b for b in range(batch)], device="cuda")
+    ids0 = torch.randint(0, cfg.vocab, (batch,), generator=torch.Generator().manual_seed(82))
+    outs = []
+    for sess in (fused, stack):
+        sess.step(ids0.cuda(), start)  # reserves the caches
+    _fill_caches((fused, stack), cfg, 83)
+    for sess in (fused, stack):
+        pos = start.clone()
+        res, nxt = [], ids0.cuda()
+        for _ in range(3):
+            logits, nxt = sess.step(nxt, pos)
+            nxt = nxt.clone()
+            res.append((logits.float().cpu().clone(), nxt.cpu()))
+            pos += 1
+        outs.append(res)
+    _assert_same(fused, stack, outs[0], outs[1], cfg.layers)
