@@ -101,7 +101,7 @@ def time_decode_attention(session, cfg, B, ctx, pos, g, stream, hip, reps=200):
     return "decode attention (decode_attention_d64)", us, nbytes
 
 
-def time_decoder_stack(session, cfg, B, ctx, pos, g, stream, hip, reps=20):
+def time_decoder_stack(session, cfg, B, ctx, pos, g, stream, hip, down_splits, reps=20):
     """The persistent decoder stack (every layer in one launch) alone, on the session's weights
     and caches, timed with HIP events on the stream it is launched on. Algorithmic bytes per
     launch: every layer's weights once, the K/V context read once, the new K/V written."""
@@ -126,7 +126,7 @@ def time_decoder_stack(session, cfg, B, ctx, pos, g, stream, hip, reps=20):
     e0 = session.engine.kv_cache_entry("layer_0")
     ws_bytes = hip.lib().dli_hip_decoder_stack_workspace(L, B, cfg.hidden, cfg.heads,
                                                           cfg.kv_heads, cfg.head_dim, cfg.ffn,
-                                                          e0["max_blocks"], 4)
+                                                          e0["max_blocks"], down_splits)
     ws = torch.zeros((ws_bytes + 3) // 4, dtype=torch.int32, device="cuda")
     x = (torch.randn(B, cfg.hidden, generator=g, device="cuda") * 0.5).to(torch.bfloat16)
     out = torch.empty_like(x)
@@ -137,7 +137,7 @@ def time_decoder_stack(session, cfg, B, ctx, pos, g, stream, hip, reps=20):
         hip.call("dli_hip_decoder_stack", layers, L, x.data_ptr(), out.data_ptr(),
                  pos.data_ptr(), hip.I64, cos.data_ptr(), sin.data_ptr(), cos.shape[0],
                  e0["block_size"], e0["max_blocks"], B, cfg.hidden, cfg.heads, cfg.kv_heads,
-                 cfg.head_dim, cfg.ffn, cfg.eps, 4, ws.data_ptr(), ws_bytes, s_ptr)
+                 cfg.head_dim, cfg.ffn, cfg.eps, down_splits, ws.data_ptr(), ws_bytes, s_ptr)
 
     us = _time_launches(stack, stream, reps)
     aborted = ctypes.c_int()
@@ -179,9 +179,9 @@ def main():
 
     cfg = QWEN2_0_5B if args.layers is None else replace(QWEN2_0_5B, layers=args.layers)
     B, ctx = args.batch, args.context
-    from dli_qwen2.graph import DEFAULT_SPLITS
+    from dli_qwen2.graph import DEFAULT_SPLITS, STACK_SPLITS
 
-    splits = dict(DEFAULT_SPLITS)
+    splits = dict(STACK_SPLITS if args.graph == "stack" else DEFAULT_SPLITS)
     if args.splits:
         splits.update({k: int(v) for k, v in (item.split("=") for item in args.splits.split(","))})
     dev = "cuda"
@@ -232,7 +232,8 @@ def main():
     step_gbs = total / (ms_per_step * 1e-3) / 1e9
 
     if args.graph == "stack":
-        kernel, dom_us, dom_bytes = time_decoder_stack(session, cfg, B, ctx, pos, g, stream, hip)
+        kernel, dom_us, dom_bytes = time_decoder_stack(session, cfg, B, ctx, pos, g, stream, hip,
+                                                       splits["down"])
     else:
         kernel, dom_us, dom_bytes = time_decode_attention(session, cfg, B, ctx, pos, g, stream, hip)
     dom_gbs = dom_bytes / (dom_us * 1e-6) / 1e9

@@ -85,12 +85,15 @@ int stackGrid(unsigned* grid) {
   return 0;
 }
 
-// Attention units go to the workgroups that do no q|k|v work (the kernel gives q|k|v tiles two
-// per workgroup to the last workgroups of the grid), so splits ~ (grid - those) / pairs.
-int attnSplits(int64_t pairs, int64_t max_blocks, int64_t qkv_tiles, int* splits) {
+// Attention units go to the workgroups that do no q|k|v work (dli_stack::qkvWorkgroups, the
+// last ones of the grid), so splits ~ (grid - those) / pairs.
+int attnSplits(int64_t pairs, int64_t max_blocks, int64_t q_tiles, int64_t kv_tiles,
+               int* splits) {
   unsigned grid = 0;
   if (int rc = stackGrid(&grid)) return rc;
-  const int64_t qkv_wgs = (qkv_tiles + 1) / 2;
+  const int64_t qkv_wgs = dli_stack::qkvWorkgroups(static_cast<int>(q_tiles),
+                                                   static_cast<int>(kv_tiles),
+                                                   static_cast<int>(grid));
   const int64_t free_wgs = static_cast<int64_t>(grid) > qkv_wgs ? grid - qkv_wgs : grid;
   *splits = decodeAttentionSplits(pairs, max_blocks, static_cast<int>(free_wgs));
   return 0;
@@ -110,8 +113,8 @@ size_t dli_hip_decoder_stack_workspace(int num_layers, int64_t batch, int64_t hi
       head_dim <= 0 || ffn <= 0 || max_blocks <= 0 || down_splits < 1)
     return 0;
   int splits = 0;
-  if (attnSplits(batch * kv_heads, max_blocks, (q_heads + 2 * kv_heads) * head_dim / 16, &splits) !=
-      0)
+  if (attnSplits(batch * kv_heads, max_blocks, q_heads * head_dim / 16,
+                 2 * kv_heads * head_dim / 16, &splits) != 0)
     return 0;
   return layoutFor(batch, hidden_size, q_heads, kv_heads, head_dim, ffn, splits, down_splits,
                    num_layers)
@@ -157,8 +160,8 @@ int dli_hip_decoder_stack(const DliDecoderLayer* layers, int num_layers, const v
       return bad("layer " + std::to_string(i) + " weights must be 16-byte aligned");
   }
   int splits = 0;
-  if (int rc = attnSplits(batch * kv_heads, max_blocks, (q_heads + 2 * kv_heads) * head_dim / 16,
-                          &splits))
+  if (int rc = attnSplits(batch * kv_heads, max_blocks, q_heads * head_dim / 16,
+                          2 * kv_heads * head_dim / 16, &splits))
     return rc;
   if (max_blocks > static_cast<int64_t>(splits) * kDecWaves * 64)
     return bad("max_blocks exceeds what the attention splits can index");
@@ -167,6 +170,8 @@ int dli_hip_decoder_stack(const DliDecoderLayer* layers, int num_layers, const v
   if (workspace == nullptr || workspace_bytes < lay.total) return bad("workspace too small");
   unsigned grid = 0;
   if (int rc = stackGrid(&grid)) return rc;
+  if ((q_heads + 2 * kv_heads) * head_dim / 16 > 2 * static_cast<int64_t>(grid))
+    return bad("more than two q|k|v tiles per workgroup");
   DeviceKernel* kernel = batch <= 16 ? &k_stack_m1 : (batch <= 32 ? &k_stack_m2 : &k_stack_m4);
 
   char* ws = static_cast<char*>(workspace);

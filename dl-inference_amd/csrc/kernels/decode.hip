@@ -45,7 +45,7 @@ __device__ void qkv_rope_append_impl(const uint16_t* x, const uint16_t* norm_w, 
   QkvEpilogue<MB, PlainMem> epi;
   epi.prefetch(p, n0);  // epilogue operands do not depend on the GEMM: fetched first
   tileLoop<1, MB, kNormWaves, kNormUnroll>(w, XGlobal{x, K}, N, K, p.M, lds, norm_w, eps,
-                                           blockIdx.x, gridDim.x, NoWait{},
+                                           blockIdx.x, gridDim.x, INT64_MAX, NoWait{},
                                            [&](int64_t) { epi.apply(p, n0, lds); });
 }
 
@@ -155,7 +155,7 @@ __device__ void gate_up_silu_impl(const uint16_t* x, const uint16_t* norm_w, flo
   using Core = SkinnyCore<2, MB, kNormWaves, kNormUnroll>;
   __shared__ float lds[Core::kLdsFloats];
   tileLoop<2, MB, kNormWaves, kNormUnroll>(
-      w_gu, XGlobal{x, K}, 2 * F, K, M, lds, norm_w, eps, blockIdx.x, gridDim.x, NoWait{},
+      w_gu, XGlobal{x, K}, 2 * F, K, M, lds, norm_w, eps, blockIdx.x, gridDim.x, INT64_MAX, NoWait{},
       [&](int64_t t) { gateUpEpilogue<MB, PlainMem>(lds, out, M, F, t); });
 }
 
@@ -174,7 +174,7 @@ __device__ void lm_head_argmax_impl(const uint16_t* xn, const uint16_t* w, void*
   __shared__ int lds_arg[kLmQuarters * Core::kTileM];
   const int64_t tiles = (V + Core::kTileN - 1) / Core::kTileN;
   tileLoop<2, MB, kWaves, 4>(w, XGlobal{xn, K}, V, K, M, lds, nullptr, 0.f, blockIdx.x,
-                             gridDim.x, NoWait{}, [&](int64_t t) {
+                             gridDim.x, INT64_MAX, NoWait{}, [&](int64_t t) {
     const int64_t n0 = t * Core::kTileN;
     if (logits != nullptr) {
       for (int idx = threadIdx.x; idx < Core::kTileN * Core::kTileM; idx += blockDim.x) {

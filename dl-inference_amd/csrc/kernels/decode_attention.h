@@ -62,6 +62,49 @@ __device__ __forceinline__ void loadKvBlock(KvBlockRegs& regs, const uint16_t* k
   }
 }
 
+// One cache block of one kv head staged in LDS (the pools' layouts: K token-major, V dim-major).
+struct KvBlockLds {
+  uint16_t k[kDecBlock * kDecD];
+  uint16_t v[kDecD * kDecBlock];
+};
+
+// Copies block `blk` of kv head kvh into dst with direct global-to-LDS loads
+// (global_load_lds_dwordx4: no registers held while the data is in flight). Copy j of lane i
+// moves bytes [1024 j + 16 i, +16) of the K block and then of the V block. One wave.
+__device__ __forceinline__ void stageKvBlock(KvBlockLds* dst, const uint16_t* k_pool,
+                                             const uint16_t* v_pool, int64_t blk, int Hkv,
+                                             int kvh, int lane) {
+  const int64_t head_stride = static_cast<int64_t>(kDecBlock) * kDecD;
+  const uint16_t* kb = k_pool + (blk * Hkv + kvh) * head_stride;
+  const uint16_t* vb = v_pool + (blk * Hkv + kvh) * head_stride;
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    __builtin_amdgcn_global_load_lds(kb + j * 512 + lane * 8, dst->k + j * 512, 16, 0, 0);
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    __builtin_amdgcn_global_load_lds(vb + j * 512 + lane * 8, dst->v + j * 512, 16, 0, 0);
+}
+
+// loadKvBlock from a block staged in LDS (same fragments, same masking).
+__device__ __forceinline__ void loadKvBlockLds(KvBlockRegs& regs, const KvBlockLds* src,
+                                               int64_t blk_index, int64_t end, int r, int g) {
+  const int64_t t_block = blk_index * kDecBlock;
+#pragma unroll
+  for (int st = 0; st < 2; ++st) {
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      const int off = 32 * st + 8 * (r / 4) + 4 * hf + (r % 4);
+      const bool ok = t_block + off < end;
+      regs.k[st][hf][0] = ok ? load16(src->k + off * kDecD + g * 8) : zero16();
+      regs.k[st][hf][1] = ok ? load16(src->k + off * kDecD + 32 + g * 8) : zero16();
+    }
+    const bool vok = t_block + 32 * st + 8 * g < end;
+#pragma unroll
+    for (int d = 0; d < 4; ++d)
+      regs.v[st][d] = vok ? load16(src->v + (d * 16 + r) * kDecBlock + 32 * st + 8 * g) : zero16();
+  }
+}
+
 struct SoftmaxState {
   float m = -INFINITY;
   float l = 0.f;
@@ -170,12 +213,14 @@ struct DecodeAttnLds {
 // wave calls it) once the cache holds the newest token, which only the block holding position
 // positions[b] needs. With kPreload each wave requests its first two cache blocks before gate()
 // (except the newest-token block), so the K/V stream overlaps the wait. The arithmetic does not
-// depend on these choices.
+// depend on these choices. With `stage` (kDecWaves blocks of LDS, which may overlap `s`) each
+// wave also stages its third block in LDS before gate(), so a wave with three blocks streams
+// nothing after the wait either.
 template <class Mem, bool kPreload, class Gate, class KvReady>
 __device__ __forceinline__ bool decodeAttentionUnit(const DecodeAttnArgs& a, int split, int pair,
                                                     unsigned arrivals, bool reset,
-                                                    DecodeAttnLds& s, Gate&& gate,
-                                                    KvReady&& kv_ready) {
+                                                    DecodeAttnLds& s, KvBlockLds* stage,
+                                                    Gate&& gate, KvReady&& kv_ready) {
   FP_EXACT;
   const int tid = freshThreadIdx();
   const int lane = tid % kWave, wave = tid / kWave;
@@ -216,7 +261,7 @@ __device__ __forceinline__ bool decodeAttentionUnit(const DecodeAttnArgs& a, int
     if (bi == newest) kv_ready();
     loadKvBlock(buf, a.k_pool, a.v_pool, __shfl(my_blk, ordinal, kWave), bi, L, a.Hkv, kvh, r, g);
   };
-  bool a_ready = false, b_ready = false;
+  bool a_ready = false, b_ready = false, c_staged = false;
   if (kPreload && active) {
     if (first < n_live && first != newest) {
       fetch(bufA, first, 0);
@@ -225,6 +270,11 @@ __device__ __forceinline__ bool decodeAttentionUnit(const DecodeAttnArgs& a, int
     if (first + stride < n_live && first + stride != newest) {
       fetch(bufB, first + stride, 1);
       b_ready = true;
+    }
+    const int64_t third = first + 2 * stride;
+    if (stage != nullptr && third < n_live && third != newest) {
+      stageKvBlock(stage + wave, a.k_pool, a.v_pool, __shfl(my_blk, 2, kWave), a.Hkv, kvh, lane);
+      c_staged = true;
     }
   }
   gate();  // also before an inactive unit arrives, so arrivals of one call never mix with the next
@@ -249,11 +299,17 @@ __device__ __forceinline__ bool decodeAttentionUnit(const DecodeAttnArgs& a, int
       if (j >= n_live) break;
       const int64_t k2 = j + stride;
       if (k2 < n_live) {
-        fetch(bufA, k2, k + 2);
+        if (c_staged && k == 0) {
+          asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the staged block has landed
+          loadKvBlockLds(bufA, stage + wave, k2, L, r, g);
+        } else {
+          fetch(bufA, k2, k + 2);
+        }
         a_ready = true;
       }
       attendBlock(st8, bufB, qf, j * kDecBlock, L, g, a.scale_log2);
     }
+    if (stage != nullptr) __syncthreads();  // staged blocks are consumed before s reuses LDS
 
     if (g == 0) {
       s.sm[wave][r] = st8.m;

@@ -116,7 +116,7 @@ __device__ __forceinline__ void normalizeFragments(
   }
 }
 
-// Weight tiles t = t_first, t_first + t_stride, ... (16 * NF rows each) against one x whose
+// Weight tiles t = t_first, t_first + t_stride, ... below t_end (16 * NF rows each) against one x whose
 // fragments are loaded once (and RMS-normalized with norm_w when it is non-NULL) and stay in
 // registers; the next tile's weights stream in while the current one is multiplied. epi(t)
 // reads the reduced tile [16 NF][16 MB] from lds (row n, column m at lds[n * 16 MB + m]).
@@ -130,14 +130,15 @@ template <int NF, int MB, int kW, int kU, class Mem = PlainMem, bool kGated = fa
           class Gate = NoWait, typename Epi>
 __device__ __forceinline__ void tileLoop(const uint16_t* w, const XGlobal& xs, int64_t N, int K,
                                          int M, float* lds, const uint16_t* norm_w, float eps,
-                                         int64_t t_first, int64_t t_stride, Gate&& gate,
-                                         Epi&& epi) {
+                                         int64_t t_first, int64_t t_stride, int64_t t_end,
+                                         Gate&& gate, Epi&& epi) {
   using Core = SkinnyCore<NF, MB, kW, kU>;
   const int lane = freshThreadIdx() % kWave;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int r = lane % 16, g = lane / 16;
   const int steps = K / 64;
-  const int64_t tiles = (N + Core::kTileN - 1) / Core::kTileN;
+  const int64_t all_tiles = (N + Core::kTileN - 1) / Core::kTileN;
+  const int64_t tiles = t_end < all_tiles ? t_end : all_tiles;
   const int64_t stride = t_stride;
   int64_t t = t_first;
   if (t >= tiles) return;

@@ -24,12 +24,14 @@
 // weights of its next tile (attention units: their first cache blocks), which do not depend on
 // the previous stage, so that stream overlaps the wait.
 //
-// Work placement. q|k|v tiles go two per workgroup to the last workgroups of the grid, which
-// have no down_proj unit and reach the stage first; attention units go to the other
-// workgroups; o_proj tiles to the first ones; gate_up tile t to workgroup (t + o_tiles) % G, so
-// workgroups with a second gate_up tile are not busy with o_proj. The q|k|v stage publishes q
-// first and then writes k/v into the cache, signalled on a second counter: attention needs the
-// new k/v only for the block holding the newest token, which its waves reach last.
+// Work placement. q|k|v tiles go to the last qkv_wgs workgroups of the grid (one per q tile,
+// two k/v tiles per workgroup), which have no down_proj unit and reach the stage first;
+// attention units go to the other workgroups; o_proj tiles to the first ones; gate_up tile t to
+// workgroup (t + o_tiles) % G, so workgroups with a second gate_up tile are not busy with
+// o_proj. q and the new k/v are signalled on separate counters: attention needs q at once, but
+// the new k/v only for the block holding the newest token, which its waves reach last. A wave
+// with a third cache block stages it in LDS (direct global-to-LDS loads) next to the two it
+// requests into registers, so nothing streams after the wait.
 //
 // Progress. The grid is at most one workgroup per CU and a workgroup fits a CU on its own, so
 // every workgroup is resident at once, and a stage only waits on earlier stages, which every
@@ -106,11 +108,16 @@ __device__ __forceinline__ T fresh(T v) {
   return v;
 }
 
+// LDS of a workgroup: the stages use it one at a time (each ends with a barrier), so the tile
+// reductions, the attention merge and the staged cache blocks share it.
 template <int MB>
 struct StackLds {
   using GuCore = SkinnyCore<2, MB, kNormWaves, kNormUnroll>;
-  float gemm[GuCore::kLdsFloats];  // the largest stage tile reduction (gate_up)
-  DecodeAttnLds attn;
+  union {
+    float gemm[GuCore::kLdsFloats];  // the largest stage tile reduction (gate_up)
+    DecodeAttnLds attn;
+    KvBlockLds kv[kDecWaves];
+  };
   int is_last;
 };
 
@@ -132,7 +139,9 @@ __device__ void decoderStack(const Args& a) {
   const int gu_tiles = a.F / 16, down_tiles = a.H / 16;
   const int pairs = a.M * a.Hkv, splits = a.attn_splits, down_splits = a.down_splits;
   const int attn_units = pairs * splits, down_units = down_tiles * down_splits;
-  const int qkv_wgs = (qkv_tiles + 1) / 2 < G ? (qkv_tiles + 1) / 2 : G;  // S1 workgroups
+  const int q_tiles = a.Hq * a.D / 16, kv_tiles = qkv_tiles - q_tiles;
+  const int qkv_wgs = dli_stack::qkvWorkgroups(q_tiles, kv_tiles, G);  // S1 workgroups
+  const int jb = bid - (G - qkv_wgs);  // index among the q|k|v workgroups, < 0 for the others
 
   for (int l = 0; l < a.layers; ++l) {
     const Layer& L = a.layer[l];
@@ -150,10 +159,11 @@ __device__ void decoderStack(const Args& a) {
     unsigned* const sync = fresh(a.sync);
     unsigned* const abort_word = sync + dli_stack::kAbortWord;
 
-    // S1: q|k|v tiles of the residual stream the previous layer finished, two per workgroup on
-    // the last workgroups of the grid (the ones without down_proj work, which reach this stage
-    // first), so that few workgroups start their attention unit late.
-    if (bid >= G - qkv_wgs) {
+    // S1: q|k|v tiles of the residual stream the previous layer finished, on the last qkv_wgs
+    // workgroups (the ones without down_proj work, which reach this stage first). q tiles come
+    // one per workgroup and k/v tiles two per workgroup when the grid has room (qkvWorkgroups),
+    // so q, which attention needs first, is ready after one tile.
+    if (jb >= 0) {
       const int H = fresh(a.H), M = fresh(a.M);
       const QkvParams qp{L.b_qkv,
                          fresh(a.cos_t),
@@ -168,23 +178,35 @@ __device__ void decoderStack(const Args& a) {
                          a.Hq,
                          a.Hkv,
                          a.D};
-      const int n_qkv = fresh((a.Hq + 2 * a.Hkv) * a.D);
-      const int t0 = bid - (G - qkv_wgs);
+      const int j = jb;
+      // this workgroup's tiles: t0, then t0 + t_stride while below t_end
+      int t0, t_stride, t_end;
+      if (qkv_wgs == q_tiles + (kv_tiles + 1) / 2) {
+        const bool q_wg = j < q_tiles;
+        t0 = q_wg ? j : q_tiles + 2 * (j - q_tiles);
+        t_stride = 1;
+        t_end = q_wg ? j + 1 : (t0 + 2 < qkv_tiles ? t0 + 2 : qkv_tiles);
+      } else {
+        t0 = j;
+        t_stride = qkv_wgs;
+        t_end = qkv_tiles;
+      }
       QkvEpilogue<MB, Mem> epi0, epi1;  // operands of this workgroup's (at most) two tiles
       epi0.prefetch(qp, static_cast<int64_t>(t0) * 16);
-      if (t0 + qkv_wgs < qkv_tiles) epi1.prefetch(qp, static_cast<int64_t>(t0 + qkv_wgs) * 16);
-      int done = 0;
+      if (t0 + t_stride < t_end) epi1.prefetch(qp, static_cast<int64_t>(t0 + t_stride) * 16);
+      unsigned kv_written = 0;
       auto finish = [&](const QkvEpilogue<MB, Mem>& e, int64_t t) {
-        // q first: attention needs it at once. The cache writes (scattered, slower to complete)
-        // follow and are signalled separately; attention needs them only for the block
-        // holding the newest token, which its waves reach last.
-        e.template apply<kQkvQ>(qp, t * 16, lds);
-        arrive(sync + dli_stack::stageWord(dli_stack::kQkvDone), 1);
-        e.template apply<kQkvCache>(qp, t * 16, lds);
-        ++done;
+        if (t < q_tiles) {  // q: published at once, attention waits for it
+          e.template apply<kQkvQ>(qp, t * 16, lds);
+          arrive(sync + dli_stack::stageWord(dli_stack::kQkvDone), 1);
+        } else {  // k/v into the cache: attention needs it only for the newest-token block
+          e.template apply<kQkvCache>(qp, t * 16, lds);
+          ++kv_written;
+        }
       };
       tileLoop<1, MB, kNormWaves, kNormUnroll, Mem, true>(
-          L.w_qkv, XGlobal{h_prev, H}, n_qkv, H, M, lds, L.input_norm, a.eps, t0, qkv_wgs,
+          L.w_qkv, XGlobal{h_prev, H}, qkv_tiles * 16, H, M, lds, L.input_norm, a.eps, t0,
+          t_stride, t_end,
           [&] {
             if (l > 0)
               waitAtLeast(sync + dli_stack::stageWord(dli_stack::kDownDone), l * down_tiles,
@@ -196,7 +218,7 @@ __device__ void decoderStack(const Args& a) {
             else
               finish(epi1, t);
           });
-      arrive(sync + dli_stack::stageWord(dli_stack::kKvDone), static_cast<unsigned>(done));
+      if (kv_written > 0) arrive(sync + dli_stack::stageWord(dli_stack::kKvDone), kv_written);
     }
 
     // S2: attention units.
@@ -219,13 +241,13 @@ __device__ void decoderStack(const Args& a) {
                               a.scale_log2};
       for (int u = bid; u < attn_units; u += G) {
         const bool merged = decodeAttentionUnit<Mem, true>(
-            da, u % splits, u / splits, gen * splits, false, smem.attn,
+            da, u % splits, u / splits, gen * splits, false, smem.attn, smem.kv,
             [&] {
-              waitAtLeast(sync + dli_stack::stageWord(dli_stack::kQkvDone), gen * qkv_tiles,
+              waitAtLeast(sync + dli_stack::stageWord(dli_stack::kQkvDone), gen * q_tiles,
                           abort_word);
             },
             [&] {
-              pollStage(sync + dli_stack::stageWord(dli_stack::kKvDone), gen * qkv_tiles,
+              pollStage(sync + dli_stack::stageWord(dli_stack::kKvDone), gen * kv_tiles,
                         abort_word);
             });
         if (merged) arrive(sync + dli_stack::stageWord(dli_stack::kAttnDone), 1);
@@ -253,7 +275,7 @@ __device__ void decoderStack(const Args& a) {
       const int H = fresh(a.H), M = fresh(a.M), F = fresh(a.F);
       tileLoop<2, MB, kNormWaves, kNormUnroll, Mem, true>(
           L.w_gate_up, XGlobal{h_mid, H}, 2 * static_cast<int64_t>(F), H, M, lds, L.post_norm,
-          a.eps, gu_first, G,
+          a.eps, gu_first, G, gu_tiles,
           [&] {
             waitAtLeast(sync + dli_stack::stageWord(dli_stack::kODone), gen * o_tiles,
                         abort_word);
@@ -263,19 +285,28 @@ __device__ void decoderStack(const Args& a) {
              static_cast<unsigned>((gu_tiles - 1 - gu_first) / G + 1));
     }
 
-    // S5: down_proj split-K + MLP residual; the last split of a tile writes h.
+    // S5: down_proj + MLP residual. With one split a tile is reduced over the full K; with
+    // several the last split of a tile to finish sums the partials and writes h.
     for (int u = bid; u < down_units; u += G) {
       const int H = fresh(a.H), M = fresh(a.M), F = fresh(a.F);
       const int tile = u % down_tiles, split = u / down_tiles;
       const int64_t n0 = static_cast<int64_t>(tile) * 16;
-      int sb, se;
-      splitRange(F / 64, split, down_splits, sb, se);
       ResidualTile<MB, kResThreads, Mem> rt;
-      DownCore::template runGated<Mem>(L.w_down, XGlobal{act, F}, H, F, M, n0, sb, se, lds, [&] {
+      auto gate = [&] {
         waitAtLeast(sync + dli_stack::stageWord(dli_stack::kGateUpDone), gen * gu_tiles,
                     abort_word);
         rt.load(h_mid, nullptr, n0, M, H);
-      });
+      };
+      if (down_splits == 1) {
+        OCore::template runGated<Mem>(L.w_down, XGlobal{act, F}, H, F, M, n0, 0, F / 64, lds,
+                                      gate);
+        rt.store(h, n0, M, H, [&](int, int idx) { return lds[idx]; });
+        arrive(sync + dli_stack::stageWord(dli_stack::kDownDone), 1);
+        continue;
+      }
+      int sb, se;
+      splitRange(F / 64, split, down_splits, sb, se);
+      DownCore::template runGated<Mem>(L.w_down, XGlobal{act, F}, H, F, M, n0, sb, se, lds, gate);
       unsigned* const tile_counters = sync + dli_stack::kPairCountersAt + pairs;
       if (splitKArrive<MB, kResThreads, Mem>(
               lds, fresh(a.down_part) + static_cast<int64_t>(tile) * down_splits * kTileElems,

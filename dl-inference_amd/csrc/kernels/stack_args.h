@@ -51,8 +51,8 @@ struct Args {
 // shards. Then the exit counter and the abort word (own lines), then one arrival counter per
 // attention pair (b, kv head) and per down_proj output tile.
 enum : int {
-  kQkvDone = 0,  // q of every q|k|v tile written
-  kKvDone,       // k/v of every q|k|v tile written into the cache
+  kQkvDone = 0,  // every q tile written
+  kKvDone,       // every k/v tile written into the cache
   kAttnDone,     // attention output of every pair written
   kODone,        // every o_proj tile (h_mid) written
   kGateUpDone,   // every gate_up tile (act) written
@@ -65,6 +65,14 @@ constexpr int stageWord(int stage) { return stage * kShards * kLineWords; }
 constexpr int kExitWord = kStages * kShards * kLineWords;
 constexpr int kAbortWord = kExitWord + kLineWords;
 constexpr int kPairCountersAt = kAbortWord + kLineWords;
+
+// Workgroups of the q|k|v stage (the last ones of the grid): one per q tile plus one per two k/v
+// tiles when the grid has room for that and at least as many others, else two tiles of any kind
+// per workgroup. The host sizes the attention split count from what this leaves free.
+constexpr int qkvWorkgroups(int q_tiles, int kv_tiles, int grid) {
+  return 2 * (q_tiles + (kv_tiles + 1) / 2) <= grid ? q_tiles + (kv_tiles + 1) / 2
+                                                    : (q_tiles + kv_tiles + 1) / 2;
+}
 
 inline int64_t syncWords(int64_t pairs, int64_t down_tiles) {
   return kPairCountersAt + pairs + down_tiles;

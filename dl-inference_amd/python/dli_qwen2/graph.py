@@ -125,7 +125,8 @@ def _stack_nodes(cfg: Qwen2Config, nodes: list, splits: dict, logits_dtype: str,
                    f"{p}.mlp.down_proj.weight"]
     _node(nodes, "model.layers", "decoder_stack", inputs, ["layers_output"],
           {"layers": cfg.layers, "q_heads": cfg.heads, "kv_heads": cfg.kv_heads,
-           "head_dim": cfg.head_dim, "eps": cfg.eps, "down_splits": splits.get("down", 4),
+           "head_dim": cfg.head_dim, "eps": cfg.eps,
+           "down_splits": splits.get("down", STACK_SPLITS["down"]),
            "kv_cache_prefix": "layer_", "check_status": int(check_status)})
     _node(nodes, "model.norm", "rms_norm", ["layers_output", "model.norm.weight"], ["norm_hidden"],
           {"eps": cfg.eps})
@@ -133,7 +134,10 @@ def _stack_nodes(cfg: Qwen2Config, nodes: list, splits: dict, logits_dtype: str,
           {"logits_dtype": logits_dtype})
 
 
+# split-K per projection (down_proj's K over 4 workgroups per tile in the fused graph, 3 in the
+# decoder stack, whose q|k|v workgroups take no down_proj unit)
 DEFAULT_SPLITS = {"o": 1, "down": 4}
+STACK_SPLITS = {"o": 1, "down": 3}
 
 
 def build_decode_graph(cfg: Qwen2Config, batch: int, fused: bool = True,
@@ -146,7 +150,7 @@ def build_decode_graph(cfg: Qwen2Config, batch: int, fused: bool = True,
     _node(nodes, "model.embed_tokens", "embedding", ["input_ids", "model.embed_tokens.weight"],
           ["hidden_states"])
     if fused and stack:
-        _stack_nodes(cfg, nodes, splits or DEFAULT_SPLITS, logits_dtype, check_status)
+        _stack_nodes(cfg, nodes, splits or STACK_SPLITS, logits_dtype, check_status)
     elif fused:
         _fused_nodes(cfg, batch, nodes, splits or DEFAULT_SPLITS, logits_dtype)
     else:

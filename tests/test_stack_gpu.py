@@ -56,14 +56,23 @@ def _assert_same(fused, stack, a, b, layers):
         assert torch.equal(ea["value"], eb["value"]), f"value cache of layer {i} differs"
 
 
+def _pair(cfg, w, batch, max_seq_len, down=1, **kw):
+    """A fused and a stack session with the same down_proj split-K (1: one workgroup reduces a
+    tile over the full K; more: the last split to finish merges the partials)."""
+    splits = {"o": 1, "down": down}
+    fused = DecodeSession(cfg, w, batch, max_seq_len=max_seq_len, fused=True, splits=splits)
+    stack = DecodeSession(cfg, w, batch, max_seq_len=max_seq_len, fused=True, stack=True,
+                          splits=splits, check_status=True, **kw)
+    return fused, stack
+
+
+@pytest.mark.parametrize("down", [1, 3])
 @pytest.mark.parametrize("batch", [1, 5, 16, 32, 40])
-def test_stack_matches_fused_graph_bitwise(batch):
+def test_stack_matches_fused_graph_bitwise(batch, down):
     cfg = tiny_config(layers=3)
     w = random_weights(cfg, seed=31, device="cuda")
     prompt = _prompt(cfg, batch, 6, 32)
-    fused = DecodeSession(cfg, w, batch, max_seq_len=256, fused=True)
-    stack = DecodeSession(cfg, w, batch, max_seq_len=256, fused=True, stack=True,
-                          check_status=True)
+    fused, stack = _pair(cfg, w, batch, 256, down)
     print(f"stack vs fused: batch {batch}", flush=True)
     _assert_same(fused, stack, _run_steps(fused, prompt, 4), _run_steps(stack, prompt, 4),
                  cfg.layers)
@@ -74,9 +83,7 @@ def test_stack_ragged_positions_cross_cache_blocks():
     cfg = tiny_config(layers=2)
     w = random_weights(cfg, seed=41, device="cuda")
     batch = 6
-    fused = DecodeSession(cfg, w, batch, max_seq_len=512, fused=True)
-    stack = DecodeSession(cfg, w, batch, max_seq_len=512, fused=True, stack=True,
-                          check_status=True)
+    fused, stack = _pair(cfg, w, batch, 512)
     start = torch.tensor([0, 61, 62, 127, 200, 300], device="cuda")
     g = torch.Generator().manual_seed(42)
     outs = []
@@ -98,8 +105,9 @@ def test_stack_graph_replay_equals_fused_eager():
     cfg = tiny_config(layers=2)
     w = random_weights(cfg, seed=51, device="cuda")
     prompt = _prompt(cfg, 8, 4, 52)
-    fused = DecodeSession(cfg, w, 8, max_seq_len=64)
-    stack = DecodeSession(cfg, w, 8, max_seq_len=64, stack=True).capture()
+    splits = {"o": 1, "down": 1}
+    fused = DecodeSession(cfg, w, 8, max_seq_len=64, splits=splits)
+    stack = DecodeSession(cfg, w, 8, max_seq_len=64, stack=True, splits=splits).capture()
     _assert_same(fused, stack, _run_steps(fused, prompt, 5), _run_steps(stack, prompt, 5),
                  cfg.layers)
 
@@ -109,8 +117,7 @@ def test_stack_qwen2_0_5b_shape_batch32_bitwise():
     cfg = QWEN2_0_5B
     w = random_weights(cfg, seed=61, device="cuda")
     prompt = _prompt(cfg, 32, 3, 62)
-    fused = DecodeSession(cfg, w, 32, max_seq_len=128, fused=True)
-    stack = DecodeSession(cfg, w, 32, max_seq_len=128, fused=True, stack=True, check_status=True)
+    fused, stack = _pair(cfg, w, 32, 128)
     _assert_same(fused, stack, _run_steps(fused, prompt, 3, start=60),
                  _run_steps(stack, prompt, 3, start=60), cfg.layers)
 
@@ -120,8 +127,7 @@ def test_stack_more_layers_than_one_launch():
     cfg = tiny_config(layers=40)
     w = random_weights(cfg, seed=71, device="cuda")
     prompt = _prompt(cfg, 4, 3, 72)
-    fused = DecodeSession(cfg, w, 4, max_seq_len=64, fused=True)
-    stack = DecodeSession(cfg, w, 4, max_seq_len=64, fused=True, stack=True, check_status=True)
+    fused, stack = _pair(cfg, w, 4, 64, down=4)
     _assert_same(fused, stack, _run_steps(fused, prompt, 2), _run_steps(stack, prompt, 2),
                  cfg.layers)
 
@@ -145,9 +151,7 @@ def test_stack_long_context_split_merge_bitwise(splits):
     cfg = tiny_config(layers=2)
     w = random_weights(cfg, seed=81, device="cuda")
     batch = 32
-    fused = DecodeSession(cfg, w, batch, max_seq_len=4096 + 64, fused=True)
-    stack = DecodeSession(cfg, w, batch, max_seq_len=4096 + 64, fused=True, stack=True,
-                          check_status=True)
+    fused, stack = _pair(cfg, w, batch, 4096 + 64)
     start = torch.tensor([4000 - 37 * b for b in range(batch)], device="cuda")
     ids0 = torch.randint(0, cfg.vocab, (batch,), generator=torch.Generator().manual_seed(82))
     outs = []
