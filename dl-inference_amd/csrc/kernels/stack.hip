@@ -26,12 +26,13 @@
 //
 // Work placement. q|k|v tiles go to the last qkv_wgs workgroups of the grid (one per q tile,
 // two k/v tiles per workgroup), which have no down_proj unit and reach the stage first;
-// attention units go to the other workgroups; o_proj tiles to the first ones; gate_up tile t to
-// workgroup (t + o_tiles) % G, so workgroups with a second gate_up tile are not busy with
-// o_proj. q and the new k/v are signalled on separate counters: attention needs q at once, but
-// the new k/v only for the block holding the newest token, which its waves reach last. A wave
-// with a third cache block stages it in LDS (direct global-to-LDS loads) next to the two it
-// requests into registers, so nothing streams after the wait.
+// attention units go to the other workgroups; o_proj tiles to the first ones; one gate_up tile
+// per attention workgroup and the rest, in runs, to the q|k|v workgroups (idle through
+// attention, so they request those tiles' weights meanwhile). q and the new k/v are signalled
+// on separate counters: attention needs q at once, but the new k/v only for the block holding
+// the newest token, which its waves reach last. A wave with a third cache block stages it in
+// LDS (direct global-to-LDS loads) next to the two it requests into registers, so nothing
+// streams after the wait.
 //
 // Progress. The grid is at most one workgroup per CU and a workgroup fits a CU on its own, so
 // every workgroup is resident at once, and a stage only waits on earlier stages, which every
@@ -267,22 +268,30 @@ __device__ void decoderStack(const Args& a) {
       arrive(sync + dli_stack::stageWord(dli_stack::kODone), 1);
     }
 
-    // S4: gate_up + SwiGLU, RMSNorm of h_mid in registers. Tile t runs on workgroup
-    // (t + o_tiles) % G: when there are more tiles than workgroups, the ones with a second tile
-    // are not the o_proj workgroups, so they request both tiles' weights during o_proj.
-    const int gu_first = (bid + G - o_tiles % G) % G;
-    if (gu_first < gu_tiles) {
+    // S4: gate_up + SwiGLU, RMSNorm of h_mid in registers. Tile bid on each workgroup without
+    // q|k|v work; the tiles beyond those in contiguous runs on the q|k|v workgroups, which are
+    // idle through attention and o_proj and request their tiles' weights meanwhile.
+    int gu_first = bid, gu_end = bid + 1;
+    if (jb >= 0) {
+      const int a_wgs = G - qkv_wgs;
+      const int rest = gu_tiles > a_wgs ? gu_tiles - a_wgs : 0;
+      const int per = (rest + qkv_wgs - 1) / qkv_wgs;
+      gu_first = a_wgs + jb * per;
+      gu_end = gu_first + per;
+    }
+    if (gu_end > gu_tiles) gu_end = gu_tiles;
+    if (gu_first < gu_end) {
       const int H = fresh(a.H), M = fresh(a.M), F = fresh(a.F);
       tileLoop<2, MB, kNormWaves, kNormUnroll, Mem, true>(
           L.w_gate_up, XGlobal{h_mid, H}, 2 * static_cast<int64_t>(F), H, M, lds, L.post_norm,
-          a.eps, gu_first, G, gu_tiles,
+          a.eps, gu_first, 1, gu_end,
           [&] {
             waitAtLeast(sync + dli_stack::stageWord(dli_stack::kODone), gen * o_tiles,
                         abort_word);
           },
           [&](int64_t t) { gateUpEpilogue<MB, Mem>(lds, act, M, F, t); });
       arrive(sync + dli_stack::stageWord(dli_stack::kGateUpDone),
-             static_cast<unsigned>((gu_tiles - 1 - gu_first) / G + 1));
+             static_cast<unsigned>(gu_end - gu_first));
     }
 
     // S5: down_proj + MLP residual. With one split a tile is reduced over the full K; with
