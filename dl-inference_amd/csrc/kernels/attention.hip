@@ -205,5 +205,5 @@ extern "C" __global__ void __launch_bounds__(dk::kDecThreads)
                              max_splits, scale_log2};
   dk::decodeAttentionUnit<dk::PlainMem, false>(a, blockIdx.x, blockIdx.y,
                                                static_cast<unsigned>(max_splits), true, lds,
-                                               nullptr, dk::NoWait{}, dk::NoWait{});
+                                               nullptr, 0, dk::NoWait{}, dk::NoWait{});
 }

@@ -39,7 +39,7 @@ template <int MB>
 __device__ void qkv_rope_append_impl(const uint16_t* x, const uint16_t* norm_w, float eps,
                                      const uint16_t* w, const QkvParams& p, int K) {
   using Core = SkinnyCore<1, MB, kNormWaves, kNormUnroll>;
-  __shared__ float lds[Core::kLdsFloats];
+  __shared__ float lds[Core::kLdsFloats + kNormLdsFloats<MB, kNormWaves>];
   const int64_t N = static_cast<int64_t>(p.Hq + 2 * p.Hkv) * p.D;
   const int64_t n0 = static_cast<int64_t>(blockIdx.x) * Core::kTileN;
   QkvEpilogue<MB, PlainMem> epi;
@@ -153,7 +153,7 @@ template <int MB>
 __device__ void gate_up_silu_impl(const uint16_t* x, const uint16_t* norm_w, float eps,
                                   const uint16_t* w_gu, uint16_t* out, int M, int64_t F, int K) {
   using Core = SkinnyCore<2, MB, kNormWaves, kNormUnroll>;
-  __shared__ float lds[Core::kLdsFloats];
+  __shared__ float lds[Core::kLdsFloats + kNormLdsFloats<MB, kNormWaves>];
   tileLoop<2, MB, kNormWaves, kNormUnroll>(
       w_gu, XGlobal{x, K}, 2 * F, K, M, lds, norm_w, eps, blockIdx.x, gridDim.x, INT64_MAX, NoWait{},
       [&](int64_t t) { gateUpEpilogue<MB, PlainMem>(lds, out, M, F, t); });

@@ -197,6 +197,28 @@ struct DecodeAttnLds {
   int is_last;
 };
 
+// Stages in stage[w], for each wave w < waves of unit `split` of pair `pair`, the third cache
+// block decodeAttentionUnit would stage at its start (never the newest-token block), so that a
+// later call with prestaged = waves on the same positions, block table and pools finds it there
+// and streams less after its gate. Loads complete in issue order: the caller issues this where
+// nothing latency-critical of the same waves follows soon.
+__device__ __forceinline__ void stageThirdKvBlocks(const DecodeAttnArgs& a, int split, int pair,
+                                                   KvBlockLds* stage, int waves) {
+  const int tid = freshThreadIdx();
+  const int lane = tid % kWave, wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  if (wave >= waves) return;
+  const int b = pair / a.Hkv, kvh = pair % a.Hkv;
+  const int64_t stride = static_cast<int64_t>(a.max_splits) * kDecWaves;
+  const int64_t third = static_cast<int64_t>(split) * kDecWaves + wave + 2 * stride;
+  const int64_t past_b = a.positions != nullptr ? loadIndex(a.positions, a.pos64, b) : a.past;
+  int64_t L = past_b + 1;
+  if (L > a.max_blocks * kDecBlock) L = a.max_blocks * kDecBlock;
+  const int64_t n_live = L > 0 ? (L + kDecBlock - 1) / kDecBlock : 0;
+  if (third >= n_live || third == n_live - 1) return;
+  const int32_t blk = a.block_table[static_cast<int64_t>(b) * a.max_blocks + third];
+  stageKvBlock(stage + wave, a.k_pool, a.v_pool, blk, a.Hkv, kvh, lane);
+}
+
 // One unit: split `split` of pair (b, kvh) = `pair`. The live cache blocks of a pair are dealt
 // round-robin over the splits x kDecWaves waves of its units: wave w of split s takes blocks
 // s * kDecWaves + w, + splits * kDecWaves, ..., so every wave streams the same number of blocks
@@ -215,12 +237,15 @@ struct DecodeAttnLds {
 // (except the newest-token block), so the K/V stream overlaps the wait. The arithmetic does not
 // depend on these choices. With `stage` (kDecWaves blocks of LDS, which may overlap `s`) each
 // wave also stages its third block in LDS before gate(), so a wave with three blocks streams
-// nothing after the wait either.
+// nothing after the wait either; waves below `prestaged` find that block already staged there
+// by stageThirdKvBlocks. The wave holding the newest-token block calls kv_ready() right after
+// gate() and requests that block into the slot left free for it.
 template <class Mem, bool kPreload, class Gate, class KvReady>
 __device__ __forceinline__ bool decodeAttentionUnit(const DecodeAttnArgs& a, int split, int pair,
                                                     unsigned arrivals, bool reset,
                                                     DecodeAttnLds& s, KvBlockLds* stage,
-                                                    Gate&& gate, KvReady&& kv_ready) {
+                                                    int prestaged, Gate&& gate,
+                                                    KvReady&& kv_ready) {
   FP_EXACT;
   const int tid = freshThreadIdx();
   const int lane = tid % kWave, wave = tid / kWave;
@@ -257,8 +282,12 @@ __device__ __forceinline__ bool decodeAttentionUnit(const DecodeAttnArgs& a, int
   for (int d = 0; d < 4; ++d) st8.o[d] = f32x4{0.f, 0.f, 0.f, 0.f};
   KvBlockRegs bufA, bufB;
   const int64_t newest = n_live - 1;  // the block holding position L - 1
+  bool kv_seen = false;  // kv_ready() has returned in this wave
   auto fetch = [&](KvBlockRegs& buf, int64_t bi, int ordinal) {
-    if (bi == newest) kv_ready();
+    if (bi == newest && !kv_seen) {
+      kv_ready();
+      kv_seen = true;
+    }
     loadKvBlock(buf, a.k_pool, a.v_pool, __shfl(my_blk, ordinal, kWave), bi, L, a.Hkv, kvh, r, g);
   };
   bool a_ready = false, b_ready = false, c_staged = false;
@@ -273,7 +302,9 @@ __device__ __forceinline__ bool decodeAttentionUnit(const DecodeAttnArgs& a, int
     }
     const int64_t third = first + 2 * stride;
     if (stage != nullptr && third < n_live && third != newest) {
-      stageKvBlock(stage + wave, a.k_pool, a.v_pool, __shfl(my_blk, 2, kWave), a.Hkv, kvh, lane);
+      if (wave >= prestaged)
+        stageKvBlock(stage + wave, a.k_pool, a.v_pool, __shfl(my_blk, 2, kWave), a.Hkv, kvh,
+                     lane);
       c_staged = true;
     }
   }
@@ -288,6 +319,24 @@ __device__ __forceinline__ bool decodeAttentionUnit(const DecodeAttnArgs& a, int
     } else {
       qf[0] = zero16();
       qf[1] = zero16();
+    }
+    // The wave holding the newest-token block waits for it now, while q is in flight, and
+    // requests it into the slot the preload left free for it (so its latency overlaps the
+    // wave's other blocks instead of following them).
+    if (kPreload && newest >= first && (newest - first) % stride == 0) {
+      const int64_t kn = (newest - first) / stride;
+      if (kn == 0) {
+        fetch(bufA, newest, 0);
+        a_ready = true;
+      } else if (kn == 1) {
+        fetch(bufB, newest, 1);
+        b_ready = true;
+      } else if (kn == 2 && stage != nullptr) {
+        kv_ready();
+        kv_seen = true;
+        stageKvBlock(stage + wave, a.k_pool, a.v_pool, __shfl(my_blk, 2, kWave), a.Hkv, kvh, lane);
+        c_staged = true;
+      }
     }
     int k = 0;  // ordinal of the wave's block
     for (int64_t i = first; i < n_live; i += 2 * stride, k += 2) {

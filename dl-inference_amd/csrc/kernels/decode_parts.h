@@ -48,17 +48,11 @@ struct KvCacheArgs {
   int64_t max_blocks;
 };
 
-// RMSNorm of x fragments held in registers, every 64-column step of K being in `xb` (lanes of
-// wave w hold steps w, w + kW, ...): x[m, k] <- bf16(x[m, k] * rsqrt(mean_k x[m, k]^2 + eps)
-// * w[k]) (rms_norm/kernel.py:6-14). Row sums of squares are reduced over the 4 lanes of a row
-// and then over the waves through lds (kW * 16 * MB floats) in a fixed order.
-template <int NF, int MB, int kW, int kU>
-__device__ __forceinline__ void normalizeFragments(
-    typename SkinnyCore<NF, MB, kW, kU>::XBatch& xb, const uint16_t* norm_w, int K, float eps,
-    float* lds, int wave, int steps, int r, int g) {
-  FP_EXACT;
-  using Core = SkinnyCore<NF, MB, kW, kU>;
-  U128 wv[kU][2];
+// RMSNorm weights of the 64-column steps a wave holds (see normalizeFragments), requested
+// ahead of x: they do not depend on it.
+template <int kW, int kU>
+__device__ __forceinline__ void loadNormWeights(U128 (&wv)[kU][2], const uint16_t* norm_w,
+                                                int wave, int steps, int g) {
 #pragma unroll
   for (int u = 0; u < kU; ++u) {
     const int s = wave + u * kW;
@@ -67,6 +61,23 @@ __device__ __forceinline__ void normalizeFragments(
     wv[u][0] = load16(norm_w + k0);
     wv[u][1] = load16(norm_w + k0 + 32);
   }
+}
+
+// LDS floats of the RMSNorm row-sum exchange (kept apart from the tile reductions' LDS).
+template <int MB, int kW>
+constexpr int kNormLdsFloats = kW * 16 * MB;
+
+// RMSNorm of x fragments held in registers, every 64-column step of K being in `xb` (lanes of
+// wave w hold steps w, w + kW, ...), with the norm weights wv (loadNormWeights):
+// x[m, k] <- bf16(x[m, k] * rsqrt(mean_k x[m, k]^2 + eps) * w[k]) (rms_norm/kernel.py:6-14).
+// Row sums of squares are reduced over the 4 lanes of a row and then over the waves through
+// norm_lds (kNormLdsFloats<MB, kW> floats, not touched by anything else in between) in a fixed
+// order.
+template <int NF, int MB, int kW, int kU>
+__device__ __forceinline__ void normalizeFragments(
+    typename SkinnyCore<NF, MB, kW, kU>::XBatch& xb, const U128 (&wv)[kU][2], int K, float eps,
+    float* norm_lds, int wave, int steps, int r, int g) {
+  FP_EXACT;
   float sq[MB];
 #pragma unroll
   for (int b = 0; b < MB; ++b) {
@@ -85,7 +96,7 @@ __device__ __forceinline__ void normalizeFragments(
     }
     sq[b] += __shfl_xor(sq[b], 16, kWave);
     sq[b] += __shfl_xor(sq[b], 32, kWave);
-    if (g == 0) lds[wave * Core::kTileM + b * 16 + r] = sq[b];
+    if (g == 0) norm_lds[wave * 16 * MB + b * 16 + r] = sq[b];
   }
   __syncthreads();
   float inv[MB];
@@ -93,10 +104,9 @@ __device__ __forceinline__ void normalizeFragments(
   for (int b = 0; b < MB; ++b) {
     float total = 0.f;
 #pragma unroll
-    for (int v = 0; v < kW; ++v) total += lds[v * Core::kTileM + b * 16 + r];
+    for (int v = 0; v < kW; ++v) total += norm_lds[v * 16 * MB + b * 16 + r];
     inv[b] = 1.0f / sqrtf(total / static_cast<float>(K) + eps);
   }
-  __syncthreads();  // lds is reused by the tile reductions
 #pragma unroll
   for (int u = 0; u < kU; ++u) {
     if (wave + u * kW >= steps) break;
@@ -120,12 +130,14 @@ __device__ __forceinline__ void normalizeFragments(
 // fragments are loaded once (and RMS-normalized with norm_w when it is non-NULL) and stay in
 // registers; the next tile's weights stream in while the current one is multiplied. epi(t)
 // reads the reduced tile [16 NF][16 MB] from lds (row n, column m at lds[n * 16 MB + m]).
-// Requires K / 64 <= kU * kW.
+// lds holds Core::kLdsFloats floats, plus kNormLdsFloats<MB, kW> after them when norm_w is
+// non-NULL. Requires K / 64 <= kU * kW.
 //
-// Load order. With an ungated x (kGated false) x is requested first: loads complete in issue
-// order, so the RMSNorm of x (VALU) overlaps the weight stream instead of waiting behind it.
-// With kGated the first two tiles' weights are requested, then gate() waits until another
-// workgroup has produced x, and x is loaded with Mem. The arithmetic is the same either way.
+// Load order. With an ungated x (kGated false) x and the norm weights are requested first:
+// loads complete in issue order, so the RMSNorm of x (VALU) overlaps the weight stream instead
+// of waiting behind it. With kGated the first two tiles' weights and the norm weights are
+// requested, then gate() waits until another workgroup has produced x, and x is loaded with
+// Mem. The arithmetic is the same either way.
 template <int NF, int MB, int kW, int kU, class Mem = PlainMem, bool kGated = false,
           class Gate = NoWait, typename Epi>
 __device__ __forceinline__ void tileLoop(const uint16_t* w, const XGlobal& xs, int64_t N, int K,
@@ -144,16 +156,22 @@ __device__ __forceinline__ void tileLoop(const uint16_t* w, const XGlobal& xs, i
   if (t >= tiles) return;
   typename Core::WBatch bufA, bufB;
   typename Core::XBatch xb;
-  if (!kGated) Core::template issueX<Mem>(xb, Core::xrows(xs, M, r, g), wave, steps);
+  U128 wv[kU][2];
+  if (!kGated) {
+    Core::template issueX<Mem>(xb, Core::xrows(xs, M, r, g), wave, steps);
+    if (norm_w != nullptr) loadNormWeights<kW, kU>(wv, norm_w, wave, steps, g);
+  }
   Core::issueW(bufA, Core::rows(w, N, K, t * Core::kTileN, r, g), wave, steps);
   if (t + stride < tiles)
     Core::issueW(bufB, Core::rows(w, N, K, (t + stride) * Core::kTileN, r, g), wave, steps);
   if (kGated) {
+    if (norm_w != nullptr) loadNormWeights<kW, kU>(wv, norm_w, wave, steps, g);
     gate();
     Core::template issueX<Mem>(xb, Core::xrows(xs, M, r, g), wave, steps);
   }
+  float* const norm_lds = lds + Core::kLdsFloats;
   if (norm_w != nullptr)
-    normalizeFragments<NF, MB, kW, kU>(xb, norm_w, K, eps, lds, wave, steps, r, g);
+    normalizeFragments<NF, MB, kW, kU>(xb, wv, K, eps, norm_lds, wave, steps, r, g);
   auto tile = [&](const typename Core::WBatch& wb, int64_t tt) {
     f32x4 acc[NF][MB];
     Core::zero(acc);

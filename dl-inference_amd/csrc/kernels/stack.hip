@@ -26,13 +26,15 @@
 //
 // Work placement. q|k|v tiles go to the last qkv_wgs workgroups of the grid (one per q tile,
 // two k/v tiles per workgroup), which have no down_proj unit and reach the stage first;
-// attention units go to the other workgroups; o_proj tiles to the first ones; one gate_up tile
-// per attention workgroup and the rest, in runs, to the q|k|v workgroups (idle through
-// attention, so they request those tiles' weights meanwhile). q and the new k/v are signalled
-// on separate counters: attention needs q at once, but the new k/v only for the block holding
-// the newest token, which its waves reach last. A wave with a third cache block stages it in
-// LDS (direct global-to-LDS loads) next to the two it requests into registers, so nothing
-// streams after the wait.
+// attention units go to the other workgroups; o_proj tiles to the q|k|v workgroups (idle
+// through attention, so they request the o_proj weights meanwhile); gate_up tiles bid,
+// bid + a_wgs, ... to the a_wgs other workgroups; down_proj units to the first ones. q and the
+// new k/v are signalled on separate counters: attention needs q at once, but the new k/v only
+// for the block holding the newest token. A wave with a third cache block stages it in LDS
+// (direct global-to-LDS loads) next to the two it requests into registers, so nothing streams
+// after the wait; waves 0..kEarly-1 stage it during the previous layer, right after their
+// attention unit, so that part of the K/V stream overlaps o_proj, gate_up and down_proj, when
+// the memory system is otherwise lightly loaded.
 //
 // Progress. The grid is at most one workgroup per CU and a workgroup fits a CU on its own, so
 // every workgroup is resident at once, and a stage only waits on earlier stages, which every
@@ -109,15 +111,29 @@ __device__ __forceinline__ T fresh(T v) {
   return v;
 }
 
-// LDS of a workgroup: the stages use it one at a time (each ends with a barrier), so the tile
-// reductions, the attention merge and the staged cache blocks share it.
+// LDS of a workgroup. Waves 0..kEarly-1 of an attention workgroup stage the third cache block
+// of their next-layer unit in kv_early while o_proj, gate_up and down_proj run (those use only
+// the union beside it); the rest of the stages use the union one at a time (each ends with a
+// barrier): the tile reductions and RMSNorm row sums, the attention merge, and the last wave's
+// staged block, which kv[kDecWaves - 1] overlays.
 template <int MB>
 struct StackLds {
   using GuCore = SkinnyCore<2, MB, kNormWaves, kNormUnroll>;
-  union {
-    float gemm[GuCore::kLdsFloats];  // the largest stage tile reduction (gate_up)
+  union Shared {
+    // the largest stage tile reduction (gate_up), then the RMSNorm row sums
+    float gemm[GuCore::kLdsFloats + kNormLdsFloats<MB, kNormWaves>];
     DecodeAttnLds attn;
+  };
+  // as many early slots as fit in 160 KB beside the union (7 up to 32 rows, 5 at 64)
+  static constexpr int kEarlyFit =
+      static_cast<int>((163840 - 256 - sizeof(Shared)) / sizeof(KvBlockLds));
+  static constexpr int kEarly = kEarlyFit < kDecWaves - 1 ? kEarlyFit : kDecWaves - 1;
+  union {
     KvBlockLds kv[kDecWaves];
+    struct {
+      KvBlockLds kv_early[kEarly];
+      Shared u;
+    } p;
   };
   int is_last;
 };
@@ -133,7 +149,7 @@ __device__ void decoderStack(const Args& a) {
                 "lds");
   static_assert(OCore::kLdsFloats <= StackLds<MB>::GuCore::kLdsFloats, "lds");
   __shared__ StackLds<MB> smem;
-  float* lds = smem.gemm;
+  float* lds = smem.p.u.gemm;
 
   const int G = gridDim.x, bid = blockIdx.x;
   const int qkv_tiles = (a.Hq + 2 * a.Hkv) * a.D / 16, o_tiles = a.H / 16;
@@ -143,6 +159,10 @@ __device__ void decoderStack(const Args& a) {
   const int q_tiles = a.Hq * a.D / 16, kv_tiles = qkv_tiles - q_tiles;
   const int qkv_wgs = dli_stack::qkvWorkgroups(q_tiles, kv_tiles, G);  // S1 workgroups
   const int jb = bid - (G - qkv_wgs);  // index among the q|k|v workgroups, < 0 for the others
+  // o_proj tile of this workgroup (then every G-th): jb on the q|k|v workgroups if they cover
+  // the tiles, else bid
+  const int o_first = o_tiles <= qkv_wgs ? (jb >= 0 ? jb : o_tiles) : bid;
+  const bool has_o = o_first < o_tiles;
 
   for (int l = 0; l < a.layers; ++l) {
     const Layer& L = a.layer[l];
@@ -222,7 +242,30 @@ __device__ void decoderStack(const Args& a) {
       if (kv_written > 0) arrive(sync + dli_stack::stageWord(dli_stack::kKvDone), kv_written);
     }
 
-    // S2: attention units.
+    // S2: attention units. A workgroup with one unit per layer stages the third cache blocks of
+    // its next-layer unit (waves 0..kEarly-1) after this one, or after its o_proj tile if it
+    // has one, so that part of the K/V stream runs under o_proj, gate_up and down_proj.
+    const bool early = attn_units <= G && bid < attn_units && !has_o;
+    auto stageNext = [&] {
+      const Layer& N = a.layer[l + 1];
+      const DecodeAttnArgs dn{q,
+                              N.k_pool,
+                              N.v_pool,
+                              N.block_table,
+                              fresh(a.positions),
+                              a.pos64,
+                              0,
+                              nullptr,
+                              nullptr,
+                              nullptr,
+                              nullptr,
+                              a.Hq,
+                              a.Hkv,
+                              a.max_blocks,
+                              splits,
+                              a.scale_log2};
+      stageThirdKvBlocks(dn, bid % splits, bid / splits, smem.kv, StackLds<MB>::kEarly);
+    };
     if (bid < attn_units) {
       const DecodeAttnArgs da{q,
                               L.k_pool,
@@ -242,7 +285,8 @@ __device__ void decoderStack(const Args& a) {
                               a.scale_log2};
       for (int u = bid; u < attn_units; u += G) {
         const bool merged = decodeAttentionUnit<Mem, true>(
-            da, u % splits, u / splits, gen * splits, false, smem.attn, smem.kv,
+            da, u % splits, u / splits, gen * splits, false, smem.p.u.attn, smem.kv,
+            early && l > 0 ? StackLds<MB>::kEarly : 0,
             [&] {
               waitAtLeast(sync + dli_stack::stageWord(dli_stack::kQkvDone), gen * q_tiles,
                           abort_word);
@@ -253,10 +297,12 @@ __device__ void decoderStack(const Args& a) {
             });
         if (merged) arrive(sync + dli_stack::stageWord(dli_stack::kAttnDone), 1);
       }
+      if (early && l + 1 < a.layers) stageNext();
     }
 
-    // S3: o_proj + attention residual.
-    for (int t = bid; t < o_tiles; t += G) {
+    // S3: o_proj + attention residual, on the q|k|v workgroups when they are enough (idle
+    // through attention, so they request the o_proj weights meanwhile).
+    for (int t = o_first; t < o_tiles; t += G) {
       const int H = fresh(a.H), M = fresh(a.M), qd = fresh(a.Hq * a.D);
       const int64_t n0 = static_cast<int64_t>(t) * 16;
       ResidualTile<MB, kResThreads, Mem> rt;
@@ -268,12 +314,17 @@ __device__ void decoderStack(const Args& a) {
       arrive(sync + dli_stack::stageWord(dli_stack::kODone), 1);
     }
 
-    // S4: gate_up + SwiGLU, RMSNorm of h_mid in registers. Tile bid on each workgroup without
-    // q|k|v work; the tiles beyond those in contiguous runs on the q|k|v workgroups, which are
-    // idle through attention and o_proj and request their tiles' weights meanwhile.
-    int gu_first = bid, gu_end = bid + 1;
-    if (jb >= 0) {
-      const int a_wgs = G - qkv_wgs;
+    // S4: gate_up + SwiGLU, RMSNorm of h_mid in registers. When o_proj ran on the q|k|v
+    // workgroups, tiles bid, bid + a_wgs, ... on each of the other a_wgs workgroups (which
+    // request their weights while o_proj runs). Otherwise tile bid on each workgroup without
+    // q|k|v work and the tiles beyond those in contiguous runs on the q|k|v workgroups, which
+    // are idle through attention and o_proj and request their tiles' weights meanwhile.
+    const int a_wgs = G - qkv_wgs;
+    int gu_first = bid, gu_stride = 1, gu_end = bid + 1;
+    if (o_tiles <= qkv_wgs && a_wgs > 0) {
+      gu_stride = a_wgs;
+      gu_end = jb < 0 ? gu_tiles : 0;
+    } else if (jb >= 0) {
       const int rest = gu_tiles > a_wgs ? gu_tiles - a_wgs : 0;
       const int per = (rest + qkv_wgs - 1) / qkv_wgs;
       gu_first = a_wgs + jb * per;
@@ -284,14 +335,14 @@ __device__ void decoderStack(const Args& a) {
       const int H = fresh(a.H), M = fresh(a.M), F = fresh(a.F);
       tileLoop<2, MB, kNormWaves, kNormUnroll, Mem, true>(
           L.w_gate_up, XGlobal{h_mid, H}, 2 * static_cast<int64_t>(F), H, M, lds, L.post_norm,
-          a.eps, gu_first, 1, gu_end,
+          a.eps, gu_first, gu_stride, gu_end,
           [&] {
             waitAtLeast(sync + dli_stack::stageWord(dli_stack::kODone), gen * o_tiles,
                         abort_word);
           },
           [&](int64_t t) { gateUpEpilogue<MB, Mem>(lds, act, M, F, t); });
       arrive(sync + dli_stack::stageWord(dli_stack::kGateUpDone),
-             static_cast<unsigned>(gu_end - gu_first));
+             static_cast<unsigned>((gu_end - gu_first + gu_stride - 1) / gu_stride));
     }
 
     // S5: down_proj + MLP residual. With one split a tile is reduced over the full K; with
