@@ -86,13 +86,18 @@ __device__ __forceinline__ void normalizeFragments(
     for (int u = 0; u < kU; ++u) {
       if (wave + u * kW >= steps) break;
 #pragma unroll
-      for (int h = 0; h < 2; ++h)
+      for (int h = 0; h < 2; ++h) {
+        // x0^2 + x1^2 + sq in one instruction (v_dot2c_f32_bf16; bf16 squares are exact). The
+        // pairs are taken from the whole fragment viewed as 8 bf16: bit-casting one 32-bit
+        // element of the fragment to bf16x2 instead is mis-folded by this compiler (every
+        // element reads element 0).
+        const bf16x8 all = __builtin_bit_cast(bf16x8, xb.x[u][b][h]);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const float lo = bf16ToFloat(static_cast<uint16_t>(xb.x[u][b][h][e]));
-          const float hi = bf16ToFloat(static_cast<uint16_t>(xb.x[u][b][h][e] >> 16));
-          sq[b] += lo * lo + hi * hi;
+          const bf16x2_t v = {all[2 * e], all[2 * e + 1]};
+          sq[b] = __builtin_amdgcn_fdot2_f32_bf16(v, v, sq[b], false);
         }
+      }
     }
     sq[b] += __shfl_xor(sq[b], 16, kWave);
     sq[b] += __shfl_xor(sq[b], 32, kWave);
