@@ -25,6 +25,10 @@ int bad(const std::string& what) {
   return fail(DLI_HIP_EINVAL, "decoder_stack: " + what);
 }
 
+// Stage timeline buffer of the next launches (dli_hip_decoder_stack_trace), NULL when off.
+unsigned long long* g_trace = nullptr;
+int g_trace_layers = 0;
+
 size_t alignUp(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 int tileRows(int64_t m) { return m <= 16 ? 16 : (m <= 32 ? 32 : 64); }
@@ -205,11 +209,14 @@ int dli_hip_decoder_stack(const DliDecoderLayer* layers, int num_layers, const v
   a.down_splits = down_splits;
   a.eps = eps;
   a.scale_log2 = static_cast<float>(1.4426950408889634 / 8.0);  // log2(e) / sqrt(64)
+  a.trace = g_trace;
+  a.trace_layers = g_trace_layers;
   // Layers run in launches of at most kMaxLayers; later launches continue from hidden_out.
   for (int first = 0; first < num_layers; first += dli_stack::kMaxLayers) {
     const int count = num_layers - first < dli_stack::kMaxLayers ? num_layers - first
                                                                   : dli_stack::kMaxLayers;
     a.layers = count;
+    a.trace_base = first;
     a.x_in = static_cast<const uint16_t*>(first == 0 ? hidden_in : hidden_out);
     for (int i = 0; i < dli_stack::kMaxLayers; ++i) {
       dli_stack::Layer& d = a.layer[i];
@@ -231,6 +238,13 @@ int dli_hip_decoder_stack(const DliDecoderLayer* layers, int num_layers, const v
     }
     if (int rc = launch(*kernel, {grid}, {kStackThreads}, 0, stream, a)) return rc;
   }
+  return 0;
+}
+
+int dli_hip_decoder_stack_trace(unsigned long long* trace, int trace_layers) {
+  if (trace != nullptr && trace_layers <= 0) return bad("trace_layers must be positive");
+  g_trace = trace;
+  g_trace_layers = trace != nullptr ? trace_layers : 0;
   return 0;
 }
 

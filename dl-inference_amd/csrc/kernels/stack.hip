@@ -72,17 +72,16 @@ __device__ __forceinline__ void arrive(unsigned* stage, unsigned n) {
                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Polls a stage counter from one wave (lane i < kShards loads shard i) until the shards sum to
-// at least target, the abort word is set, or kSpinLimit polls have passed (which sets the abort
-// word). The loop condition is uniform over the wave.
+// Polls a stage counter from one wave (lane i < kShards loads shard i with an agent-scope
+// vector load) until the shards sum to at least target, the abort word is set, or kSpinLimit
+// polls have passed (which sets the abort word). The loop condition is uniform over the wave.
 __device__ __forceinline__ void pollStage(const unsigned* stage, unsigned target,
                                           unsigned* abort_word) {
   const int lane = freshThreadIdx() % kWave;
   for (int spins = 0;; ++spins) {
     unsigned v = lane < dli_stack::kShards ? loadAgent(stage + lane * dli_stack::kLineWords) : 0u;
-    v += __shfl_xor(v, 1, kWave);
-    v += __shfl_xor(v, 2, kWave);
-    v += __shfl_xor(v, 4, kWave);
+#pragma unroll
+    for (int o = 1; o < dli_stack::kShards; o *= 2) v += __shfl_xor(v, o, kWave);
     if (__builtin_amdgcn_readfirstlane(v) >= target) break;
     if (spins % kAbortPollEvery == 0 &&
         __builtin_amdgcn_readfirstlane(loadAgent(abort_word)) != 0u)
@@ -100,6 +99,15 @@ __device__ __forceinline__ void waitAtLeast(const unsigned* stage, unsigned targ
                                             unsigned* abort_word) {
   if (threadIdx.x < kWave) pollStage(stage, target, abort_word);
   __syncthreads();
+}
+
+// Stage timeline (Args::trace): thread 0 stamps event e of this workgroup in layer l.
+__device__ __forceinline__ void stamp(const Args& a, int l, int e) {
+  unsigned long long* const t = a.trace;
+  if (t == nullptr || a.trace_base + l >= a.trace_layers) return;
+  if (threadIdx.x == 0)
+    t[(static_cast<int64_t>(a.trace_base + l) * gridDim.x + blockIdx.x) * dli_stack::kTraceEvents +
+      e] = __builtin_amdgcn_s_memrealtime();
 }
 
 // Returns v unchanged through an empty asm statement, so the compiler cannot hoist what is
@@ -179,6 +187,7 @@ __device__ void decoderStack(const Args& a) {
         l == 0 ? fresh(a.x_in) : static_cast<const uint16_t*>(slab - a.slab_elems + a.off_h);
     unsigned* const sync = fresh(a.sync);
     unsigned* const abort_word = sync + dli_stack::kAbortWord;
+    stamp(a, l, dli_stack::kTrLayerStart);
 
     // S1: q|k|v tiles of the residual stream the previous layer finished, on the last qkv_wgs
     // workgroups (the ones without down_proj work, which reach this stage first). q tiles come
@@ -220,6 +229,7 @@ __device__ void decoderStack(const Args& a) {
         if (t < q_tiles) {  // q: published at once, attention waits for it
           e.template apply<kQkvQ>(qp, t * 16, lds);
           arrive(sync + dli_stack::stageWord(dli_stack::kQkvDone), 1);
+          stamp(a, l, dli_stack::kTrQPublished);
         } else {  // k/v into the cache: attention needs it only for the newest-token block
           e.template apply<kQkvCache>(qp, t * 16, lds);
           ++kv_written;
@@ -232,6 +242,7 @@ __device__ void decoderStack(const Args& a) {
             if (l > 0)
               waitAtLeast(sync + dli_stack::stageWord(dli_stack::kDownDone), l * down_tiles,
                           abort_word);
+            stamp(a, l, dli_stack::kTrQkvWait);
           },
           [&](int64_t t) {
             if (t == t0)
@@ -239,7 +250,10 @@ __device__ void decoderStack(const Args& a) {
             else
               finish(epi1, t);
           });
-      if (kv_written > 0) arrive(sync + dli_stack::stageWord(dli_stack::kKvDone), kv_written);
+      if (kv_written > 0) {
+        arrive(sync + dli_stack::stageWord(dli_stack::kKvDone), kv_written);
+        stamp(a, l, dli_stack::kTrKvPublished);
+      }
     }
 
     // S2: attention units. A workgroup with one unit per layer stages the third cache blocks of
@@ -290,14 +304,22 @@ __device__ void decoderStack(const Args& a) {
             [&] {
               waitAtLeast(sync + dli_stack::stageWord(dli_stack::kQkvDone), gen * q_tiles,
                           abort_word);
+              stamp(a, l, dli_stack::kTrAttnWait);
             },
             [&] {
               pollStage(sync + dli_stack::stageWord(dli_stack::kKvDone), gen * kv_tiles,
                         abort_word);
             });
-        if (merged) arrive(sync + dli_stack::stageWord(dli_stack::kAttnDone), 1);
+        stamp(a, l, dli_stack::kTrAttnUnit);
+        if (merged) {
+          arrive(sync + dli_stack::stageWord(dli_stack::kAttnDone), 1);
+          stamp(a, l, dli_stack::kTrAttnMerged);
+        }
       }
-      if (early && l + 1 < a.layers) stageNext();
+      if (early && l + 1 < a.layers) {
+        stageNext();
+        stamp(a, l, dli_stack::kTrStagedNext);
+      }
     }
 
     // S3: o_proj + attention residual, on the q|k|v workgroups when they are enough (idle
@@ -308,10 +330,12 @@ __device__ void decoderStack(const Args& a) {
       ResidualTile<MB, kResThreads, Mem> rt;
       OCore::template runGated<Mem>(L.w_o, XGlobal{attn, qd}, H, qd, M, n0, 0, qd / 64, lds, [&] {
         waitAtLeast(sync + dli_stack::stageWord(dli_stack::kAttnDone), gen * pairs, abort_word);
+        stamp(a, l, dli_stack::kTrOWait);
         rt.load(h_prev, nullptr, n0, M, H);
       });
       rt.store(h_mid, n0, M, H, [&](int, int idx) { return lds[idx]; });
       arrive(sync + dli_stack::stageWord(dli_stack::kODone), 1);
+      stamp(a, l, dli_stack::kTrODone);
     }
 
     // S4: gate_up + SwiGLU, RMSNorm of h_mid in registers. When o_proj ran on the q|k|v
@@ -339,10 +363,12 @@ __device__ void decoderStack(const Args& a) {
           [&] {
             waitAtLeast(sync + dli_stack::stageWord(dli_stack::kODone), gen * o_tiles,
                         abort_word);
+            stamp(a, l, dli_stack::kTrGuWait);
           },
           [&](int64_t t) { gateUpEpilogue<MB, Mem>(lds, act, M, F, t); });
       arrive(sync + dli_stack::stageWord(dli_stack::kGateUpDone),
              static_cast<unsigned>((gu_end - gu_first + gu_stride - 1) / gu_stride));
+      stamp(a, l, dli_stack::kTrGuDone);
     }
 
     // S5: down_proj + MLP residual. With one split a tile is reduced over the full K; with
@@ -355,6 +381,7 @@ __device__ void decoderStack(const Args& a) {
       auto gate = [&] {
         waitAtLeast(sync + dli_stack::stageWord(dli_stack::kGateUpDone), gen * gu_tiles,
                     abort_word);
+        stamp(a, l, dli_stack::kTrDownWait);
         rt.load(h_mid, nullptr, n0, M, H);
       };
       if (down_splits == 1) {
@@ -362,6 +389,7 @@ __device__ void decoderStack(const Args& a) {
                                       gate);
         rt.store(h, n0, M, H, [&](int, int idx) { return lds[idx]; });
         arrive(sync + dli_stack::stageWord(dli_stack::kDownDone), 1);
+        stamp(a, l, dli_stack::kTrDownDone);
         continue;
       }
       int sb, se;
@@ -373,6 +401,7 @@ __device__ void decoderStack(const Args& a) {
               split, down_splits, tile_counters + tile, gen * down_splits, false, rt, h, n0, M, H,
               &smem.is_last))
         arrive(sync + dli_stack::stageWord(dli_stack::kDownDone), 1);
+      stamp(a, l, dli_stack::kTrDownDone);
     }
   }
 

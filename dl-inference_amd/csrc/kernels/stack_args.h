@@ -40,9 +40,33 @@ struct Args {
   float* attn_o;          // attention unit partials O
   float* down_part;       // down_proj split-K partial tiles
   unsigned* sync;         // arrival counters (zero before the first launch; left at zero)
+  // Stage timeline, or NULL: stamp (s_memrealtime, 100 MHz) of event e of workgroup w in layer
+  // trace_base + l at trace[((trace_base + l) * grid + w) * kTraceEvents + e] while
+  // trace_base + l < trace_layers.
+  unsigned long long* trace;
+  int trace_base, trace_layers;
   int64_t max_pos, block_size, max_blocks;
   int layers, M, H, Hq, Hkv, D, F, pos64, attn_splits, down_splits;
   float eps, scale_log2;
+};
+
+// Events of the stage timeline (Args::trace), per layer and workgroup; 0 = not reached.
+enum : int {
+  kTrLayerStart = 0,  // the workgroup enters the layer
+  kTrQkvWait,         // S1: the previous layer's h is complete
+  kTrQPublished,      // S1: this workgroup's q tile is published
+  kTrKvPublished,     // S1: this workgroup's k/v tiles are in the cache
+  kTrAttnWait,        // S2: q complete
+  kTrAttnUnit,        // S2: the unit's partial (or output) is written
+  kTrAttnMerged,      // S2: this workgroup merged a pair and published it
+  kTrOWait,           // S3: attention complete
+  kTrODone,           // S3: o_proj tile published
+  kTrGuWait,          // S4: h_mid complete
+  kTrGuDone,          // S4: gate_up tiles published
+  kTrDownWait,        // S5: act complete
+  kTrDownDone,        // S5: down_proj unit done (tile published if it merged)
+  kTrStagedNext,      // early staging of the next layer's cache blocks issued
+  kTraceEvents = 16
 };
 
 // Layout of `sync` in 32-bit words. A stage counter is split into kShards sub-counters, each on
@@ -59,7 +83,8 @@ enum : int {
   kDownDone,     // every down_proj tile (h) written
   kStages
 };
-constexpr int kShards = 8;
+constexpr int kShards = 64;
+static_assert(kShards <= 64 && (kShards & (kShards - 1)) == 0, "one lane per shard");
 constexpr int kLineWords = 64;
 constexpr int stageWord(int stage) { return stage * kShards * kLineWords; }
 constexpr int kExitWord = kStages * kShards * kLineWords;

@@ -333,6 +333,17 @@ int dli_hip_decoder_stack(const DliDecoderLayer* layers, int num_layers, const v
  * free). Equal counts make the two paths bit-identical. splits in [0, 32]. */
 int dli_hip_set_decode_attention_splits(int splits);
 
+/* Stage timeline of the decoder stack (no counterpart in the reference; its profiler exists only
+ * as a design, .codex/profiling_design.md). With trace non-NULL, every later
+ * dli_hip_decoder_stack launch in the process stamps the 100 MHz real-time counter
+ * (s_memrealtime) at the stage boundaries of each workgroup:
+ * trace[(layer * grid + workgroup) * 16 + event] for layer < trace_layers, where grid is the
+ * launch's workgroup count (one per CU) and the events are those of dli_stack::kTr* in
+ * csrc/kernels/stack_args.h (0 = layer entry ... 12 = down_proj done). The buffer holds
+ * trace_layers * grid * 16 uint64 of device memory and must stay valid while such launches run;
+ * events a workgroup does not reach are left as they were. NULL turns it off. */
+int dli_hip_decoder_stack_trace(unsigned long long* trace, int trace_layers);
+
 /* Synchronizes `stream`, then *aborted = 1 when a launch since the last query gave up waiting
  * for another workgroup (its outputs are invalid; this can only happen when the workgroups
  * were not all resident at once), else 0. Clears the flag. */
