@@ -39,14 +39,14 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 // partials, then one activation slab per layer of a launch (q, attn, h_mid, act, h; bf16
 // elements, offsets relative to the slab).
 struct StackLayout {
-  size_t sync, attn_ml, attn_o, down_part, slabs, total;
+  size_t sync, attn_tag, down_tag, slabs, total;
   int64_t slab_elems, off_attn, off_h_mid, off_act, off_h;
 };
 
 StackLayout layoutFor(int64_t m, int64_t hidden, int64_t q_heads, int64_t kv_heads,
                       int64_t head_dim, int64_t ffn, int attn_splits, int down_splits,
                       int num_layers) {
-  const int64_t pairs = m * kv_heads, down_tiles = hidden / 16, rows = m * q_heads;
+  const int64_t down_tiles = hidden / 16, rows = m * q_heads;
   StackLayout l{};
   size_t at = 0;
   auto take = [&](size_t bytes) {
@@ -54,11 +54,11 @@ StackLayout layoutFor(int64_t m, int64_t hidden, int64_t q_heads, int64_t kv_hea
     at += alignUp(bytes, 256);
     return here;
   };
-  l.sync = take(static_cast<size_t>(dli_stack::syncWords(pairs, down_tiles)) * sizeof(unsigned));
-  l.attn_ml = take(static_cast<size_t>(rows) * attn_splits * 2 * sizeof(float));
-  l.attn_o = take(static_cast<size_t>(rows) * attn_splits * head_dim * sizeof(float));
-  l.down_part =
-      take(static_cast<size_t>(down_tiles) * down_splits * 16 * tileRows(m) * sizeof(float));
+  l.sync = take(static_cast<size_t>(dli_stack::syncWords()) * sizeof(unsigned));
+  // tagged words (8 bytes): attention partials O, m, l per (row, split); down_proj partial tiles
+  l.attn_tag = take(static_cast<size_t>(rows) * attn_splits * (head_dim + 2) * sizeof(uint64_t));
+  l.down_tag =
+      take(static_cast<size_t>(down_tiles) * down_splits * 16 * tileRows(m) * sizeof(uint64_t));
   int64_t e = 0;  // slab elements, each part 256-byte aligned (128 bf16)
   auto part = [&](int64_t elems) {
     const int64_t here = e;
@@ -191,9 +191,8 @@ int dli_hip_decoder_stack(const DliDecoderLayer* layers, int num_layers, const v
   a.cos_t = cos_table;
   a.sin_t = sin_table;
   a.positions = positions;
-  a.attn_ml = reinterpret_cast<float*>(ws + lay.attn_ml);
-  a.attn_o = reinterpret_cast<float*>(ws + lay.attn_o);
-  a.down_part = reinterpret_cast<float*>(ws + lay.down_part);
+  a.attn_tag = reinterpret_cast<uint64_t*>(ws + lay.attn_tag);
+  a.down_tag = reinterpret_cast<uint64_t*>(ws + lay.down_tag);
   a.sync = reinterpret_cast<unsigned*>(ws + lay.sync);
   a.max_pos = max_pos;
   a.block_size = block_size;

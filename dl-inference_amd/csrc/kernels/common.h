@@ -21,6 +21,52 @@ struct NoWait {
   __device__ __forceinline__ void operator()() const {}
 };
 
+// Tagged words: an fp32 value and a 32-bit tag in one 8-byte word, written with one agent-scope
+// (single-copy atomic) store. A reader that sees the tag it expects has the value that came with
+// it, without a counter or a store acknowledgement in between. For hand-offs between workgroups
+// that are all resident at once (a persistent launch), each word written by one workgroup per
+// tag value.
+constexpr int kTagSpinLimit = 1 << 20;
+
+__device__ __forceinline__ void storeTagged(uint64_t* p, float v, unsigned tag) {
+  __hip_atomic_store(p, (static_cast<uint64_t>(tag) << 32) | __float_as_uint(v), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// v[i] = the value at p[i] once its tag is `tag`, for i < n (all n loads in flight at once, the
+// set reread until every tag matches). Gives up after kTagSpinLimit rounds, or once *abort_word
+// is non-zero, and then sets *abort_word (the values are then invalid).
+template <int N>
+__device__ __forceinline__ void loadTagged(float (&v)[N], const uint64_t* const (&p)[N], int n,
+                                           unsigned tag, unsigned* abort_word) {
+  for (int spins = 0;; ++spins) {
+    uint64_t w[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+      w[i] = i < n ? __hip_atomic_load(p[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                   : static_cast<uint64_t>(tag) << 32;
+    bool ok = true;
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      ok = ok && static_cast<unsigned>(w[i] >> 32) == tag;
+      v[i] = __uint_as_float(static_cast<unsigned>(w[i]));
+    }
+    if (ok) return;
+    if (spins >= kTagSpinLimit ||
+        (spins % 64 == 63 &&
+         __hip_atomic_load(abort_word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u)) {
+      __hip_atomic_store(abort_word, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+
+// Timeline hook of a stage helper: mark(point) at its internal points (a no-op by default).
+struct NoMark {
+  __device__ __forceinline__ void operator()(int) const {}
+};
+
 // threadIdx.x passed through an empty asm statement. Per-lane offsets computed from it are then
 // recomputed where a long kernel uses them, instead of being computed once at the start and
 // held in registers (or spilled to scratch) across everything in between.
@@ -86,6 +132,29 @@ __device__ __forceinline__ float ld(const T* p) {
 template <typename T>
 __device__ __forceinline__ void st(T* p, float v) {
   Num<T>::store(p, v);
+}
+
+// Reductions over the four 16-lane rows of a wave (lanes l, l ^ 16, l ^ 32, l ^ 48) with the
+// gfx950 permlane swaps (VALU, no LDS round trip). permlaneNN_swap(x, x) yields, in every lane,
+// {x[l & ~NN], x[l | NN]}; every lane then combines the same two operands in the same order,
+// and since IEEE addition and fmax are commutative the results equal the xor-shuffle forms
+// v op v[l ^ 16], then op v[l ^ 32], bit for bit.
+__device__ __forceinline__ float rowsSum(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+__device__ __forceinline__ float rowsMax(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
 __device__ __forceinline__ float waveSum(float v) {

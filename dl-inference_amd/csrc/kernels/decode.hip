@@ -60,7 +60,7 @@ __device__ void linear_residual_impl(const uint16_t* x, const uint16_t* w, const
   ResidualTile<MB, kResThreads, PlainMem> rt;
   rt.load(residual, bias, n0, M, N);  // residual and bias fetched before the weights
   Core::run(w, XGlobal{x, K}, N, K, M, n0, 0, K / 64, lds);
-  rt.store(out, n0, M, N, [&](int, int idx) { return lds[idx]; });
+  rt.store(out, n0, M, N, [&](int e) { return lds[e]; });
 }
 
 // out = residual + bf16(x W^T + b) with K split over grid.y (16 weight rows, 8 waves per

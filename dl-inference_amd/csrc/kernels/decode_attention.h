@@ -14,7 +14,8 @@
 //   S = K Q^T    A = 16 keys x 32 dims (two MFMAs per 64 dims), B = Q^T (16 heads).
 //                The A rows of half hf are keys t0 + 8*(r/4) + 4*hf + r%4, so the output lane
 //                (r, g) holds keys t0 + 8g + 4hf + i (i < 4) of head r: eight consecutive keys.
-//   online softmax per head column (max/sum over the 4 lane groups with xor-shuffles)
+//   online softmax per head column, one maximum per 64-key block over the 4 lane rows
+//                (permlane swaps); each lane keeps its own share of the sum
 //   O^T += V^T P^T  A = V^T (16 dims x 32 keys, dim-major cache blocks give 16-byte runs),
 //                B = P^T straight from the registers above (no LDS round trip).
 // The 8 waves of a unit merge (m, l, O) through LDS; the last unit of a pair to finish merges
@@ -38,11 +39,14 @@ struct KvBlockRegs {
   U128 v[2][4];     // [sub-tile][16-dim group]
 };
 
+// K/V fragments of cache block `blk` (kv head kvh). The loads are unconditional: every cache
+// block a unit reads is live, so all of its 64 positions are in the pool, and positions past the
+// sequence end are masked by attendBlock (scores to -inf, V to zero). Branch-free loads also let
+// the compiler wait for exactly the block it computes next (s_waitcnt vmcnt(n)) instead of for
+// every load in flight.
 __device__ __forceinline__ void loadKvBlock(KvBlockRegs& regs, const uint16_t* k_pool,
-                                            const uint16_t* v_pool, int64_t blk,
-                                            int64_t blk_index, int64_t end, int Hkv, int kvh,
+                                            const uint16_t* v_pool, int64_t blk, int Hkv, int kvh,
                                             int r, int g) {
-  const int64_t t_block = blk_index * kDecBlock;
   const int64_t head_stride = static_cast<int64_t>(kDecBlock) * kDecD;
   const uint16_t* kbase = k_pool + (blk * Hkv + kvh) * head_stride;
   const uint16_t* vbase = v_pool + (blk * Hkv + kvh) * head_stride;
@@ -51,14 +55,12 @@ __device__ __forceinline__ void loadKvBlock(KvBlockRegs& regs, const uint16_t* k
 #pragma unroll
     for (int hf = 0; hf < 2; ++hf) {
       const int off = 32 * st + 8 * (r / 4) + 4 * hf + (r % 4);
-      const bool ok = t_block + off < end;
-      regs.k[st][hf][0] = ok ? load16(kbase + off * kDecD + g * 8) : zero16();
-      regs.k[st][hf][1] = ok ? load16(kbase + off * kDecD + 32 + g * 8) : zero16();
+      regs.k[st][hf][0] = load16(kbase + off * kDecD + g * 8);
+      regs.k[st][hf][1] = load16(kbase + off * kDecD + 32 + g * 8);
     }
-    const bool vok = t_block + 32 * st + 8 * g < end;
 #pragma unroll
     for (int d = 0; d < 4; ++d)
-      regs.v[st][d] = vok ? load16(vbase + (d * 16 + r) * kDecBlock + 32 * st + 8 * g) : zero16();
+      regs.v[st][d] = load16(vbase + (d * 16 + r) * kDecBlock + 32 * st + 8 * g);
   }
 }
 
@@ -85,90 +87,115 @@ __device__ __forceinline__ void stageKvBlock(KvBlockLds* dst, const uint16_t* k_
     __builtin_amdgcn_global_load_lds(vb + j * 512 + lane * 8, dst->v + j * 512, 16, 0, 0);
 }
 
-// loadKvBlock from a block staged in LDS (same fragments, same masking).
-__device__ __forceinline__ void loadKvBlockLds(KvBlockRegs& regs, const KvBlockLds* src,
-                                               int64_t blk_index, int64_t end, int r, int g) {
-  const int64_t t_block = blk_index * kDecBlock;
+// loadKvBlock from a block staged in LDS (same fragments).
+__device__ __forceinline__ void loadKvBlockLds(KvBlockRegs& regs, const KvBlockLds* src, int r,
+                                               int g) {
 #pragma unroll
   for (int st = 0; st < 2; ++st) {
 #pragma unroll
     for (int hf = 0; hf < 2; ++hf) {
       const int off = 32 * st + 8 * (r / 4) + 4 * hf + (r % 4);
-      const bool ok = t_block + off < end;
-      regs.k[st][hf][0] = ok ? load16(src->k + off * kDecD + g * 8) : zero16();
-      regs.k[st][hf][1] = ok ? load16(src->k + off * kDecD + 32 + g * 8) : zero16();
+      regs.k[st][hf][0] = load16(src->k + off * kDecD + g * 8);
+      regs.k[st][hf][1] = load16(src->k + off * kDecD + 32 + g * 8);
     }
-    const bool vok = t_block + 32 * st + 8 * g < end;
 #pragma unroll
     for (int d = 0; d < 4; ++d)
-      regs.v[st][d] = vok ? load16(src->v + (d * 16 + r) * kDecBlock + 32 * st + 8 * g) : zero16();
+      regs.v[st][d] = load16(src->v + (d * 16 + r) * kDecBlock + 32 * st + 8 * g);
   }
 }
 
+// Online-softmax state of one wave: m is the running maximum (log2 domain) of each head
+// column, the same in the four lanes of a column; l is this lane's share of the running sum
+// (the lanes of a column are added once, at the end: rowsSum); o is the unnormalized O^T.
 struct SoftmaxState {
   float m = -INFINITY;
   float l = 0.f;
   f32x4 o[4];
 };
 
+// One 64-key cache block: S for both 32-key sub-tiles first (four independent MFMA chains),
+// then one max over the block's keys, P, and O^T += V^T P^T.
 __device__ __forceinline__ void attendBlock(SoftmaxState& st8, const KvBlockRegs& regs,
                                             const U128 (&qf)[2], int64_t t_block, int64_t end,
                                             int g, float scale_log2) {
   FP_EXACT;
+  f32x4 sc[2][2];
 #pragma unroll
-  for (int st = 0; st < 2; ++st) {
-    const int64_t t0 = t_block + 32 * st;
-    if (t0 >= end) break;  // uniform per wave
-    f32x4 sc[2];
+  for (int st = 0; st < 2; ++st)
 #pragma unroll
     for (int hf = 0; hf < 2; ++hf) {
-      sc[hf] = f32x4{0.f, 0.f, 0.f, 0.f};
-      sc[hf] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(asBf16x8(regs.k[st][hf][0]), asBf16x8(qf[0]), sc[hf], 0, 0, 0);
-      sc[hf] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(asBf16x8(regs.k[st][hf][1]), asBf16x8(qf[1]), sc[hf], 0, 0, 0);
+      sc[st][hf] = f32x4{0.f, 0.f, 0.f, 0.f};
+      sc[st][hf] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(asBf16x8(regs.k[st][hf][0]), asBf16x8(qf[0]), sc[st][hf], 0, 0, 0);
+      sc[st][hf] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(asBf16x8(regs.k[st][hf][1]), asBf16x8(qf[1]), sc[st][hf], 0, 0, 0);
     }
-    float mx = -INFINITY;
+  // keys of the block below end (uniform per wave; >= 1 for a live block)
+  const int64_t rem64 = end - t_block;
+  const int rem = rem64 < kDecBlock ? static_cast<int>(rem64) : kDecBlock;
+  float mx = -INFINITY;
+#pragma unroll
+  for (int st = 0; st < 2; ++st)
 #pragma unroll
     for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int64_t tok = t0 + 8 * g + 4 * hf + e;
-        const float v = tok < end ? sc[hf][e] * scale_log2 : -INFINITY;
-        sc[hf][e] = v;
+        const int key = 32 * st + 8 * g + 4 * hf + e;
+        const float v = (rem == kDecBlock || key < rem) ? sc[st][hf][e] * scale_log2 : -INFINITY;
+        sc[st][hf][e] = v;
         mx = fmaxf(mx, v);
       }
-    mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
-    const float m_new = fmaxf(st8.m, mx);
-    const float alpha = exp2f(st8.m - m_new);
-    float p[2][4];
-    float sum = 0.f;
+  mx = rowsMax(mx);
+  const float m_new = fmaxf(st8.m, mx);
+  const float alpha = exp2f(st8.m - m_new);
+  float p[2][2][4];
+  float sum = 0.f;
+#pragma unroll
+  for (int st = 0; st < 2; ++st)
 #pragma unroll
     for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        p[hf][e] = exp2f(sc[hf][e] - m_new);
-        sum += p[hf][e];
+        p[st][hf][e] = exp2f(sc[st][hf][e] - m_new);
+        sum += p[st][hf][e];
       }
-    sum += __shfl_xor(sum, 16, kWave);
-    sum += __shfl_xor(sum, 32, kWave);
-    st8.l = st8.l * alpha + sum;
-    st8.m = m_new;
+  st8.l = st8.l * alpha + sum;
+  st8.m = m_new;
+#pragma unroll
+  for (int d = 0; d < 4; ++d) st8.o[d] *= alpha;
+#pragma unroll
+  for (int st = 0; st < 2; ++st) {
+    // V rows of keys past the end are zeroed (whole 8-key groups of a lane), so stale pool
+    // contents there never reach O even where P is 0.
+    U128 vf[4];
+#pragma unroll
+    for (int d = 0; d < 4; ++d)
+      vf[d] = (rem == kDecBlock || 32 * st + 8 * g < rem) ? regs.v[st][d] : zero16();
     // P in two bf16 terms (hi + lo) so the P*V products carry ~16 significant bits of P.
     U128 phi, plo;
 #pragma unroll
     for (int w2 = 0; w2 < 4; ++w2) {
-      const float a0 = p[w2 / 2][(w2 % 2) * 2], a1 = p[w2 / 2][(w2 % 2) * 2 + 1];
+      const float a0 = p[st][w2 / 2][(w2 % 2) * 2], a1 = p[st][w2 / 2][(w2 % 2) * 2 + 1];
       phi[w2] = packBf16x2(a0, a1);
       plo[w2] = packBf16x2(a0 - bf16ToFloat(static_cast<uint16_t>(phi[w2])),
                              a1 - bf16ToFloat(static_cast<uint16_t>(phi[w2] >> 16)));
     }
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
-      st8.o[d] *= alpha;
-      st8.o[d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(asBf16x8(regs.v[st][d]), asBf16x8(phi), st8.o[d], 0, 0, 0);
-      st8.o[d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(asBf16x8(regs.v[st][d]), asBf16x8(plo), st8.o[d], 0, 0, 0);
+      st8.o[d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(asBf16x8(vf[d]), asBf16x8(phi), st8.o[d], 0, 0, 0);
+      st8.o[d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(asBf16x8(vf[d]), asBf16x8(plo), st8.o[d], 0, 0, 0);
     }
   }
+}
+
+// Folds split partial (mc, lc, oc) into the running merge (M, l, acc) (splits in order).
+__device__ __forceinline__ void combineSplit(float& M, float& l, float& acc, float mc, float lc,
+                                             float oc) {
+  FP_EXACT;
+  const float m_new = fmaxf(M, mc);
+  const float al = M == -INFINITY ? 0.f : exp2f(M - m_new);
+  const float e = mc == -INFINITY ? 0.f : exp2f(mc - m_new);
+  l = l * al + lc * e;
+  acc = acc * al + oc * e;
+  M = m_new;
 }
 
 struct DecodeAttnArgs {
@@ -187,7 +214,14 @@ struct DecodeAttnArgs {
   int64_t max_blocks;
   int max_splits;
   float scale_log2;  // softmax scale * log2(e)
+  // Tagged partials (persistent launches, every unit resident): [B Hq][max_splits][kTagSlot]
+  // words (O[64], m, l), or NULL for the counter protocol. See decodeAttentionUnit.
+  uint64_t* ws_tag = nullptr;
+  unsigned tag = 0;
+  unsigned* abort_word = nullptr;
 };
+
+constexpr int kTagSlot = kDecD + 2;  // tagged words per (row, split): O, then m and l
 
 // LDS of one unit (kDecWaves waves).
 struct DecodeAttnLds {
@@ -230,6 +264,12 @@ __device__ __forceinline__ void stageThirdKvBlocks(const DecodeAttnArgs& a, int 
 // Returns true in the unit that wrote the pair's output rows. Requires max_blocks <= max_splits
 // * kDecWaves * 64 (a wave keeps its block ids in 64 lanes).
 //
+// With a.ws_tag (every unit of the call resident at once) there is no counter: units of split
+// s > 0 store their partials as tagged words (storeTagged, tag a.tag) and are done; the unit of
+// split 0 merges its own partial with theirs as their words arrive (loadTagged) and writes the
+// output. The merge arithmetic and split order are the same as the counter protocol's, so both
+// give bit-identical outputs.
+//
 // When q and the newest token's k/v are produced by another workgroup of the same launch:
 // gate() (every thread of the workgroup calls it) returns once q is ready, and kv_ready() (one
 // wave calls it) once the cache holds the newest token, which only the block holding position
@@ -240,12 +280,16 @@ __device__ __forceinline__ void stageThirdKvBlocks(const DecodeAttnArgs& a, int 
 // nothing after the wait either; waves below `prestaged` find that block already staged there
 // by stageThirdKvBlocks. The wave holding the newest-token block calls kv_ready() right after
 // gate() and requests that block into the slot left free for it.
-template <class Mem, bool kPreload, class Gate, class KvReady>
+//
+// mark(p) (every thread calls it) marks internal points for a timeline: 0 when this wave's
+// blocks are attended, 1 when every wave's are (after the barrier), 2 after the unit's arrival,
+// 3 and 4 when this wave has attended its first and second block.
+template <class Mem, bool kPreload, class Gate, class KvReady, class Mark = NoMark>
 __device__ __forceinline__ bool decodeAttentionUnit(const DecodeAttnArgs& a, int split, int pair,
                                                     unsigned arrivals, bool reset,
                                                     DecodeAttnLds& s, KvBlockLds* stage,
                                                     int prestaged, Gate&& gate,
-                                                    KvReady&& kv_ready) {
+                                                    KvReady&& kv_ready, Mark mark = Mark{}) {
   FP_EXACT;
   const int tid = freshThreadIdx();
   const int lane = tid % kWave, wave = tid / kWave;
@@ -269,7 +313,8 @@ __device__ __forceinline__ bool decodeAttentionUnit(const DecodeAttnArgs& a, int
       n_live > static_cast<int64_t>(max_splits) * kDecWaves ? max_splits
                                                             : (n_live + kDecWaves - 1) / kDecWaves);
   const bool active = split < n_active;  // uniform per workgroup
-  if (!active && max_splits == 1) {  // empty sequence: zeros
+  const bool tagged = a.ws_tag != nullptr && max_splits > 1;
+  if (!active && (max_splits == 1 || (tagged && split == 0))) {  // empty sequence: zeros
     for (int idx = threadIdx.x; idx < group * kDecD; idx += blockDim.x)
       Mem::storeU16(a.out + (static_cast<int64_t>(b) * a.Hq + kvh * group + idx / kDecD) * kDecD +
                         idx % kDecD,
@@ -288,7 +333,7 @@ __device__ __forceinline__ bool decodeAttentionUnit(const DecodeAttnArgs& a, int
       kv_ready();
       kv_seen = true;
     }
-    loadKvBlock(buf, a.k_pool, a.v_pool, __shfl(my_blk, ordinal, kWave), bi, L, a.Hkv, kvh, r, g);
+    loadKvBlock(buf, a.k_pool, a.v_pool, __shfl(my_blk, ordinal, kWave), a.Hkv, kvh, r, g);
   };
   bool a_ready = false, b_ready = false, c_staged = false;
   if (kPreload && active) {
@@ -345,24 +390,29 @@ __device__ __forceinline__ bool decodeAttentionUnit(const DecodeAttnArgs& a, int
       if (j < n_live && !b_ready) fetch(bufB, j, k + 1);
       a_ready = b_ready = false;
       attendBlock(st8, bufA, qf, i * kDecBlock, L, g, a.scale_log2);
+      if (k == 0) mark(3);
       if (j >= n_live) break;
       const int64_t k2 = j + stride;
       if (k2 < n_live) {
         if (c_staged && k == 0) {
           asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the staged block has landed
-          loadKvBlockLds(bufA, stage + wave, k2, L, r, g);
+          loadKvBlockLds(bufA, stage + wave, r, g);
         } else {
           fetch(bufA, k2, k + 2);
         }
         a_ready = true;
       }
       attendBlock(st8, bufB, qf, j * kDecBlock, L, g, a.scale_log2);
+      if (k == 0) mark(4);
     }
+    mark(0);
     if (stage != nullptr) __syncthreads();  // staged blocks are consumed before s reuses LDS
+    mark(1);
 
+    const float l_col = rowsSum(st8.l);
     if (g == 0) {
       s.sm[wave][r] = st8.m;
-      s.sl[wave][r] = st8.l;
+      s.sl[wave][r] = l_col;
     }
 #pragma unroll
     for (int d = 0; d < 4; ++d)
@@ -386,6 +436,42 @@ __device__ __forceinline__ bool decodeAttentionUnit(const DecodeAttnArgs& a, int
         Mem::storeU16(a.out + row * kDecD + d, floatToBf16(acc / l));
         continue;
       }
+      if (tagged) {
+        if (split != 0) {
+          uint64_t* const mine = a.ws_tag + (row * max_splits + split) * kTagSlot;
+          storeTagged(mine + d, acc, a.tag);
+          if (d == 0) {
+            storeTagged(mine + kDecD, M, a.tag);
+            storeTagged(mine + kDecD + 1, l, a.tag);
+          }
+          continue;
+        }
+        // split 0: own partial first, then splits 1.. in order as their words arrive
+        float Mt = -INFINITY, lt = 0.f, at = 0.f;
+        combineSplit(Mt, lt, at, M, l, acc);
+        constexpr int kChunk = 4;
+        for (int s0 = 1; s0 < n_active; s0 += kChunk) {
+          const uint64_t* ptr[3 * kChunk];
+          const int live = n_active - s0 < kChunk ? n_active - s0 : kChunk;
+#pragma unroll
+          for (int c = 0; c < kChunk; ++c) {
+            const uint64_t* slot =
+                a.ws_tag + (row * max_splits + s0 + (c < live ? c : 0)) * kTagSlot;
+            ptr[c] = slot + kDecD;
+            ptr[kChunk + c] = slot + kDecD + 1;
+            ptr[2 * kChunk + c] = slot + d;
+          }
+          float v[3 * kChunk];
+          // the words of the first `live` splits of each kind: ptr is laid out kind-major, so
+          // every index below 3 * kChunk is loaded (dead chunk slots repeat a live split)
+          loadTagged<3 * kChunk>(v, ptr, 3 * kChunk, a.tag, a.abort_word);
+#pragma unroll
+          for (int c = 0; c < kChunk; ++c)
+            if (c < live) combineSplit(Mt, lt, at, v[c], v[kChunk + c], v[2 * kChunk + c]);
+        }
+        Mem::storeU16(a.out + row * kDecD + d, floatToBf16(at / lt));
+        continue;
+      }
       const int64_t slot = row * max_splits + split;
       if (d == 0) {
         __hip_atomic_store(a.ws_ml + slot * 2, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -395,6 +481,7 @@ __device__ __forceinline__ bool decodeAttentionUnit(const DecodeAttnArgs& a, int
     }
   }
   if (max_splits == 1) return true;
+  if (tagged) return split == 0;
 
   // Arrive: every partial store of this workgroup has completed before the counter moves.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -407,6 +494,7 @@ __device__ __forceinline__ bool decodeAttentionUnit(const DecodeAttnArgs& a, int
       __hip_atomic_store(a.counters + pair, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   __syncthreads();
+  mark(2);
   if (!s.is_last) return false;
 
   // Merge the splits that hold keys (the rest wrote nothing this call), in split order. The
@@ -434,12 +522,7 @@ __device__ __forceinline__ bool decodeAttentionUnit(const DecodeAttnArgs& a, int
 #pragma unroll
       for (int c = 0; c < kCombineChunk; ++c) {
         if (s0 + c >= n) break;
-        const float m_new = fmaxf(M, ms[c]);
-        const float al = M == -INFINITY ? 0.f : exp2f(M - m_new);
-        const float e = ms[c] == -INFINITY ? 0.f : exp2f(ms[c] - m_new);
-        l = l * al + ls[c] * e;
-        acc = acc * al + os[c] * e;
-        M = m_new;
+        combineSplit(M, l, acc, ms[c], ls[c], os[c]);
       }
     }
     Mem::storeU16(a.out + row * kDecD + d, n > 0 ? floatToBf16(acc / l) : uint16_t{0});  // no keys: zeros

@@ -99,8 +99,7 @@ __device__ __forceinline__ void normalizeFragments(
         }
       }
     }
-    sq[b] += __shfl_xor(sq[b], 16, kWave);
-    sq[b] += __shfl_xor(sq[b], 32, kWave);
+    sq[b] = rowsSum(sq[b]);
     if (g == 0) norm_lds[wave * 16 * MB + b * 16 + r] = sq[b];
   }
   __syncthreads();
@@ -143,12 +142,15 @@ __device__ __forceinline__ void normalizeFragments(
 // of waiting behind it. With kGated the first two tiles' weights and the norm weights are
 // requested, then gate() waits until another workgroup has produced x, and x is loaded with
 // Mem. The arithmetic is the same either way.
+//
+// mark(p) (every thread calls it) marks points for a timeline: 0 once x is loaded (and
+// normalized), 1 when the first tile is reduced.
 template <int NF, int MB, int kW, int kU, class Mem = PlainMem, bool kGated = false,
-          class Gate = NoWait, typename Epi>
+          class Gate = NoWait, typename Epi, class Mark = NoMark>
 __device__ __forceinline__ void tileLoop(const uint16_t* w, const XGlobal& xs, int64_t N, int K,
                                          int M, float* lds, const uint16_t* norm_w, float eps,
                                          int64_t t_first, int64_t t_stride, int64_t t_end,
-                                         Gate&& gate, Epi&& epi) {
+                                         Gate&& gate, Epi&& epi, Mark mark = Mark{}) {
   using Core = SkinnyCore<NF, MB, kW, kU>;
   const int lane = freshThreadIdx() % kWave;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -177,11 +179,13 @@ __device__ __forceinline__ void tileLoop(const uint16_t* w, const XGlobal& xs, i
   float* const norm_lds = lds + Core::kLdsFloats;
   if (norm_w != nullptr)
     normalizeFragments<NF, MB, kW, kU>(xb, wv, K, eps, norm_lds, wave, steps, r, g);
+  mark(0);
   auto tile = [&](const typename Core::WBatch& wb, int64_t tt) {
     f32x4 acc[NF][MB];
     Core::zero(acc);
     Core::compute(acc, wb, xb, wave, steps);
     Core::reduce(acc, lds, r, g, wave);
+    if (tt == t_first) mark(1);
     epi(tt);
     __syncthreads();  // lds is reused by the next tile
   };
@@ -336,39 +340,67 @@ __device__ __forceinline__ void gateUpEpilogue(const float* lds, uint16_t* out, 
 
 // out[m, n] = bf16(residual[m, n] + bf16(y[n][m] + b[n])) for the tile at weight row n0, with
 // kThreadsT threads; load() fetches the residual (and bias) so they can be requested early.
+// Thread item (m, half) owns the 8 consecutive outputs n0 + 8 half, ..., + 7 of row m, so a row
+// segment is read and written with one 16-byte access when N is a multiple of 8 and the
+// pointers are 16-byte aligned (element by element otherwise); the values are the same either
+// way.
 template <int MB, int kThreadsT, class Mem>
 struct ResidualTile {
   static constexpr int kTileN = 16;
   static constexpr int kTileM = 16 * MB;
   static constexpr int kElems = kTileN * kTileM;
-  static constexpr int kItems = (kElems + kThreadsT - 1) / kThreadsT;
-  float res[kItems], bv[kItems];
+  static constexpr int kItems = 2 * kTileM;
+  static_assert(kItems <= kThreadsT, "one item per thread");
+  float res[8], bv[8];
+
+  __device__ __forceinline__ static bool vectorOk(const void* p, int64_t N) {
+    return N % 8 == 0 && (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
+  }
 
   __device__ __forceinline__ void load(const uint16_t* residual, const uint16_t* bias, int64_t n0,
                                        int M, int64_t N) {
+    const int idx = threadIdx.x;
+    const int m = idx / 2;
+    const int64_t n = n0 + 8 * (idx % 2);
+    const bool live = idx < kItems && m < M;
+    if (live && n + 8 <= N && vectorOk(residual, N)) {
+      const U128 r = Mem::load16(residual + m * N + n);
 #pragma unroll
-    for (int it = 0; it < kItems; ++it) {
-      const int idx = threadIdx.x + it * kThreadsT;
-      const int nl = idx / kTileM, m = idx % kTileM;
-      const int64_t n = n0 + nl;
-      const bool live = idx < kElems && m < M && n < N;
-      res[it] = live ? bf16ToFloat(Mem::loadU16(residual + m * N + n)) : 0.f;
-      bv[it] = live && bias != nullptr ? bf16ToFloat(bias[n]) : 0.f;
+      for (int e = 0; e < 4; ++e) {
+        res[2 * e] = bf16ToFloat(static_cast<uint16_t>(r[e]));
+        res[2 * e + 1] = bf16ToFloat(static_cast<uint16_t>(r[e] >> 16));
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        res[j] = live && n + j < N ? bf16ToFloat(Mem::loadU16(residual + m * N + n + j)) : 0.f;
     }
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      bv[j] = live && bias != nullptr && n + j < N ? bf16ToFloat(bias[n + j]) : 0.f;
   }
 
-  // y(idx) returns the fp32 GEMM result of item idx (row nl = idx / kTileM, column m).
+  // y(e) returns the fp32 GEMM result of tile element e = nl * kTileM + m (row nl, column m).
   template <class Y>
   __device__ __forceinline__ void store(uint16_t* out, int64_t n0, int M, int64_t N, Y&& y) const {
     FP_EXACT;
+    const int idx = threadIdx.x;
+    const int m = idx / 2, half = idx % 2;
+    const int64_t n = n0 + 8 * half;
+    if (idx >= kItems || m >= M) return;
+    float v[8];
 #pragma unroll
-    for (int it = 0; it < kItems; ++it) {
-      const int idx = threadIdx.x + it * kThreadsT;
-      const int nl = idx / kTileM, m = idx % kTileM;
-      const int64_t n = n0 + nl;
-      if (idx >= kElems || m >= M || n >= N) continue;
-      Mem::storeU16(out + m * N + n, floatToBf16(res[it] + roundBf16(y(it, idx) + bv[it])));
+    for (int j = 0; j < 8; ++j) v[j] = res[j] + roundBf16(y((8 * half + j) * kTileM + m) + bv[j]);
+    if (n + 8 <= N && vectorOk(out, N)) {
+      U128 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = packBf16x2(v[2 * e], v[2 * e + 1]);
+      Mem::store16(out + m * N + n, o);
+      return;
     }
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (n + j < N) Mem::storeU16(out + m * N + n + j, floatToBf16(v[j]));
   }
 };
 
@@ -402,24 +434,56 @@ __device__ __forceinline__ bool splitKArrive(const float* lds, float* partials, 
   }
   __syncthreads();
   if (!*is_last) return false;
-  constexpr int kItems = ResidualTile<MB, kThreadsT, Mem>::kItems;
-  float sum[kItems];
-#pragma unroll
-  for (int it = 0; it < kItems; ++it) {
-    const int idx = threadIdx.x + it * kThreadsT;
+  // The sums replace this workgroup's own partial in lds (every thread has stored it above).
+  float* const sums = const_cast<float*>(lds);
+  for (int idx = threadIdx.x; idx < kElems; idx += kThreadsT) {
     float part[kMaxSplits];
 #pragma unroll
     for (int sp = 0; sp < kMaxSplits; ++sp)
-      part[sp] = (idx < kElems && sp < splits)
-                     ? __hip_atomic_load(partials + sp * kElems + idx, __ATOMIC_RELAXED,
-                                         __HIP_MEMORY_SCOPE_AGENT)
-                     : 0.f;
+      part[sp] = sp < splits ? __hip_atomic_load(partials + sp * kElems + idx, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT)
+                             : 0.f;
     float y = part[0];
 #pragma unroll
     for (int sp = 1; sp < kMaxSplits; ++sp) y += part[sp];  // split order; absent = +0
-    sum[it] = y;
+    sums[idx] = y;
   }
-  rt.store(out, n0, M, N, [&](int it, int) { return sum[it]; });
+  __syncthreads();
+  rt.store(out, n0, M, N, [&](int e) { return sums[e]; });
+  return true;
+}
+
+// Split-K tail for a persistent launch (every workgroup resident at once), no counter: split
+// s > 0 stores its reduced partial (lds) as tagged words (storeTagged) and returns false; split 0
+// adds the other splits' words to its own partial in split order as they arrive (loadTagged),
+// writes out = residual + bf16(sum + b) through rt and returns true. The sums are those of
+// splitKArrive, bit for bit. partials: this tile's [splits][16 x 16 MB] tagged words.
+template <int MB, int kThreadsT, class Mem>
+__device__ __forceinline__ bool splitKTagged(float* lds, uint64_t* partials, int split,
+                                             int splits, unsigned tag, unsigned* abort_word,
+                                             const ResidualTile<MB, kThreadsT, Mem>& rt,
+                                             uint16_t* out, int64_t n0, int M, int64_t N) {
+  FP_EXACT;
+  constexpr int kElems = 16 * 16 * MB;
+  if (split != 0) {
+    for (int idx = threadIdx.x; idx < kElems; idx += kThreadsT)
+      storeTagged(partials + static_cast<int64_t>(split) * kElems + idx, lds[idx], tag);
+    return false;
+  }
+  for (int idx = threadIdx.x; idx < kElems; idx += kThreadsT) {
+    const uint64_t* ptr[kMaxSplits - 1];
+#pragma unroll
+    for (int sp = 1; sp < kMaxSplits; ++sp)
+      ptr[sp - 1] = partials + static_cast<int64_t>(sp < splits ? sp : 0) * kElems + idx;
+    float part[kMaxSplits - 1];
+    loadTagged<kMaxSplits - 1>(part, ptr, splits - 1, tag, abort_word);
+    float y = lds[idx];
+#pragma unroll
+    for (int sp = 1; sp < kMaxSplits; ++sp) y += sp < splits ? part[sp - 1] : 0.f;  // split order
+    lds[idx] = y;
+  }
+  __syncthreads();
+  rt.store(out, n0, M, N, [&](int e) { return lds[e]; });
   return true;
 }
 

@@ -55,6 +55,9 @@ struct PlainMem {
   __device__ __forceinline__ static uint16_t loadU16(const uint16_t* p) { return *p; }
   __device__ __forceinline__ static void storeU16(uint16_t* p, uint16_t v) { *p = v; }
   __device__ __forceinline__ static void storeU32(uint32_t* p, uint32_t v) { *p = v; }
+  __device__ __forceinline__ static void store16(void* p, U128 v) {
+    *reinterpret_cast<U128*>(p) = v;
+  }
 };
 
 struct WriteThroughMem {
@@ -67,6 +70,11 @@ struct WriteThroughMem {
   }
   __device__ __forceinline__ static void storeU32(uint32_t* p, uint32_t v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  // 16 bytes with the same cache policy the agent-scope stores above get (sc1: written through
+  // to the coherent memory side). The caller's s_waitcnt vmcnt(0) covers it like any store.
+  __device__ __forceinline__ static void store16(void* p, U128 v) {
+    asm volatile("global_store_dwordx4 %0, %1, off sc1" : : "v"(p), "v"(v) : "memory");
   }
 };
 
@@ -222,11 +230,12 @@ struct SkinnyCore {
   // batches are requested, then gate() (called by every thread) waits until x is ready, and only
   // then are the x batches loaded (with Mem). The batches are accumulated in the order run()
   // uses, so both give bit-identical tiles.
-  template <class Mem, class Gate>
+  // mark(0) (every thread calls it) marks the point where the tile is reduced.
+  template <class Mem, class Gate, class Mark = NoMark>
   __device__ __forceinline__ static void runGated(const uint16_t* __restrict__ w, const XGlobal& xs,
                                                   int64_t N, int64_t K, int M, int64_t n0,
                                                   int step_begin, int step_end, float* lds,
-                                                  Gate&& gate) {
+                                                  Gate&& gate, Mark mark = Mark{}) {
     const int lane = freshThreadIdx() % kWave;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int r = lane % 16, g = lane / 16;
@@ -260,6 +269,7 @@ struct SkinnyCore {
       }
     }
     reduce(acc, lds, r, g, wave);
+    mark(0);
   }
 
   // Partial tiles -> LDS [wave][n][m], then a fixed-order sum over waves into lds[0..tile).

@@ -8,7 +8,7 @@
 //   S2 attn    decode attention units (pair = (sequence, kv head), split)    (decode_attention.h)
 //   S3 o       h_mid = h + attn W_o^T                                         (16-row tiles)
 //   S4 gate_up act = bf16(silu(gate)) * up of RMSNorm(h_mid)                  (32-row tiles)
-//   S5 down    h = h_mid + act W_down^T, split-K, last arriver merges        (16-row tiles)
+//   S5 down    h = h_mid + act W_down^T, split-K, split 0 merges             (16-row tiles)
 //
 // Every tile is computed with the same code and order as the one-stage kernels, so the stack
 // and the five-launch path give bit-identical results.
@@ -101,13 +101,26 @@ __device__ __forceinline__ void waitAtLeast(const unsigned* stage, unsigned targ
   __syncthreads();
 }
 
-// Stage timeline (Args::trace): thread 0 stamps event e of this workgroup in layer l.
-__device__ __forceinline__ void stamp(const Args& a, int l, int e) {
+// Stage timeline (Args::trace). Thread 0 keeps the stamps of the current layer in LDS (a
+// global store would count against the wave's vmcnt and delay a later s_waitcnt) and writes
+// them out when the workgroup enters the next layer and at the end: flushStamps.
+__device__ __forceinline__ void stamp(const Args& a, int l, int e, unsigned long long* lds) {
+  if (a.trace == nullptr || a.trace_base + l >= a.trace_layers) return;
+  if (threadIdx.x == 0) lds[e] = __builtin_amdgcn_s_memrealtime();
+}
+
+__device__ __forceinline__ void flushStamps(const Args& a, int l, unsigned long long* lds) {
   unsigned long long* const t = a.trace;
   if (t == nullptr || a.trace_base + l >= a.trace_layers) return;
-  if (threadIdx.x == 0)
-    t[(static_cast<int64_t>(a.trace_base + l) * gridDim.x + blockIdx.x) * dli_stack::kTraceEvents +
-      e] = __builtin_amdgcn_s_memrealtime();
+  if (threadIdx.x == 0) {
+    unsigned long long* const row =
+        t + (static_cast<int64_t>(a.trace_base + l) * gridDim.x + blockIdx.x) *
+                dli_stack::kTraceEvents;
+    for (int e = 0; e < dli_stack::kTraceEvents; ++e) {
+      row[e] = lds[e];
+      lds[e] = 0;
+    }
+  }
 }
 
 // Returns v unchanged through an empty asm statement, so the compiler cannot hoist what is
@@ -144,6 +157,7 @@ struct StackLds {
     } p;
   };
   int is_last;
+  unsigned long long trace[dli_stack::kTraceEvents];  // stamps of the current layer
 };
 
 template <int MB>
@@ -172,9 +186,15 @@ __device__ void decoderStack(const Args& a) {
   const int o_first = o_tiles <= qkv_wgs ? (jb >= 0 ? jb : o_tiles) : bid;
   const bool has_o = o_first < o_tiles;
 
+  if (threadIdx.x == 0)
+    for (int e = 0; e < dli_stack::kTraceEvents; ++e) smem.trace[e] = 0;
+  // launch epoch (advanced only by the last workgroup out, after every workgroup has read it)
+  const unsigned epoch = __builtin_amdgcn_readfirstlane(loadAgent(a.sync + dli_stack::kEpochWord));
   for (int l = 0; l < a.layers; ++l) {
+    if (l > 0) flushStamps(a, l - 1, smem.trace);
     const Layer& L = a.layer[l];
     const unsigned gen = static_cast<unsigned>(l + 1);
+    const unsigned tag = dli_stack::partialTag(epoch, l);
     // This layer's activation slab and the residual stream entering it. Every pointer and size
     // below passes through fresh() so that no address is computed once for all layers.
     uint16_t* const slab = fresh(a.slabs) + l * fresh(a.slab_elems);
@@ -187,7 +207,7 @@ __device__ void decoderStack(const Args& a) {
         l == 0 ? fresh(a.x_in) : static_cast<const uint16_t*>(slab - a.slab_elems + a.off_h);
     unsigned* const sync = fresh(a.sync);
     unsigned* const abort_word = sync + dli_stack::kAbortWord;
-    stamp(a, l, dli_stack::kTrLayerStart);
+    stamp(a, l, dli_stack::kTrLayerStart, smem.trace);
 
     // S1: q|k|v tiles of the residual stream the previous layer finished, on the last qkv_wgs
     // workgroups (the ones without down_proj work, which reach this stage first). q tiles come
@@ -229,7 +249,7 @@ __device__ void decoderStack(const Args& a) {
         if (t < q_tiles) {  // q: published at once, attention waits for it
           e.template apply<kQkvQ>(qp, t * 16, lds);
           arrive(sync + dli_stack::stageWord(dli_stack::kQkvDone), 1);
-          stamp(a, l, dli_stack::kTrQPublished);
+          stamp(a, l, dli_stack::kTrQPublished, smem.trace);
         } else {  // k/v into the cache: attention needs it only for the newest-token block
           e.template apply<kQkvCache>(qp, t * 16, lds);
           ++kv_written;
@@ -242,17 +262,18 @@ __device__ void decoderStack(const Args& a) {
             if (l > 0)
               waitAtLeast(sync + dli_stack::stageWord(dli_stack::kDownDone), l * down_tiles,
                           abort_word);
-            stamp(a, l, dli_stack::kTrQkvWait);
+            stamp(a, l, dli_stack::kTrQkvWait, smem.trace);
           },
           [&](int64_t t) {
             if (t == t0)
               finish(epi0, t);
             else
               finish(epi1, t);
-          });
+          },
+          [&](int p) { stamp(a, l, dli_stack::kTrQkvNorm + p, smem.trace); });
       if (kv_written > 0) {
         arrive(sync + dli_stack::stageWord(dli_stack::kKvDone), kv_written);
-        stamp(a, l, dli_stack::kTrKvPublished);
+        stamp(a, l, dli_stack::kTrKvPublished, smem.trace);
       }
     }
 
@@ -281,6 +302,7 @@ __device__ void decoderStack(const Args& a) {
       stageThirdKvBlocks(dn, bid % splits, bid / splits, smem.kv, StackLds<MB>::kEarly);
     };
     if (bid < attn_units) {
+      // split partials as tagged words: split 0 merges as they arrive, no pair counter
       const DecodeAttnArgs da{q,
                               L.k_pool,
                               L.v_pool,
@@ -288,15 +310,18 @@ __device__ void decoderStack(const Args& a) {
                               fresh(a.positions),
                               a.pos64,
                               0,
-                              fresh(a.attn_ml),
-                              fresh(a.attn_o),
-                              sync + dli_stack::kPairCountersAt,
+                              nullptr,
+                              nullptr,
+                              nullptr,
                               attn,
                               a.Hq,
                               a.Hkv,
                               a.max_blocks,
                               splits,
-                              a.scale_log2};
+                              a.scale_log2,
+                              fresh(a.attn_tag),
+                              tag,
+                              abort_word};
       for (int u = bid; u < attn_units; u += G) {
         const bool merged = decodeAttentionUnit<Mem, true>(
             da, u % splits, u / splits, gen * splits, false, smem.p.u.attn, smem.kv,
@@ -304,21 +329,22 @@ __device__ void decoderStack(const Args& a) {
             [&] {
               waitAtLeast(sync + dli_stack::stageWord(dli_stack::kQkvDone), gen * q_tiles,
                           abort_word);
-              stamp(a, l, dli_stack::kTrAttnWait);
+              stamp(a, l, dli_stack::kTrAttnWait, smem.trace);
             },
             [&] {
               pollStage(sync + dli_stack::stageWord(dli_stack::kKvDone), gen * kv_tiles,
                         abort_word);
-            });
-        stamp(a, l, dli_stack::kTrAttnUnit);
+            },
+            [&](int point) { stamp(a, l, dli_stack::kTrAttnWave0 + point, smem.trace); });
+        stamp(a, l, dli_stack::kTrAttnUnit, smem.trace);
         if (merged) {
           arrive(sync + dli_stack::stageWord(dli_stack::kAttnDone), 1);
-          stamp(a, l, dli_stack::kTrAttnMerged);
+          stamp(a, l, dli_stack::kTrAttnMerged, smem.trace);
         }
       }
       if (early && l + 1 < a.layers) {
         stageNext();
-        stamp(a, l, dli_stack::kTrStagedNext);
+        stamp(a, l, dli_stack::kTrStagedNext, smem.trace);
       }
     }
 
@@ -330,12 +356,12 @@ __device__ void decoderStack(const Args& a) {
       ResidualTile<MB, kResThreads, Mem> rt;
       OCore::template runGated<Mem>(L.w_o, XGlobal{attn, qd}, H, qd, M, n0, 0, qd / 64, lds, [&] {
         waitAtLeast(sync + dli_stack::stageWord(dli_stack::kAttnDone), gen * pairs, abort_word);
-        stamp(a, l, dli_stack::kTrOWait);
+        stamp(a, l, dli_stack::kTrOWait, smem.trace);
         rt.load(h_prev, nullptr, n0, M, H);
       });
-      rt.store(h_mid, n0, M, H, [&](int, int idx) { return lds[idx]; });
+      rt.store(h_mid, n0, M, H, [&](int e) { return lds[e]; });
       arrive(sync + dli_stack::stageWord(dli_stack::kODone), 1);
-      stamp(a, l, dli_stack::kTrODone);
+      stamp(a, l, dli_stack::kTrODone, smem.trace);
     }
 
     // S4: gate_up + SwiGLU, RMSNorm of h_mid in registers. When o_proj ran on the q|k|v
@@ -363,12 +389,13 @@ __device__ void decoderStack(const Args& a) {
           [&] {
             waitAtLeast(sync + dli_stack::stageWord(dli_stack::kODone), gen * o_tiles,
                         abort_word);
-            stamp(a, l, dli_stack::kTrGuWait);
+            stamp(a, l, dli_stack::kTrGuWait, smem.trace);
           },
-          [&](int64_t t) { gateUpEpilogue<MB, Mem>(lds, act, M, F, t); });
+          [&](int64_t t) { gateUpEpilogue<MB, Mem>(lds, act, M, F, t); },
+          [&](int p) { stamp(a, l, dli_stack::kTrGuNorm + p, smem.trace); });
       arrive(sync + dli_stack::stageWord(dli_stack::kGateUpDone),
              static_cast<unsigned>((gu_end - gu_first + gu_stride - 1) / gu_stride));
-      stamp(a, l, dli_stack::kTrGuDone);
+      stamp(a, l, dli_stack::kTrGuDone, smem.trace);
     }
 
     // S5: down_proj + MLP residual. With one split a tile is reduced over the full K; with
@@ -381,33 +408,37 @@ __device__ void decoderStack(const Args& a) {
       auto gate = [&] {
         waitAtLeast(sync + dli_stack::stageWord(dli_stack::kGateUpDone), gen * gu_tiles,
                     abort_word);
-        stamp(a, l, dli_stack::kTrDownWait);
+        stamp(a, l, dli_stack::kTrDownWait, smem.trace);
         rt.load(h_mid, nullptr, n0, M, H);
       };
       if (down_splits == 1) {
         OCore::template runGated<Mem>(L.w_down, XGlobal{act, F}, H, F, M, n0, 0, F / 64, lds,
-                                      gate);
-        rt.store(h, n0, M, H, [&](int, int idx) { return lds[idx]; });
+                                      gate, [&](int) {
+                                        stamp(a, l, dli_stack::kTrDownReduced, smem.trace);
+                                      });
+        rt.store(h, n0, M, H, [&](int e) { return lds[e]; });
         arrive(sync + dli_stack::stageWord(dli_stack::kDownDone), 1);
-        stamp(a, l, dli_stack::kTrDownDone);
+        stamp(a, l, dli_stack::kTrDownDone, smem.trace);
         continue;
       }
       int sb, se;
       splitRange(F / 64, split, down_splits, sb, se);
-      DownCore::template runGated<Mem>(L.w_down, XGlobal{act, F}, H, F, M, n0, sb, se, lds, gate);
-      unsigned* const tile_counters = sync + dli_stack::kPairCountersAt + pairs;
-      if (splitKArrive<MB, kResThreads, Mem>(
-              lds, fresh(a.down_part) + static_cast<int64_t>(tile) * down_splits * kTileElems,
-              split, down_splits, tile_counters + tile, gen * down_splits, false, rt, h, n0, M, H,
-              &smem.is_last))
+      DownCore::template runGated<Mem>(
+          L.w_down, XGlobal{act, F}, H, F, M, n0, sb, se, lds, gate,
+          [&](int) { stamp(a, l, dli_stack::kTrDownReduced, smem.trace); });
+      if (splitKTagged<MB, kResThreads, Mem>(
+              lds, fresh(a.down_tag) + static_cast<int64_t>(tile) * down_splits * kTileElems,
+              split, down_splits, tag, abort_word, rt, h, n0, M, H))
         arrive(sync + dli_stack::stageWord(dli_stack::kDownDone), 1);
-      stamp(a, l, dli_stack::kTrDownDone);
+      stamp(a, l, dli_stack::kTrDownDone, smem.trace);
     }
   }
 
-  // Leave: the last workgroup out resets every counter but the abort word.
+  flushStamps(a, a.layers - 1, smem.trace);
+
+  // Leave: the last workgroup out resets every counter but the abort word and advances the
+  // epoch.
   unsigned* const sync = a.sync;
-  unsigned* const pair_counters = sync + dli_stack::kPairCountersAt;
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   if (threadIdx.x == 0) {
@@ -420,10 +451,11 @@ __device__ void decoderStack(const Args& a) {
   for (int i = threadIdx.x; i < dli_stack::kStages * dli_stack::kShards; i += blockDim.x)
     __hip_atomic_store(sync + i * dli_stack::kLineWords, 0u, __ATOMIC_RELAXED,
                        __HIP_MEMORY_SCOPE_AGENT);
-  if (threadIdx.x == 0)
+  if (threadIdx.x == 0) {
     __hip_atomic_store(sync + dli_stack::kExitWord, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  for (int i = threadIdx.x; i < pairs + down_tiles; i += blockDim.x)
-    __hip_atomic_store(pair_counters + i, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(sync + dli_stack::kEpochWord, epoch + 1u, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+  }
 }
 
 }  // namespace

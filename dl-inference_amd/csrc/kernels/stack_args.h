@@ -36,9 +36,8 @@ struct Args {
   const float* cos_t;  // [max_pos, D / 2]
   const float* sin_t;
   const void* positions;  // [M] int32/int64: slot of each row's new token
-  float* attn_ml;         // attention unit partials (m, l)
-  float* attn_o;          // attention unit partials O
-  float* down_part;       // down_proj split-K partial tiles
+  uint64_t* attn_tag;     // attention unit partials, tagged words [M Hq][splits][O, m, l]
+  uint64_t* down_tag;     // down_proj split partial tiles, tagged words [tiles][splits][tile]
   unsigned* sync;         // arrival counters (zero before the first launch; left at zero)
   // Stage timeline, or NULL: stamp (s_memrealtime, 100 MHz) of event e of workgroup w in layer
   // trace_base + l at trace[((trace_base + l) * grid + w) * kTraceEvents + e] while
@@ -66,14 +65,25 @@ enum : int {
   kTrDownWait,        // S5: act complete
   kTrDownDone,        // S5: down_proj unit done (tile published if it merged)
   kTrStagedNext,      // early staging of the next layer's cache blocks issued
-  kTraceEvents = 16
+  kTrAttnWave0,       // S2: wave 0 has attended its cache blocks
+  kTrAttnWaves,       // S2: every wave has attended its cache blocks
+  kTrAttnArrived,     // S2: the unit's partial is stored and counted
+  kTrAttnBlock1,      // S2: wave 0 has attended its first cache block
+  kTrAttnBlock2,      // S2: wave 0 has attended its second cache block
+  kTrQkvNorm,         // S1: x loaded and normalized
+  kTrQkvReduced,      // S1: first tile reduced
+  kTrGuNorm,          // S4: h_mid loaded and normalized
+  kTrGuReduced,       // S4: first tile reduced
+  kTrDownReduced,     // S5: tile (or split partial) reduced
+  kTraceEvents = 24
 };
 
 // Layout of `sync` in 32-bit words. A stage counter is split into kShards sub-counters, each on
-// its own 256-byte line: a workgroup adds to sub-counter blockIdx.x % kShards (about one per
-// XCD), so arrivals do not all serialize on one address, and a waiting workgroup sums the
-// shards. Then the exit counter and the abort word (own lines), then one arrival counter per
-// attention pair (b, kv head) and per down_proj output tile.
+// its own 256-byte line: a workgroup adds to sub-counter blockIdx.x % kShards, so arrivals do
+// not all serialize on one address, and a waiting workgroup sums the shards. Then the exit
+// counter, the abort word and the launch epoch (own lines). The epoch, read by every workgroup
+// at the start and advanced by the last one out, goes into the tags of the tagged partials, so
+// a word left by an earlier launch or layer never carries the tag a reader expects.
 enum : int {
   kQkvDone = 0,  // every q tile written
   kKvDone,       // every k/v tile written into the cache
@@ -89,7 +99,13 @@ constexpr int kLineWords = 64;
 constexpr int stageWord(int stage) { return stage * kShards * kLineWords; }
 constexpr int kExitWord = kStages * kShards * kLineWords;
 constexpr int kAbortWord = kExitWord + kLineWords;
-constexpr int kPairCountersAt = kAbortWord + kLineWords;
+constexpr int kEpochWord = kAbortWord + kLineWords;
+
+// Tag of the tagged partials of layer l (l < 256) in the launch of `epoch`; never 0, the value
+// of a zero-filled workspace.
+constexpr unsigned partialTag(unsigned epoch, int l) {
+  return ((epoch & 0xFFFFFFu) << 8) | static_cast<unsigned>(l + 1);
+}
 
 // Workgroups of the q|k|v stage (the last ones of the grid): one per q tile plus one per two k/v
 // tiles when the grid has room for that and at least as many others, else two tiles of any kind
@@ -99,8 +115,6 @@ constexpr int qkvWorkgroups(int q_tiles, int kv_tiles, int grid) {
                                                     : (q_tiles + kv_tiles + 1) / 2;
 }
 
-inline int64_t syncWords(int64_t pairs, int64_t down_tiles) {
-  return kPairCountersAt + pairs + down_tiles;
-}
+inline int64_t syncWords() { return kEpochWord + 1; }
 
 }  // namespace dli_stack

@@ -337,10 +337,10 @@ int dli_hip_set_decode_attention_splits(int splits);
  * as a design, .codex/profiling_design.md). With trace non-NULL, every later
  * dli_hip_decoder_stack launch in the process stamps the 100 MHz real-time counter
  * (s_memrealtime) at the stage boundaries of each workgroup:
- * trace[(layer * grid + workgroup) * 16 + event] for layer < trace_layers, where grid is the
+ * trace[(layer * grid + workgroup) * 24 + event] for layer < trace_layers, where grid is the
  * launch's workgroup count (one per CU) and the events are those of dli_stack::kTr* in
  * csrc/kernels/stack_args.h (0 = layer entry ... 12 = down_proj done). The buffer holds
- * trace_layers * grid * 16 uint64 of device memory and must stay valid while such launches run;
+ * trace_layers * grid * 24 uint64 of device memory and must stay valid while such launches run;
  * events a workgroup does not reach are left as they were. NULL turns it off. */
 int dli_hip_decoder_stack_trace(unsigned long long* trace, int trace_layers);
 
