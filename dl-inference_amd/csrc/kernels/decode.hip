@@ -100,7 +100,7 @@ __device__ void linear_partial_impl(const uint16_t* x, const uint16_t* w, float*
   splitRange(K / 64, blockIdx.y, splits, sb, se);
   Core::run(w, XGlobal{x, K}, N, K, M, n0, sb, se, lds);
   float* dst = partials + static_cast<int64_t>(blockIdx.y) * M * N;
-  for (int idx = threadIdx.x; idx < Core::kTileN * Core::kTileM; idx += blockDim.x) {
+  for (int idx = threadIdx.x; idx < Core::kTileN * Core::kTileM; idx += kThreads) {
     const int nl = idx % Core::kTileN, m = idx / Core::kTileN;  // n fastest: coalesced stores
     const int64_t n = n0 + nl;
     if (m < M && n < N) dst[m * N + n] = lds[nl * Core::kTileM + m];
@@ -177,7 +177,7 @@ __device__ void lm_head_argmax_impl(const uint16_t* xn, const uint16_t* w, void*
                              gridDim.x, INT64_MAX, NoWait{}, [&](int64_t t) {
     const int64_t n0 = t * Core::kTileN;
     if (logits != nullptr) {
-      for (int idx = threadIdx.x; idx < Core::kTileN * Core::kTileM; idx += blockDim.x) {
+      for (int idx = threadIdx.x; idx < Core::kTileN * Core::kTileM; idx += kThreads) {
         const int nl = idx % Core::kTileN, m = idx / Core::kTileN;  // n fastest: coalesced stores
         const int64_t n = n0 + nl;
         if (m >= M || n >= V) continue;
@@ -191,7 +191,7 @@ __device__ void lm_head_argmax_impl(const uint16_t* xn, const uint16_t* w, void*
     // argmax: thread (m, q) scans rows 4q..4q+3 of the tile, then one thread per m merges the
     // quarters in order (first index among equal maxima).
     float* qv = lds + Core::kTileN * Core::kTileM;
-    for (int idx = threadIdx.x; idx < kLmQuarters * Core::kTileM; idx += blockDim.x) {
+    for (int idx = threadIdx.x; idx < kLmQuarters * Core::kTileM; idx += kThreads) {
       const int m = idx % Core::kTileM, q = idx / Core::kTileM;
       float best = -INFINITY;
       int arg = -1;
@@ -208,7 +208,7 @@ __device__ void lm_head_argmax_impl(const uint16_t* xn, const uint16_t* w, void*
       lds_arg[q * Core::kTileM + m] = arg;
     }
     __syncthreads();
-    for (int m = threadIdx.x; m < M; m += blockDim.x) {
+    for (int m = threadIdx.x; m < M; m += kThreads) {
       float best = -INFINITY;
       int arg = -1;
       for (int q = 0; q < kLmQuarters; ++q) {
@@ -237,12 +237,12 @@ __device__ void argmax_finalize_impl(const float* part_val, const int32_t* part_
   float best = -INFINITY;
   int32_t arg = 0x7fffffff;
   constexpr int kBatch = 8;  // loads of kBatch partials in flight per thread
-  for (int t0 = threadIdx.x; t0 < tiles; t0 += kBatch * blockDim.x) {
+  for (int t0 = threadIdx.x; t0 < tiles; t0 += kBatch * kThreads) {
     float v[kBatch];
     int32_t ix[kBatch];
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
-      const int t = t0 + u * blockDim.x;
+      const int t = t0 + u * kThreads;
       v[u] = t < tiles ? vals[t] : -INFINITY;
       ix[u] = t < tiles ? idxs[t] : 0x7fffffff;
     }
@@ -305,7 +305,7 @@ __device__ void argmax_finalize_impl(const float* part_val, const int32_t* part_
     linear_residual_splitk_impl<MB>(x, w, bias, residual, out, M, N, K, splits, partials,         \
                                     counters);                                                    \
   }                                                                                               \
-  extern "C" __global__ void __launch_bounds__(kThreads) linear_partial_m##MB(                    \
+  extern "C" __global__ void __launch_bounds__(kThreads, 2) linear_partial_m##MB(                 \
       const uint16_t* x, const uint16_t* w, float* partials, int M, int64_t N, int K,             \
       int splits) {                                                                               \
     linear_partial_impl<MB>(x, w, partials, M, N, K, splits);                                     \
@@ -315,7 +315,7 @@ __device__ void argmax_finalize_impl(const float* part_val, const int32_t* part_
       int M, int64_t F, int K) {                                                                  \
     gate_up_silu_impl<MB>(x, norm_w, eps, w_gu, out, M, F, K);                                    \
   }                                                                                               \
-  extern "C" __global__ void __launch_bounds__(kThreads) lm_head_argmax_m##MB(                    \
+  extern "C" __global__ void __launch_bounds__(kThreads, 2) lm_head_argmax_m##MB(                  \
       const uint16_t* xn, const uint16_t* w, void* logits, int logits_f32, float* part_val,       \
       int32_t* part_idx, int M, int64_t V, int K) {                                               \
     lm_head_argmax_impl<MB>(xn, w, logits, logits_f32, part_val, part_idx, M, V, K);              \

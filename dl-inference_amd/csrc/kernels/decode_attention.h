@@ -315,7 +315,7 @@ __device__ __forceinline__ bool decodeAttentionUnit(const DecodeAttnArgs& a, int
   const bool active = split < n_active;  // uniform per workgroup
   const bool tagged = a.ws_tag != nullptr && max_splits > 1;
   if (!active && (max_splits == 1 || (tagged && split == 0))) {  // empty sequence: zeros
-    for (int idx = threadIdx.x; idx < group * kDecD; idx += blockDim.x)
+    for (int idx = threadIdx.x; idx < group * kDecD; idx += kDecThreads)
       Mem::storeU16(a.out + (static_cast<int64_t>(b) * a.Hq + kvh * group + idx / kDecD) * kDecD +
                         idx % kDecD,
                     uint16_t{0});
@@ -419,7 +419,7 @@ __device__ __forceinline__ bool decodeAttentionUnit(const DecodeAttnArgs& a, int
 #pragma unroll
       for (int e = 0; e < 4; ++e) s.so[wave][d * 16 + 4 * g + e][r] = st8.o[d][e];
     __syncthreads();
-    for (int idx = threadIdx.x; idx < group * kDecD; idx += blockDim.x) {
+    for (int idx = threadIdx.x; idx < group * kDecD; idx += kDecThreads) {
       const int hl = idx / kDecD, d = idx % kDecD;
       float M = -INFINITY;
 #pragma unroll
@@ -502,7 +502,7 @@ __device__ __forceinline__ bool decodeAttentionUnit(const DecodeAttnArgs& a, int
   // memory round trips overlap.
   constexpr int kCombineChunk = 8;
   const int n = n_active;
-  for (int idx = threadIdx.x; idx < group * kDecD; idx += blockDim.x) {
+  for (int idx = threadIdx.x; idx < group * kDecD; idx += kDecThreads) {
     const int hl = idx / kDecD, d = idx % kDecD;
     const int64_t row = static_cast<int64_t>(b) * a.Hq + kvh * group + hl;
     float M = -INFINITY, l = 0.f, acc = 0.f;

@@ -325,7 +325,7 @@ __device__ __forceinline__ void gateUpEpilogue(const float* lds, uint16_t* out, 
   FP_EXACT;
   constexpr int kTileM = 16 * MB;
   const int64_t f0 = t * 16;
-  for (int idx = threadIdx.x; idx < 16 * kTileM; idx += blockDim.x) {
+  for (int idx = threadIdx.x; idx < 16 * kTileM; idx += kNormThreads) {
     const int j = idx % 16, m = idx / 16;
     const int64_t f = f0 + j;
     if (m >= M || f >= F) continue;
@@ -420,7 +420,7 @@ __device__ __forceinline__ bool splitKArrive(const float* lds, float* partials, 
                                              int* is_last) {
   FP_EXACT;
   constexpr int kElems = 16 * 16 * MB;
-  for (int idx = threadIdx.x; idx < kElems; idx += blockDim.x)
+  for (int idx = threadIdx.x; idx < kElems; idx += kThreadsT)
     __hip_atomic_store(partials + static_cast<int64_t>(split) * kElems + idx, lds[idx],
                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");

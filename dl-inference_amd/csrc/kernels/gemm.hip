@@ -97,7 +97,7 @@ __device__ void skinny_linear_impl(const uint16_t* x, const uint16_t* w, const u
   __shared__ float lds[Core::kLdsFloats];
   const int64_t n0 = static_cast<int64_t>(blockIdx.x) * Core::kTileN;
   Core::run(w, XGlobal{x, K}, N, K, static_cast<int>(M), n0, 0, static_cast<int>(K / 64), lds);
-  for (int idx = threadIdx.x; idx < Core::kTileN * Core::kTileM; idx += blockDim.x) {
+  for (int idx = threadIdx.x; idx < Core::kTileN * Core::kTileM; idx += 4 * kWave) {
     const int nl = idx / Core::kTileM, m = idx % Core::kTileM;
     const int64_t n = n0 + nl;
     if (m >= M || n >= N) continue;

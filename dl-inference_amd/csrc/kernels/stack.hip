@@ -448,7 +448,7 @@ __device__ void decoderStack(const Args& a) {
   }
   __syncthreads();
   if (!smem.is_last) return;
-  for (int i = threadIdx.x; i < dli_stack::kStages * dli_stack::kShards; i += blockDim.x)
+  for (int i = threadIdx.x; i < dli_stack::kStages * dli_stack::kShards; i += kStackThreads)
     __hip_atomic_store(sync + i * dli_stack::kLineWords, 0u, __ATOMIC_RELAXED,
                        __HIP_MEMORY_SCOPE_AGENT);
   if (threadIdx.x == 0) {
