@@ -21,6 +21,20 @@ struct NoWait {
   __device__ __forceinline__ void operator()() const {}
 };
 
+// Global-memory view of a pointer into device memory. Accesses through it compile to global_*
+// instructions; through a generic pointer whose origin the compiler cannot trace (a pointer that
+// passed through an asm statement, a select, a struct) they become flat_* instructions, which
+// also count against lgkmcnt and so merge their waits with those of LDS operations.
+#define DK_GLOBAL __attribute__((address_space(1)))
+template <typename T>
+__device__ __forceinline__ DK_GLOBAL T* gp(T* p) {
+  return (DK_GLOBAL T*)p;
+}
+template <typename T>
+__device__ __forceinline__ const DK_GLOBAL T* gp(const T* p) {
+  return (const DK_GLOBAL T*)p;
+}
+
 // Tagged words: an fp32 value and a 32-bit tag in one 8-byte word, written with one agent-scope
 // (single-copy atomic) store. A reader that sees the tag it expects has the value that came with
 // it, without a counter or a store acknowledgement in between. For hand-offs between workgroups
@@ -29,8 +43,8 @@ struct NoWait {
 constexpr int kTagSpinLimit = 1 << 20;
 
 __device__ __forceinline__ void storeTagged(uint64_t* p, float v, unsigned tag) {
-  __hip_atomic_store(p, (static_cast<uint64_t>(tag) << 32) | __float_as_uint(v), __ATOMIC_RELAXED,
-                     __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(gp(p), (static_cast<uint64_t>(tag) << 32) | __float_as_uint(v),
+                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // v[i] = the value at p[i] once its tag is `tag`, for i < n (all n loads in flight at once, the
@@ -43,7 +57,7 @@ __device__ __forceinline__ void loadTagged(float (&v)[N], const uint64_t* const 
     uint64_t w[N];
 #pragma unroll
     for (int i = 0; i < N; ++i)
-      w[i] = i < n ? __hip_atomic_load(p[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+      w[i] = i < n ? __hip_atomic_load(gp(p[i]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
                    : static_cast<uint64_t>(tag) << 32;
     bool ok = true;
 #pragma unroll
@@ -54,8 +68,8 @@ __device__ __forceinline__ void loadTagged(float (&v)[N], const uint64_t* const 
     if (ok) return;
     if (spins >= kTagSpinLimit ||
         (spins % 64 == 63 &&
-         __hip_atomic_load(abort_word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u)) {
-      __hip_atomic_store(abort_word, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+         __hip_atomic_load(gp(abort_word), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u)) {
+      __hip_atomic_store(gp(abort_word), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       return;
     }
     __builtin_amdgcn_s_sleep(1);
@@ -197,7 +211,8 @@ __device__ __forceinline__ float blockMax(float v, float* scratch) {
 }
 
 __device__ __forceinline__ int64_t loadIndex(const void* p, int is64, int64_t i) {
-  return is64 ? static_cast<const int64_t*>(p)[i] : static_cast<int64_t>(static_cast<const int32_t*>(p)[i]);
+  return is64 ? gp(static_cast<const int64_t*>(p))[i]
+              : static_cast<int64_t>(gp(static_cast<const int32_t*>(p))[i]);
 }
 
 }  // namespace dk

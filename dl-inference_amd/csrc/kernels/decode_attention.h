@@ -55,12 +55,12 @@ __device__ __forceinline__ void loadKvBlock(KvBlockRegs& regs, const uint16_t* k
 #pragma unroll
     for (int hf = 0; hf < 2; ++hf) {
       const int off = 32 * st + 8 * (r / 4) + 4 * hf + (r % 4);
-      regs.k[st][hf][0] = load16(kbase + off * kDecD + g * 8);
-      regs.k[st][hf][1] = load16(kbase + off * kDecD + 32 + g * 8);
+      regs.k[st][hf][0] = gload16(kbase + off * kDecD + g * 8);
+      regs.k[st][hf][1] = gload16(kbase + off * kDecD + 32 + g * 8);
     }
 #pragma unroll
     for (int d = 0; d < 4; ++d)
-      regs.v[st][d] = load16(vbase + (d * 16 + r) * kDecBlock + 32 * st + 8 * g);
+      regs.v[st][d] = gload16(vbase + (d * 16 + r) * kDecBlock + 32 * st + 8 * g);
   }
 }
 
@@ -232,7 +232,7 @@ struct DecodeAttnLds {
 };
 
 // Stages in stage[w], for each wave w < waves of unit `split` of pair `pair`, the third cache
-// block decodeAttentionUnit would stage at its start (never the newest-token block), so that a
+// block decodeAttentionUnit would stage at its start, so that a
 // later call with prestaged = waves on the same positions, block table and pools finds it there
 // and streams less after its gate. Loads complete in issue order: the caller issues this where
 // nothing latency-critical of the same waves follows soon.
@@ -247,16 +247,19 @@ __device__ __forceinline__ void stageThirdKvBlocks(const DecodeAttnArgs& a, int 
   const int64_t past_b = a.positions != nullptr ? loadIndex(a.positions, a.pos64, b) : a.past;
   int64_t L = past_b + 1;
   if (L > a.max_blocks * kDecBlock) L = a.max_blocks * kDecBlock;
-  const int64_t n_live = L > 0 ? (L + kDecBlock - 1) / kDecBlock : 0;
-  if (third >= n_live || third == n_live - 1) return;
-  const int32_t blk = a.block_table[static_cast<int64_t>(b) * a.max_blocks + third];
+  const int64_t L_old = L > 0 ? L - 1 : 0;  // the blocks hold keys [0, L - 1)
+  const int64_t n_live = (L_old + kDecBlock - 1) / kDecBlock;
+  if (third >= n_live) return;
+  const int32_t blk = gp(a.block_table)[static_cast<int64_t>(b) * a.max_blocks + third];
   stageKvBlock(stage + wave, a.k_pool, a.v_pool, blk, a.Hkv, kvh, lane);
 }
 
-// One unit: split `split` of pair (b, kvh) = `pair`. The live cache blocks of a pair are dealt
-// round-robin over the splits x kDecWaves waves of its units: wave w of split s takes blocks
-// s * kDecWaves + w, + splits * kDecWaves, ..., so every wave streams the same number of blocks
-// whatever the sequence length. With one split the normalized output is written directly.
+// One unit: split `split` of pair (b, kvh) = `pair`. The cache blocks holding keys
+// [0, positions[b]) are dealt round-robin over the splits x kDecWaves waves of its units: wave w
+// of split s takes blocks s * kDecWaves + w, + splits * kDecWaves, ..., so every wave streams the
+// same number of blocks whatever the sequence length; the newest key, positions[b], is attended
+// as a one-key block by the next wave in that order, after its blocks. With one split the
+// normalized output is written directly.
 // Otherwise each unit stores its (m, l, O) partial with agent-scope stores and arrives at
 // counters[pair]; the unit whose arrival brings the counter to `arrivals` reads every partial
 // with agent-scope loads and merges them in split order (no cross-workgroup fence), resetting
@@ -264,22 +267,21 @@ __device__ __forceinline__ void stageThirdKvBlocks(const DecodeAttnArgs& a, int 
 // Returns true in the unit that wrote the pair's output rows. Requires max_blocks <= max_splits
 // * kDecWaves * 64 (a wave keeps its block ids in 64 lanes).
 //
-// With a.ws_tag (every unit of the call resident at once) there is no counter: units of split
-// s > 0 store their partials as tagged words (storeTagged, tag a.tag) and are done; the unit of
-// split 0 merges its own partial with theirs as their words arrive (loadTagged) and writes the
-// output. The merge arithmetic and split order are the same as the counter protocol's, so both
-// give bit-identical outputs.
+// With a.ws_tag (every unit of the call resident at once) there is no counter: every active
+// unit but the last stores its partial as tagged words (storeTagged, tag a.tag) and is done; the
+// last active unit, which holds the fewest blocks, merges the others' partials as their words
+// arrive (loadTagged) with its own and writes the output. The merge arithmetic and split order
+// are the same as the counter protocol's, so both give bit-identical outputs.
 //
 // When q and the newest token's k/v are produced by another workgroup of the same launch:
-// gate() (every thread of the workgroup calls it) returns once q is ready, and kv_ready() (one
-// wave calls it) once the cache holds the newest token, which only the block holding position
-// positions[b] needs. With kPreload each wave requests its first two cache blocks before gate()
-// (except the newest-token block), so the K/V stream overlaps the wait. The arithmetic does not
-// depend on these choices. With `stage` (kDecWaves blocks of LDS, which may overlap `s`) each
-// wave also stages its third block in LDS before gate(), so a wave with three blocks streams
-// nothing after the wait either; waves below `prestaged` find that block already staged there
-// by stageThirdKvBlocks. The wave holding the newest-token block calls kv_ready() right after
-// gate() and requests that block into the slot left free for it.
+// gate() (every thread of the workgroup calls it) returns once q is ready, and kv_ready() (the
+// wave that attends the newest key calls it, after its blocks) once the cache holds the newest
+// token; that wave reads the token with agent-scope loads. Every cache block a unit reads was
+// complete before the call, so with kPreload each wave requests its first two blocks before
+// gate() and the K/V stream overlaps the wait. The arithmetic does not depend on these choices.
+// With `stage` (kDecWaves blocks of LDS, which may overlap `s`) each wave also stages its third
+// block in LDS before gate(), so a wave with three blocks streams nothing after the wait either;
+// waves below `prestaged` find that block already staged there by stageThirdKvBlocks.
 //
 // mark(p) (every thread calls it) marks internal points for a timeline: 0 when this wave's
 // blocks are attended, 1 when every wave's are (after the barrier), 2 after the unit's arrival,
@@ -303,18 +305,27 @@ __device__ __forceinline__ bool decodeAttentionUnit(const DecodeAttnArgs& a, int
   // one block id per lane (lane k holds the id of the wave's k-th block).
   const int32_t* table = a.block_table + static_cast<int64_t>(b) * a.max_blocks;
   const int64_t my_blk_index = first + static_cast<int64_t>(lane) * stride;
-  const int32_t my_blk = my_blk_index < a.max_blocks ? table[my_blk_index] : 0;
+  const int32_t my_blk = my_blk_index < a.max_blocks ? gp(table)[my_blk_index] : 0;
   const int64_t past_b = a.positions != nullptr ? loadIndex(a.positions, a.pos64, b) : a.past;
   int64_t L = past_b + 1;
   if (L > a.max_blocks * kDecBlock) L = a.max_blocks * kDecBlock;
-  const int64_t n_live = L > 0 ? (L + kDecBlock - 1) / kDecBlock : 0;
-  // splits holding at least one block (split s holds block s * kDecWaves first)
+  // Keys [0, L - 1) come from cache blocks that were complete before this call; the newest key
+  // L - 1 (written by this step) is attended on its own by the wave next in the round-robin
+  // after the last block (newest_wave, which holds no more blocks than any other wave), after
+  // its blocks and once kv_ready() has returned.
+  const int64_t L_old = L > 0 ? L - 1 : 0;
+  const int64_t n_live = (L_old + kDecBlock - 1) / kDecBlock;
+  const int64_t newest_wave = L > 0 ? n_live % stride : -1;
+  // splits holding a block or the newest key (split s holds block s * kDecWaves first)
   const int n_active = static_cast<int>(
-      n_live > static_cast<int64_t>(max_splits) * kDecWaves ? max_splits
-                                                            : (n_live + kDecWaves - 1) / kDecWaves);
+      L <= 0 ? 0
+             : (n_live >= stride ? max_splits : n_live / kDecWaves + 1));
   const bool active = split < n_active;  // uniform per workgroup
   const bool tagged = a.ws_tag != nullptr && max_splits > 1;
-  if (!active && (max_splits == 1 || (tagged && split == 0))) {  // empty sequence: zeros
+  // the unit that writes the output in the tagged protocol: the last active split, which holds
+  // the fewest blocks
+  const int merger = n_active > 0 ? n_active - 1 : 0;
+  if (!active && (max_splits == 1 || (tagged && split == merger))) {  // empty sequence: zeros
     for (int idx = threadIdx.x; idx < group * kDecD; idx += kDecThreads)
       Mem::storeU16(a.out + (static_cast<int64_t>(b) * a.Hq + kvh * group + idx / kDecD) * kDecD +
                         idx % kDecD,
@@ -326,27 +337,20 @@ __device__ __forceinline__ bool decodeAttentionUnit(const DecodeAttnArgs& a, int
 #pragma unroll
   for (int d = 0; d < 4; ++d) st8.o[d] = f32x4{0.f, 0.f, 0.f, 0.f};
   KvBlockRegs bufA, bufB;
-  const int64_t newest = n_live - 1;  // the block holding position L - 1
-  bool kv_seen = false;  // kv_ready() has returned in this wave
-  auto fetch = [&](KvBlockRegs& buf, int64_t bi, int ordinal) {
-    if (bi == newest && !kv_seen) {
-      kv_ready();
-      kv_seen = true;
-    }
+  auto fetch = [&](KvBlockRegs& buf, int ordinal) {
     loadKvBlock(buf, a.k_pool, a.v_pool, __shfl(my_blk, ordinal, kWave), a.Hkv, kvh, r, g);
   };
   bool a_ready = false, b_ready = false, c_staged = false;
   if (kPreload && active) {
-    if (first < n_live && first != newest) {
-      fetch(bufA, first, 0);
+    if (first < n_live) {
+      fetch(bufA, 0);
       a_ready = true;
     }
-    if (first + stride < n_live && first + stride != newest) {
-      fetch(bufB, first + stride, 1);
+    if (first + stride < n_live) {
+      fetch(bufB, 1);
       b_ready = true;
     }
-    const int64_t third = first + 2 * stride;
-    if (stage != nullptr && third < n_live && third != newest) {
+    if (stage != nullptr && first + 2 * stride < n_live) {
       if (wave >= prestaged)
         stageKvBlock(stage + wave, a.k_pool, a.v_pool, __shfl(my_blk, 2, kWave), a.Hkv, kvh,
                      lane);
@@ -365,31 +369,13 @@ __device__ __forceinline__ bool decodeAttentionUnit(const DecodeAttnArgs& a, int
       qf[0] = zero16();
       qf[1] = zero16();
     }
-    // The wave holding the newest-token block waits for it now, while q is in flight, and
-    // requests it into the slot the preload left free for it (so its latency overlaps the
-    // wave's other blocks instead of following them).
-    if (kPreload && newest >= first && (newest - first) % stride == 0) {
-      const int64_t kn = (newest - first) / stride;
-      if (kn == 0) {
-        fetch(bufA, newest, 0);
-        a_ready = true;
-      } else if (kn == 1) {
-        fetch(bufB, newest, 1);
-        b_ready = true;
-      } else if (kn == 2 && stage != nullptr) {
-        kv_ready();
-        kv_seen = true;
-        stageKvBlock(stage + wave, a.k_pool, a.v_pool, __shfl(my_blk, 2, kWave), a.Hkv, kvh, lane);
-        c_staged = true;
-      }
-    }
     int k = 0;  // ordinal of the wave's block
     for (int64_t i = first; i < n_live; i += 2 * stride, k += 2) {
-      if (!a_ready) fetch(bufA, i, k);
+      if (!a_ready) fetch(bufA, k);
       const int64_t j = i + stride;
-      if (j < n_live && !b_ready) fetch(bufB, j, k + 1);
+      if (j < n_live && !b_ready) fetch(bufB, k + 1);
       a_ready = b_ready = false;
-      attendBlock(st8, bufA, qf, i * kDecBlock, L, g, a.scale_log2);
+      attendBlock(st8, bufA, qf, i * kDecBlock, L_old, g, a.scale_log2);
       if (k == 0) mark(3);
       if (j >= n_live) break;
       const int64_t k2 = j + stride;
@@ -398,12 +384,52 @@ __device__ __forceinline__ bool decodeAttentionUnit(const DecodeAttnArgs& a, int
           asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the staged block has landed
           loadKvBlockLds(bufA, stage + wave, r, g);
         } else {
-          fetch(bufA, k2, k + 2);
+          fetch(bufA, k + 2);
         }
         a_ready = true;
       }
-      attendBlock(st8, bufB, qf, j * kDecBlock, L, g, a.scale_log2);
+      attendBlock(st8, bufB, qf, j * kDecBlock, L_old, g, a.scale_log2);
       if (k == 0) mark(4);
+    }
+    if (newest_wave == first) {
+      // The newest key as a one-key block: K row 0 and V column 0 of the fragments (lanes r = 0
+      // and g = 0), everything else zero and masked (end = L).
+      kv_ready();
+      const int64_t pos = L - 1;
+      const int64_t blk = gp(table)[pos / kDecBlock];
+      const int64_t off = pos % kDecBlock;
+      const int64_t head_stride = static_cast<int64_t>(kDecBlock) * kDecD;
+      const uint16_t* kb = a.k_pool + (blk * a.Hkv + kvh) * head_stride + off * kDecD;
+      const uint16_t* vb = a.v_pool + (blk * a.Hkv + kvh) * head_stride + off;
+      KvBlockRegs nk;
+#pragma unroll
+      for (int st = 0; st < 2; ++st) {
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+          nk.k[st][hf][0] = zero16();
+          nk.k[st][hf][1] = zero16();
+        }
+#pragma unroll
+        for (int d = 0; d < 4; ++d) nk.v[st][d] = zero16();
+      }
+      // Agent-scope loads: the preload above may have brought the (then stale) lines of this
+      // slot into this XCD's L2, and another workgroup of the launch has just written it.
+      if (r == 0) {
+        const uint32_t* kw = reinterpret_cast<const uint32_t*>(kb + g * 8);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          nk.k[0][0][0][e] = __hip_atomic_load(gp(kw + e), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          nk.k[0][0][1][e] =
+              __hip_atomic_load(gp(kw + 16 + e), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+      if (g == 0) {
+#pragma unroll
+        for (int d = 0; d < 4; ++d)
+          nk.v[0][d][0] = static_cast<uint32_t>(__hip_atomic_load(
+              gp(vb + (d * 16 + r) * kDecBlock), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+      }
+      attendBlock(st8, nk, qf, pos, L, g, a.scale_log2);
     }
     mark(0);
     if (stage != nullptr) __syncthreads();  // staged blocks are consumed before s reuses LDS
@@ -437,7 +463,7 @@ __device__ __forceinline__ bool decodeAttentionUnit(const DecodeAttnArgs& a, int
         continue;
       }
       if (tagged) {
-        if (split != 0) {
+        if (split != merger) {
           uint64_t* const mine = a.ws_tag + (row * max_splits + split) * kTagSlot;
           storeTagged(mine + d, acc, a.tag);
           if (d == 0) {
@@ -446,13 +472,13 @@ __device__ __forceinline__ bool decodeAttentionUnit(const DecodeAttnArgs& a, int
           }
           continue;
         }
-        // split 0: own partial first, then splits 1.. in order as their words arrive
+        // the merger (last active split): splits 0.. in order as their words arrive, then its
+        // own partial
         float Mt = -INFINITY, lt = 0.f, at = 0.f;
-        combineSplit(Mt, lt, at, M, l, acc);
         constexpr int kChunk = 4;
-        for (int s0 = 1; s0 < n_active; s0 += kChunk) {
+        for (int s0 = 0; s0 < merger; s0 += kChunk) {
           const uint64_t* ptr[3 * kChunk];
-          const int live = n_active - s0 < kChunk ? n_active - s0 : kChunk;
+          const int live = merger - s0 < kChunk ? merger - s0 : kChunk;
 #pragma unroll
           for (int c = 0; c < kChunk; ++c) {
             const uint64_t* slot =
@@ -469,29 +495,30 @@ __device__ __forceinline__ bool decodeAttentionUnit(const DecodeAttnArgs& a, int
           for (int c = 0; c < kChunk; ++c)
             if (c < live) combineSplit(Mt, lt, at, v[c], v[kChunk + c], v[2 * kChunk + c]);
         }
+        combineSplit(Mt, lt, at, M, l, acc);
         Mem::storeU16(a.out + row * kDecD + d, floatToBf16(at / lt));
         continue;
       }
       const int64_t slot = row * max_splits + split;
       if (d == 0) {
-        __hip_atomic_store(a.ws_ml + slot * 2, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(a.ws_ml + slot * 2 + 1, l, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(gp(a.ws_ml) + slot * 2, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(gp(a.ws_ml) + slot * 2 + 1, l, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
-      __hip_atomic_store(a.ws_o + slot * kDecD + d, acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(gp(a.ws_o) + slot * kDecD + d, acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
   if (max_splits == 1) return true;
-  if (tagged) return split == 0;
+  if (tagged) return split == merger;
 
   // Arrive: every partial store of this workgroup has completed before the counter moves.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   if (threadIdx.x == 0) {
     const unsigned old =
-        __hip_atomic_fetch_add(a.counters + pair, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_fetch_add(gp(a.counters) + pair, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     s.is_last = old + 1 == arrivals;
     if (s.is_last && reset)
-      __hip_atomic_store(a.counters + pair, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(gp(a.counters) + pair, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   __syncthreads();
   mark(2);
@@ -512,11 +539,11 @@ __device__ __forceinline__ bool decodeAttentionUnit(const DecodeAttnArgs& a, int
       for (int c = 0; c < kCombineChunk; ++c) {
         const bool live = s0 + c < n;
         const int64_t slot = row * max_splits + (live ? s0 + c : 0);
-        ms[c] = live ? __hip_atomic_load(a.ws_ml + slot * 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+        ms[c] = live ? __hip_atomic_load(gp(a.ws_ml) + slot * 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
                      : -INFINITY;
-        ls[c] = live ? __hip_atomic_load(a.ws_ml + slot * 2 + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+        ls[c] = live ? __hip_atomic_load(gp(a.ws_ml) + slot * 2 + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
                      : 0.f;
-        os[c] = live ? __hip_atomic_load(a.ws_o + slot * kDecD + d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+        os[c] = live ? __hip_atomic_load(gp(a.ws_o) + slot * kDecD + d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
                      : 0.f;
       }
 #pragma unroll

@@ -58,8 +58,8 @@ __device__ __forceinline__ void loadNormWeights(U128 (&wv)[kU][2], const uint16_
     const int s = wave + u * kW;
     if (s >= steps) break;  // uniform: wave comes from readfirstlane
     const int64_t k0 = static_cast<int64_t>(s) * 64 + g * 8;
-    wv[u][0] = load16(norm_w + k0);
-    wv[u][1] = load16(norm_w + k0 + 32);
+    wv[u][0] = gload16(norm_w + k0);
+    wv[u][1] = gload16(norm_w + k0 + 32);
   }
 }
 
@@ -253,12 +253,12 @@ struct QkvEpilogue {
           n < q_rows ? n : (n < q_rows + k_rows ? n - q_rows : n - q_rows - k_rows);
       const int d = static_cast<int>(local % p.D);
       const bool rot = live && n < q_rows + k_rows && pos[it] < p.max_pos;
-      cs[it][0] = rot ? p.cos_t[pos[it] * half + d / 2] : 1.f;
-      cs[it][1] = rot ? p.sin_t[pos[it] * half + d / 2] : 0.f;
-      bs[it][0] = (live && p.bias != nullptr) ? bf16ToFloat(p.bias[n]) : 0.f;
-      bs[it][1] = (live && p.bias != nullptr) ? bf16ToFloat(p.bias[n + 1]) : 0.f;
+      cs[it][0] = rot ? gp(p.cos_t)[pos[it] * half + d / 2] : 1.f;
+      cs[it][1] = rot ? gp(p.sin_t)[pos[it] * half + d / 2] : 0.f;
+      bs[it][0] = (live && p.bias != nullptr) ? bf16ToFloat(gp(p.bias)[n]) : 0.f;
+      bs[it][1] = (live && p.bias != nullptr) ? bf16ToFloat(gp(p.bias)[n + 1]) : 0.f;
       blk[it] = (live && n >= q_rows && pos[it] < capacity)
-                    ? p.kv.block_table[m * p.kv.max_blocks + pos[it] / p.kv.block_size]
+                    ? gp(p.kv.block_table)[m * p.kv.max_blocks + pos[it] / p.kv.block_size]
                     : -1;
     }
   }
@@ -377,7 +377,7 @@ struct ResidualTile {
     }
 #pragma unroll
     for (int j = 0; j < 8; ++j)
-      bv[j] = live && bias != nullptr && n + j < N ? bf16ToFloat(bias[n + j]) : 0.f;
+      bv[j] = live && bias != nullptr && n + j < N ? bf16ToFloat(gp(bias)[n + j]) : 0.f;
   }
 
   // y(e) returns the fp32 GEMM result of tile element e = nl * kTileM + m (row nl, column m).
@@ -421,16 +421,16 @@ __device__ __forceinline__ bool splitKArrive(const float* lds, float* partials, 
   FP_EXACT;
   constexpr int kElems = 16 * 16 * MB;
   for (int idx = threadIdx.x; idx < kElems; idx += kThreadsT)
-    __hip_atomic_store(partials + static_cast<int64_t>(split) * kElems + idx, lds[idx],
+    __hip_atomic_store(gp(partials) + static_cast<int64_t>(split) * kElems + idx, lds[idx],
                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   if (threadIdx.x == 0) {
     const unsigned old =
-        __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_fetch_add(gp(counter), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     *is_last = old + 1 == arrivals;
     if (*is_last && reset)
-      __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(gp(counter), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   __syncthreads();
   if (!*is_last) return false;
@@ -440,7 +440,7 @@ __device__ __forceinline__ bool splitKArrive(const float* lds, float* partials, 
     float part[kMaxSplits];
 #pragma unroll
     for (int sp = 0; sp < kMaxSplits; ++sp)
-      part[sp] = sp < splits ? __hip_atomic_load(partials + sp * kElems + idx, __ATOMIC_RELAXED,
+      part[sp] = sp < splits ? __hip_atomic_load(gp(partials) + sp * kElems + idx, __ATOMIC_RELAXED,
                                                  __HIP_MEMORY_SCOPE_AGENT)
                              : 0.f;
     float y = part[0];

@@ -36,6 +36,11 @@ __device__ __forceinline__ U128 load16(const void* p) {
 
 __device__ __forceinline__ U128 zero16() { return U128{0u, 0u, 0u, 0u}; }
 
+// 16 bytes of device memory (a global load whatever the compiler knows of p's origin).
+__device__ __forceinline__ U128 gload16(const void* p) {
+  return *gp(reinterpret_cast<const U128*>(p));
+}
+
 // Memory-access policies for activations.
 //   PlainMem         ordinary loads and stores: the data crosses a kernel boundary (which makes
 //                    writes visible to every XCD) before it is read.
@@ -49,27 +54,23 @@ __device__ __forceinline__ U128 zero16() { return U128{0u, 0u, 0u, 0u}; }
 //                    L2 serve repeated reads of a line, where agent-scope loads would send every
 //                    workgroup's request to the same memory channel.
 struct PlainMem {
-  __device__ __forceinline__ static U128 load16(const void* p) {
-    return *reinterpret_cast<const U128*>(p);
-  }
-  __device__ __forceinline__ static uint16_t loadU16(const uint16_t* p) { return *p; }
-  __device__ __forceinline__ static void storeU16(uint16_t* p, uint16_t v) { *p = v; }
-  __device__ __forceinline__ static void storeU32(uint32_t* p, uint32_t v) { *p = v; }
+  __device__ __forceinline__ static U128 load16(const void* p) { return gload16(p); }
+  __device__ __forceinline__ static uint16_t loadU16(const uint16_t* p) { return *gp(p); }
+  __device__ __forceinline__ static void storeU16(uint16_t* p, uint16_t v) { *gp(p) = v; }
+  __device__ __forceinline__ static void storeU32(uint32_t* p, uint32_t v) { *gp(p) = v; }
   __device__ __forceinline__ static void store16(void* p, U128 v) {
-    *reinterpret_cast<U128*>(p) = v;
+    *gp(reinterpret_cast<U128*>(p)) = v;
   }
 };
 
 struct WriteThroughMem {
-  __device__ __forceinline__ static U128 load16(const void* p) {
-    return *reinterpret_cast<const U128*>(p);
-  }
-  __device__ __forceinline__ static uint16_t loadU16(const uint16_t* p) { return *p; }
+  __device__ __forceinline__ static U128 load16(const void* p) { return gload16(p); }
+  __device__ __forceinline__ static uint16_t loadU16(const uint16_t* p) { return *gp(p); }
   __device__ __forceinline__ static void storeU16(uint16_t* p, uint16_t v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(gp(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   __device__ __forceinline__ static void storeU32(uint32_t* p, uint32_t v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(gp(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   // 16 bytes with the same cache policy the agent-scope stores above get (sc1: written through
   // to the coherent memory side). The caller's s_waitcnt vmcnt(0) covers it like any store.
@@ -143,8 +144,8 @@ struct SkinnyCore {
       const int64_t k0 = static_cast<int64_t>(s) * 64;
 #pragma unroll
       for (int f = 0; f < NF; ++f) {
-        bt.a[u][f][0] = load16(rw.w[f] + k0);
-        bt.a[u][f][1] = load16(rw.w[f] + k0 + 32);
+        bt.a[u][f][0] = gload16(rw.w[f] + k0);
+        bt.a[u][f][1] = gload16(rw.w[f] + k0 + 32);
       }
     }
   }

@@ -59,7 +59,7 @@ constexpr int kSpinLimit = 1 << 20;
 constexpr int kAbortPollEvery = 64;
 
 __device__ __forceinline__ unsigned loadAgent(const unsigned* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return __hip_atomic_load(gp(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Adds n to this workgroup's shard of a stage counter once every thread's stores have
@@ -68,7 +68,7 @@ __device__ __forceinline__ void arrive(unsigned* stage, unsigned n) {
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   if (threadIdx.x == 0)
-    __hip_atomic_fetch_add(stage + (blockIdx.x % dli_stack::kShards) * dli_stack::kLineWords, n,
+    __hip_atomic_fetch_add(gp(stage) + (blockIdx.x % dli_stack::kShards) * dli_stack::kLineWords, n,
                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -87,7 +87,7 @@ __device__ __forceinline__ void pollStage(const unsigned* stage, unsigned target
         __builtin_amdgcn_readfirstlane(loadAgent(abort_word)) != 0u)
       break;
     if (spins >= kSpinLimit) {
-      __hip_atomic_store(abort_word, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(gp(abort_word), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       break;
     }
     __builtin_amdgcn_s_sleep(1);
@@ -442,18 +442,18 @@ __device__ void decoderStack(const Args& a) {
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   if (threadIdx.x == 0) {
-    const unsigned old = __hip_atomic_fetch_add(sync + dli_stack::kExitWord, 1u, __ATOMIC_RELAXED,
+    const unsigned old = __hip_atomic_fetch_add(gp(sync) + dli_stack::kExitWord, 1u, __ATOMIC_RELAXED,
                                                 __HIP_MEMORY_SCOPE_AGENT);
     smem.is_last = old + 1 == static_cast<unsigned>(G);
   }
   __syncthreads();
   if (!smem.is_last) return;
   for (int i = threadIdx.x; i < dli_stack::kStages * dli_stack::kShards; i += kStackThreads)
-    __hip_atomic_store(sync + i * dli_stack::kLineWords, 0u, __ATOMIC_RELAXED,
+    __hip_atomic_store(gp(sync) + i * dli_stack::kLineWords, 0u, __ATOMIC_RELAXED,
                        __HIP_MEMORY_SCOPE_AGENT);
   if (threadIdx.x == 0) {
-    __hip_atomic_store(sync + dli_stack::kExitWord, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(sync + dli_stack::kEpochWord, epoch + 1u, __ATOMIC_RELAXED,
+    __hip_atomic_store(gp(sync) + dli_stack::kExitWord, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(gp(sync) + dli_stack::kEpochWord, epoch + 1u, __ATOMIC_RELAXED,
                        __HIP_MEMORY_SCOPE_AGENT);
   }
 }
