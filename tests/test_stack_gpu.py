@@ -168,3 +168,44 @@ def test_stack_long_context_split_merge_bitwise(splits):
             pos += 1
         outs.append(res)
     _assert_same(fused, stack, outs[0], outs[1], cfg.layers)
+
+
+def test_stack_trace_timeline():
+    """dli_hip_decoder_stack_trace: every workgroup stamps its layer entries in order, each
+    layer's stage stamps after its entry, and the stamps do not change the results (the traced
+    run matches the fused graph bit for bit). Off again, the buffer is left alone."""
+    cfg = tiny_config(layers=3)
+    w = random_weights(cfg, seed=71, device="cuda")
+    prompt = _prompt(cfg, 8, 3, 72)
+    fused, stack = _pair(cfg, w, 8, 128, down=3)
+    grid = torch.cuda.get_device_properties(0).multi_processor_count
+    events = 24  # dli_stack::kTraceEvents
+    trace = torch.zeros(cfg.layers * grid * events, dtype=torch.int64, device="cuda")
+    hip.call("dli_hip_decoder_stack_trace", trace.data_ptr(), cfg.layers)
+    try:
+        traced = _run_steps(stack, prompt, 1)
+        torch.cuda.synchronize()
+    finally:
+        hip.call("dli_hip_decoder_stack_trace", None, 0)
+    _assert_same(fused, stack, _run_steps(fused, prompt, 1), traced, cfg.layers)
+    t = trace.view(cfg.layers, grid, events).cpu()
+    start = t[:, :, 0]  # kTrLayerStart: written by every workgroup in every layer
+    assert bool((start > 0).all()), "a workgroup did not stamp a layer entry"
+    assert bool((start[1:] >= start[:-1]).all()), "layer entries out of order"
+    later = t[:, :, 1:]
+    reached = later > 0  # a workgroup without work in a stage leaves its events at 0
+    assert bool(reached.any()), "no stage stamps"
+    assert bool((later[reached] >= start.unsqueeze(2).expand_as(later)[reached]).all())
+    # the stamps of one layer end before the next layer's entries of the same workgroup
+    assert bool((later[:-1].amax(dim=2) <= start[1:]).all())
+    before = trace.clone()
+    _run_steps(stack, prompt[:, :1], 0, start=3)
+    torch.cuda.synchronize()
+    assert torch.equal(trace, before), "the trace buffer changed after tracing was turned off"
+
+
+def test_stack_trace_rejects_bad_arguments():
+    buf = torch.zeros(16, dtype=torch.int64, device="cuda")
+    with pytest.raises(hip.HipError):
+        hip.call("dli_hip_decoder_stack_trace", buf.data_ptr(), 0)
+    hip.call("dli_hip_decoder_stack_trace", None, 0)
