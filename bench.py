@@ -44,6 +44,11 @@ def parse():
     ap.add_argument("--graph", choices=("stack", "fused"), default="stack",
                     help="stack: all decoder layers in one persistent launch; fused: five "
                          "launches per layer")
+    ap.add_argument("--profile", default=None, metavar="PATH",
+                    help="after timing, run --profile-steps eager steps under a dli.ProfileSession "
+                         "and write its dli.profile.v1 JSON to PATH (per-node CPU and GPU time; "
+                         "summary: python -m dli.profile summarize PATH)")
+    ap.add_argument("--profile-steps", type=int, default=5)
     ap.add_argument("--calibration-copy-mib", type=int, default=0,
                     help="after timing, copy this many MiB device-to-device 3 times (a plain copy "
                          "of known size that scales rocprofv3's FETCH_SIZE / WRITE_SIZE)")
@@ -237,6 +242,14 @@ def main():
     else:
         kernel, dom_us, dom_bytes = time_decode_attention(session, cfg, B, ctx, pos, g, stream, hip)
     dom_gbs = dom_bytes / (dom_us * 1e-6) / 1e9
+
+    if args.profile:
+        prof_session = dli.ProfileSession()
+        for _ in range(args.profile_steps):
+            session.run_eager(profile=prof_session)
+        prof_session.finalize()
+        prof_session.write_json(args.profile)
+        del prof_session
 
     if args.calibration_copy_mib > 0:
         src = torch.empty(args.calibration_copy_mib << 20, dtype=torch.uint8, device=dev)

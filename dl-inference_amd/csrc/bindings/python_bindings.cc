@@ -1,6 +1,7 @@
 // Python module _dli_native (reference surface: src/python_bindings.cc:49-85): Graph,
-// Engine.load_library / run, load_weights. Additions: Engine.run(..., stream=) (hipStream_t
-// as int, so kernels join torch's current stream), registry and KV-cache controls, and
+// Engine.load_library / run, load_weights. Additions: Engine.run(..., stream=, profile=)
+// (hipStream_t as int, so kernels join torch's current stream; a ProfileSession, the
+// reference's .codex/profiling_design.md), registry and KV-cache controls, and
 // load_weights(device_id=).
 #include <ATen/ATen.h>
 #include <pybind11/pybind11.h>
@@ -13,6 +14,7 @@
 #include "dli/engine.h"
 #include "dli/graph.h"
 #include "dli/logging.h"
+#include "dli/profiler.h"
 #include "dli/tensor.h"
 #include "dli/weights.h"
 
@@ -58,6 +60,27 @@ PYBIND11_MODULE(_dli_native, m) {
       .def_readwrite("outputs", &dli::Graph::outputs)
       .def_property_readonly("nodes", [](const dli::Graph& g) { return g.nodes; });
 
+  py::class_<dli::ProfileSession>(m, "ProfileSession")
+      .def(py::init([](bool cpu, bool gpu, bool record_shapes, std::size_t max_events) {
+             dli::ProfileConfig config;
+             config.cpu = cpu;
+             config.gpu = gpu;
+             config.record_shapes = record_shapes;
+             config.max_events = max_events;
+             return new dli::ProfileSession(config);
+           }),
+           py::arg("cpu") = true, py::arg("gpu") = true, py::arg("record_shapes") = false,
+           py::arg("max_events") = 1000000)
+      .def(
+          "finalize",
+          [](dli::ProfileSession& s) {
+            py::gil_scoped_release release;
+            s.finalize();
+          })
+      .def_property_readonly("finalized", &dli::ProfileSession::finalized)
+      .def("to_json", &dli::ProfileSession::toJson)
+      .def("write_json", &dli::ProfileSession::writeJson, py::arg("path"));
+
   py::class_<dli::Engine>(m, "Engine")
       .def(py::init<>())
       .def(
@@ -70,17 +93,18 @@ PYBIND11_MODULE(_dli_native, m) {
       .def(
           "run",
           [](dli::Engine& engine, const dli::Graph& graph, const py::dict& inputs,
-             std::uintptr_t stream) {
+             std::uintptr_t stream, dli::ProfileSession* profile) {
             auto tensors = toTensorMap(inputs);
             dli::TensorMap result;
             {
               py::gil_scoped_release release;
               engine.setStream(streamFrom(stream));
-              result = engine.run(graph, std::move(tensors));
+              result = engine.run(graph, std::move(tensors), dli::RunOptions{profile});
             }
             return toDict(result);
           },
-          py::arg("graph"), py::arg("inputs"), py::arg("stream") = 0)
+          py::arg("graph"), py::arg("inputs"), py::arg("stream") = 0,
+          py::arg("profile") = nullptr)
       .def("has_operator",
            [](const dli::Engine& e, const std::string& name) { return e.registry().contains(name); })
       .def("operator_names", [](const dli::Engine& e) { return e.registry().names(); })

@@ -6,6 +6,7 @@
 #include "dli/aten_operator.h"
 #include "dli/logging.h"
 #include "dli/utils.h"
+#include "dli_hip.h"
 
 namespace dli {
 
@@ -27,10 +28,33 @@ Operator& Engine::operatorFor(const std::string& type) {
 }
 
 TensorMap Engine::run(const Graph& graph, TensorMap tensors) {
+  return run(graph, std::move(tensors), RunOptions{});
+}
+
+TensorMap Engine::run(const Graph& graph, TensorMap tensors, const RunOptions& options) {
   ExecutionContext context;
   context.kv_cache = &kv_cache_;
   context.stream = stream_;
+  context.profiler = options.profiler;
   kv_cache_.setStream(stream_);
+  ProfileSession* const profiler = options.profiler;
+  std::int64_t run_id = -1;
+  if (profiler != nullptr) {
+    int capturing = 0;
+    if (profiler->config().gpu && dli_hip_available() != 0 &&
+        dli_hip_stream_is_capturing(stream_, &capturing) != 0)
+      capturing = 1;  // cannot tell: no device timing for this run
+    run_id = profiler->beginRun(stream_, capturing != 0);
+  }
+  // Ends the run record on every exit path (error status while unwinding).
+  struct RunEnd {
+    ProfileSession* p;
+    std::int64_t id;
+    bool ok = false;
+    ~RunEnd() {
+      if (p != nullptr) p->endRun(id, ok);
+    }
+  } run_end{profiler, run_id};
 
   std::vector<const Tensor*> inputs;
   std::vector<Tensor> produced;
@@ -51,7 +75,14 @@ TensorMap Engine::run(const Graph& graph, TensorMap tensors) {
 
     Operator& op = operatorFor(node.op_type);
     LOG_DEBUG << "node '" << node.name << "' op " << node.op_type;
-    op.compute(inputs, outputs, node.attributes, context);
+    if (profiler != nullptr) {
+      ProfileSession::Scope scope = profiler->beginOperator(
+          run_id, static_cast<std::int64_t>(&node - graph.nodes.data()), node, inputs);
+      op.compute(inputs, outputs, node.attributes, context);
+      scope.finish(true, &outputs);
+    } else {
+      op.compute(inputs, outputs, node.attributes, context);
+    }
 
     for (std::size_t i = 0; i < node.outputs.size(); ++i) {
       LOG_DEBUG << "node '" << node.name << "' output " << node.outputs[i] << ' '
@@ -60,6 +91,7 @@ TensorMap Engine::run(const Graph& graph, TensorMap tensors) {
     }
   }
 
+  run_end.ok = true;
   if (graph.outputs.empty()) return tensors;
   TensorMap result;
   for (const std::string& name : graph.outputs) {

@@ -49,6 +49,7 @@ struct Runtime {
   Status (*eventElapsedTime)(float*, EventT, EventT) = nullptr;
   Status (*eventDestroy)(EventT) = nullptr;
   Status (*deviceGetAttribute)(int*, int, int) = nullptr;
+  Status (*streamIsCapturing)(StreamT, int*) = nullptr;
 
   template <typename F>
   bool bind(F& slot, const char* symbol) {
@@ -83,7 +84,8 @@ struct Runtime {
                     bind(eventSynchronize, "hipEventSynchronize") &&
                     bind(eventElapsedTime, "hipEventElapsedTime") &&
                     bind(eventDestroy, "hipEventDestroy") &&
-                    bind(deviceGetAttribute, "hipDeviceGetAttribute");
+                    bind(deviceGetAttribute, "hipDeviceGetAttribute") &&
+                    bind(streamIsCapturing, "hipStreamIsCapturing");
     if (!ok) {
       dlclose(handle);
       handle = nullptr;
@@ -349,6 +351,16 @@ int dli_hip_event_elapsed_ms(void* start, void* stop, float* ms) {
   if (ms == nullptr) return fail(DLI_HIP_EINVAL, "ms is NULL");
   if (int rc = requireRuntime()) return rc;
   return check(runtime().eventElapsedTime(ms, start, stop), "hipEventElapsedTime");
+}
+
+int dli_hip_stream_is_capturing(void* stream, int* capturing) {
+  if (capturing == nullptr) return fail(DLI_HIP_EINVAL, "capturing is NULL");
+  if (int rc = requireRuntime()) return rc;
+  int status = 0;  // hipStreamCaptureStatus: 0 none, 1 active, 2 invalidated
+  if (int rc = check(runtime().streamIsCapturing(stream, &status), "hipStreamIsCapturing"))
+    return rc;
+  *capturing = status != 0 ? 1 : 0;
+  return 0;
 }
 
 int dli_hip_event_destroy(void* event) {

@@ -11,7 +11,7 @@ import os as _os
 import torch as _torch  # noqa: F401  (must precede the native import)
 
 from . import _dli_native
-from ._dli_native import Graph, Node, load_weights, set_log_level
+from ._dli_native import Graph, Node, ProfileSession, load_weights, set_log_level
 
 _PACKAGE_ROOT = _os.path.dirname(_os.path.dirname(_os.path.dirname(_os.path.abspath(__file__))))
 LIB_DIR = _os.path.join(_PACKAGE_ROOT, "lib")
@@ -30,14 +30,15 @@ def hip_library_path() -> str:
 class Engine(_dli_native.Engine):
     """Graph engine. run() enqueues kernels on torch's current stream unless told otherwise."""
 
-    def run(self, graph, inputs, stream=None):  # noqa: D401
+    def run(self, graph, inputs, stream=None, profile=None):  # noqa: D401
+        """Runs graph on inputs; with profile (a ProfileSession) every node is timed."""
         if stream is None:
             stream = 0
             if _torch.cuda.is_available() and any(
                 isinstance(t, _torch.Tensor) and t.is_cuda for t in inputs.values()
             ):
                 stream = _torch.cuda.current_stream().cuda_stream
-        return super().run(graph, inputs, int(stream))
+        return super().run(graph, inputs, int(stream), profile)
 
     def load_plugin(self) -> "Engine":
         """Loads the gfx950 plugin; raises if it was not built."""
@@ -48,5 +49,5 @@ class Engine(_dli_native.Engine):
         return self
 
 
-__all__ = ["Engine", "Graph", "Node", "load_weights", "plugin_path", "hip_library_path",
-           "set_log_level"]
+__all__ = ["Engine", "Graph", "Node", "ProfileSession", "load_weights", "plugin_path",
+           "hip_library_path", "set_log_level"]

@@ -93,6 +93,7 @@ _SIGNATURES = {
                                                          _c_void_p],
     "dli_hip_decoder_stack_status": [_c_void_p, ctypes.POINTER(_int), _c_void_p],
     "dli_hip_decoder_stack_trace": [_c_void_p, _int],
+    "dli_hip_stream_is_capturing": [_c_void_p, ctypes.POINTER(_int)],
     "dli_hip_set_decode_attention_splits": [_int],
 }
 _RESTYPES = {

@@ -40,8 +40,9 @@ class DecodeSession:
         self._out = None
 
     # -- one step ---------------------------------------------------------------------------
-    def run_eager(self):
-        return self.engine.run(self.graph, self.inputs)
+    def run_eager(self, profile=None):
+        """One step without graph capture; profile: a dli.ProfileSession timing every node."""
+        return self.engine.run(self.graph, self.inputs, profile=profile)
 
     def capture(self, chain_ids: bool = False):
         """Warm up once (loads kernels, allocates caches and scratch), then capture a step.

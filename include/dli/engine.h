@@ -15,6 +15,7 @@
 
 #include "dli/graph.h"
 #include "dli/operator.h"
+#include "dli/profiler.h"
 #include "dli/tensor.h"
 
 namespace dli {
@@ -33,6 +34,8 @@ class Engine {
   const KVCache& kvCache() const { return kv_cache_; }
 
   TensorMap run(const Graph& graph, TensorMap inputs);
+  // With options.profiler, every node is timed into that session (include/dli/profiler.h).
+  TensorMap run(const Graph& graph, TensorMap inputs, const RunOptions& options);
 
   // Stream for subsequent run() calls (hipStream_t as void*; nullptr = null stream).
   void setStream(void* stream);

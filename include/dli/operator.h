@@ -20,10 +20,14 @@
 
 namespace dli {
 
+class ProfileSession;
+
 struct ExecutionContext {
   KVCache* kv_cache = nullptr;
   // HIP stream (hipStream_t) on which operators enqueue their kernels; nullptr = null stream.
   void* stream = nullptr;
+  // The run's profiling session, or nullptr (include/dli/profiler.h); operators may read it.
+  ProfileSession* profiler = nullptr;
 };
 
 class Operator {

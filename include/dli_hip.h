@@ -101,6 +101,9 @@ int dli_hip_event_record(void* event, void* stream);
 int dli_hip_event_synchronize(void* event);
 int dli_hip_event_elapsed_ms(void* start, void* stop, float* ms);
 int dli_hip_event_destroy(void* event);
+/* *capturing = 1 while `stream` is being captured into a graph (or its capture was
+ * invalidated), else 0. */
+int dli_hip_stream_is_capturing(void* stream, int* capturing);
 
 /* ---------------------------------------------------------------------------------------
  * 2. Kernel entry points

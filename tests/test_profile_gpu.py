@@ -1,0 +1,78 @@
+"""Device timing of dli.ProfileSession (the reference's .codex/profiling_design.md, validation
+items 6-7): per-node HIP event pairs on the run's stream, resolved by finalize(), consistent with
+an independent event pair around the whole run; no device timing while the stream is captured."""
+from __future__ import annotations
+
+import json
+
+import pytest
+import torch
+
+import dli
+
+pytestmark = pytest.mark.gpu
+
+
+def _graph():
+    return dli.Graph.from_json(json.dumps({
+        "format": "dli.graph.v1", "model_type": "profile_gpu", "inputs": ["x", "nw", "w"],
+        "outputs": ["z"],
+        "nodes": [
+            {"name": "norm", "op": "rms_norm", "inputs": ["x", "nw"], "outputs": ["h"],
+             "attrs": {"eps": 1e-6}},
+            {"name": "proj", "op": "linear", "inputs": ["h", "w"], "outputs": ["y"]},
+            {"name": "act", "op": "silu", "inputs": ["y"], "outputs": ["z"]},
+        ]}))
+
+
+def _inputs():
+    g = torch.Generator().manual_seed(0)
+    return {"x": torch.randn(32, 896, generator=g).to(torch.bfloat16).cuda(),
+            "nw": torch.ones(896, dtype=torch.bfloat16).cuda(),
+            "w": (torch.randn(4864, 896, generator=g) * 0.02).to(torch.bfloat16).cuda()}
+
+
+def test_gpu_times_per_node_and_against_an_outer_event_pair():
+    engine, graph, inputs = dli.Engine().load_plugin(), _graph(), _inputs()
+    ref = engine.run(graph, inputs)["z"]
+    stream = torch.cuda.current_stream()
+    p = dli.ProfileSession()
+    outer = []
+    for _ in range(5):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        out = engine.run(graph, inputs, profile=p)["z"]
+        b.record(stream)
+        outer.append((a, b))
+        assert torch.equal(out, ref)  # profiling does not change results
+    p.finalize()
+    torch.cuda.synchronize()
+    doc = json.loads(p.to_json())
+    assert doc["metadata"]["gpu_timing"] is True
+    assert len(doc["events"]) == 15
+    for e in doc["events"]:
+        assert e["gpu_duration_ns"] is not None and e["gpu_duration_ns"] > 0, e
+        assert e["device"] == 0 and e["status"] == "ok"
+        assert int(e["stream"], 16) == stream.cuda_stream
+    for r, (a, b) in enumerate(outer):
+        total_ns = a.elapsed_time(b) * 1e6
+        nodes_ns = sum(e["gpu_duration_ns"] for e in doc["events"] if e["run_id"] == r)
+        # the node spans lie inside the outer pair (event resolution is about a microsecond)
+        assert nodes_ns <= total_ns + 5000, (r, nodes_ns, total_ns)
+        assert nodes_ns >= 0.2 * total_ns, (r, nodes_ns, total_ns)
+
+
+def test_no_device_timing_under_graph_capture():
+    engine, graph, inputs = dli.Engine().load_plugin(), _graph(), _inputs()
+    engine.run(graph, inputs)  # warm-up: operators created, workspaces allocated
+    torch.cuda.synchronize()
+    p = dli.ProfileSession()
+    cuda_graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(cuda_graph):
+        out = engine.run(graph, inputs, profile=p)["z"]
+    cuda_graph.replay()
+    torch.cuda.synchronize()
+    p.finalize()
+    doc = json.loads(p.to_json())
+    assert all(e["gpu_duration_ns"] is None for e in doc["events"])
+    assert torch.equal(out, engine.run(graph, inputs)["z"])
