@@ -2,7 +2,7 @@
 // Engine.load_library / run, load_weights. Additions: Engine.run(..., stream=, profile=)
 // (hipStream_t as int, so kernels join torch's current stream; a ProfileSession, the
 // reference's .codex/profiling_design.md), registry and KV-cache controls, and
-// load_weights(device_id=).
+// load_weights(device_id=), and the C++ greedy decode driver (GreedyDecoder).
 #include <ATen/ATen.h>
 #include <pybind11/pybind11.h>
 #include <pybind11/stl.h>
@@ -13,6 +13,7 @@
 
 #include "dli/engine.h"
 #include "dli/graph.h"
+#include "dli/greedy.h"
 #include "dli/logging.h"
 #include "dli/profiler.h"
 #include "dli/tensor.h"
@@ -142,6 +143,45 @@ PYBIND11_MODULE(_dli_native, m) {
           },
           py::arg("name"), py::arg("dtype"), py::arg("batch"), py::arg("heads"),
           py::arg("head_dim"), py::arg("device_id") = 0);
+
+  py::class_<dli::GreedyDecoder>(m, "GreedyDecoder")
+      .def(py::init([](dli::Engine& engine, const dli::Graph& graph, const py::dict& weights,
+                       std::int64_t batch, std::int64_t block_size, std::int64_t max_seq_len,
+                       bool capture) {
+             auto tensors = toTensorMap(weights);
+             py::gil_scoped_release release;
+             return std::make_unique<dli::GreedyDecoder>(
+                 engine, graph, std::move(tensors), batch,
+                 dli::GreedyOptions{block_size, max_seq_len, capture});
+           }),
+           py::arg("engine"), py::arg("graph"), py::arg("weights"), py::arg("batch"),
+           py::arg("block_size") = 64, py::arg("max_seq_len") = 4096, py::arg("capture") = true,
+           py::keep_alive<1, 2>())
+      .def_property_readonly("batch", &dli::GreedyDecoder::batch)
+      .def_property_readonly("captured", &dli::GreedyDecoder::captured)
+      .def(
+          "step",
+          [](dli::GreedyDecoder& d, const at::Tensor& ids, const at::Tensor& positions) {
+            dli::TensorMap out;
+            {
+              py::gil_scoped_release release;
+              out = d.step(dli::Tensor(ids), dli::Tensor(positions));
+            }
+            return toDict(out);
+          },
+          py::arg("ids"), py::arg("positions"))
+      .def(
+          "generate",
+          [](dli::GreedyDecoder& d, const at::Tensor& prompt, std::int64_t steps,
+             std::int64_t start) {
+            dli::Tensor out;
+            {
+              py::gil_scoped_release release;
+              out = d.generate(dli::Tensor(prompt), steps, start);
+            }
+            return out.torchTensor();
+          },
+          py::arg("prompt"), py::arg("steps"), py::arg("start") = 0);
 
   m.def(
       "load_weights",

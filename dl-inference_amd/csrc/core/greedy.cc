@@ -1,0 +1,182 @@
+// Greedy decode driver (include/dli/greedy.h): the C++ counterpart of
+// python/dli_qwen2/session.py's DecodeSession.generate, with the step captured into a HIP graph
+// through ATen's graph capture.
+#include "dli/greedy.h"
+
+#include <ATen/ATen.h>
+#include <ATen/hip/HIPGraph.h>
+#include <c10/hip/HIPGuard.h>
+#include <c10/hip/HIPStream.h>
+
+#include <algorithm>
+#include <optional>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+namespace dli {
+
+struct GreedyDecoder::Impl {
+  Engine& engine;
+  Graph graph;
+  TensorMap inputs;
+  std::int64_t batch = 0;
+  GreedyOptions options;
+  bool on_device = false;
+  int device_id = 0;
+  Tensor ids;        // static step inputs (the captured graph reads these buffers)
+  Tensor positions;
+  std::unique_ptr<at::cuda::CUDAGraph> hip_graph;
+  TensorMap captured_out;
+
+  Impl(Engine& e, Graph g, TensorMap w, std::int64_t b, GreedyOptions o)
+      : engine(e), graph(std::move(g)), inputs(std::move(w)), batch(b), options(o) {}
+
+  void* currentStream() const {
+    return on_device ? static_cast<void*>(c10::hip::getCurrentHIPStream(device_id).stream())
+                     : nullptr;
+  }
+
+  TensorMap runEager() {
+    engine.setStream(currentStream());
+    return engine.run(graph, inputs);
+  }
+
+  void capture() {
+    c10::hip::HIPStream stream = c10::hip::getStreamFromPool(false, device_id);
+    c10::hip::HIPStreamGuard guard(stream);
+    void* const previous = engine.stream();
+    engine.setStream(stream.stream());
+    try {
+      // Warm-up on the capture stream: operators are created and every lazily allocated cache
+      // and workspace exists before capture (nothing may be allocated from the device while
+      // the stream is captured). It writes KV position 0, which the first real step rewrites.
+      engine.run(graph, inputs);
+      stream.synchronize();
+      hip_graph = std::make_unique<at::cuda::CUDAGraph>();
+      hip_graph->capture_begin();
+      try {
+        captured_out = engine.run(graph, inputs);
+      } catch (...) {
+        try {
+          hip_graph->capture_end();
+        } catch (...) {
+        }
+        hip_graph.reset();
+        throw;
+      }
+      hip_graph->capture_end();
+    } catch (...) {
+      engine.setStream(previous);
+      throw;
+    }
+    engine.setStream(previous);
+  }
+};
+
+namespace {
+
+void requireIds(const Tensor& t, std::int64_t batch, const char* what) {
+  if (!t.defined() || t.dtype() != DType::Int64 || t.rank() != 1 || t.dim(0) != batch)
+    throw std::invalid_argument(std::string(what) + " must be int64 [" + std::to_string(batch) +
+                                "]");
+}
+
+bool listed(const std::vector<std::string>& names, const std::string& name) {
+  return std::find(names.begin(), names.end(), name) != names.end();
+}
+
+}  // namespace
+
+GreedyDecoder::GreedyDecoder(Engine& engine, Graph graph, TensorMap weights, std::int64_t batch,
+                             GreedyOptions options) {
+  if (batch <= 0) throw std::invalid_argument("batch must be positive");
+  if (options.block_size <= 0 || options.max_seq_len <= 0)
+    throw std::invalid_argument("block_size and max_seq_len must be positive");
+  for (const char* name : {"input_ids", "positions"}) {
+    if (!listed(graph.inputs, name))
+      throw std::invalid_argument(std::string("decode graph has no input ") + name);
+    if (weights.count(name) != 0)
+      throw std::invalid_argument(std::string(name) + " is a step input, not a weight");
+  }
+  if (!listed(graph.outputs, "next_ids"))
+    throw std::invalid_argument("decode graph has no output next_ids");
+  impl_ = std::make_unique<Impl>(engine, std::move(graph), std::move(weights), batch, options);
+  Impl& s = *impl_;
+  for (const auto& [name, t] : s.inputs) {
+    if (t.isCuda()) {
+      s.on_device = true;
+      s.device_id = t.deviceId();
+      break;
+    }
+  }
+  s.ids = s.on_device ? Tensor::cuda(DType::Int64, {batch}, s.device_id)
+                      : Tensor::zeros(DType::Int64, {batch});
+  s.positions = s.on_device ? Tensor::cuda(DType::Int64, {batch}, s.device_id)
+                            : Tensor::zeros(DType::Int64, {batch});
+  if (s.on_device) {
+    s.ids.torchTensor().zero_();
+    s.positions.torchTensor().zero_();
+  }
+  s.inputs["input_ids"] = s.ids;
+  s.inputs["positions"] = s.positions;
+  engine.kvCache().configure(options.block_size, options.max_seq_len);
+  if (s.on_device && options.capture) s.capture();
+}
+
+GreedyDecoder::~GreedyDecoder() = default;
+
+std::int64_t GreedyDecoder::batch() const { return impl_->batch; }
+
+bool GreedyDecoder::captured() const { return impl_->hip_graph != nullptr; }
+
+TensorMap GreedyDecoder::step(const Tensor& ids, const Tensor& positions) {
+  Impl& s = *impl_;
+  requireIds(ids, s.batch, "ids");
+  requireIds(positions, s.batch, "positions");
+  const at::Tensor& pos = positions.torchTensor();
+  const std::int64_t lo = pos.min().item<std::int64_t>();
+  const std::int64_t hi = pos.max().item<std::int64_t>();
+  if (lo < 0 || hi >= s.options.max_seq_len)
+    throw std::out_of_range("position outside the KV cache capacity [0, " +
+                            std::to_string(s.options.max_seq_len) + ")");
+  s.ids.torchTensor().copy_(ids.torchTensor());
+  s.positions.torchTensor().copy_(pos);
+  if (s.hip_graph) {
+    s.hip_graph->replay();
+    return s.captured_out;
+  }
+  return s.runEager();
+}
+
+Tensor GreedyDecoder::generate(const Tensor& prompt, std::int64_t steps, std::int64_t start) {
+  Impl& s = *impl_;
+  if (!prompt.defined() || prompt.dtype() != DType::Int64 || prompt.rank() != 2 ||
+      prompt.dim(0) != s.batch || prompt.dim(1) < 1)
+    throw std::invalid_argument("prompt must be int64 [" + std::to_string(s.batch) +
+                                ", S] with S >= 1");
+  if (steps < 1 || start < 0) throw std::invalid_argument("steps must be >= 1 and start >= 0");
+  const std::int64_t length = prompt.dim(1);
+  // the last step to run feeds the (steps - 1)-th generated token
+  if (start + length + steps - 2 >= s.options.max_seq_len)
+    throw std::out_of_range("prompt plus generated tokens exceed max_seq_len");
+  const at::Device device = s.ids.torchTensor().device();
+  const at::Tensor tokens = prompt.torchTensor().to(device).contiguous();
+  at::Tensor pos = at::full({s.batch}, start, at::TensorOptions().dtype(at::kLong).device(device));
+  at::Tensor next;
+  auto advance = [&](const at::Tensor& in) {
+    TensorMap out = step(Tensor(in), Tensor(pos));
+    next = out.at("next_ids").torchTensor().clone();
+    pos.add_(1);
+  };
+  for (std::int64_t t = 0; t < length; ++t) advance(tokens.select(1, t).contiguous());
+  std::vector<at::Tensor> generated;
+  generated.reserve(static_cast<std::size_t>(steps));
+  for (std::int64_t i = 0; i < steps; ++i) {
+    generated.push_back(next);
+    if (i + 1 < steps) advance(next);
+  }
+  return Tensor(at::stack(generated, 1).cpu());
+}
+
+}  // namespace dli

@@ -11,7 +11,8 @@ import os as _os
 import torch as _torch  # noqa: F401  (must precede the native import)
 
 from . import _dli_native
-from ._dli_native import Graph, Node, ProfileSession, load_weights, set_log_level
+from ._dli_native import (GreedyDecoder, Graph, Node, ProfileSession, load_weights,
+                          set_log_level)
 
 _PACKAGE_ROOT = _os.path.dirname(_os.path.dirname(_os.path.dirname(_os.path.abspath(__file__))))
 LIB_DIR = _os.path.join(_PACKAGE_ROOT, "lib")
@@ -49,5 +50,5 @@ class Engine(_dli_native.Engine):
         return self
 
 
-__all__ = ["Engine", "Graph", "Node", "ProfileSession", "load_weights", "plugin_path",
+__all__ = ["Engine", "GreedyDecoder", "Graph", "Node", "ProfileSession", "load_weights", "plugin_path",
            "hip_library_path", "set_log_level"]

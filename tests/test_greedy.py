@@ -1,0 +1,75 @@
+"""C++ greedy decode driver (dli.GreedyDecoder) argument checks and the dli.weights.v1 writer
+(dli.weights.save_weights) round trip through the C++ loader. Decoding itself needs the gfx950
+plugin: tests/test_greedy_gpu.py."""
+from __future__ import annotations
+
+import json
+
+import pytest
+import torch
+
+import dli
+from dli.weights import save_weights
+
+
+def _graph(outputs=("next_ids",)):
+    return dli.Graph.from_json(json.dumps({
+        "format": "dli.graph.v1", "model_type": "greedy_test",
+        "inputs": ["input_ids", "positions", "table"], "outputs": list(outputs),
+        "nodes": [{"name": "emb", "op": "aten", "inputs": ["table", "input_ids"],
+                   "outputs": ["next_ids"], "attrs": {"name": "aten::embedding"}}]}))
+
+
+def test_weights_round_trip_all_dtypes(tmp_path):
+    g = torch.Generator().manual_seed(0)
+    tensors = {
+        "f32": torch.randn(3, 5, generator=g),
+        "bf16": torch.randn(7, 9, generator=g).to(torch.bfloat16),
+        "f16": torch.randn(4, generator=g).to(torch.float16),
+        "i64": torch.randint(-2**40, 2**40, (6,), generator=g),
+        "i32": torch.randint(-2**30, 2**30, (2, 3), generator=g, dtype=torch.int32),
+        "empty": torch.zeros(0, 4),
+    }
+    path = save_weights(tmp_path, "m", tensors)
+    assert path.name == "m.dli.weights.json"
+    manifest = json.loads(path.read_text())
+    assert manifest["format"] == "dli.weights.v1" and manifest["data"] == "m.dli.weights.bin"
+    assert all(m["offset"] % 64 == 0 for m in manifest["tensors"].values())
+    assert manifest["tensors"]["bf16"]["dtype"] == "bfloat16"
+    assert manifest["tensors"]["bf16"]["nbytes"] == 7 * 9 * 2
+    back = dli.load_weights(str(path))
+    assert set(back) == set(tensors)
+    for name, t in tensors.items():
+        assert back[name].dtype == t.dtype and back[name].shape == t.shape
+        assert torch.equal(back[name], t), name  # bit-exact, bf16 included
+
+
+def test_weights_writer_rejects_unsupported_dtype(tmp_path):
+    with pytest.raises(TypeError):
+        save_weights(tmp_path, "bad", {"b": torch.zeros(2, dtype=torch.bool)})
+
+
+def test_decoder_rejects_bad_graphs_and_arguments():
+    e = dli.Engine()
+    table = {"table": torch.randn(10, 4)}
+    with pytest.raises(ValueError, match="next_ids"):
+        dli.GreedyDecoder(e, _graph(outputs=("y",)), table, 2)
+    with pytest.raises(ValueError, match="step input"):
+        dli.GreedyDecoder(e, _graph(), {**table, "input_ids": torch.zeros(2, dtype=torch.int64)}, 2)
+    with pytest.raises(ValueError, match="batch"):
+        dli.GreedyDecoder(e, _graph(), table, 0)
+    d = dli.GreedyDecoder(e, _graph(), table, 2, max_seq_len=8)
+    assert d.batch == 2 and not d.captured  # host weights: eager steps
+    pos = torch.zeros(2, dtype=torch.int64)
+    with pytest.raises(ValueError, match="ids"):
+        d.step(torch.zeros(3, dtype=torch.int64), pos)
+    with pytest.raises(ValueError, match="ids"):
+        d.step(torch.zeros(2, dtype=torch.int32), pos)
+    with pytest.raises(IndexError):
+        d.step(torch.zeros(2, dtype=torch.int64), torch.tensor([0, 8]))
+    with pytest.raises(ValueError, match="prompt"):
+        d.generate(torch.zeros(2, 0, dtype=torch.int64), 3)
+    with pytest.raises(ValueError, match="prompt"):
+        d.generate(torch.zeros(3, 2, dtype=torch.int64), 3)
+    with pytest.raises(IndexError):  # 6 prompt positions + 3 tokens need positions up to 7 + 1
+        d.generate(torch.zeros(2, 6, dtype=torch.int64), 4)
