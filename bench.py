@@ -34,7 +34,10 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--batch", type=int, default=32)
+    ap.add_argument("--workload", choices=("decode", "alexnet"), default="decode",
+                    help="decode (default): the Qwen2 decode step; alexnet: the AlexNet-style "
+                         "fp32 CNN forward (batch 64) on the MFMA GEMM operators")
+    ap.add_argument("--batch", type=int, default=None, help="decode 32, alexnet 64")
     ap.add_argument("--context", type=int, default=4096)
     ap.add_argument("--layers", type=int, default=None, help="override (for quick local checks)")
     ap.add_argument("--cpu-baseline-steps", type=int, default=3)
@@ -168,12 +171,119 @@ def _time_launches(fn, stream, reps):
     return a0.elapsed_time(a1) * 1000.0 / reps
 
 
+FP32_MFMA_PEAK_TFLOPS = 157.3
+
+
+def bench_alexnet(args):
+    """AlexNet-style fp32 CNN forward (conv 64/192/384/256/256 3x3, FC 4096-4096-10) at batch 64
+    on 3x32x32 inputs: one step = one replay of the captured dli.graph.v1 forward. Reports
+    images/s, the step's fp32 MFMA roofline, the slowest node's roofline (per-node HIP events of
+    dli.ProfileSession over eager runs), parity against ATen on the CPU, and the ATen CPU forward
+    timed on this host."""
+    import torch
+
+    import dli
+    import dli_alexnet as net
+
+    B = args.batch or 64
+    dev = "cuda"
+    weights = net.random_weights(seed=0, device=dev)
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn((B,) + net.IMAGE, generator=g).to(dev)
+    engine = dli.Engine().load_plugin()
+    graph = net.build_graph(B, fused=True)
+    inputs = {"x": x, **weights}
+    out = engine.run(graph, inputs)["logits"]
+    torch.cuda.synchronize()
+    # parity on the benchmark batch: ATen fp32 on the CPU, same inputs
+    ref = net.torch_forward(x.cpu(), {k: v.cpu() for k, v in weights.items()})
+    rel_err = float((out.cpu() - ref).norm() / ref.norm())
+    hip_graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(hip_graph):
+        out = engine.run(graph, inputs)["logits"]
+    for _ in range(args.warmup):
+        hip_graph.replay()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(args.steps):
+        hip_graph.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = e0.elapsed_time(e1) / args.steps
+    flops = net.flops_per_image() * B
+    tflops = flops / (ms * 1e-3) / 1e12
+
+    # slowest node (HIP event pairs per node, eager runs)
+    prof = dli.ProfileSession()
+    for _ in range(6):
+        engine.run(graph, inputs, profile=prof)
+    prof.finalize()
+    doc = json.loads(prof.to_json())
+    per = {}
+    for e in doc["events"]:
+        if e["run_id"] > 0 and e["gpu_duration_ns"] is not None:
+            per.setdefault(e["node_name"], []).append(e["gpu_duration_ns"])
+    med = {k: sorted(v)[(len(v) - 1) // 2] for k, v in per.items()}
+    node_flops = {}
+    hw = net.IMAGE[1] * net.IMAGE[2]
+    for i, (cin, cout) in enumerate(net.CONVS):
+        node_flops[f"features.conv{i}"] = 2 * B * hw * cout * cin * 9
+        if i in net.POOL_AFTER:
+            hw //= 4
+    for i, (fin, fout) in enumerate(net.FCS):
+        node_flops[f"classifier.fc{i}"] = 2 * B * fin * fout
+    top = max(med, key=med.get)
+    top_tflops = node_flops.get(top, 0) / (med[top] * 1e-9) / 1e12
+
+    cpu = None
+    if not args.no_cpu_baseline and args.cpu_baseline_steps > 0:
+        xc, wc = x.cpu(), {k: v.cpu() for k, v in weights.items()}
+        net.torch_forward(xc, wc)
+        t1 = time.perf_counter()
+        for _ in range(args.cpu_baseline_steps):
+            net.torch_forward(xc, wc)
+        cpu_s = (time.perf_counter() - t1) / args.cpu_baseline_steps
+        cpu = {"value": round(B / cpu_s, 2), "unit": "images/s", "cores": torch.get_num_threads(),
+               "kind": "port",
+               "sample": f"{args.cpu_baseline_steps} forwards (after 1 warm-up) of the same "
+                         f"batch-{B} network with ATen fp32 CPU ops (the ops the reference's "
+                         f"CPU path runs); {cpu_s * 1000:.1f} ms/forward"}
+    print(json.dumps({
+        "metric": "AlexNet-style fp32 CNN images/s + % fp32 MFMA peak, batch 64",
+        "value": round(B / (ms * 1e-3), 1), "unit": "images/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "AlexNet-style CNN fp32 forward, batch 64, 3x32x32 input: conv "
+                               "64/192/384/256/256 3x3 (fused ReLU), max_pool 2 after conv 1-2, "
+                               "FC 4096-4096-10", "global_batch": B,
+                   "graph": "dli.graph.v1 forward, HIP-graph replay"},
+        "roofline": {"bound": "mfma", "kernel": top, "achieved": round(top_tflops, 2),
+                     "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(top_tflops / FP32_MFMA_PEAK_TFLOPS, 4), "traffic": None,
+                     "avg_us": round(med[top] / 1000, 2), "flops_per_launch": node_flops.get(top)},
+        "step_roofline": {"bound": "mfma", "flops_per_step": flops, "achieved": round(tflops, 2),
+                          "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                          "frac": round(tflops / FP32_MFMA_PEAK_TFLOPS, 4)},
+        "node_us": {k: round(v / 1000, 2) for k, v in med.items()},
+        "parity": {"relative_l2_vs_aten_cpu": rel_err},
+        "cpu_baseline": cpu, "wall_s_timed": round(wall, 3),
+        "device": torch.cuda.get_device_name(0)}), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 "
                                    "(multi-GPU decode is data-parallel by batch, see DESIGN.md)"}))
         sys.exit(2)
+    if args.workload == "alexnet":
+        bench_alexnet(args)
+        return
 
     import torch
 
@@ -183,7 +293,7 @@ def main():
     from dataclasses import replace
 
     cfg = QWEN2_0_5B if args.layers is None else replace(QWEN2_0_5B, layers=args.layers)
-    B, ctx = args.batch, args.context
+    B, ctx = args.batch or 32, args.context
     from dli_qwen2.graph import DEFAULT_SPLITS, STACK_SPLITS
 
     splits = dict(STACK_SPLITS if args.graph == "stack" else DEFAULT_SPLITS)

@@ -66,6 +66,32 @@ FloatKernels k_attention("attention", "attention");
 FloatKernels k_paged_attention("attention", "paged_attention");
 FloatKernels k_kv_append("attention", "kv_append");
 FloatKernels k_conv2d("conv", "conv2d");
+DeviceKernel k_mfma_linear64("mfma_gemm", "mfma_linear_f32_t64");
+DeviceKernel k_mfma_linear128("mfma_gemm", "mfma_linear_f32_t128");
+DeviceKernel k_mfma_matmul64("mfma_gemm", "mfma_matmul_f32_t64");
+DeviceKernel k_mfma_matmul128("mfma_gemm", "mfma_matmul_f32_t128");
+DeviceKernel k_mfma_conv64("mfma_gemm", "mfma_conv2d_f32_t64");
+DeviceKernel k_mfma_conv128("mfma_gemm", "mfma_conv2d_f32_t128");
+DeviceKernel k_mfma_bf16_64("mfma_gemm", "mfma_linear_bf16_t64");
+DeviceKernel k_mfma_bf16_128("mfma_gemm", "mfma_linear_bf16_t128");
+DeviceKernel k_mfma_splitk("mfma_gemm", "mfma_linear_f32_splitk_t64");
+DeviceKernel k_splitk_reduce("mfma_gemm", "splitk_reduce_f32");
+
+// Split count of an fp32 linear: 64 x 64 tiles are split over K (chunks of at least 1024) until
+// there are about 512 workgroups (two per CU); 1 = no split.
+int64_t linearSplits(int64_t m, int64_t n, int64_t k) {
+  const int64_t tiles = ((m + 63) / 64) * ((n + 63) / 64);
+  int64_t splits = 1;
+  while (splits < 16 && tiles * splits * 2 <= 512 && k / (splits * 2) >= 1024) splits *= 2;
+  return splits;
+}
+
+// MFMA GEMM tiles: 128 x 128 once those alone give every CU a workgroup, else 64 x 64.
+bool bigTiles(int64_t rows, int64_t cols) {
+  return ((rows + 127) / 128) * ((cols + 127) / 128) >= 256;
+}
+
+constexpr int64_t kMaxGridY = 65535;
 
 int binary(FloatKernels& kernels, const char* op, int dtype, const void* a, const void* b,
            void* out, int64_t total, int64_t width, void* stream) {
@@ -199,45 +225,131 @@ int dli_hip_conv2d(int dtype, const void* x, const void* weight, const void* bia
                    int64_t n, int64_t in_c, int64_t h, int64_t w, int64_t out_c, int64_t kernel_h,
                    int64_t kernel_w, int64_t out_h, int64_t out_w, int64_t stride_h,
                    int64_t stride_w, int64_t pad_h, int64_t pad_w, void* stream) {
-  DeviceKernel* k = k_conv2d.pick(dtype);
-  if (k == nullptr) return badDtype("conv2d", dtype);
+  return dli_hip_conv2d_act(dtype, x, weight, bias, out, n, in_c, h, w, out_c, kernel_h, kernel_w,
+                            out_h, out_w, stride_h, stride_w, pad_h, pad_w, DLI_ACT_NONE, stream);
+}
+
+int dli_hip_conv2d_act(int dtype, const void* x, const void* weight, const void* bias, void* out,
+                       int64_t n, int64_t in_c, int64_t h, int64_t w, int64_t out_c,
+                       int64_t kernel_h, int64_t kernel_w, int64_t out_h, int64_t out_w,
+                       int64_t stride_h, int64_t stride_w, int64_t pad_h, int64_t pad_w,
+                       int activation, void* stream) {
+  if (activation != DLI_ACT_NONE && activation != DLI_ACT_RELU)
+    return badArg("conv2d", "unknown activation");
   if (stride_h <= 0 || stride_w <= 0 || pad_h < 0 || pad_w < 0)
     return badArg("conv2d", "stride must be positive, padding non-negative");
-  if (n < 0 || in_c < 0 || out_c < 0 || out_h < 0 || out_w < 0)
+  if (n < 0 || in_c < 0 || out_c < 0 || out_h < 0 || out_w < 0 || h < 0 || w < 0 ||
+      kernel_h < 0 || kernel_w < 0)
     return badArg("conv2d", "negative size");
   const int64_t total = n * out_c * out_h * out_w;
   if (total == 0) return 0;
-  return launch(*k, {strideBlocks(total)}, {256}, 0, stream, x, weight, bias, out, n, in_c, h, w,
-                out_c, kernel_h, kernel_w, out_h, out_w, stride_h, stride_w, pad_h, pad_w);
+  if (x == nullptr || weight == nullptr || out == nullptr) return badArg("conv2d", "NULL pointer");
+  const int relu = activation == DLI_ACT_RELU ? 1 : 0;
+  // fp32: implicit GEMM on MFMA, 32-bit index math (every element index below 2^31)
+  const int64_t pixels = n * out_h * out_w, patch = in_c * kernel_h * kernel_w;
+  const int64_t limit = int64_t{1} << 31;
+  if (dtype == DLI_F32 && n * in_c * h * w < limit && total < limit && out_c * patch < limit &&
+      pixels < limit && (out_h - 1) * stride_h + kernel_h < limit &&
+      (out_w - 1) * stride_w + kernel_w < limit) {
+    const bool big = bigTiles(out_c, pixels);
+    const int64_t tile = big ? 128 : 64;
+    if ((out_c + tile - 1) / tile <= kMaxGridY) {
+      auto i32 = [](int64_t v) { return static_cast<int>(v); };
+      return launch(big ? k_mfma_conv128 : k_mfma_conv64,
+                    {static_cast<unsigned>((pixels + tile - 1) / tile),
+                     static_cast<unsigned>((out_c + tile - 1) / tile)},
+                    {256}, 0, stream, x, weight, bias, out, i32(n), i32(in_c), i32(h), i32(w),
+                    i32(out_c), i32(kernel_h), i32(kernel_w), i32(out_h), i32(out_w),
+                    i32(stride_h), i32(stride_w), i32(pad_h), i32(pad_w), relu);
+    }
+  }
+  DeviceKernel* k = k_conv2d.pick(dtype);
+  if (k == nullptr) return badDtype("conv2d", dtype);
+  int rc = launch(*k, {strideBlocks(total)}, {256}, 0, stream, x, weight, bias, out, n, in_c, h, w,
+                  out_c, kernel_h, kernel_w, out_h, out_w, stride_h, stride_w, pad_h, pad_w);
+  if (rc == 0 && relu) rc = unary(k_relu, "relu", dtype, out, out, total, stream);
+  return rc;
 }
 
 int dli_hip_linear(int dtype, int out_dtype, const void* x, const void* w, const void* bias,
                    void* out, int64_t m, int64_t n, int64_t k, void* stream) {
+  return dli_hip_linear_act(dtype, out_dtype, x, w, bias, out, m, n, k, DLI_ACT_NONE, nullptr, 0,
+                            stream);
+}
+
+size_t dli_hip_linear_workspace(int dtype, int64_t m, int64_t n, int64_t k) {
+  if (dtype != DLI_F32 || m <= 0 || n <= 0 || k <= 0) return 0;
+  const int64_t splits = linearSplits(m, n, k);
+  return splits > 1 ? static_cast<size_t>(splits * m * n) * sizeof(float) : 0;
+}
+
+int dli_hip_linear_act(int dtype, int out_dtype, const void* x, const void* w, const void* bias,
+                       void* out, int64_t m, int64_t n, int64_t k, int activation,
+                       void* workspace, size_t workspace_bytes, void* stream) {
+  if (activation != DLI_ACT_NONE && activation != DLI_ACT_RELU)
+    return badArg("linear", "unknown activation");
   if (out_dtype != dtype && out_dtype != DLI_F32)
     return badArg("linear", "out_dtype must equal dtype or be float32");
   if (m < 0 || n < 0 || k < 0) return badArg("linear", "negative size");
   if (m == 0 || n == 0) return 0;
   if (x == nullptr || w == nullptr || out == nullptr) return badArg("linear", "NULL pointer");
   const int out_f32 = out_dtype == DLI_F32 ? 1 : 0;
-  // bf16 weight streaming for decode-sized m: MFMA skinny kernel.
-  if (dtype == DLI_BF16 && m <= 64 && k % 64 == 0 && aligned16(x) && aligned16(w)) {
-    DeviceKernel* sk = m <= 16 ? &k_skinny1 : (m <= 32 ? &k_skinny2 : &k_skinny4);
-    return launch(*sk, {blocksFor(n, 32)}, {256}, 0, stream, x, w, bias, out, m, n, k, out_f32);
+  const int relu = activation == DLI_ACT_RELU ? 1 : 0;
+  const bool big = bigTiles(m, n);
+  const int64_t tile = big ? 128 : 64;
+  const Dim3 grid{static_cast<unsigned>((n + tile - 1) / tile),
+                  static_cast<unsigned>((m + tile - 1) / tile)};
+  const bool grid_ok = (m + tile - 1) / tile <= kMaxGridY;
+  if (dtype == DLI_F32 && grid_ok) {
+    const int64_t splits = linearSplits(m, n, k);
+    const size_t need = static_cast<size_t>(splits * m * n) * sizeof(float);
+    if (splits > 1 && workspace != nullptr && workspace_bytes >= need) {
+      const int64_t per = (k + splits - 1) / splits;
+      int rc = launch(k_mfma_splitk,
+                      {static_cast<unsigned>((n + 63) / 64), static_cast<unsigned>((m + 63) / 64),
+                       static_cast<unsigned>(splits)},
+                      {256}, 0, stream, x, w, workspace, m, n, k, per);
+      if (rc != 0) return rc;
+      return launch(k_splitk_reduce, {strideBlocks(m * n)}, {256}, 0, stream, workspace, bias,
+                    out, m, n, static_cast<int>(splits), relu);
+    }
+    return launch(big ? k_mfma_linear128 : k_mfma_linear64, grid, {256}, 0, stream, x, w, bias,
+                  out, m, n, k, relu);
   }
-  DeviceKernel* kt = k_gemm.pick(dtype);
-  if (kt == nullptr) return badDtype("linear", dtype);
-  if ((m + 63) / 64 > 65535) return badArg("linear", "m too large");
-  return launch(*kt, {blocksFor(n, 64), blocksFor(m, 64)}, {256}, 0, stream, x, w, bias, out, m,
+  int rc;
+  if (dtype == DLI_BF16 && m <= 64 && k % 64 == 0 && aligned16(x) && aligned16(w)) {
+    // bf16 weight streaming for decode-sized m: MFMA skinny kernel.
+    DeviceKernel* sk = m <= 16 ? &k_skinny1 : (m <= 32 ? &k_skinny2 : &k_skinny4);
+    rc = launch(*sk, {blocksFor(n, 32)}, {256}, 0, stream, x, w, bias, out, m, n, k, out_f32);
+  } else if (dtype == DLI_BF16 && k % 8 == 0 && aligned16(x) && aligned16(w) && grid_ok) {
+    return launch(big ? k_mfma_bf16_128 : k_mfma_bf16_64, grid, {256}, 0, stream, x, w, bias, out,
+                  m, n, k, out_f32, relu);
+  } else {
+    DeviceKernel* kt = k_gemm.pick(dtype);
+    if (kt == nullptr) return badDtype("linear", dtype);
+    if ((m + 63) / 64 > kMaxGridY) return badArg("linear", "m too large");
+    rc = launch(*kt, {blocksFor(n, 64), blocksFor(m, 64)}, {256}, 0, stream, x, w, bias, out, m,
                 n, k, 1, out_f32);
+  }
+  if (rc == 0 && relu) rc = unary(k_relu, "relu", out_dtype, out, out, m * n, stream);
+  return rc;
 }
 
 int dli_hip_matmul(int dtype, const void* a, const void* b, void* out, int64_t m, int64_t n,
                    int64_t k, void* stream) {
-  DeviceKernel* kt = k_gemm.pick(dtype);
-  if (kt == nullptr) return badDtype("matmul", dtype);
   if (m < 0 || n < 0 || k < 0) return badArg("matmul", "negative size");
   if (m == 0 || n == 0) return 0;
-  if ((m + 63) / 64 > 65535) return badArg("matmul", "m too large");
+  if (a == nullptr || b == nullptr || out == nullptr) return badArg("matmul", "NULL pointer");
+  const bool big = bigTiles(m, n);
+  const int64_t tile = big ? 128 : 64;
+  if (dtype == DLI_F32 && (m + tile - 1) / tile <= kMaxGridY)
+    return launch(big ? k_mfma_matmul128 : k_mfma_matmul64,
+                  {static_cast<unsigned>((n + tile - 1) / tile),
+                   static_cast<unsigned>((m + tile - 1) / tile)},
+                  {256}, 0, stream, a, b, out, m, n, k);
+  DeviceKernel* kt = k_gemm.pick(dtype);
+  if (kt == nullptr) return badDtype("matmul", dtype);
+  if ((m + 63) / 64 > kMaxGridY) return badArg("matmul", "m too large");
   const void* no_bias = nullptr;
   return launch(*kt, {blocksFor(n, 64), blocksFor(m, 64)}, {256}, 0, stream, a, b, no_bias, out, m,
                 n, k, 0, 0);

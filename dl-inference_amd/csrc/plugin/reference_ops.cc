@@ -96,8 +96,19 @@ class EmbeddingOp final : public Operator {
   }
 };
 
+// Extension attribute of linear and conv2d: activation = "relu" applies ReLU in the GEMM
+// epilogue (the reference graph has a separate relu node instead). Absent or "none": no
+// activation.
+int activationAttr(const Attributes& attrs, const std::string& op) {
+  const std::string a = attrs.value_or<std::string>("activation", "none");
+  if (a == "none") return DLI_ACT_NONE;
+  if (a == "relu") return DLI_ACT_RELU;
+  throw std::invalid_argument(op + ": unsupported activation " + a);
+}
+
 // linear/template.cc:20-32 — x [..., k] * w[n, k]^T (+ b[n]). Extension: attr
-// out_dtype = "float32" keeps an fp32 result for low-precision inputs (e.g. logits).
+// out_dtype = "float32" keeps an fp32 result for low-precision inputs (e.g. logits); attr
+// activation (above).
 class LinearOp final : public Operator {
  public:
   std::string type() const override { return "linear"; }
@@ -124,8 +135,16 @@ class LinearOp final : public Operator {
     const std::string requested = attrs.value_or<std::string>("out_dtype", "");
     if (!requested.empty()) out_dtype = dtypeFromString(requested);
     *out[0] = allocLike(out_dtype, withLast(in[0]->shape(), n), *in[0]);
-    check(dli_hip_linear(hipDtype(in[0]->dtype()), hipDtype(out_dtype), ptr(*in[0]), ptr(*in[1]),
-                         has_bias ? ptr(*in[2]) : nullptr, ptr(*out[0]), m, n, k, ctx.stream),
+    const int act = activationAttr(attrs, type());
+    const int dt = hipDtype(in[0]->dtype());
+    // split-K scratch for fp32 shapes with few output tiles (from the caching allocator)
+    const std::size_t ws_bytes = dli_hip_linear_workspace(dt, m, n, k);
+    Tensor ws;
+    if (ws_bytes > 0)
+      ws = allocLike(DType::Float32, {static_cast<std::int64_t>(ws_bytes / sizeof(float))}, *in[0]);
+    check(dli_hip_linear_act(dt, hipDtype(out_dtype), ptr(*in[0]), ptr(*in[1]),
+                             has_bias ? ptr(*in[2]) : nullptr, ptr(*out[0]), m, n, k, act,
+                             ws_bytes > 0 ? ptr(ws) : nullptr, ws_bytes, ctx.stream),
           type());
   }
 };
@@ -314,7 +333,8 @@ std::int64_t pooledExtent(std::int64_t in, std::int64_t k, std::int64_t s, std::
   return (in + 2 * p - k) / s + 1;
 }
 
-// conv2d/template.cc:7-35 — NCHW direct convolution; attrs stride [1,1], padding [0,0].
+// conv2d/template.cc:7-35 — NCHW convolution; attrs stride [1,1], padding [0,0]; extension
+// attr activation (above).
 class Conv2dOp final : public Operator {
  public:
   std::string type() const override { return "conv2d"; }
@@ -339,10 +359,11 @@ class Conv2dOp final : public Operator {
     const bool has_bias = in.size() == 3;
     if (has_bias && static_cast<std::int64_t>(in[2]->numel()) != oc)
       throw std::invalid_argument("conv2d bias size must match output channels");
+    const int act = activationAttr(attrs, type());
     *out[0] = allocLike(x.dtype(), {n, oc, oh, ow}, x);
-    check(dli_hip_conv2d(hipDtype(x.dtype()), ptr(x), ptr(w), has_bias ? ptr(*in[2]) : nullptr,
-                         ptr(*out[0]), n, c, h, wd, oc, kh, kw, oh, ow, stride[0], stride[1],
-                         pad[0], pad[1], ctx.stream),
+    check(dli_hip_conv2d_act(hipDtype(x.dtype()), ptr(x), ptr(w),
+                             has_bias ? ptr(*in[2]) : nullptr, ptr(*out[0]), n, c, h, wd, oc, kh,
+                             kw, oh, ow, stride[0], stride[1], pad[0], pad[1], act, ctx.stream),
           type());
   }
 };

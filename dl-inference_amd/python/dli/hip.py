@@ -64,8 +64,12 @@ _SIGNATURES = {
     "dli_hip_max_pool2d": [_int, _c_void_p, _c_void_p] + [_i64] * 12 + [_c_void_p],
     "dli_hip_conv2d": [_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p] + [_i64] * 13
     + [_c_void_p],
+    "dli_hip_conv2d_act": [_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p] + [_i64] * 13
+    + [_int, _c_void_p],
     "dli_hip_linear": [_int, _int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64,
                        _c_void_p],
+    "dli_hip_linear_act": [_int, _int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64,
+                           _i64, _int, _c_void_p, _size, _c_void_p],
     "dli_hip_matmul": [_int, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _c_void_p],
     "dli_hip_rotary": [_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p]
     + [_i64] * 8 + [_c_void_p, _int, _c_void_p],
@@ -73,6 +77,7 @@ _SIGNATURES = {
     + [_int, _float, _c_void_p],
     "dli_hip_kv_append": [_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p]
     + [_i64] * 7 + [_c_void_p, _int, _c_void_p],
+    "dli_hip_linear_workspace": [_int, _i64, _i64, _i64],
     "dli_hip_paged_attention_workspace": [_i64] * 5,
     "dli_hip_paged_attention": [_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p]
     + [_i64] * 8 + [_c_void_p, _int, _int, _float, _c_void_p, _size, _c_void_p],
@@ -100,6 +105,7 @@ _RESTYPES = {
     "dli_hip_load_error": ctypes.c_char_p,
     "dli_hip_last_error": ctypes.c_char_p,
     "dli_hip_target_arch": ctypes.c_char_p,
+    "dli_hip_linear_workspace": _size,
     "dli_hip_paged_attention_workspace": _size,
     "dli_hip_splitk_workspace": _size,
     "dli_hip_lm_head_argmax_workspace": _size,

@@ -51,6 +51,12 @@ enum {
   DLI_HIP_ENODEV = -2,
 };
 
+/* Activations fused into a GEMM epilogue (dli_hip_linear_act, dli_hip_conv2d_act). */
+enum {
+  DLI_ACT_NONE = 0,
+  DLI_ACT_RELU = 1,
+};
+
 /* memcpy kinds, numbered as cudaMemcpyKind in include/dli/cuda_runtime.h:8-12. */
 enum {
   DLI_MEMCPY_HOST_TO_DEVICE = 1,
@@ -150,20 +156,44 @@ int dli_hip_max_pool2d(int dtype, const void* x, void* out, int64_t n, int64_t c
                        int64_t kernel_w, int64_t stride_h, int64_t stride_w, int64_t pad_h,
                        int64_t pad_w, void* stream);
 
-/* Direct NCHW convolution with zero padding (conv2d/kernel.py:6-49); bias may be NULL. */
+/* NCHW convolution with zero padding (conv2d/kernel.py:6-49); bias may be NULL. fp32 runs as
+ * an implicit GEMM on MFMA (the input patches are gathered while staging, never
+ * materialised); bf16/fp16 use a direct kernel. fp32 accumulation. */
 int dli_hip_conv2d(int dtype, const void* x, const void* weight, const void* bias, void* out,
                    int64_t n, int64_t in_c, int64_t h, int64_t w, int64_t out_c,
                    int64_t kernel_h, int64_t kernel_w, int64_t out_h, int64_t out_w,
                    int64_t stride_h, int64_t stride_w, int64_t pad_h, int64_t pad_w,
                    void* stream);
 
+/* dli_hip_conv2d followed by `activation` (DLI_ACT_*), fused into the GEMM epilogue on the
+ * MFMA path. No counterpart in the reference, whose graph runs conv2d and relu as two nodes
+ * (conv2d/kernel.py:6-49, relu/kernel.py:6); the plugin uses it for a conv2d node with
+ * attribute activation = "relu". */
+int dli_hip_conv2d_act(int dtype, const void* x, const void* weight, const void* bias,
+                       void* out, int64_t n, int64_t in_c, int64_t h, int64_t w, int64_t out_c,
+                       int64_t kernel_h, int64_t kernel_w, int64_t out_h, int64_t out_w,
+                       int64_t stride_h, int64_t stride_w, int64_t pad_h, int64_t pad_w,
+                       int activation, void* stream);
+
 /* out[m, n] = sum_k x[m, k] * w[n, k] (+ bias[n]) (linear/kernel.py:6-44;
  * linear/template.cc:23-32). x, w, bias share `dtype`; out_dtype is dtype or DLI_F32.
- * bias may be NULL. fp32 accumulation; bf16/fp16 use MFMA. */
+ * bias may be NULL. fp32 accumulation. MFMA: fp32 always (16x16x4 f32); bf16 as a weight
+ * stream for m <= 64 (K % 64 == 0), else as tiled bf16 MFMA (K % 8 == 0, 16-byte aligned). */
 int dli_hip_linear(int dtype, int out_dtype, const void* x, const void* w, const void* bias,
                    void* out, int64_t m, int64_t n, int64_t k, void* stream);
 
-/* out[m, n] = sum_k a[m, k] * b[k, n] (matmul/kernel.py:6-40). */
+/* dli_hip_linear followed by `activation` (DLI_ACT_*), fused into the epilogue on the tiled
+ * MFMA paths. No counterpart in the reference (linear and relu are separate nodes there); the
+ * plugin uses it for every linear node (attribute activation = "relu" to fuse). A workspace of
+ * dli_hip_linear_workspace(dtype, m, n, k) bytes (no zeroing needed) lets fp32 shapes with few
+ * output tiles and a long K split K over more workgroups, summing the splits in a fixed order;
+ * with workspace NULL or smaller, no split. */
+int dli_hip_linear_act(int dtype, int out_dtype, const void* x, const void* w, const void* bias,
+                       void* out, int64_t m, int64_t n, int64_t k, int activation,
+                       void* workspace, size_t workspace_bytes, void* stream);
+size_t dli_hip_linear_workspace(int dtype, int64_t m, int64_t n, int64_t k);
+
+/* out[m, n] = sum_k a[m, k] * b[k, n] (matmul/kernel.py:6-40); fp32 on MFMA. */
 int dli_hip_matmul(int dtype, const void* a, const void* b, void* out, int64_t m, int64_t n,
                    int64_t k, void* stream);
 
