@@ -76,6 +76,8 @@ DeviceKernel k_mfma_bf16_64("mfma_gemm", "mfma_linear_bf16_t64");
 DeviceKernel k_mfma_bf16_128("mfma_gemm", "mfma_linear_bf16_t128");
 DeviceKernel k_mfma_splitk("mfma_gemm", "mfma_linear_f32_splitk_t64");
 DeviceKernel k_splitk_reduce("mfma_gemm", "splitk_reduce_f32");
+DeviceKernel k_mfma_conv_splitk("mfma_gemm", "mfma_conv2d_f32_splitk_t64");
+DeviceKernel k_conv_splitk_reduce("mfma_gemm", "conv_splitk_reduce_f32");
 
 // Split count of an fp32 linear: 64 x 64 tiles are split over K (chunks of at least 1024) until
 // there are about 512 workgroups (two per CU); 1 = no split.
@@ -226,14 +228,26 @@ int dli_hip_conv2d(int dtype, const void* x, const void* weight, const void* bia
                    int64_t kernel_w, int64_t out_h, int64_t out_w, int64_t stride_h,
                    int64_t stride_w, int64_t pad_h, int64_t pad_w, void* stream) {
   return dli_hip_conv2d_act(dtype, x, weight, bias, out, n, in_c, h, w, out_c, kernel_h, kernel_w,
-                            out_h, out_w, stride_h, stride_w, pad_h, pad_w, DLI_ACT_NONE, stream);
+                            out_h, out_w, stride_h, stride_w, pad_h, pad_w, DLI_ACT_NONE, nullptr,
+                            0, stream);
+}
+
+size_t dli_hip_conv2d_workspace(int dtype, int64_t n, int64_t in_c, int64_t out_c,
+                                int64_t kernel_h, int64_t kernel_w, int64_t out_h, int64_t out_w) {
+  if (dtype != DLI_F32 || n <= 0 || in_c <= 0 || out_c <= 0 || kernel_h <= 0 || kernel_w <= 0 ||
+      out_h <= 0 || out_w <= 0)
+    return 0;
+  const int64_t pixels = n * out_h * out_w;
+  if (bigTiles(out_c, pixels)) return 0;
+  const int64_t splits = linearSplits(out_c, pixels, in_c * kernel_h * kernel_w);
+  return splits > 1 ? static_cast<size_t>(splits * out_c * pixels) * sizeof(float) : 0;
 }
 
 int dli_hip_conv2d_act(int dtype, const void* x, const void* weight, const void* bias, void* out,
                        int64_t n, int64_t in_c, int64_t h, int64_t w, int64_t out_c,
                        int64_t kernel_h, int64_t kernel_w, int64_t out_h, int64_t out_w,
                        int64_t stride_h, int64_t stride_w, int64_t pad_h, int64_t pad_w,
-                       int activation, void* stream) {
+                       int activation, void* workspace, size_t workspace_bytes, void* stream) {
   if (activation != DLI_ACT_NONE && activation != DLI_ACT_RELU)
     return badArg("conv2d", "unknown activation");
   if (stride_h <= 0 || stride_w <= 0 || pad_h < 0 || pad_w < 0)
@@ -248,13 +262,30 @@ int dli_hip_conv2d_act(int dtype, const void* x, const void* weight, const void*
   // fp32: implicit GEMM on MFMA, 32-bit index math (every element index below 2^31)
   const int64_t pixels = n * out_h * out_w, patch = in_c * kernel_h * kernel_w;
   const int64_t limit = int64_t{1} << 31;
-  if (dtype == DLI_F32 && n * in_c * h * w < limit && total < limit && out_c * patch < limit &&
+  if (dtype == DLI_F32 && kernel_h < 65536 && kernel_w < 65536 && n * in_c * h * w < limit &&
+      total < limit && out_c * patch < limit &&
       pixels < limit && (out_h - 1) * stride_h + kernel_h < limit &&
       (out_w - 1) * stride_w + kernel_w < limit) {
     const bool big = bigTiles(out_c, pixels);
     const int64_t tile = big ? 128 : 64;
+    auto i32 = [](int64_t v) { return static_cast<int>(v); };
+    const int64_t splits = big ? 1 : linearSplits(out_c, pixels, patch);
+    const size_t need = static_cast<size_t>(splits * out_c * pixels) * sizeof(float);
+    if (splits > 1 && workspace != nullptr && workspace_bytes >= need &&
+        (out_c + 63) / 64 <= kMaxGridY) {
+      const int64_t per = (patch + splits - 1) / splits;
+      int rc = launch(k_mfma_conv_splitk,
+                      {static_cast<unsigned>((pixels + 63) / 64),
+                       static_cast<unsigned>((out_c + 63) / 64), static_cast<unsigned>(splits)},
+                      {256}, 0, stream, x, weight, workspace, i32(n), i32(in_c), i32(h), i32(w),
+                      i32(out_c), i32(kernel_h), i32(kernel_w), i32(out_h), i32(out_w),
+                      i32(stride_h), i32(stride_w), i32(pad_h), i32(pad_w), i32(per));
+      if (rc != 0) return rc;
+      return launch(k_conv_splitk_reduce, {strideBlocks(out_c * pixels)}, {256}, 0, stream,
+                    workspace, bias, out, out_c, pixels, out_h * out_w,
+                    static_cast<int>(splits), relu);
+    }
     if ((out_c + tile - 1) / tile <= kMaxGridY) {
-      auto i32 = [](int64_t v) { return static_cast<int>(v); };
       return launch(big ? k_mfma_conv128 : k_mfma_conv64,
                     {static_cast<unsigned>((pixels + tile - 1) / tile),
                      static_cast<unsigned>((out_c + tile - 1) / tile)},

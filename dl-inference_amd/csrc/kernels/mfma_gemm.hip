@@ -10,8 +10,9 @@
 //                           x while staging (never materialised); out NCHW, optional fused ReLU
 //  mfma_linear_bf16_<t>     bf16 x, w (K % 8 == 0), bf16 MFMA 16x16x32, fp32 accumulation,
 //                           bf16 or fp32 out, optional ReLU
-//  mfma_linear_f32_splitk   fp32 linear with K split over grid.z into a workspace, then
-//  + splitk_reduce_f32      a fixed-order sum with bias and ReLU
+//  mfma_linear_f32_splitk   fp32 linear / conv2d with K split over grid.z into a workspace,
+//  mfma_conv2d_f32_splitk   then a fixed-order sum with bias and ReLU (splitk_reduce_f32,
+//                           conv_splitk_reduce_f32)
 //
 // Work split: a 256-thread workgroup owns a BM x BN tile of C (4 waves, 2 x 2, each BM/2 x BN/2
 // as 16 x 16 MFMA tiles) and walks K in BK-wide slices. A slice of A and B is loaded from global
@@ -54,42 +55,85 @@ struct KRows {  // p[k * ld + row] (matmul's b [K, N])
   }
 };
 
-// Patch element k = (c, ky, kx) of output pixel `row` = (n, oy, ox) of a zero-padded NCHW conv.
-// 32-bit index math (the host checks that every index fits).
+// Source hooks used by gemmF32 (no-ops for the plain layouts): begin() once per workgroup,
+// prepare() for every K slice before it is fetched (threads < BK fill a per-slice table),
+// load(row, k, kl, tab) with kl = k - slice start.
+struct NoTable {
+  __device__ __forceinline__ void begin(int64_t, int, int) {}
+  template <int BK>
+  __device__ __forceinline__ void prepareT(int64_t, int, int2*) const {}
+};
+
+struct RowsKT : RowsK, NoTable {
+  __device__ __forceinline__ float load(int64_t row, int64_t k, int, const int2*) const {
+    return RowsK::load(row, k);
+  }
+};
+
+struct KRowsT : KRows, NoTable {
+  __device__ __forceinline__ float load(int64_t row, int64_t k, int, const int2*) const {
+    return KRows::load(row, k);
+  }
+};
+
+// Input patch of a zero-padded NCHW conv: column `row` = output pixel (n, oy, ox), k = (c, ky,
+// kx) over k_base + [0, K). The tile's columns are fixed per thread (row = c0 + t % BN), so
+// begin() decomposes the pixel once; prepare() tabulates (c * H * W + ky * W + kx, ky, kx) for
+// the BK k of a slice, and a load is a table read, two bounds checks and one gather. 32-bit
+// index math (the host checks that every index fits).
 struct ConvPatch {
   static constexpr bool kFastK = false;
   const float* x;
-  int rows, K, C, H, W, KH, KW, OH, OW, SH, SW, PH, PW;
-  __device__ __forceinline__ float load(int64_t row64, int64_t k64) const {
-    const int row = static_cast<int>(row64), k = static_cast<int>(k64);
-    if (row >= rows || k >= K) return 0.f;
-    const int ox = row % OW, t = row / OW;
-    const int oy = t % OH, n = t / OH;
-    const int khw = KH * KW;
-    const int c = k / khw, rem = k - c * khw;
-    const int ky = rem / KW, kx = rem - ky * KW;
-    const int iy = oy * SH + ky - PH, ix = ox * SW + kx - PW;
+  int rows, K, k_base, C, H, W, KH, KW, OH, OW, SH, SW, PH, PW;
+  bool valid = false;
+  int iy0 = 0, ix0 = 0, base = 0;
+  __device__ __forceinline__ void begin(int64_t c0, int t, int bn) {
+    const int pixel = static_cast<int>(c0) + t % bn;
+    valid = pixel < rows;
+    const int ox = pixel % OW, q = pixel / OW;
+    const int oy = q % OH, n = q / OH;
+    iy0 = oy * SH - PH;
+    ix0 = ox * SW - PW;
+    base = n * C * H * W + iy0 * W + ix0;
+  }
+  template <int BK>
+  __device__ __forceinline__ void prepareT(int64_t k0, int t, int2* tab) const {
+    const int k = static_cast<int>(k0) + t;
+    if (t < BK && k < K) {
+      const int kk = k_base + k, khw = KH * KW;
+      const int c = kk / khw, rem = kk - c * khw;
+      const int ky = rem / KW, kx = rem - ky * KW;
+      tab[t] = int2{(c * H + ky) * W + kx, (ky << 16) | kx};
+    }
+  }
+  __device__ __forceinline__ float load(int64_t, int64_t k, int kl, const int2* tab) const {
+    if (!valid || k >= K) return 0.f;
+    const int2 e = tab[kl];
+    const int iy = iy0 + (e.y >> 16), ix = ix0 + (e.y & 0xFFFF);
     if (iy < 0 || iy >= H || ix < 0 || ix >= W) return 0.f;
-    return gp(x)[((n * C + c) * H + iy) * W + ix];
+    return gp(x)[base + e.x];
   }
 };
 
 // ---- fp32 core ---------------------------------------------------------------------------------
-// v_mfma_f32_16x16x4_f32: lane l supplies A[l % 16][l / 16] and B[l / 16][l % 16] and receives
-// D[(l / 16) * 4 + i][l % 16], i < 4.
+// v_mfma_f32_16x16x4_f32: lane l supplies A[l % 16][kk] and B[kk][l % 16] for the step's k
+// index kk = l / 16 and receives D[(l / 16) * 4 + i][l % 16], i < 4.
 template <int BM, int BN, class ASrc, class BSrc, class Epi>
-__device__ __forceinline__ void gemmF32(const ASrc& A, const BSrc& B, int64_t R, int64_t Cn,
-                                        int64_t K, const Epi& epi) {
-  constexpr int BK = 32, LDK = BK + 4;  // pitch 36: the 16 rows x 4 k of a fragment read hit
-                                        // 64 distinct banks
+__device__ __forceinline__ void gemmF32(ASrc A, BSrc B, int64_t R, int64_t Cn, int64_t K,
+                                        const Epi& epi) {
+  // 32-wide K slices (64 measured no faster on the CNN layers and wastes half a slice when K is
+  // small). Pitch 36 floats: 16-byte aligned rows whose starts fall in distinct banks for the
+  // 16 rows of a fragment read.
+  constexpr int BK = 32, LDK = BK + 4;
   constexpr int TM = BM / 32, TN = BN / 32;
   constexpr int AE = BM * BK / kGemmThreads, BE = BN * BK / kGemmThreads;
-  __shared__ float As[BM * LDK];
-  __shared__ float Bs[BN * LDK];
+  __shared__ __attribute__((aligned(16))) float As[BM * LDK];
+  __shared__ __attribute__((aligned(16))) float Bs[BN * LDK];
   const int t = threadIdx.x, lane = t % kWave, wave = t / kWave;
   const int wr = wave / 2, wc = wave % 2;
   const int64_t r0 = static_cast<int64_t>(blockIdx.y) * BM;
   const int64_t c0 = static_cast<int64_t>(blockIdx.x) * BN;
+  __shared__ int2 ktab[2][BK];  // per-slice k table of a source that has one (double-buffered)
   float ra[AE], rb[BE];
   auto slot = [&](int e, int rows_in_tile, bool fast_k, int& row, int& k) {
     if (fast_k) {
@@ -100,20 +144,21 @@ __device__ __forceinline__ void gemmF32(const ASrc& A, const BSrc& B, int64_t R,
       k = e / rows_in_tile;
     }
   };
-  auto fetch = [&](int64_t k0) {
+  auto fetch = [&](int64_t k0, const int2* tab) {
 #pragma unroll
     for (int i = 0; i < AE; ++i) {
       int row, k;
       slot(t + i * kGemmThreads, BM, ASrc::kFastK, row, k);
-      ra[i] = A.load(r0 + row, k0 + k);
+      ra[i] = A.load(r0 + row, k0 + k, k, tab);
     }
 #pragma unroll
     for (int i = 0; i < BE; ++i) {
       int row, k;
       slot(t + i * kGemmThreads, BN, BSrc::kFastK, row, k);
-      rb[i] = B.load(c0 + row, k0 + k);
+      rb[i] = B.load(c0 + row, k0 + k, k, tab);
     }
   };
+  auto prepare = [&](int64_t k0, int2* tab) { B.template prepareT<BK>(k0, t, tab); };
   auto stash = [&] {
 #pragma unroll
     for (int i = 0; i < AE; ++i) {
@@ -134,24 +179,45 @@ __device__ __forceinline__ void gemmF32(const ASrc& A, const BSrc& B, int64_t R,
 #pragma unroll
     for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
   const int fr = lane % 16, fk = lane / 16;
-  fetch(0);
-  for (int64_t k0 = 0; k0 < K; k0 += BK) {
+  A.begin(r0, t, BM);
+  B.begin(c0, t, BN);
+  prepare(0, ktab[0]);
+  __syncthreads();
+  fetch(0, ktab[0]);
+  int slice = 0;
+  for (int64_t k0 = 0; k0 < K; k0 += BK, ++slice) {
+    // the table of slice + 1 goes to the buffer that slice - 1's fetch read two barriers ago
+    if (k0 + BK < K) prepare(k0 + BK, ktab[(slice + 1) & 1]);
     __syncthreads();  // every wave is done reading the previous slice
     stash();
     __syncthreads();
-    if (k0 + BK < K) fetch(k0 + BK);
+    if (k0 + BK < K) fetch(k0 + BK, ktab[(slice + 1) & 1]);
+    // In each 32-k half of a slice, MFMA step s uses k = fk * 8 + s for lane group fk (A and B alike, so each step is still
+    // a 4-term slice of the dot products): a lane's 8 k of a row are contiguous in LDS and come
+    // in two 16-byte reads.
 #pragma unroll
-    for (int s = 0; s < BK / 4; ++s) {
-      float a[TM], b[TN];
-#pragma unroll
-      for (int i = 0; i < TM; ++i) a[i] = As[(wr * (BM / 2) + i * 16 + fr) * LDK + s * 4 + fk];
-#pragma unroll
-      for (int j = 0; j < TN; ++j) b[j] = Bs[(wc * (BN / 2) + j * 16 + fr) * LDK + s * 4 + fk];
+    for (int kh = 0; kh < BK / 32; ++kh) {
+      float4 a4[TM][2], b4[TN][2];
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < TN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i], b[j], acc[i][j], 0, 0, 0);
+        for (int h = 0; h < 2; ++h)
+          a4[i][h] = *reinterpret_cast<const float4*>(
+              &As[(wr * (BM / 2) + i * 16 + fr) * LDK + kh * 32 + fk * 8 + h * 4]);
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          b4[j][h] = *reinterpret_cast<const float4*>(
+              &Bs[(wc * (BN / 2) + j * 16 + fr) * LDK + kh * 32 + fk * 8 + h * 4]);
+#pragma unroll
+      for (int s = 0; s < 8; ++s)
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(
+                a4[i][s / 4][s % 4], b4[j][s / 4][s % 4], acc[i][j], 0, 0, 0);
     }
   }
 #pragma unroll
@@ -291,26 +357,58 @@ struct ConvOut {
   extern "C" __global__ void __launch_bounds__(kGemmThreads)                                   \
       mfma_linear_f32_t##BM(const float* x, const float* w, const float* bias, float* out,     \
                             int64_t M, int64_t N, int64_t K, int relu) {                       \
-    gemmF32<BM, BN>(RowsK{x, M, K, K}, RowsK{w, N, K, K}, M, N, K,                             \
+    gemmF32<BM, BN>(RowsKT{{x, M, K, K}}, RowsKT{{w, N, K, K}}, M, N, K,                       \
                     RowMajorOut<float, float>{out, bias, N, relu});                            \
   }                                                                                            \
   extern "C" __global__ void __launch_bounds__(kGemmThreads)                                   \
       mfma_matmul_f32_t##BM(const float* a, const float* b, float* out, int64_t M, int64_t N,  \
                             int64_t K) {                                                       \
-    gemmF32<BM, BN>(RowsK{a, M, K, K}, KRows{b, N, K, N}, M, N, K,                             \
+    gemmF32<BM, BN>(RowsKT{{a, M, K, K}}, KRowsT{{b, N, K, N}}, M, N, K,                       \
                     RowMajorOut<float, float>{out, nullptr, N, 0});                            \
   }                                                                                            \
   extern "C" __global__ void __launch_bounds__(kGemmThreads) mfma_conv2d_f32_t##BM(            \
       const float* x, const float* weight, const float* bias, float* out, int N, int C, int H, \
       int W, int OC, int KH, int KW, int OH, int OW, int SH, int SW, int PH, int PW, int relu) { \
     const int K = C * KH * KW, pixels = N * OH * OW;                                           \
-    gemmF32<BM, BN>(RowsK{weight, OC, K, K},                                                   \
-                    ConvPatch{x, pixels, K, C, H, W, KH, KW, OH, OW, SH, SW, PH, PW}, OC,      \
+    gemmF32<BM, BN>(RowsKT{{weight, OC, K, K}},                                                \
+                    ConvPatch{x, pixels, K, 0, C, H, W, KH, KW, OH, OW, SH, SW, PH, PW}, OC,   \
                     pixels, K, ConvOut{out, bias, OC, static_cast<int64_t>(OH) * OW, relu});   \
   }
 
 DK_MFMA_F32(64, 64)
 DK_MFMA_F32(128, 128)
+
+// Split-K conv2d for layers whose output tiles leave CUs with one workgroup: split z takes the
+// patch elements [z * k_per_split, ...) and writes its partial [OC][pixels] tile to part[z];
+// conv_splitk_reduce_f32 sums the splits in order, adds the bias, applies ReLU, writes NCHW.
+extern "C" __global__ void __launch_bounds__(kGemmThreads) mfma_conv2d_f32_splitk_t64(
+    const float* x, const float* weight, float* part, int N, int C, int H, int W, int OC, int KH,
+    int KW, int OH, int OW, int SH, int SW, int PH, int PW, int k_per_split) {
+  const int K = C * KH * KW, pixels = N * OH * OW;
+  const int kb = static_cast<int>(blockIdx.z) * k_per_split;
+  const int kl = K - kb < k_per_split ? K - kb : k_per_split;
+  gemmF32<64, 64>(RowsKT{{weight + kb, OC, kl, K}},
+                  ConvPatch{x, pixels, kl, kb, C, H, W, KH, KW, OH, OW, SH, SW, PH, PW}, OC,
+                  pixels, kl,
+                  RowMajorOut<float, float>{part + static_cast<int64_t>(blockIdx.z) * OC * pixels,
+                                            nullptr, pixels, 0});
+}
+
+extern "C" __global__ void __launch_bounds__(kGemmThreads)
+    conv_splitk_reduce_f32(const float* part, const float* bias, float* out, int64_t OC,
+                           int64_t pixels, int64_t OHW, int splits, int relu) {
+  const int64_t total = OC * pixels;
+  for (int64_t e = static_cast<int64_t>(blockIdx.x) * kGemmThreads + threadIdx.x; e < total;
+       e += static_cast<int64_t>(gridDim.x) * kGemmThreads) {
+    float v = gp(part)[e];
+    for (int z = 1; z < splits; ++z) v += gp(part)[z * total + e];
+    const int64_t oc = e / pixels, pixel = e - oc * pixels;
+    if (bias != nullptr) v += gp(bias)[oc];
+    if (relu) v = fmaxf(v, 0.f);
+    const int64_t n = pixel / OHW, q = pixel - n * OHW;
+    gp(out)[(n * OC + oc) * OHW + q] = v;
+  }
+}
 
 // Split-K fp32 linear for few output tiles and a long K (fully connected layers at small batch):
 // split z = blockIdx.z takes k in [z * k_per_split, (z + 1) * k_per_split) and writes its
@@ -320,7 +418,7 @@ extern "C" __global__ void __launch_bounds__(kGemmThreads)
                                int64_t K, int64_t k_per_split) {
   const int64_t kb = static_cast<int64_t>(blockIdx.z) * k_per_split;
   const int64_t kl = K - kb < k_per_split ? K - kb : k_per_split;
-  gemmF32<64, 64>(RowsK{x + kb, M, kl, K}, RowsK{w + kb, N, kl, K}, M, N, kl,
+  gemmF32<64, 64>(RowsKT{{x + kb, M, kl, K}}, RowsKT{{w + kb, N, kl, K}}, M, N, kl,
                   RowMajorOut<float, float>{part + blockIdx.z * M * N, nullptr, N, 0});
 }
 

@@ -361,9 +361,14 @@ class Conv2dOp final : public Operator {
       throw std::invalid_argument("conv2d bias size must match output channels");
     const int act = activationAttr(attrs, type());
     *out[0] = allocLike(x.dtype(), {n, oc, oh, ow}, x);
-    check(dli_hip_conv2d_act(hipDtype(x.dtype()), ptr(x), ptr(w),
-                             has_bias ? ptr(*in[2]) : nullptr, ptr(*out[0]), n, c, h, wd, oc, kh,
-                             kw, oh, ow, stride[0], stride[1], pad[0], pad[1], act, ctx.stream),
+    const int dt = hipDtype(x.dtype());
+    const std::size_t ws_bytes = dli_hip_conv2d_workspace(dt, n, c, oc, kh, kw, oh, ow);
+    Tensor ws;
+    if (ws_bytes > 0)
+      ws = allocLike(DType::Float32, {static_cast<std::int64_t>(ws_bytes / sizeof(float))}, x);
+    check(dli_hip_conv2d_act(dt, ptr(x), ptr(w), has_bias ? ptr(*in[2]) : nullptr, ptr(*out[0]),
+                             n, c, h, wd, oc, kh, kw, oh, ow, stride[0], stride[1], pad[0],
+                             pad[1], act, ws_bytes > 0 ? ptr(ws) : nullptr, ws_bytes, ctx.stream),
           type());
   }
 };

@@ -65,7 +65,8 @@ _SIGNATURES = {
     "dli_hip_conv2d": [_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p] + [_i64] * 13
     + [_c_void_p],
     "dli_hip_conv2d_act": [_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p] + [_i64] * 13
-    + [_int, _c_void_p],
+    + [_int, _c_void_p, _size, _c_void_p],
+    "dli_hip_conv2d_workspace": [_int] + [_i64] * 7,
     "dli_hip_linear": [_int, _int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64,
                        _c_void_p],
     "dli_hip_linear_act": [_int, _int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64,
@@ -106,6 +107,7 @@ _RESTYPES = {
     "dli_hip_last_error": ctypes.c_char_p,
     "dli_hip_target_arch": ctypes.c_char_p,
     "dli_hip_linear_workspace": _size,
+    "dli_hip_conv2d_workspace": _size,
     "dli_hip_paged_attention_workspace": _size,
     "dli_hip_splitk_workspace": _size,
     "dli_hip_lm_head_argmax_workspace": _size,

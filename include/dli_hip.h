@@ -168,12 +168,17 @@ int dli_hip_conv2d(int dtype, const void* x, const void* weight, const void* bia
 /* dli_hip_conv2d followed by `activation` (DLI_ACT_*), fused into the GEMM epilogue on the
  * MFMA path. No counterpart in the reference, whose graph runs conv2d and relu as two nodes
  * (conv2d/kernel.py:6-49, relu/kernel.py:6); the plugin uses it for a conv2d node with
- * attribute activation = "relu". */
+ * attribute activation = "relu". workspace as for dli_hip_linear_act (NULL: no split). */
 int dli_hip_conv2d_act(int dtype, const void* x, const void* weight, const void* bias,
                        void* out, int64_t n, int64_t in_c, int64_t h, int64_t w, int64_t out_c,
                        int64_t kernel_h, int64_t kernel_w, int64_t out_h, int64_t out_w,
                        int64_t stride_h, int64_t stride_w, int64_t pad_h, int64_t pad_w,
-                       int activation, void* stream);
+                       int activation, void* workspace, size_t workspace_bytes, void* stream);
+/* Workspace bytes that let dli_hip_conv2d_act split an fp32 conv's patch dimension over more
+ * workgroups when its output tiles alone leave CUs idle (0: no split). No zeroing needed; the
+ * splits are summed in a fixed order. */
+size_t dli_hip_conv2d_workspace(int dtype, int64_t n, int64_t in_c, int64_t out_c,
+                                int64_t kernel_h, int64_t kernel_w, int64_t out_h, int64_t out_w);
 
 /* out[m, n] = sum_k x[m, k] * w[n, k] (+ bias[n]) (linear/kernel.py:6-44;
  * linear/template.cc:23-32). x, w, bias share `dtype`; out_dtype is dtype or DLI_F32.

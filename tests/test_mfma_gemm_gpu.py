@@ -93,6 +93,8 @@ CONVS = [  # (N, C, H, W, OC, KH, KW, stride, pad)
     (2, 8, 9, 9, 7, 5, 5, (1, 1), (2, 2)),
     (4, 16, 7, 7, 33, 1, 1, (1, 1), (0, 0)),      # 1x1
     (16, 16, 32, 32, 256, 3, 3, (1, 1), (1, 1)),  # 128 x 128 tiles
+    (2, 256, 8, 8, 256, 3, 3, (1, 1), (1, 1)),    # split-K (2 ways)
+    (2, 512, 6, 6, 64, 3, 3, (1, 1), (1, 1)),     # split-K (4 ways)
 ]
 
 
@@ -107,6 +109,11 @@ def test_conv2d_f32_implicit_gemm(case):
     fused = run_op("conv2d", {"x": x, "weight": w, "bias": b},
                    attrs={**attrs, "activation": "relu"})["output"]
     close_f32(fused, ops.relu(ref))
+    from dli import hip
+
+    oh, ow = (h + 2 * pad[0] - kh) // stride[0] + 1, (w_ + 2 * pad[1] - kw) // stride[1] + 1
+    if c >= 256:  # the plugin passes a workspace, so these split K
+        assert hip.lib().dli_hip_conv2d_workspace(hip.F32, n, c, oc, kh, kw, oh, ow) > 0
     nob = run_op("conv2d", {"x": x, "weight": w}, attrs=attrs)["output"]
     close_f32(nob, ops.conv2d(to_np(x), to_np(w), None, stride, pad))
 
