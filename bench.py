@@ -34,9 +34,10 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", choices=("decode", "alexnet"), default="decode",
+    ap.add_argument("--workload", choices=("decode", "alexnet", "prefill"), default="decode",
                     help="decode (default): the Qwen2 decode step; alexnet: the AlexNet-style "
-                         "fp32 CNN forward (batch 64) on the MFMA GEMM operators")
+                         "fp32 CNN forward (batch 64) on the MFMA GEMM operators; prefill: the "
+                         "operators of one Qwen2 decoder layer at batch 4 x 2048 tokens")
     ap.add_argument("--batch", type=int, default=None, help="decode 32, alexnet 64")
     ap.add_argument("--context", type=int, default=4096)
     ap.add_argument("--layers", type=int, default=None, help="override (for quick local checks)")
@@ -275,6 +276,97 @@ def bench_alexnet(args):
         "device": torch.cuda.get_device_name(0)}), flush=True)
 
 
+BF16_MFMA_PEAK_TFLOPS = 2500.0
+
+
+def bench_prefill(args):
+    """One Qwen2 decoder layer's operators at prefill size (batch 4 x 2048 tokens, hidden 896,
+    14 / 2 heads, head_dim 64, MLP 4864, bf16), each timed on its own through the C ABI with
+    HIP events (--steps launches after --warmup): RMSNorm, the q|k|v, o, gate|up and down
+    projections (tiled bf16 MFMA linear), causal GQA attention (flash-style MFMA kernel),
+    SiLU * up and the residual adds. value = the layer's 274.4 GFLOP over the summed operator
+    times. The operators run on synthetic inputs of their real shapes, not chained."""
+    import torch
+
+    from dli import hip
+
+    B, S, H, Hq, Hkv, D, F = 4, 2048, 896, 14, 2, 64, 4864
+    T = B * S
+    dev = "cuda"
+    g = torch.Generator(device=dev).manual_seed(0)
+
+    def rnd(*shape, scale=1.0):
+        return (torch.randn(shape, generator=g, device=dev) * scale).to(torch.bfloat16)
+
+    stream = torch.cuda.current_stream()
+    sp = stream.cuda_stream
+    x, nw = rnd(T, H), rnd(H)
+    w_qkv, b_qkv = rnd((Hq + 2 * Hkv) * D, H, scale=0.02), rnd((Hq + 2 * Hkv) * D, scale=0.02)
+    w_o, w_gu, w_down = rnd(H, Hq * D, scale=0.02), rnd(2 * F, H, scale=0.02), rnd(H, F, scale=0.02)
+    q, k, v = rnd(B, Hq, S, D), rnd(B, Hkv, S, D), rnd(B, Hkv, S, D)
+    att = torch.empty(B, Hq, S, D, dtype=torch.bfloat16, device=dev)
+    hn = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
+    qkv = torch.empty(T, (Hq + 2 * Hkv) * D, dtype=torch.bfloat16, device=dev)
+    o = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
+    gu = torch.empty(T, 2 * F, dtype=torch.bfloat16, device=dev)
+    act = torch.empty(T, F, dtype=torch.bfloat16, device=dev)
+    dn = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
+    scale = 1.0 / D ** 0.5
+    ops = [  # name, flops, launch
+        ("rms_norm", 0, lambda: hip.call("dli_hip_rms_norm", hip.BF16, x.data_ptr(), nw.data_ptr(),
+                                          hn.data_ptr(), T, H, 1e-6, sp)),
+        ("qkv_proj", 2 * T * H * (Hq + 2 * Hkv) * D,
+         lambda: hip.call("dli_hip_linear", hip.BF16, hip.BF16, hn.data_ptr(), w_qkv.data_ptr(),
+                          b_qkv.data_ptr(), qkv.data_ptr(), T, (Hq + 2 * Hkv) * D, H, sp)),
+        ("attention", 2 * 2 * B * Hq * D * (S * (S + 1) // 2),
+         lambda: hip.call("dli_hip_attention", hip.BF16, q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                          att.data_ptr(), B, Hq, Hkv, S, S, D, 1, scale, sp)),
+        ("o_proj", 2 * T * Hq * D * H,
+         lambda: hip.call("dli_hip_linear", hip.BF16, hip.BF16, att.data_ptr(), w_o.data_ptr(),
+                          None, o.data_ptr(), T, H, Hq * D, sp)),
+        ("residual_add", 0, lambda: hip.call("dli_hip_add", hip.BF16, x.data_ptr(), o.data_ptr(),
+                                              o.data_ptr(), T * H, T * H, sp)),
+        ("post_norm", 0, lambda: hip.call("dli_hip_rms_norm", hip.BF16, o.data_ptr(),
+                                           nw.data_ptr(), hn.data_ptr(), T, H, 1e-6, sp)),
+        ("gate_up_proj", 2 * T * H * 2 * F,
+         lambda: hip.call("dli_hip_linear", hip.BF16, hip.BF16, hn.data_ptr(), w_gu.data_ptr(),
+                          None, gu.data_ptr(), T, 2 * F, H, sp)),
+        ("silu", 0, lambda: hip.call("dli_hip_silu", hip.BF16, gu.data_ptr(), gu.data_ptr(),
+                                      T * F, sp)),
+        ("mul", 0, lambda: hip.call("dli_hip_mul", hip.BF16, gu.data_ptr(), gu.data_ptr(),
+                                     act.data_ptr(), T * F, T * F, sp)),
+        ("down_proj", 2 * T * F * H,
+         lambda: hip.call("dli_hip_linear", hip.BF16, hip.BF16, act.data_ptr(), w_down.data_ptr(),
+                          None, dn.data_ptr(), T, H, F, sp)),
+        ("residual_add2", 0, lambda: hip.call("dli_hip_add", hip.BF16, o.data_ptr(),
+                                               dn.data_ptr(), dn.data_ptr(), T * H, T * H, sp)),
+    ]
+    per = {}
+    for name, flops, fn in ops:
+        us = _time_launches(fn, stream, max(args.steps, 5))
+        per[name] = {"us": round(us, 2),
+                     "tflops": round(flops / (us * 1e-6) / 1e12, 1) if flops else None}
+    total_us = sum(p["us"] for p in per.values())
+    flops = sum(f for _, f, _ in ops)
+    gemm = max((n for n, f, _ in ops if f), key=lambda n: per[n]["us"])
+    gemm_flops = dict((n, f) for n, f, _ in ops)[gemm]
+    top = gemm_flops / (per[gemm]["us"] * 1e-6) / 1e12
+    print(json.dumps({
+        "metric": "Qwen2 decoder-layer prefill bf16 TFLOP/s (operators timed separately)",
+        "value": round(flops / (total_us * 1e-6) / 1e12, 1), "unit": "TFLOP/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(total_us / 1000, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "Qwen2 decoder layer prefill, batch 4 x 2048 tokens, hidden 896, "
+                               "14/2 heads, head_dim 64, MLP 4864", "flops_per_layer": flops},
+        "roofline": {"bound": "mfma", "kernel": gemm, "achieved": round(top, 1),
+                     "peak": BF16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(top / BF16_MFMA_PEAK_TFLOPS, 4), "traffic": None,
+                     "avg_us": per[gemm]["us"], "flops_per_launch": gemm_flops},
+        "ops": per, "cpu_baseline": None,
+        "device": torch.cuda.get_device_name(0)}), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -283,6 +375,9 @@ def main():
         sys.exit(2)
     if args.workload == "alexnet":
         bench_alexnet(args)
+        return
+    if args.workload == "prefill":
+        bench_prefill(args)
         return
 
     import torch

@@ -66,6 +66,7 @@ FloatKernels k_attention("attention", "attention");
 FloatKernels k_paged_attention("attention", "paged_attention");
 FloatKernels k_kv_append("attention", "kv_append");
 FloatKernels k_conv2d("conv", "conv2d");
+DeviceKernel k_flash_attention("flash_attention", "flash_attention_bf16");
 DeviceKernel k_mfma_linear64("mfma_gemm", "mfma_linear_f32_t64");
 DeviceKernel k_mfma_linear128("mfma_gemm", "mfma_linear_f32_t128");
 DeviceKernel k_mfma_matmul64("mfma_gemm", "mfma_matmul_f32_t64");
@@ -417,6 +418,17 @@ int dli_hip_attention(int dtype, const void* q, const void* k, const void* v, vo
   if (batch < 0 || seq_q < 0 || seq_k < 0) return badArg("attention", "negative size");
   const int64_t rows = batch * q_heads * seq_q;
   if (rows == 0) return 0;
+  if (q == nullptr || k == nullptr || v == nullptr || out == nullptr)
+    return badArg("attention", "NULL pointer");
+  // bf16 with head_dim 64 (prefill): flash-style MFMA kernel, 64 queries per workgroup
+  if (dtype == DLI_BF16 && head_dim == 64 && seq_k > 0 && batch * q_heads <= 65535 &&
+      aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out)) {
+    const float log2e = 1.4426950408889634f;
+    return launch(k_flash_attention,
+                  {static_cast<unsigned>((seq_q + 63) / 64), static_cast<unsigned>(batch * q_heads)},
+                  {256}, 0, stream, q, k, v, out, q_heads, kv_heads, seq_q, seq_k, causal,
+                  scale * log2e);
+  }
   if (rows > 0x7fffffff) return badArg("attention", "too many query rows");
   return launch(*ka, {static_cast<unsigned>(rows)}, {64}, 0, stream, q, k, v, out, batch, q_heads,
                 kv_heads, seq_q, seq_k, head_dim, causal, scale);

@@ -1,0 +1,184 @@
+// Flash-style attention for prefill on gfx950: softmax(q k^T * scale [+ causal mask]) v over
+// contiguous bf16 [B, H, S, 64] q / k / v with grouped KV heads (attention/kernel.py:6-62; the
+// same masking as attention.hip: with the causal flag, query i sees keys [0, Sk - Sq + i]).
+//
+// A 256-thread workgroup owns 64 queries of one (batch, q head); wave w owns 16 of them. Keys go
+// by in tiles of 64: the workgroup stages K as [key][d] and V transposed as [d][key] in LDS (the
+// next tile's loads are in flight while the current one is used), and each wave
+//   1. scores the tile transposed, S^T = K Q^T, with v_mfma_f32_16x16x32_bf16 (A = 16 keys x 32 d
+//      from LDS, B = 32 d x 16 queries from registers): lane l then holds the scores of query
+//      l % 16 for keys 4 (l / 16) + i of each 16-key block;
+//   2. runs the online softmax per query (a column of S^T: the lane's 16 values, then lanes
+//      l ^ 16 and l ^ 32) in fp32, base 2, scale folded in;
+//   3. accumulates O^T += V^T P^T with the same MFMA: the lane's probabilities, rounded to bf16,
+//      are already the B operand (8 keys per lane group: 4 from each of two 16-key blocks), and
+//      A takes V^T rows over those same 8 keys from LDS. k order only has to agree between A and
+//      B, so no shuffle of P is needed.
+// Query tiles are walked from the last (most keys under a causal mask) to the first.
+#include "common.h"
+#include "skinny.h"
+
+using namespace dk;
+
+namespace {
+
+constexpr int kFlashThreads = 256;
+constexpr int kD = 64;        // head dim
+constexpr int kTileQ = 64;    // queries per workgroup
+constexpr int kTileK = 64;    // keys per tile
+constexpr int kPitch = 72;    // LDS row pitch in bf16 (144 bytes: 16-byte aligned rows)
+
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float xorMax(float v) {
+  v = fmaxf(v, __shfl_xor(v, 16, kWave));
+  return fmaxf(v, __shfl_xor(v, 32, kWave));
+}
+
+__device__ __forceinline__ float xorSum(float v) {
+  v += __shfl_xor(v, 16, kWave);
+  return v + __shfl_xor(v, 32, kWave);
+}
+
+__device__ void flashAttention(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                               uint16_t* out, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t Sk,
+                               int causal, float scale_log2) {
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[kTileK * kPitch];
+  __shared__ __attribute__((aligned(16))) uint16_t Vt[kD * kPitch];
+  const int t = threadIdx.x, lane = t % kWave, wave = t / kWave;
+  const int r = lane % 16, g = lane / 16;
+  const int64_t bh = blockIdx.y;  // b * Hq + h
+  const int64_t b = bh / Hq, h = bh % Hq;
+  const int64_t kvh = h / (Hq / Hkv);
+  const int64_t q0 = static_cast<int64_t>(gridDim.x - 1 - blockIdx.x) * kTileQ;
+  const uint16_t* kbase = k + (b * Hkv + kvh) * Sk * kD;
+  const uint16_t* vbase = v + (b * Hkv + kvh) * Sk * kD;
+
+  // this lane's query (clamped into range for the loads; its results are not stored)
+  const int64_t qi = q0 + wave * 16 + r;
+  const int64_t qrow = qi < Sq ? qi : Sq - 1;
+  const uint16_t* qp = q + (bh * Sq + qrow) * kD + g * 8;
+  const U128 qf0 = gload16(qp), qf1 = gload16(qp + 32);
+  // keys this query may see, and the keys any query of the workgroup sees
+  const int64_t shift = Sk - Sq;
+  int64_t limit = causal ? shift + qi + 1 : Sk;
+  limit = limit < 0 ? 0 : (limit > Sk ? Sk : limit);
+  int64_t wg_keys = causal ? shift + (q0 + kTileQ) : Sk;
+  wg_keys = wg_keys < 0 ? 0 : (wg_keys > Sk ? Sk : wg_keys);
+
+  // staging: thread t moves 16-byte chunks c = t and t + 256 of the K tile and of the V tile
+  // (row c / 8, columns (c % 8) * 8 ..)
+  U128 kr[2], vr[2];
+  auto fetch = [&](int64_t k0) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int c = t + u * kFlashThreads;
+      const int64_t key = k0 + c / 8;
+      const int64_t off = key * kD + (c % 8) * 8;
+      kr[u] = key < Sk ? gload16(kbase + off) : zero16();
+      vr[u] = key < Sk ? gload16(vbase + off) : zero16();
+    }
+  };
+  auto stash = [&] {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int c = t + u * kFlashThreads;
+      const int key = c / 8, d0 = (c % 8) * 8;
+      *reinterpret_cast<U128*>(&Ks[key * kPitch + d0]) = kr[u];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        Vt[(d0 + 2 * j) * kPitch + key] = static_cast<uint16_t>(vr[u][j] & 0xFFFFu);
+        Vt[(d0 + 2 * j + 1) * kPitch + key] = static_cast<uint16_t>(vr[u][j] >> 16);
+      }
+    }
+  };
+
+  f32x4 o[4];  // O^T tiles: d = 16 dt + 4 g + i, query r
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, l_run = 0.f;
+
+  const int tiles = static_cast<int>((wg_keys + kTileK - 1) / kTileK);
+  if (tiles > 0) fetch(0);
+  for (int kt = 0; kt < tiles; ++kt) {
+    const int64_t k0 = static_cast<int64_t>(kt) * kTileK;
+    __syncthreads();  // the previous tile is no longer read
+    stash();
+    __syncthreads();
+    if (kt + 1 < tiles) fetch(k0 + kTileK);
+
+    // 1. S^T for 4 blocks of 16 keys
+    f32x4 s[4];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      s[kk] = f32x4{0.f, 0.f, 0.f, 0.f};
+      const uint16_t* krow = &Ks[(kk * 16 + r) * kPitch + g * 8];
+      s[kk] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+          asBf16x8(*reinterpret_cast<const U128*>(krow)), asBf16x8(qf0), s[kk], 0, 0, 0);
+      s[kk] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+          asBf16x8(*reinterpret_cast<const U128*>(krow + 32)), asBf16x8(qf1), s[kk], 0, 0, 0);
+    }
+    // 2. online softmax of query r over this tile (masked keys: -inf)
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t key = k0 + kk * 16 + g * 4 + i;
+        const float x = key < limit ? s[kk][i] * scale_log2 : -INFINITY;
+        s[kk][i] = x;
+        tmax = fmaxf(tmax, x);
+      }
+    tmax = xorMax(tmax);
+    const float m_new = fmaxf(m_run, tmax);
+    // a query that has seen no key yet keeps m = -inf and probabilities 0
+    const float base = m_new == -INFINITY ? 0.f : m_new;
+    const float alpha = exp2f(m_run - base);  // 0 while m_run = -inf
+    float psum = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float p = exp2f(s[kk][i] - base);
+        s[kk][i] = p;
+        psum += p;
+      }
+    l_run = l_run * alpha + xorSum(psum);
+    m_run = m_new;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) o[dt] *= alpha;
+    // 3. O^T += V^T P^T, 32 keys per MFMA: blocks (0, 1), then (2, 3)
+#pragma unroll
+    for (int kc = 0; kc < 2; ++kc) {
+      const bf16x4_t lo = __builtin_convertvector(s[2 * kc], bf16x4_t);
+      const bf16x4_t hi = __builtin_convertvector(s[2 * kc + 1], bf16x4_t);
+      const bf16x8 pb = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) {
+        const uint16_t* vrow = &Vt[(dt * 16 + r) * kPitch + kc * 32 + g * 4];
+        const uint2 a0 = *reinterpret_cast<const uint2*>(vrow);
+        const uint2 a1 = *reinterpret_cast<const uint2*>(vrow + 16);
+        const U128 va{a0.x, a0.y, a1.x, a1.y};
+        o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(asBf16x8(va), pb, o[dt], 0, 0, 0);
+      }
+    }
+  }
+  if (qi >= Sq) return;
+  const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
+  uint16_t* orow = out + (bh * Sq + qi) * kD + g * 4;
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) {
+    const uint32_t lo = packBf16x2(o[dt][0] * inv, o[dt][1] * inv);
+    const uint32_t hi = packBf16x2(o[dt][2] * inv, o[dt][3] * inv);
+    *gp(reinterpret_cast<uint2*>(orow + dt * 16)) = uint2{lo, hi};
+  }
+}
+
+}  // namespace
+
+extern "C" __global__ void __launch_bounds__(kFlashThreads)
+    flash_attention_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* out,
+                         int64_t Hq, int64_t Hkv, int64_t Sq, int64_t Sk, int causal,
+                         float scale_log2) {
+  flashAttention(q, k, v, out, Hq, Hkv, Sq, Sk, causal, scale_log2);
+}

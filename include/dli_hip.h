@@ -217,7 +217,9 @@ int dli_hip_rotary(int dtype, const void* q, const void* k, const float* cos_tab
 
 /* Softmax attention over contiguous [B, H, S, D] tensors (attention/kernel.py:6-62), with
  * grouped KV heads (q head h reads kv head h / (q_heads / kv_heads)) and the causal rule
- * key <= (seq_k - seq_q) + query. scale is usually 1/sqrt(head_dim). head_dim <= 256. */
+ * key <= (seq_k - seq_q) + query. scale is usually 1/sqrt(head_dim). head_dim <= 256.
+ * bf16 with head_dim 64 and 16-byte aligned tensors (prefill) runs as a flash-style MFMA
+ * kernel; other cases as one wave per query row. */
 int dli_hip_attention(int dtype, const void* q, const void* k, const void* v, void* out,
                       int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t seq_q,
                       int64_t seq_k, int64_t head_dim, int causal, float scale, void* stream);
