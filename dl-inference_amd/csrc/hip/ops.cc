@@ -80,12 +80,14 @@ DeviceKernel k_splitk_reduce("mfma_gemm", "splitk_reduce_f32");
 DeviceKernel k_mfma_conv_splitk("mfma_gemm", "mfma_conv2d_f32_splitk_t64");
 DeviceKernel k_conv_splitk_reduce("mfma_gemm", "conv_splitk_reduce_f32");
 
-// Split count of an fp32 linear: 64 x 64 tiles are split over K (chunks of at least 1024) until
-// there are about 512 workgroups (two per CU); 1 = no split.
+// Split count of an fp32 linear: 64 x 64 tiles are split over K (chunks of at least 256, eight
+// 32-wide slices) until there are about 512 workgroups (two per CU); 1 = no split. A workgroup
+// walks its K chunk one slice per load round trip, so a few tiles over a long K would otherwise
+// take that many round trips.
 int64_t linearSplits(int64_t m, int64_t n, int64_t k) {
   const int64_t tiles = ((m + 63) / 64) * ((n + 63) / 64);
   int64_t splits = 1;
-  while (splits < 16 && tiles * splits * 2 <= 512 && k / (splits * 2) >= 1024) splits *= 2;
+  while (splits < 16 && tiles * splits * 2 <= 512 && k / (splits * 2) >= 256) splits *= 2;
   return splits;
 }
 
@@ -422,6 +424,7 @@ int dli_hip_attention(int dtype, const void* q, const void* k, const void* v, vo
     return badArg("attention", "NULL pointer");
   // bf16 with head_dim 64 (prefill): flash-style MFMA kernel, 64 queries per workgroup
   if (dtype == DLI_BF16 && head_dim == 64 && seq_k > 0 && batch * q_heads <= 65535 &&
+      seq_q < (int64_t{1} << 30) && seq_k < (int64_t{1} << 30) &&
       aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out)) {
     const float log2e = 1.4426950408889634f;
     return launch(k_flash_attention,

@@ -65,6 +65,11 @@ __device__ void flashAttention(const uint16_t* q, const uint16_t* k, const uint1
   limit = limit < 0 ? 0 : (limit > Sk ? Sk : limit);
   int64_t wg_keys = causal ? shift + (q0 + kTileQ) : Sk;
   wg_keys = wg_keys < 0 ? 0 : (wg_keys > Sk ? Sk : wg_keys);
+  // keys every query of this wave may see (its first query has the fewest): tiles below this
+  // need no mask
+  int64_t wave_keys = causal ? shift + q0 + wave * 16 + 1 : Sk;
+  wave_keys = wave_keys < 0 ? 0 : (wave_keys > Sk ? Sk : wave_keys);
+  const int lim32 = static_cast<int>(limit);
 
   // staging: thread t moves 16-byte chunks c = t and t + 256 of the K tile and of the V tile
   // (row c / 8, columns (c % 8) * 8 ..)
@@ -120,15 +125,25 @@ __device__ void flashAttention(const uint16_t* q, const uint16_t* k, const uint1
     }
     // 2. online softmax of query r over this tile (masked keys: -inf)
     float tmax = -INFINITY;
+    if (k0 + kTileK <= wave_keys) {  // uniform over the wave: every key visible
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk)
+      for (int kk = 0; kk < 4; ++kk)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int64_t key = k0 + kk * 16 + g * 4 + i;
-        const float x = key < limit ? s[kk][i] * scale_log2 : -INFINITY;
-        s[kk][i] = x;
-        tmax = fmaxf(tmax, x);
-      }
+        for (int i = 0; i < 4; ++i) {
+          s[kk][i] *= scale_log2;
+          tmax = fmaxf(tmax, s[kk][i]);
+        }
+    } else {
+      const int key0 = static_cast<int>(k0) + g * 4;  // sequence lengths < 2^30 (host check)
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float x = key0 + kk * 16 + i < lim32 ? s[kk][i] * scale_log2 : -INFINITY;
+          s[kk][i] = x;
+          tmax = fmaxf(tmax, x);
+        }
+    }
     tmax = xorMax(tmax);
     const float m_new = fmaxf(m_run, tmax);
     // a query that has seen no key yet keeps m = -inf and probabilities 0
