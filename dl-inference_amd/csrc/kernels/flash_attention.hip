@@ -26,7 +26,11 @@ constexpr int kFlashThreads = 256;
 constexpr int kD = 64;        // head dim
 constexpr int kTileQ = 64;    // queries per workgroup
 constexpr int kTileK = 64;    // keys per tile
-constexpr int kPitch = 72;    // LDS row pitch in bf16 (144 bytes: 16-byte aligned rows)
+constexpr int kPitch = 72;    // K row pitch in bf16 (144 bytes: 16-byte aligned rows)
+// V^T row pitch in bf16 (136 bytes: 8-byte aligned for the fragment reads). The stash writes
+// 4-byte words to rows d0 + j of 8 column groups d0 = 8m: at 34 words per row those rows start
+// 16 banks apart (at 36 words, every other group landed on the same banks).
+constexpr int kVPitch = 68;
 
 typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
 
@@ -44,7 +48,7 @@ __device__ void flashAttention(const uint16_t* q, const uint16_t* k, const uint1
                                uint16_t* out, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t Sk,
                                int causal, float scale_log2) {
   __shared__ __attribute__((aligned(16))) uint16_t Ks[kTileK * kPitch];
-  __shared__ __attribute__((aligned(16))) uint16_t Vt[kD * kPitch];
+  __shared__ __attribute__((aligned(16))) uint16_t Vt[kD * kVPitch];
   const int t = threadIdx.x, lane = t % kWave, wave = t / kWave;
   const int r = lane % 16, g = lane / 16;
   const int64_t bh = blockIdx.y;  // b * Hq + h
@@ -71,30 +75,31 @@ __device__ void flashAttention(const uint16_t* q, const uint16_t* k, const uint1
   wave_keys = wave_keys < 0 ? 0 : (wave_keys > Sk ? Sk : wave_keys);
   const int lim32 = static_cast<int>(limit);
 
-  // staging: thread t moves 16-byte chunks c = t and t + 256 of the K tile and of the V tile
-  // (row c / 8, columns (c % 8) * 8 ..)
+  // staging: thread t moves the 16-byte chunks of keys 2 (t / 8) and 2 (t / 8) + 1 at columns
+  // d0 = (t % 8) * 8 of the K tile and of the V tile. Two adjacent keys of the same columns let
+  // the transposed V store write 4-byte words (keys 2p, 2p + 1 of one d).
+  const int pair_key = 2 * (t / 8), d0 = (t % 8) * 8;
   U128 kr[2], vr[2];
   auto fetch = [&](int64_t k0) {
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-      const int c = t + u * kFlashThreads;
-      const int64_t key = k0 + c / 8;
-      const int64_t off = key * kD + (c % 8) * 8;
+      const int64_t key = k0 + pair_key + u;
+      const int64_t off = key * kD + d0;
       kr[u] = key < Sk ? gload16(kbase + off) : zero16();
       vr[u] = key < Sk ? gload16(vbase + off) : zero16();
     }
   };
   auto stash = [&] {
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int c = t + u * kFlashThreads;
-      const int key = c / 8, d0 = (c % 8) * 8;
-      *reinterpret_cast<U128*>(&Ks[key * kPitch + d0]) = kr[u];
+    for (int u = 0; u < 2; ++u)
+      *reinterpret_cast<U128*>(&Ks[(pair_key + u) * kPitch + d0]) = kr[u];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        Vt[(d0 + 2 * j) * kPitch + key] = static_cast<uint16_t>(vr[u][j] & 0xFFFFu);
-        Vt[(d0 + 2 * j + 1) * kPitch + key] = static_cast<uint16_t>(vr[u][j] >> 16);
-      }
+    for (int j = 0; j < 4; ++j) {
+      // vr[u][j] = (V[key u][d0 + 2j], V[key u][d0 + 2j + 1]) as lo | hi << 16
+      const uint32_t even = (vr[0][j] & 0xFFFFu) | (vr[1][j] << 16);
+      const uint32_t odd = (vr[0][j] >> 16) | (vr[1][j] & 0xFFFF0000u);
+      *reinterpret_cast<uint32_t*>(&Vt[(d0 + 2 * j) * kVPitch + pair_key]) = even;
+      *reinterpret_cast<uint32_t*>(&Vt[(d0 + 2 * j + 1) * kVPitch + pair_key]) = odd;
     }
   };
 
@@ -170,7 +175,7 @@ __device__ void flashAttention(const uint16_t* q, const uint16_t* k, const uint1
       const bf16x8 pb = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) {
-        const uint16_t* vrow = &Vt[(dt * 16 + r) * kPitch + kc * 32 + g * 4];
+        const uint16_t* vrow = &Vt[(dt * 16 + r) * kVPitch + kc * 32 + g * 4];
         const uint2 a0 = *reinterpret_cast<const uint2*>(vrow);
         const uint2 a1 = *reinterpret_cast<const uint2*>(vrow + 16);
         const U128 va{a0.x, a0.y, a1.x, a1.y};
