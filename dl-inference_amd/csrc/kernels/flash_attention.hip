@@ -9,7 +9,7 @@
 //      from LDS, B = 32 d x 16 queries from registers): lane l then holds the scores of query
 //      l % 16 for keys 4 (l / 16) + i of each 16-key block;
 //   2. runs the online softmax per query (a column of S^T: the lane's 16 values, then lanes
-//      l ^ 16 and l ^ 32) in fp32, base 2, scale folded in;
+//      l ^ 16 and l ^ 32 through permlane swaps) in fp32, base 2, scale folded in;
 //   3. accumulates O^T += V^T P^T with the same MFMA: the lane's probabilities, rounded to bf16,
 //      are already the B operand (8 keys per lane group: 4 from each of two 16-key blocks), and
 //      A takes V^T rows over those same 8 keys from LDS. k order only has to agree between A and
@@ -33,16 +33,6 @@ constexpr int kPitch = 72;    // K row pitch in bf16 (144 bytes: 16-byte aligned
 constexpr int kVPitch = 68;
 
 typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ float xorMax(float v) {
-  v = fmaxf(v, __shfl_xor(v, 16, kWave));
-  return fmaxf(v, __shfl_xor(v, 32, kWave));
-}
-
-__device__ __forceinline__ float xorSum(float v) {
-  v += __shfl_xor(v, 16, kWave);
-  return v + __shfl_xor(v, 32, kWave);
-}
 
 __device__ void flashAttention(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                                uint16_t* out, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t Sk,
@@ -128,42 +118,42 @@ __device__ void flashAttention(const uint16_t* q, const uint16_t* k, const uint1
       s[kk] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
           asBf16x8(*reinterpret_cast<const U128*>(krow + 32)), asBf16x8(qf1), s[kk], 0, 0, 0);
     }
-    // 2. online softmax of query r over this tile (masked keys: -inf)
+    // 2. online softmax of query r over this tile (masked keys: -inf). The running max is kept
+    // in scaled units; max(s * c) = c * max(s) for the positive scale c, so each probability is
+    // one fma and one v_exp_f32 (every argument <= 0 or -inf, results in [0, 1], no range
+    // reduction needed).
     float tmax = -INFINITY;
     if (k0 + kTileK <= wave_keys) {  // uniform over the wave: every key visible
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          s[kk][i] *= scale_log2;
-          tmax = fmaxf(tmax, s[kk][i]);
-        }
+        for (int i = 0; i < 4; ++i) tmax = fmaxf(tmax, s[kk][i]);
     } else {
       const int key0 = static_cast<int>(k0) + g * 4;  // sequence lengths < 2^30 (host check)
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float x = key0 + kk * 16 + i < lim32 ? s[kk][i] * scale_log2 : -INFINITY;
+          const float x = key0 + kk * 16 + i < lim32 ? s[kk][i] : -INFINITY;
           s[kk][i] = x;
           tmax = fmaxf(tmax, x);
         }
     }
-    tmax = xorMax(tmax);
-    const float m_new = fmaxf(m_run, tmax);
+    tmax = rowsMax(tmax);  // over lanes r, r + 16, r + 32, r + 48: the query's 64 keys
+    const float m_new = fmaxf(m_run, tmax * scale_log2);
     // a query that has seen no key yet keeps m = -inf and probabilities 0
     const float base = m_new == -INFINITY ? 0.f : m_new;
-    const float alpha = exp2f(m_run - base);  // 0 while m_run = -inf
+    const float alpha = __builtin_amdgcn_exp2f(m_run - base);  // 0 while m_run = -inf
     float psum = 0.f;
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float p = exp2f(s[kk][i] - base);
+        const float p = __builtin_amdgcn_exp2f(fmaf(s[kk][i], scale_log2, -base));
         s[kk][i] = p;
         psum += p;
       }
-    l_run = l_run * alpha + xorSum(psum);
+    l_run = l_run * alpha + rowsSum(psum);
     m_run = m_new;
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) o[dt] *= alpha;
