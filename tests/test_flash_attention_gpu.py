@@ -26,6 +26,8 @@ CASES = [  # B, Hq, Hkv, Sq, Sk
     (1, 4, 2, 37, 200),    # fewer queries than keys (cache prefix)
     (1, 2, 2, 130, 70),    # more queries than keys: the first queries see no key when causal
     (3, 6, 3, 257, 257),
+    (2, 16, 4, 2000, 2000),  # long, ragged last query tile
+    (4, 16, 2, 1000, 1100),  # long, with a cache prefix
 ]
 
 
