@@ -118,17 +118,42 @@ struct ConvPatch {
 // ---- fp32 core ---------------------------------------------------------------------------------
 // v_mfma_f32_16x16x4_f32: lane l supplies A[l % 16][kk] and B[kk][l % 16] for the step's k
 // index kk = l / 16 and receives D[(l / 16) * 4 + i][l % 16], i < 4.
+// LDS layout of one operand's K slice, chosen by how the source is staged:
+//   kFastK (lanes take consecutive k of a row): [row][k], pitch BK + 4 floats (16-byte aligned
+//     rows whose starts fall in distinct banks for the 16 rows of a fragment read), and a
+//     lane's 4 consecutive k come in one 16-byte read;
+//   otherwise (lanes take consecutive rows): [k][row], pitch ROWS + 2, so the stash writes
+//     consecutive words and the four lane groups of a fragment read (k 8 apart) start 16
+//     banks apart; 4 single reads.
+template <bool kFastK, int ROWS, int BK>
+struct SliceLayout {
+  static constexpr int kPitch = kFastK ? BK + 4 : ROWS + 2;
+  static constexpr int kFloats = kFastK ? ROWS * kPitch : BK * kPitch;
+  __device__ __forceinline__ static int at(int row, int k) {
+    return kFastK ? row * kPitch + k : k * kPitch + row;
+  }
+  // x[row][k .. k + 3], k a multiple of 4
+  __device__ __forceinline__ static float4 four(const float* x, int row, int k) {
+    if constexpr (kFastK) {
+      return *reinterpret_cast<const float4*>(&x[at(row, k)]);
+    } else {
+      return float4{x[at(row, k)], x[at(row, k + 1)], x[at(row, k + 2)], x[at(row, k + 3)]};
+    }
+  }
+};
+
 template <int BM, int BN, class ASrc, class BSrc, class Epi>
 __device__ __forceinline__ void gemmF32(ASrc A, BSrc B, int64_t R, int64_t Cn, int64_t K,
                                         const Epi& epi) {
   // 32-wide K slices (64 measured no faster on the CNN layers and wastes half a slice when K is
-  // small). Pitch 36 floats: 16-byte aligned rows whose starts fall in distinct banks for the
-  // 16 rows of a fragment read.
-  constexpr int BK = 32, LDK = BK + 4;
+  // small).
+  constexpr int BK = 32;
+  using LA = SliceLayout<ASrc::kFastK, BM, BK>;
+  using LB = SliceLayout<BSrc::kFastK, BN, BK>;
   constexpr int TM = BM / 32, TN = BN / 32;
   constexpr int AE = BM * BK / kGemmThreads, BE = BN * BK / kGemmThreads;
-  __shared__ __attribute__((aligned(16))) float As[BM * LDK];
-  __shared__ __attribute__((aligned(16))) float Bs[BN * LDK];
+  __shared__ __attribute__((aligned(16))) float As[LA::kFloats];
+  __shared__ __attribute__((aligned(16))) float Bs[LB::kFloats];
   const int t = threadIdx.x, lane = t % kWave, wave = t / kWave;
   const int wr = wave / 2, wc = wave % 2;
   const int64_t r0 = static_cast<int64_t>(blockIdx.y) * BM;
@@ -164,13 +189,13 @@ __device__ __forceinline__ void gemmF32(ASrc A, BSrc B, int64_t R, int64_t Cn, i
     for (int i = 0; i < AE; ++i) {
       int row, k;
       slot(t + i * kGemmThreads, BM, ASrc::kFastK, row, k);
-      As[row * LDK + k] = ra[i];
+      As[LA::at(row, k)] = ra[i];
     }
 #pragma unroll
     for (int i = 0; i < BE; ++i) {
       int row, k;
       slot(t + i * kGemmThreads, BN, BSrc::kFastK, row, k);
-      Bs[row * LDK + k] = rb[i];
+      Bs[LB::at(row, k)] = rb[i];
     }
   };
   f32x4 acc[TM][TN];
@@ -192,9 +217,8 @@ __device__ __forceinline__ void gemmF32(ASrc A, BSrc B, int64_t R, int64_t Cn, i
     stash();
     __syncthreads();
     if (k0 + BK < K) fetch(k0 + BK, ktab[(slice + 1) & 1]);
-    // In each 32-k half of a slice, MFMA step s uses k = fk * 8 + s for lane group fk (A and B alike, so each step is still
-    // a 4-term slice of the dot products): a lane's 8 k of a row are contiguous in LDS and come
-    // in two 16-byte reads.
+    // In each 32-k half of a slice, MFMA step s uses k = fk * 8 + s for lane group fk (A and B
+    // alike, so each step is still a 4-term slice of the dot products).
 #pragma unroll
     for (int kh = 0; kh < BK / 32; ++kh) {
       float4 a4[TM][2], b4[TN][2];
@@ -202,14 +226,12 @@ __device__ __forceinline__ void gemmF32(ASrc A, BSrc B, int64_t R, int64_t Cn, i
       for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int h = 0; h < 2; ++h)
-          a4[i][h] = *reinterpret_cast<const float4*>(
-              &As[(wr * (BM / 2) + i * 16 + fr) * LDK + kh * 32 + fk * 8 + h * 4]);
+          a4[i][h] = LA::four(As, wr * (BM / 2) + i * 16 + fr, kh * 32 + fk * 8 + h * 4);
 #pragma unroll
       for (int j = 0; j < TN; ++j)
 #pragma unroll
         for (int h = 0; h < 2; ++h)
-          b4[j][h] = *reinterpret_cast<const float4*>(
-              &Bs[(wc * (BN / 2) + j * 16 + fr) * LDK + kh * 32 + fk * 8 + h * 4]);
+          b4[j][h] = LB::four(Bs, wc * (BN / 2) + j * 16 + fr, kh * 32 + fk * 8 + h * 4);
 #pragma unroll
       for (int s = 0; s < 8; ++s)
 #pragma unroll
