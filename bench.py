@@ -371,7 +371,8 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 "
-                                   "(multi-GPU decode is data-parallel by batch, see DESIGN.md)"}))
+                                   "(multi-GPU decode would be data-parallel by batch: each GPU its own "
+                                   "sequences and KV cache, no per-step collective)"}))
         sys.exit(2)
     if args.workload == "alexnet":
         bench_alexnet(args)
