@@ -58,3 +58,23 @@ def test_cpp_driver_from_files(tmp_path):
     d = dli.GreedyDecoder(engine, dli.Graph.from_json_file(str(graph_path)), weights, BATCH,
                           max_seq_len=MAX_SEQ)
     assert torch.equal(d.generate(prompt, STEPS), expect)
+
+
+@pytest.mark.slow
+def test_cpp_driver_qwen2_0_5b_shape_matches_python_session():
+    """Full Qwen2-0.5B shape through the decoder stack: batch 32, 512 random prompt tokens, 64
+    greedy tokens; the C++ driver and the Python session replay the same captured step, so
+    their tokens are equal."""
+    from dli_qwen2 import QWEN2_0_5B
+
+    cfg, b, prompt_len, steps = QWEN2_0_5B, 32, 512, 64
+    w = random_weights(cfg, seed=71, device="cuda")
+    prompt = torch.randint(0, cfg.vocab, (b, prompt_len), generator=torch.Generator().manual_seed(72))
+    session = DecodeSession(cfg, w, b, max_seq_len=prompt_len + steps + 8, stack=True).capture()
+    expect = session.generate(prompt.cuda(), steps).cpu()
+    del session
+    engine = dli.Engine().load_plugin()
+    d = dli.GreedyDecoder(engine, build_decode_graph(cfg, b, fused=True, stack=True),
+                          pack_fused_weights(cfg, w, drop_unfused=True), b,
+                          max_seq_len=prompt_len + steps + 8)
+    assert torch.equal(d.generate(prompt, steps), expect)
