@@ -206,7 +206,18 @@ size_t dli_hip_lm_head_argmax_workspace(int64_t m, int64_t vocab) {
 int dli_hip_lm_head_argmax(const void* xn, const void* w, void* logits, int logits_dtype,
                            int64_t* ids, int64_t m, int64_t vocab, int64_t hidden_size,
                            void* workspace, size_t workspace_bytes, void* stream) {
+  return dli_hip_lm_head_argmax_norm(xn, nullptr, 0.f, w, logits, logits_dtype, ids, m, vocab,
+                                     hidden_size, workspace, workspace_bytes, stream);
+}
+
+int dli_hip_lm_head_argmax_norm(const void* x, const void* norm_weight, float eps, const void* w,
+                                void* logits, int logits_dtype, int64_t* ids, int64_t m,
+                                int64_t vocab, int64_t hidden_size, void* workspace,
+                                size_t workspace_bytes, void* stream) {
   const char* op = "lm_head_argmax";
+  const void* xn = x;
+  if (norm_weight != nullptr && (hidden_size % 64 != 0 || !aligned16(norm_weight)))
+    return bad(op, "norm weight needs hidden_size % 64 == 0 and 16-byte alignment");
   if (int rc = checkSkinny(op, m, hidden_size)) return rc;
   if (hidden_size > kMaxLmK) return bad(op, "hidden_size above 1024 is not supported");
   if (vocab <= 0 || vocab >= (int64_t{1} << 31)) return bad(op, "vocab must be in [1, 2^31)");
@@ -224,7 +235,7 @@ int dli_hip_lm_head_argmax(const void* xn, const void* w, void* logits, int logi
   const int logits_f32 = logits_dtype == DLI_F32 ? 1 : 0;
   if (int rc = launch(*k_lm_head.pick(m), {blocks}, {kThreads}, 0, stream,
                       xn, w, logits, logits_f32, part_val, part_idx, static_cast<int>(m), vocab,
-                      static_cast<int>(hidden_size)))
+                      static_cast<int>(hidden_size), norm_weight, eps))
     return rc;
   return launch(k_argmax_final, {static_cast<unsigned>(m)}, {kThreads}, 0, stream,
                 static_cast<const float*>(part_val), static_cast<const int32_t*>(part_idx),

@@ -16,8 +16,9 @@
 //  gate_up_silu            [optional RMSNorm of x in registers] -> gate/up = xn W^T ->
 //                          bf16(bf16(silu(gate)) * up) (weights interleaved in 16-row blocks:
 //                          [gate 16 rows | up 16 rows] per output block of 16)
-//  lm_head_argmax          logits = xn W^T (fp32) -> logits out + per-tile argmax partials;
-//                          argmax_finalize reduces them (first index of the maximum)
+//  lm_head_argmax          [optional final RMSNorm of x in registers] -> logits = xn W^T
+//                          (fp32) -> logits out + per-tile argmax partials; argmax_finalize
+//                          reduces them (first index of the maximum)
 // qkv_rope_append, gate_up_silu and lm_head_argmax walk their weight tiles grid-strided
 // (tileLoop), sized by the host to the workgroups that are resident at once, so the weight
 // stream never waits on a second dispatch round.
@@ -164,16 +165,21 @@ constexpr int kLmQuarters = kLmTileN / 4;
 
 // Logits of vocab tiles of 32 rows (grid-strided over the workgroups) plus each tile's argmax
 // partial per row: part_*[m * tiles + t]. Requires K / 64 <= 4 * kWaves.
+// With norm_w non-NULL, xn is the un-normalized residual stream and its final RMSNorm
+// (model.norm, bf16 output) is applied in registers first (tileLoop's prologue).
 template <int MB>
 __device__ void lm_head_argmax_impl(const uint16_t* xn, const uint16_t* w, void* logits,
                                     int logits_f32, float* part_val, int32_t* part_idx, int M,
-                                    int64_t V, int K) {
+                                    int64_t V, int K, const uint16_t* norm_w, float eps) {
   using Core = SkinnyCore<2, MB, kWaves>;
   static_assert(Core::kTileN == kLmTileN, "lm_head tile");
+  // the tile reductions, then the argmax quarters (inside the reductions' area) or, during the
+  // prologue only, the RMSNorm row sums (after it)
+  static_assert(kNormLdsFloats<MB, kWaves> <= kLmQuarters * Core::kTileM, "lm_head lds");
   __shared__ float lds[Core::kLdsFloats + kLmQuarters * Core::kTileM];
   __shared__ int lds_arg[kLmQuarters * Core::kTileM];
   const int64_t tiles = (V + Core::kTileN - 1) / Core::kTileN;
-  tileLoop<2, MB, kWaves, 4>(w, XGlobal{xn, K}, V, K, M, lds, nullptr, 0.f, blockIdx.x,
+  tileLoop<2, MB, kWaves, 4>(w, XGlobal{xn, K}, V, K, M, lds, norm_w, eps, blockIdx.x,
                              gridDim.x, INT64_MAX, NoWait{}, [&](int64_t t) {
     const int64_t n0 = t * Core::kTileN;
     if (logits != nullptr) {
@@ -317,8 +323,8 @@ __device__ void argmax_finalize_impl(const float* part_val, const int32_t* part_
   }                                                                                               \
   extern "C" __global__ void __launch_bounds__(kThreads, 2) lm_head_argmax_m##MB(                  \
       const uint16_t* xn, const uint16_t* w, void* logits, int logits_f32, float* part_val,       \
-      int32_t* part_idx, int M, int64_t V, int K) {                                               \
-    lm_head_argmax_impl<MB>(xn, w, logits, logits_f32, part_val, part_idx, M, V, K);              \
+      int32_t* part_idx, int M, int64_t V, int K, const uint16_t* norm_w, float eps) {            \
+    lm_head_argmax_impl<MB>(xn, w, logits, logits_f32, part_val, part_idx, M, V, K, norm_w, eps); \
   }
 
 DK_DECODE_KERNELS(1)

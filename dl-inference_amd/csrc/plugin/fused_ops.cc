@@ -199,20 +199,27 @@ class GateUpSiluOp final : public Operator {
   }
 };
 
-// inputs: xn [B, H], w [V, H]; outputs: (logits [B, V],) next_ids int64 [B]
+// inputs: xn [B, H], w [V, H] (, model.norm weight [H]: x is then the un-normalized residual
+// stream and the final RMSNorm, attr eps, runs in the kernel); outputs: (logits [B, V],)
+// next_ids int64 [B]
 class LmHeadArgmaxOp final : public Operator {
  public:
   std::string type() const override { return "lm_head_argmax"; }
   void compute(const std::vector<const Tensor*>& in, const std::vector<Tensor*>& out,
                const Attributes& attrs, ExecutionContext& ctx) const override {
     if (out.size() != 1 && out.size() != 2) throw std::invalid_argument("lm_head_argmax arity");
-    requireArity(in, out, 2, 2, out.size(), type());
+    requireArity(in, out, 2, 3, out.size(), type());
     requireCudaInputs(in, type());
     for (const Tensor* t : in) requireBf16(*t, type(), "inputs");
     const Tensor &x = *in[0], &w = *in[1];
     const std::int64_t hidden = x.shape().back(), m = rowsOf(x);
     if (w.rank() != 2 || w.dim(1) != hidden)
       throw std::invalid_argument("lm_head_argmax weight shape mismatch");
+    // optional third input: model.norm's weight, the final RMSNorm applied in the kernel
+    const Tensor* norm = in.size() == 3 ? in[2] : nullptr;
+    if (norm != nullptr && static_cast<std::int64_t>(norm->numel()) != hidden)
+      throw std::invalid_argument("lm_head_argmax norm weight must have hidden elements");
+    const float eps = static_cast<float>(attrDouble(attrs, "eps", 1e-6));
     const std::int64_t vocab = w.dim(0);
     const DType logits_dtype = dtypeFromString(attrs.value_or<std::string>("logits_dtype", "float32"));
     Tensor* logits = out.size() == 2 ? out[0] : nullptr;
@@ -221,9 +228,10 @@ class LmHeadArgmaxOp final : public Operator {
     *ids = Tensor::cuda(DType::Int64, {m}, x.deviceId());
     const std::size_t ws_bytes = dli_hip_lm_head_argmax_workspace(m, vocab);
     Tensor ws = Tensor::cuda(DType::Float32, {static_cast<std::int64_t>((ws_bytes + 3) / 4)}, x.deviceId());
-    check(dli_hip_lm_head_argmax(ptr(x), ptr(w), logits ? ptr(*logits) : nullptr,
-                                 hipDtype(logits_dtype), static_cast<std::int64_t*>(ptr(*ids)), m,
-                                 vocab, hidden, ptr(ws), ws_bytes, ctx.stream),
+    check(dli_hip_lm_head_argmax_norm(ptr(x), norm ? ptr(*norm) : nullptr, eps, ptr(w),
+                                      logits ? ptr(*logits) : nullptr, hipDtype(logits_dtype),
+                                      static_cast<std::int64_t*>(ptr(*ids)), m, vocab, hidden,
+                                      ptr(ws), ws_bytes, ctx.stream),
           type());
   }
 };

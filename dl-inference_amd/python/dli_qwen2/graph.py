@@ -7,7 +7,8 @@ grouped KV heads, fp32 logits and an `argmax` node.
 
 fused graph (fused=True): 5 launches per layer on the fused operators of the gfx950 plugin
 (qkv_rope_append and gate_up_silu with their RMSNorm inside, paged_attention, and
-linear_residual for o_proj and for down_proj), then model.norm and one lm_head_argmax node.
+linear_residual for o_proj and for down_proj), then one lm_head_argmax node that also applies
+model.norm.
 Same rounding points, same tensor names for inputs and outputs.
 
 stack graph (fused=True, stack=True): the decoder layers of the fused graph as one
@@ -105,16 +106,20 @@ def _fused_nodes(cfg: Qwen2Config, batch: int, nodes: list, splits: dict, logits
               [f"{t}_gated", f"{p}.mlp.down_proj.weight", f"{t}_after_attention"],
               [f"{t}_output"], {"splits": splits.get("down", 1)})
         h = f"{t}_output"
-    _node(nodes, "model.norm", "rms_norm", [h, "model.norm.weight"], ["norm_hidden"],
-          {"eps": cfg.eps})
-    _node(nodes, "lm_head", "lm_head_argmax", ["norm_hidden", "lm_head.weight"], OUTPUTS,
-          {"logits_dtype": logits_dtype})
+    _head_nodes(cfg, nodes, h, logits_dtype)
+
+
+def _head_nodes(cfg: Qwen2Config, nodes: list, h: str, logits_dtype: str):
+    """model.norm + lm_head + greedy choice as one lm_head_argmax node: the final RMSNorm runs
+    in registers inside the lm_head kernel (its third input is model.norm's weight)."""
+    _node(nodes, "lm_head", "lm_head_argmax", [h, "lm_head.weight", "model.norm.weight"], OUTPUTS,
+          {"logits_dtype": logits_dtype, "eps": cfg.eps})
 
 
 def _stack_nodes(cfg: Qwen2Config, nodes: list, splits: dict, logits_dtype: str,
                  check_status: bool = False):
-    """Every decoder layer in one decoder_stack node (one persistent launch), then model.norm
-    and lm_head_argmax as in the fused graph. Same rounding points and values as the fused
+    """Every decoder layer in one decoder_stack node (one persistent launch), then the head
+    (model.norm inside lm_head_argmax) as in the fused graph. Same rounding points and values as the fused
     graph with o split 1."""
     inputs = ["hidden_states", "positions", "rotary_cos", "rotary_sin"]
     for i in range(cfg.layers):
@@ -128,10 +133,7 @@ def _stack_nodes(cfg: Qwen2Config, nodes: list, splits: dict, logits_dtype: str,
            "head_dim": cfg.head_dim, "eps": cfg.eps,
            "down_splits": splits.get("down", STACK_SPLITS["down"]),
            "kv_cache_prefix": "layer_", "check_status": int(check_status)})
-    _node(nodes, "model.norm", "rms_norm", ["layers_output", "model.norm.weight"], ["norm_hidden"],
-          {"eps": cfg.eps})
-    _node(nodes, "lm_head", "lm_head_argmax", ["norm_hidden", "lm_head.weight"], OUTPUTS,
-          {"logits_dtype": logits_dtype})
+    _head_nodes(cfg, nodes, "layers_output", logits_dtype)
 
 
 # split-K per projection (down_proj's K over 4 workgroups per tile in the fused graph, 3 in the

@@ -319,6 +319,15 @@ size_t dli_hip_lm_head_argmax_workspace(int64_t m, int64_t vocab);
 int dli_hip_lm_head_argmax(const void* xn, const void* w, void* logits, int logits_dtype,
                            int64_t* ids, int64_t m, int64_t vocab, int64_t hidden_size,
                            void* workspace, size_t workspace_bytes, void* stream);
+/* dli_hip_lm_head_argmax of the final RMSNorm of x: xn = bf16(x * rsqrt(mean(x^2) + eps) *
+ * norm_weight) is computed in registers by every workgroup (rms_norm/kernel.py:6-14), so the
+ * model.norm node needs no launch of its own. norm_weight [hidden] may be NULL (x is already
+ * normalized). No counterpart in the reference, where model.norm and lm_head are two nodes
+ * (export.py:420-443). */
+int dli_hip_lm_head_argmax_norm(const void* x, const void* norm_weight, float eps, const void* w,
+                                void* logits, int logits_dtype, int64_t* ids, int64_t m,
+                                int64_t vocab, int64_t hidden_size, void* workspace,
+                                size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------------------
  * 4. Persistent decoder stack: all decoder layers of one batched decode step in one launch

@@ -184,6 +184,30 @@ def test_lm_head_argmax_random_logits_match_oracle():
     np.testing.assert_array_equal(ids[clear], np.argmax(ref, axis=-1)[clear])
 
 
+@pytest.mark.parametrize("B", [1, 5, 32, 48])
+def test_lm_head_argmax_with_final_norm(B):
+    """Third input = model.norm's weight: the final RMSNorm (bf16 output) runs in the kernel's
+    registers. Against the oracle (RMSNorm rounded to bf16, then fp32 logits) and against the
+    separate rms_norm node followed by the two-input form."""
+    H, V = 896, 20000
+    x, nw, w = rand((B, H), 52, 4.0), rand((H,), 53), rand((V, H), 54, 0.05)
+    out = run_op("lm_head_argmax", {"x": x, "w": w, "nw": nw}, outputs=("logits", "ids"),
+                 attrs={"eps": 1e-6})
+    xn = R(ops.rms_norm(to_np(x), to_np(nw), 1e-6))
+    ref = ops.linear(xn, to_np(w))
+    # an element of xn may round to the neighbouring bf16 value (fp32 vs float64 row sums)
+    assert_close(out["logits"], ref, "bfloat16")
+    ids = out["ids"].cpu().numpy()
+    np.testing.assert_array_equal(ids, np.argmax(to_np(out["logits"]), axis=-1))
+    h = run_op("rms_norm", {"x": x, "weight": nw}, attrs={"eps": 1e-6})["output"]
+    two = run_op("lm_head_argmax", {"x": h, "w": w}, outputs=("logits", "ids"))
+    assert_close(out["logits"], to_np(two["logits"]), "bfloat16")
+    top2 = np.sort(ref, axis=-1)[:, -2:]
+    clear = (top2[:, 1] - top2[:, 0]) > 0.05  # winners no rounding of xn can flip
+    np.testing.assert_array_equal(ids[clear], np.argmax(ref, axis=-1)[clear])
+    np.testing.assert_array_equal(ids[clear], two["ids"].cpu().numpy()[clear])
+
+
 @pytest.mark.parametrize("B,positions,max_seq", [
     (8, [0, 1, 63, 64, 65, 1000, 2047, 4095], 4160),  # ragged lengths, partial last blocks
     (32, None, 4160),                                  # the decode workload: every row at 4095
