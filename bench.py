@@ -100,8 +100,8 @@ def time_decode_attention(session, cfg, B, ctx, pos, g, stream, hip, reps=200):
     s_ptr = stream.cuda_stream
 
     def attn():
-        hip.call("dli_hip_paged_attention", hip.BF16, q.data_ptr(), e["key"].data_ptr(),
-                 e["value"].data_ptr(), e["block_table"].data_ptr(), out.data_ptr(), B, cfg.heads,
+        hip.call("dli_hip_paged_attention", hip.BF16, q.data_ptr(), e["key_pool"].data_ptr(),
+                 e["value_pool"].data_ptr(), e["block_table"].data_ptr(), out.data_ptr(), B, cfg.heads,
                  cfg.kv_heads, 1, cfg.head_dim, e["block_size"], e["max_blocks"], 0,
                  pos.data_ptr(), hip.I64, 1, cfg.head_dim ** -0.5, ws.data_ptr(), ws_bytes, s_ptr)
 
@@ -130,8 +130,8 @@ def time_decoder_stack(session, cfg, B, ctx, pos, g, stream, hip, down_splits, r
         t = [session.inputs[n] for n in names]
         layer_bytes += sum(x.numel() * x.element_size() for x in t)
         e = session.engine.kv_cache_entry(f"layer_{i}")
-        layers[i] = hip.DecoderLayer(*[x.data_ptr() for x in t], e["key"].data_ptr(),
-                                     e["value"].data_ptr(), e["block_table"].data_ptr())
+        layers[i] = hip.DecoderLayer(*[x.data_ptr() for x in t], e["key_pool"].data_ptr(),
+                                     e["value_pool"].data_ptr(), e["block_table"].data_ptr())
     e0 = session.engine.kv_cache_entry("layer_0")
     ws_bytes = hip.lib().dli_hip_decoder_stack_workspace(L, B, cfg.hidden, cfg.heads,
                                                           cfg.kv_heads, cfg.head_dim, cfg.ffn,
@@ -146,7 +146,8 @@ def time_decoder_stack(session, cfg, B, ctx, pos, g, stream, hip, down_splits, r
         hip.call("dli_hip_decoder_stack", layers, L, x.data_ptr(), out.data_ptr(),
                  pos.data_ptr(), hip.I64, cos.data_ptr(), sin.data_ptr(), cos.shape[0],
                  e0["block_size"], e0["max_blocks"], B, cfg.hidden, cfg.heads, cfg.kv_heads,
-                 cfg.head_dim, cfg.ffn, cfg.eps, down_splits, ws.data_ptr(), ws_bytes, s_ptr)
+                 cfg.head_dim, cfg.ffn, cfg.eps, down_splits, ws.data_ptr(), ws_bytes, None,
+                 s_ptr)
 
     us = _time_launches(stack, stream, reps)
     aborted = ctypes.c_int()
@@ -410,7 +411,7 @@ def main():
     # seeded synthetic context: positions [0, ctx-1) of every layer's K/V pools
     for i in range(cfg.layers):
         e = session.engine.kv_cache_entry(f"layer_{i}")
-        for pool in (e["key"], e["value"]):
+        for pool in (e["key_pool"], e["value_pool"]):
             pool.copy_(torch.randn(pool.shape, generator=g, device=dev, dtype=torch.float32)
                        .to(pool.dtype))
     torch.cuda.synchronize()

@@ -125,8 +125,8 @@ PYBIND11_MODULE(_dli_native, m) {
             const dli::KVCacheEntry* entry = e.kvCache().get(name);
             if (entry == nullptr) return py::none();
             py::dict d;
-            d["key"] = py::cast(entry->key.torchTensor());
-            d["value"] = py::cast(entry->value.torchTensor());
+            d["key_pool"] = py::cast(entry->key_pool.torchTensor());
+            d["value_pool"] = py::cast(entry->value_pool.torchTensor());
             d["block_table"] = py::cast(entry->block_table.torchTensor());
             d["block_size"] = entry->block_size;
             d["max_blocks"] = entry->max_blocks;
@@ -181,7 +181,9 @@ PYBIND11_MODULE(_dli_native, m) {
             }
             return out.torchTensor();
           },
-          py::arg("prompt"), py::arg("steps"), py::arg("start") = 0);
+          py::arg("prompt"), py::arg("steps"), py::arg("start") = 0)
+      .def("check_status", &dli::GreedyDecoder::checkStatus,
+           py::call_guard<py::gil_scoped_release>());
 
   m.def(
       "load_weights",

@@ -24,9 +24,12 @@ struct GreedyDecoder::Impl {
   GreedyOptions options;
   bool on_device = false;
   int device_id = 0;
-  Tensor ids;        // static step inputs (the captured graph reads these buffers)
+  bool has_status = false;  // the graph lists a "status" output (decoder_stack launch status)
+  Tensor ids;               // static step inputs (the captured graph reads these buffers)
   Tensor positions;
+  Tensor status;            // the status output of the last run (a persistent device word)
   std::unique_ptr<at::cuda::CUDAGraph> hip_graph;
+  std::optional<c10::hip::HIPStream> capture_stream;
   TensorMap captured_out;
 
   Impl(Engine& e, Graph g, TensorMap w, std::int64_t b, GreedyOptions o)
@@ -37,40 +40,73 @@ struct GreedyDecoder::Impl {
                      : nullptr;
   }
 
-  TensorMap runEager() {
-    engine.setStream(currentStream());
-    return engine.run(graph, inputs);
+  TensorMap keepStatus(TensorMap out) {
+    if (has_status) status = out.at("status");
+    return out;
   }
 
-  void capture() {
+  TensorMap runEager() {
+    engine.setStream(currentStream());
+    return keepStatus(engine.run(graph, inputs));
+  }
+
+  // The first step on a device with capture on: the step runs eagerly on the capture stream
+  // with the real ids and positions (so operators are created and every lazily allocated cache
+  // and workspace exists, and nothing but this step's own tokens is written to the KV cache),
+  // then the same step is recorded into a HIP graph that later steps replay.
+  TensorMap runThenCapture() {
+    // the static inputs were written on the current stream
+    c10::hip::getCurrentHIPStream(device_id).synchronize();
     c10::hip::HIPStream stream = c10::hip::getStreamFromPool(false, device_id);
     c10::hip::HIPStreamGuard guard(stream);
     void* const previous = engine.stream();
     engine.setStream(stream.stream());
+    TensorMap first;
     try {
-      // Warm-up on the capture stream: operators are created and every lazily allocated cache
-      // and workspace exists before capture (nothing may be allocated from the device while
-      // the stream is captured). It writes KV position 0, which the first real step rewrites.
-      engine.run(graph, inputs);
+      first = keepStatus(engine.run(graph, inputs));
       stream.synchronize();
-      hip_graph = std::make_unique<at::cuda::CUDAGraph>();
-      hip_graph->capture_begin();
+      auto g = std::make_unique<at::cuda::CUDAGraph>();
+      g->capture_begin();
       try {
         captured_out = engine.run(graph, inputs);
       } catch (...) {
         try {
-          hip_graph->capture_end();
+          g->capture_end();
         } catch (...) {
         }
-        hip_graph.reset();
         throw;
       }
-      hip_graph->capture_end();
+      g->capture_end();
+      hip_graph = std::move(g);
     } catch (...) {
       engine.setStream(previous);
       throw;
     }
     engine.setStream(previous);
+    return first;
+  }
+
+  // One step on the static inputs (already copied in).
+  TensorMap run() {
+    if (hip_graph) {
+      hip_graph->replay();
+      if (has_status) status = captured_out.at("status");
+      return captured_out;
+    }
+    if (on_device && options.capture) return runThenCapture();
+    return runEager();
+  }
+
+  // Raises if a step since the last check reported a failed launch (the graph's status output,
+  // non-zero when a decoder_stack wait gave up and its outputs are invalid), clearing the word.
+  // Synchronizes with the device: called where the caller synchronizes anyway.
+  void checkStatus() {
+    if (!has_status || !status.defined()) return;
+    at::Tensor& word = status.torchTensor();
+    if (word.item<std::int32_t>() == 0) return;
+    word.zero_();
+    throw std::runtime_error(
+        "decode step failed: a decoder_stack workgroup gave up waiting (its outputs are invalid)");
   }
 };
 
@@ -120,8 +156,8 @@ GreedyDecoder::GreedyDecoder(Engine& engine, Graph graph, TensorMap weights, std
   }
   s.inputs["input_ids"] = s.ids;
   s.inputs["positions"] = s.positions;
+  s.has_status = listed(s.graph.outputs, "status");
   engine.kvCache().configure(options.block_size, options.max_seq_len);
-  if (s.on_device && options.capture) s.capture();
 }
 
 GreedyDecoder::~GreedyDecoder() = default;
@@ -140,14 +176,13 @@ TensorMap GreedyDecoder::step(const Tensor& ids, const Tensor& positions) {
   if (lo < 0 || hi >= s.options.max_seq_len)
     throw std::out_of_range("position outside the KV cache capacity [0, " +
                             std::to_string(s.options.max_seq_len) + ")");
+  s.checkStatus();  // a failure of an earlier step (the reads above synchronized)
   s.ids.torchTensor().copy_(ids.torchTensor());
   s.positions.torchTensor().copy_(pos);
-  if (s.hip_graph) {
-    s.hip_graph->replay();
-    return s.captured_out;
-  }
-  return s.runEager();
+  return s.run();
 }
+
+void GreedyDecoder::checkStatus() { impl_->checkStatus(); }
 
 Tensor GreedyDecoder::generate(const Tensor& prompt, std::int64_t steps, std::int64_t start) {
   Impl& s = *impl_;
@@ -160,23 +195,29 @@ Tensor GreedyDecoder::generate(const Tensor& prompt, std::int64_t steps, std::in
   // the last step to run feeds the (steps - 1)-th generated token
   if (start + length + steps - 2 >= s.options.max_seq_len)
     throw std::out_of_range("prompt plus generated tokens exceed max_seq_len");
+  s.checkStatus();
   const at::Device device = s.ids.torchTensor().device();
   const at::Tensor tokens = prompt.torchTensor().to(device).contiguous();
-  at::Tensor pos = at::full({s.batch}, start, at::TensorOptions().dtype(at::kLong).device(device));
+  at::Tensor& pos = s.positions.torchTensor();
+  pos.fill_(start);
   at::Tensor next;
+  // positions are checked above for the whole run, so no step synchronizes with the host
   auto advance = [&](const at::Tensor& in) {
-    TensorMap out = step(Tensor(in), Tensor(pos));
+    s.ids.torchTensor().copy_(in);
+    TensorMap out = s.run();
     next = out.at("next_ids").torchTensor().clone();
     pos.add_(1);
   };
-  for (std::int64_t t = 0; t < length; ++t) advance(tokens.select(1, t).contiguous());
+  for (std::int64_t t = 0; t < length; ++t) advance(tokens.select(1, t));
   std::vector<at::Tensor> generated;
   generated.reserve(static_cast<std::size_t>(steps));
   for (std::int64_t i = 0; i < steps; ++i) {
     generated.push_back(next);
     if (i + 1 < steps) advance(next);
   }
-  return Tensor(at::stack(generated, 1).cpu());
+  Tensor result(at::stack(generated, 1).cpu());  // synchronizes
+  s.checkStatus();
+  return result;
 }
 
 }  // namespace dli

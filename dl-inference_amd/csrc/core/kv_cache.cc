@@ -42,8 +42,8 @@ void allocatePools(KVCacheEntry& e, DType dtype, int device_id) {
   // Zero-filled once, so that attention kernels reading a partially filled block see finite
   // values in the slots they mask out.
   const auto options = at::TensorOptions().dtype(toTorchDType(dtype)).device(at::kCUDA, device_id);
-  e.key = Tensor(at::zeros({blocks, e.heads, e.block_size, e.head_dim}, options));
-  e.value = Tensor(at::zeros({blocks, e.heads, e.head_dim, e.block_size}, options));
+  e.key_pool = Tensor(at::zeros({blocks, e.heads, e.block_size, e.head_dim}, options));
+  e.value_pool = Tensor(at::zeros({blocks, e.heads, e.head_dim, e.block_size}, options));
   e.block_table = identityBlockTable(e.batch, e.max_blocks, device_id);
 }
 
@@ -71,7 +71,7 @@ KVCacheEntry& KVCache::reserve(const std::string& name, DType dtype, std::int64_
   if (KVCacheEntry* existing = find(name)) {
     if (existing->batch != batch || existing->heads != heads || existing->head_dim != head_dim)
       throw std::invalid_argument("KV cache append shape mismatch");
-    if (existing->key.dtype() != dtype) throw std::invalid_argument("KV cache dtype mismatch");
+    if (existing->key_pool.dtype() != dtype) throw std::invalid_argument("KV cache dtype mismatch");
     return *existing;
   }
   if (batch <= 0 || heads <= 0 || head_dim <= 0)
@@ -93,20 +93,20 @@ void KVCache::grow(KVCacheEntry& e, std::int64_t needed_tokens) {
   if (blocks == e.max_blocks) return;
   KVCacheEntry bigger = e;
   bigger.max_blocks = blocks;
-  allocatePools(bigger, e.key.dtype(), e.key.deviceId());
+  allocatePools(bigger, e.key_pool.dtype(), e.key_pool.deviceId());
   // Physical block (b * old_max + i) moves to (b * new_max + i); copy per sequence.
   const std::size_t block_bytes =
-      static_cast<std::size_t>(e.heads * e.block_size * e.head_dim) * byteSize(e.key.dtype());
+      static_cast<std::size_t>(e.heads * e.block_size * e.head_dim) * byteSize(e.key_pool.dtype());
   for (std::int64_t b = 0; b < e.batch; ++b) {
     const std::size_t src = static_cast<std::size_t>(b * e.max_blocks) * block_bytes;
     const std::size_t dst = static_cast<std::size_t>(b * blocks) * block_bytes;
     const std::size_t bytes = static_cast<std::size_t>(e.max_blocks) * block_bytes;
-    hipCheck(dli_hip_memcpy_async(static_cast<char*>(bigger.key.deviceData()) + dst,
-                                  static_cast<const char*>(e.key.deviceData()) + src, bytes,
+    hipCheck(dli_hip_memcpy_async(static_cast<char*>(bigger.key_pool.deviceData()) + dst,
+                                  static_cast<const char*>(e.key_pool.deviceData()) + src, bytes,
                                   DLI_MEMCPY_DEVICE_TO_DEVICE, stream_),
              "KV cache grow");
-    hipCheck(dli_hip_memcpy_async(static_cast<char*>(bigger.value.deviceData()) + dst,
-                                  static_cast<const char*>(e.value.deviceData()) + src, bytes,
+    hipCheck(dli_hip_memcpy_async(static_cast<char*>(bigger.value_pool.deviceData()) + dst,
+                                  static_cast<const char*>(e.value_pool.deviceData()) + src, bytes,
                                   DLI_MEMCPY_DEVICE_TO_DEVICE, stream_),
              "KV cache grow");
   }
@@ -119,7 +119,7 @@ void KVCache::append(const std::string& name, const Tensor& key, const Tensor& v
   const std::int64_t seq = key.dim(2);
   if (e.length + seq > e.capacity()) grow(e, e.length + seq);
   hipCheck(dli_hip_kv_append(hipDtype(key.dtype()), key.deviceData(), value.deviceData(),
-                             e.key.deviceData(), e.value.deviceData(),
+                             e.key_pool.deviceData(), e.value_pool.deviceData(),
                              static_cast<const std::int32_t*>(e.block_table.deviceData()), e.batch,
                              e.heads, seq, e.head_dim, e.block_size, e.max_blocks, e.length,
                              nullptr, DLI_I64, stream_),
@@ -137,7 +137,7 @@ void KVCache::appendAt(const std::string& name, const Tensor& key, const Tensor&
     throw std::invalid_argument("KV cache positions must hold one entry per sequence");
   KVCacheEntry& e = reserve(name, key.dtype(), key.dim(0), key.dim(1), key.dim(3), key.deviceId());
   hipCheck(dli_hip_kv_append(hipDtype(key.dtype()), key.deviceData(), value.deviceData(),
-                             e.key.deviceData(), e.value.deviceData(),
+                             e.key_pool.deviceData(), e.value_pool.deviceData(),
                              static_cast<const std::int32_t*>(e.block_table.deviceData()), e.batch,
                              e.heads, key.dim(2), e.head_dim, e.block_size, e.max_blocks, 0,
                              positions.deviceData(),

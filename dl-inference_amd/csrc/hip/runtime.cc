@@ -50,6 +50,10 @@ struct Runtime {
   Status (*eventDestroy)(EventT) = nullptr;
   Status (*deviceGetAttribute)(int*, int, int) = nullptr;
   Status (*streamIsCapturing)(StreamT, int*) = nullptr;
+  Status (*moduleGetGlobal)(void**, size_t*, ModuleT, const char*) = nullptr;
+  Status (*moduleLaunchCooperativeKernel)(FunctionT, unsigned, unsigned, unsigned, unsigned,
+                                          unsigned, unsigned, unsigned, StreamT, void**) = nullptr;
+  Status (*moduleOccupancy)(int*, FunctionT, int, size_t) = nullptr;
 
   template <typename F>
   bool bind(F& slot, const char* symbol) {
@@ -85,7 +89,10 @@ struct Runtime {
                     bind(eventElapsedTime, "hipEventElapsedTime") &&
                     bind(eventDestroy, "hipEventDestroy") &&
                     bind(deviceGetAttribute, "hipDeviceGetAttribute") &&
-                    bind(streamIsCapturing, "hipStreamIsCapturing");
+                    bind(streamIsCapturing, "hipStreamIsCapturing") &&
+                    bind(moduleGetGlobal, "hipModuleGetGlobal") &&
+                    bind(moduleLaunchCooperativeKernel, "hipModuleLaunchCooperativeKernel") &&
+                    bind(moduleOccupancy, "hipModuleOccupancyMaxActiveBlocksPerMultiprocessor");
     if (!ok) {
       dlclose(handle);
       handle = nullptr;
@@ -224,6 +231,45 @@ int launchRaw(DeviceKernel& kernel, Dim3 grid, Dim3 block, unsigned lds_bytes, v
   return check(runtime().moduleLaunchKernel(fn, grid.x, grid.y, grid.z, block.x, block.y, block.z,
                                             lds_bytes, stream, args, nullptr),
                kernel.name());
+}
+
+int launchResidentRaw(DeviceKernel& kernel, Dim3 grid, Dim3 block, unsigned lds_bytes,
+                      void* stream, void** args) {
+  void* fn = nullptr;
+  if (int rc = kernel.resolve(&fn)) return rc;
+  int per_cu = 0;
+  if (int rc = check(runtime().moduleOccupancy(&per_cu, fn,
+                                               static_cast<int>(block.x * block.y * block.z),
+                                               lds_bytes),
+                     "hipModuleOccupancyMaxActiveBlocksPerMultiprocessor"))
+    return rc;
+  int cus = 0;
+  if (int rc = computeUnits(&cus)) return rc;
+  if (static_cast<int64_t>(grid.x) * grid.y * grid.z > static_cast<int64_t>(per_cu) * cus)
+    return fail(DLI_HIP_EINVAL, std::string(kernel.name()) + ": " +
+                                    std::to_string(grid.x * grid.y * grid.z) +
+                                    " workgroups cannot all be resident (" +
+                                    std::to_string(per_cu) + " per CU, " + std::to_string(cus) +
+                                    " CUs)");
+  int capturing = 0;
+  if (int rc = check(runtime().streamIsCapturing(stream, &capturing), "hipStreamIsCapturing"))
+    return rc;
+  if (capturing != 0)  // a graph node: residency is checked above, the replay launches it
+    return check(runtime().moduleLaunchKernel(fn, grid.x, grid.y, grid.z, block.x, block.y,
+                                              block.z, lds_bytes, stream, args, nullptr),
+                 kernel.name());
+  return check(runtime().moduleLaunchCooperativeKernel(fn, grid.x, grid.y, grid.z, block.x,
+                                                       block.y, block.z, lds_bytes, stream, args),
+               kernel.name());
+}
+
+int moduleGlobal(const char* module, const char* name, void** ptr, size_t* bytes) {
+  if (int rc = requireRuntime()) return rc;
+  int device = 0;
+  if (int rc = check(runtime().getDevice(&device), "hipGetDevice")) return rc;
+  ModuleT loaded = nullptr;
+  if (int rc = loadEmbeddedModule(device, module, &loaded)) return rc;
+  return check(runtime().moduleGetGlobal(ptr, bytes, loaded, name), "hipModuleGetGlobal");
 }
 
 }  // namespace dli::hip

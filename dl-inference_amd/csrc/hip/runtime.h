@@ -49,6 +49,27 @@ class DeviceKernel {
 int launchRaw(DeviceKernel& kernel, Dim3 grid, Dim3 block, unsigned lds_bytes, void* stream,
               void** args);
 
+// launchRaw for a kernel whose workgroups wait on each other (a persistent launch): refuses a
+// grid larger than the device can hold resident at once (occupancy query), and launches
+// cooperatively (hipModuleLaunchCooperativeKernel, which waits until the whole grid can be
+// resident) unless the stream is being captured, where a plain kernel node is recorded.
+int launchResidentRaw(DeviceKernel& kernel, Dim3 grid, Dim3 block, unsigned lds_bytes,
+                      void* stream, void** args);
+
+// Device address and size of the global variable `name` of embedded code object `module`, for
+// the current device (the module is loaded on that device first). hipModuleGetGlobal is the
+// module-API lookup of a __device__ variable: each device that loads the module holds its own
+// copy at its own address.
+int moduleGlobal(const char* module, const char* name, void** ptr, size_t* bytes);
+
+template <typename... Args>
+int launchResident(DeviceKernel& kernel, Dim3 grid, Dim3 block, unsigned lds_bytes,
+                   void* stream, Args... args) {
+  if (grid.x == 0 || grid.y == 0 || grid.z == 0) return 0;
+  void* params[] = {static_cast<void*>(&args)..., nullptr};
+  return launchResidentRaw(kernel, grid, block, lds_bytes, stream, params);
+}
+
 template <typename... Args>
 int launch(DeviceKernel& kernel, Dim3 grid, Dim3 block, unsigned lds_bytes, void* stream,
            Args... args) {

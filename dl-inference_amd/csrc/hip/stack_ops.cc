@@ -131,7 +131,8 @@ int dli_hip_decoder_stack(const DliDecoderLayer* layers, int num_layers, const v
                           int64_t block_size, int64_t max_blocks, int64_t batch,
                           int64_t hidden_size, int64_t q_heads, int64_t kv_heads,
                           int64_t head_dim, int64_t ffn, float eps, int down_splits,
-                          void* workspace, size_t workspace_bytes, void* stream) {
+                          void* workspace, size_t workspace_bytes, unsigned* status,
+                          void* stream) {
   if (layers == nullptr || num_layers < 0) return bad("layers is NULL");
   if (num_layers == 0) return 0;
   if (batch <= 0 || batch > 64) return bad("batch must be in [1, 64]");
@@ -194,6 +195,7 @@ int dli_hip_decoder_stack(const DliDecoderLayer* layers, int num_layers, const v
   a.attn_tag = reinterpret_cast<uint64_t*>(ws + lay.attn_tag);
   a.down_tag = reinterpret_cast<uint64_t*>(ws + lay.down_tag);
   a.sync = reinterpret_cast<unsigned*>(ws + lay.sync);
+  a.status = status;
   a.max_pos = max_pos;
   a.block_size = block_size;
   a.max_blocks = max_blocks;
@@ -235,7 +237,7 @@ int dli_hip_decoder_stack(const DliDecoderLayer* layers, int num_layers, const v
       d.v_pool = static_cast<uint16_t*>(L.value_pool);
       d.block_table = L.block_table;
     }
-    if (int rc = launch(*kernel, {grid}, {kStackThreads}, 0, stream, a)) return rc;
+    if (int rc = launchResident(*kernel, {grid}, {kStackThreads}, 0, stream, a)) return rc;
   }
   return 0;
 }

@@ -43,7 +43,8 @@
 // the abort word set for the host to read (the outputs are then invalid).
 //
 // The counters only grow during a launch; the last workgroup to finish resets them all to zero
-// (except the abort word), so the next launch starts from zero without a memset.
+// (and, when the launch reports into a status word, moves the abort word there), so the next
+// launch starts from zero without a memset.
 #include "decode_attention.h"
 #include "decode_parts.h"
 #include "stack_args.h"
@@ -452,6 +453,15 @@ __device__ void decoderStack(const Args& a) {
     __hip_atomic_store(gp(sync) + i * dli_stack::kLineWords, 0u, __ATOMIC_RELAXED,
                        __HIP_MEMORY_SCOPE_AGENT);
   if (threadIdx.x == 0) {
+    if (a.status != nullptr) {
+      // every other workgroup arrived after its last wait, so a give-up is visible here
+      const unsigned aborted = loadAgent(sync + dli_stack::kAbortWord);
+      if (aborted != 0u) {
+        __hip_atomic_fetch_or(gp(a.status), aborted, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(gp(sync) + dli_stack::kAbortWord, 0u, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
     __hip_atomic_store(gp(sync) + dli_stack::kExitWord, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __hip_atomic_store(gp(sync) + dli_stack::kEpochWord, epoch + 1u, __ATOMIC_RELAXED,
                        __HIP_MEMORY_SCOPE_AGENT);

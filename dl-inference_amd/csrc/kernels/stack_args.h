@@ -39,6 +39,11 @@ struct Args {
   uint64_t* attn_tag;     // attention unit partials, tagged words [M Hq][splits][O, m, l]
   uint64_t* down_tag;     // down_proj split partial tiles, tagged words [tiles][splits][tile]
   unsigned* sync;         // arrival counters (zero before the first launch; left at zero)
+  // Launch status, or NULL. When set, the last workgroup out ORs the abort word into *status
+  // (non-zero: a wait of this launch gave up, its outputs are invalid) and clears the abort word,
+  // so the next launch starts clean; the caller reads and zeroes *status. When NULL the abort word
+  // stays set for dli_hip_decoder_stack_status.
+  unsigned* status;
   // Stage timeline, or NULL: stamp (s_memrealtime, 100 MHz) of event e of workgroup w in layer
   // trace_base + l at trace[((trace_base + l) * grid + w) * kTraceEvents + e] while
   // trace_base + l < trace_layers.

@@ -56,7 +56,10 @@ inline std::vector<std::int64_t> withLast(std::vector<std::int64_t> shape, std::
 // Zero-initialised device scratch kept across calls of one operator instance (split-K partials,
 // attention partials and the arrival counters that kernels leave at zero; the nodes of one
 // operator instance run in stream order). Allocated on first use, outside any captured region
-// in a decode session, and replaced by a larger zeroed buffer when a node needs more.
+// in a decode session, and replaced by a larger zeroed buffer when a node needs more. A replaced
+// buffer is kept alive with the operator (the engine caches one operator per type, so a HIP
+// graph captured earlier may still point at it), and the device is synchronized after the
+// zero fill, which runs on torch's current stream, before any kernel on another stream uses it.
 class PersistentWorkspace {
  public:
   void* get(std::size_t bytes, int device_id) {
@@ -64,14 +67,25 @@ class PersistentWorkspace {
     std::lock_guard<std::mutex> lock(mutex_);
     if (!buffer_.defined() || buffer_.nbytes() < bytes || buffer_.deviceId() != device_id) {
       const auto words = static_cast<std::int64_t>((bytes + 3) / 4);
+      if (buffer_.defined()) retired_.push_back(buffer_);
       buffer_ = Tensor(at::zeros({words}, at::TensorOptions().dtype(at::kInt).device(at::kCUDA, device_id)));
+      if (int rc = dli_hip_device_synchronize())
+        throw std::runtime_error(std::string("workspace zero fill: ") + dli_hip_last_error() +
+                                 " (" + std::to_string(rc) + ")");
     }
     return buffer_.deviceData();
   }
 
+  // The current buffer (int32 words); undefined before the first get().
+  Tensor tensor() const {
+    std::lock_guard<std::mutex> lock(mutex_);
+    return buffer_;
+  }
+
  private:
-  std::mutex mutex_;
+  mutable std::mutex mutex_;
   Tensor buffer_;
+  std::vector<Tensor> retired_;
 };
 
 template <typename Op>

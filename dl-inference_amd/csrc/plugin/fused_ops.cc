@@ -65,7 +65,7 @@ class QkvRopeAppendOp final : public Operator {
     check(dli_hip_qkv_rope_append(
               ptr(x), nw ? ptr(*nw) : nullptr, ptr(w), ptr(b), static_cast<const float*>(ptr(cos)),
               static_cast<const float*>(ptr(sin)), cos.dim(0), ptr(pos), hipDtype(pos.dtype()),
-              ptr(*out[0]), ptr(e.key), ptr(e.value),
+              ptr(*out[0]), ptr(e.key_pool), ptr(e.value_pool),
               static_cast<const std::int32_t*>(ptr(e.block_table)), e.block_size, e.max_blocks, m,
               hidden, hq, hkv, d, eps, ctx.stream),
           type());
@@ -88,13 +88,13 @@ class PagedAttentionOp final : public Operator {
     if (ctx.kv_cache == nullptr) throw std::invalid_argument("paged_attention missing KV cache");
     const KVCacheEntry* e = ctx.kv_cache->get(attrs.require<std::string>("kv_cache"));
     if (e == nullptr) throw std::invalid_argument("paged_attention: unknown kv_cache entry");
-    if (e->batch != q.dim(0) || e->head_dim != q.dim(3) || e->key.dtype() != q.dtype())
+    if (e->batch != q.dim(0) || e->head_dim != q.dim(3) || e->key_pool.dtype() != q.dtype())
       throw std::invalid_argument("paged_attention: q does not match the cache entry");
     const std::int64_t B = q.dim(0), Hq = q.dim(1), D = q.dim(3);
     const float scale = static_cast<float>(attrDouble(attrs, "scale", 1.0 / std::sqrt(static_cast<double>(D))));
     *out[0] = Tensor::cuda(q.dtype(), q.shape(), q.deviceId());
     const std::size_t ws_bytes = dli_hip_paged_attention_workspace(B, Hq, 1, D, e->capacity());
-    check(dli_hip_paged_attention(hipDtype(q.dtype()), ptr(q), ptr(e->key), ptr(e->value),
+    check(dli_hip_paged_attention(hipDtype(q.dtype()), ptr(q), ptr(e->key_pool), ptr(e->value_pool),
                                   static_cast<const std::int32_t*>(ptr(e->block_table)), ptr(*out[0]),
                                   B, Hq, e->heads, 1, D, e->block_size, e->max_blocks, 0, ptr(pos),
                                   hipDtype(pos.dtype()), 1, scale,
@@ -251,7 +251,9 @@ class DecoderStackOp final : public Operator {
     const auto layers = attrs.require<std::int64_t>("layers");
     if (layers < 1 || in.size() != kHead + kPerLayer * static_cast<std::size_t>(layers))
       throw std::invalid_argument("decoder_stack expects 4 + 7 * layers inputs");
-    requireArity(in, out, in.size(), in.size(), 1, type());
+    if (out.size() != 1 && out.size() != 2)
+      throw std::invalid_argument("decoder_stack outputs: hidden (, status)");
+    requireArity(in, out, in.size(), in.size(), out.size(), type());
     requireCudaInputs(in, type());
     const Tensor &x = *in[0], &pos = *in[1], &cos = *in[2], &sin = *in[3];
     requireBf16(x, type(), "hidden");
@@ -297,33 +299,43 @@ class DecoderStackOp final : public Operator {
       }
       table[static_cast<std::size_t>(i)] =
           DliDecoderLayer{ptr(ln1), ptr(wqkv), ptr(bqkv), ptr(wo), ptr(ln2), ptr(wgu), ptr(wd),
-                          ptr(e.key), ptr(e.value),
+                          ptr(e.key_pool), ptr(e.value_pool),
                           static_cast<const std::int32_t*>(ptr(e.block_table))};
     }
     *out[0] = Tensor::cuda(DType::BFloat16, x.shape(), x.deviceId());
     const std::size_t ws_bytes = dli_hip_decoder_stack_workspace(
         static_cast<int>(layers), m, hidden, hq, hkv, d, ffn, max_blocks,
         static_cast<int>(down_splits));
+    // The launch status accumulates in one persistent word per operator instance (the same
+    // buffer every run, so a captured graph keeps reporting into it); the second output, when
+    // the node lists one, is that word. A driver reads it after a synchronization it makes anyway
+    // and zeroes it.
+    void* status = status_.get(sizeof(unsigned), x.deviceId());
     check(dli_hip_decoder_stack(table.data(), static_cast<int>(layers), ptr(x), ptr(*out[0]),
                                 ptr(pos), hipDtype(pos.dtype()),
                                 static_cast<const float*>(ptr(cos)),
                                 static_cast<const float*>(ptr(sin)), cos.dim(0), block_size,
                                 max_blocks, m, hidden, hq, hkv, d, ffn, eps,
                                 static_cast<int>(down_splits),
-                                workspace_.get(ws_bytes, x.deviceId()), ws_bytes, ctx.stream),
+                                workspace_.get(ws_bytes, x.deviceId()), ws_bytes,
+                                static_cast<unsigned*>(status), ctx.stream),
           type());
+    if (out.size() == 2) *out[1] = status_.tensor().withShape({1});
     // check_status (tests): wait for the launch and fail if a wait in it gave up
     if (attrs.value_or<std::int64_t>("check_status", 0) != 0) {
-      int aborted = 0;
-      check(dli_hip_decoder_stack_status(workspace_.get(ws_bytes, x.deviceId()), &aborted,
-                                         ctx.stream),
-            type());
-      if (aborted) throw std::runtime_error("decoder_stack: a workgroup gave up waiting");
+      check(dli_hip_stream_synchronize(ctx.stream), type());
+      at::Tensor word = status_.tensor().torchTensor();
+      const bool aborted = word.item<std::int32_t>() != 0;
+      if (aborted) {
+        word.zero_();
+        throw std::runtime_error("decoder_stack: a workgroup gave up waiting");
+      }
     }
   }
 
  private:
   mutable PersistentWorkspace workspace_;
+  mutable PersistentWorkspace status_;
 };
 
 class ArgmaxOp final : public Operator {

@@ -266,7 +266,7 @@ class AttentionOp final : public Operator {
     const KVCacheEntry& e = *cache.get(cache_name);
     const std::size_t ws_bytes = dli_hip_paged_attention_workspace(B, Hq, Sq, D, e.capacity());
     check(dli_hip_paged_attention(
-              dt, ptr(q), ptr(e.key), ptr(e.value),
+              dt, ptr(q), ptr(e.key_pool), ptr(e.value_pool),
               static_cast<const std::int32_t*>(ptr(e.block_table)), ptr(*out[0]), B, Hq, Hkv, Sq,
               D, e.block_size, e.max_blocks, past, positions ? ptr(*positions) : nullptr,
               positions ? hipDtype(positions->dtype()) : DLI_I64, causal ? 1 : 0, scale,

@@ -98,7 +98,7 @@ _SIGNATURES = {
     "dli_hip_decoder_stack_workspace": [_int] + [_i64] * 7 + [_int],
     "dli_hip_decoder_stack": [_c_void_p, _int, _c_void_p, _c_void_p, _c_void_p, _int, _c_void_p,
                               _c_void_p] + [_i64] * 9 + [_float, _int, _c_void_p, _size,
-                                                         _c_void_p],
+                                                         _c_void_p, _c_void_p],
     "dli_hip_decoder_stack_status": [_c_void_p, ctypes.POINTER(_int), _c_void_p],
     "dli_hip_decoder_stack_trace": [_c_void_p, _int],
     "dli_hip_stream_is_capturing": [_c_void_p, ctypes.POINTER(_int)],

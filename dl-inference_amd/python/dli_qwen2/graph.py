@@ -12,7 +12,10 @@ model.norm.
 Same rounding points, same tensor names for inputs and outputs.
 
 stack graph (fused=True, stack=True): the decoder layers of the fused graph as one
-decoder_stack node (one persistent launch for all layers), bit-identical to the fused graph.
+decoder_stack node (one persistent launch for all layers), bit-identical to the fused graph. It
+has a third output, `status` (int32 [1], the launch status the decoder_stack node accumulates:
+non-zero when a wait in the persistent launch gave up and the step's outputs are invalid), which
+the decode drivers check where they synchronize anyway.
 """
 from __future__ import annotations
 
@@ -128,7 +131,7 @@ def _stack_nodes(cfg: Qwen2Config, nodes: list, splits: dict, logits_dtype: str,
                    f"{p}.self_attn.qkv_proj.bias", f"{p}.self_attn.o_proj.weight",
                    f"{p}.post_attention_layernorm.weight", f"{p}.mlp.gate_up_proj.weight",
                    f"{p}.mlp.down_proj.weight"]
-    _node(nodes, "model.layers", "decoder_stack", inputs, ["layers_output"],
+    _node(nodes, "model.layers", "decoder_stack", inputs, ["layers_output", "status"],
           {"layers": cfg.layers, "q_heads": cfg.heads, "kv_heads": cfg.kv_heads,
            "head_dim": cfg.head_dim, "eps": cfg.eps,
            "down_splits": splits.get("down", STACK_SPLITS["down"]),
@@ -158,8 +161,9 @@ def build_decode_graph(cfg: Qwen2Config, batch: int, fused: bool = True,
     else:
         _reference_nodes(cfg, batch, nodes)
     model_type = "qwen2_decode" if not fused else ("qwen2_decode_stack" if stack else "qwen2_decode_fused")
+    outputs = OUTPUTS + ["status"] if fused and stack else OUTPUTS
     graph = {"format": "dli.graph.v1", "model_type": model_type,
-             "inputs": INPUTS, "outputs": OUTPUTS, "nodes": nodes}
+             "inputs": INPUTS, "outputs": outputs, "nodes": nodes}
     return dli.Graph.from_json(json.dumps(graph))
 
 

@@ -38,11 +38,12 @@ class DecodeSession:
         self.max_seq_len = max_seq_len
         self._graph = None
         self._out = None
+        self._status = None
 
     # -- one step ---------------------------------------------------------------------------
     def run_eager(self, profile=None):
         """One step without graph capture; profile: a dli.ProfileSession timing every node."""
-        return self.engine.run(self.graph, self.inputs, profile=profile)
+        return self._keep_status(self.engine.run(self.graph, self.inputs, profile=profile))
 
     def capture(self, chain_ids: bool = False):
         """Warm up once (loads kernels, allocates caches and scratch), then capture a step.
@@ -57,12 +58,31 @@ class DecodeSession:
                 self.ids.copy_(out["next_ids"])
         self._graph = graph
         self._out = out
+        self._keep_status(out)
         return self
 
+    def check_status(self):
+        """Raises if a step since the last check reported a failed launch: the stack graph's
+        `status` output is non-zero when a wait in the persistent decoder_stack launch gave up
+        (the step's outputs are then invalid). Clears the word. Synchronizes with the device."""
+        status = self._status
+        if status is None or int(status.item()) == 0:
+            return
+        status.zero_()
+        raise RuntimeError("decode step failed: a decoder_stack workgroup gave up waiting "
+                           "(its outputs are invalid)")
+
+    def _keep_status(self, out):
+        if "status" in out:
+            self._status = out["status"]
+        return out
+
     def step(self, ids: torch.Tensor, positions: torch.Tensor):
-        """Runs one decode step for ids [B] at positions [B]; returns (logits, next_ids)."""
+        """Runs one decode step for ids [B] at positions [B]; returns (logits, next_ids). A
+        failed launch of an earlier step raises here (the position check synchronizes)."""
         if int(positions.max()) >= self.max_seq_len:
             raise ValueError("position exceeds the KV cache capacity")
+        self.check_status()
         self.ids.copy_(ids)
         self.positions.copy_(positions)
         if self._graph is not None:
@@ -70,6 +90,7 @@ class DecodeSession:
             out = self._out
         else:
             out = self.run_eager()
+        self._keep_status(out)
         return out["logits"], out["next_ids"]
 
     def replay(self):
@@ -92,4 +113,7 @@ class DecodeSession:
             generated.append(next_ids.clone())
             _, next_ids = self.step(next_ids.clone(), pos)
             pos += 1
-        return torch.stack(generated, dim=1)
+        out = torch.stack(generated, dim=1)
+        torch.cuda.synchronize()
+        self.check_status()
+        return out

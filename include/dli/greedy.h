@@ -14,10 +14,16 @@
 // The prompt is fed one position per step through the same graph (its KV entries are written by
 // the step's own cache appends), then each step's next_ids becomes the next input.
 //
-// On a device, the step is captured once into a HIP graph (ATen's graph capture, so operator
-// outputs come from a private memory pool that stays valid across replays) and replayed per
-// step; the ids and positions are copied into the graph's static input buffers first. With
-// capture off, or for host tensors, every step is an eager Engine::run.
+// On a device, the first step runs eagerly with its real ids and positions (creating operators,
+// caches and workspaces) and is then captured into a HIP graph (ATen's graph capture, so
+// operator outputs come from a private memory pool that stays valid across replays) that every
+// later step replays; the ids and positions are copied into the graph's static input buffers
+// first. With capture off, or for host tensors, every step is an eager Engine::run.
+//
+// A graph that lists an output named "status" (the decoder_stack launch status, non-zero when a
+// wait in the persistent launch gave up and the step's outputs are invalid) is checked where the
+// driver synchronizes with the device anyway: at the start of step() (for earlier steps) and at
+// the end of generate(). A failure raises std::runtime_error and clears the word.
 
 #include <cstdint>
 #include <memory>
@@ -51,8 +57,12 @@ class GreedyDecoder {
   TensorMap step(const Tensor& ids, const Tensor& positions);
 
   // prompt int64 [B, S] (host or device): positions start .. start + S - 1 take the prompt, then
-  // `steps` greedy tokens follow. Returns the generated ids, int64 [B, steps], on the host.
+  // `steps` greedy tokens follow. Returns the generated ids, int64 [B, steps], on the host. No
+  // step synchronizes with the host (the position range is checked once up front).
   Tensor generate(const Tensor& prompt, std::int64_t steps, std::int64_t start = 0);
+
+  // Synchronizes, then raises if a step since the last check reported a failed launch.
+  void checkStatus();
 
  private:
   struct Impl;

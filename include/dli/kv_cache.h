@@ -6,8 +6,8 @@
 // reallocated and fully copied on every append). Here each named entry (one per attention
 // layer) owns two block pools that are allocated once:
 //
-//   key   [num_blocks, heads, block_size, head_dim]   token-major inside a block
-//   value [num_blocks, heads, head_dim, block_size]   dim-major inside a block
+//   key_pool   [num_blocks, heads, block_size, head_dim]   token-major inside a block
+//   value_pool [num_blocks, heads, head_dim, block_size]   dim-major inside a block
 //
 // plus an int32 block table [batch, max_blocks] mapping (sequence, logical block) to a
 // physical block. An append writes only the new tokens (one scatter kernel, no host sync).
@@ -27,9 +27,13 @@
 
 namespace dli {
 
+// The pools are named key_pool / value_pool, not key / value as in the reference's entry
+// (include/dli/kv_cache.h of the reference: contiguous [B,H,S,D] tensors that its attention
+// template binds directly as K and V), so that code written against that layout fails to compile
+// here instead of reading a paged pool as [B,H,S,D].
 struct KVCacheEntry {
-  Tensor key;
-  Tensor value;
+  Tensor key_pool;
+  Tensor value_pool;
   Tensor block_table;  // int32 [batch, max_blocks], device
   std::int64_t batch = 0;
   std::int64_t heads = 0;

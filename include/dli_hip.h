@@ -367,14 +367,21 @@ size_t dli_hip_decoder_stack_workspace(int num_layers, int64_t batch, int64_t hi
  * hidden_size] (hidden_out may equal hidden_in). Each layer appends its new k/v at
  * positions[b] and attends over keys [0, positions[b]]. The workspace must be zero-filled
  * before its first use; every call leaves it ready for the next one on the same stream. Calls
- * that share a workspace must not overlap. */
+ * that share a workspace must not overlap.
+ * The launch is refused when the device cannot hold every workgroup resident at once, and runs
+ * as a cooperative launch outside stream capture. status (device memory, may be NULL): when
+ * non-NULL, a launch in which a wait gave up ORs a non-zero value into *status and clears the
+ * workspace's abort word, so later launches run normally; the caller reads *status after a
+ * synchronization it already makes and zeroes it. With status NULL the abort word stays set for
+ * dli_hip_decoder_stack_status. */
 int dli_hip_decoder_stack(const DliDecoderLayer* layers, int num_layers, const void* hidden_in,
                           void* hidden_out, const void* positions, int positions_dtype,
                           const float* cos_table, const float* sin_table, int64_t max_pos,
                           int64_t block_size, int64_t max_blocks, int64_t batch,
                           int64_t hidden_size, int64_t q_heads, int64_t kv_heads,
                           int64_t head_dim, int64_t ffn, float eps, int down_splits,
-                          void* workspace, size_t workspace_bytes, void* stream);
+                          void* workspace, size_t workspace_bytes, unsigned* status,
+                          void* stream);
 
 /* Sets the key-range split count of MFMA decode attention for every later call of
  * dli_hip_paged_attention and dli_hip_decoder_stack in the process (0 = choose per call: the

@@ -18,6 +18,8 @@ import torch
 import dli
 from support import one_node_graph
 
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
 REF_OPS = ["add", "attention", "batch_norm2d", "conv2d", "embedding", "linear", "matmul",
            "max_pool2d", "mul", "relu", "reshape", "rms_norm", "rotary_embedding", "silu",
            "softmax", "transpose"]
@@ -192,3 +194,24 @@ def test_device_library_has_no_torch_dependency():
     out = subprocess.run(["ldd", dli.hip_library_path()], capture_output=True, text=True,
                          check=True).stdout
     assert "torch" not in out and "c10" not in out
+
+
+def _compile_snippet(tmp_path, body):
+    torch_dir = os.path.dirname(torch.__file__)
+    src = tmp_path / "snippet.cc"
+    src.write_text('#include "dli/kv_cache.h"\nint probe(dli::KVCacheEntry& e) {\n' + body +
+                   "\n  return 0;\n}\n")
+    return subprocess.run(
+        ["g++", "-std=c++20", "-fsyntax-only", f"-I{ROOT}/include",
+         "-isystem", f"{torch_dir}/include", "-isystem",
+         f"{torch_dir}/include/torch/csrc/api/include", str(src)],
+        capture_output=True, text=True)
+
+
+def test_reference_kv_entry_fields_do_not_compile(tmp_path):
+    """Plugin source written against the reference's KV entry (contiguous [B,H,S,D] tensors
+    `key` / `value`, which its attention template binds straight as K and V) must not compile
+    against the paged entry here, whose pools are `key_pool` / `value_pool`."""
+    assert _compile_snippet(tmp_path, "(void)e.key_pool; (void)e.value_pool;").returncode == 0
+    bad = _compile_snippet(tmp_path, "(void)e.key; (void)e.value;")
+    assert bad.returncode != 0 and "key" in bad.stderr

@@ -70,7 +70,7 @@ def test_qkv_rope_append(B, H, hq, hkv, positions, norm):
     k = R(ops.rotary(k, to_np(cos), to_np(sin), positions=pnp))
     assert_close(out, q, "bfloat16")
     entry = e.kv_cache_entry("L")
-    kp, vp, table = to_np(entry["key"]), to_np(entry["value"]), entry["block_table"].cpu().numpy()
+    kp, vp, table = to_np(entry["key_pool"]), to_np(entry["value_pool"]), entry["block_table"].cpu().numpy()
     bs = entry["block_size"]
     for i, p in enumerate(positions):
         blk = table[i, p // bs]
@@ -226,14 +226,14 @@ def test_paged_attention_decode(B, positions, max_seq):
     e.reserve_kv_cache("L", "bfloat16", B, hkv, d)
     entry = e.kv_cache_entry("L")
     g = torch.Generator(device=DEV).manual_seed(60)
-    for pool in (entry["key"], entry["value"]):
+    for pool in (entry["key_pool"], entry["value_pool"]):
         pool.copy_(torch.randn(pool.shape, generator=g, device=DEV).to(pool.dtype))
     q = rand((B, hq, 1, d), 61)
     pos = torch.tensor(positions, dtype=torch.int64, device=DEV)
     for _ in range(2):  # the second call reuses the workspace counters the first left at zero
         out = run_op("paged_attention", {"q": q, "pos": pos}, attrs={"kv_cache": "L"},
                      engine=e)["output"]
-    kp, vp = to_np(entry["key"]), to_np(entry["value"])
+    kp, vp = to_np(entry["key_pool"]), to_np(entry["value_pool"])
     table, bs = entry["block_table"].cpu().numpy(), entry["block_size"]
     for i, p in enumerate(positions):
         n = p + 1

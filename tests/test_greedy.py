@@ -73,3 +73,44 @@ def test_decoder_rejects_bad_graphs_and_arguments():
         d.generate(torch.zeros(3, 2, dtype=torch.int64), 3)
     with pytest.raises(IndexError):  # 6 prompt positions + 3 tokens need positions up to 7 + 1
         d.generate(torch.zeros(2, 6, dtype=torch.int64), 4)
+
+
+def _status_graph():
+    """A decode-step graph with a `status` output, as the decoder_stack graph has: here
+    status = clone(flag) on the host, so the test controls what a step reports."""
+    return dli.Graph.from_json(json.dumps({
+        "format": "dli.graph.v1", "model_type": "greedy_status_test",
+        "inputs": ["input_ids", "positions", "table", "flag"],
+        "outputs": ["next_ids", "status"],
+        "nodes": [
+            {"name": "emb", "op": "aten", "inputs": ["table", "input_ids"],
+             "outputs": ["ids2"], "attrs": {
+                 "name": "aten::embedding", "padding_idx": -1, "scale_grad_by_freq": False,
+                 "sparse": False, "attr_order": ["padding_idx", "scale_grad_by_freq", "sparse"]}},
+            {"name": "pick", "op": "aten", "inputs": ["ids2"], "outputs": ["next_ids"],
+             "attrs": {"name": "aten::select", "overload": "int", "dim": 1, "index": 0,
+                       "attr_order": ["dim", "index"]}},
+            {"name": "status", "op": "aten", "inputs": ["flag"], "outputs": ["status"],
+             "attrs": {"name": "aten::abs"}}]}))
+
+
+def test_decoder_raises_on_a_reported_launch_failure():
+    """A step whose `status` output is non-zero (a decoder_stack wait gave up) makes the next
+    synchronizing call raise; generate() checks once at its end, after its own sync."""
+    e = dli.Engine()
+    table = torch.arange(40, dtype=torch.int64).reshape(10, 4)
+    ok = dli.GreedyDecoder(e, _status_graph(), {"table": table,
+                                                "flag": torch.zeros(1, dtype=torch.int32)}, 2)
+    pos = torch.zeros(2, dtype=torch.int64)
+    ok.step(torch.zeros(2, dtype=torch.int64), pos)
+    ok.step(torch.zeros(2, dtype=torch.int64), pos + 1)
+    ok.check_status()
+
+    bad = dli.GreedyDecoder(e, _status_graph(), {"table": table,
+                                                 "flag": torch.ones(1, dtype=torch.int32)}, 2)
+    bad.step(torch.zeros(2, dtype=torch.int64), pos)  # reports, nothing checked yet
+    with pytest.raises(RuntimeError, match="gave up waiting"):
+        bad.step(torch.zeros(2, dtype=torch.int64), pos + 1)
+    bad.check_status()  # the word was cleared when it was reported
+    with pytest.raises(RuntimeError, match="gave up waiting"):
+        bad.generate(torch.zeros(2, 1, dtype=torch.int64), 2)

@@ -38,12 +38,31 @@ def test_cpp_driver_matches_python_session(stack, capture):
     weights = pack_fused_weights(cfg, w, drop_unfused=True)
     engine = dli.Engine().load_plugin()
     d = dli.GreedyDecoder(engine, graph, weights, BATCH, max_seq_len=MAX_SEQ, capture=capture)
-    assert d.captured == capture
+    assert not d.captured  # the first step runs eagerly, then is captured
     got = d.generate(prompt, STEPS)
+    assert d.captured == capture
     assert got.dtype == torch.int64 and got.shape == (BATCH, STEPS) and not got.is_cuda
     assert torch.equal(got, expect)
     # a second generation from position 0 rewrites the cache and repeats the tokens
     assert torch.equal(d.generate(prompt.cuda(), STEPS), expect)
+
+
+@pytest.mark.parametrize("stack", [False, True], ids=["fused", "stack"])
+def test_cpp_driver_continues_a_cached_prefix(stack):
+    """A decoder built on an engine whose cache already holds a prefix (written by another
+    decoder) continues it exactly: its first step, which precedes the capture, writes only its
+    own position, so generate(start > 0) gives the tokens of one uninterrupted generation."""
+    cfg, w, prompt = _case(53)
+    expect = _python_tokens(cfg, w, prompt, stack)
+    graph = build_decode_graph(cfg, BATCH, fused=True, stack=stack)
+    weights = pack_fused_weights(cfg, w, drop_unfused=True)
+    engine = dli.Engine().load_plugin()
+    first = dli.GreedyDecoder(engine, graph, weights, BATCH, max_seq_len=MAX_SEQ, capture=False)
+    first.generate(prompt[:, :4], 1)  # positions 0..3 hold the prompt's first four tokens
+    second = dli.GreedyDecoder(engine, graph, weights, BATCH, max_seq_len=MAX_SEQ, capture=True)
+    got = second.generate(prompt[:, 4:], STEPS, start=4)
+    assert second.captured
+    assert torch.equal(got, expect)
 
 
 def test_cpp_driver_from_files(tmp_path):

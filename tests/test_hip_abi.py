@@ -110,7 +110,7 @@ def test_decoder_stack_rejects_invalid_arguments():
              batch=32, hidden=896, hq=14, hkv=2, d=64, ffn=4864, splits=4):
         return lib.dli_hip_decoder_stack(layers, n, fake, fake, positions, pos_dtype, fake, fake,
                                          1024, block_size, 64, batch, hidden, hq, hkv, d, ffn,
-                                         1e-6, splits, fake, 1 << 20, None)
+                                         1e-6, splits, fake, 1 << 20, None, None)
 
     assert call(n=0) == 0  # no layers: nothing to do
     assert call(layers=None) == -1

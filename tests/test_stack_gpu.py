@@ -52,8 +52,8 @@ def _assert_same(fused, stack, a, b, layers):
     for i in range(layers):
         ea = fused.engine.kv_cache_entry(f"layer_{i}")
         eb = stack.engine.kv_cache_entry(f"layer_{i}")
-        assert torch.equal(ea["key"], eb["key"]), f"key cache of layer {i} differs"
-        assert torch.equal(ea["value"], eb["value"]), f"value cache of layer {i} differs"
+        assert torch.equal(ea["key_pool"], eb["key_pool"]), f"key cache of layer {i} differs"
+        assert torch.equal(ea["value_pool"], eb["value_pool"]), f"value cache of layer {i} differs"
 
 
 def _pair(cfg, w, batch, max_seq_len, down=1, **kw):
@@ -137,7 +137,7 @@ def _fill_caches(sessions, cfg, seed):
     for i in range(cfg.layers):
         g = torch.Generator(device="cuda").manual_seed(seed + i)
         pools = [sess.engine.kv_cache_entry(f"layer_{i}") for sess in sessions]
-        for name in ("key", "value"):
+        for name in ("key_pool", "value_pool"):
             val = torch.randn(pools[0][name].shape, generator=g, device="cuda").to(torch.bfloat16)
             for p in pools:
                 p[name].copy_(val)
