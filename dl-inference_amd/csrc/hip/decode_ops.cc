@@ -5,6 +5,7 @@
 #include <cstdlib>
 #include <string>
 
+#include "../kernels/scratch.h"
 #include "runtime.h"
 
 namespace dli::hip {
@@ -243,6 +244,61 @@ int dli_hip_lm_head_argmax_norm(const void* x, const void* norm_weight, float ep
 }
 
 }  // extern "C"
+
+namespace dli::hip {
+namespace {
+
+// Device address of the decode module's static `scratch` array on the current device, looked
+// up once per device (with that device current) by name on the loaded module, which also loads
+// the module and the two lm_head kernels there, so later calls load and allocate nothing. Each
+// device holds its own copy at its own address.
+int lmHeadScratch(void** out) {
+  static std::array<std::atomic<void*>, 64> per_device{};
+  static std::mutex mutex;
+  int device = 0;
+  if (int rc = dli_hip_get_device(&device)) return rc;
+  if (device < 0 || device >= 64) return fail(DLI_HIP_EINVAL, "device index out of range");
+  void* p = per_device[device].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    std::lock_guard<std::mutex> lock(mutex);
+    p = per_device[device].load(std::memory_order_relaxed);
+    if (p == nullptr) {
+      size_t bytes = 0;
+      if (int rc = moduleGlobal("decode", "scratch", &p, &bytes)) return rc;
+      if (p == nullptr || bytes != dli_scratch::kLmHeadBytes)
+        return fail(DLI_HIP_ENODEV, "decode module scratch has an unexpected size");
+      void* fn = nullptr;
+      for (DeviceKernel* k : {&k_lm_head.m1, &k_lm_head.m2, &k_lm_head.m4, &k_argmax_final})
+        if (int rc = k->resolve(&fn)) return rc;
+      per_device[device].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return 0;
+}
+
+}  // namespace
+}  // namespace dli::hip
+
+extern "C" int dli_hip_lm_head_argmax_norm_noalloc(const void* x, const void* norm_weight,
+                                                   float eps, const void* w, void* logits,
+                                                   int logits_dtype, int64_t* ids, int64_t m,
+                                                   int64_t vocab, int64_t hidden_size,
+                                                   void* stream) {
+  const char* op = "lm_head_argmax_noalloc";
+  if (int rc = checkSkinny(op, m, hidden_size)) return rc;
+  if (vocab <= 0 || vocab >= (int64_t{1} << 31)) return bad(op, "vocab must be in [1, 2^31)");
+  const size_t need = dli_hip_lm_head_argmax_workspace(m, vocab);
+  if (need > dli_scratch::kLmHeadBytes)
+    return bad(op, "m = " + std::to_string(m) + " rows over vocab " + std::to_string(vocab) +
+                       " need " + std::to_string(need) + " bytes of scratch, above its " +
+                       std::to_string(dli_scratch::kLmHeadBytes) + "-byte maximum");
+  void* scratch = nullptr;
+  if (int rc = lmHeadScratch(&scratch)) return rc;
+  // the same kernels as dli_hip_lm_head_argmax_norm, with the static scratch as the workspace
+  return dli_hip_lm_head_argmax_norm(x, norm_weight, eps, w, logits, logits_dtype, ids, m, vocab,
+                                     hidden_size, scratch, dli_scratch::kLmHeadBytes, stream);
+}
 
 namespace dli::hip {
 

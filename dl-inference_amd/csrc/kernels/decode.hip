@@ -23,8 +23,17 @@
 // (tileLoop), sized by the host to the workgroups that are resident at once, so the weight
 // stream never waits on a second dispatch round.
 #include "decode_parts.h"
+#include "scratch.h"
 
 using namespace dk;
+
+// Device scratch of dli_hip_lm_head_argmax_norm_noalloc (the per-tile argmax partials that the
+// other lm_head entry points keep in a caller's workspace), for callers that cannot allocate.
+// One copy per device that loads this module, zero at load, held until the process ends. Its
+// name stays in the code object's symbol table (no `static`), because the host finds it with
+// hipModuleGetGlobal on the loaded module; host code only ever uses the address that lookup
+// returns.
+__device__ __align__(256) unsigned char scratch[dli_scratch::kLmHeadBytes];
 
 namespace {
 

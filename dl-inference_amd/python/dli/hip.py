@@ -95,6 +95,8 @@ _SIGNATURES = {
     + [_c_void_p, _size, _c_void_p],
     "dli_hip_lm_head_argmax_norm": [_c_void_p, _c_void_p, _float, _c_void_p, _c_void_p, _int,
                                     _c_void_p, _i64, _i64, _i64, _c_void_p, _size, _c_void_p],
+    "dli_hip_lm_head_argmax_norm_noalloc": [_c_void_p, _c_void_p, _float, _c_void_p, _c_void_p,
+                                            _int, _c_void_p, _i64, _i64, _i64, _c_void_p],
     "dli_hip_decoder_stack_workspace": [_int] + [_i64] * 7 + [_int],
     "dli_hip_decoder_stack": [_c_void_p, _int, _c_void_p, _c_void_p, _c_void_p, _int, _c_void_p,
                               _c_void_p] + [_i64] * 9 + [_float, _int, _c_void_p, _size,

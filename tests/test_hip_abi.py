@@ -100,6 +100,18 @@ def test_fused_decode_entry_points_reject_invalid_arguments():
     assert lib.dli_hip_splitk_workspace(896, 32, 4) == 4 * 32 * 896 * 4 + 256
 
 
+def test_noalloc_lm_head_rejects_oversized_calls_before_the_device():
+    """The no-alloc lm_head entry point checks the call against its 4 MiB static scratch first."""
+    lib = hip.load()
+    fake = ctypes.c_void_p(256)  # never dereferenced
+    assert lib.dli_hip_lm_head_argmax_norm_noalloc(fake, None, 1e-6, fake, None, hip.F32, fake,
+                                                   64, 600000, 64, None) == -1
+    assert b"above its 4194304-byte maximum" in lib.dli_hip_last_error()
+    assert lib.dli_hip_lm_head_argmax_norm_noalloc(fake, None, 1e-6, fake, None, hip.F32, fake,
+                                                   65, 1000, 64, None) == -1
+    assert b"batch rows" in lib.dli_hip_last_error()
+
+
 def test_decoder_stack_rejects_invalid_arguments():
     """dli_hip_decoder_stack checks every argument before it touches the device."""
     lib = hip.load()
