@@ -499,7 +499,7 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic",
-        "config": {"workload": "Qwen2-0.5B-shape bf16 greedy decode, batch 32, context 4096",
+        "config": {"workload": f"Qwen2-0.5B-shape bf16 greedy decode, batch {B}, context {ctx}",
                    "model": "qwen2-0.5b-shape (random init)", "global_batch": B,
                    "seq_len": ctx, "layers": cfg.layers, "parallelism": "none (1 GPU)",
                    "graph": ("decoder_stack (one persistent launch for all layers)"

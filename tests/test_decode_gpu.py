@@ -63,10 +63,32 @@ def test_capture_replay_equals_eager():
         assert torch.equal(ia, ib)
 
 
-def _teacher_forced_parity(cfg, w, batch, prompt_len, steps, rows, seed, agree_min, stack=False):
+def _flip_report(logits, ref, exact, gpu_ids, expect):
+    """Per-token check of the steps where the GPU's greedy token differs from the oracle's argmax
+    (same prefix). A flip from the oracle's b to the GPU's a is accepted only as a near-tie:
+    the oracle's margin ref[b] - ref[a] is within 4 sqrt(2) sigma, and each of the two logits the
+    GPU got wrong is within 6 sigma of the oracle's value, where sigma is that step's RMS of
+    (bf16 oracle - fp32 model) over the vocabulary: the rounding noise the graph's bf16 rounding
+    points produce at that step. Returns the flips as dicts; raises on one outside the band."""
+    sigma = (ref - exact).pow(2).mean(-1).sqrt()  # [R, T]
+    flips = []
+    for r, t in (~(gpu_ids == expect)).nonzero().tolist():
+        a, b = int(gpu_ids[r, t]), int(expect[r, t])
+        gap = float(ref[r, t, b] - ref[r, t, a])
+        e_a = float((logits[r, t, a] - ref[r, t, a]).abs())
+        e_b = float((logits[r, t, b] - ref[r, t, b]).abs())
+        sg = float(sigma[r, t])
+        flips.append({"row": r, "step": t, "gpu": a, "oracle": b, "gap": gap, "err_gpu_tok": e_a,
+                      "err_oracle_tok": e_b, "sigma": sg})
+        assert gap <= 4 * 2 ** 0.5 * sg and e_a <= 6 * sg and e_b <= 6 * sg, (
+            f"token flip outside the rounding-noise band: {flips[-1]}")
+    return flips
+
+
+def _teacher_forced_parity(cfg, w, batch, prompt_len, steps, seed, agree_min, stack=False):
     """Free-running greedy decode on the GPU, then the oracle teacher-forced on the GPU's own
-    tokens (one batched CPU pass over prompt + generated tokens), so both score the same
-    prefixes at every step.
+    tokens (one batched CPU pass over prompt + generated tokens) for every row, so both score
+    the same prefixes at every step.
 
     Two bf16 implementations that sum in different orders cannot promise identical tokens or
     logits: every node output is rounded to bf16, and where the two orders round a value
@@ -77,39 +99,41 @@ def _teacher_forced_parity(cfg, w, batch, prompt_len, steps, rows, seed, agree_m
       2. the GPU's logits are no further from the bf16 oracle, and no further from the fp32
          model, than bf16 rounding itself moves the oracle (relative L2 error per step, ratio
          bounds below); a wrong index, sign or operand gives errors of order 1 and fails;
-      3. wherever the GPU token differs from the oracle's argmax, the oracle's own gap between
-         the two is within twice that step's max logit error (a near-tie), and the tokens agree
-         on at least `agree_min` of the steps.
+      3. every token flip passes the per-token near-tie test of _flip_report, and the tokens
+         agree on at least `agree_min` of the (row, step) pairs.
+    The first step at which a row's tokens differ from the oracle's argmax is also the step at
+    which a free-running oracle would first diverge from the GPU (the prefixes agree up to it).
     """
     prompt = _prompt(cfg, batch, prompt_len, seed)
     session = DecodeSession(cfg, w, batch, max_seq_len=prompt_len + steps + 8, stack=stack).capture()
     got = _run_steps(session, prompt, steps - 1)  # logits after the prompt + steps-1 tokens
-    logits = torch.stack([lg[rows] for lg, _ in got], 1)  # [R, T, V]
+    logits = torch.stack([lg for lg, _ in got], 1)  # [B, T, V]
     ids = torch.stack([nx for _, nx in got], 1)  # [B, T]
-    assert torch.equal(ids[rows], torch.argmax(logits, -1)), "next_ids != argmax(logits)"
-    expect, _, ref = Qwen2Oracle(cfg, w).teacher_forced(prompt[rows], ids[rows])
-    _, _, exact = Qwen2Oracle(cfg, w, round_bf16=False).teacher_forced(prompt[rows], ids[rows])
+    assert torch.equal(ids, torch.argmax(logits, -1)), "next_ids != argmax(logits)"
+    expect, _, ref = Qwen2Oracle(cfg, w).teacher_forced(prompt, ids)
+    _, _, exact = Qwen2Oracle(cfg, w, round_bf16=False).teacher_forced(prompt, ids)
 
     def rel(a, b):  # [R, T]
         return (a - b).norm(dim=-1) / b.norm(dim=-1)
 
     err_bf16, err_fp32, noise = rel(logits, ref), rel(logits, exact), rel(ref, exact)
-    print(f"\nteacher-forced parity, rows {rows}, {logits.shape[1]} steps: relative logit error "
-          f"vs bf16 oracle mean {float(err_bf16.mean()):.3e} max {float(err_bf16.max()):.3e}; "
+    print(f"\nteacher-forced parity, {batch} rows, {logits.shape[1]} steps: relative logit "
+          f"error vs bf16 oracle mean {float(err_bf16.mean()):.3e} max {float(err_bf16.max()):.3e}; "
           f"vs fp32 model mean {float(err_fp32.mean()):.3e} max {float(err_fp32.max()):.3e}; "
           f"bf16 oracle vs fp32 model mean {float(noise.mean()):.3e} max {float(noise.max()):.3e}")
     assert float(err_bf16.mean()) <= 1.25 * float(noise.mean())
     assert float(err_fp32.mean()) <= 1.25 * float(noise.mean())
     assert float(err_bf16.max()) <= 1.5 * float(noise.max())
     assert float(err_fp32.max()) <= 1.5 * float(noise.max())
-    max_err = (logits - ref).abs().amax(-1)
-    agree = ids[rows] == expect
-    chosen = ref.gather(-1, ids[rows][..., None])[..., 0]
-    gap = ref.amax(-1) - chosen  # oracle's preference for its argmax over the GPU token
-    bad = (~agree) & (gap > 2 * max_err)
-    assert not bool(bad.any()), f"token flips outside the noise band at {bad.nonzero().tolist()}"
+    flips = _flip_report(logits, ref, exact, ids, expect)
+    agree = ids == expect
     rate = float(agree.float().mean())
-    print(f"token agreement {rate:.3f}, max abs logit error {float(max_err.max()):.3e}")
+    first = [int((~agree[r]).nonzero()[0]) if not bool(agree[r].all()) else None
+             for r in range(batch)]
+    worst = max((f["gap"] / f["sigma"] for f in flips), default=0.0)
+    print(f"token agreement {rate:.3f} over {agree.numel()} (row, step) pairs; {len(flips)} flips, "
+          f"largest oracle margin at a flip {worst:.2f} sigma; first divergence step per row "
+          f"{first}", flush=True)
     assert rate >= agree_min, f"token agreement {rate:.3f} < {agree_min}"
 
 
@@ -117,17 +141,106 @@ def _teacher_forced_parity(cfg, w, batch, prompt_len, steps, rows, seed, agree_m
 def test_tiny_decode_teacher_forced_parity(stack):
     cfg = tiny_config()
     w = random_weights(cfg, seed=31, device="cuda")
-    _teacher_forced_parity(cfg, w, batch=6, prompt_len=12, steps=24, rows=[0, 3, 5], seed=32,
-                           agree_min=0.9, stack=stack)
+    _teacher_forced_parity(cfg, w, batch=6, prompt_len=12, steps=24, seed=32, agree_min=0.9,
+                           stack=stack)
 
 
 @pytest.mark.slow
-@pytest.mark.parametrize("stack", [False, True], ids=["fused", "stack"])
-def test_qwen2_0_5b_shape_64_steps_teacher_forced_parity(stack):
-    """Full Qwen2-0.5B shape, batch 32, 512 random prompt tokens, 64 greedy steps (fused graph,
-    or every layer in the persistent decoder stack); the oracle scores rows 0, 17 and 31 on the
-    CPU."""
+@pytest.mark.parametrize("batch", [1, 8, 32])
+def test_qwen2_0_5b_shape_64_steps_teacher_forced_parity(batch):
+    """Full Qwen2-0.5B shape through the decoder stack (the product graph), 512 random prompt
+    tokens, 64 greedy steps; the oracle scores every row on the CPU."""
     cfg = QWEN2_0_5B
     w = random_weights(cfg, seed=41, device="cuda")
-    _teacher_forced_parity(cfg, w, batch=32, prompt_len=512, steps=64, rows=[0, 17, 31], seed=42,
-                           agree_min=0.9, stack=stack)
+    # measured agreement: 0.969 (batch 1, 64 tokens), 0.947 (batch 8), 0.958 (batch 32)
+    _teacher_forced_parity(cfg, w, batch=batch, prompt_len=512, steps=64, seed=42,
+                           agree_min={1: 0.9, 8: 0.92, 32: 0.93}[batch], stack=True)
+
+
+def _fill_paged_cache(engine, oracle, layers, batch, fill):
+    """Copies the oracle's synthetic context (positions [0, fill) of its preallocated caches)
+    into the paged pools of the engine's cache entries layer_0.. (layouts in
+    include/dli/kv_cache.h: key [blocks, Hkv, 64, D], value [blocks, Hkv, D, 64])."""
+    for i in range(layers):
+        e = engine.kv_cache_entry(f"layer_{i}")
+        bs = e["block_size"]
+        nblk = (fill + bs - 1) // bs
+        table = e["block_table"].long()
+        kp, vp = e["key_pool"], e["value_pool"]
+        hkv, d = kp.shape[1], kp.shape[3]
+        for b in range(batch):
+            k = torch.zeros(hkv, nblk * bs, d)
+            v = torch.zeros(hkv, nblk * bs, d)
+            k[:, :fill] = oracle.k_static[i][b, :, :fill]
+            v[:, :fill] = oracle.v_static[i][b, :, :fill]
+            blocks = table[b, :nblk]
+            kp[blocks] = k.view(hkv, nblk, bs, d).permute(1, 0, 2, 3).to(kp.dtype).cuda()
+            vp[blocks] = v.view(hkv, nblk, bs, d).permute(1, 0, 3, 2).to(vp.dtype).cuda()
+
+
+@pytest.mark.slow
+@pytest.mark.parametrize("batch", [1, 8, 32])
+def test_qwen2_0_5b_shape_step_at_context_4096_matches_oracle(batch):
+    """The bench workload's step: every row at position 4095 over a seeded synthetic context of
+    4095 keys per layer, through the decoder stack; the oracle's preallocated-cache step on the
+    same context. Logits: within the noise bounds of _teacher_forced_parity (relative L2 error
+    against the bf16 oracle and the fp32 model no larger than bf16 rounding moves the oracle);
+    tokens: the oracle's argmax except near-ties (_flip_report)."""
+    cfg, ctx = QWEN2_0_5B, 4096
+    w = random_weights(cfg, seed=43, device="cuda")
+    ids = torch.randint(0, cfg.vocab, (batch,), generator=torch.Generator().manual_seed(44))
+    oracle = Qwen2Oracle(cfg, w)
+    oracle.reset_static(batch, ctx, seed=45, fill=ctx - 1)
+    exact_oracle = Qwen2Oracle(cfg, w, round_bf16=False)
+    exact_oracle.k_static, exact_oracle.v_static = oracle.k_static, oracle.v_static
+    session = DecodeSession(cfg, w, batch, max_seq_len=ctx + 8, stack=True)
+    pos = torch.full((batch,), ctx - 1, dtype=torch.int64, device="cuda")
+    session.step(ids.cuda(), pos)  # creates the cache entries (the context is written next)
+    torch.cuda.synchronize()
+    _fill_paged_cache(session.engine, oracle, cfg.layers, batch, ctx - 1)
+    torch.cuda.synchronize()
+    logits, nxt = session.step(ids.cuda(), pos)
+    logits = logits.float().cpu()[:, None]  # [B, 1, V]
+    nxt = nxt.cpu()[:, None]
+    ref = oracle.step_static(ids, ctx - 1)[:, None]
+    exact = exact_oracle.step_static(ids, ctx - 1)[:, None]
+    session.check_status()
+    assert torch.equal(nxt, torch.argmax(logits, -1))
+
+    def rel(a, b):
+        return (a - b).norm(dim=-1) / b.norm(dim=-1)
+
+    err_bf16, err_fp32, noise = rel(logits, ref), rel(logits, exact), rel(ref, exact)
+    print(f"\ncontext {ctx}, batch {batch}: relative logit error vs bf16 oracle mean "
+          f"{float(err_bf16.mean()):.3e} max {float(err_bf16.max()):.3e}; vs fp32 model mean "
+          f"{float(err_fp32.mean()):.3e} max {float(err_fp32.max()):.3e}; bf16 oracle vs fp32 "
+          f"model mean {float(noise.mean()):.3e} max {float(noise.max()):.3e}", flush=True)
+    # 2e-2 is the per-operator bf16 bar. End to end at this context the bf16 model's own
+    # rounding noise is larger (the bf16 oracle sits about 3.4e-2 from the fp32 model), so the
+    # logits are held to that measured noise instead, as in _teacher_forced_parity.
+    assert float(err_bf16.mean()) <= 1.25 * float(noise.mean())
+    assert float(err_fp32.mean()) <= 1.25 * float(noise.mean())
+    assert float(err_bf16.max()) <= 1.5 * float(noise.max())
+    assert float(err_fp32.max()) <= 1.5 * float(noise.max())
+    expect = torch.argmax(ref, -1)
+    flips = _flip_report(logits, ref, exact, nxt, expect)
+    print(f"tokens: {batch - len(flips)}/{batch} equal to the oracle's argmax; flips {flips}",
+          flush=True)
+
+
+@pytest.mark.slow
+def test_qwen2_0_5b_shape_fp32_reference_graph_identical_greedy_ids():
+    """The reference's own precision: the reference-style graph (the exporter's 19 nodes per
+    layer) in fp32 at the Qwen2-0.5B shape, batch 4, 512 random prompt tokens fed through the
+    decode step, then 64 greedy tokens. They must equal the fp32 oracle's free-running greedy
+    tokens exactly (prefill as one batched pass, then one step per token)."""
+    cfg = QWEN2_0_5B
+    w = random_weights(cfg, seed=47, device="cuda", dtype=torch.float32)
+    prompt = _prompt(cfg, 4, 512, 48)
+    session = DecodeSession(cfg, w, 4, max_seq_len=512 + 64 + 8, fused=False).capture()
+    got = session.generate(prompt.cuda(), 64).cpu()
+    expect, margins = Qwen2Oracle(cfg, w, round_bf16=False).generate(prompt, 64)
+    first = [(got[r] != expect[r]).nonzero()[:1].tolist() for r in range(4)]
+    print(f"\nfp32 greedy over 64 steps: smallest top-1/top-2 oracle margin "
+          f"{float(margins.min()):.3e}; first differing step per row {first}", flush=True)
+    assert torch.equal(got, expect)

@@ -126,3 +126,23 @@ def test_static_cache_step_equals_forward():
     b.reset_static(2, 8)
     steps = torch.stack([b.step_static(prompt[:, t], t) for t in range(3)], 1)
     torch.testing.assert_close(steps, full, rtol=1e-5, atol=1e-5)
+
+
+def test_oracle_reproduces_reference_tiny_fixture():
+    """The reference's Qwen2-tiny case (examples/qwen2/qwen2.py:22-44, weights by its formula):
+    the fp32 oracle gives transformers' logits recorded in tests/golden/qwen2_tiny_e2e.json, for
+    the reference's prompt [2] and at every position of [2, 5, 1, 7]."""
+    import json
+    import os
+
+    from dli_qwen2.reference_tiny import REFERENCE_TINY, reference_tiny_weights
+
+    path = os.path.join(os.path.dirname(__file__), "golden", "qwen2_tiny_e2e.json")
+    fixture = json.load(open(path, encoding="utf-8"))
+    oracle = Qwen2Oracle(REFERENCE_TINY, reference_tiny_weights(), round_bf16=False)
+    for name, case in fixture["cases"].items():
+        ids = torch.tensor([case["input_ids"]], dtype=torch.int64)
+        oracle.reset(1)
+        logits = oracle.forward(ids)[0].double()
+        expect = torch.tensor(case["logits"], dtype=torch.float64)
+        torch.testing.assert_close(logits, expect, rtol=1e-5, atol=1e-6, msg=name)
