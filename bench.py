@@ -11,8 +11,8 @@ decoder layer in one persistent decoder_stack launch, then model.norm and lm_hea
 Prints one JSON line: decode tok/s (whole job), ms/step, the step's HBM roofline fraction
 (algorithmic bytes = weights + KV read + KV write + bf16 logits), the dominant kernel's roofline
 (the decoder stack, or decode attention for the fused graph, timed live with HIP events on its
-stream) and a CPU baseline (the CPU oracle timed on a bounded sample of the same step on this
-host).
+stream) and a CPU baseline (the same step as the reference-style graph through the dli Engine and
+the ATen CPU reference plugin on this host's cores, a bounded sample of steps).
 """
 from __future__ import annotations
 
@@ -34,14 +34,17 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", choices=("decode", "alexnet", "prefill"), default="decode",
+    ap.add_argument("--workload", choices=("decode", "alexnet", "prefill", "linear"),
+                    default="decode",
                     help="decode (default): the Qwen2 decode step; alexnet: the AlexNet-style "
                          "fp32 CNN forward (batch 64) on the MFMA GEMM operators; prefill: the "
-                         "operators of one Qwen2 decoder layer at batch 4 x 2048 tokens")
+                         "operators of one Qwen2 decoder layer at batch 4 x 2048 tokens; linear: "
+                         "the single fp32 linear layer [64,1024] x [4096,1024]^T + b")
     ap.add_argument("--batch", type=int, default=None, help="decode 32, alexnet 64")
     ap.add_argument("--context", type=int, default=4096)
     ap.add_argument("--layers", type=int, default=None, help="override (for quick local checks)")
-    ap.add_argument("--cpu-baseline-steps", type=int, default=3)
+    ap.add_argument("--cpu-baseline-steps", type=int, default=8)
+    ap.add_argument("--cpu-baseline-warmup", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--splits", default=None, help="split-K per projection, e.g. o=2,down=4")
     ap.add_argument("--eager", action="store_true", help="run the step without graph capture")
@@ -84,6 +87,68 @@ def step_bytes(cfg, batch, context):
     kv_write = batch * cfg.kv_bytes_per_token()
     logits = batch * cfg.vocab * 2
     return weights + kv_read + kv_write, weights, kv_read, kv_write, logits
+
+
+def cpu_description():
+    """Core count and CPU model of this host (recorded with every CPU baseline)."""
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo", encoding="utf-8"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return os.cpu_count(), model
+
+
+def cpu_engine_decode_baseline(cfg, weights, B, ctx, ids, steps, warmup):
+    """The same decode step on the host: the reference-style dli.graph.v1 decode graph (the
+    exporter's 19 nodes per layer, python/dli_export/export.py:272-446) run through the dli
+    Engine with the ATen CPU reference plugin (lib/libdli_aten_ops.so) on all host cores, in
+    fp32 (the reference's precision) with the bf16 weights' values. The host KV cache holds a
+    synthetic context of ctx - 1 keys per layer; every step writes position ctx - 1 and attends
+    over ctx keys. Median wall time per step over `steps` steps after `warmup`."""
+    import statistics
+
+    import torch
+
+    import dli
+    from dli_qwen2 import DecodeSession
+
+    cores, model = cpu_description()
+    torch.set_num_threads(cores)
+    w32 = {k: v.detach().to("cpu", torch.float32) for k, v in weights.items()}
+    engine = dli.Engine().load_aten_plugin()
+    session = DecodeSession(cfg, w32, B, max_seq_len=ctx, fused=False, engine=engine,
+                            device="cpu")
+    ids = ids.cpu()
+    pos = torch.full((B,), ctx - 1, dtype=torch.int64)
+    session.step(ids, pos)  # creates the host cache entries
+    g = torch.Generator().manual_seed(3)
+    for i in range(cfg.layers):  # synthetic context: a seeded 64-key block, repeated
+        e = engine.kv_cache_entry(f"layer_{i}")
+        for pool, axis in ((e["key_pool"], 2), (e["value_pool"], 3)):
+            shape = list(pool.shape)
+            shape[axis] = 64
+            block = torch.randn(shape, generator=g)
+            reps = [1, 1, 1, 1]
+            reps[axis] = pool.shape[axis] // 64
+            pool.copy_(block.repeat(*reps))
+    for _ in range(warmup):
+        session.step(ids, pos)
+    times = []
+    for _ in range(steps):
+        t0 = time.perf_counter()
+        session.step(ids, pos)
+        times.append(time.perf_counter() - t0)
+    step_s = statistics.median(times)
+    return {"value": round(B / step_s, 2), "unit": "tok/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"median of {steps} decode steps after {warmup} warm-ups of the same "
+                      f"batch-{B}, context-{ctx} step: the reference-style dli.graph.v1 graph "
+                      f"through the dli Engine + ATen CPU reference plugin, fp32 with the bf16 "
+                      f"weights' values; {step_s * 1000:.1f} ms/step; {cores} cores ({model})"}
 
 
 def time_decode_attention(session, cfg, B, ctx, pos, g, stream, hip, reps=200):
@@ -368,6 +433,99 @@ def bench_prefill(args):
         "device": torch.cuda.get_device_name(0)}), flush=True)
 
 
+FP32_LINEAR = (64, 1024, 4096)  # config 1: x [64, 1024], W [4096, 1024], b [4096]
+
+
+def linear_inputs(seed=0):
+    """x ~ N(0, 1); W and b ~ U(-1/32, 1/32) (Kaiming-uniform bound 1/sqrt(1024)); seeded on the
+    host, so every device sees the same bits."""
+    import torch
+
+    m, k, n = FP32_LINEAR
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(m, k, generator=g)
+    w = torch.rand(n, k, generator=g) * (2 / 32) - 1 / 32
+    b = torch.rand(n, generator=g) * (2 / 32) - 1 / 32
+    return x, w, b
+
+
+def bench_linear(args):
+    """Config 1, the single fp32 linear layer y = x W^T + b at [64, 1024] x [4096, 1024]^T: the
+    gfx950 fp32 MFMA linear (dli_hip_linear_act with its split-K workspace) timed with HIP events
+    over --steps launches, against the reference's CPU path on this host: one "aten" node
+    (aten::linear through the c10 dispatcher, src/aten_operator.cc:65-106) run by the dli Engine,
+    median of >= 20 calls, bit-compared with torch.nn.functional.linear. Roofline: 536,870,912
+    flop per call against the fp32 MFMA peak (the call's 18,104,320 bytes take 2.3 us at 8 TB/s,
+    its flops 3.4 us at 157.3 TFLOP/s)."""
+    import statistics
+
+    import torch
+    import torch.nn.functional as F
+
+    import dli
+    from dli import hip
+
+    m, k, n = FP32_LINEAR
+    flops = 2 * m * n * k
+    nbytes = 4 * (m * k + n * k + n + m * n)
+    x, w, b = linear_inputs()
+    expect = F.linear(x, w, b)
+    xd, wd, bd = x.cuda(), w.cuda(), b.cuda()
+    out = torch.empty(m, n, device="cuda")
+    ws_bytes = hip.lib().dli_hip_linear_workspace(hip.F32, m, n, k)
+    ws = torch.empty(max(ws_bytes, 4), dtype=torch.uint8, device="cuda")
+    stream = torch.cuda.current_stream()
+
+    def launch():
+        hip.call("dli_hip_linear_act", hip.F32, hip.F32, xd.data_ptr(), wd.data_ptr(),
+                 bd.data_ptr(), out.data_ptr(), m, n, k, 0, ws.data_ptr() if ws_bytes else None,
+                 ws_bytes, stream.cuda_stream)
+
+    us = _time_launches(launch, stream, max(args.steps, 20))
+    got = out.cpu()
+    rel = float(((got - expect).abs() / expect.abs().clamp_min(1e-6)).max())
+    max_abs = float((got - expect).abs().max())
+    # the reference's CPU path: Engine + "aten" node
+    cores, model = cpu_description()
+    torch.set_num_threads(cores)
+    engine = dli.Engine()
+    graph = dli.Graph.from_json(json.dumps({
+        "format": "dli.graph.v1", "model_type": "single_linear", "inputs": ["x", "w", "b"],
+        "outputs": ["y"], "nodes": [{"name": "fc", "op": "aten", "inputs": ["x", "w", "b"],
+                                     "outputs": ["y"], "attrs": {"name": "aten::linear"}}]}))
+    feeds = {"x": x, "w": w, "b": b}
+    y = engine.run(graph, feeds)["y"]
+    for _ in range(3):
+        engine.run(graph, feeds)
+    times = []
+    for _ in range(max(args.cpu_baseline_steps, 20)):
+        t0 = time.perf_counter()
+        engine.run(graph, feeds)
+        times.append(time.perf_counter() - t0)
+    cpu_us = statistics.median(times) * 1e6
+    tflops = flops / (us * 1e-6) / 1e12
+    print(json.dumps({
+        "metric": "single linear fp32 [64,1024]x[4096,1024]^T+b us/call", "value": round(us, 2),
+        "unit": "us/call", "n_gpus": 1, "steps": max(args.steps, 20), "warmup": 5,
+        "ms_per_step": round(us / 1000, 5), "higher_is_better": False, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "single linear layer fp32, x [64,1024] ~N(0,1), W [4096,1024] and "
+                               "b [4096] ~U(-1/32,1/32), y = x W^T + b"},
+        "roofline": {"bound": "mfma", "kernel": "dli_hip_linear_act fp32 (16x16x4 f32 MFMA)",
+                     "achieved": round(tflops, 2), "peak": FP32_MFMA_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(tflops / FP32_MFMA_PEAK_TFLOPS, 4),
+                     "traffic": None, "avg_us": round(us, 2), "flops_per_launch": flops,
+                     "bytes_per_launch": nbytes},
+        "parity": {"max_relative_error_vs_torch_cpu": rel, "max_abs_error": max_abs,
+                   "cpu_aten_node_bit_identical_to_F_linear": bool(torch.equal(y, expect))},
+        "cpu_baseline": {"value": round(cpu_us, 2), "unit": "us/call", "cores": cores,
+                         "kind": "port",
+                         "sample": f"median of {len(times)} calls after 4 warm-ups: one \"aten\" "
+                                   f"node (aten::linear) through the dli Engine on the host; "
+                                   f"{cores} cores ({model})"},
+        "device": torch.cuda.get_device_name(0)}), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -380,6 +538,9 @@ def main():
         return
     if args.workload == "prefill":
         bench_prefill(args)
+        return
+    if args.workload == "linear":
+        bench_linear(args)
         return
 
     import torch
@@ -468,23 +629,8 @@ def main():
 
     cpu = None
     if not args.no_cpu_baseline and args.cpu_baseline_steps > 0:
-        sys.path.insert(0, ROOT)
-        from oracle.qwen2 import Qwen2Oracle
-
-        threads = torch.get_num_threads()
-        oracle = Qwen2Oracle(cfg, {k: v for k, v in weights.items()})
-        oracle.reset_static(B, ctx, seed=2, fill=ctx - 1)
-        cpu_ids = ids.cpu()
-        oracle.step_static(cpu_ids, ctx - 1)  # warm-up
-        t1 = time.perf_counter()
-        for _ in range(args.cpu_baseline_steps):
-            oracle.step_static(cpu_ids, ctx - 1)
-        cpu_s = (time.perf_counter() - t1) / args.cpu_baseline_steps
-        cpu = {"value": round(B / cpu_s, 2), "unit": "tok/s", "cores": threads, "kind": "port",
-               "sample": f"{args.cpu_baseline_steps} decode steps (after 1 warm-up) of the same "
-                         f"batch-{B}, context-{ctx} step; torch fp32 CPU oracle with bf16 "
-                         f"rounding points; {cpu_s * 1000:.1f} ms/step"}
-        del oracle
+        cpu = cpu_engine_decode_baseline(cfg, weights, B, ctx, ids, args.cpu_baseline_steps,
+                                         args.cpu_baseline_warmup)
 
     result = {
         "metric": METRIC,

@@ -23,7 +23,8 @@ void hipCheck(int rc, const char* what) {
 }
 
 void validatePair(const Tensor& key, const Tensor& value) {
-  if (!key.isCuda() || !value.isCuda()) throw std::invalid_argument("KV cache expects CUDA tensors");
+  if (key.isCuda() != value.isCuda())
+    throw std::invalid_argument("KV cache key/value must be on the same device");
   if (key.rank() != 4 || value.rank() != 4)
     throw std::invalid_argument("KV cache expects rank-4 tensors");
   if (key.shape() != value.shape()) throw std::invalid_argument("KV key/value shape mismatch");
@@ -41,10 +42,36 @@ void allocatePools(KVCacheEntry& e, DType dtype, int device_id) {
   const std::int64_t blocks = e.batch * e.max_blocks;
   // Zero-filled once, so that attention kernels reading a partially filled block see finite
   // values in the slots they mask out.
-  const auto options = at::TensorOptions().dtype(toTorchDType(dtype)).device(at::kCUDA, device_id);
+  auto options = at::TensorOptions().dtype(toTorchDType(dtype));
+  options = device_id == kCpuDevice ? options.device(at::kCPU)
+                                    : options.device(at::kCUDA, device_id);
   e.key_pool = Tensor(at::zeros({blocks, e.heads, e.block_size, e.head_dim}, options));
   e.value_pool = Tensor(at::zeros({blocks, e.heads, e.head_dim, e.block_size}, options));
-  e.block_table = identityBlockTable(e.batch, e.max_blocks, device_id);
+  if (device_id == kCpuDevice) {
+    e.block_table = Tensor(at::arange(blocks, at::TensorOptions().dtype(at::kInt))
+                               .view({e.batch, e.max_blocks}));
+  } else {
+    e.block_table = identityBlockTable(e.batch, e.max_blocks, device_id);
+  }
+}
+
+// Host entries hold one block per sequence (block_size = capacity), so sequence b's keys are
+// key_pool[b] = [heads, capacity, head_dim] and its values value_pool[b] = [heads, head_dim,
+// capacity]: contiguous per head, which the ATen CPU attention reads without a gather. Token s
+// of sequence b goes to position start[b] + s.
+void appendHost(KVCacheEntry& e, const Tensor& key, const Tensor& value,
+                const std::vector<std::int64_t>& start) {
+  const std::int64_t seq = key.dim(2);
+  at::Tensor kp = e.key_pool.torchTensor(), vp = e.value_pool.torchTensor();
+  const at::Tensor& k = key.torchTensor();
+  const at::Tensor& v = value.torchTensor();
+  for (std::int64_t b = 0; b < e.batch; ++b) {
+    const std::int64_t p = start[static_cast<std::size_t>(b)];
+    if (p < 0 || p + seq > e.capacity())
+      throw std::out_of_range("KV cache position outside the host cache capacity");
+    kp[b].narrow(1, p, seq).copy_(k[b]);
+    vp[b].narrow(2, p, seq).copy_(v[b].transpose(-1, -2));
+  }
 }
 
 }  // namespace
@@ -83,11 +110,18 @@ KVCacheEntry& KVCache::reserve(const std::string& name, DType dtype, std::int64_
   entry.head_dim = head_dim;
   entry.block_size = block_size_;
   entry.max_blocks = (max_seq_len_ + block_size_ - 1) / block_size_;
+  if (device_id == kCpuDevice) {  // one block per sequence on the host
+    entry.block_size *= entry.max_blocks;
+    entry.max_blocks = 1;
+  }
   allocatePools(entry, dtype, device_id);
   return entries_.emplace(name, std::move(entry)).first->second;
 }
 
 void KVCache::grow(KVCacheEntry& e, std::int64_t needed_tokens) {
+  if (!e.key_pool.isCuda())
+    throw std::out_of_range("host KV cache holds " + std::to_string(e.capacity()) +
+                            " tokens per sequence (configure a larger max_seq_len)");
   std::int64_t blocks = e.max_blocks;
   while (blocks * e.block_size < needed_tokens) blocks *= 2;
   if (blocks == e.max_blocks) return;
@@ -115,9 +149,15 @@ void KVCache::grow(KVCacheEntry& e, std::int64_t needed_tokens) {
 
 void KVCache::append(const std::string& name, const Tensor& key, const Tensor& value) {
   validatePair(key, value);
-  KVCacheEntry& e = reserve(name, key.dtype(), key.dim(0), key.dim(1), key.dim(3), key.deviceId());
+  KVCacheEntry& e = reserve(name, key.dtype(), key.dim(0), key.dim(1), key.dim(3),
+                            key.isCuda() ? key.deviceId() : kCpuDevice);
   const std::int64_t seq = key.dim(2);
   if (e.length + seq > e.capacity()) grow(e, e.length + seq);
+  if (!key.isCuda()) {
+    appendHost(e, key, value, std::vector<std::int64_t>(static_cast<std::size_t>(e.batch), e.length));
+    e.length += seq;
+    return;
+  }
   hipCheck(dli_hip_kv_append(hipDtype(key.dtype()), key.deviceData(), value.deviceData(),
                              e.key_pool.deviceData(), e.value_pool.deviceData(),
                              static_cast<const std::int32_t*>(e.block_table.deviceData()), e.batch,
@@ -130,12 +170,20 @@ void KVCache::append(const std::string& name, const Tensor& key, const Tensor& v
 void KVCache::appendAt(const std::string& name, const Tensor& key, const Tensor& value,
                        const Tensor& positions) {
   validatePair(key, value);
-  if (!positions.isCuda()) throw std::invalid_argument("KV cache positions must be on the device");
+  if (positions.isCuda() != key.isCuda())
+    throw std::invalid_argument("KV cache positions must be on the key's device");
   if (positions.dtype() != DType::Int64 && positions.dtype() != DType::Int32)
     throw std::invalid_argument("KV cache positions must be int64 or int32");
   if (static_cast<std::int64_t>(positions.numel()) != key.dim(0))
     throw std::invalid_argument("KV cache positions must hold one entry per sequence");
-  KVCacheEntry& e = reserve(name, key.dtype(), key.dim(0), key.dim(1), key.dim(3), key.deviceId());
+  KVCacheEntry& e = reserve(name, key.dtype(), key.dim(0), key.dim(1), key.dim(3),
+                            key.isCuda() ? key.deviceId() : kCpuDevice);
+  if (!key.isCuda()) {
+    const at::Tensor pos = positions.torchTensor().to(at::kLong).contiguous();
+    const std::int64_t* p = pos.data_ptr<std::int64_t>();
+    appendHost(e, key, value, std::vector<std::int64_t>(p, p + e.batch));
+    return;
+  }
   hipCheck(dli_hip_kv_append(hipDtype(key.dtype()), key.deviceData(), value.deviceData(),
                              e.key_pool.deviceData(), e.value_pool.deviceData(),
                              static_cast<const std::int32_t*>(e.block_table.deviceData()), e.batch,

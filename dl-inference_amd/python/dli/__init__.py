@@ -23,6 +23,11 @@ def plugin_path() -> str:
     return _os.path.join(LIB_DIR, "libdli_hip_ops.so")
 
 
+def aten_plugin_path() -> str:
+    """Path of the ATen CPU reference plugin (the same operator names on host tensors)."""
+    return _os.path.join(LIB_DIR, "libdli_aten_ops.so")
+
+
 def hip_library_path() -> str:
     """Path of the device C ABI library (include/dli_hip.h)."""
     return _os.path.join(LIB_DIR, "libdli_hip.so")
@@ -41,6 +46,14 @@ class Engine(_dli_native.Engine):
                 stream = _torch.cuda.current_stream().cuda_stream
         return super().run(graph, inputs, int(stream), profile)
 
+    def load_aten_plugin(self) -> "Engine":
+        """Loads the ATen CPU reference plugin (graphs then run on host tensors)."""
+        path = aten_plugin_path()
+        if not _os.path.exists(path):
+            raise RuntimeError(f"ATen CPU reference plugin is not built: {path}")
+        self.load_library(path)
+        return self
+
     def load_plugin(self) -> "Engine":
         """Loads the gfx950 plugin; raises if it was not built."""
         path = plugin_path()
@@ -51,4 +64,4 @@ class Engine(_dli_native.Engine):
 
 
 __all__ = ["Engine", "GreedyDecoder", "Graph", "Node", "ProfileSession", "load_weights", "plugin_path",
-           "hip_library_path", "set_log_level"]
+           "aten_plugin_path", "hip_library_path", "set_log_level"]

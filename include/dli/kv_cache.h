@@ -17,6 +17,11 @@
 // Positions are either tracked on the host (reference semantics: every sequence has the same
 // length, append() advances it) or passed per sequence as a device tensor (appendAt), which
 // keeps a decode step free of host state so it can be captured into a HIP graph.
+//
+// Host entries (key/value on the CPU, device id kCpuDevice: the ATen CPU reference plugin) use
+// the same structure with one block per sequence (block_size = capacity, identity table), so a
+// sequence's keys are [heads, capacity, head_dim] and its values [heads, head_dim, capacity],
+// each contiguous; they do not grow beyond the configured max_seq_len.
 
 #include <cstdint>
 #include <map>
@@ -26,6 +31,8 @@
 #include "dli/tensor.h"
 
 namespace dli {
+
+constexpr int kCpuDevice = -1;  // device id of host KV cache entries
 
 // The pools are named key_pool / value_pool, not key / value as in the reference's entry
 // (include/dli/kv_cache.h of the reference: contiguous [B,H,S,D] tensors that its attention

@@ -1,0 +1,111 @@
+"""The ATen CPU reference plugin (lib/libdli_aten_ops.so) on the CPU: the reference's operator
+known answers, the reference-style Qwen2 decode graph against the oracle, the reference's
+Qwen2-tiny fixture, and the config-1 single linear layer through the reference's "aten" node
+(aten::linear through c10's dispatcher, src/aten_operator.cc:65-106) bit for bit against
+torch.nn.functional.linear."""
+from __future__ import annotations
+
+import json
+import os
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+import dli
+from dli_qwen2 import DecodeSession, random_weights, tiny_config
+from dli_qwen2.reference_tiny import REFERENCE_TINY, reference_tiny_weights
+from oracle.qwen2 import Qwen2Oracle
+from support import assert_close, kat_inputs, kat_outputs, load_kat, one_node_graph
+
+KAT = load_kat()
+
+
+def _engine():
+    return dli.Engine().load_aten_plugin()
+
+
+def test_registers_the_reference_operator_names():
+    from test_core import REF_OPS
+
+    names = set(_engine().operator_names())
+    assert set(REF_OPS) <= names and "argmax" in names
+
+
+@pytest.mark.parametrize("case", KAT, ids=[c["op"] for c in KAT])
+def test_reference_known_answers(case):
+    inputs = kat_inputs(case)
+    engine = _engine()
+    outs = engine.run(one_node_graph(case["op"], inputs, list(case["outputs"]), case["attrs"]),
+                      inputs)
+    for name, expected in kat_outputs(case).items():
+        assert_close(outs[name], expected, "float32")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_tiny_decode_graph_matches_oracle(dtype):
+    """The reference-style decode graph (19 nodes per layer, batch 3) stepped on host tensors
+    through the Engine: greedy tokens equal the oracle's (fp32: the plain model; bf16: the oracle
+    with the graph's bf16 rounding points), logits within the dtype's bar."""
+    cfg = tiny_config()
+    w = random_weights(cfg, seed=5, dtype=dtype)
+    prompt = torch.randint(0, cfg.vocab, (3, 6), generator=torch.Generator().manual_seed(6))
+    session = DecodeSession(cfg, w, 3, max_seq_len=32, fused=False, engine=_engine(), device="cpu")
+    pos = torch.zeros(3, dtype=torch.int64)
+    logits = []
+    for t in range(6):
+        lg, _ = session.step(prompt[:, t], pos)
+        logits.append(lg.float())
+        pos += 1
+    oracle = Qwen2Oracle(cfg, w, round_bf16=dtype == torch.bfloat16)
+    oracle.reset(3)
+    ref = oracle.forward(prompt)  # [B, S, V]
+    got = torch.stack(logits, 1)
+    tol = dict(rtol=1e-4, atol=1e-5) if dtype == torch.float32 else dict(rtol=2e-2, atol=2e-2)
+    torch.testing.assert_close(got, ref, **tol)
+    assert torch.equal(got.argmax(-1), ref.argmax(-1))
+
+
+def test_reference_qwen2_tiny_fixture():
+    fixture = json.load(open(os.path.join(os.path.dirname(__file__), "golden",
+                                          "qwen2_tiny_e2e.json"), encoding="utf-8"))
+    spec = fixture["cases"]["extended"]
+    session = DecodeSession(REFERENCE_TINY, reference_tiny_weights(), 1, max_seq_len=16,
+                            fused=False, engine=_engine(), device="cpu")
+    for t, token in enumerate(spec["input_ids"]):
+        lg, _ = session.step(torch.tensor([token]), torch.tensor([t]))
+        torch.testing.assert_close(lg[0].double(), torch.tensor(spec["logits"][t], dtype=torch.float64),
+                                   rtol=1e-5, atol=1e-6)
+
+
+def linear_config1_inputs(seed: int = 0):
+    """Config 1's single linear layer: x ~ N(0, 1) [64, 1024]; W [4096, 1024] and b [4096]
+    ~ U(-1/32, 1/32) (Kaiming-uniform bound 1/sqrt(1024)), seeded on the CPU."""
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(64, 1024, generator=g)
+    w = torch.rand(4096, 1024, generator=g) * (2 / 32) - 1 / 32
+    b = torch.rand(4096, generator=g) * (2 / 32) - 1 / 32
+    return x, w, b
+
+
+def aten_linear_graph():
+    return dli.Graph.from_json(json.dumps({
+        "format": "dli.graph.v1", "model_type": "single_linear", "inputs": ["x", "w", "b"],
+        "outputs": ["y"],
+        "nodes": [{"name": "fc", "op": "aten", "inputs": ["x", "w", "b"], "outputs": ["y"],
+                   "attrs": {"name": "aten::linear"}}]}))
+
+
+def test_config1_aten_linear_is_bit_identical_to_torch():
+    """The reference's CPU path for config 1: one "aten" node (aten::linear through the c10
+    dispatcher) on the Engine, bit for bit equal to torch.nn.functional.linear on the same seeded
+    inputs; the ATen plugin's own linear node gives the same bits."""
+    x, w, b = linear_config1_inputs()
+    expect = F.linear(x, w, b)
+    engine = dli.Engine()
+    y = engine.run(aten_linear_graph(), {"x": x, "w": w, "b": b})["y"]
+    assert y.dtype == torch.float32 and y.shape == (64, 4096)
+    assert torch.equal(y, expect)
+    y2 = _engine().run(one_node_graph("linear", {"x": x, "w": w, "b": b}),
+                       {"x": x, "w": w, "b": b})["output"]
+    assert torch.equal(y2, expect)
