@@ -55,6 +55,8 @@ FloatKernels k_maxpool("elementwise", "max_pool2d");
 FloatKernels k_embedding("elementwise", "embedding");
 FloatKernels k_softmax("elementwise", "softmax");
 FloatKernels k_transpose("elementwise", "transpose2d");
+DeviceKernel k_permute16("elementwise", "permute_0213_u128");
+DeviceKernel k_permute2("elementwise", "permute_0213_u16");
 FloatKernels k_rotary("elementwise", "rotary");
 FloatKernels k_argmax("elementwise", "argmax");
 FloatKernels k_rms_norm("norm", "rms_norm");
@@ -196,6 +198,27 @@ int dli_hip_transpose2d(int dtype, const void* x, void* out, int64_t rows, int64
   if ((rows + 31) / 32 > 65535) return badArg("transpose", "too many rows");
   return launch(*k, {blocksFor(cols, 32), blocksFor(rows, 32)}, {256}, 0, stream, x, out, rows,
                 cols);
+}
+
+int dli_hip_permute_0213(int dtype, const void* x, void* out, int64_t n0, int64_t n1, int64_t n2,
+                         int64_t n3, void* stream) {
+  const char* op = "permute_0213";
+  int64_t elem = 0;
+  switch (dtype) {
+    case DLI_F32: case DLI_I32: elem = 4; break;
+    case DLI_BF16: case DLI_F16: elem = 2; break;
+    case DLI_I64: elem = 8; break;
+    default: return badDtype(op, dtype);
+  }
+  if (n0 < 0 || n1 < 0 || n2 < 0 || n3 < 0) return badArg(op, "negative size");
+  if (n0 == 0 || n1 == 0 || n2 == 0 || n3 == 0) return 0;
+  if (x == nullptr || out == nullptr) return badArg(op, "NULL pointer");
+  const int64_t row_bytes = n3 * elem;
+  const bool wide = row_bytes % 16 == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0 &&
+                    (reinterpret_cast<uintptr_t>(out) & 15u) == 0;
+  const int64_t row = wide ? row_bytes / 16 : row_bytes / 2;
+  return launch(wide ? k_permute16 : k_permute2, {strideBlocks(n0 * n1 * n2 * row)}, {256}, 0,
+                stream, x, out, n0, n1, n2, row);
 }
 
 int dli_hip_batch_norm2d(int dtype, const void* x, const void* weight, const void* bias,

@@ -144,6 +144,27 @@ __device__ void transpose2d_impl(const void* x, void* out, int64_t rows, int64_t
   }
 }
 
+// out[a, c, b, :] = x[a, b, c, :] for x [n0, n1, n2, row] (permutation [0, 2, 1, 3]): the
+// [B, S, H, D] <-> [B, H, S, D] change of a prefill graph, which the reference's 2-D transpose
+// (transpose/kernel.py:6-20) cannot express. Rows of `row` units (16 bytes each when the row
+// bytes allow, else 2 bytes) are copied whole, so reads and writes stay contiguous per row.
+template <typename U>
+__device__ void permute_0213_impl(const void* x, void* out, int64_t n0, int64_t n1, int64_t n2,
+                                  int64_t row) {
+  const U* px = static_cast<const U*>(x);
+  U* po = static_cast<U*>(out);
+  const int64_t total = n0 * n1 * n2 * row;
+  DK_GRID_STRIDE(i, total) {
+    const int64_t e = i % row;
+    int64_t r = i / row;  // output row (a, c, b)
+    const int64_t b = r % n1;
+    r /= n1;
+    const int64_t c = r % n2;
+    const int64_t a = r / n2;
+    po[i] = px[((a * n1 + b) * n2 + c) * row + e];
+  }
+}
+
 // rotary/kernel.py:6-35 — interleaved pairs (2p, 2p+1). One thread per (vector, pair) for q,
 // then for k. Pairs beyond `pairs` (dims >= 2*pairs) are copied unchanged.
 template <typename T>
@@ -265,3 +286,13 @@ DK_FLOAT_KERNELS(rotary, 256,
                   max_pos, start_pos, positions, pos64))
 DK_FLOAT_KERNELS(argmax, 256, (const void* x, int64_t* ids, int64_t rows, int64_t width),
                  (x, ids, rows, width))
+
+extern "C" __global__ void __launch_bounds__(256)
+    permute_0213_u128(const void* x, void* out, int64_t n0, int64_t n1, int64_t n2, int64_t row) {
+  typedef uint32_t Chunk16 __attribute__((ext_vector_type(4)));
+  permute_0213_impl<Chunk16>(x, out, n0, n1, n2, row);
+}
+extern "C" __global__ void __launch_bounds__(256)
+    permute_0213_u16(const void* x, void* out, int64_t n0, int64_t n1, int64_t n2, int64_t row) {
+  permute_0213_impl<uint16_t>(x, out, n0, n1, n2, row);
+}

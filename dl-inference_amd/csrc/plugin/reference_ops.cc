@@ -263,6 +263,14 @@ class AttentionOp final : public Operator {
       past = before ? before->length : 0;
       cache.append(cache_name, k, v);
     }
+    if (positions == nullptr && past == 0) {
+      // A prompt from an empty cache: the cache now holds exactly k and v, so attending over
+      // them directly is the same computation, and runs on the contiguous (flash) kernel.
+      check(dli_hip_attention(dt, ptr(q), ptr(k), ptr(v), ptr(*out[0]), B, Hq, Hkv, Sq, k.dim(2),
+                              D, causal ? 1 : 0, scale, ctx.stream),
+            type());
+      return;
+    }
     const KVCacheEntry& e = *cache.get(cache_name);
     const std::size_t ws_bytes = dli_hip_paged_attention_workspace(B, Hq, Sq, D, e.capacity());
     check(dli_hip_paged_attention(
@@ -309,7 +317,8 @@ class SoftmaxOp final : public Operator {
   }
 };
 
-// transpose/template.cc:7-18 — 2-D only, perm [1, 0] (same restriction as the reference).
+// transpose/template.cc:7-18 — 2-D, perm [1, 0]. Extension: rank 4 with perm [0, 2, 1, 3] (the
+// [B, S, H, D] <-> [B, H, S, D] change a prefill graph needs around rotary and attention).
 class TransposeOp final : public Operator {
  public:
   std::string type() const override { return "transpose"; }
@@ -319,8 +328,16 @@ class TransposeOp final : public Operator {
     requireCudaInputs(in, type());
     requireFloating(*in[0], type());
     const auto perm = attrs.require<std::vector<std::int64_t>>("perm");
+    if (in[0]->rank() == 4 && perm == std::vector<std::int64_t>{0, 2, 1, 3}) {
+      const Tensor& x = *in[0];
+      *out[0] = allocLike(x.dtype(), {x.dim(0), x.dim(2), x.dim(1), x.dim(3)}, x);
+      check(dli_hip_permute_0213(hipDtype(x.dtype()), ptr(x), ptr(*out[0]), x.dim(0), x.dim(1),
+                                 x.dim(2), x.dim(3), ctx.stream),
+            type());
+      return;
+    }
     if (in[0]->rank() != 2 || perm != std::vector<std::int64_t>{1, 0})
-      throw std::invalid_argument("transpose supports 2D perm [1,0]");
+      throw std::invalid_argument("transpose supports 2D perm [1,0] and 4D perm [0,2,1,3]");
     const std::int64_t rows = in[0]->dim(0), cols = in[0]->dim(1);
     *out[0] = allocLike(in[0]->dtype(), {cols, rows}, *in[0]);
     check(dli_hip_transpose2d(hipDtype(in[0]->dtype()), ptr(*in[0]), ptr(*out[0]), rows, cols,

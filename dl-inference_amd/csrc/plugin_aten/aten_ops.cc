@@ -327,7 +327,8 @@ class ReshapeOp final : public Operator {
   }
 };
 
-// transpose/template.cc:7-18: 2-D, perm [1, 0].
+// transpose/template.cc:7-18: 2-D, perm [1, 0]; extension as the device plugin: rank 4 with
+// perm [0, 2, 1, 3].
 class TransposeOp final : public Operator {
  public:
   std::string type() const override { return "transpose"; }
@@ -336,8 +337,12 @@ class TransposeOp final : public Operator {
     requireArity(in, out, 1, 1, 1, type());
     requireFloating(*in[0], type());
     const auto perm = attrs.require<std::vector<std::int64_t>>("perm");
+    if (in[0]->rank() == 4 && perm == std::vector<std::int64_t>{0, 2, 1, 3}) {
+      *out[0] = Tensor(in[0]->torchTensor().transpose(1, 2).contiguous());
+      return;
+    }
     if (in[0]->rank() != 2 || perm != std::vector<std::int64_t>{1, 0})
-      throw std::invalid_argument("transpose supports 2D perm [1,0]");
+      throw std::invalid_argument("transpose supports 2D perm [1,0] and 4D perm [0,2,1,3]");
     *out[0] = Tensor(in[0]->torchTensor().t().contiguous());
   }
 };

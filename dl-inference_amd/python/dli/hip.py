@@ -59,6 +59,7 @@ _SIGNATURES = {
                           _c_void_p],
     "dli_hip_softmax": [_int, _c_void_p, _c_void_p, _i64, _i64, _c_void_p],
     "dli_hip_transpose2d": [_int, _c_void_p, _c_void_p, _i64, _i64, _c_void_p],
+    "dli_hip_permute_0213": [_int, _c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _c_void_p],
     "dli_hip_batch_norm2d": [_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                              _c_void_p, _i64, _i64, _i64, _float, _c_void_p],
     "dli_hip_max_pool2d": [_int, _c_void_p, _c_void_p] + [_i64] * 12 + [_c_void_p],

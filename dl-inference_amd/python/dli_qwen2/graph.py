@@ -167,6 +167,94 @@ def build_decode_graph(cfg: Qwen2Config, batch: int, fused: bool = True,
     return dli.Graph.from_json(json.dumps(graph))
 
 
+def _prefill_layer_nodes(cfg: Qwen2Config, batch: int, seq: int, i: int, h: str, nodes: list) -> str:
+    """One decoder layer over [B, S, H] activations (the exporter's node sequence,
+    python/dli_export/export.py:272-424, with the [B, S, H, D] <-> [B, H, S, D] transposes a
+    prompt of S tokens needs around rotary and attention). Returns the layer's output name."""
+    p, t = f"model.layers.{i}", f"layers_{i}"
+    q_w = cfg.heads * cfg.head_dim
+    _node(nodes, f"{p}.input_layernorm", "rms_norm", [h, f"{p}.input_layernorm.weight"],
+          [f"{t}_input_norm"], {"eps": cfg.eps})
+    for proj in ("q", "k", "v"):
+        _node(nodes, f"{p}.self_attn.{proj}_proj", "linear",
+              [f"{t}_input_norm", f"{p}.self_attn.{proj}_proj.weight",
+               f"{p}.self_attn.{proj}_proj.bias"], [f"{t}_{proj}"])
+    for proj, heads in (("q", cfg.heads), ("k", cfg.kv_heads), ("v", cfg.kv_heads)):
+        _node(nodes, f"{p}.self_attn.{proj}_reshape", "reshape", [f"{t}_{proj}"],
+              [f"{t}_{proj}_bshd"], {"shape": [batch, seq, heads, cfg.head_dim]})
+        _node(nodes, f"{p}.self_attn.{proj}_transpose", "transpose", [f"{t}_{proj}_bshd"],
+              [f"{t}_{proj}_heads"], {"perm": [0, 2, 1, 3]})
+    _node(nodes, f"{p}.self_attn.rotary_embedding", "rotary_embedding",
+          [f"{t}_q_heads", f"{t}_k_heads", "rotary_cos", "rotary_sin"],
+          [f"{t}_q_rotary", f"{t}_k_rotary"], {"start_pos": 0})
+    _node(nodes, f"{p}.self_attn.attention", "attention",
+          [f"{t}_q_rotary", f"{t}_k_rotary", f"{t}_v_heads"], [f"{t}_attention"],
+          {"causal": True, "kv_cache": f"layer_{i}"})
+    _node(nodes, f"{p}.self_attn.attention_transpose", "transpose", [f"{t}_attention"],
+          [f"{t}_attention_bshd"], {"perm": [0, 2, 1, 3]})
+    _node(nodes, f"{p}.self_attn.merge", "reshape", [f"{t}_attention_bshd"],
+          [f"{t}_attention_merged"], {"shape": [batch, seq, q_w]})
+    _node(nodes, f"{p}.self_attn.o_proj", "linear",
+          [f"{t}_attention_merged", f"{p}.self_attn.o_proj.weight"], [f"{t}_attention_proj"])
+    _node(nodes, f"{p}.attention_residual", "add", [h, f"{t}_attention_proj"],
+          [f"{t}_after_attention"])
+    _node(nodes, f"{p}.post_attention_layernorm", "rms_norm",
+          [f"{t}_after_attention", f"{p}.post_attention_layernorm.weight"],
+          [f"{t}_post_attention_norm"], {"eps": cfg.eps})
+    _node(nodes, f"{p}.mlp.gate_proj", "linear",
+          [f"{t}_post_attention_norm", f"{p}.mlp.gate_proj.weight"], [f"{t}_gate"])
+    _node(nodes, f"{p}.mlp.up_proj", "linear",
+          [f"{t}_post_attention_norm", f"{p}.mlp.up_proj.weight"], [f"{t}_up"])
+    _node(nodes, f"{p}.mlp.act_fn", "silu", [f"{t}_gate"], [f"{t}_silu"])
+    _node(nodes, f"{p}.mlp.mul", "mul", [f"{t}_silu", f"{t}_up"], [f"{t}_gated"])
+    _node(nodes, f"{p}.mlp.down_proj", "linear", [f"{t}_gated", f"{p}.mlp.down_proj.weight"],
+          [f"{t}_mlp_down"])
+    _node(nodes, f"{p}.mlp_residual", "add", [f"{t}_after_attention", f"{t}_mlp_down"],
+          [f"{t}_output"])
+    return f"{t}_output"
+
+
+def build_prefill_graph(cfg: Qwen2Config, batch: int, seq: int, layers: int | None = None,
+                        from_hidden: bool = False, fused_head: bool = True) -> "dli.Graph":
+    """Prefill of a `seq`-token prompt per sequence (every sequence starts at position 0 of an
+    empty KV cache; the cache entries layer_0.. are filled with the prompt's keys and values, so
+    decode-step graphs continue at position `seq`).
+
+    from_hidden=False: input_ids int64 [B, S] -> embedding -> the decoder layers -> the last
+    token's hidden state (an "aten" select node) -> model.norm + lm_head + greedy choice
+    (lm_head_argmax; with fused_head=False the reference's rms_norm, linear and argmax nodes);
+    outputs logits [B, V] and next_ids [B] (the first generated token).
+    from_hidden=True: hidden_states [B, S, H] -> the decoder layers (the first `layers`) ->
+    output hidden [B, S, H] (one decoder layer of prefill, the config-3 workload)."""
+    n_layers = cfg.layers if layers is None else layers
+    nodes: list = []
+    h = "hidden_states"
+    if not from_hidden:
+        _node(nodes, "model.embed_tokens", "embedding",
+              ["input_ids", "model.embed_tokens.weight"], [h])
+    for i in range(n_layers):
+        h = _prefill_layer_nodes(cfg, batch, seq, i, h, nodes)
+    if from_hidden:
+        _node(nodes, "output", "reshape", [h], ["output"], {"shape": [batch, seq, cfg.hidden]})
+        graph = {"format": "dli.graph.v1", "model_type": "qwen2_prefill_layers",
+                 "inputs": ["hidden_states"], "outputs": ["output"], "nodes": nodes}
+        return dli.Graph.from_json(json.dumps(graph))
+    _node(nodes, "last_token", "aten", [h], ["last_hidden"],
+          {"name": "aten::select", "overload": "int", "dim": 1, "index": seq - 1,
+           "attr_order": ["dim", "index"]})
+    if fused_head:
+        _head_nodes(cfg, nodes, "last_hidden", "float32")
+    else:
+        _node(nodes, "model.norm", "rms_norm", ["last_hidden", "model.norm.weight"],
+              ["norm_hidden"], {"eps": cfg.eps})
+        _node(nodes, "lm_head", "linear", ["norm_hidden", "lm_head.weight"], ["logits"],
+              {"out_dtype": "float32"})
+        _node(nodes, "greedy", "argmax", ["logits"], ["next_ids"])
+    graph = {"format": "dli.graph.v1", "model_type": "qwen2_prefill",
+             "inputs": ["input_ids"], "outputs": OUTPUTS, "nodes": nodes}
+    return dli.Graph.from_json(json.dumps(graph))
+
+
 def interleave_gate_up(gate: torch.Tensor, up: torch.Tensor, block: int = 16) -> torch.Tensor:
     """[F, H] x 2 -> [2F, H]: rows [2*block*i, +block) gate block i, then up block i."""
     f, hsz = gate.shape

@@ -12,14 +12,14 @@ import torch
 import dli
 
 from .config import Qwen2Config
-from .graph import build_decode_graph, pack_fused_weights
+from .graph import build_decode_graph, build_prefill_graph, pack_fused_weights
 
 
 class DecodeSession:
     def __init__(self, cfg: Qwen2Config, weights: dict, batch: int, max_seq_len: int,
                  fused: bool = True, engine: "dli.Engine | None" = None, splits: dict | None = None,
                  block_size: int = 64, logits_dtype: str = "float32", device: str = "cuda",
-                 stack: bool = False, check_status: bool = False):
+                 stack: bool = False, check_status: bool = False, prefill: bool = False):
         self.cfg = cfg
         self.batch = batch
         self.fused = fused
@@ -29,7 +29,12 @@ class DecodeSession:
         self.graph = build_decode_graph(cfg, batch, fused=fused, splits=splits,
                                         logits_dtype=logits_dtype, stack=stack,
                                         check_status=check_status)
-        tensors = pack_fused_weights(cfg, weights, drop_unfused=True) if fused else dict(weights)
+        # prefill=True: generate() runs the prompt through one prefill graph (the layers over
+        # [B, S] tokens at once), which reads the unpacked q/k/v and gate/up weights
+        self.prefill = prefill
+        self._prefill_graphs: dict = {}
+        tensors = (pack_fused_weights(cfg, weights, drop_unfused=not prefill) if fused
+                   else dict(weights))
         self.ids = torch.zeros(batch, dtype=torch.int64, device=device)
         self.positions = torch.zeros(batch, dtype=torch.int64, device=device)
         tensors["input_ids"] = self.ids
@@ -99,21 +104,49 @@ class DecodeSession:
         return self._out
 
     # -- greedy generation ----------------------------------------------------------------------
+    def run_prefill(self, prompt: torch.Tensor):
+        """Runs the prompt [B, S] (positions 0..S-1 of every sequence) through the prefill graph
+        (build_prefill_graph): the cache entries receive the prompt's keys and values and the
+        first greedy token comes back. Returns (logits [B, V], next_ids [B])."""
+        b, s = prompt.shape
+        if b != self.batch:
+            raise ValueError("prompt batch differs from the session's")
+        if s > self.max_seq_len:
+            raise ValueError("prompt exceeds the KV cache capacity")
+        graph = self._prefill_graphs.get(s)
+        if graph is None:
+            graph = build_prefill_graph(self.cfg, b, s, fused_head=prompt.is_cuda)
+            self._prefill_graphs[s] = graph
+        self.engine.set_kv_cache_length(0)  # the prompt starts every sequence at position 0
+        inputs = dict(self.inputs)
+        inputs["input_ids"] = prompt.contiguous()
+        out = self.engine.run(graph, inputs)
+        return out["logits"], out["next_ids"]
+
     def generate(self, prompt: torch.Tensor, steps: int, start: int = 0):
-        """prompt [B, S] int64 (device). Feeds the prompt one position per step (prefill through
-        the decode step), then decodes `steps` greedy tokens. Returns [B, steps] int64."""
+        """prompt [B, S] int64 (device). Feeds the prompt, then decodes `steps` greedy tokens.
+        Returns [B, steps] int64. The prompt goes through the prefill graph in one run when the
+        session was built with prefill=True (start must then be 0), else one position per decode
+        step."""
         b, s = prompt.shape
         pos = torch.full((b,), start, dtype=torch.int64, device=prompt.device)
         next_ids = None
-        for t in range(s):
-            _, next_ids = self.step(prompt[:, t], pos)
-            pos += 1
+        if self.prefill:
+            if start != 0:
+                raise ValueError("a prefill graph starts at position 0")
+            _, next_ids = self.run_prefill(prompt)
+            pos += s
+        else:
+            for t in range(s):
+                _, next_ids = self.step(prompt[:, t], pos)
+                pos += 1
         generated = []
         for _ in range(steps):
             generated.append(next_ids.clone())
             _, next_ids = self.step(next_ids.clone(), pos)
             pos += 1
         out = torch.stack(generated, dim=1)
-        torch.cuda.synchronize()
+        if out.is_cuda:
+            torch.cuda.synchronize()
         self.check_status()
         return out

@@ -144,6 +144,12 @@ int dli_hip_softmax(int dtype, const void* x, void* out, int64_t rows, int64_t w
 int dli_hip_transpose2d(int dtype, const void* x, void* out, int64_t rows, int64_t cols,
                         void* stream);
 
+/* out[a, c, b, :] = x[a, b, c, :] for x [n0, n1, n2, n3] (permutation [0, 2, 1, 3]): the
+ * [B, S, H, D] <-> [B, H, S, D] layout change of a prefill graph. Extends the reference's
+ * transpose (transpose/kernel.py:6-20, 2-D only); any dtype code (a copy). */
+int dli_hip_permute_0213(int dtype, const void* x, void* out, int64_t n0, int64_t n1, int64_t n2,
+                         int64_t n3, void* stream);
+
 /* Eval batch norm on NCHW (batch_norm2d/kernel.py:6-28). */
 int dli_hip_batch_norm2d(int dtype, const void* x, const void* weight, const void* bias,
                          const void* running_mean, const void* running_var, void* out,

@@ -57,13 +57,27 @@ class Qwen2Oracle:
         """ids [B, S] int64: the next S tokens of every sequence (all at the same position).
         Returns fp32 logits [B, S, V] ([B, 1, V] with last_only, [B, n, V] for the last n
         positions with logits_last=n)."""
-        cfg, w, _bf16 = self.cfg, self.w, self.rnd
-        b, s = ids.shape
-        pos = torch.arange(self.length, self.length + s)[None].expand(b, s)
+        w = self.w
         h = w["model.embed_tokens.weight"][ids]  # [B, S, H]
+        h = self.forward_hidden(h, range(self.cfg.layers))
+        if last_only:
+            h = h[:, -1:]
+        elif logits_last is not None:
+            h = h[:, h.shape[1] - logits_last:]
+        x = self.rnd(_rms_norm(h, w["model.norm.weight"], self.cfg.eps))
+        return x @ w["lm_head.weight"].T
+
+    def forward_hidden(self, h: torch.Tensor, layers) -> torch.Tensor:
+        """The decoder layers `layers` (indices) applied to hidden states h [B, S, H] at the
+        next S positions of every sequence (the cache grows by S); returns the residual stream
+        after them (one layer of prefill when layers = [i] and the cache is fresh)."""
+        cfg, w, _bf16 = self.cfg, self.w, self.rnd
+        h = h.detach().to("cpu", torch.float32)
+        b, s = h.shape[:2]
+        pos = torch.arange(self.length, self.length + s)[None].expand(b, s)
         scale = 1.0 / math.sqrt(cfg.head_dim)
         group = cfg.heads // cfg.kv_heads
-        for i in range(cfg.layers):
+        for i in layers:
             p = f"model.layers.{i}"
             x = _bf16(_rms_norm(h, w[f"{p}.input_layernorm.weight"], cfg.eps))
             q = _bf16(x @ w[f"{p}.self_attn.q_proj.weight"].T + w[f"{p}.self_attn.q_proj.bias"])
@@ -94,12 +108,7 @@ class Qwen2Oracle:
             d = _bf16(a @ w[f"{p}.mlp.down_proj.weight"].T)
             h = _bf16(h + d)
         self.length += s
-        if last_only:
-            h = h[:, -1:]
-        elif logits_last is not None:
-            h = h[:, h.shape[1] - logits_last:]
-        x = _bf16(_rms_norm(h, w["model.norm.weight"], cfg.eps))
-        return x @ w["lm_head.weight"].T
+        return h
 
     # -- preallocated cache (CPU baseline timing) ------------------------------------------------
     def reset_static(self, batch: int, capacity: int, seed: int = 0, fill: int = 0):

@@ -109,3 +109,35 @@ def test_config1_aten_linear_is_bit_identical_to_torch():
     y2 = _engine().run(one_node_graph("linear", {"x": x, "w": w, "b": b}),
                        {"x": x, "w": w, "b": b})["output"]
     assert torch.equal(y2, expect)
+
+
+def test_prefill_graph_then_decode_matches_oracle_greedy():
+    """The prefill graph (all layers over the [B, S] prompt at once, build_prefill_graph) then
+    decode steps, on host tensors in fp32: the same greedy tokens as the oracle's free-running
+    greedy (batched prefill, then one token per step)."""
+    cfg = tiny_config()
+    w = random_weights(cfg, seed=7, dtype=torch.float32)
+    prompt = torch.randint(0, cfg.vocab, (3, 9), generator=torch.Generator().manual_seed(8))
+    session = DecodeSession(cfg, w, 3, max_seq_len=32, fused=False, engine=_engine(),
+                            device="cpu", prefill=True)
+    got = session.generate(prompt, 6)
+    expect, _ = Qwen2Oracle(cfg, w, round_bf16=False).generate(prompt, 6)
+    assert torch.equal(got, expect)
+
+
+def test_prefill_layer_graph_matches_oracle_layer():
+    """One decoder layer of prefill (config 3's computation at a small size) on host tensors in
+    bf16: the oracle's layer with the graph's bf16 rounding points, within the bf16 bar."""
+    from dli_qwen2 import build_prefill_graph
+
+    cfg = tiny_config()
+    w = random_weights(cfg, seed=9)
+    h = torch.randn(2, 40, cfg.hidden, generator=torch.Generator().manual_seed(10)).to(torch.bfloat16)
+    engine = _engine()
+    engine.configure_kv_cache(block_size=64, max_seq_len=64)
+    out = engine.run(build_prefill_graph(cfg, 2, 40, layers=1, from_hidden=True),
+                     {**w, "hidden_states": h})["output"]
+    oracle = Qwen2Oracle(cfg, w)
+    oracle.reset(2)
+    ref = oracle.forward_hidden(h.float(), [0])
+    torch.testing.assert_close(out.float(), ref, rtol=2e-2, atol=2e-2)

@@ -18,6 +18,20 @@ def _prompt(cfg, batch, length, seed):
     return torch.randint(0, cfg.vocab, (batch, length), generator=g)
 
 
+def _run_prefill_steps(session, prompt, steps):
+    """The prompt through the prefill graph in one run, then `steps` greedy decode steps; the
+    same (logits, next_ids) list as _run_steps."""
+    b, s = prompt.shape
+    logits, nxt = session.run_prefill(prompt.cuda())
+    out = [(logits.float().cpu().clone(), nxt.cpu().clone())]
+    pos = torch.full((b,), s, dtype=torch.int64, device="cuda")
+    for _ in range(steps):
+        logits, nxt = session.step(nxt.clone(), pos)
+        out.append((logits.float().cpu().clone(), nxt.cpu().clone()))
+        pos += 1
+    return out
+
+
 def _run_steps(session, prompt, steps):
     """Feeds the prompt then `steps` greedy tokens; returns per-step (logits, next_ids) after the
     prompt's last token and after each generated token."""
@@ -85,7 +99,8 @@ def _flip_report(logits, ref, exact, gpu_ids, expect):
     return flips
 
 
-def _teacher_forced_parity(cfg, w, batch, prompt_len, steps, seed, agree_min, stack=False):
+def _teacher_forced_parity(cfg, w, batch, prompt_len, steps, seed, agree_min, stack=False,
+                           prefill=False):
     """Free-running greedy decode on the GPU, then the oracle teacher-forced on the GPU's own
     tokens (one batched CPU pass over prompt + generated tokens) for every row, so both score
     the same prefixes at every step.
@@ -105,8 +120,10 @@ def _teacher_forced_parity(cfg, w, batch, prompt_len, steps, seed, agree_min, st
     which a free-running oracle would first diverge from the GPU (the prefixes agree up to it).
     """
     prompt = _prompt(cfg, batch, prompt_len, seed)
-    session = DecodeSession(cfg, w, batch, max_seq_len=prompt_len + steps + 8, stack=stack).capture()
-    got = _run_steps(session, prompt, steps - 1)  # logits after the prompt + steps-1 tokens
+    session = DecodeSession(cfg, w, batch, max_seq_len=prompt_len + steps + 8, stack=stack,
+                            prefill=prefill).capture()
+    run = _run_prefill_steps if prefill else _run_steps
+    got = run(session, prompt, steps - 1)  # logits after the prompt + steps-1 tokens
     logits = torch.stack([lg for lg, _ in got], 1)  # [B, T, V]
     ids = torch.stack([nx for _, nx in got], 1)  # [B, T]
     assert torch.equal(ids, torch.argmax(logits, -1)), "next_ids != argmax(logits)"
@@ -137,12 +154,24 @@ def _teacher_forced_parity(cfg, w, batch, prompt_len, steps, seed, agree_min, st
     assert rate >= agree_min, f"token agreement {rate:.3f} < {agree_min}"
 
 
+@pytest.mark.parametrize("prefill", [False, True], ids=["stepwise", "prefill"])
 @pytest.mark.parametrize("stack", [False, True], ids=["fused", "stack"])
-def test_tiny_decode_teacher_forced_parity(stack):
+def test_tiny_decode_teacher_forced_parity(stack, prefill):
     cfg = tiny_config()
     w = random_weights(cfg, seed=31, device="cuda")
     _teacher_forced_parity(cfg, w, batch=6, prompt_len=12, steps=24, seed=32, agree_min=0.9,
-                           stack=stack)
+                           stack=stack, prefill=prefill)
+
+
+@pytest.mark.slow
+def test_qwen2_0_5b_shape_prefill_graph_then_decode_teacher_forced_parity():
+    """The 512-token prompt through the prefill graph (all layers over [8, 512] tokens: tiled
+    bf16 MFMA linears, flash attention), then 64 greedy steps through the decoder stack;
+    every row scored by the oracle."""
+    cfg = QWEN2_0_5B
+    w = random_weights(cfg, seed=41, device="cuda")
+    _teacher_forced_parity(cfg, w, batch=8, prompt_len=512, steps=64, seed=42, agree_min=0.92,
+                           stack=True, prefill=True)
 
 
 @pytest.mark.slow
