@@ -26,6 +26,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "dl-inference_amd", "python"))
 
 METRIC = "decode tok/s + % HBM roofline, Qwen2-0.5B-shape bf16 b=32 ctx4096"
+METRIC_7B = "decode tok/s + % HBM roofline, Qwen2-7B-shape bf16 b=64 ctx8192"
 HBM_PEAK_GBS = 8000.0
 
 
@@ -40,8 +41,11 @@ def parse():
                          "fp32 CNN forward (batch 64) on the MFMA GEMM operators; prefill: the "
                          "operators of one Qwen2 decoder layer at batch 4 x 2048 tokens; linear: "
                          "the single fp32 linear layer [64,1024] x [4096,1024]^T + b")
-    ap.add_argument("--batch", type=int, default=None, help="decode 32, alexnet 64")
-    ap.add_argument("--context", type=int, default=4096)
+    ap.add_argument("--model", choices=("0.5b", "7b"), default="0.5b",
+                    help="decode model shape: 0.5b (Qwen2-0.5B, batch 32, context 4096) or 7b "
+                         "(Qwen2-7B, batch 64, context 8192: the large-hidden decode graph)")
+    ap.add_argument("--batch", type=int, default=None, help="decode 32 (7b: 64), alexnet 64")
+    ap.add_argument("--context", type=int, default=None, help="decode 4096 (7b: 8192)")
     ap.add_argument("--layers", type=int, default=None, help="override (for quick local checks)")
     ap.add_argument("--cpu-baseline-steps", type=int, default=8)
     ap.add_argument("--cpu-baseline-warmup", type=int, default=2)
@@ -62,18 +66,26 @@ def parse():
     return ap.parse_args()
 
 
+# (graph, batch, context) -> the committed PMC summary of that workload's dominant kernel
 TRAFFIC_PROFILES = {
-    "stack": os.path.join(ROOT, "profiles", "decoder_stack_pmc_qwen2-0.5b_b32_ctx4096.txt"),
-    "fused": os.path.join(ROOT, "profiles", "decode_attention_pmc_qwen2-0.5b_b32_ctx4096.txt"),
+    ("stack", 32, 4096): os.path.join(ROOT, "profiles",
+                                      "decoder_stack_pmc_qwen2-0.5b_b32_ctx4096.txt"),
+    ("fused", 32, 4096): os.path.join(ROOT, "profiles",
+                                      "decode_attention_pmc_qwen2-0.5b_b32_ctx4096.txt"),
+    ("large", 64, 8192): os.path.join(ROOT, "profiles",
+                                      "decode_attention_d128_pmc_qwen2-7b_b64_ctx8192.txt"),
 }
 
 
-def profiled_traffic(graph):
+def profiled_traffic(graph, batch, context):
     """HBM bytes per launch of the dominant kernel measured by two rocprofv3 --pmc runs
     (FETCH_SIZE, WRITE_SIZE) scaled by a copy kernel of known size; recorded in the committed
-    profile."""
+    profile of the same workload (None for a workload without one)."""
+    path = TRAFFIC_PROFILES.get((graph, batch, context))
+    if path is None:
+        return None
     try:
-        for line in open(TRAFFIC_PROFILES[graph]):
+        for line in open(path):
             if line.startswith("traffic_bytes_per_launch:"):
                 return int(float(line.split(":")[1].split()[0]))
     except OSError:
@@ -172,7 +184,7 @@ def time_decode_attention(session, cfg, B, ctx, pos, g, stream, hip, reps=200):
 
     us = _time_launches(attn, stream, reps)
     nbytes = B * ctx * cfg.kv_heads * cfg.head_dim * 2 * 2 + 2 * B * cfg.heads * cfg.head_dim * 2
-    return "decode attention (decode_attention_d64)", us, nbytes
+    return f"decode attention (decode_attention_d{cfg.head_dim})", us, nbytes
 
 
 def time_decoder_stack(session, cfg, B, ctx, pos, g, stream, hip, down_splits, reps=20):
@@ -575,14 +587,19 @@ def main():
 
     import dli
     from dli import hip
-    from dli_qwen2 import QWEN2_0_5B, DecodeSession, random_weights
+    from dli_qwen2 import QWEN2_0_5B, QWEN2_7B, DecodeSession, random_weights
     from dataclasses import replace
 
-    cfg = QWEN2_0_5B if args.layers is None else replace(QWEN2_0_5B, layers=args.layers)
-    B, ctx = args.batch or 32, args.context
-    from dli_qwen2.graph import DEFAULT_SPLITS, STACK_SPLITS
+    large = args.model == "7b"
+    base = QWEN2_7B if large else QWEN2_0_5B
+    cfg = base if args.layers is None else replace(base, layers=args.layers)
+    B = args.batch or (64 if large else 32)
+    ctx = args.context or (8192 if large else 4096)
+    from dli_qwen2.graph import DEFAULT_SPLITS, LARGE_SPLITS, STACK_SPLITS
 
-    splits = dict(STACK_SPLITS if args.graph == "stack" else DEFAULT_SPLITS)
+    graph_kind = "large" if large else args.graph
+    splits = dict({"stack": STACK_SPLITS, "fused": DEFAULT_SPLITS,
+                   "large": LARGE_SPLITS}[graph_kind])
     if args.splits:
         splits.update({k: int(v) for k, v in (item.split("=") for item in args.splits.split(","))})
     dev = "cuda"
@@ -632,7 +649,7 @@ def main():
     total += logit_bytes
     step_gbs = total / (ms_per_step * 1e-3) / 1e9
 
-    if args.graph == "stack":
+    if graph_kind == "stack":
         kernel, dom_us, dom_bytes = time_decoder_stack(session, cfg, B, ctx, pos, g, stream, hip,
                                                        splits["down"])
     else:
@@ -656,12 +673,17 @@ def main():
         del src, dst
 
     cpu = None
-    if not args.no_cpu_baseline and args.cpu_baseline_steps > 0:
+    if not args.no_cpu_baseline and args.cpu_baseline_steps > 0 and not large:
         cpu = cpu_engine_decode_baseline(cfg, weights, B, ctx, ids, args.cpu_baseline_steps,
                                          args.cpu_baseline_warmup)
 
+    graph_desc = {"stack": "decoder_stack (one persistent launch for all layers)",
+                  "fused": "fused (five launches per layer)",
+                  "large": "large-hidden graph (reference nodes, head_dim-128 MFMA decode "
+                           "attention, o/down linears fused with their residual adds)"}[graph_kind]
+    shape = "Qwen2-7B" if large else "Qwen2-0.5B"
     result = {
-        "metric": METRIC,
+        "metric": METRIC_7B if large else METRIC,
         "value": round(tok_s, 1),
         "unit": "tok/s",
         "n_gpus": 1,
@@ -673,24 +695,26 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic",
-        "config": {"workload": f"Qwen2-0.5B-shape bf16 greedy decode, batch {B}, context {ctx}",
-                   "model": "qwen2-0.5b-shape (random init)", "global_batch": B,
+        "config": {"workload": f"{shape}-shape bf16 greedy decode, batch {B}, context {ctx}",
+                   "model": f"{shape.lower()}-shape (random init)", "global_batch": B,
                    "seq_len": ctx, "layers": cfg.layers, "parallelism": "none (1 GPU)",
-                   "graph": ("decoder_stack (one persistent launch for all layers)"
-                             if args.graph == "stack" else "fused (five launches per layer)")
-                   + " dli.graph.v1 decode step, HIP-graph replay",
+                   "graph": graph_desc + " dli.graph.v1 decode step, HIP-graph replay",
                    "splits": splits},
         "roofline": {"bound": "hbm", "kernel": kernel,
                      "achieved": round(dom_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(dom_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": profiled_traffic(args.graph),
+                     "traffic": profiled_traffic(graph_kind, B, ctx),
                      "avg_us": round(dom_us, 2), "bytes_per_launch": dom_bytes},
         "step_roofline": {"bound": "hbm", "bytes_per_step": total, "achieved": round(step_gbs, 1),
                           "peak": HBM_PEAK_GBS, "unit": "GB/s",
                           "frac": round(step_gbs / HBM_PEAK_GBS, 4),
                           "bytes": {"weights": w_bytes, "kv_read": kv_read, "kv_write": kv_write,
                                     "logits_bf16": logit_bytes}},
-        "cpu_baseline": cpu,
+        "cpu_baseline": cpu if not large else {
+            "value": None, "unit": "tok/s", "cores": None, "kind": "port",
+            "sample": "not run for this shape: one host step would hold 30 GB of fp32 weights "
+                      "and a 60 GB fp32 cache; the 0.5B line carries the Engine + ATen CPU "
+                      "baseline"},
         "wall_s_timed": round(wall, 3),
         "device": torch.cuda.get_device_name(0),
     }

@@ -42,6 +42,7 @@ MbKernels k_lm_head("decode", "lm_head_argmax");
 DeviceKernel k_res_norm("decode", "residual_rms_norm");
 DeviceKernel k_argmax_final("decode", "argmax_finalize");
 DeviceKernel k_dec_attn("attention", "decode_attention_d64");
+DeviceKernel k_dec_attn128("attention", "decode_attention_d128");
 
 int bad(const char* op, const std::string& what) {
   return fail(DLI_HIP_EINVAL, std::string(op) + ": " + what);
@@ -315,11 +316,12 @@ namespace {
 constexpr int kDecWaves = 8;
 constexpr int kDecBlock = 64;
 
-// Workspace: partials [ml: rows x splits x 2][o: rows x splits x 64] fp32 inside a region sized
-// for kMaxDecodeSplits, then per-(sequence, kv head) arrival counters (rows of them, which is
-// at least batch * kv_heads), 256-B aligned.
-size_t partialBytes(int64_t rows) {
-  return alignUp(static_cast<size_t>(rows) * kMaxDecodeSplits * (2 + 64) * sizeof(float), 256);
+// Workspace: partials [ml: rows x splits x 2][o: rows x splits x head_dim] fp32 inside a region
+// sized for kMaxDecodeSplits, then per-(sequence, kv head) arrival counters (rows of them, which
+// is at least batch * kv_heads), 256-B aligned.
+size_t partialBytes(int64_t rows, int64_t head_dim = 64) {
+  return alignUp(static_cast<size_t>(rows) * kMaxDecodeSplits * (2 + head_dim) * sizeof(float),
+                 256);
 }
 
 }  // namespace
@@ -350,8 +352,8 @@ int decodeAttentionFast(int dtype, const void* q, const void* key_pool, const vo
                         int64_t max_blocks, int64_t past, const void* positions,
                         int positions_dtype, float scale, void* workspace, size_t workspace_bytes,
                         void* stream) {
-  if (dtype != DLI_BF16 || seq_q != 1 || head_dim != 64 || q_heads / kv_heads > 16 ||
-      block_size != kDecBlock || !aligned16(q))
+  if (dtype != DLI_BF16 || seq_q != 1 || (head_dim != 64 && head_dim != 128) ||
+      q_heads / kv_heads > 16 || block_size != kDecBlock || !aligned16(q))
     return 1;
   if (batch * kv_heads > 65535) return 1;
   int cus = 0;
@@ -359,15 +361,24 @@ int decodeAttentionFast(int dtype, const void* q, const void* key_pool, const vo
   const int splits = decodeAttentionSplits(batch * kv_heads, max_blocks, cus);
   if (splits > kMaxDecodeSplits) return 1;
   const int64_t rows = batch * q_heads;
-  const size_t need = partialBytes(rows) + static_cast<size_t>(rows) * sizeof(unsigned);
+  const size_t need = partialBytes(rows, head_dim) + static_cast<size_t>(rows) * sizeof(unsigned);
   if (splits > 1 && (workspace == nullptr || workspace_bytes < need)) return 1;
   float* ws_ml = static_cast<float*>(workspace);
   float* ws_o = splits > 1 ? ws_ml + rows * splits * 2 : nullptr;
   unsigned* counters =
-      splits > 1 ? reinterpret_cast<unsigned*>(static_cast<char*>(workspace) + partialBytes(rows))
+      splits > 1 ? reinterpret_cast<unsigned*>(static_cast<char*>(workspace) +
+                                               partialBytes(rows, head_dim))
                  : nullptr;
   const int pos64 = positions_dtype == DLI_I64 ? 1 : 0;
   const float scale_log2 = scale * 1.4426950408889634f;
+  if (head_dim == 128)
+    return launch(k_dec_attn128,
+                  {static_cast<unsigned>(splits), static_cast<unsigned>(batch * kv_heads)},
+                  {kDecWaves * 64}, 0, stream, static_cast<const uint16_t*>(q),
+                  static_cast<const uint16_t*>(key_pool), static_cast<const uint16_t*>(value_pool),
+                  block_table, positions, pos64, past, ws_ml, ws_o, counters,
+                  static_cast<uint16_t*>(out), static_cast<int>(q_heads),
+                  static_cast<int>(kv_heads), max_blocks, splits, scale_log2);
   return launch(k_dec_attn, {static_cast<unsigned>(splits), static_cast<unsigned>(batch * kv_heads)},
                 {kDecWaves * 64}, 0, stream, static_cast<const uint16_t*>(q),
                 static_cast<const uint16_t*>(key_pool), static_cast<const uint16_t*>(value_pool),
@@ -378,9 +389,9 @@ int decodeAttentionFast(int dtype, const void* q, const void* key_pool, const vo
 
 size_t decodeAttentionWorkspace(int64_t batch, int64_t q_heads, int64_t seq_q, int64_t head_dim,
                                 int64_t max_tokens) {
-  if (seq_q != 1 || head_dim != 64) return 0;
+  if (seq_q != 1 || (head_dim != 64 && head_dim != 128)) return 0;
   const int64_t rows = batch * q_heads;
-  return partialBytes(rows) + static_cast<size_t>(rows) * sizeof(unsigned);
+  return partialBytes(rows, head_dim) + static_cast<size_t>(rows) * sizeof(unsigned);
 }
 
 }  // namespace dli::hip

@@ -207,3 +207,21 @@ extern "C" __global__ void __launch_bounds__(dk::kDecThreads)
                                                static_cast<unsigned>(max_splits), true, lds,
                                                nullptr, 0, dk::NoWait{}, dk::NoWait{});
 }
+
+// ---------------------------------------------------------------------------------------------
+// Decode attention for head_dim 128 (decode_attention_d128.h): grid (splits, batch * kv_heads).
+// ---------------------------------------------------------------------------------------------
+#include "decode_attention_d128.h"
+
+extern "C" __global__ void __launch_bounds__(dk::kD128Threads)
+    decode_attention_d128(const uint16_t* q, const uint16_t* k_pool, const uint16_t* v_pool,
+                          const int32_t* block_table, const void* positions, int pos64,
+                          int64_t past, float* ws_ml, float* ws_o, unsigned* counters,
+                          uint16_t* out, int Hq, int Hkv, int64_t max_blocks, int splits,
+                          float scale_log2) {
+  __shared__ dk::DecodeAttn128Lds lds;
+  const dk::DecodeAttn128Args a{q,     k_pool, v_pool,   block_table, positions, pos64,
+                                past,  ws_ml,  ws_o,     counters,    out,       Hq,
+                                Hkv,   max_blocks, splits, scale_log2};
+  dk::decodeAttention128Unit(a, blockIdx.x, blockIdx.y, lds);
+}

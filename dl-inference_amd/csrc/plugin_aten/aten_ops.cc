@@ -168,6 +168,28 @@ class LinearOp final : public Operator {
   }
 };
 
+// The device plugin's linear_residual (o_proj / down_proj with their residual add):
+// out = residual + round(x W^T (+ b)); inputs x, w, residual (, bias); attr splits ignored.
+class LinearResidualOp final : public Operator {
+ public:
+  std::string type() const override { return "linear_residual"; }
+  void compute(const std::vector<const Tensor*>& in, const std::vector<Tensor*>& out,
+               const Attributes&, ExecutionContext&) const override {
+    requireArity(in, out, 3, 4, 1, type());
+    requireFloating(*in[0], type());
+    for (const Tensor* t : in) requireSameDType(*in[0], *t, type());
+    if (in[1]->rank() != 2 || in[1]->dim(1) != in[0]->shape().back())
+      throw std::invalid_argument("linear_residual weight shape mismatch");
+    at::Tensor y = at::linear(f32(*in[0]), f32(*in[1]),
+                              in.size() == 4 ? c10::optional<at::Tensor>(f32(*in[3]))
+                                             : c10::nullopt);
+    y = y.to(toTorchDType(in[0]->dtype())).to(at::kFloat);  // the linear node's rounding point
+    const at::Tensor res = f32(*in[2]);
+    if (res.numel() != y.numel()) throw std::invalid_argument("linear_residual residual shape");
+    *out[0] = result(res.view(y.sizes()) + y, in[0]->dtype());
+  }
+};
+
 // matmul/kernel.py:6-40: a [m, k] @ b [k, n].
 class MatmulOp final : public Operator {
  public:
@@ -434,6 +456,7 @@ extern "C" __attribute__((visibility("default"))) bool dli_register_operators(
     add<RmsNormOp>(registry);
     add<EmbeddingOp>(registry);
     add<LinearOp>(registry);
+    add<LinearResidualOp>(registry);
     add<MatmulOp>(registry);
     add<RotaryOp>(registry);
     add<AttentionOp>(registry);

@@ -84,6 +84,55 @@ def _reference_nodes(cfg: Qwen2Config, batch: int, nodes: list):
     _node(nodes, "greedy", "argmax", ["logits"], ["next_ids"])
 
 
+def _large_nodes(cfg: Qwen2Config, batch: int, nodes: list, splits: dict):
+    """Decode step for hidden sizes the fused norm-prologue kernels do not hold in registers
+    (hidden > 1024, e.g. the Qwen2-7B shape): the reference node sequence with o_proj and
+    down_proj each fused with their residual add (linear_residual, split-K for down_proj).
+    Attention over the paged cache runs on the MFMA decode kernel for head_dim 64 or 128."""
+    h = "hidden_states"
+    q_w = cfg.heads * cfg.head_dim
+    for i in range(cfg.layers):
+        p = f"model.layers.{i}"
+        t = f"layers_{i}"
+        _node(nodes, f"{p}.input_layernorm", "rms_norm", [h, f"{p}.input_layernorm.weight"],
+              [f"{t}_input_norm"], {"eps": cfg.eps})
+        for proj, heads in (("q", cfg.heads), ("k", cfg.kv_heads), ("v", cfg.kv_heads)):
+            _node(nodes, f"{p}.self_attn.{proj}_proj", "linear",
+                  [f"{t}_input_norm", f"{p}.self_attn.{proj}_proj.weight",
+                   f"{p}.self_attn.{proj}_proj.bias"], [f"{t}_{proj}"])
+            _node(nodes, f"{p}.self_attn.{proj}_reshape", "reshape", [f"{t}_{proj}"],
+                  [f"{t}_{proj}_heads"], {"shape": [batch, heads, 1, cfg.head_dim]})
+        _node(nodes, f"{p}.self_attn.rotary_embedding", "rotary_embedding",
+              [f"{t}_q_heads", f"{t}_k_heads", "rotary_cos", "rotary_sin", "positions"],
+              [f"{t}_q_rotary", f"{t}_k_rotary"])
+        _node(nodes, f"{p}.self_attn.attention", "attention",
+              [f"{t}_q_rotary", f"{t}_k_rotary", f"{t}_v_heads", "positions"], [f"{t}_attention"],
+              {"causal": True, "kv_cache": f"layer_{i}"})
+        _node(nodes, f"{p}.self_attn.merge", "reshape", [f"{t}_attention"],
+              [f"{t}_attention_merged"], {"shape": [batch, q_w]})
+        _node(nodes, f"{p}.self_attn.o_proj", "linear_residual",
+              [f"{t}_attention_merged", f"{p}.self_attn.o_proj.weight", h],
+              [f"{t}_after_attention"], {"splits": splits.get("o", 1)})
+        _node(nodes, f"{p}.post_attention_layernorm", "rms_norm",
+              [f"{t}_after_attention", f"{p}.post_attention_layernorm.weight"],
+              [f"{t}_post_attention_norm"], {"eps": cfg.eps})
+        _node(nodes, f"{p}.mlp.gate_proj", "linear",
+              [f"{t}_post_attention_norm", f"{p}.mlp.gate_proj.weight"], [f"{t}_gate"])
+        _node(nodes, f"{p}.mlp.up_proj", "linear",
+              [f"{t}_post_attention_norm", f"{p}.mlp.up_proj.weight"], [f"{t}_up"])
+        _node(nodes, f"{p}.mlp.act_fn", "silu", [f"{t}_gate"], [f"{t}_silu"])
+        _node(nodes, f"{p}.mlp.mul", "mul", [f"{t}_silu", f"{t}_up"], [f"{t}_gated"])
+        _node(nodes, f"{p}.mlp.down_proj", "linear_residual",
+              [f"{t}_gated", f"{p}.mlp.down_proj.weight", f"{t}_after_attention"],
+              [f"{t}_output"], {"splits": splits.get("down", 1)})
+        h = f"{t}_output"
+    _node(nodes, "model.norm", "rms_norm", [h, "model.norm.weight"], ["norm_hidden"],
+          {"eps": cfg.eps})
+    _node(nodes, "lm_head", "linear", ["norm_hidden", "lm_head.weight"], ["logits"],
+          {"out_dtype": "float32"})
+    _node(nodes, "greedy", "argmax", ["logits"], ["next_ids"])
+
+
 def _fused_nodes(cfg: Qwen2Config, batch: int, nodes: list, splits: dict, logits_dtype: str):
     h = "hidden_states"
     for i in range(cfg.layers):
@@ -143,6 +192,14 @@ def _stack_nodes(cfg: Qwen2Config, nodes: list, splits: dict, logits_dtype: str,
 # decoder stack, whose q|k|v workgroups take no down_proj unit)
 DEFAULT_SPLITS = {"o": 1, "down": 4}
 STACK_SPLITS = {"o": 1, "down": 3}
+LARGE_SPLITS = {"o": 1, "down": 2}
+FUSED_MAX_HIDDEN = 1024  # the fused kernels keep a tile's activation rows in registers
+
+
+def uses_large_graph(cfg: Qwen2Config, fused: bool) -> bool:
+    """True when a fused decode graph is requested for a hidden size above what the fused
+    kernels hold (the step is then the large-hidden graph, _large_nodes)."""
+    return fused and cfg.hidden > FUSED_MAX_HIDDEN
 
 
 def build_decode_graph(cfg: Qwen2Config, batch: int, fused: bool = True,
@@ -150,10 +207,17 @@ def build_decode_graph(cfg: Qwen2Config, batch: int, fused: bool = True,
                        stack: bool = False, check_status: bool = False) -> "dli.Graph":
     """fused=False: the reference's node sequence; fused=True: five launches per layer;
     stack=True (with fused): all layers in one decoder_stack node (check_status: the node waits
-    for its launch and fails if a workgroup gave up waiting; for tests, not for capture)."""
+    for its launch and fails if a workgroup gave up waiting; for tests, not for capture). With
+    fused=True and a hidden size above 1024 (the Qwen2-7B shape) the step is the large-hidden
+    graph instead (_large_nodes), whatever `stack` says."""
     nodes: list = []
     _node(nodes, "model.embed_tokens", "embedding", ["input_ids", "model.embed_tokens.weight"],
           ["hidden_states"])
+    if uses_large_graph(cfg, fused):
+        _large_nodes(cfg, batch, nodes, splits or LARGE_SPLITS)
+        graph = {"format": "dli.graph.v1", "model_type": "qwen2_decode_large",
+                 "inputs": INPUTS, "outputs": OUTPUTS, "nodes": nodes}
+        return dli.Graph.from_json(json.dumps(graph))
     if fused and stack:
         _stack_nodes(cfg, nodes, splits or STACK_SPLITS, logits_dtype, check_status)
     elif fused:

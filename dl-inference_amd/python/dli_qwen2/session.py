@@ -12,7 +12,8 @@ import torch
 import dli
 
 from .config import Qwen2Config
-from .graph import build_decode_graph, build_prefill_graph, pack_fused_weights
+from .graph import (build_decode_graph, build_prefill_graph, pack_fused_weights,
+                    uses_large_graph)
 
 
 class DecodeSession:
@@ -23,7 +24,7 @@ class DecodeSession:
         self.cfg = cfg
         self.batch = batch
         self.fused = fused
-        self.stack = fused and stack
+        self.stack = fused and stack and not uses_large_graph(cfg, fused)
         self.engine = engine or dli.Engine().load_plugin()
         self.engine.configure_kv_cache(block_size=block_size, max_seq_len=max_seq_len)
         self.graph = build_decode_graph(cfg, batch, fused=fused, splits=splits,
@@ -33,8 +34,8 @@ class DecodeSession:
         # [B, S] tokens at once), which reads the unpacked q/k/v and gate/up weights
         self.prefill = prefill
         self._prefill_graphs: dict = {}
-        tensors = (pack_fused_weights(cfg, weights, drop_unfused=not prefill) if fused
-                   else dict(weights))
+        tensors = (pack_fused_weights(cfg, weights, drop_unfused=not prefill)
+                   if fused and not uses_large_graph(cfg, fused) else dict(weights))
         self.ids = torch.zeros(batch, dtype=torch.int64, device=device)
         self.positions = torch.zeros(batch, dtype=torch.int64, device=device)
         tensors["input_ids"] = self.ids

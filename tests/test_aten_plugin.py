@@ -141,3 +141,20 @@ def test_prefill_layer_graph_matches_oracle_layer():
     oracle.reset(2)
     ref = oracle.forward_hidden(h.float(), [0])
     torch.testing.assert_close(out.float(), ref, rtol=2e-2, atol=2e-2)
+
+
+def test_large_hidden_decode_graph_matches_oracle():
+    """The large-hidden decode graph (hidden above what the fused kernels hold, head_dim 128 as
+    in the Qwen2-7B geometry) on host tensors in fp32: greedy tokens and logits of the oracle."""
+    from dli_qwen2 import Qwen2Config
+    from dli_qwen2.graph import uses_large_graph
+
+    cfg = Qwen2Config(hidden=1152, layers=2, heads=9, kv_heads=3, head_dim=128, ffn=512,
+                      vocab=300, max_pos=64, tied_embeddings=False)
+    assert uses_large_graph(cfg, True)
+    w = random_weights(cfg, seed=11, dtype=torch.float32)
+    prompt = torch.randint(0, cfg.vocab, (2, 5), generator=torch.Generator().manual_seed(12))
+    session = DecodeSession(cfg, w, 2, max_seq_len=32, engine=_engine(), device="cpu")
+    got = session.generate(prompt, 4)
+    expect, _ = Qwen2Oracle(cfg, w, round_bf16=False).generate(prompt, 4)
+    assert torch.equal(got, expect)

@@ -273,3 +273,60 @@ def test_qwen2_0_5b_shape_fp32_reference_graph_identical_greedy_ids():
     print(f"\nfp32 greedy over 64 steps: smallest top-1/top-2 oracle margin "
           f"{float(margins.min()):.3e}; first differing step per row {first}", flush=True)
     assert torch.equal(got, expect)
+
+
+@pytest.mark.slow
+def test_qwen2_7b_shape_two_layers_teacher_forced_parity():
+    """The Qwen2-7B geometry (hidden 3584, 28 / 4 heads, head_dim 128, MLP 18944, vocab 152064,
+    untied lm_head) with 2 of its 28 layers, batch 64: the large-hidden decode graph (head_dim-128
+    MFMA decode attention, skinny MFMA linears) against the oracle, every row scored."""
+    from dataclasses import replace
+
+    from dli_qwen2 import QWEN2_7B
+
+    cfg = replace(QWEN2_7B, layers=2)
+    w = random_weights(cfg, seed=91, device="cuda")
+    _teacher_forced_parity(cfg, w, batch=64, prompt_len=16, steps=8, seed=92, agree_min=0.9)
+
+
+@pytest.mark.slow
+def test_qwen2_7b_shape_step_at_context_8192_matches_oracle():
+    """The config-5 step geometry at context 8192 (position 8191 over a seeded 8191-key context
+    per layer) with 2 of the 28 layers, batch 8, against the oracle's preallocated-cache step."""
+    from dataclasses import replace
+
+    from dli_qwen2 import QWEN2_7B
+
+    cfg, ctx, batch = replace(QWEN2_7B, layers=2), 8192, 8
+    w = random_weights(cfg, seed=93, device="cuda")
+    ids = torch.randint(0, cfg.vocab, (batch,), generator=torch.Generator().manual_seed(94))
+    oracle = Qwen2Oracle(cfg, w)
+    oracle.reset_static(batch, ctx, seed=95, fill=ctx - 1)
+    exact_oracle = Qwen2Oracle(cfg, w, round_bf16=False)
+    exact_oracle.k_static, exact_oracle.v_static = oracle.k_static, oracle.v_static
+    session = DecodeSession(cfg, w, batch, max_seq_len=ctx + 8)
+    pos = torch.full((batch,), ctx - 1, dtype=torch.int64, device="cuda")
+    session.step(ids.cuda(), pos)
+    torch.cuda.synchronize()
+    _fill_paged_cache(session.engine, oracle, cfg.layers, batch, ctx - 1)
+    torch.cuda.synchronize()
+    logits, nxt = session.step(ids.cuda(), pos)
+    logits = logits.float().cpu()[:, None]
+    nxt = nxt.cpu()[:, None]
+    ref = oracle.step_static(ids, ctx - 1)[:, None]
+    exact = exact_oracle.step_static(ids, ctx - 1)[:, None]
+    assert torch.equal(nxt, torch.argmax(logits, -1))
+
+    def rel(a, b):
+        return (a - b).norm(dim=-1) / b.norm(dim=-1)
+
+    err_bf16, err_fp32, noise = rel(logits, ref), rel(logits, exact), rel(ref, exact)
+    print(f"\n7B geometry, 2 layers, context {ctx}, batch {batch}: relative logit error vs bf16 "
+          f"oracle mean {float(err_bf16.mean()):.3e}; vs fp32 model mean "
+          f"{float(err_fp32.mean()):.3e}; bf16 oracle vs fp32 model mean "
+          f"{float(noise.mean()):.3e}", flush=True)
+    assert float(err_bf16.mean()) <= 1.25 * float(noise.mean())
+    assert float(err_fp32.mean()) <= 1.25 * float(noise.mean())
+    assert float(err_bf16.max()) <= 1.5 * float(noise.max())
+    flips = _flip_report(logits, ref, exact, nxt, torch.argmax(ref, -1))
+    print(f"tokens: {batch - len(flips)}/{batch} equal to the oracle's argmax", flush=True)

@@ -208,17 +208,22 @@ def test_lm_head_argmax_with_final_norm(B):
     np.testing.assert_array_equal(ids[clear], two["ids"].cpu().numpy()[clear])
 
 
-@pytest.mark.parametrize("B,positions,max_seq", [
-    (8, [0, 1, 63, 64, 65, 1000, 2047, 4095], 4160),  # ragged lengths, partial last blocks
-    (32, None, 4160),                                  # the decode workload: every row at 4095
-    (3, [5, 130, 517], 600),                           # short cache: one split per sequence
-    (2, [-1, 10], 256),                                # an empty sequence yields zeros
+@pytest.mark.parametrize("B,positions,max_seq,geometry", [
+    (8, [0, 1, 63, 64, 65, 1000, 2047, 4095], 4160, (14, 2, 64)),  # ragged, partial last blocks
+    (32, None, 4160, (14, 2, 64)),       # the decode workload: every row at 4095
+    (3, [5, 130, 517], 600, (14, 2, 64)),  # short cache: one split per sequence
+    (2, [-1, 10], 256, (14, 2, 64)),     # an empty sequence yields zeros
+    # head_dim 128 (the Qwen2-7B geometry, 28 / 4 heads): ragged lengths over several splits,
+    # an empty sequence, and long contexts with one split per (sequence, kv head)
+    (8, [-1, 0, 31, 32, 63, 64, 1000, 8191], 8256, (28, 4, 128)),
+    (64, [8191] * 64, 8256, (28, 4, 128)),
+    (3, [5, 130, 517], 600, (28, 4, 128)),
 ])
-def test_paged_attention_decode(B, positions, max_seq):
+def test_paged_attention_decode(B, positions, max_seq, geometry):
     """paged_attention (decode, 64-key blocks): every (sequence, kv head) is split over
     workgroups whose partials the last one merges; compared with the oracle's attention over the
     cache contents of each sequence (attention/kernel.py:6-62 with past = position)."""
-    hq, hkv, d = 14, 2, 64
+    hq, hkv, d = geometry
     if positions is None:
         positions = [4095] * B
     e = dli.Engine().load_plugin()
