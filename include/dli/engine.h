@@ -4,9 +4,10 @@
 // reference: nodes run in file order, inputs are looked up by name, outputs are moved into the
 // tensor map, and the result is graph.outputs (or every tensor when that list is empty).
 //
-// Differences in mechanism: names are resolved to slot indices once per graph, operators are
-// created once per op type and reused (operators are stateless: compute() is const), and the
-// kernels of every node go on one caller-chosen HIP stream.
+// Differences in mechanism: operators are created once per op type and reused (operators are
+// stateless: compute() is const), debug logging is formatted only when enabled, and the kernels
+// of every node go on one caller-chosen HIP stream. Inputs are looked up by name in the run's
+// tensor map for every node, as in the reference.
 
 #include <map>
 #include <memory>
