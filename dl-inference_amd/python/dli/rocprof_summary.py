@@ -4,6 +4,8 @@
     python -m dli.rocprof_summary pmc --fetch FETCH_counter_collection.csv \
         --write WRITE_counter_collection.csv --kernel REGEX [--kernel REGEX ...] \
         --copy-kernel REGEX --copy-bytes N
+    python -m dli.rocprof_summary mfma --counters MFMA_counter_collection.csv \
+        --stats RUN_kernel_stats.csv --kernel REGEX [--kernel REGEX ...]
 
 ``pmc`` averages FETCH_SIZE and WRITE_SIZE (KiB per dispatch) over the dispatches of each
 kernel and scales them by the factor that makes the same counters read the known size of a
@@ -104,6 +106,36 @@ def traffic_bytes(fetch_csv: str, write_csv: str, kernel: str, copy_kernel: str,
     return f * copy_bytes / copy_f + w * copy_bytes / copy_w
 
 
+def mfma(counters_csv: str, stats_csv: str, kernels: list[str], simds: int, xcds: int) -> str:
+    """MFMA evidence per kernel from one --pmc pass of SQ_INSTS_VALU_MFMA_MOPS_<type> (units of
+    512 flop), SQ_VALU_MFMA_BUSY_CYCLES and GRBM_GUI_ACTIVE, plus the average durations of a
+    --kernel-trace --stats run: MFMA flop per dispatch, the achieved MFMA rate over the traced
+    average duration, and MFMA busy = busy cycles summed over SIMDs / (active cycles x SIMDs).
+    rocprofv3 sums a counter over its hardware instances, so GRBM_GUI_ACTIVE arrives as the sum
+    over the XCDs' GRBM blocks; the active cycles of the device are that sum / xcds."""
+    busy = counter_means(counters_csv, "SQ_VALU_MFMA_BUSY_CYCLES")
+    active = counter_means(counters_csv, "GRBM_GUI_ACTIVE")
+    mops = OrderedDict()
+    for kind in ("BF16", "F16", "F32", "F64"):
+        for k, v in counter_means(counters_csv, f"SQ_INSTS_VALU_MFMA_MOPS_{kind}").items():
+            n, prev = mops.get(k, (v[0], 0.0))
+            mops[k] = (n, prev + v[1])
+    stats = {r["Name"]: float(r["AverageNs"]) for r in csv.DictReader(open(stats_csv))}
+    out = [f"{'kernel':48s} {'n':>5s} {'mfma_GFLOP':>11s} {'avg_us':>9s} {'TFLOP/s':>9s} "
+           f"{'mfma_busy%':>10s}"]
+    for pattern in kernels:
+        n, m = _match(mops, pattern)
+        _, b = _match(busy, pattern)
+        _, a = _match(active, pattern)
+        rx = re.compile(pattern)
+        durs = [v for k, v in stats.items() if rx.search(k)]
+        avg_us = sum(durs) / len(durs) / 1e3 if durs else float("nan")
+        flop = m * 512
+        out.append(f"{_short(pattern):48s} {n:5d} {flop / 1e9:11.2f} {avg_us:9.2f} "
+                   f"{flop / (avg_us * 1e-6) / 1e12:9.1f} {100 * b / (a / xcds * simds):10.1f}")
+    return "\n".join(out)
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(prog="python -m dli.rocprof_summary")
     sub = ap.add_subparsers(dest="cmd", required=True)
@@ -116,9 +148,17 @@ def main(argv=None):
     pm.add_argument("--kernel", action="append", required=True)
     pm.add_argument("--copy-kernel", required=True)
     pm.add_argument("--copy-bytes", type=int, required=True)
+    mf = sub.add_parser("mfma")
+    mf.add_argument("--counters", required=True)
+    mf.add_argument("--stats", required=True)
+    mf.add_argument("--kernel", action="append", required=True)
+    mf.add_argument("--simds", type=int, default=1024, help="SIMDs of the device (256 CUs x 4)")
+    mf.add_argument("--xcds", type=int, default=8, help="GRBM instances GRBM_GUI_ACTIVE sums over")
     args = ap.parse_args(argv)
     if args.cmd == "stats":
         print(kernel_stats(args.csv, args.top))
+    elif args.cmd == "mfma":
+        print(mfma(args.counters, args.stats, args.kernel, args.simds, args.xcds))
     else:
         print(pmc(args.fetch, args.write, args.kernel, args.copy_kernel, args.copy_bytes))
 
