@@ -3,6 +3,7 @@
 #include <cmath>
 #include <string>
 
+#include "../kernels/conv_small.h"
 #include "runtime.h"
 
 namespace dli::hip {
@@ -73,6 +74,8 @@ DeviceKernel k_mfma_linear64("mfma_gemm", "mfma_linear_f32_t64");
 DeviceKernel k_mfma_linear128("mfma_gemm", "mfma_linear_f32_t128");
 DeviceKernel k_mfma_matmul64("mfma_gemm", "mfma_matmul_f32_t64");
 DeviceKernel k_mfma_matmul128("mfma_gemm", "mfma_matmul_f32_t128");
+DeviceKernel k_conv_small9("conv", "conv2d_small_f32_p9");
+DeviceKernel k_conv_small27("conv", "conv2d_small_f32_p27");
 DeviceKernel k_mfma_conv64("mfma_gemm", "mfma_conv2d_f32_t64");
 DeviceKernel k_mfma_conv128("mfma_gemm", "mfma_conv2d_f32_t128");
 DeviceKernel k_mfma_bf16_64("mfma_gemm", "mfma_linear_bf16_t64");
@@ -292,9 +295,27 @@ int dli_hip_conv2d_act(int dtype, const void* x, const void* weight, const void*
       total < limit && out_c * patch < limit &&
       pixels < limit && (out_h - 1) * stride_h + kernel_h < limit &&
       (out_w - 1) * stride_w + kernel_w < limit) {
+    auto i32 = [](int64_t v) { return static_cast<int>(v); };
+    // a patch too short for MFMA tiles (an RGB input layer): direct, output-write bound
+    if ((patch == 9 || patch == 27) && (out_c + dk::kSmallOc - 1) / dk::kSmallOc <= kMaxGridY) {
+      dk::SmallConvTable tab{};
+      tab.patch = i32(patch);
+      for (int k = 0; k < tab.patch; ++k) {
+        const int c = k / i32(kernel_h * kernel_w), ky = (k / i32(kernel_w)) % i32(kernel_h),
+                  kx = k % i32(kernel_w);
+        tab.offset[k] = (c * i32(h) + ky) * i32(w) + kx;
+        tab.ky[k] = ky;
+        tab.kx[k] = kx;
+      }
+      return launch(patch == 9 ? k_conv_small9 : k_conv_small27,
+                    {static_cast<unsigned>((pixels + 255) / 256),
+                     static_cast<unsigned>((out_c + dk::kSmallOc - 1) / dk::kSmallOc)},
+                    {256}, 0, stream, x, weight, bias, out, i32(n), i32(in_c), i32(h), i32(w),
+                    i32(out_c), i32(out_h), i32(out_w), i32(stride_h), i32(stride_w), i32(pad_h),
+                    i32(pad_w), relu, tab);
+    }
     const bool big = bigTiles(out_c, pixels);
     const int64_t tile = big ? 128 : 64;
-    auto i32 = [](int64_t v) { return static_cast<int>(v); };
     const int64_t splits = big ? 1 : linearSplits(out_c, pixels, patch);
     const size_t need = static_cast<size_t>(splits * out_c * pixels) * sizeof(float);
     if (splits > 1 && workspace != nullptr && workspace_bytes >= need &&

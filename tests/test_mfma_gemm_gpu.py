@@ -1,5 +1,6 @@
 """MFMA GEMMs of the generic operators (csrc/kernels/mfma_gemm.hip) through the plugin: fp32
-linear / matmul / conv2d (implicit GEMM), tiled bf16 linear, and the fused ReLU epilogue
+linear / matmul / conv2d (implicit GEMM; a conv whose patch has 9 or 27 elements takes the
+direct kernels conv2d_small_f32_p9 / _p27 in csrc/kernels/conv.hip), tiled bf16 linear, and the fused ReLU epilogue
 (attribute activation = "relu"), against the CPU oracle at the parity contract's tolerances
 (fp32 1e-4 relative, bf16 2e-2). Ragged shapes cover every tile edge; the larger cases take the
 128 x 128 tile path. Last, the reference's TinyAlexNet end-to-end case
@@ -114,6 +115,30 @@ def test_conv2d_f32_implicit_gemm(case):
     oh, ow = (h + 2 * pad[0] - kh) // stride[0] + 1, (w_ + 2 * pad[1] - kw) // stride[1] + 1
     if c >= 256:  # the plugin passes a workspace, so these split K
         assert hip.lib().dli_hip_conv2d_workspace(hip.F32, n, c, oc, kh, kw, oh, ow) > 0
+    nob = run_op("conv2d", {"x": x, "weight": w}, attrs=attrs)["output"]
+    close_f32(nob, ops.conv2d(to_np(x), to_np(w), None, stride, pad))
+
+
+# patch = C x KH x KW of 9 or 27: the direct kernels conv2d_small_f32_p9 / _p27 instead of MFMA
+SMALL_CONVS = [  # (N, C, H, W, OC, KH, KW, stride, pad)
+    (64, 3, 32, 32, 64, 3, 3, (1, 1), (1, 1)),    # the AlexNet-style input layer, batch 64
+    (2, 3, 9, 10, 20, 3, 3, (1, 2), (0, 1)),      # channels not a multiple of 16, strided
+    (3, 1, 17, 15, 5, 3, 3, (2, 2), (2, 2)),      # one channel, padding wider than the kernel
+    (1, 3, 3, 3, 33, 3, 3, (1, 1), (1, 1)),       # a 3 x 3 image: every tap but the centre clipped
+]
+
+
+@pytest.mark.parametrize("case", SMALL_CONVS, ids=[str(i) for i in range(len(SMALL_CONVS))])
+def test_conv2d_f32_small_patch(case):
+    n, c, h, w_, oc, kh, kw, stride, pad = case
+    assert c * kh * kw in (9, 27)
+    x, w, b = rand((n, c, h, w_), 19), rand((oc, c, kh, kw), 20, scale=0.2), rand((oc,), 21)
+    attrs = {"stride": list(stride), "padding": list(pad)}
+    ref = ops.conv2d(to_np(x), to_np(w), to_np(b), stride, pad)
+    close_f32(run_op("conv2d", {"x": x, "weight": w, "bias": b}, attrs=attrs)["output"], ref)
+    fused = run_op("conv2d", {"x": x, "weight": w, "bias": b},
+                   attrs={**attrs, "activation": "relu"})["output"]
+    close_f32(fused, ops.relu(ref))
     nob = run_op("conv2d", {"x": x, "weight": w}, attrs=attrs)["output"]
     close_f32(nob, ops.conv2d(to_np(x), to_np(w), None, stride, pad))
 
