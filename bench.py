@@ -360,17 +360,20 @@ BF16_MFMA_PEAK_TFLOPS = 2500.0
 def bench_prefill(args):
     """Config 3: one Qwen2 decoder layer of prefill in bf16 at batch 4 x 2048 tokens (hidden 896,
     14 / 2 heads, head_dim 64, MLP 4864; activations ~N(0, 1), weights ~N(0, 0.02)) as the
-    chained dli.graph.v1 prefill graph (build_prefill_graph: RMSNorm, q/k/v, o, gate, up, down
-    tiled bf16 MFMA linears, the [B,S,H,D] <-> [B,H,S,D] transposes, RoPE, KV-cache append and
-    causal GQA flash attention, SiLU * up, residual adds) through the Engine and the gfx950
-    plugin. One step = one replay of the captured layer; value = 274.4 GFLOP per layer over the
+    chained dli.graph.v1 prefill graph in its fused form (build_prefill_graph fused=True:
+    RMSNorm, q/k/v tiled bf16 MFMA linears, the [B,S,H,D] <-> [B,H,S,D] transposes, RoPE,
+    KV-cache append and causal GQA flash attention, o_proj and down_proj with the residual add in
+    their GEMM epilogue, gate/up as one GEMM with SwiGLU in its epilogue) through the Engine and
+    the gfx950 plugin. One step = one replay of the captured layer; value = 274.4 GFLOP per layer over the
     step time. The per-node GPU times (dli.ProfileSession, eager runs) name the dominant kernel
     for the roofline. CPU baseline: the same graph through the Engine and the ATen CPU reference
     plugin on this host's cores (bf16, one run after one warm-up)."""
     import torch
 
     import dli
-    from dli_qwen2 import QWEN2_0_5B, build_prefill_graph, random_weights
+    from dataclasses import replace
+
+    from dli_qwen2 import QWEN2_0_5B, build_prefill_graph, pack_fused_weights, random_weights
 
     cfg = QWEN2_0_5B
     B, S = args.batch or 4, 2048
@@ -379,15 +382,19 @@ def bench_prefill(args):
     node_flops = {
         "q_proj": 2 * T * H * Hq * D, "k_proj": 2 * T * H * Hkv * D, "v_proj": 2 * T * H * Hkv * D,
         "attention": 2 * 2 * B * Hq * D * (S * (S + 1) // 2), "o_proj": 2 * T * Hq * D * H,
-        "gate_proj": 2 * T * H * F, "up_proj": 2 * T * H * F, "down_proj": 2 * T * F * H}
+        "gate_up": 2 * 2 * T * H * F, "down_proj": 2 * T * F * H}
     flops = sum(node_flops.values())
     w = {k: v for k, v in random_weights(cfg, seed=0, device="cuda").items()
          if k.startswith("model.layers.0.") or k.startswith("rotary")}
+    w = pack_fused_weights(replace(cfg, layers=1), w)  # + the interleaved gate/up weight
     g = torch.Generator().manual_seed(1)
     h = torch.randn(B, S, H, generator=g).to(torch.bfloat16).cuda()
     engine = dli.Engine().load_plugin()
     engine.configure_kv_cache(block_size=64, max_seq_len=S)
-    graph = build_prefill_graph(cfg, B, S, layers=1, from_hidden=True)
+    # the fused layer (o_proj and down_proj with their residual adds, gate/up with SwiGLU in one
+    # GEMM); the CPU baseline runs the reference's node sequence (same values)
+    graph = build_prefill_graph(cfg, B, S, layers=1, from_hidden=True, fused=True)
+    ref_graph = build_prefill_graph(cfg, B, S, layers=1, from_hidden=True)
     inputs = {**w, "hidden_states": h}
 
     def run(profile=None):
@@ -438,10 +445,10 @@ def bench_prefill(args):
         cpu_engine.configure_kv_cache(block_size=64, max_seq_len=S)
         cpu_inputs = {k: v.cpu() for k, v in inputs.items()}
         cpu_engine.set_kv_cache_length(0)
-        ref = cpu_engine.run(graph, cpu_inputs)["output"]  # warm-up, and the parity reference
+        ref = cpu_engine.run(ref_graph, cpu_inputs)["output"]  # warm-up, and the parity reference
         cpu_engine.set_kv_cache_length(0)
         t1 = time.perf_counter()
-        cpu_engine.run(graph, cpu_inputs)
+        cpu_engine.run(ref_graph, cpu_inputs)
         cpu_s = time.perf_counter() - t1
         got = run().float().cpu()
         rel = float((got - ref.float()).norm() / ref.float().norm())

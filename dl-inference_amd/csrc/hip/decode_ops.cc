@@ -41,6 +41,24 @@ MbKernels k_gate_up("decode", "gate_up_silu");
 MbKernels k_lm_head("decode", "lm_head_argmax");
 DeviceKernel k_res_norm("decode", "residual_rms_norm");
 DeviceKernel k_argmax_final("decode", "argmax_finalize");
+// many-row (prefill) forms of linear_residual and gate_up_silu: tiled MFMA GEMMs with the same
+// epilogues (mfma_gemm.hip)
+DeviceKernel k_mfma_linres64("mfma_gemm", "mfma_linear_residual_bf16_t64");
+DeviceKernel k_mfma_linres128("mfma_gemm", "mfma_linear_residual_bf16_t128");
+DeviceKernel k_mfma_gu64("mfma_gemm", "mfma_gate_up_silu_bf16_t64");
+DeviceKernel k_mfma_gu128("mfma_gemm", "mfma_gate_up_silu_bf16_t128");
+
+// Tiled launch of those: 128 x 128 tiles once they alone give every CU a workgroup, else 64 x 64;
+// grid (column tiles, row tiles).
+bool tiledGrid(int64_t rows, int64_t cols, bool* big, unsigned (&grid)[2]) {
+  *big = ((rows + 127) / 128) * ((cols + 127) / 128) >= 256;
+  const int64_t tile = *big ? 128 : 64;
+  const int64_t gx = (cols + tile - 1) / tile, gy = (rows + tile - 1) / tile;
+  if (gy > 65535 || gx > (int64_t{1} << 31)) return false;
+  grid[0] = static_cast<unsigned>(gx);
+  grid[1] = static_cast<unsigned>(gy);
+  return true;
+}
 DeviceKernel k_dec_attn("attention", "decode_attention_d64");
 DeviceKernel k_dec_attn128("attention", "decode_attention_d128");
 
@@ -152,6 +170,16 @@ int dli_hip_linear_residual(const void* x, const void* w, const void* bias, cons
                             void* out, int64_t m, int64_t n, int64_t k, int splits,
                             void* workspace, size_t workspace_bytes, void* stream) {
   const char* op = "linear_residual";
+  if (m > 64) {  // many rows (a prompt): one tiled MFMA GEMM, no split
+    if (n <= 0) return bad(op, "n must be positive");
+    if (k <= 0 || k % 8 != 0) return bad(op, "k must be a positive multiple of 8");
+    if (!aligned16(x) || !aligned16(w)) return bad(op, "x and w must be 16-byte aligned");
+    bool big = false;
+    unsigned grid[2];
+    if (!tiledGrid(m, n, &big, grid)) return bad(op, "too many rows");
+    return launch(big ? k_mfma_linres128 : k_mfma_linres64, {grid[0], grid[1]}, {256}, 0,
+                  stream, x, w, bias, residual, out, m, n, k);
+  }
   if (int rc = checkSkinny(op, m, k)) return rc;
   if (n <= 0) return bad(op, "n must be positive");
   if (splits < 1 || splits > k / 64 || splits > kMaxNormSplits)
@@ -188,6 +216,22 @@ int dli_hip_gate_up_silu(const void* hidden, const void* norm_weight, const void
                          void* out, int64_t m, int64_t ffn, int64_t hidden_size, float eps,
                          void* stream) {
   const char* op = "gate_up_silu";
+  if (m > 64) {
+    // many rows (a prompt): one tiled MFMA GEMM over the interleaved weight, SwiGLU in its
+    // epilogue
+    if (ffn <= 0 || ffn % 16 != 0) return bad(op, "ffn must be a positive multiple of 16");
+    if (hidden_size <= 0 || hidden_size % 8 != 0)
+      return bad(op, "hidden_size must be a positive multiple of 8");
+    if (norm_weight != nullptr)
+      return bad(op, "the RMSNorm prologue is for at most 64 rows (normalize first)");
+    if (!aligned16(hidden) || !aligned16(w_gate_up))
+      return bad(op, "hidden and w_gate_up must be 16-byte aligned");
+    bool big = false;
+    unsigned grid[2];
+    if (!tiledGrid(m, 2 * ffn, &big, grid)) return bad(op, "too many rows");
+    return launch(big ? k_mfma_gu128 : k_mfma_gu64, {grid[0], grid[1]}, {256}, 0, stream, hidden,
+                  w_gate_up, out, m, ffn, hidden_size);
+  }
   if (int rc = checkSkinny(op, m, hidden_size)) return rc;
   if (ffn <= 0 || ffn % 16 != 0) return bad(op, "ffn must be a positive multiple of 16");
   if (hidden_size > kMaxLmK) return bad(op, "hidden_size above 1024 is not supported");

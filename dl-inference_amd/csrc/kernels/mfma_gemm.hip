@@ -10,6 +10,8 @@
 //                           x while staging (never materialised); out NCHW, optional fused ReLU
 //  mfma_linear_bf16_<t>     bf16 x, w (K % 8 == 0), bf16 MFMA 16x16x32, fp32 accumulation,
 //                           bf16 or fp32 out, optional ReLU
+//  mfma_linear_residual_bf16_<t>  the same plus a residual add (bf16 out)
+//  mfma_gate_up_silu_bf16_<t>     the same over an interleaved gate/up weight, SwiGLU epilogue
 //  mfma_linear_f32_splitk   fp32 linear / conv2d with K split over grid.z into a workspace,
 //  mfma_conv2d_f32_splitk   then a fixed-order sum with bias and ReLU (splitk_reduce_f32,
 //                           conv_splitk_reduce_f32)
@@ -242,16 +244,32 @@ __device__ __forceinline__ void gemmF32(ASrc A, BSrc B, int64_t R, int64_t Cn, i
                 a4[i][s / 4][s % 4], b4[j][s / 4][s % 4], acc[i][j], 0, 0, 0);
     }
   }
+  if constexpr (Epi::kPairs) {
+    // column blocks 2 p and 2 p + 1 (16 wide) of a wave's tile go to one epi.pair call: the
+    // C columns of an interleaved [gate 16 | up 16] weight pair up in the same lane
+    static_assert(TN % 2 == 0, "column block pairs");
 #pragma unroll
-  for (int i = 0; i < TM; ++i)
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int j = 0; j < TN; ++j)
+      for (int j = 0; j < TN; j += 2)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int64_t row = r0 + wr * (BM / 2) + i * 16 + fk * 4 + v;
-        const int64_t col = c0 + wc * (BN / 2) + j * 16 + fr;
-        if (row < R && col < Cn) epi(row, col, acc[i][j][v]);
-      }
+        for (int v = 0; v < 4; ++v) {
+          const int64_t row = r0 + wr * (BM / 2) + i * 16 + fk * 4 + v;
+          const int64_t col = c0 + wc * (BN / 2) + j * 16 + fr;
+          if (row < R && col + 16 < Cn) epi.pair(row, col, acc[i][j][v], acc[i][j + 1][v]);
+        }
+  } else {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int64_t row = r0 + wr * (BM / 2) + i * 16 + fk * 4 + v;
+          const int64_t col = c0 + wc * (BN / 2) + j * 16 + fr;
+          if (row < R && col < Cn) epi(row, col, acc[i][j][v]);
+        }
+  }
 }
 
 // ---- bf16 core ---------------------------------------------------------------------------------
@@ -330,16 +348,32 @@ __device__ __forceinline__ void gemmBf16(const uint16_t* a, const uint16_t* b, i
                                                               acc[i][j], 0, 0, 0);
     }
   }
+  if constexpr (Epi::kPairs) {
+    // column blocks 2 p and 2 p + 1 (16 wide) of a wave's tile go to one epi.pair call: the
+    // C columns of an interleaved [gate 16 | up 16] weight pair up in the same lane
+    static_assert(TN % 2 == 0, "column block pairs");
 #pragma unroll
-  for (int i = 0; i < TM; ++i)
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int j = 0; j < TN; ++j)
+      for (int j = 0; j < TN; j += 2)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int64_t row = r0 + wr * (BM / 2) + i * 16 + fk * 4 + v;
-        const int64_t col = c0 + wc * (BN / 2) + j * 16 + fr;
-        if (row < R && col < Cn) epi(row, col, acc[i][j][v]);
-      }
+        for (int v = 0; v < 4; ++v) {
+          const int64_t row = r0 + wr * (BM / 2) + i * 16 + fk * 4 + v;
+          const int64_t col = c0 + wc * (BN / 2) + j * 16 + fr;
+          if (row < R && col + 16 < Cn) epi.pair(row, col, acc[i][j][v], acc[i][j + 1][v]);
+        }
+  } else {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int64_t row = r0 + wr * (BM / 2) + i * 16 + fk * 4 + v;
+          const int64_t col = c0 + wc * (BN / 2) + j * 16 + fr;
+          if (row < R && col < Cn) epi(row, col, acc[i][j][v]);
+        }
+  }
 }
 
 // ---- epilogues ---------------------------------------------------------------------------------
@@ -347,6 +381,7 @@ __device__ __forceinline__ void gemmBf16(const uint16_t* a, const uint16_t* b, i
 // out[row * ldo + col] = act(v + bias[col]) as T
 template <typename T, typename BiasT>
 struct RowMajorOut {
+  static constexpr bool kPairs = false;
   T* out;
   const BiasT* bias;
   int64_t ldo;
@@ -358,8 +393,40 @@ struct RowMajorOut {
   }
 };
 
+// out[row, col] = bf16(residual[row, col] + bf16(v + bias[col])): a linear whose output is
+// added to the residual stream, rounded where the unfused graph rounds (linear, then add).
+struct ResidualOut {
+  static constexpr bool kPairs = false;
+  bf16* out;
+  const bf16* residual;
+  const bf16* bias;
+  int64_t ldo;
+  __device__ __forceinline__ void operator()(int64_t row, int64_t col, float v) const {
+    if (bias != nullptr) v += ld(bias + col);
+    const float o = Num<bf16>::round(v);
+    st(out + row * ldo + col, ld(residual + row * ldo + col) + o);
+  }
+};
+
+// SwiGLU of a [gate 16 | up 16]-interleaved weight (the layout of the fused decode weights):
+// C columns 32 b + j (gate) and 32 b + 16 + j (up) give act[row, 16 b + j] =
+// bf16(bf16(silu(bf16(gate))) * bf16(up)), the rounding points of the unfused linear, silu and
+// mul nodes.
+struct SwiGluOut {
+  static constexpr bool kPairs = true;
+  bf16* out;
+  int64_t ffn;
+  __device__ __forceinline__ void pair(int64_t row, int64_t col, float gate, float up) const {
+    FP_EXACT;
+    const float g = Num<bf16>::round(gate), u = Num<bf16>::round(up);
+    const float sg = Num<bf16>::round(g / (1.0f + expf(-g)));
+    st(out + row * ffn + (col / 32) * 16 + col % 16, sg * u);
+  }
+};
+
 // out[n, oc, oy, ox] = act(v + bias[oc]) for C row oc and C column pixel (n, oy, ox)
 struct ConvOut {
+  static constexpr bool kPairs = false;
   float* out;
   const float* bias;
   int64_t OC, OHW;
@@ -473,3 +540,23 @@ extern "C" __global__ void __launch_bounds__(kGemmThreads)
 
 DK_MFMA_BF16(64, 64)
 DK_MFMA_BF16(128, 128)
+
+// bf16 linear + residual (bf16 out) and SwiGLU of an interleaved gate/up weight (N = 2 * ffn,
+// ffn % 16 == 0): the ResidualOut and SwiGluOut epilogues above.
+#define DK_MFMA_BF16_FUSED(BM, BN)                                                              \
+  extern "C" __global__ void __launch_bounds__(kGemmThreads) mfma_linear_residual_bf16_t##BM(  \
+      const uint16_t* x, const uint16_t* w, const uint16_t* bias, const uint16_t* residual,    \
+      uint16_t* out, int64_t M, int64_t N, int64_t K) {                                        \
+    gemmBf16<BM, BN>(x, w, M, N, K,                                                            \
+                     ResidualOut{reinterpret_cast<bf16*>(out),                                  \
+                                 reinterpret_cast<const bf16*>(residual),                      \
+                                 reinterpret_cast<const bf16*>(bias), N});                     \
+  }                                                                                            \
+  extern "C" __global__ void __launch_bounds__(kGemmThreads) mfma_gate_up_silu_bf16_t##BM(     \
+      const uint16_t* x, const uint16_t* w_gate_up, uint16_t* out, int64_t M, int64_t ffn,      \
+      int64_t K) {                                                                             \
+    gemmBf16<BM, BN>(x, w_gate_up, M, 2 * ffn, K, SwiGluOut{reinterpret_cast<bf16*>(out), ffn}); \
+  }
+
+DK_MFMA_BF16_FUSED(64, 64)
+DK_MFMA_BF16_FUSED(128, 128)

@@ -231,10 +231,15 @@ def build_decode_graph(cfg: Qwen2Config, batch: int, fused: bool = True,
     return dli.Graph.from_json(json.dumps(graph))
 
 
-def _prefill_layer_nodes(cfg: Qwen2Config, batch: int, seq: int, i: int, h: str, nodes: list) -> str:
+def _prefill_layer_nodes(cfg: Qwen2Config, batch: int, seq: int, i: int, h: str, nodes: list,
+                         fused: bool = False) -> str:
     """One decoder layer over [B, S, H] activations (the exporter's node sequence,
     python/dli_export/export.py:272-424, with the [B, S, H, D] <-> [B, H, S, D] transposes a
-    prompt of S tokens needs around rotary and attention). Returns the layer's output name."""
+    prompt of S tokens needs around rotary and attention). With fused, o_proj + residual and
+    down_proj + residual are linear_residual nodes and gate_proj, up_proj, act_fn and mul one
+    gate_up_silu node over the interleaved mlp.gate_up_proj.weight (pack_fused_weights): the
+    same values (each fused kernel rounds where the nodes it replaces round). Returns the layer's
+    output name."""
     p, t = f"model.layers.{i}", f"layers_{i}"
     q_w = cfg.heads * cfg.head_dim
     _node(nodes, f"{p}.input_layernorm", "rms_norm", [h, f"{p}.input_layernorm.weight"],
@@ -258,13 +263,25 @@ def _prefill_layer_nodes(cfg: Qwen2Config, batch: int, seq: int, i: int, h: str,
           [f"{t}_attention_bshd"], {"perm": [0, 2, 1, 3]})
     _node(nodes, f"{p}.self_attn.merge", "reshape", [f"{t}_attention_bshd"],
           [f"{t}_attention_merged"], {"shape": [batch, seq, q_w]})
-    _node(nodes, f"{p}.self_attn.o_proj", "linear",
-          [f"{t}_attention_merged", f"{p}.self_attn.o_proj.weight"], [f"{t}_attention_proj"])
-    _node(nodes, f"{p}.attention_residual", "add", [h, f"{t}_attention_proj"],
-          [f"{t}_after_attention"])
+    if fused:
+        _node(nodes, f"{p}.self_attn.o_proj", "linear_residual",
+              [f"{t}_attention_merged", f"{p}.self_attn.o_proj.weight", h],
+              [f"{t}_after_attention"])
+    else:
+        _node(nodes, f"{p}.self_attn.o_proj", "linear",
+              [f"{t}_attention_merged", f"{p}.self_attn.o_proj.weight"], [f"{t}_attention_proj"])
+        _node(nodes, f"{p}.attention_residual", "add", [h, f"{t}_attention_proj"],
+              [f"{t}_after_attention"])
     _node(nodes, f"{p}.post_attention_layernorm", "rms_norm",
           [f"{t}_after_attention", f"{p}.post_attention_layernorm.weight"],
           [f"{t}_post_attention_norm"], {"eps": cfg.eps})
+    if fused:
+        _node(nodes, f"{p}.mlp.gate_up", "gate_up_silu",
+              [f"{t}_post_attention_norm", f"{p}.mlp.gate_up_proj.weight"], [f"{t}_gated"])
+        _node(nodes, f"{p}.mlp.down_proj", "linear_residual",
+              [f"{t}_gated", f"{p}.mlp.down_proj.weight", f"{t}_after_attention"],
+              [f"{t}_output"])
+        return f"{t}_output"
     _node(nodes, f"{p}.mlp.gate_proj", "linear",
           [f"{t}_post_attention_norm", f"{p}.mlp.gate_proj.weight"], [f"{t}_gate"])
     _node(nodes, f"{p}.mlp.up_proj", "linear",
@@ -279,7 +296,8 @@ def _prefill_layer_nodes(cfg: Qwen2Config, batch: int, seq: int, i: int, h: str,
 
 
 def build_prefill_graph(cfg: Qwen2Config, batch: int, seq: int, layers: int | None = None,
-                        from_hidden: bool = False, fused_head: bool = True) -> "dli.Graph":
+                        from_hidden: bool = False, fused_head: bool = True,
+                        fused: bool = False) -> "dli.Graph":
     """Prefill of a `seq`-token prompt per sequence (every sequence starts at position 0 of an
     empty KV cache; the cache entries layer_0.. are filled with the prompt's keys and values, so
     decode-step graphs continue at position `seq`).
@@ -289,7 +307,8 @@ def build_prefill_graph(cfg: Qwen2Config, batch: int, seq: int, layers: int | No
     (lm_head_argmax; with fused_head=False the reference's rms_norm, linear and argmax nodes);
     outputs logits [B, V] and next_ids [B] (the first generated token).
     from_hidden=True: hidden_states [B, S, H] -> the decoder layers (the first `layers`) ->
-    output hidden [B, S, H] (one decoder layer of prefill, the config-3 workload)."""
+    output hidden [B, S, H] (one decoder layer of prefill, the config-3 workload).
+    fused: the layers' fused form (_prefill_layer_nodes), which reads mlp.gate_up_proj.weight."""
     n_layers = cfg.layers if layers is None else layers
     nodes: list = []
     h = "hidden_states"
@@ -297,7 +316,7 @@ def build_prefill_graph(cfg: Qwen2Config, batch: int, seq: int, layers: int | No
         _node(nodes, "model.embed_tokens", "embedding",
               ["input_ids", "model.embed_tokens.weight"], [h])
     for i in range(n_layers):
-        h = _prefill_layer_nodes(cfg, batch, seq, i, h, nodes)
+        h = _prefill_layer_nodes(cfg, batch, seq, i, h, nodes, fused)
     if from_hidden:
         _node(nodes, "output", "reshape", [h], ["output"], {"shape": [batch, seq, cfg.hidden]})
         graph = {"format": "dli.graph.v1", "model_type": "qwen2_prefill_layers",

@@ -116,7 +116,8 @@ class DecodeSession:
             raise ValueError("prompt exceeds the KV cache capacity")
         graph = self._prefill_graphs.get(s)
         if graph is None:
-            graph = build_prefill_graph(self.cfg, b, s, fused_head=prompt.is_cuda)
+            on_gpu = prompt.is_cuda and self.fused and not uses_large_graph(self.cfg, self.fused)
+            graph = build_prefill_graph(self.cfg, b, s, fused_head=prompt.is_cuda, fused=on_gpu)
             self._prefill_graphs[s] = graph
         self.engine.set_kv_cache_length(0)  # the prompt starts every sequence at position 0
         inputs = dict(self.inputs)

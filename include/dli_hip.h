@@ -293,7 +293,8 @@ int dli_hip_qkv_rope_append(const void* hidden, const void* norm_weight, const v
  * [2, min(8, k / 64)] splits K over workgroups: each stores a partial tile in the workspace and
  * the last to finish a tile sums them in split order and writes it. The workspace
  * (dli_hip_splitk_workspace bytes) must be zero-filled before its first use; every call leaves
- * its arrival counters at zero again. */
+ * its arrival counters at zero again. With m > 64 (a prompt: k % 8 == 0) one tiled MFMA GEMM
+ * computes it with the add in its epilogue; splits and the workspace are then not used. */
 int dli_hip_linear_residual(const void* x, const void* w, const void* bias, const void* residual,
                             void* out, int64_t m, int64_t n, int64_t k, int splits,
                             void* workspace, size_t workspace_bytes, void* stream);
@@ -313,7 +314,9 @@ int dli_hip_linear_residual_norm(const void* x, const void* w, const void* bias,
  * gate/up projections of xn -> silu(gate) * up, out [m, ffn]; hidden <= 1024. w_gate_up
  * interleaves the two weights in blocks of 16 rows: rows [32i, 32i+16) = gate rows
  * [16i, 16i+16), rows [32i+16, 32i+32) = up rows [16i, 16i+16). Replaces
- * post_attention_layernorm, gate_proj, up_proj, act_fn and mul (export.py:378-414). */
+ * post_attention_layernorm, gate_proj, up_proj, act_fn and mul (export.py:378-414). With
+ * m > 64 (a prompt) one tiled MFMA GEMM over the interleaved weight computes it, the SwiGLU in
+ * its epilogue (any hidden_size % 8 == 0); norm_weight must then be NULL (normalize first). */
 int dli_hip_gate_up_silu(const void* hidden, const void* norm_weight, const void* w_gate_up,
                          void* out, int64_t m, int64_t ffn, int64_t hidden_size, float eps,
                          void* stream);

@@ -91,8 +91,16 @@ def test_fused_decode_entry_points_reject_invalid_arguments():
     assert lib.dli_hip_lm_head_argmax(None, None, None, hip.F32, None, 2, 100, 2048, None, 0,
                                       None) == -1
     assert b"hidden_size above 1024" in lib.dli_hip_last_error()
-    assert lib.dli_hip_gate_up_silu(None, None, None, None, 65, 32, 64, 1e-6, None) == -1
+    assert lib.dli_hip_gate_up_silu(None, None, None, None, 0, 32, 64, 1e-6, None) == -1
     assert b"batch rows" in lib.dli_hip_last_error()
+    # more than 64 rows take the tiled GEMM, which has no RMSNorm prologue
+    assert lib.dli_hip_gate_up_silu(None, fake, None, None, 65, 32, 64, 1e-6, None) == -1
+    assert b"at most 64 rows" in lib.dli_hip_last_error()
+    assert lib.dli_hip_gate_up_silu(None, None, None, None, 65, 30, 64, 1e-6, None) == -1
+    assert b"multiple of 16" in lib.dli_hip_last_error()
+    assert lib.dli_hip_linear_residual(None, None, None, None, None, 100, 64, 12, 1, None, 0,
+                                       None) == -1
+    assert b"multiple of 8" in lib.dli_hip_last_error()
     assert lib.dli_hip_qkv_rope_append(None, None, None, None, None, None, 8, None, hip.I64, None,
                                        None, None, None, 64, 1, 2, 64, 2, 1, 16, 1e-6, None) == -1
     assert b"positions" in lib.dli_hip_last_error()
