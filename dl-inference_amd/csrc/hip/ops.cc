@@ -70,6 +70,7 @@ FloatKernels k_paged_attention("attention", "paged_attention");
 FloatKernels k_kv_append("attention", "kv_append");
 FloatKernels k_conv2d("conv", "conv2d");
 DeviceKernel k_flash_attention("flash_attention", "flash_attention_bf16");
+DeviceKernel k_flash_attention_q32("flash_attention", "flash_attention_bf16_q32");
 DeviceKernel k_mfma_linear64("mfma_gemm", "mfma_linear_f32_t64");
 DeviceKernel k_mfma_linear128("mfma_gemm", "mfma_linear_f32_t128");
 DeviceKernel k_mfma_matmul64("mfma_gemm", "mfma_matmul_f32_t64");
@@ -466,13 +467,16 @@ int dli_hip_attention(int dtype, const void* q, const void* k, const void* v, vo
   if (rows == 0) return 0;
   if (q == nullptr || k == nullptr || v == nullptr || out == nullptr)
     return badArg("attention", "NULL pointer");
-  // bf16 with head_dim 64 (prefill): flash-style MFMA kernel, 64 queries per workgroup
+  // bf16 with head_dim 64 (prefill): flash-style MFMA kernel, 128 queries per workgroup (64 for
+  // query sequences of at most 64)
   if (dtype == DLI_BF16 && head_dim == 64 && seq_k > 0 && batch * q_heads <= 65535 &&
       seq_q < (int64_t{1} << 30) && seq_k < (int64_t{1} << 30) &&
       aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out)) {
     const float log2e = 1.4426950408889634f;
-    return launch(k_flash_attention,
-                  {static_cast<unsigned>((seq_q + 63) / 64), static_cast<unsigned>(batch * q_heads)},
+    const int64_t tile_q = seq_q > 64 ? 128 : 64;
+    return launch(tile_q == 128 ? k_flash_attention_q32 : k_flash_attention,
+                  {static_cast<unsigned>((seq_q + tile_q - 1) / tile_q),
+                   static_cast<unsigned>(batch * q_heads)},
                   {256}, 0, stream, q, k, v, out, q_heads, kv_heads, seq_q, seq_k, causal,
                   scale * log2e);
   }

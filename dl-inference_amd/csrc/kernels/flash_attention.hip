@@ -9,11 +9,13 @@
 //      from LDS, B = 32 d x 16 queries from registers): lane l then holds the scores of query
 //      l % 16 for keys 4 (l / 16) + i of each 16-key block;
 //   2. runs the online softmax per query (a column of S^T: the lane's 16 values, then lanes
-//      l ^ 16 and l ^ 32 through permlane swaps) in fp32, base 2, scale folded in;
+//      l ^ 16 and l ^ 32 through permlane swaps) in fp32, base 2, scale folded in, with a lazy
+//      rescale of the running output;
 //   3. accumulates O^T += V^T P^T with the same MFMA: the lane's probabilities, rounded to bf16,
 //      are already the B operand (8 keys per lane group: 4 from each of two 16-key blocks), and
 //      A takes V^T rows over those same 8 keys from LDS. k order only has to agree between A and
-//      B, so no shuffle of P is needed.
+//      B, so no shuffle of P is needed. The row sums of P come from the same MFMA with an
+//      all-ones A operand (the matrix cores have slack; the vector ALUs do not).
 // Query tiles are walked from the last (most keys under a causal mask) to the first.
 #include "common.h"
 #include "skinny.h"
@@ -30,6 +32,8 @@ constexpr int kPitch = 72;    // K row pitch in bf16 (144 bytes: 16-byte aligned
 // 4-byte words to rows d0 + j of 8 column groups d0 = 8m: at 34 words per row those rows start
 // 16 banks apart (at 36 words, every other group landed on the same banks).
 constexpr int kVPitch = 68;
+// log2 of the largest probability the lazy rescale lets through before moving the reference
+constexpr float kRescaleLog2 = 8.f;
 
 typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
 
@@ -44,10 +48,15 @@ __device__ void flashAttention(const uint16_t* q, const uint16_t* k, const uint1
   __shared__ __attribute__((aligned(16))) uint16_t Vt[kD * kVPitch];
   const int t = threadIdx.x, lane = t % kWave, wave = t / kWave;
   const int r = lane % 16, g = lane / 16;
-  const int64_t bh = blockIdx.y;  // b * Hq + h
+  // Workgroups are dispatched in linear-id order, and the query tile is the slow index of that
+  // order, walked from the last tile (most keys under a causal mask) to the first: the longest
+  // workgroups start first and the short ones fill in behind them. (With the tile as the fast
+  // index, a long tile dispatched late set the kernel's end: 114 us against 67 us at 4 x 2048.)
+  const uint64_t lin = blockIdx.x + static_cast<uint64_t>(gridDim.x) * blockIdx.y;
+  const int64_t bh = lin % gridDim.y;  // b * Hq + h
   const int64_t b = bh / Hq, h = bh % Hq;
   const int64_t kvh = h / (Hq / Hkv);
-  const int64_t q0 = static_cast<int64_t>(gridDim.x - 1 - blockIdx.x) * kTileQ;
+  const int64_t q0 = static_cast<int64_t>(gridDim.x - 1 - lin / gridDim.y) * kTileQ;
   const int64_t qw = q0 + wave * 16 * QB;  // the wave's first query
   const uint16_t* kbase = k + (b * Hkv + kvh) * Sk * kD;
   const uint16_t* vbase = v + (b * Hkv + kvh) * Sk * kD;
@@ -78,14 +87,25 @@ __device__ void flashAttention(const uint16_t* q, const uint16_t* k, const uint1
   // d0 = (t % 8) * 8 of the K tile and of the V tile. Two adjacent keys of the same columns let
   // the transposed V store write 4-byte words (keys 2p, 2p + 1 of one d).
   const int pair_key = 2 * (t / 8), d0 = (t % 8) * 8;
+  const uint16_t* kp = kbase + pair_key * kD + d0;
+  const uint16_t* vp = vbase + pair_key * kD + d0;
   U128 kr[2], vr[2];
   auto fetch = [&](int64_t k0) {
+    const uint16_t* kq = kp + k0 * kD;
+    const uint16_t* vq = vp + k0 * kD;
+    if (k0 + kTileK <= Sk) {  // uniform: every key of the tile exists
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int64_t key = k0 + pair_key + u;
-      const int64_t off = key * kD + d0;
-      kr[u] = key < Sk ? gload16(kbase + off) : zero16();
-      vr[u] = key < Sk ? gload16(vbase + off) : zero16();
+      for (int u = 0; u < 2; ++u) {
+        kr[u] = gload16(kq + u * kD);
+        vr[u] = gload16(vq + u * kD);
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const bool in = k0 + pair_key + u < Sk;
+        kr[u] = in ? gload16(kq + u * kD) : zero16();
+        vr[u] = in ? gload16(vq + u * kD) : zero16();
+      }
     }
   };
   auto stash = [&] {
@@ -103,14 +123,18 @@ __device__ void flashAttention(const uint16_t* q, const uint16_t* k, const uint1
   };
 
   f32x4 o[QB][4];  // O^T tiles: d = 16 dt + 4 g + i, query 16 qb + r
-  float m_run[QB], l_run[QB];
+  // row sums of the bf16 probabilities, as an MFMA against an all-ones A operand: every element
+  // of lane (r, g) ends up holding the sum for query 16 qb + r (only element 0 is kept current)
+  f32x4 lsum[QB];
+  float m_run[QB];
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
     m_run[qb] = -INFINITY;
-    l_run[qb] = 0.f;
+    lsum[qb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) o[qb][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
+  const U128 ones{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};  // bf16 1.0 x 8
 
   const int tiles = static_cast<int>((wg_keys + kTileK - 1) / kTileK);
   if (tiles > 0) fetch(0);
@@ -136,9 +160,9 @@ __device__ void flashAttention(const uint16_t* q, const uint16_t* k, const uint1
                                                             s[qb][kk], 0, 0, 0);
       }
     }
-    // 2. online softmax per query (masked keys: -inf). The running max is kept in scaled units;
-    // max(s * c) = c * max(s) for the positive scale c, so each probability is one fma and one
-    // v_exp_f32 (every argument <= 0 or -inf, results in [0, 1], no range reduction needed).
+    // 2. online softmax per query (masked keys: -inf). The reference point is kept in scaled
+    // units; max(s * c) = c * max(s) for the positive scale c, so each probability is one fma
+    // and one v_exp_f32 (every argument <= kRescaleLog2 or -inf).
     const bool full = k0 + kTileK <= wave_keys;  // uniform over the wave: every key visible
     bf16x8 pb[QB][2];
 #pragma unroll
@@ -161,23 +185,25 @@ __device__ void flashAttention(const uint16_t* q, const uint16_t* k, const uint1
           }
       }
       tmax = rowsMax(tmax);  // over lanes r, r + 16, r + 32, r + 48: the query's 64 keys
-      const float m_new = fmaxf(m_run[qb], tmax * scale_log2);
-      // a query that has seen no key yet keeps m = -inf and probabilities 0
-      const float base = m_new == -INFINITY ? 0.f : m_new;
-      const float alpha = __builtin_amdgcn_exp2f(m_run[qb] - base);  // 0 while m_run = -inf
-      float psum = 0.f;
+      // Lazy rescale: the reference point m_run moves only when a score passes it by more than
+      // kRescaleLog2 (base 2), so probabilities stay below 2^kRescaleLog2 and the o / lsum
+      // rescale runs on few tiles. The final o / l is unchanged by the choice of reference.
+      // A query that has seen no key yet keeps m = -inf and probabilities 0.
+      const float tm = tmax * scale_log2;
+      const bool grow = tm > m_run[qb] + kRescaleLog2;  // false while tm = -inf
+      if (__builtin_amdgcn_ballot_w64(grow)) {
+        const float alpha = grow ? __builtin_amdgcn_exp2f(m_run[qb] - tm) : 1.f;  // 0 from -inf
+        m_run[qb] = grow ? tm : m_run[qb];
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) o[qb][dt] *= alpha;
+        lsum[qb][0] *= alpha;
+      }
+      const float base = m_run[qb] == -INFINITY ? 0.f : m_run[qb];
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float pv = __builtin_amdgcn_exp2f(fmaf(s[qb][kk][i], scale_log2, -base));
-          s[qb][kk][i] = pv;
-          psum += pv;
-        }
-      l_run[qb] = l_run[qb] * alpha + rowsSum(psum);
-      m_run[qb] = m_new;
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt) o[qb][dt] *= alpha;
+        for (int i = 0; i < 4; ++i)
+          s[qb][kk][i] = __builtin_amdgcn_exp2f(fmaf(s[qb][kk][i], scale_log2, -base));
       // keys of 32-key chunk kc, lane group g: 4 g + i of blocks 2 kc and 2 kc + 1
 #pragma unroll
       for (int kc = 0; kc < 2; ++kc) {
@@ -200,12 +226,19 @@ __device__ void flashAttention(const uint16_t* q, const uint16_t* k, const uint1
           o[qb][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(asBf16x8(va), pb[qb][kc],
                                                               o[qb][dt], 0, 0, 0);
       }
+#pragma unroll
+    for (int kc = 0; kc < 2; ++kc)
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb)
+        lsum[qb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(asBf16x8(ones), pb[qb][kc], lsum[qb],
+                                                           0, 0, 0);
   }
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
     const int64_t qi = qw + qb * 16 + r;
     if (qi >= Sq) continue;
-    const float inv = l_run[qb] > 0.f ? 1.f / l_run[qb] : 0.f;
+    const float l = lsum[qb][0];
+    const float inv = l > 0.f ? 1.f / l : 0.f;
     uint16_t* orow = out + (bh * Sq + qi) * kD + g * 4;
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) {
@@ -218,11 +251,24 @@ __device__ void flashAttention(const uint16_t* q, const uint16_t* k, const uint1
 
 }  // namespace
 
-// 16 queries per wave. With QB = 2 (32 per wave, 128 per workgroup) the kernel needs 150 VGPRs,
-// halving occupancy, and measured slower at the Qwen2 prefill size (140 us against 125 us).
-extern "C" __global__ void __launch_bounds__(kFlashThreads)
+// amdgpu_waves_per_eu(2) caps the kernels at 256 VGPRs, which makes the compiler pick the VGPR
+// form of the MFMAs: in the AGPR form every tile moved the score and output accumulators through
+// v_accvgpr_read / write (80 extra VALU instructions per tile). Grid: {ceil(Sq / (64 QB)), B Hq}.
+//
+// 16 queries per wave (64 per workgroup): short query sequences.
+extern "C" __global__ void __launch_bounds__(kFlashThreads) __attribute__((amdgpu_waves_per_eu(2)))
     flash_attention_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* out,
                          int64_t Hq, int64_t Hkv, int64_t Sq, int64_t Sk, int causal,
                          float scale_log2) {
   flashAttention<1>(q, k, v, out, Hq, Hkv, Sq, Sk, causal, scale_log2);
+}
+
+// 32 queries per wave (128 per workgroup): each K and V^T fragment read from LDS feeds two MFMAs,
+// and one staged tile serves twice the queries. 154 VGPRs, 3 waves per SIMD; at the Qwen2
+// prefill size (4 x 2048 tokens, 14 / 2 heads, causal) 56 us against 67 us for the 16-query form.
+extern "C" __global__ void __launch_bounds__(kFlashThreads) __attribute__((amdgpu_waves_per_eu(2)))
+    flash_attention_bf16_q32(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                             uint16_t* out, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t Sk,
+                             int causal, float scale_log2) {
+  flashAttention<2>(q, k, v, out, Hq, Hkv, Sq, Sk, causal, scale_log2);
 }
