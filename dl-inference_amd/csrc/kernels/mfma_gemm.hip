@@ -302,11 +302,16 @@ __device__ __forceinline__ void gemmBf16(const uint16_t* a, const uint16_t* b, i
   constexpr int TM = BM / 32, TN = BN / 32;
   constexpr int VPR = BK / 8;  // 16-byte chunks per tile row
   constexpr int AV = BM * VPR / kGemmThreads, BV = BN * VPR / kGemmThreads;
-  // two buffers as separate arrays: the buffer index is static at every access
-  __shared__ __attribute__((aligned(16))) uint16_t As0[BM * BK];
-  __shared__ __attribute__((aligned(16))) uint16_t Bs0[BN * BK];
-  __shared__ __attribute__((aligned(16))) uint16_t As1[BM * BK];
-  __shared__ __attribute__((aligned(16))) uint16_t Bs1[BN * BK];
+  // the two operand buffers, then (after the last slice) the fp32 accumulator tile of the
+  // epilogue, row pitch BN + 4 floats (the 4 row groups of an MFMA tile store land 16 banks apart)
+  constexpr int CP = BN + 4;
+  constexpr int kOperandBytes = 2 * (BM + BN) * BK * 2, kTileBytes = BM * CP * 4;
+  __shared__ __attribute__((aligned(16)))
+  uint8_t smem[kOperandBytes > kTileBytes ? kOperandBytes : kTileBytes];
+  uint16_t* const As0 = reinterpret_cast<uint16_t*>(smem);
+  uint16_t* const Bs0 = As0 + BM * BK;
+  uint16_t* const As1 = Bs0 + BN * BK;
+  uint16_t* const Bs1 = As1 + BM * BK;
   const int t = threadIdx.x, lane = t % kWave, wave = t / kWave;
   const int wr = wave / 2, wc = wave % 2;
   int64_t r0, c0;
@@ -449,35 +454,91 @@ __device__ __forceinline__ void gemmBf16(const uint16_t* a, const uint16_t* b, i
     tailStep(As0, Bs0, ra1, rb1, As1, Bs1, s, nk);
     if (s + 1 < nk) tailStep(As1, Bs1, ra0, rb0, As0, Bs0, s + 1, nk);
   }
+  // Epilogue through LDS (every step ended with a barrier, so the operand buffers are free): the
+  // accumulators go to LDS as fp32, then each thread takes runs of 8 consecutive columns of a
+  // row, so bias / residual loads and output stores are 16-byte vectors. Runs that cross the
+  // right edge, and outputs the vector forms cannot address, go element by element through the
+  // same arithmetic.
+  float* const ct = reinterpret_cast<float*>(smem);
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        ct[(wr * (BM / 2) + i * 16 + fk * 4 + v) * CP + wc * (BN / 2) + j * 16 + fr] =
+            acc[i][j][v];
+  __syncthreads();
+  const bool vec = epi.vectorOk();
   if constexpr (Epi::kPairs) {
-    // column blocks 2 p and 2 p + 1 (16 wide) of a wave's tile go to one epi.pair call: the
-    // C columns of an interleaved [gate 16 | up 16] weight pair up in the same lane
-    static_assert(TN % 2 == 0, "column block pairs");
+    // [gate 16 | up 16] column groups: run h (0, 1) of group b pairs gate columns 32 b + 8 h ..
+    // with up columns 32 b + 16 + 8 h ..
+    constexpr int kRuns = BM * BN / 16;
+    static_assert(BN % 32 == 0 && kRuns % kGemmThreads == 0, "pair runs");
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+    for (int q = 0; q < kRuns / kGemmThreads; ++q) {
+      const int e = t + q * kGemmThreads;
+      const int row = e / (BN / 16), p = e % (BN / 16);
+      const int cg = (p / 2) * 32 + (p % 2) * 8;
+      const int64_t grow = r0 + row, gcol = c0 + cg;
+      if (grow >= R) continue;
+      float g[8], u[8];
 #pragma unroll
-      for (int j = 0; j < TN; j += 2)
+      for (int k = 0; k < 8; ++k) {
+        g[k] = ct[row * CP + cg + k];
+        u[k] = ct[row * CP + cg + 16 + k];
+      }
+      if (vec && gcol + 24 <= Cn) {
+        epi.pair8(grow, gcol, g, u);
+      } else {
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const int64_t row = r0 + wr * (BM / 2) + i * 16 + fk * 4 + v;
-          const int64_t col = c0 + wc * (BN / 2) + j * 16 + fr;
-          if (row < R && col + 16 < Cn) epi.pair(row, col, acc[i][j][v], acc[i][j + 1][v]);
-        }
+        for (int k = 0; k < 8; ++k)
+          if (gcol + 16 + k < Cn) epi.pair(grow, gcol + k, g[k], u[k]);
+      }
+    }
   } else {
+    constexpr int kRuns = BM * BN / 8;
+    static_assert(kRuns % kGemmThreads == 0, "runs");
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+    for (int q = 0; q < kRuns / kGemmThreads; ++q) {
+      const int e = t + q * kGemmThreads;
+      const int row = e / (BN / 8), c8 = (e % (BN / 8)) * 8;
+      const int64_t grow = r0 + row, gcol = c0 + c8;
+      if (grow >= R) continue;
+      float v[8];
 #pragma unroll
-      for (int j = 0; j < TN; ++j)
+      for (int k = 0; k < 8; ++k) v[k] = ct[row * CP + c8 + k];
+      if (vec && gcol + 8 <= Cn) {
+        epi.vec8(grow, gcol, v);
+      } else {
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const int64_t row = r0 + wr * (BM / 2) + i * 16 + fk * 4 + v;
-          const int64_t col = c0 + wc * (BN / 2) + j * 16 + fr;
-          if (row < R && col < Cn) epi(row, col, acc[i][j][v]);
-        }
+        for (int k = 0; k < 8; ++k)
+          if (gcol + k < Cn) epi(grow, gcol + k, v[k]);
+      }
+    }
   }
 }
 
 // ---- epilogues ---------------------------------------------------------------------------------
+// Scalar form epi(row, col, v) for any output; the bf16 GEMM also calls vec8(row, col, v[8]) (or
+// pair8 for kPairs) for 8 consecutive columns when vectorOk(): the same arithmetic per element,
+// with 16-byte loads and stores.
+
+__device__ __forceinline__ bool aligned16(const void* p) {
+  return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
+}
+// 8 bf16 of a 16-byte vector as floats
+__device__ __forceinline__ void unpackBf16x8(const U128& w, float (&f)[8]) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    f[2 * k] = __uint_as_float(w[k] << 16);
+    f[2 * k + 1] = __uint_as_float(w[k] & 0xFFFF0000u);
+  }
+}
+__device__ __forceinline__ U128 packBf16x8(const float (&f)[8]) {
+  return U128{packBf16x2(f[0], f[1]), packBf16x2(f[2], f[3]), packBf16x2(f[4], f[5]),
+              packBf16x2(f[6], f[7])};
+}
 
 // out[row * ldo + col] = act(v + bias[col]) as T
 template <typename T, typename BiasT>
@@ -510,6 +571,29 @@ struct RowMajorOutBf16OrF32 {
     else
       st(static_cast<bf16*>(out) + row * ldo + col, v);
   }
+  __device__ __forceinline__ bool vectorOk() const {
+    return ldo % 8 == 0 && aligned16(out) && aligned16(bias);
+  }
+  __device__ __forceinline__ void vec8(int64_t row, int64_t col, float (&v)[8]) const {
+    if (bias != nullptr) {
+      float b[8];
+      unpackBf16x8(gload16(bias + col), b);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) v[k] += b[k];
+    }
+    if (relu)
+#pragma unroll
+      for (int k = 0; k < 8; ++k) v[k] = fmaxf(v[k], 0.f);
+    if (out_f32) {
+      float* o = static_cast<float*>(out) + row * ldo + col;
+      *gp(reinterpret_cast<U128*>(o)) = U128{__float_as_uint(v[0]), __float_as_uint(v[1]),
+                                             __float_as_uint(v[2]), __float_as_uint(v[3])};
+      *gp(reinterpret_cast<U128*>(o + 4)) = U128{__float_as_uint(v[4]), __float_as_uint(v[5]),
+                                                 __float_as_uint(v[6]), __float_as_uint(v[7])};
+    } else {
+      *gp(reinterpret_cast<U128*>(static_cast<bf16*>(out) + row * ldo + col)) = packBf16x8(v);
+    }
+  }
 };
 
 // out[row, col] = bf16(residual[row, col] + bf16(v + bias[col])): a linear whose output is
@@ -524,6 +608,22 @@ struct ResidualOut {
     if (bias != nullptr) v += ld(bias + col);
     const float o = Num<bf16>::round(v);
     st(out + row * ldo + col, ld(residual + row * ldo + col) + o);
+  }
+  __device__ __forceinline__ bool vectorOk() const {
+    return ldo % 8 == 0 && aligned16(out) && aligned16(residual) && aligned16(bias);
+  }
+  __device__ __forceinline__ void vec8(int64_t row, int64_t col, float (&v)[8]) const {
+    if (bias != nullptr) {
+      float b[8];
+      unpackBf16x8(gload16(bias + col), b);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) v[k] += b[k];
+    }
+    float r[8];
+    unpackBf16x8(gload16(residual + row * ldo + col), r);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = r[k] + Num<bf16>::round(v[k]);
+    *gp(reinterpret_cast<U128*>(out + row * ldo + col)) = packBf16x8(v);
   }
 };
 
@@ -540,6 +640,20 @@ struct SwiGluOut {
     const float g = Num<bf16>::round(gate), u = Num<bf16>::round(up);
     const float sg = Num<bf16>::round(g / (1.0f + expf(-g)));
     st(out + row * ffn + (col / 32) * 16 + col % 16, sg * u);
+  }
+  __device__ __forceinline__ bool vectorOk() const { return ffn % 8 == 0 && aligned16(out); }
+  // gate columns col .. col + 7 (col % 16 == 0 or 8) with up columns col + 16 .. col + 23
+  __device__ __forceinline__ void pair8(int64_t row, int64_t col, const float (&gate)[8],
+                                        const float (&up)[8]) const {
+    FP_EXACT;
+    float o[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const float g = Num<bf16>::round(gate[k]), u = Num<bf16>::round(up[k]);
+      const float sg = Num<bf16>::round(g / (1.0f + expf(-g)));
+      o[k] = sg * u;
+    }
+    *gp(reinterpret_cast<U128*>(out + row * ffn + (col / 32) * 16 + col % 16)) = packBf16x8(o);
   }
 };
 
