@@ -61,6 +61,7 @@ DeviceKernel k_permute2("elementwise", "permute_0213_u16");
 FloatKernels k_rotary("elementwise", "rotary");
 FloatKernels k_argmax("elementwise", "argmax");
 FloatKernels k_rms_norm("norm", "rms_norm");
+DeviceKernel k_rms_norm_rows("norm", "rms_norm_rows_bf16_k");
 FloatKernels k_gemm("gemm", "gemm_tiled");
 DeviceKernel k_skinny1("gemm", "skinny_linear_m1");
 DeviceKernel k_skinny2("gemm", "skinny_linear_m2");
@@ -167,6 +168,14 @@ int dli_hip_rms_norm(int dtype, const void* x, const void* weight, void* out, in
   if (k == nullptr) return badDtype("rms_norm", dtype);
   if (rows < 0 || hidden <= 0) return badArg("rms_norm", "rows must be >= 0 and hidden > 0");
   if (rows == 0) return 0;
+  // bf16 rows of up to 2048 elements in 16-byte chunks: one wave per row
+  if (dtype == DLI_BF16 && hidden % 8 == 0 && hidden <= 2048 && aligned16(x) &&
+      aligned16(weight) && aligned16(out)) {
+    const int64_t groups = (rows + 3) / 4;
+    const unsigned blocks = static_cast<unsigned>(groups < 65535 ? groups : 65535);
+    return launch(k_rms_norm_rows, {blocks}, {256}, 0, stream, x, weight, out, rows,
+                  static_cast<int>(hidden), eps);
+  }
   const unsigned blocks = static_cast<unsigned>(rows < 65535 ? rows : 65535);
   return launch(*k, {blocks}, {256}, 0, stream, x, weight, out, rows, hidden, eps);
 }

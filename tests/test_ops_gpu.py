@@ -54,7 +54,8 @@ def test_activations(dtype):
 
 
 @pytest.mark.parametrize("dtype", FLOATS)
-@pytest.mark.parametrize("rows,hidden", [(1, 896), (37, 896), (5, 4096), (3, 3000), (2, 4)])
+@pytest.mark.parametrize("rows,hidden", [(1, 896), (37, 896), (1029, 2048), (8192, 896), (5, 4096),
+                                         (3, 3000), (2, 4), (6, 8)])
 def test_rms_norm(dtype, rows, hidden):
     x, w = rand((rows, hidden), dtype, 4), rand((hidden,), dtype, 5)
     out = run_op("rms_norm", {"x": x, "weight": w}, attrs={"eps": 1e-6})["output"]
