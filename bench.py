@@ -384,15 +384,18 @@ def bench_prefill(args):
         "attention": 2 * 2 * B * Hq * D * (S * (S + 1) // 2), "o_proj": 2 * T * Hq * D * H,
         "gate_up": 2 * 2 * T * H * F, "down_proj": 2 * T * F * H}
     flops = sum(node_flops.values())
+    # the fused layer's one q|k|v GEMM (with RoPE and the head layout in its epilogue)
+    node_flops["qkv_rope_heads"] = sum(node_flops[f"{x}_proj"] for x in "qkv")
     w = {k: v for k, v in random_weights(cfg, seed=0, device="cuda").items()
          if k.startswith("model.layers.0.") or k.startswith("rotary")}
-    w = pack_fused_weights(replace(cfg, layers=1), w)  # + the interleaved gate/up weight
+    w = pack_fused_weights(replace(cfg, layers=1), w)  # + packed q|k|v and gate/up weights
     g = torch.Generator().manual_seed(1)
     h = torch.randn(B, S, H, generator=g).to(torch.bfloat16).cuda()
     engine = dli.Engine().load_plugin()
     engine.configure_kv_cache(block_size=64, max_seq_len=S)
-    # the fused layer (o_proj and down_proj with their residual adds, gate/up with SwiGLU in one
-    # GEMM); the CPU baseline runs the reference's node sequence (same values)
+    # the fused layer (q|k|v with RoPE and the head layout in one GEMM, o_proj and down_proj with
+    # their residual adds, gate/up with SwiGLU in one GEMM); the CPU baseline runs the reference's
+    # node sequence (same values up to rounding)
     graph = build_prefill_graph(cfg, B, S, layers=1, from_hidden=True, fused=True)
     ref_graph = build_prefill_graph(cfg, B, S, layers=1, from_hidden=True)
     inputs = {**w, "hidden_states": h}

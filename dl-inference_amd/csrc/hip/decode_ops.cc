@@ -47,6 +47,8 @@ DeviceKernel k_mfma_linres64("mfma_gemm", "mfma_linear_residual_bf16_t64");
 DeviceKernel k_mfma_linres128("mfma_gemm", "mfma_linear_residual_bf16_t128");
 DeviceKernel k_mfma_gu64("mfma_gemm", "mfma_gate_up_silu_bf16_t64");
 DeviceKernel k_mfma_gu128("mfma_gemm", "mfma_gate_up_silu_bf16_t128");
+DeviceKernel k_mfma_qkvh64("mfma_gemm", "mfma_qkv_heads_bf16_t64");
+DeviceKernel k_mfma_qkvh128("mfma_gemm", "mfma_qkv_heads_bf16_t128");
 
 // Tiled launch of those: 128 x 128 tiles once they alone give every CU a workgroup, else 64 x 64;
 // grid (column tiles, row tiles).
@@ -242,6 +244,38 @@ int dli_hip_gate_up_silu(const void* hidden, const void* norm_weight, const void
   if (int rc = tileGrid(ffn / 16, m, &grid, norm_weight != nullptr)) return rc;
   return launch(*k_gate_up.pick(m), {grid}, {kNormThreads}, 0, stream, hidden, norm_weight, eps,
                 w_gate_up, out, static_cast<int>(m), ffn, static_cast<int>(hidden_size));
+}
+
+int dli_hip_qkv_rope_heads(const void* x, const void* w_qkv, const void* b_qkv, const float* cos,
+                           const float* sin, int64_t max_pos, void* q_out, void* k_out,
+                           void* v_out, int64_t batch, int64_t seq, int64_t hidden_size,
+                           int64_t q_heads, int64_t kv_heads, int64_t head_dim, int64_t start_pos,
+                           void* stream) {
+  const char* op = "qkv_rope_heads";
+  if (batch < 0 || seq < 0) return bad(op, "negative size");
+  const int64_t m = batch * seq;
+  if (m == 0) return 0;
+  if (hidden_size <= 0 || hidden_size % 8 != 0)
+    return bad(op, "hidden_size must be a positive multiple of 8");
+  if (head_dim <= 0 || head_dim % 8 != 0 || head_dim > 1024)
+    return bad(op, "head_dim must be a multiple of 8 in [8, 1024]");
+  if (q_heads <= 0 || kv_heads <= 0 || q_heads > 4096 || kv_heads > 4096)
+    return bad(op, "q_heads and kv_heads must be in [1, 4096]");
+  if (max_pos < 0) return bad(op, "negative max_pos");
+  if (x == nullptr || w_qkv == nullptr || b_qkv == nullptr || cos == nullptr || sin == nullptr ||
+      q_out == nullptr || k_out == nullptr || v_out == nullptr)
+    return bad(op, "NULL pointer");
+  if (!aligned16(x) || !aligned16(w_qkv) || !aligned16(b_qkv) || !aligned16(q_out) ||
+      !aligned16(k_out) || !aligned16(v_out))
+    return bad(op, "x, w_qkv, b_qkv and the outputs must be 16-byte aligned");
+  const int64_t n = (q_heads + 2 * kv_heads) * head_dim;
+  bool big = false;
+  unsigned grid[2];
+  if (!tiledGrid(m, n, &big, grid)) return bad(op, "too many rows");
+  return launch(big ? k_mfma_qkvh128 : k_mfma_qkvh64, {grid[0], grid[1]}, {256}, 0, stream, x,
+                w_qkv, b_qkv, cos, sin, max_pos, q_out, k_out, v_out, m, hidden_size, seq,
+                start_pos, static_cast<int>(q_heads), static_cast<int>(kv_heads),
+                static_cast<int>(head_dim));
 }
 
 size_t dli_hip_lm_head_argmax_workspace(int64_t m, int64_t vocab) {

@@ -508,9 +508,9 @@ __device__ __forceinline__ void gemmBf16(const uint16_t* a, const uint16_t* b, i
       float v[8];
 #pragma unroll
       for (int k = 0; k < 8; ++k) v[k] = ct[row * CP + c8 + k];
-      if (vec && gcol + 8 <= Cn) {
+      if (Epi::kVectorOnly || (vec && gcol + 8 <= Cn)) {
         epi.vec8(grow, gcol, v);
-      } else {
+      } else if constexpr (!Epi::kVectorOnly) {
 #pragma unroll
         for (int k = 0; k < 8; ++k)
           if (gcol + k < Cn) epi(grow, gcol + k, v[k]);
@@ -559,6 +559,7 @@ struct RowMajorOut {
 // inlined copies, one per output type, took the kernel past 256 registers)
 struct RowMajorOutBf16OrF32 {
   static constexpr bool kPairs = false;
+  static constexpr bool kVectorOnly = false;
   void* out;
   const bf16* bias;
   int64_t ldo;
@@ -600,6 +601,7 @@ struct RowMajorOutBf16OrF32 {
 // added to the residual stream, rounded where the unfused graph rounds (linear, then add).
 struct ResidualOut {
   static constexpr bool kPairs = false;
+  static constexpr bool kVectorOnly = false;
   bf16* out;
   const bf16* residual;
   const bf16* bias;
@@ -633,6 +635,7 @@ struct ResidualOut {
 // mul nodes.
 struct SwiGluOut {
   static constexpr bool kPairs = true;
+  static constexpr bool kVectorOnly = false;
   bf16* out;
   int64_t ffn;
   __device__ __forceinline__ void pair(int64_t row, int64_t col, float gate, float up) const {
@@ -654,6 +657,63 @@ struct SwiGluOut {
       o[k] = sg * u;
     }
     *gp(reinterpret_cast<U128*>(out + row * ffn + (col / 32) * 16 + col % 16)) = packBf16x8(o);
+  }
+};
+
+// The q|k|v projection of a prefill prompt straight into attention's layout: C row = token
+// (b, s) of [B, S], C column = (q | k | v, head, d) of the packed [q; k; v] weight. Each value is
+// rounded as the linear node rounds it (bf16(v + bias)); q and k then get the interleaved RoPE of
+// position start_pos + s, rounded as the rotary node rounds it (pairs (2p, 2p + 1), positions
+// outside the table copied unchanged); results go to q [B, Hq, S, D], k and v [B, Hkv, S, D]
+// (rotary/kernel.py:6-35, and the reshape + transpose nodes a prompt needs). Vector form only:
+// the host requires D % 8 == 0 and 16-byte aligned pointers, so every 8-column run lies in one
+// head.
+struct QkvHeadsOut {
+  static constexpr bool kPairs = false;
+  static constexpr bool kVectorOnly = true;
+  bf16* q;
+  bf16* k;
+  bf16* v;
+  const bf16* bias;
+  const float* cosT;
+  const float* sinT;
+  int64_t seq, max_pos, start_pos;
+  int q_heads, kv_heads, head_dim;
+  __device__ __forceinline__ bool vectorOk() const { return true; }
+  __device__ __forceinline__ void operator()(int64_t, int64_t, float) const {}
+  __device__ __forceinline__ void vec8(int64_t row, int64_t col, float (&x)[8]) const {
+    FP_EXACT;
+    float b8[8];
+    unpackBf16x8(gload16(bias + col), b8);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = Num<bf16>::round(x[e] + b8[e]);
+    const int64_t qw = static_cast<int64_t>(q_heads) * head_dim;
+    const int64_t kw = static_cast<int64_t>(kv_heads) * head_dim;
+    bf16* base;
+    int64_t c, heads;
+    if (col < qw) {
+      base = q, c = col, heads = q_heads;
+    } else if (col < qw + kw) {
+      base = k, c = col - qw, heads = kv_heads;
+    } else {
+      base = v, c = col - qw - kw, heads = kv_heads;
+    }
+    const int64_t h = c / head_dim, d = c % head_dim;
+    const int64_t b = row / seq, s = row % seq;
+    const int64_t pos = start_pos + s;
+    if (base != v && pos >= 0 && pos < max_pos) {
+      const int64_t half = head_dim / 2;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int64_t p = d / 2 + j;
+        const float cs = gp(cosT)[pos * half + p], sn = gp(sinT)[pos * half + p];
+        const float x0 = x[2 * j], x1 = x[2 * j + 1];
+        x[2 * j] = x0 * cs - x1 * sn;
+        x[2 * j + 1] = x0 * sn + x1 * cs;
+      }
+    }
+    *gp(reinterpret_cast<U128*>(base + ((b * heads + h) * seq + s) * head_dim + d)) =
+        packBf16x8(x);
   }
 };
 
@@ -797,3 +857,23 @@ DK_MFMA_BF16(128, 128)
 
 DK_MFMA_BF16_FUSED(64, 64)
 DK_MFMA_BF16_FUSED(128, 128)
+
+// q|k|v projection + RoPE + head layout of a prefill prompt (QkvHeadsOut): x [B * S, K],
+// w_qkv [(Hq + 2 Hkv) D, K], b_qkv [(Hq + 2 Hkv) D].
+#define DK_MFMA_QKV_HEADS(BM, BN)                                                               \
+  extern "C" __global__ void __launch_bounds__(kGemmThreads) DK_BF16_OCCUPANCY                 \
+      mfma_qkv_heads_bf16_t##BM(const uint16_t* x, const uint16_t* w_qkv, const uint16_t* b_qkv, \
+                                const float* cos, const float* sin, int64_t max_pos,           \
+                                uint16_t* q, uint16_t* k, uint16_t* v, int64_t M, int64_t K,   \
+                                int64_t seq, int64_t start_pos, int q_heads, int kv_heads,     \
+                                int head_dim) {                                                \
+    const int64_t n = static_cast<int64_t>(q_heads + 2 * kv_heads) * head_dim;                 \
+    gemmBf16<BM, BN>(x, w_qkv, M, n, K,                                                        \
+                     QkvHeadsOut{reinterpret_cast<bf16*>(q), reinterpret_cast<bf16*>(k),       \
+                                 reinterpret_cast<bf16*>(v),                                   \
+                                 reinterpret_cast<const bf16*>(b_qkv), cos, sin, seq, max_pos, \
+                                 start_pos, q_heads, kv_heads, head_dim});                     \
+  }
+
+DK_MFMA_QKV_HEADS(64, 64)
+DK_MFMA_QKV_HEADS(128, 128)

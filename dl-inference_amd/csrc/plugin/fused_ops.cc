@@ -4,6 +4,8 @@
 //
 //   qkv_rope_append        (input_layernorm,) q/k/v_proj, reshapes, rotary_embedding, KV
 //                          append
+//   qkv_rope_heads         q/k/v_proj, reshapes, [B,S,H,D] -> [B,H,S,D] transposes and
+//                          rotary_embedding of a prompt (prefill)
 //   paged_attention        attention over the already appended paged KV cache (decode)
 //   linear_residual        o_proj + attention_residual, down_proj + mlp_residual
 //   linear_residual_norm   the same plus the RMSNorm that follows the residual update
@@ -68,6 +70,42 @@ class QkvRopeAppendOp final : public Operator {
               ptr(*out[0]), ptr(e.key_pool), ptr(e.value_pool),
               static_cast<const std::int32_t*>(ptr(e.block_table)), e.block_size, e.max_blocks, m,
               hidden, hq, hkv, d, eps, ctx.stream),
+          type());
+  }
+};
+
+// inputs: x [B, S, H] (normalized), w_qkv [N, H], b_qkv [N], cos, sin [max_pos, D / 2];
+// attrs q_heads, kv_heads, head_dim, start_pos (0); outputs q [B, Hq, S, D], k and v
+// [B, Hkv, S, D] with RoPE on q and k at positions start_pos + s.
+class QkvRopeHeadsOp final : public Operator {
+ public:
+  std::string type() const override { return "qkv_rope_heads"; }
+  void compute(const std::vector<const Tensor*>& in, const std::vector<Tensor*>& out,
+               const Attributes& attrs, ExecutionContext& ctx) const override {
+    requireArity(in, out, 5, 5, 3, type());
+    requireCudaInputs(in, type());
+    const Tensor &x = *in[0], &w = *in[1], &b = *in[2], &cos = *in[3], &sin = *in[4];
+    for (const Tensor* t : {&x, &w, &b}) requireBf16(*t, type(), "activations/weights");
+    requireFloat(cos, type());
+    requireFloat(sin, type());
+    const auto hq = attrs.require<std::int64_t>("q_heads");
+    const auto hkv = attrs.require<std::int64_t>("kv_heads");
+    const auto d = attrs.require<std::int64_t>("head_dim");
+    const auto start = attrs.value_or<std::int64_t>("start_pos", 0);
+    if (x.rank() != 3) throw std::invalid_argument("qkv_rope_heads x must be [B, S, H]");
+    const std::int64_t B = x.dim(0), S = x.dim(1), hidden = x.dim(2);
+    const std::int64_t n = (hq + 2 * hkv) * d;
+    if (w.rank() != 2 || w.dim(0) != n || w.dim(1) != hidden || static_cast<std::int64_t>(b.numel()) != n)
+      throw std::invalid_argument("qkv_rope_heads weight shapes do not match the attributes");
+    if (cos.rank() != 2 || cos.dim(1) != d / 2 || cos.shape() != sin.shape())
+      throw std::invalid_argument("qkv_rope_heads cos/sin must be [max_pos, head_dim/2]");
+    *out[0] = Tensor::cuda(DType::BFloat16, {B, hq, S, d}, x.deviceId());
+    *out[1] = Tensor::cuda(DType::BFloat16, {B, hkv, S, d}, x.deviceId());
+    *out[2] = Tensor::cuda(DType::BFloat16, {B, hkv, S, d}, x.deviceId());
+    check(dli_hip_qkv_rope_heads(ptr(x), ptr(w), ptr(b), static_cast<const float*>(ptr(cos)),
+                                 static_cast<const float*>(ptr(sin)), cos.dim(0), ptr(*out[0]),
+                                 ptr(*out[1]), ptr(*out[2]), B, S, hidden, hq, hkv, d, start,
+                                 ctx.stream),
           type());
   }
 };
@@ -361,6 +399,7 @@ class ArgmaxOp final : public Operator {
 
 void registerFusedOps(OperatorRegistry* registry) {
   add<QkvRopeAppendOp>(registry);
+  add<QkvRopeHeadsOp>(registry);
   add<PagedAttentionOp>(registry);
   add<LinearResidualOp>(registry);
   add<LinearResidualNormOp>(registry);

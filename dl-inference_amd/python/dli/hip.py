@@ -91,6 +91,8 @@ _SIGNATURES = {
     "dli_hip_linear_residual_norm": [_c_void_p] * 7 + [_i64] * 3
     + [_float, _int, _c_void_p, _size, _c_void_p],
     "dli_hip_gate_up_silu": [_c_void_p] * 4 + [_i64] * 3 + [_float, _c_void_p],
+    "dli_hip_qkv_rope_heads": [_c_void_p] * 5 + [_i64] + [_c_void_p] * 3 + [_i64] * 7
+    + [_c_void_p],
     "dli_hip_lm_head_argmax_workspace": [_i64, _i64],
     "dli_hip_lm_head_argmax": [_c_void_p] * 3 + [_int, _c_void_p] + [_i64] * 3
     + [_c_void_p, _size, _c_void_p],

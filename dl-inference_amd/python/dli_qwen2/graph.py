@@ -235,7 +235,9 @@ def _prefill_layer_nodes(cfg: Qwen2Config, batch: int, seq: int, i: int, h: str,
                          fused: bool = False) -> str:
     """One decoder layer over [B, S, H] activations (the exporter's node sequence,
     python/dli_export/export.py:272-424, with the [B, S, H, D] <-> [B, H, S, D] transposes a
-    prompt of S tokens needs around rotary and attention). With fused, o_proj + residual and
+    prompt of S tokens needs around rotary and attention). With fused, q/k/v_proj, their
+    reshapes and transposes and rotary_embedding are one qkv_rope_heads node over the packed
+    self_attn.qkv_proj.{weight,bias}, o_proj + residual and
     down_proj + residual are linear_residual nodes and gate_proj, up_proj, act_fn and mul one
     gate_up_silu node over the interleaved mlp.gate_up_proj.weight (pack_fused_weights): the
     same values (each fused kernel rounds where the nodes it replaces round). Returns the layer's
@@ -244,18 +246,26 @@ def _prefill_layer_nodes(cfg: Qwen2Config, batch: int, seq: int, i: int, h: str,
     q_w = cfg.heads * cfg.head_dim
     _node(nodes, f"{p}.input_layernorm", "rms_norm", [h, f"{p}.input_layernorm.weight"],
           [f"{t}_input_norm"], {"eps": cfg.eps})
-    for proj in ("q", "k", "v"):
-        _node(nodes, f"{p}.self_attn.{proj}_proj", "linear",
-              [f"{t}_input_norm", f"{p}.self_attn.{proj}_proj.weight",
-               f"{p}.self_attn.{proj}_proj.bias"], [f"{t}_{proj}"])
-    for proj, heads in (("q", cfg.heads), ("k", cfg.kv_heads), ("v", cfg.kv_heads)):
-        _node(nodes, f"{p}.self_attn.{proj}_reshape", "reshape", [f"{t}_{proj}"],
-              [f"{t}_{proj}_bshd"], {"shape": [batch, seq, heads, cfg.head_dim]})
-        _node(nodes, f"{p}.self_attn.{proj}_transpose", "transpose", [f"{t}_{proj}_bshd"],
-              [f"{t}_{proj}_heads"], {"perm": [0, 2, 1, 3]})
-    _node(nodes, f"{p}.self_attn.rotary_embedding", "rotary_embedding",
-          [f"{t}_q_heads", f"{t}_k_heads", "rotary_cos", "rotary_sin"],
-          [f"{t}_q_rotary", f"{t}_k_rotary"], {"start_pos": 0})
+    if fused:
+        _node(nodes, f"{p}.self_attn.qkv_rope_heads", "qkv_rope_heads",
+              [f"{t}_input_norm", f"{p}.self_attn.qkv_proj.weight",
+               f"{p}.self_attn.qkv_proj.bias", "rotary_cos", "rotary_sin"],
+              [f"{t}_q_rotary", f"{t}_k_rotary", f"{t}_v_heads"],
+              {"q_heads": cfg.heads, "kv_heads": cfg.kv_heads, "head_dim": cfg.head_dim,
+               "start_pos": 0})
+    else:
+        for proj in ("q", "k", "v"):
+            _node(nodes, f"{p}.self_attn.{proj}_proj", "linear",
+                  [f"{t}_input_norm", f"{p}.self_attn.{proj}_proj.weight",
+                   f"{p}.self_attn.{proj}_proj.bias"], [f"{t}_{proj}"])
+        for proj, heads in (("q", cfg.heads), ("k", cfg.kv_heads), ("v", cfg.kv_heads)):
+            _node(nodes, f"{p}.self_attn.{proj}_reshape", "reshape", [f"{t}_{proj}"],
+                  [f"{t}_{proj}_bshd"], {"shape": [batch, seq, heads, cfg.head_dim]})
+            _node(nodes, f"{p}.self_attn.{proj}_transpose", "transpose", [f"{t}_{proj}_bshd"],
+                  [f"{t}_{proj}_heads"], {"perm": [0, 2, 1, 3]})
+        _node(nodes, f"{p}.self_attn.rotary_embedding", "rotary_embedding",
+              [f"{t}_q_heads", f"{t}_k_heads", "rotary_cos", "rotary_sin"],
+              [f"{t}_q_rotary", f"{t}_k_rotary"], {"start_pos": 0})
     _node(nodes, f"{p}.self_attn.attention", "attention",
           [f"{t}_q_rotary", f"{t}_k_rotary", f"{t}_v_heads"], [f"{t}_attention"],
           {"causal": True, "kv_cache": f"layer_{i}"})

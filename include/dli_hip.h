@@ -321,6 +321,21 @@ int dli_hip_gate_up_silu(const void* hidden, const void* norm_weight, const void
                          void* out, int64_t m, int64_t ffn, int64_t hidden_size, float eps,
                          void* stream);
 
+/* Prefill form of the attention inputs: [q | k | v] = x W_qkv^T + b over the B * S tokens of a
+ * prompt (x [batch, seq, hidden_size] bf16, normalized), each value rounded to bf16 as the
+ * linear node rounds it; interleaved RoPE on q and k at position start_pos + s (cos/sin fp32
+ * [max_pos, head_dim / 2]; positions outside the table unchanged), rounded as the rotary node
+ * rounds it; q_out [batch, q_heads, seq, head_dim], k_out and v_out [batch, kv_heads, seq,
+ * head_dim]. One tiled MFMA GEMM with the RoPE and the head layout in its epilogue. Replaces
+ * q/k/v_proj, the three reshapes, the three [B,S,H,D] -> [B,H,S,D] transposes and
+ * rotary_embedding of a prompt layer (export.py:280-349; rotary/kernel.py:6-35). head_dim % 8
+ * == 0, hidden_size % 8 == 0, pointers (except cos/sin) 16-byte aligned. */
+int dli_hip_qkv_rope_heads(const void* x, const void* w_qkv, const void* b_qkv, const float* cos,
+                           const float* sin, int64_t max_pos, void* q_out, void* k_out,
+                           void* v_out, int64_t batch, int64_t seq, int64_t hidden_size,
+                           int64_t q_heads, int64_t kv_heads, int64_t head_dim, int64_t start_pos,
+                           void* stream);
+
 /* logits = xn W^T (fp32 accumulation) -> ids[m] = argmax (first maximum); hidden <= 1024.
  * logits may be NULL (only ids) or float32 / bfloat16 [m, vocab]. Replaces lm_head
  * (export.py:426-443) plus the greedy token choice. */

@@ -1,4 +1,4 @@
-"""Per-operator parity of the fused decode operators (plugin ops qkv_rope_append,
+"""Per-operator parity of the fused operators (plugin ops qkv_rope_append, qkv_rope_heads,
 linear_residual, linear_residual_norm, gate_up_silu, lm_head_argmax) against the CPU oracle.
 
 Each fused op stands for a run of nodes of the reference's decoder graph
@@ -112,6 +112,33 @@ def test_linear_residual_norm(B, N, K, splits, bias):
     h = _residual_oracle(x, w, res, inputs.get("b"))
     assert_close(out["h"], h, "bfloat16")
     assert_close(out["xn"], R(ops.rms_norm(h, to_np(nw), 1e-6)), "bfloat16")
+
+
+@pytest.mark.parametrize("B,S,H,Hq,Hkv,D,start,max_pos", [
+    (1, 1, 64, 2, 1, 64, 0, 16),
+    (3, 37, 256, 4, 2, 64, 5, 30),       # ragged; positions 30.. are past the table (unrotated)
+    (2, 100, 896, 14, 2, 64, 0, 128),    # Qwen2-0.5B heads, 64-row tiles
+    (1, 300, 128, 2, 1, 128, 7, 512),    # head_dim 128
+    (2, 2048, 896, 14, 2, 64, 0, 2048),  # 128-row tiles (288 of them)
+])
+def test_qkv_rope_heads(B, S, H, Hq, Hkv, D, start, max_pos):
+    """Prefill q|k|v: linear (bf16 rounding), [B,S,H,D] -> [B,H,S,D], RoPE on q and k."""
+    n = (Hq + 2 * Hkv) * D
+    x, w, b = rand((B, S, H), 60), rand((n, H), 61, 0.05), rand((n,), 62, 0.1)
+    cos, sin = rope_tables(max_pos, D)
+    out = run_op("qkv_rope_heads", {"x": x, "w": w, "b": b, "cos": cos, "sin": sin},
+                 outputs=("q", "k", "v"),
+                 attrs={"q_heads": Hq, "kv_heads": Hkv, "head_dim": D, "start_pos": start})
+    # the linear in float64 through torch on the CPU (the oracle's einsum is slow at 4096 rows)
+    lin = R((x.cpu().double() @ w.cpu().double().T + b.cpu().double()).numpy())
+    heads = lambda a, h: a.reshape(B, S, h, D).transpose(0, 2, 1, 3)
+    qr, kr = lin[..., :Hq * D], lin[..., Hq * D:(Hq + Hkv) * D]
+    vr = lin[..., (Hq + Hkv) * D:]
+    cn, sn = to_np(cos), to_np(sin)
+    assert tuple(out["q"].shape) == (B, Hq, S, D) and tuple(out["v"].shape) == (B, Hkv, S, D)
+    assert_close(out["q"], R(ops.rotary(heads(qr, Hq), cn, sn, start_pos=start)), "bfloat16")
+    assert_close(out["k"], R(ops.rotary(heads(kr, Hkv), cn, sn, start_pos=start)), "bfloat16")
+    assert_close(out["v"], heads(vr, Hkv), "bfloat16")
 
 
 @pytest.mark.parametrize("B,N,K,splits,bias", CASES + [(16, 4096, 1024, 1, True),

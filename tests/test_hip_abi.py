@@ -101,6 +101,18 @@ def test_fused_decode_entry_points_reject_invalid_arguments():
     assert lib.dli_hip_linear_residual(None, None, None, None, None, 100, 64, 12, 1, None, 0,
                                        None) == -1
     assert b"multiple of 8" in lib.dli_hip_last_error()
+    # prefill q|k|v + RoPE + head layout: shape checks before any pointer is used
+    assert lib.dli_hip_qkv_rope_heads(None, None, None, None, None, 16, None, None, None, 0, 5,
+                                      64, 2, 1, 64, 0, None) == 0  # no rows: nothing to do
+    assert lib.dli_hip_qkv_rope_heads(None, None, None, None, None, 16, None, None, None, 1, 5,
+                                      64, 2, 1, 60, 0, None) == -1
+    assert b"head_dim must be a multiple of 8" in lib.dli_hip_last_error()
+    assert lib.dli_hip_qkv_rope_heads(None, None, None, None, None, 16, None, None, None, 1, 5,
+                                      60, 2, 1, 64, 0, None) == -1
+    assert b"hidden_size must be a positive multiple of 8" in lib.dli_hip_last_error()
+    assert lib.dli_hip_qkv_rope_heads(None, None, None, None, None, 16, None, None, None, 1, 5,
+                                      64, 2, 1, 64, 0, None) == -1
+    assert b"NULL pointer" in lib.dli_hip_last_error()
     assert lib.dli_hip_qkv_rope_append(None, None, None, None, None, None, 8, None, hip.I64, None,
                                        None, None, None, 64, 1, 2, 64, 2, 1, 16, 1e-6, None) == -1
     assert b"positions" in lib.dli_hip_last_error()
