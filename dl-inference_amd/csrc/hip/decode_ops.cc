@@ -53,7 +53,10 @@ DeviceKernel k_mfma_qkvh128("mfma_gemm", "mfma_qkv_heads_bf16_t128");
 // Tiled launch of those: 128 x 128 tiles once they alone give every CU a workgroup, else 64 x 64;
 // grid (column tiles, row tiles).
 bool tiledGrid(int64_t rows, int64_t cols, bool* big, unsigned (&grid)[2]) {
-  *big = ((rows + 127) / 128) * ((cols + 127) / 128) >= 256;
+  // 128 x 128 tiles once there are enough of them to fill most of the 256 CUs (measured at
+  // 896 columns: 2048 rows / 112 tiles ran faster in 64 x 64 tiles, 4096 rows / 224 tiles in
+  // 128 x 128 tiles)
+  *big = ((rows + 127) / 128) * ((cols + 127) / 128) >= 168;
   const int64_t tile = *big ? 128 : 64;
   const int64_t gx = (cols + tile - 1) / tile, gy = (rows + tile - 1) / tile;
   if (gy > 65535 || gx > (int64_t{1} << 31)) return false;
@@ -265,10 +268,12 @@ int dli_hip_qkv_rope_heads(const void* x, const void* w_qkv, const void* b_qkv, 
   if (x == nullptr || w_qkv == nullptr || b_qkv == nullptr || cos == nullptr || sin == nullptr ||
       q_out == nullptr || k_out == nullptr || v_out == nullptr)
     return bad(op, "NULL pointer");
-  if (!aligned16(x) || !aligned16(w_qkv) || !aligned16(b_qkv) || !aligned16(q_out) ||
-      !aligned16(k_out) || !aligned16(v_out))
-    return bad(op, "x, w_qkv, b_qkv and the outputs must be 16-byte aligned");
+  if (!aligned16(x) || !aligned16(w_qkv) || !aligned16(b_qkv) || !aligned16(cos) ||
+      !aligned16(sin) || !aligned16(q_out) || !aligned16(k_out) || !aligned16(v_out))
+    return bad(op, "x, w_qkv, b_qkv, cos, sin and the outputs must be 16-byte aligned");
   const int64_t n = (q_heads + 2 * kv_heads) * head_dim;
+  if (m >= (int64_t{1} << 31) || n >= (int64_t{1} << 31))
+    return bad(op, "batch * seq and the q|k|v width must be below 2^31");
   bool big = false;
   unsigned grid[2];
   if (!tiledGrid(m, n, &big, grid)) return bad(op, "too many rows");

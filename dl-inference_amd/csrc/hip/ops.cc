@@ -409,9 +409,14 @@ int dli_hip_linear_act(int dtype, int out_dtype, const void* x, const void* w, c
     // bf16 weight streaming for decode-sized m: MFMA skinny kernel.
     DeviceKernel* sk = m <= 16 ? &k_skinny1 : (m <= 32 ? &k_skinny2 : &k_skinny4);
     rc = launch(*sk, {blocksFor(n, 32)}, {256}, 0, stream, x, w, bias, out, m, n, k, out_f32);
-  } else if (dtype == DLI_BF16 && k % 8 == 0 && aligned16(x) && aligned16(w) && grid_ok) {
-    return launch(big ? k_mfma_bf16_128 : k_mfma_bf16_64, grid, {256}, 0, stream, x, w, bias, out,
-                  m, n, k, out_f32, relu);
+  } else if (dtype == DLI_BF16 && k % 8 == 0 && aligned16(x) && aligned16(w) &&
+             (m + 63) / 64 <= kMaxGridY) {
+    // the bf16 GEMM's own tile rule (its 128 x 128 tiles pay off from about 168 of them)
+    const bool b128 = ((m + 127) / 128) * ((n + 127) / 128) >= 168;
+    const int64_t bt = b128 ? 128 : 64;
+    return launch(b128 ? k_mfma_bf16_128 : k_mfma_bf16_64,
+                  {static_cast<unsigned>((n + bt - 1) / bt), static_cast<unsigned>((m + bt - 1) / bt)},
+                  {256}, 0, stream, x, w, bias, out, m, n, k, out_f32, relu);
   } else {
     DeviceKernel* kt = k_gemm.pick(dtype);
     if (kt == nullptr) return badDtype("linear", dtype);

@@ -497,23 +497,41 @@ __device__ __forceinline__ void gemmBf16(const uint16_t* a, const uint16_t* b, i
       }
     }
   } else {
-    constexpr int kRuns = BM * BN / 8;
-    static_assert(kRuns % kGemmThreads == 0, "runs");
+    // thread t's runs: rows t / (BN / 8) + q * (256 / (BN / 8)), all at column run c8. The
+    // loads of every run go out before any result is stored: the compiler must assume a store
+    // may alias a later run's input, so a load-compute-store loop per run waited for each load.
+    constexpr int kRuns = BM * BN / 8, kPer = kRuns / kGemmThreads;
+    static_assert(kRuns % kGemmThreads == 0 && kGemmThreads % (BN / 8) == 0, "runs");
+    const int c8 = (t % (BN / 8)) * 8, row0 = t / (BN / 8);
+    constexpr int kRowStep = kGemmThreads / (BN / 8);
+    const int64_t gcol = c0 + c8;
+    if (Epi::kVectorOnly || (vec && gcol + 8 <= Cn)) {
+      const auto cd = epi.column(gcol);
+      typename Epi::Run rd[kPer];
 #pragma unroll
-    for (int q = 0; q < kRuns / kGemmThreads; ++q) {
-      const int e = t + q * kGemmThreads;
-      const int row = e / (BN / 8), c8 = (e % (BN / 8)) * 8;
-      const int64_t grow = r0 + row, gcol = c0 + c8;
-      if (grow >= R) continue;
-      float v[8];
+      for (int q = 0; q < kPer; ++q) {
+        const int64_t grow = r0 + row0 + q * kRowStep;
+        if (grow < R) rd[q] = epi.fetch(grow, gcol);
+      }
 #pragma unroll
-      for (int k = 0; k < 8; ++k) v[k] = ct[row * CP + c8 + k];
-      if (Epi::kVectorOnly || (vec && gcol + 8 <= Cn)) {
-        epi.vec8(grow, gcol, v);
-      } else if constexpr (!Epi::kVectorOnly) {
+      for (int q = 0; q < kPer; ++q) {
+        const int row = row0 + q * kRowStep;
+        const int64_t grow = r0 + row;
+        if (grow >= R) continue;
+        float v[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[k] = ct[row * CP + c8 + k];
+        epi.vec8(grow, gcol, v, cd, rd[q]);
+      }
+    } else if constexpr (!Epi::kVectorOnly) {
+#pragma unroll
+      for (int q = 0; q < kPer; ++q) {
+        const int row = row0 + q * kRowStep;
+        const int64_t grow = r0 + row;
+        if (grow >= R) continue;
 #pragma unroll
         for (int k = 0; k < 8; ++k)
-          if (gcol + k < Cn) epi(grow, gcol + k, v[k]);
+          if (gcol + k < Cn) epi(grow, gcol + k, ct[row * CP + c8 + k]);
       }
     }
   }
@@ -575,10 +593,16 @@ struct RowMajorOutBf16OrF32 {
   __device__ __forceinline__ bool vectorOk() const {
     return ldo % 8 == 0 && aligned16(out) && aligned16(bias);
   }
-  __device__ __forceinline__ void vec8(int64_t row, int64_t col, float (&v)[8]) const {
+  struct Run {};
+  __device__ __forceinline__ U128 column(int64_t col) const {
+    return bias != nullptr ? gload16(bias + col) : zero16();
+  }
+  __device__ __forceinline__ Run fetch(int64_t, int64_t) const { return {}; }
+  __device__ __forceinline__ void vec8(int64_t row, int64_t col, float (&v)[8], const U128& bw,
+                                       const Run&) const {
     if (bias != nullptr) {
       float b[8];
-      unpackBf16x8(gload16(bias + col), b);
+      unpackBf16x8(bw, b);
 #pragma unroll
       for (int k = 0; k < 8; ++k) v[k] += b[k];
     }
@@ -614,15 +638,23 @@ struct ResidualOut {
   __device__ __forceinline__ bool vectorOk() const {
     return ldo % 8 == 0 && aligned16(out) && aligned16(residual) && aligned16(bias);
   }
-  __device__ __forceinline__ void vec8(int64_t row, int64_t col, float (&v)[8]) const {
+  using Run = U128;  // the residual run
+  __device__ __forceinline__ U128 column(int64_t col) const {
+    return bias != nullptr ? gload16(bias + col) : zero16();
+  }
+  __device__ __forceinline__ Run fetch(int64_t row, int64_t col) const {
+    return gload16(residual + row * ldo + col);
+  }
+  __device__ __forceinline__ void vec8(int64_t row, int64_t col, float (&v)[8], const U128& bw,
+                                       const Run& rw) const {
     if (bias != nullptr) {
       float b[8];
-      unpackBf16x8(gload16(bias + col), b);
+      unpackBf16x8(bw, b);
 #pragma unroll
       for (int k = 0; k < 8; ++k) v[k] += b[k];
     }
     float r[8];
-    unpackBf16x8(gload16(residual + row * ldo + col), r);
+    unpackBf16x8(rw, r);
 #pragma unroll
     for (int k = 0; k < 8; ++k) v[k] = r[k] + Num<bf16>::round(v[k]);
     *gp(reinterpret_cast<U128*>(out + row * ldo + col)) = packBf16x8(v);
@@ -666,8 +698,8 @@ struct SwiGluOut {
 // position start_pos + s, rounded as the rotary node rounds it (pairs (2p, 2p + 1), positions
 // outside the table copied unchanged); results go to q [B, Hq, S, D], k and v [B, Hkv, S, D]
 // (rotary/kernel.py:6-35, and the reshape + transpose nodes a prompt needs). Vector form only:
-// the host requires D % 8 == 0 and 16-byte aligned pointers, so every 8-column run lies in one
-// head.
+// the host requires D % 8 == 0 and 16-byte aligned pointers (cos/sin too), so every 8-column
+// run lies in one head and reads 16 bytes of each table row.
 struct QkvHeadsOut {
   static constexpr bool kPairs = false;
   static constexpr bool kVectorOnly = true;
@@ -681,39 +713,73 @@ struct QkvHeadsOut {
   int q_heads, kv_heads, head_dim;
   __device__ __forceinline__ bool vectorOk() const { return true; }
   __device__ __forceinline__ void operator()(int64_t, int64_t, float) const {}
-  __device__ __forceinline__ void vec8(int64_t row, int64_t col, float (&x)[8]) const {
+  // column-invariant part of a run: the bias and where the run goes
+  struct Col {
+    U128 bias;
+    bf16* base;
+    uint32_t heads, h, d;
+  };
+  struct Run {  // the table rows of the run's position
+    U128 cs, sn;
+  };
+  __device__ __forceinline__ Col column(int64_t col) const {
+    // 32-bit index arithmetic (the host bounds rows, columns and seq below 2^31)
+    const uint32_t qw = static_cast<uint32_t>(q_heads * head_dim);
+    const uint32_t kw = static_cast<uint32_t>(kv_heads * head_dim);
+    const uint32_t cu = static_cast<uint32_t>(col);
+    Col c;
+    c.bias = gload16(bias + col);
+    uint32_t rel;
+    if (cu < qw) {
+      c.base = q, rel = cu, c.heads = q_heads;
+    } else if (cu < qw + kw) {
+      c.base = k, rel = cu - qw, c.heads = kv_heads;
+    } else {
+      c.base = v, rel = cu - qw - kw, c.heads = kv_heads;
+    }
+    c.h = rel / static_cast<uint32_t>(head_dim);
+    c.d = rel - c.h * static_cast<uint32_t>(head_dim);
+    return c;
+  }
+  __device__ __forceinline__ int64_t position(int64_t row) const {
+    return start_pos + static_cast<uint32_t>(row) % static_cast<uint32_t>(seq);
+  }
+  __device__ __forceinline__ Run fetch(int64_t row, int64_t col) const {
+    // pairs d / 2 .. d / 2 + 3: 16 bytes of each table row (head_dim / 2 % 4 == 0); col is
+    // recomputed into the head offset the way column() does
+    const uint32_t hd = static_cast<uint32_t>(head_dim);
+    const uint32_t qkw = static_cast<uint32_t>((q_heads + kv_heads) * head_dim);
+    const int64_t pos = position(row);
+    Run r{zero16(), zero16()};
+    if (static_cast<uint32_t>(col) < qkw && pos >= 0 && pos < max_pos) {
+      const int64_t at = pos * (head_dim / 2) + (static_cast<uint32_t>(col) % hd) / 2;
+      r.cs = gload16(cosT + at);
+      r.sn = gload16(sinT + at);
+    }
+    return r;
+  }
+  __device__ __forceinline__ void vec8(int64_t row, int64_t, float (&x)[8], const Col& c,
+                                       const Run& r) const {
     FP_EXACT;
     float b8[8];
-    unpackBf16x8(gload16(bias + col), b8);
+    unpackBf16x8(c.bias, b8);
 #pragma unroll
     for (int e = 0; e < 8; ++e) x[e] = Num<bf16>::round(x[e] + b8[e]);
-    const int64_t qw = static_cast<int64_t>(q_heads) * head_dim;
-    const int64_t kw = static_cast<int64_t>(kv_heads) * head_dim;
-    bf16* base;
-    int64_t c, heads;
-    if (col < qw) {
-      base = q, c = col, heads = q_heads;
-    } else if (col < qw + kw) {
-      base = k, c = col - qw, heads = kv_heads;
-    } else {
-      base = v, c = col - qw - kw, heads = kv_heads;
-    }
-    const int64_t h = c / head_dim, d = c % head_dim;
-    const int64_t b = row / seq, s = row % seq;
+    const uint32_t ru = static_cast<uint32_t>(row), sq = static_cast<uint32_t>(seq);
+    const uint32_t b = ru / sq, s = ru - b * sq;
     const int64_t pos = start_pos + s;
-    if (base != v && pos >= 0 && pos < max_pos) {
-      const int64_t half = head_dim / 2;
+    if (c.base != v && pos >= 0 && pos < max_pos) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int64_t p = d / 2 + j;
-        const float cs = gp(cosT)[pos * half + p], sn = gp(sinT)[pos * half + p];
+        const float cs = __uint_as_float(r.cs[j]), sn = __uint_as_float(r.sn[j]);
         const float x0 = x[2 * j], x1 = x[2 * j + 1];
         x[2 * j] = x0 * cs - x1 * sn;
         x[2 * j + 1] = x0 * sn + x1 * cs;
       }
     }
-    *gp(reinterpret_cast<U128*>(base + ((b * heads + h) * seq + s) * head_dim + d)) =
-        packBf16x8(x);
+    const uint64_t off =
+        (static_cast<uint64_t>(b * c.heads + c.h) * sq + s) * static_cast<uint32_t>(head_dim) + c.d;
+    *gp(reinterpret_cast<U128*>(c.base + off)) = packBf16x8(x);
   }
 };
 
