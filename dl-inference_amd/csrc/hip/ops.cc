@@ -62,6 +62,7 @@ FloatKernels k_rotary("elementwise", "rotary");
 FloatKernels k_argmax("elementwise", "argmax");
 FloatKernels k_rms_norm("norm", "rms_norm");
 DeviceKernel k_rms_norm_rows("norm", "rms_norm_rows_bf16_k");
+DeviceKernel k_kv_append_tiles("attention", "kv_append_tiles_bf16_k");
 FloatKernels k_gemm("gemm", "gemm_tiled");
 DeviceKernel k_skinny1("gemm", "skinny_linear_m1");
 DeviceKernel k_skinny2("gemm", "skinny_linear_m2");
@@ -468,9 +469,10 @@ int dli_hip_rotary(int dtype, const void* q, const void* k, const float* cos_tab
                 pos64);
 }
 
-int dli_hip_attention(int dtype, const void* q, const void* k, const void* v, void* out,
-                      int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t seq_q,
-                      int64_t seq_k, int64_t head_dim, int causal, float scale, void* stream) {
+// attention with out as [B, Hq, Sq, D] (out_bshd 0) or [B, Sq, Hq, D] (1, flash path only)
+static int attentionImpl(int dtype, const void* q, const void* k, const void* v, void* out,
+                  int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t seq_q, int64_t seq_k,
+                  int64_t head_dim, int causal, float scale, int out_bshd, void* stream) {
   DeviceKernel* ka = k_attention.pick(dtype);
   if (ka == nullptr) return badDtype("attention", dtype);
   if (head_dim <= 0 || head_dim > 256) return badArg("attention", "head_dim must be in [1, 256]");
@@ -492,11 +494,29 @@ int dli_hip_attention(int dtype, const void* q, const void* k, const void* v, vo
                   {static_cast<unsigned>((seq_q + tile_q - 1) / tile_q),
                    static_cast<unsigned>(batch * q_heads)},
                   {256}, 0, stream, q, k, v, out, q_heads, kv_heads, seq_q, seq_k, causal,
-                  scale * log2e);
+                  scale * log2e, out_bshd);
   }
+  if (out_bshd)
+    return badArg("attention", "a [B, S, H, D] output needs bf16, head_dim 64, seq_k > 0 and "
+                               "16-byte aligned tensors (the flash kernel)");
   if (rows > 0x7fffffff) return badArg("attention", "too many query rows");
   return launch(*ka, {static_cast<unsigned>(rows)}, {64}, 0, stream, q, k, v, out, batch, q_heads,
                 kv_heads, seq_q, seq_k, head_dim, causal, scale);
+}
+
+int dli_hip_attention(int dtype, const void* q, const void* k, const void* v, void* out,
+                      int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t seq_q,
+                      int64_t seq_k, int64_t head_dim, int causal, float scale, void* stream) {
+  return attentionImpl(dtype, q, k, v, out, batch, q_heads, kv_heads, seq_q, seq_k, head_dim,
+                       causal, scale, 0, stream);
+}
+
+int dli_hip_attention_bshd(int dtype, const void* q, const void* k, const void* v, void* out,
+                           int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t seq_q,
+                           int64_t seq_k, int64_t head_dim, int causal, float scale,
+                           void* stream) {
+  return attentionImpl(dtype, q, k, v, out, batch, q_heads, kv_heads, seq_q, seq_k, head_dim,
+                       causal, scale, 1, stream);
 }
 
 int dli_hip_kv_append(int dtype, const void* key, const void* value, void* key_pool,
@@ -512,6 +532,16 @@ int dli_hip_kv_append(int dtype, const void* key, const void* value, void* key_p
   const int64_t total = batch * heads * seq * head_dim;
   if (total == 0) return 0;
   const int pos64 = positions_dtype == DLI_I64 ? 1 : 0;
+  // bf16 with 16-byte rows: 64 tokens of one head per workgroup, values transposed in LDS
+  if (dtype == DLI_BF16 && head_dim % 8 == 0 && head_dim <= 256 && batch * heads <= 65535 &&
+      aligned16(key) && aligned16(value) && aligned16(key_pool)) {
+    const int64_t chunks = (seq + 63) / 64;
+    if (chunks <= 0x7fffffff)
+      return launch(k_kv_append_tiles, {static_cast<unsigned>(chunks),
+                                        static_cast<unsigned>(batch * heads)},
+                    {256}, 0, stream, key, value, key_pool, value_pool, block_table, heads, seq,
+                    static_cast<int>(head_dim), block_size, max_blocks, start, positions, pos64);
+  }
   return launch(*ka, {strideBlocks(total)}, {256}, 0, stream, key, value, key_pool, value_pool,
                 block_table, batch, heads, seq, head_dim, block_size, max_blocks, start, positions,
                 pos64);

@@ -10,6 +10,7 @@
 // lane j scores key j, online softmax across rounds (running max / sum in fp32), then the
 // wave accumulates p_j * v_j with each lane owning head_dim/64 output dims.
 #include "common.h"
+#include "skinny.h"
 
 using namespace dk;
 
@@ -166,7 +167,56 @@ __device__ void kv_append_impl(const void* key, const void* value, void* k_pool,
   }
 }
 
+// bf16 tokens, head_dim % 8 == 0 and <= 256, 16-byte aligned: one 256-thread workgroup per
+// (b, h, 64 new tokens). Key rows go out as 16-byte runs (the key pool is token-major); the value
+// chunk is staged in LDS and written d-major (the value pool holds [block][H][D][block_size]), 64
+// consecutive lanes storing 64 consecutive slots of one d. Same placement as kv_append_impl.
+constexpr int kAppendTokens = 64;
+
+__device__ void kv_append_tiles_bf16(const uint16_t* key, const uint16_t* value, uint16_t* k_pool,
+                                     uint16_t* v_pool, const int32_t* block_table, int64_t H,
+                                     int64_t S, int D, int64_t block_size, int64_t max_blocks,
+                                     int64_t start, const void* positions, int pos64) {
+  __shared__ __attribute__((aligned(16))) uint16_t vs[kAppendTokens * (256 + 8)];
+  const int pitch = D + 8;
+  const int64_t bh = blockIdx.y, b = bh / H, h = bh % H;
+  const int64_t s0 = static_cast<int64_t>(blockIdx.x) * kAppendTokens;
+  const int64_t base_pos = (positions != nullptr ? loadIndex(positions, pos64, b) : start) + s0;
+  const int64_t capacity = max_blocks * block_size;
+  const int chunks = D / 8;  // 16-byte chunks per token
+  const uint16_t* kin = key + (bh * S + s0) * D;
+  const uint16_t* vin = value + (bh * S + s0) * D;
+  for (int c = threadIdx.x; c < kAppendTokens * chunks; c += blockDim.x) {
+    const int t = c / chunks, part = c % chunks;
+    if (s0 + t >= S) continue;
+    const U128 kw = gload16(kin + t * D + part * 8);
+    *reinterpret_cast<U128*>(&vs[t * pitch + part * 8]) = gload16(vin + t * D + part * 8);
+    const int64_t pos = base_pos + t;
+    if (pos < 0 || pos >= capacity) continue;
+    const int64_t blk = block_table[b * max_blocks + pos / block_size];
+    *gp(reinterpret_cast<U128*>(k_pool + ((blk * H + h) * block_size + pos % block_size) * D +
+                                part * 8)) = kw;
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < kAppendTokens * D; e += blockDim.x) {
+    const int d = e / kAppendTokens, t = e % kAppendTokens;
+    const int64_t pos = base_pos + t;
+    if (s0 + t >= S || pos < 0 || pos >= capacity) continue;
+    const int64_t blk = block_table[b * max_blocks + pos / block_size];
+    *gp(v_pool + ((blk * H + h) * D + d) * block_size + pos % block_size) = vs[t * pitch + d];
+  }
+}
+
 }  // namespace
+
+extern "C" __global__ void __launch_bounds__(256)
+    kv_append_tiles_bf16_k(const uint16_t* key, const uint16_t* value, uint16_t* k_pool,
+                           uint16_t* v_pool, const int32_t* block_table, int64_t H, int64_t S,
+                           int D, int64_t block_size, int64_t max_blocks, int64_t start,
+                           const void* positions, int pos64) {
+  kv_append_tiles_bf16(key, value, k_pool, v_pool, block_table, H, S, D, block_size, max_blocks,
+                       start, positions, pos64);
+}
 
 DK_FLOAT_KERNELS(attention, 64,
                  (const void* q, const void* k, const void* v, void* out, int64_t B, int64_t Hq,

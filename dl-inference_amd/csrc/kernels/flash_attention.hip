@@ -42,7 +42,7 @@ typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
 template <int QB>
 __device__ void flashAttention(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                                uint16_t* out, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t Sk,
-                               int causal, float scale_log2) {
+                               int causal, float scale_log2, int out_bshd) {
   constexpr int kTileQ = 64 * QB;
   __shared__ __attribute__((aligned(16))) uint16_t Ks[kTileK * kPitch];
   __shared__ __attribute__((aligned(16))) uint16_t Vt[kD * kVPitch];
@@ -239,7 +239,8 @@ __device__ void flashAttention(const uint16_t* q, const uint16_t* k, const uint1
     if (qi >= Sq) continue;
     const float l = lsum[qb][0];
     const float inv = l > 0.f ? 1.f / l : 0.f;
-    uint16_t* orow = out + (bh * Sq + qi) * kD + g * 4;
+    // out [B, Hq, Sq, D], or [B, Sq, Hq, D] (the layout the transpose after attention makes)
+    uint16_t* orow = out + (out_bshd ? (b * Sq + qi) * Hq + h : bh * Sq + qi) * kD + g * 4;
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) {
       const uint32_t lo = packBf16x2(o[qb][dt][0] * inv, o[qb][dt][1] * inv);
@@ -259,8 +260,8 @@ __device__ void flashAttention(const uint16_t* q, const uint16_t* k, const uint1
 extern "C" __global__ void __launch_bounds__(kFlashThreads) __attribute__((amdgpu_waves_per_eu(2)))
     flash_attention_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* out,
                          int64_t Hq, int64_t Hkv, int64_t Sq, int64_t Sk, int causal,
-                         float scale_log2) {
-  flashAttention<1>(q, k, v, out, Hq, Hkv, Sq, Sk, causal, scale_log2);
+                         float scale_log2, int out_bshd) {
+  flashAttention<1>(q, k, v, out, Hq, Hkv, Sq, Sk, causal, scale_log2, out_bshd);
 }
 
 // 32 queries per wave (128 per workgroup): each K and V^T fragment read from LDS feeds two MFMAs,
@@ -269,6 +270,6 @@ extern "C" __global__ void __launch_bounds__(kFlashThreads) __attribute__((amdgp
 extern "C" __global__ void __launch_bounds__(kFlashThreads) __attribute__((amdgpu_waves_per_eu(2)))
     flash_attention_bf16_q32(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                              uint16_t* out, int64_t Hq, int64_t Hkv, int64_t Sq, int64_t Sk,
-                             int causal, float scale_log2) {
-  flashAttention<2>(q, k, v, out, Hq, Hkv, Sq, Sk, causal, scale_log2);
+                             int causal, float scale_log2, int out_bshd) {
+  flashAttention<2>(q, k, v, out, Hq, Hkv, Sq, Sk, causal, scale_log2, out_bshd);
 }

@@ -243,14 +243,24 @@ class AttentionOp final : public Operator {
       if (static_cast<std::int64_t>(positions->numel()) != B)
         throw std::invalid_argument("attention positions must have one entry per sequence");
     }
-    *out[0] = allocLike(q.dtype(), q.shape(), q);
+    // extension: output_layout "bshd" returns [B, S, H, D] (the layout a prompt's transpose node
+    // after attention makes), written by the flash kernel directly
+    const std::string layout = attrs.value_or<std::string>("output_layout", "bhsd");
+    if (layout != "bhsd" && layout != "bshd")
+      throw std::invalid_argument("attention output_layout must be \"bhsd\" or \"bshd\"");
+    const bool bshd = layout == "bshd";
+    *out[0] = allocLike(q.dtype(), bshd ? std::vector<std::int64_t>{B, Sq, Hq, D} : q.shape(), q);
     const int dt = hipDtype(q.dtype());
+    auto contiguous = [&](const Tensor& kk, const Tensor& vv) {
+      auto fn = bshd ? dli_hip_attention_bshd : dli_hip_attention;
+      check(fn(dt, ptr(q), ptr(kk), ptr(vv), ptr(*out[0]), B, Hq, Hkv, Sq, kk.dim(2), D,
+               causal ? 1 : 0, scale, ctx.stream),
+            type());
+    };
 
     if (cache_name.empty()) {
       if (positions != nullptr) throw std::invalid_argument("attention positions require kv_cache");
-      check(dli_hip_attention(dt, ptr(q), ptr(k), ptr(v), ptr(*out[0]), B, Hq, Hkv, Sq, k.dim(2), D,
-                              causal ? 1 : 0, scale, ctx.stream),
-            type());
+      contiguous(k, v);
       return;
     }
     if (ctx.kv_cache == nullptr) throw std::invalid_argument("attention missing KV cache");
@@ -266,11 +276,10 @@ class AttentionOp final : public Operator {
     if (positions == nullptr && past == 0) {
       // A prompt from an empty cache: the cache now holds exactly k and v, so attending over
       // them directly is the same computation, and runs on the contiguous (flash) kernel.
-      check(dli_hip_attention(dt, ptr(q), ptr(k), ptr(v), ptr(*out[0]), B, Hq, Hkv, Sq, k.dim(2),
-                              D, causal ? 1 : 0, scale, ctx.stream),
-            type());
+      contiguous(k, v);
       return;
     }
+    if (bshd) throw std::invalid_argument("attention output_layout \"bshd\" needs an empty cache");
     const KVCacheEntry& e = *cache.get(cache_name);
     const std::size_t ws_bytes = dli_hip_paged_attention_workspace(B, Hq, Sq, D, e.capacity());
     check(dli_hip_paged_attention(

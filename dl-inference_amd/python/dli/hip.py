@@ -77,6 +77,8 @@ _SIGNATURES = {
     + [_i64] * 8 + [_c_void_p, _int, _c_void_p],
     "dli_hip_attention": [_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p] + [_i64] * 6
     + [_int, _float, _c_void_p],
+    "dli_hip_attention_bshd": [_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p] + [_i64] * 6
+    + [_int, _float, _c_void_p],
     "dli_hip_kv_append": [_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p]
     + [_i64] * 7 + [_c_void_p, _int, _c_void_p],
     "dli_hip_linear_workspace": [_int, _i64, _i64, _i64],

@@ -237,7 +237,8 @@ def _prefill_layer_nodes(cfg: Qwen2Config, batch: int, seq: int, i: int, h: str,
     python/dli_export/export.py:272-424, with the [B, S, H, D] <-> [B, H, S, D] transposes a
     prompt of S tokens needs around rotary and attention). With fused, q/k/v_proj, their
     reshapes and transposes and rotary_embedding are one qkv_rope_heads node over the packed
-    self_attn.qkv_proj.{weight,bias}, o_proj + residual and
+    self_attn.qkv_proj.{weight,bias}, attention writes [B, S, H, D] itself (output_layout
+    "bshd", no transpose node), o_proj + residual and
     down_proj + residual are linear_residual nodes and gate_proj, up_proj, act_fn and mul one
     gate_up_silu node over the interleaved mlp.gate_up_proj.weight (pack_fused_weights): the
     same values (each fused kernel rounds where the nodes it replaces round). Returns the layer's
@@ -266,11 +267,16 @@ def _prefill_layer_nodes(cfg: Qwen2Config, batch: int, seq: int, i: int, h: str,
         _node(nodes, f"{p}.self_attn.rotary_embedding", "rotary_embedding",
               [f"{t}_q_heads", f"{t}_k_heads", "rotary_cos", "rotary_sin"],
               [f"{t}_q_rotary", f"{t}_k_rotary"], {"start_pos": 0})
-    _node(nodes, f"{p}.self_attn.attention", "attention",
-          [f"{t}_q_rotary", f"{t}_k_rotary", f"{t}_v_heads"], [f"{t}_attention"],
-          {"causal": True, "kv_cache": f"layer_{i}"})
-    _node(nodes, f"{p}.self_attn.attention_transpose", "transpose", [f"{t}_attention"],
-          [f"{t}_attention_bshd"], {"perm": [0, 2, 1, 3]})
+    if fused:  # the attention kernel writes [B, S, H, D] itself
+        _node(nodes, f"{p}.self_attn.attention", "attention",
+              [f"{t}_q_rotary", f"{t}_k_rotary", f"{t}_v_heads"], [f"{t}_attention_bshd"],
+              {"causal": True, "kv_cache": f"layer_{i}", "output_layout": "bshd"})
+    else:
+        _node(nodes, f"{p}.self_attn.attention", "attention",
+              [f"{t}_q_rotary", f"{t}_k_rotary", f"{t}_v_heads"], [f"{t}_attention"],
+              {"causal": True, "kv_cache": f"layer_{i}"})
+        _node(nodes, f"{p}.self_attn.attention_transpose", "transpose", [f"{t}_attention"],
+              [f"{t}_attention_bshd"], {"perm": [0, 2, 1, 3]})
     _node(nodes, f"{p}.self_attn.merge", "reshape", [f"{t}_attention_bshd"],
           [f"{t}_attention_merged"], {"shape": [batch, seq, q_w]})
     if fused:

@@ -230,6 +230,17 @@ int dli_hip_attention(int dtype, const void* q, const void* k, const void* v, vo
                       int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t seq_q,
                       int64_t seq_k, int64_t head_dim, int causal, float scale, void* stream);
 
+/* dli_hip_attention with out as [batch, seq_q, q_heads, head_dim], written by the attention
+ * kernel itself: the layout the merge reshape after attention (export.py:358-375) needs, which a
+ * prompt's [B, H, S, D] output reaches only through a transpose node. No counterpart in the
+ * reference (it fuses that transpose); the fused prefill graph uses it. Only the flash path
+ * (bf16, head_dim 64, seq_k > 0, 16-byte aligned tensors): any other call is rejected
+ * (DLI_HIP_EINVAL). */
+int dli_hip_attention_bshd(int dtype, const void* q, const void* k, const void* v, void* out,
+                           int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t seq_q,
+                           int64_t seq_k, int64_t head_dim, int causal, float scale,
+                           void* stream);
+
 /* Writes key/value [B, H, S, D] into the paged cache (layout in include/dli/kv_cache.h):
  * token s of sequence b goes to position p = start + s, or positions[b] + s when positions is
  * non-NULL. Tokens at p >= max_blocks * block_size are dropped. */

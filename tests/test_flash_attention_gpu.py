@@ -41,6 +41,19 @@ def test_flash_attention_matches_oracle(case, causal):
     assert_close(out, ops.attention(to_np(q), to_np(k), to_np(v), causal=causal), "bfloat16")
 
 
+@pytest.mark.parametrize("case", [(2, 14, 2, 100, 100), (1, 4, 2, 37, 200), (2, 16, 4, 2000, 2000)],
+                         ids=str)
+def test_flash_attention_bshd_output(case):
+    """output_layout "bshd": the same values as the [B, H, S, D] output, transposed."""
+    b, hq, hkv, sq, sk = case
+    q, k, v = rand((b, hq, sq, 64), 7), rand((b, hkv, sk, 64), 8), rand((b, hkv, sk, 64), 9)
+    bhsd = run_op("attention", {"q": q, "k": k, "v": v}, attrs={"causal": True})["output"]
+    bshd = run_op("attention", {"q": q, "k": k, "v": v},
+                  attrs={"causal": True, "output_layout": "bshd"})["output"]
+    assert tuple(bshd.shape) == (b, sq, hq, 64)
+    assert torch.equal(bshd, bhsd.transpose(1, 2).contiguous())
+
+
 def test_flash_attention_qwen2_prefill_size():
     b, hq, hkv, s = 4, 14, 2, 2048
     q, k, v = rand((b, hq, s, 64), 4), rand((b, hkv, s, 64), 5), rand((b, hkv, s, 64), 6)

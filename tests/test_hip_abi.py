@@ -68,6 +68,11 @@ def test_invalid_arguments_are_rejected_with_a_message():
     assert b"unsupported dtype" in lib.dli_hip_last_error()
     assert lib.dli_hip_attention(hip.F32, None, None, None, None, 1, 3, 2, 1, 1, 8, 1, 1.0, None) == -1
     assert b"multiple of kv_heads" in lib.dli_hip_last_error()
+    # the [B, S, H, D] output exists only on the flash path (bf16, head_dim 64)
+    fake = ctypes.c_void_p(256)  # never dereferenced: rejected before any launch
+    assert lib.dli_hip_attention_bshd(hip.F32, fake, fake, fake, fake, 1, 2, 2, 4, 4, 8, 1, 1.0,
+                                      None) == -1
+    assert b"flash kernel" in lib.dli_hip_last_error()
     assert lib.dli_hip_rotary(hip.F32, None, None, None, None, None, None, 1, 1, 1, 1, 3, 1, 4, 0,
                               None, hip.I64, None) == -1
     assert lib.dli_hip_linear(hip.BF16, hip.F16, None, None, None, None, 1, 1, 1, None) == -1
