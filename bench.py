@@ -605,11 +605,11 @@ def main():
     cfg = base if args.layers is None else replace(base, layers=args.layers)
     B = args.batch or (64 if large else 32)
     ctx = args.context or (8192 if large else 4096)
-    from dli_qwen2.graph import DEFAULT_SPLITS, LARGE_SPLITS, STACK_SPLITS
+    from dli_qwen2.graph import DEFAULT_SPLITS, STACK_SPLITS, large_splits
 
     graph_kind = "large" if large else args.graph
     splits = dict({"stack": STACK_SPLITS, "fused": DEFAULT_SPLITS,
-                   "large": LARGE_SPLITS}[graph_kind])
+                   "large": large_splits(B)}[graph_kind])
     if args.splits:
         splits.update({k: int(v) for k, v in (item.split("=") for item in args.splits.split(","))})
     dev = "cuda"

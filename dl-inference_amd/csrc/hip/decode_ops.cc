@@ -126,6 +126,12 @@ int partialThenResidual(const char* op, const void* x, const void* w, const void
 }
 
 }  // namespace
+
+// ops.cc: the tiled bf16 GEMM for decode-sized m (K split into a workspace)
+bool tiledDecodeLinear(int64_t m, int64_t n);
+int tiledBf16(const void* x, const void* w, const void* bias, const void* residual, void* out,
+              int64_t m, int64_t n, int64_t k, void* workspace, size_t workspace_bytes,
+              void* stream);
 }  // namespace dli::hip
 
 using namespace dli::hip;
@@ -175,6 +181,14 @@ int dli_hip_linear_residual(const void* x, const void* w, const void* bias, cons
                             void* out, int64_t m, int64_t n, int64_t k, int splits,
                             void* workspace, size_t workspace_bytes, void* stream) {
   const char* op = "linear_residual";
+  // outputs wider than the fused decode kernels hold (n > 1024, a large hidden size) with more
+  // than 8 rows: the tiled GEMM, K split into the workspace as far as it holds (the splits
+  // argument sizes the workspace only)
+  if (m > 8 && m <= 64 && n > 1024 && k % 8 == 0 && aligned16(x) && aligned16(w) &&
+      tiledDecodeLinear(m, n)) {
+    if (splits < 1) return bad(op, "splits must be positive");
+    return tiledBf16(x, w, bias, residual, out, m, n, k, workspace, workspace_bytes, stream);
+  }
   if (m > 64) {  // many rows (a prompt): one tiled MFMA GEMM, no split
     if (n <= 0) return bad(op, "n must be positive");
     if (k <= 0 || k % 8 != 0) return bad(op, "k must be a positive multiple of 8");

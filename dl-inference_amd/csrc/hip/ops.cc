@@ -83,6 +83,9 @@ DeviceKernel k_mfma_conv64("mfma_gemm", "mfma_conv2d_f32_t64");
 DeviceKernel k_mfma_conv128("mfma_gemm", "mfma_conv2d_f32_t128");
 DeviceKernel k_mfma_bf16_64("mfma_gemm", "mfma_linear_bf16_t64");
 DeviceKernel k_mfma_bf16_128("mfma_gemm", "mfma_linear_bf16_t128");
+DeviceKernel k_mfma_bf16_splitk("mfma_gemm", "mfma_linear_bf16_splitk_t64");
+DeviceKernel k_splitk_reduce_bf16("mfma_gemm", "splitk_reduce_bf16");
+DeviceKernel k_mfma_linres64_g("mfma_gemm", "mfma_linear_residual_bf16_t64");
 DeviceKernel k_mfma_splitk("mfma_gemm", "mfma_linear_f32_splitk_t64");
 DeviceKernel k_splitk_reduce("mfma_gemm", "splitk_reduce_f32");
 DeviceKernel k_mfma_conv_splitk("mfma_gemm", "mfma_conv2d_f32_splitk_t64");
@@ -131,6 +134,47 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 }  // namespace
 
+// K splits of the tiled bf16 GEMM for decode-sized m: double while the 64 x 64 tiles times the
+// splits stay within 1024 workgroups (four per CU: with two K slices in flight per workgroup
+// that keeps enough weight bytes in flight for HBM; 224 workgroups streamed 2 TB/s) and each
+// part keeps at least 256 columns (at most 16 parts).
+int64_t bf16Splits(int64_t m, int64_t n, int64_t k) {
+  const int64_t tiles = ((m + 63) / 64) * ((n + 63) / 64);
+  int64_t splits = 1;
+  while (splits < 16 && tiles * splits * 2 <= 1024 && k / (splits * 2) >= 256) splits *= 2;
+  return splits;
+}
+
+// decode-sized bf16 linears that run faster on the tiled MFMA GEMM than on the skinny kernels
+// (measured at m = 1, 8, 32, 64 on Qwen2-0.5B and -7B shapes: from m = 64 on every shape, from
+// m = 32 on the wide ones, never at m <= 8)
+bool tiledDecodeLinear(int64_t m, int64_t n) { return m > 32 || (m > 8 && n >= 8192); }
+
+// The tiled bf16 GEMM over decode-sized m, K split when the workspace allows it: out =
+// bf16(x w^T + bias) or, with a residual, bf16(residual + bf16(x w^T + bias)).
+int tiledBf16(const void* x, const void* w, const void* bias,
+              const void* residual, void* out, int64_t m, int64_t n, int64_t k, void* workspace,
+              size_t workspace_bytes, void* stream) {
+  int64_t splits = bf16Splits(m, n, k);
+  const size_t part = static_cast<size_t>(m * n) * sizeof(float);
+  while (splits > 1 && (workspace == nullptr || workspace_bytes < part * splits)) splits /= 2;
+  const Dim3 grid{static_cast<unsigned>((n + 63) / 64), static_cast<unsigned>((m + 63) / 64)};
+  if (splits == 1) {
+    if (residual != nullptr)
+      return launch(k_mfma_linres64_g, grid, {256}, 0, stream, x, w, bias, residual, out, m, n, k);
+    return launch(k_mfma_bf16_64, grid, {256}, 0, stream, x, w, bias, out, m, n, k, 0, 0);
+  }
+  const int64_t per = ((k + splits - 1) / splits + 63) / 64 * 64;
+  const int64_t parts = (k + per - 1) / per;
+  if (int rc = launch(k_mfma_bf16_splitk, {grid.x, grid.y, static_cast<unsigned>(parts)}, {256},
+                      0, stream, x, w, static_cast<float*>(workspace), m, n, k, per))
+    return rc;
+  return launch(k_splitk_reduce_bf16, {strideBlocks(m * n)}, {256}, 0, stream,
+                static_cast<const float*>(workspace), bias, residual, out, m, n,
+                static_cast<int>(parts));
+}
+
+
 int decodeAttentionFast(int dtype, const void* q, const void* key_pool, const void* value_pool,
                         const int32_t* block_table, void* out, int64_t batch, int64_t q_heads,
                         int64_t kv_heads, int64_t seq_q, int64_t head_dim, int64_t block_size,
@@ -169,8 +213,8 @@ int dli_hip_rms_norm(int dtype, const void* x, const void* weight, void* out, in
   if (k == nullptr) return badDtype("rms_norm", dtype);
   if (rows < 0 || hidden <= 0) return badArg("rms_norm", "rows must be >= 0 and hidden > 0");
   if (rows == 0) return 0;
-  // bf16 rows of up to 2048 elements in 16-byte chunks: one wave per row
-  if (dtype == DLI_BF16 && hidden % 8 == 0 && hidden <= 2048 && aligned16(x) &&
+  // bf16 rows of up to 4096 elements in 16-byte chunks: one wave per row
+  if (dtype == DLI_BF16 && hidden % 8 == 0 && hidden <= 4096 && aligned16(x) &&
       aligned16(weight) && aligned16(out)) {
     const int64_t groups = (rows + 3) / 4;
     const unsigned blocks = static_cast<unsigned>(groups < 65535 ? groups : 65535);
@@ -367,7 +411,13 @@ int dli_hip_linear(int dtype, int out_dtype, const void* x, const void* w, const
 }
 
 size_t dli_hip_linear_workspace(int dtype, int64_t m, int64_t n, int64_t k) {
-  if (dtype != DLI_F32 || m <= 0 || n <= 0 || k <= 0) return 0;
+  if (m <= 0 || n <= 0 || k <= 0) return 0;
+  if (dtype == DLI_BF16) {  // decode-sized m on the tiled GEMM: K split over fp32 parts
+    if (m > 64 || !tiledDecodeLinear(m, n) || k % 8 != 0) return 0;  // (fp32-out calls ignore it)
+    const int64_t splits = bf16Splits(m, n, k);
+    return splits > 1 ? static_cast<size_t>(splits * m * n) * sizeof(float) : 0;
+  }
+  if (dtype != DLI_F32) return 0;
   const int64_t splits = linearSplits(m, n, k);
   return splits > 1 ? static_cast<size_t>(splits * m * n) * sizeof(float) : 0;
 }
@@ -406,7 +456,15 @@ int dli_hip_linear_act(int dtype, int out_dtype, const void* x, const void* w, c
                   out, m, n, k, relu);
   }
   int rc;
-  if (dtype == DLI_BF16 && m <= 64 && k % 64 == 0 && aligned16(x) && aligned16(w)) {
+  if (dtype == DLI_BF16 && m <= 64 && tiledDecodeLinear(m, n) && k % 8 == 0 && aligned16(x) &&
+      aligned16(w) && !relu) {
+    if (out_f32)  // fp32 logits: one pass, no split (the parts' sum is rounded to bf16)
+      return launch(k_mfma_bf16_64,
+                    {static_cast<unsigned>((n + 63) / 64), static_cast<unsigned>((m + 63) / 64)},
+                    {256}, 0, stream, x, w, bias, out, m, n, k, out_f32, 0);
+    return tiledBf16(x, w, bias, nullptr, out, m, n, k, workspace, workspace_bytes,
+                     stream);
+  } else if (dtype == DLI_BF16 && m <= 64 && k % 64 == 0 && aligned16(x) && aligned16(w)) {
     // bf16 weight streaming for decode-sized m: MFMA skinny kernel.
     DeviceKernel* sk = m <= 16 ? &k_skinny1 : (m <= 32 ? &k_skinny2 : &k_skinny4);
     rc = launch(*sk, {blocksFor(n, 32)}, {256}, 0, stream, x, w, bias, out, m, n, k, out_f32);

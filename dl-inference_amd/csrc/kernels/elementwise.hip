@@ -216,11 +216,24 @@ __device__ void argmax_impl(const void* x, int64_t* ids, int64_t rows, int64_t w
   for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
     float v = -INFINITY;
     int64_t idx = width;  // sentinel larger than any index
-    for (int64_t i = threadIdx.x; i < width; i += blockDim.x) {
-      const float e = ld(px + r * width + i);
-      if (e > v || idx == width) {  // indices grow, so strict '>' keeps the first maximum
-        v = e;
-        idx = i;
+    // kBatch loads in flight per thread (one at a time, a 152k-wide row took 230 us), then
+    // the same in-order scan: indices grow, so strict '>' keeps the first maximum
+    constexpr int kBatch = 8;
+    const int64_t step = blockDim.x;
+    for (int64_t i0 = threadIdx.x; i0 < width; i0 += kBatch * step) {
+      float e[kBatch];
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        const int64_t i = i0 + u * step;
+        e[u] = i < width ? ld(px + r * width + i) : -INFINITY;
+      }
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        const int64_t i = i0 + u * step;
+        if (i < width && (e[u] > v || idx == width)) {
+          v = e[u];
+          idx = i;
+        }
       }
     }
 #pragma unroll

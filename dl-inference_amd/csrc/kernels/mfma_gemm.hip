@@ -295,9 +295,11 @@ __device__ __forceinline__ void gemmF32(ASrc A, BSrc B, int64_t R, int64_t Cn, i
 // block from memory.
 constexpr int kGroupRows = 8;
 
+// ld: row stride of a and b in elements (K for whole rows; a split-K part passes a and b offset
+// to its first column, its own K and the full row stride).
 template <int BM, int BN, class Epi>
 __device__ __forceinline__ void gemmBf16(const uint16_t* a, const uint16_t* b, int64_t R,
-                                         int64_t Cn, int64_t K, const Epi& epi) {
+                                         int64_t Cn, int64_t K, int64_t ld, const Epi& epi) {
   constexpr int BK = 64;
   constexpr int TM = BM / 32, TN = BN / 32;
   constexpr int VPR = BK / 8;  // 16-byte chunks per tile row
@@ -335,12 +337,12 @@ __device__ __forceinline__ void gemmBf16(const uint16_t* a, const uint16_t* b, i
 #pragma unroll
   for (int i = 0; i < AV; ++i) {
     const int64_t row = r0 + (t + i * kGemmThreads) / VPR;
-    pa[i] = a + (row < R ? row : R - 1) * K + kc;
+    pa[i] = a + (row < R ? row : R - 1) * ld + kc;
   }
 #pragma unroll
   for (int i = 0; i < BV; ++i) {
     const int64_t row = c0 + (t + i * kGemmThreads) / VPR;
-    pb[i] = b + (row < Cn ? row : Cn - 1) * K + kc;
+    pb[i] = b + (row < Cn ? row : Cn - 1) * ld + kc;
   }
   auto fetch = [&](U128 (&xa)[AV], U128 (&xb)[BV], int64_t k0) {
     if (k0 + BK <= K) {
@@ -894,7 +896,7 @@ extern "C" __global__ void __launch_bounds__(kGemmThreads)
       mfma_linear_bf16_t##BM(                                                                  \
       const uint16_t* x, const uint16_t* w, const uint16_t* bias, void* out, int64_t M,        \
       int64_t N, int64_t K, int out_f32, int relu) {                                           \
-    gemmBf16<BM, BN>(x, w, M, N, K,                                                            \
+    gemmBf16<BM, BN>(x, w, M, N, K, K,                                                         \
                      RowMajorOutBf16OrF32{out, reinterpret_cast<const bf16*>(bias), N, relu,   \
                                           out_f32});                                           \
   }
@@ -909,7 +911,7 @@ DK_MFMA_BF16(128, 128)
       mfma_linear_residual_bf16_t##BM(                                                         \
       const uint16_t* x, const uint16_t* w, const uint16_t* bias, const uint16_t* residual,    \
       uint16_t* out, int64_t M, int64_t N, int64_t K) {                                        \
-    gemmBf16<BM, BN>(x, w, M, N, K,                                                            \
+    gemmBf16<BM, BN>(x, w, M, N, K, K,                                                         \
                      ResidualOut{reinterpret_cast<bf16*>(out),                                  \
                                  reinterpret_cast<const bf16*>(residual),                      \
                                  reinterpret_cast<const bf16*>(bias), N});                     \
@@ -918,7 +920,8 @@ DK_MFMA_BF16(128, 128)
       mfma_gate_up_silu_bf16_t##BM(                                                            \
       const uint16_t* x, const uint16_t* w_gate_up, uint16_t* out, int64_t M, int64_t ffn,      \
       int64_t K) {                                                                             \
-    gemmBf16<BM, BN>(x, w_gate_up, M, 2 * ffn, K, SwiGluOut{reinterpret_cast<bf16*>(out), ffn}); \
+    gemmBf16<BM, BN>(x, w_gate_up, M, 2 * ffn, K, K,                                           \
+                     SwiGluOut{reinterpret_cast<bf16*>(out), ffn});                             \
   }
 
 DK_MFMA_BF16_FUSED(64, 64)
@@ -934,7 +937,7 @@ DK_MFMA_BF16_FUSED(128, 128)
                                 int64_t seq, int64_t start_pos, int q_heads, int kv_heads,     \
                                 int head_dim) {                                                \
     const int64_t n = static_cast<int64_t>(q_heads + 2 * kv_heads) * head_dim;                 \
-    gemmBf16<BM, BN>(x, w_qkv, M, n, K,                                                        \
+    gemmBf16<BM, BN>(x, w_qkv, M, n, K, K,                                                     \
                      QkvHeadsOut{reinterpret_cast<bf16*>(q), reinterpret_cast<bf16*>(k),       \
                                  reinterpret_cast<bf16*>(v),                                   \
                                  reinterpret_cast<const bf16*>(b_qkv), cos, sin, seq, max_pos, \
@@ -943,3 +946,33 @@ DK_MFMA_BF16_FUSED(128, 128)
 
 DK_MFMA_QKV_HEADS(64, 64)
 DK_MFMA_QKV_HEADS(128, 128)
+
+// bf16 linear with K split over grid.z (decode-sized m with few output tiles): part z covers
+// columns [z * per, min(K, (z + 1) * per)) (per % 64 == 0) and writes its fp32 sums to
+// part[z][M][N]; splitk_reduce_bf16 then adds the parts in z order.
+extern "C" __global__ void __launch_bounds__(kGemmThreads) DK_BF16_OCCUPANCY
+    mfma_linear_bf16_splitk_t64(const uint16_t* x, const uint16_t* w, float* part, int64_t M,
+                                int64_t N, int64_t K, int64_t per) {
+  const int64_t k0 = static_cast<int64_t>(blockIdx.z) * per;
+  const int64_t len = K - k0 < per ? K - k0 : per;
+  gemmBf16<64, 64>(x + k0, w + k0, M, N, len, K,
+                   RowMajorOutBf16OrF32{part + static_cast<int64_t>(blockIdx.z) * M * N, nullptr,
+                                        N, 0, 1});
+}
+
+// out[m, n] = bf16(v + bias[n]), or with a residual bf16(residual[m, n] + bf16(v + bias[n])),
+// v = the sum of the split parts in split order: the rounding points of RowMajorOut and
+// ResidualOut.
+extern "C" __global__ void __launch_bounds__(256)
+    splitk_reduce_bf16(const float* part, const uint16_t* bias, const uint16_t* residual,
+                       uint16_t* out, int64_t M, int64_t N, int splits) {
+  const int64_t total = M * N;
+  for (int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; e < total;
+       e += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    float v = gp(part)[e];
+    for (int z = 1; z < splits; ++z) v += gp(part)[z * total + e];
+    if (bias != nullptr) v += bf16ToFloat(gp(bias)[e % N]);
+    if (residual != nullptr) v = bf16ToFloat(gp(residual)[e]) + Num<bf16>::round(v);
+    gp(out)[e] = floatToBf16(v);
+  }
+}

@@ -48,12 +48,12 @@ __device__ void rms_norm_impl(const void* x, const void* weight, void* out, int6
   }
 }
 
-// bf16 rows with hidden % 8 == 0 and hidden <= 64 * 8 * kRowChunks, 16-byte aligned: one wave
+// bf16 rows with hidden % 8 == 0 and hidden <= 64 * 8 * kRowChunks (4096), 16-byte aligned: one wave
 // per row (4 rows per 256-thread block, grid-stride over rows), the row held in registers as
 // 16-byte chunks (chunk c of the row in lane c % 64), sum of squares reduced inside the wave
 // (no LDS, no barrier), 16-byte loads and stores. Per element the same arithmetic as the
 // block-per-row kernel: x * inv * w with inv = 1 / sqrt(mean(x^2) + eps), rounded once.
-constexpr int kRowChunks = 4;
+constexpr int kRowChunks = 8;
 
 __device__ void rms_norm_rows_bf16(const uint16_t* x, const uint16_t* weight, uint16_t* out,
                                    int64_t rows, int hidden, float eps) {

@@ -192,7 +192,16 @@ def _stack_nodes(cfg: Qwen2Config, nodes: list, splits: dict, logits_dtype: str,
 # decoder stack, whose q|k|v workgroups take no down_proj unit)
 DEFAULT_SPLITS = {"o": 1, "down": 4}
 STACK_SPLITS = {"o": 1, "down": 3}
+# K splits of o_proj and down_proj in the large-hidden graph. From 9 rows they run on the tiled
+# MFMA GEMM, which splits K into the node's workspace as far as these counts size it (it picks 8
+# for o_proj and 16 for down_proj at hidden 3584); up to 8 rows the skinny split-K kernels take
+# them (at most 8 splits).
 LARGE_SPLITS = {"o": 1, "down": 2}
+LARGE_SPLITS_TILED = {"o": 8, "down": 16}
+
+
+def large_splits(batch: int) -> dict:
+    return dict(LARGE_SPLITS_TILED if batch > 8 else LARGE_SPLITS)
 FUSED_MAX_HIDDEN = 1024  # the fused kernels keep a tile's activation rows in registers
 
 
@@ -214,7 +223,7 @@ def build_decode_graph(cfg: Qwen2Config, batch: int, fused: bool = True,
     _node(nodes, "model.embed_tokens", "embedding", ["input_ids", "model.embed_tokens.weight"],
           ["hidden_states"])
     if uses_large_graph(cfg, fused):
-        _large_nodes(cfg, batch, nodes, splits or LARGE_SPLITS)
+        _large_nodes(cfg, batch, nodes, splits or large_splits(batch))
         graph = {"format": "dli.graph.v1", "model_type": "qwen2_decode_large",
                  "inputs": INPUTS, "outputs": OUTPUTS, "nodes": nodes}
         return dli.Graph.from_json(json.dumps(graph))

@@ -142,7 +142,13 @@ def test_qkv_rope_heads(B, S, H, Hq, Hkv, D, start, max_pos):
 
 
 @pytest.mark.parametrize("B,N,K,splits,bias", CASES + [(16, 4096, 1024, 1, True),
-                                                      (16, 4096, 1024, 2, True)])
+                                                      (16, 4096, 1024, 2, True),
+                                                      # n > 1024 at 33-64 rows: the tiled GEMM,
+                                                      # K split as far as the workspace holds
+                                                      (64, 3584, 3584, 4, True),
+                                                      (48, 2048, 4096, 2, False),
+                                                      (40, 1032, 1000, 4, True),
+                                                      (64, 1536, 6144, 1, False)])
 def test_linear_residual(B, N, K, splits, bias):
     """splits > 1: the last split to finish a tile sums the partials; the second call checks that
     the first left every arrival counter at zero."""

@@ -73,7 +73,11 @@ def test_embedding(dtype, ids_dtype):
 
 @pytest.mark.parametrize("dtype", FLOATS)
 @pytest.mark.parametrize("m,n,k", [(1, 896, 896), (7, 130, 64), (16, 1152, 896), (32, 4864, 896),
-                                   (33, 96, 4864), (64, 200, 128), (100, 70, 40), (3, 5, 7)])
+                                   (33, 96, 4864), (64, 200, 128), (100, 70, 40), (3, 5, 7),
+                                   # decode-sized bf16 on the tiled GEMM: K split into parts
+                                   # (tail parts, k % 64 != 0), wide outputs from 16 rows
+                                   (64, 3584, 3584), (48, 9000, 520), (16, 8200, 896),
+                                   (40, 1032, 1000)])
 @pytest.mark.parametrize("bias", [False, True])
 def test_linear(dtype, m, n, k, bias):
     scale = 1.0 / np.sqrt(k)
