@@ -85,7 +85,8 @@ DeviceKernel k_mfma_bf16_64("mfma_gemm", "mfma_linear_bf16_t64");
 DeviceKernel k_mfma_bf16_128("mfma_gemm", "mfma_linear_bf16_t128");
 DeviceKernel k_mfma_bf16_splitk("mfma_gemm", "mfma_linear_bf16_splitk_t64");
 DeviceKernel k_splitk_reduce_bf16("mfma_gemm", "splitk_reduce_bf16");
-DeviceKernel k_mfma_linres64_g("mfma_gemm", "mfma_linear_residual_bf16_t64");
+DeviceKernel k_mfma_bf16_stream("mfma_gemm", "mfma_linear_bf16_stream_t64");
+DeviceKernel k_mfma_linres_stream("mfma_gemm", "mfma_linear_residual_bf16_stream_t64");
 DeviceKernel k_mfma_splitk("mfma_gemm", "mfma_linear_f32_splitk_t64");
 DeviceKernel k_splitk_reduce("mfma_gemm", "splitk_reduce_f32");
 DeviceKernel k_mfma_conv_splitk("mfma_gemm", "mfma_conv2d_f32_splitk_t64");
@@ -135,13 +136,14 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 }  // namespace
 
 // K splits of the tiled bf16 GEMM for decode-sized m: double while the 64 x 64 tiles times the
-// splits stay within 1024 workgroups (four per CU: with two K slices in flight per workgroup
-// that keeps enough weight bytes in flight for HBM; 224 workgroups streamed 2 TB/s) and each
-// part keeps at least 256 columns (at most 16 parts).
+// splits stay within 256 workgroups and each part keeps at least 256 columns (at most 16 parts).
+// Measured at 64 rows with weights that miss the caches: 3584 x 3584 best at 4 parts (13 us),
+// 3584 x 18944 at 4 (33 us), 512 x 3584 at 7-8 (11 us), 18944 x 3584 unsplit (42 us); more
+// parts only add fp32 partial traffic.
 int64_t bf16Splits(int64_t m, int64_t n, int64_t k) {
   const int64_t tiles = ((m + 63) / 64) * ((n + 63) / 64);
   int64_t splits = 1;
-  while (splits < 16 && tiles * splits * 2 <= 1024 && k / (splits * 2) >= 256) splits *= 2;
+  while (splits < 16 && tiles * splits * 2 <= 256 && k / (splits * 2) >= 256) splits *= 2;
   return splits;
 }
 
@@ -161,10 +163,11 @@ int tiledBf16(const void* x, const void* w, const void* bias,
   const Dim3 grid{static_cast<unsigned>((n + 63) / 64), static_cast<unsigned>((m + 63) / 64)};
   if (splits == 1) {
     if (residual != nullptr)
-      return launch(k_mfma_linres64_g, grid, {256}, 0, stream, x, w, bias, residual, out, m, n, k);
-    return launch(k_mfma_bf16_64, grid, {256}, 0, stream, x, w, bias, out, m, n, k, 0, 0);
+      return launch(k_mfma_linres_stream, grid, {256}, 0, stream, x, w, bias, residual, out, m,
+                    n, k);
+    return launch(k_mfma_bf16_stream, grid, {256}, 0, stream, x, w, bias, out, m, n, k, 0);
   }
-  const int64_t per = ((k + splits - 1) / splits + 63) / 64 * 64;
+  const int64_t per = ((k + splits - 1) / splits + 127) / 128 * 128;  // whole 128-wide slices
   const int64_t parts = (k + per - 1) / per;
   if (int rc = launch(k_mfma_bf16_splitk, {grid.x, grid.y, static_cast<unsigned>(parts)}, {256},
                       0, stream, x, w, static_cast<float*>(workspace), m, n, k, per))
@@ -458,10 +461,10 @@ int dli_hip_linear_act(int dtype, int out_dtype, const void* x, const void* w, c
   int rc;
   if (dtype == DLI_BF16 && m <= 64 && tiledDecodeLinear(m, n) && k % 8 == 0 && aligned16(x) &&
       aligned16(w) && !relu) {
-    if (out_f32)  // fp32 logits: one pass, no split (the parts' sum is rounded to bf16)
-      return launch(k_mfma_bf16_64,
+    if (out_f32)  // fp32 logits: one pass, no split (the split reduce writes bf16)
+      return launch(k_mfma_bf16_stream,
                     {static_cast<unsigned>((n + 63) / 64), static_cast<unsigned>((m + 63) / 64)},
-                    {256}, 0, stream, x, w, bias, out, m, n, k, out_f32, 0);
+                    {256}, 0, stream, x, w, bias, out, m, n, k, out_f32);
     return tiledBf16(x, w, bias, nullptr, out, m, n, k, workspace, workspace_bytes,
                      stream);
   } else if (dtype == DLI_BF16 && m <= 64 && k % 64 == 0 && aligned16(x) && aligned16(w)) {

@@ -297,10 +297,12 @@ constexpr int kGroupRows = 8;
 
 // ld: row stride of a and b in elements (K for whole rows; a split-K part passes a and b offset
 // to its first column, its own K and the full row stride).
-template <int BM, int BN, class Epi>
+// BK: K columns per slice, 64 or 128 (128 doubles the bytes each workgroup has in flight: the
+// decode-sized kernels, whose few workgroups stream the weights).
+template <int BM, int BN, int BK = 64, class Epi>
 __device__ __forceinline__ void gemmBf16(const uint16_t* a, const uint16_t* b, int64_t R,
                                          int64_t Cn, int64_t K, int64_t ld, const Epi& epi) {
-  constexpr int BK = 64;
+  static_assert(BK == 64 || BK == 128, "slice width");
   constexpr int TM = BM / 32, TN = BN / 32;
   constexpr int VPR = BK / 8;  // 16-byte chunks per tile row
   constexpr int AV = BM * VPR / kGemmThreads, BV = BN * VPR / kGemmThreads;
@@ -328,7 +330,11 @@ __device__ __forceinline__ void gemmBf16(const uint16_t* a, const uint16_t* b, i
     r0 = static_cast<int64_t>(first + in % gs) * BM;
     c0 = static_cast<int64_t>(in / gs) * BN;
   }
-  auto at = [](int row, int c) { return row * BK + (c ^ ((row >> 1) & 7)) * 8; };
+  // 64-wide slices: rows of 128 bytes, two rows fill the 64 banks, chunk c at c ^ ((r >> 1) & 7);
+  // 128-wide: rows of 256 bytes, chunk c of 16 at c ^ (r & 15)
+  auto at = [](int row, int c) {
+    return row * BK + (BK == 64 ? c ^ ((row >> 1) & 7) : c ^ (row & 15)) * 8;
+  };
   // the thread's source rows, clamped into range (a clamped row loads a real row whose results
   // the epilogue drops); k past K loads zeros, in the last slice only
   const uint16_t* pa[AV];
@@ -400,11 +406,46 @@ __device__ __forceinline__ void gemmBf16(const uint16_t* a, const uint16_t* b, i
                                                             acc[i][j], 0, 0, 0);
   };
   constexpr int kMm = TM * TN, kRd = TM + TN, kWr = AV + BV;
-  static_assert(kMm >= kRd && kMm >= kWr, "MFMAs to interleave the memory instructions with");
+  static_assert(kMm >= kRd && (BK == 128 ? 2 * kMm >= kWr : kMm >= kWr),
+                "MFMAs to interleave the memory instructions with");
   // A step whose stash and fetch both cover a whole slice: multiply (as, bs); write (xa, xb),
   // the next slice, into (na, nb); load slice k0f into (xa, xb) once written.
   auto wholeStep = [&](const uint16_t* as, const uint16_t* bs, U128 (&xa)[AV], U128 (&xb)[BV],
                        uint16_t* na, uint16_t* nb, int64_t k0f) {
+    if constexpr (BK == 128) {
+      // four 32-column sub-slices, fragments double-buffered in registers: each sub-slice's
+      // reads go out during the MFMAs of the one before, the stash and the next loads during
+      // the last two
+      U128 fa[2][TM], fb[2][TN];
+      frags(as, bs, 0, fa[0], fb[0]);
+      frags(as, bs, 1, fa[1], fb[1]);
+      mma(fa[0], fb[0]);
+      frags(as, bs, 2, fa[0], fb[0]);
+#pragma unroll
+      for (int i = 0; i < kRd; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      }
+      mma(fa[1], fb[1]);
+      frags(as, bs, 3, fa[1], fb[1]);
+#pragma unroll
+      for (int i = 0; i < kRd; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+      }
+      stash(xa, xb, na, nb);
+      fetchWhole(xa, xb, k0f);
+      mma(fa[0], fb[0]);
+      mma(fa[1], fb[1]);
+#pragma unroll
+      for (int i = 0; i < kWr / 2; ++i) {  // two LDS writes and two loads per MFMA
+        __builtin_amdgcn_sched_group_barrier(0x200, 2, 2);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 2);
+        __builtin_amdgcn_sched_group_barrier(0x020, 2, 2);
+      }
+      __syncthreads();
+      return;
+    }
     U128 fa0[TM], fb0[TN], fa1[TM], fb1[TN];
     frags(as, bs, 0, fa0, fb0);
     frags(as, bs, 1, fa1, fb1);
@@ -431,10 +472,11 @@ __device__ __forceinline__ void gemmBf16(const uint16_t* a, const uint16_t* b, i
   auto tailStep = [&](const uint16_t* as, const uint16_t* bs, U128 (&xa)[AV], U128 (&xb)[BV],
                       uint16_t* na, uint16_t* nb, int64_t s, int64_t nk) {
     U128 fa[TM], fb[TN];
-    frags(as, bs, 0, fa, fb);
-    mma(fa, fb);
-    frags(as, bs, 1, fa, fb);
-    mma(fa, fb);
+#pragma unroll
+    for (int sub = 0; sub < BK / 32; ++sub) {
+      frags(as, bs, sub, fa, fb);
+      mma(fa, fb);
+    }
     if (s + 1 < nk) stash(xa, xb, na, nb);
     __syncthreads();
     if (s + 3 < nk) fetch(xa, xb, (s + 3) * BK);
@@ -955,9 +997,28 @@ extern "C" __global__ void __launch_bounds__(kGemmThreads) DK_BF16_OCCUPANCY
                                 int64_t N, int64_t K, int64_t per) {
   const int64_t k0 = static_cast<int64_t>(blockIdx.z) * per;
   const int64_t len = K - k0 < per ? K - k0 : per;
-  gemmBf16<64, 64>(x + k0, w + k0, M, N, len, K,
-                   RowMajorOutBf16OrF32{part + static_cast<int64_t>(blockIdx.z) * M * N, nullptr,
-                                        N, 0, 1});
+  gemmBf16<64, 64, 128>(x + k0, w + k0, M, N, len, K,
+                        RowMajorOutBf16OrF32{part + static_cast<int64_t>(blockIdx.z) * M * N,
+                                             nullptr, N, 0, 1});
+}
+
+// The same tile and slice shape without a split: decode-sized m (at most 64 rows), bias, bf16 or
+// fp32 out; and with a residual (bf16 out).
+extern "C" __global__ void __launch_bounds__(kGemmThreads) DK_BF16_OCCUPANCY
+    mfma_linear_bf16_stream_t64(const uint16_t* x, const uint16_t* w, const uint16_t* bias,
+                                void* out, int64_t M, int64_t N, int64_t K, int out_f32) {
+  gemmBf16<64, 64, 128>(x, w, M, N, K, K,
+                        RowMajorOutBf16OrF32{out, reinterpret_cast<const bf16*>(bias), N, 0,
+                                             out_f32});
+}
+extern "C" __global__ void __launch_bounds__(kGemmThreads) DK_BF16_OCCUPANCY
+    mfma_linear_residual_bf16_stream_t64(const uint16_t* x, const uint16_t* w,
+                                         const uint16_t* bias, const uint16_t* residual,
+                                         uint16_t* out, int64_t M, int64_t N, int64_t K) {
+  gemmBf16<64, 64, 128>(x, w, M, N, K, K,
+                        ResidualOut{reinterpret_cast<bf16*>(out),
+                                    reinterpret_cast<const bf16*>(residual),
+                                    reinterpret_cast<const bf16*>(bias), N});
 }
 
 // out[m, n] = bf16(v + bias[n]), or with a residual bf16(residual[m, n] + bf16(v + bias[n])),

@@ -193,11 +193,10 @@ def _stack_nodes(cfg: Qwen2Config, nodes: list, splits: dict, logits_dtype: str,
 DEFAULT_SPLITS = {"o": 1, "down": 4}
 STACK_SPLITS = {"o": 1, "down": 3}
 # K splits of o_proj and down_proj in the large-hidden graph. From 9 rows they run on the tiled
-# MFMA GEMM, which splits K into the node's workspace as far as these counts size it (it picks 8
-# for o_proj and 16 for down_proj at hidden 3584); up to 8 rows the skinny split-K kernels take
-# them (at most 8 splits).
+# MFMA GEMM, which splits K into the node's workspace as far as these counts size it (it picks 4
+# for both at hidden 3584); up to 8 rows the skinny split-K kernels take them (at most 8).
 LARGE_SPLITS = {"o": 1, "down": 2}
-LARGE_SPLITS_TILED = {"o": 8, "down": 16}
+LARGE_SPLITS_TILED = {"o": 4, "down": 4}
 
 
 def large_splits(batch: int) -> dict:
