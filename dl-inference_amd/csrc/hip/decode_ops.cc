@@ -47,6 +47,7 @@ DeviceKernel k_mfma_linres64("mfma_gemm", "mfma_linear_residual_bf16_t64");
 DeviceKernel k_mfma_linres128("mfma_gemm", "mfma_linear_residual_bf16_t128");
 DeviceKernel k_mfma_gu64("mfma_gemm", "mfma_gate_up_silu_bf16_t64");
 DeviceKernel k_mfma_gu128("mfma_gemm", "mfma_gate_up_silu_bf16_t128");
+DeviceKernel k_mfma_gu_stream("mfma_gemm", "mfma_gate_up_silu_bf16_stream_t64");
 DeviceKernel k_mfma_qkvh64("mfma_gemm", "mfma_qkv_heads_bf16_t64");
 DeviceKernel k_mfma_qkvh128("mfma_gemm", "mfma_qkv_heads_bf16_t128");
 
@@ -235,9 +236,9 @@ int dli_hip_gate_up_silu(const void* hidden, const void* norm_weight, const void
                          void* out, int64_t m, int64_t ffn, int64_t hidden_size, float eps,
                          void* stream) {
   const char* op = "gate_up_silu";
-  if (m > 64) {
-    // many rows (a prompt): one tiled MFMA GEMM over the interleaved weight, SwiGLU in its
-    // epilogue
+  if (m > 64 || (m > 0 && hidden_size > kMaxLmK && norm_weight == nullptr)) {
+    // many rows (a prompt), or a hidden size the skinny kernels do not hold: one tiled MFMA
+    // GEMM over the interleaved weight, SwiGLU in its epilogue
     if (ffn <= 0 || ffn % 16 != 0) return bad(op, "ffn must be a positive multiple of 16");
     if (hidden_size <= 0 || hidden_size % 8 != 0)
       return bad(op, "hidden_size must be a positive multiple of 8");
@@ -245,6 +246,9 @@ int dli_hip_gate_up_silu(const void* hidden, const void* norm_weight, const void
       return bad(op, "the RMSNorm prologue is for at most 64 rows (normalize first)");
     if (!aligned16(hidden) || !aligned16(w_gate_up))
       return bad(op, "hidden and w_gate_up must be 16-byte aligned");
+    if (m <= 64)  // decode-sized rows: 64 x 64 tiles, 128-wide K slices
+      return launch(k_mfma_gu_stream, {static_cast<unsigned>((2 * ffn + 63) / 64), 1}, {256}, 0,
+                    stream, hidden, w_gate_up, out, m, ffn, hidden_size);
     bool big = false;
     unsigned grid[2];
     if (!tiledGrid(m, 2 * ffn, &big, grid)) return bad(op, "too many rows");

@@ -1021,6 +1021,13 @@ extern "C" __global__ void __launch_bounds__(kGemmThreads) DK_BF16_OCCUPANCY
                                     reinterpret_cast<const bf16*>(bias), N});
 }
 
+extern "C" __global__ void __launch_bounds__(kGemmThreads) DK_BF16_OCCUPANCY
+    mfma_gate_up_silu_bf16_stream_t64(const uint16_t* x, const uint16_t* w_gate_up, uint16_t* out,
+                                      int64_t M, int64_t ffn, int64_t K) {
+  gemmBf16<64, 64, 128>(x, w_gate_up, M, 2 * ffn, K, K,
+                        SwiGluOut{reinterpret_cast<bf16*>(out), ffn});
+}
+
 // out[m, n] = bf16(v + bias[n]), or with a residual bf16(residual[m, n] + bf16(v + bias[n])),
 // v = the sum of the split parts in split order: the rounding points of RowMajorOut and
 // ResidualOut.

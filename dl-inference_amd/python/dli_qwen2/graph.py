@@ -84,11 +84,14 @@ def _reference_nodes(cfg: Qwen2Config, batch: int, nodes: list):
     _node(nodes, "greedy", "argmax", ["logits"], ["next_ids"])
 
 
-def _large_nodes(cfg: Qwen2Config, batch: int, nodes: list, splits: dict):
+def _large_nodes(cfg: Qwen2Config, batch: int, nodes: list, splits: dict,
+                 fused_mlp: bool = False):
     """Decode step for hidden sizes the fused norm-prologue kernels do not hold in registers
     (hidden > 1024, e.g. the Qwen2-7B shape): the reference node sequence with o_proj and
     down_proj each fused with their residual add (linear_residual, split-K for down_proj).
-    Attention over the paged cache runs on the MFMA decode kernel for head_dim 64 or 128."""
+    Attention over the paged cache runs on the MFMA decode kernel for head_dim 64 or 128.
+    fused_mlp: gate_proj, up_proj, act_fn and mul as one gate_up_silu node over the interleaved
+    mlp.gate_up_proj.weight (pack_large_weights; the GPU plugin's operator, same rounding)."""
     h = "hidden_states"
     q_w = cfg.heads * cfg.head_dim
     for i in range(cfg.layers):
@@ -116,12 +119,16 @@ def _large_nodes(cfg: Qwen2Config, batch: int, nodes: list, splits: dict):
         _node(nodes, f"{p}.post_attention_layernorm", "rms_norm",
               [f"{t}_after_attention", f"{p}.post_attention_layernorm.weight"],
               [f"{t}_post_attention_norm"], {"eps": cfg.eps})
-        _node(nodes, f"{p}.mlp.gate_proj", "linear",
-              [f"{t}_post_attention_norm", f"{p}.mlp.gate_proj.weight"], [f"{t}_gate"])
-        _node(nodes, f"{p}.mlp.up_proj", "linear",
-              [f"{t}_post_attention_norm", f"{p}.mlp.up_proj.weight"], [f"{t}_up"])
-        _node(nodes, f"{p}.mlp.act_fn", "silu", [f"{t}_gate"], [f"{t}_silu"])
-        _node(nodes, f"{p}.mlp.mul", "mul", [f"{t}_silu", f"{t}_up"], [f"{t}_gated"])
+        if fused_mlp:
+            _node(nodes, f"{p}.mlp.gate_up", "gate_up_silu",
+                  [f"{t}_post_attention_norm", f"{p}.mlp.gate_up_proj.weight"], [f"{t}_gated"])
+        else:
+            _node(nodes, f"{p}.mlp.gate_proj", "linear",
+                  [f"{t}_post_attention_norm", f"{p}.mlp.gate_proj.weight"], [f"{t}_gate"])
+            _node(nodes, f"{p}.mlp.up_proj", "linear",
+                  [f"{t}_post_attention_norm", f"{p}.mlp.up_proj.weight"], [f"{t}_up"])
+            _node(nodes, f"{p}.mlp.act_fn", "silu", [f"{t}_gate"], [f"{t}_silu"])
+            _node(nodes, f"{p}.mlp.mul", "mul", [f"{t}_silu", f"{t}_up"], [f"{t}_gated"])
         _node(nodes, f"{p}.mlp.down_proj", "linear_residual",
               [f"{t}_gated", f"{p}.mlp.down_proj.weight", f"{t}_after_attention"],
               [f"{t}_output"], {"splits": splits.get("down", 1)})
@@ -212,17 +219,19 @@ def uses_large_graph(cfg: Qwen2Config, fused: bool) -> bool:
 
 def build_decode_graph(cfg: Qwen2Config, batch: int, fused: bool = True,
                        splits: dict | None = None, logits_dtype: str = "float32",
-                       stack: bool = False, check_status: bool = False) -> "dli.Graph":
+                       stack: bool = False, check_status: bool = False,
+                       large_fused_mlp: bool = False) -> "dli.Graph":
     """fused=False: the reference's node sequence; fused=True: five launches per layer;
     stack=True (with fused): all layers in one decoder_stack node (check_status: the node waits
     for its launch and fails if a workgroup gave up waiting; for tests, not for capture). With
     fused=True and a hidden size above 1024 (the Qwen2-7B shape) the step is the large-hidden
-    graph instead (_large_nodes), whatever `stack` says."""
+    graph instead (_large_nodes, with its MLP as one gate_up_silu node when large_fused_mlp),
+    whatever `stack` says."""
     nodes: list = []
     _node(nodes, "model.embed_tokens", "embedding", ["input_ids", "model.embed_tokens.weight"],
           ["hidden_states"])
     if uses_large_graph(cfg, fused):
-        _large_nodes(cfg, batch, nodes, splits or large_splits(batch))
+        _large_nodes(cfg, batch, nodes, splits or large_splits(batch), large_fused_mlp)
         graph = {"format": "dli.graph.v1", "model_type": "qwen2_decode_large",
                  "inputs": INPUTS, "outputs": OUTPUTS, "nodes": nodes}
         return dli.Graph.from_json(json.dumps(graph))
@@ -368,6 +377,17 @@ def interleave_gate_up(gate: torch.Tensor, up: torch.Tensor, block: int = 16) ->
     g = gate.reshape(f // block, block, hsz)
     u = up.reshape(f // block, block, hsz)
     return torch.stack([g, u], dim=1).reshape(2 * f, hsz).contiguous()
+
+
+def pack_large_weights(cfg: Qwen2Config, weights: dict) -> dict:
+    """The large-hidden graph's fused MLP weight: mlp.gate_up_proj.weight (16-row interleave of
+    gate and up) in place of gate_proj and up_proj."""
+    out = dict(weights)
+    for i in range(cfg.layers):
+        p = f"model.layers.{i}.mlp"
+        out[f"{p}.gate_up_proj.weight"] = interleave_gate_up(out.pop(f"{p}.gate_proj.weight"),
+                                                              out.pop(f"{p}.up_proj.weight"))
+    return out
 
 
 def pack_fused_weights(cfg: Qwen2Config, weights: dict, drop_unfused: bool = False) -> dict:

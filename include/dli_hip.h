@@ -326,8 +326,9 @@ int dli_hip_linear_residual_norm(const void* x, const void* w, const void* bias,
  * interleaves the two weights in blocks of 16 rows: rows [32i, 32i+16) = gate rows
  * [16i, 16i+16), rows [32i+16, 32i+32) = up rows [16i, 16i+16). Replaces
  * post_attention_layernorm, gate_proj, up_proj, act_fn and mul (export.py:378-414). With
- * m > 64 (a prompt) one tiled MFMA GEMM over the interleaved weight computes it, the SwiGLU in
- * its epilogue (any hidden_size % 8 == 0); norm_weight must then be NULL (normalize first). */
+ * m > 64 (a prompt), and at any m with hidden_size > 1024, one tiled MFMA GEMM over the
+ * interleaved weight computes it, the SwiGLU in its epilogue (any hidden_size % 8 == 0);
+ * norm_weight must then be NULL (normalize first). */
 int dli_hip_gate_up_silu(const void* hidden, const void* norm_weight, const void* w_gate_up,
                          void* out, int64_t m, int64_t ffn, int64_t hidden_size, float eps,
                          void* stream);

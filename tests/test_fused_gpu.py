@@ -177,6 +177,18 @@ def test_gate_up_silu(B, H, F, norm):
     assert_close(out, R(R(ops.silu(g)) * u), "bfloat16")
 
 
+@pytest.mark.parametrize("B,H,F", [(48, 1536, 1024), (64, 2048, 2064), (9, 1032, 96),
+                                   (1, 1152, 512)])
+def test_gate_up_silu_large_hidden(B, H, F):
+    """hidden > 1024 at decode-sized rows (no RMSNorm prologue; the skinny kernels stop at 1024):
+    the tiled GEMM with the SwiGLU epilogue; F = 2064 leaves a half 64-column tile."""
+    x, wg, wu = rand((B, H), 34), rand((F, H), 35, 0.05), rand((F, H), 36, 0.05)
+    out = run_op("gate_up_silu", {"x": x, "w": interleave_gate_up(wg, wu)})["output"]
+    g = R(ops.linear(to_np(x), to_np(wg)))
+    u = R(ops.linear(to_np(x), to_np(wu)))
+    assert_close(out, R(R(ops.silu(g)) * u), "bfloat16")
+
+
 @pytest.mark.parametrize("B,H,V", [(1, 128, 1000), (5, 896, 4099), (32, 896, 151936 // 8),
                                    (48, 256, 777)])
 @pytest.mark.parametrize("logits_dtype", ["float32", "bfloat16"])
