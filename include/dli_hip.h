@@ -197,8 +197,9 @@ int dli_hip_linear(int dtype, int out_dtype, const void* x, const void* w, const
  * MFMA paths. No counterpart in the reference (linear and relu are separate nodes there); the
  * plugin uses it for every linear node (attribute activation = "relu" to fuse). A workspace of
  * dli_hip_linear_workspace(dtype, m, n, k) bytes (no zeroing needed) lets fp32 shapes with few
- * output tiles and a long K split K over more workgroups, summing the splits in a fixed order;
- * with workspace NULL or smaller, no split. */
+ * output tiles and a long K, and bf16 shapes with 33-64 rows (or 9-32 rows and n >= 8192, which
+ * run on the tiled GEMM) and few output tiles, split K over more workgroups, summing the splits
+ * in a fixed order; with workspace NULL or smaller, fewer or no splits. */
 int dli_hip_linear_act(int dtype, int out_dtype, const void* x, const void* w, const void* bias,
                        void* out, int64_t m, int64_t n, int64_t k, int activation,
                        void* workspace, size_t workspace_bytes, void* stream);
@@ -305,7 +306,11 @@ int dli_hip_qkv_rope_append(const void* hidden, const void* norm_weight, const v
  * the last to finish a tile sums them in split order and writes it. The workspace
  * (dli_hip_splitk_workspace bytes) must be zero-filled before its first use; every call leaves
  * its arrival counters at zero again. With m > 64 (a prompt: k % 8 == 0) one tiled MFMA GEMM
- * computes it with the add in its epilogue; splits and the workspace are then not used. */
+ * computes it with the add in its epilogue; splits and the workspace are then not used. With
+ * 9-64 rows and n > 1024 (outputs wider than the fused decode kernels hold, 33+ rows or
+ * n >= 8192) the tiled GEMM splits K into fp32 parts in the workspace, as many as the workspace
+ * of `splits` holds (up to its own choice), summed in split order with the residual by a second
+ * kernel. */
 int dli_hip_linear_residual(const void* x, const void* w, const void* bias, const void* residual,
                             void* out, int64_t m, int64_t n, int64_t k, int splits,
                             void* workspace, size_t workspace_bytes, void* stream);
