@@ -119,6 +119,28 @@ struct ConvPatch {
   }
 };
 
+// ---- tile order ----------------------------------------------------------------------------------
+// Workgroups are handed to the 8 XCDs round robin by linear id, so XCD x gets the x-th contiguous
+// range of tiles of a grouped order (kGroupRows row blocks per group, row blocks fastest): the
+// tiles one XCD runs at once share A row blocks and B column blocks in its L2. (gridDim.x, y) =
+// (column tiles, row tiles); each blockIdx.z slice (a K split) is mapped the same way. At
+// 8192 x 896 x 4864 (down_proj over a 4 x 2048 prompt) this took the bf16 GEMM from 110 to
+// 79 us; with the plain order, the 7 column tiles of a row block ran on 7 XCDs, each fetching
+// the row block from memory.
+constexpr int kGroupRows = 8;
+
+__device__ __forceinline__ void groupedTile(int BM, int BN, int64_t& r0, int64_t& c0) {
+  const uint64_t nn = gridDim.x, nm = gridDim.y, T = nn * nm;
+  const uint64_t L = blockIdx.x + nn * blockIdx.y;
+  const uint64_t x = L % 8, l = L / 8;
+  const uint64_t g = x * (T / 8) + (x < T % 8 ? x : T % 8) + l;  // a bijection of [0, T)
+  const uint64_t per = kGroupRows * nn, grp = g / per, first = grp * kGroupRows;
+  const uint64_t gs = nm - first < kGroupRows ? nm - first : kGroupRows;
+  const uint64_t in = g - grp * per;
+  r0 = static_cast<int64_t>(first + in % gs) * BM;
+  c0 = static_cast<int64_t>(in / gs) * BN;
+}
+
 // ---- fp32 core ---------------------------------------------------------------------------------
 // v_mfma_f32_16x16x4_f32: lane l supplies A[l % 16][kk] and B[kk][l % 16] for the step's k
 // index kk = l / 16 and receives D[(l / 16) * 4 + i][l % 16], i < 4.
@@ -160,8 +182,8 @@ __device__ __forceinline__ void gemmF32(ASrc A, BSrc B, int64_t R, int64_t Cn, i
   __shared__ __attribute__((aligned(16))) float Bs[LB::kFloats];
   const int t = threadIdx.x, lane = t % kWave, wave = t / kWave;
   const int wr = wave / 2, wc = wave % 2;
-  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * BM;
-  const int64_t c0 = static_cast<int64_t>(blockIdx.x) * BN;
+  int64_t r0, c0;
+  groupedTile(BM, BN, r0, c0);
   __shared__ int2 ktab[2][BK];  // per-slice k table of a source that has one (double-buffered)
   float ra[AE], rb[BE];
   auto slot = [&](int e, int rows_in_tile, bool fast_k, int& row, int& k) {
@@ -287,13 +309,7 @@ __device__ __forceinline__ void gemmF32(ASrc A, BSrc B, int64_t R, int64_t Cn, i
 // (rows r..r+15, one chunk) and the 16 lanes of a stash write (two rows) then fall on 16
 // different 4-bank groups of the 64 banks (no conflicts; SQ_LDS_BANK_CONFLICT reads 0).
 //
-// Tile order: workgroups are handed to the 8 XCDs round robin by linear id, so XCD x gets the
-// x-th contiguous range of tiles of a grouped order (kGroupRows row blocks per group, row blocks
-// fastest): the tiles one XCD runs at once share A row blocks and B column blocks in its L2.
-// At 8192 x 896 x 4864 (down_proj over a 4 x 2048 prompt) this took the GEMM from 110 to 79 us;
-// with the plain order, the 7 column tiles of a row block ran on 7 XCDs, each fetching the row
-// block from memory.
-constexpr int kGroupRows = 8;
+// Tiles in the XCD-grouped order (groupedTile).
 
 // ld: row stride of a and b in elements (K for whole rows; a split-K part passes a and b offset
 // to its first column, its own K and the full row stride).
@@ -319,17 +335,7 @@ __device__ __forceinline__ void gemmBf16(const uint16_t* a, const uint16_t* b, i
   const int t = threadIdx.x, lane = t % kWave, wave = t / kWave;
   const int wr = wave / 2, wc = wave % 2;
   int64_t r0, c0;
-  {
-    const uint64_t nn = gridDim.x, nm = gridDim.y, T = nn * nm;
-    const uint64_t L = blockIdx.x + nn * blockIdx.y;
-    const uint64_t x = L % 8, l = L / 8;
-    const uint64_t g = x * (T / 8) + (x < T % 8 ? x : T % 8) + l;  // a bijection of [0, T)
-    const uint64_t per = kGroupRows * nn, grp = g / per, first = grp * kGroupRows;
-    const uint64_t gs = nm - first < kGroupRows ? nm - first : kGroupRows;
-    const uint64_t in = g - grp * per;
-    r0 = static_cast<int64_t>(first + in % gs) * BM;
-    c0 = static_cast<int64_t>(in / gs) * BN;
-  }
+  groupedTile(BM, BN, r0, c0);
   // 64-wide slices: rows of 128 bytes, two rows fill the 64 banks, chunk c at c ^ ((r >> 1) & 7);
   // 128-wide: rows of 256 bytes, chunk c of 16 at c ^ (r & 15)
   auto at = [](int row, int c) {
