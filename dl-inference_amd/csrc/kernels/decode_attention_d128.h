@@ -157,7 +157,12 @@ __device__ __forceinline__ void decodeAttention128Unit(const DecodeAttn128Args& 
   const int group = a.Hq / a.Hkv;
   const int64_t stride = static_cast<int64_t>(a.splits) * kD128Waves;
   const int64_t first = static_cast<int64_t>(split) * kD128Waves + wave;
+  // The wave's cache block ids, one per lane (lane k holds the id of the wave's k-th block; the
+  // split count keeps that below 64), loaded once: a block id read in the loop made every fetch
+  // wait, in order, for the loads issued before it.
   const int32_t* table = a.block_table + static_cast<int64_t>(b) * a.max_blocks;
+  const int64_t my_blk_index = first + static_cast<int64_t>(lane) * stride;
+  const int32_t my_blk = my_blk_index < a.max_blocks ? gp(table)[my_blk_index] : 0;
   const int64_t past_b = a.positions != nullptr ? loadIndex(a.positions, a.pos64, b) : a.past;
   int64_t L = past_b + 1;
   if (L > a.max_blocks * kD128Block) L = a.max_blocks * kD128Block;
@@ -181,7 +186,7 @@ __device__ __forceinline__ void decodeAttention128Unit(const DecodeAttn128Args& 
   const int64_t halves = 2 * my_blocks;
   KvHalf128 buf[2];
   auto fetch = [&](KvHalf128& h, int64_t j) {
-    const int64_t blk = gp(table)[first + (j / 2) * stride];
+    const int64_t blk = __builtin_amdgcn_readlane(my_blk, static_cast<int>(j / 2));
     loadKvHalf128(h, a.k_pool, a.v_pool, blk, a.Hkv, kvh, static_cast<int>(j % 2), r, g);
   };
   if (halves > 0) fetch(buf[0], 0);
