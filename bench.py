@@ -689,8 +689,9 @@ def main():
 
     graph_desc = {"stack": "decoder_stack (one persistent launch for all layers)",
                   "fused": "fused (five launches per layer)",
-                  "large": "large-hidden graph (reference nodes, head_dim-128 MFMA decode "
-                           "attention, o/down linears fused with their residual adds)"}[graph_kind]
+                  "large": "large-hidden graph (per layer: q|k|v + RoPE + KV append, "
+                           "head_dim-128 MFMA decode attention, o_proj and down_proj each with "
+                           "their residual add and the RMSNorm after it, gate_up + SwiGLU)"}[graph_kind]
     shape = "Qwen2-7B" if large else "Qwen2-0.5B"
     result = {
         "metric": METRIC_7B if large else METRIC,

@@ -130,9 +130,70 @@ int partialThenResidual(const char* op, const void* x, const void* w, const void
 
 // ops.cc: the tiled bf16 GEMM for decode-sized m (K split into a workspace)
 bool tiledDecodeLinear(int64_t m, int64_t n);
+int64_t bf16Splits(int64_t m, int64_t n, int64_t k);
 int tiledBf16(const void* x, const void* w, const void* bias, const void* residual, void* out,
               int64_t m, int64_t n, int64_t k, void* workspace, size_t workspace_bytes,
               void* stream);
+int tiledBf16Parts(const void* x, const void* w, int64_t m, int64_t n, int64_t k,
+                   void* workspace, size_t workspace_bytes, void* stream, int* parts_out);
+
+namespace {
+
+// Reduces of the large-hidden decode projections (mfma_gemm.hip): they read the fp32 parts
+// [parts, m, n] that decodeParts writes.
+DeviceKernel k_reduce_qkv("mfma_gemm", "splitk_reduce_qkv_rope_append");
+DeviceKernel k_reduce_res_norm("mfma_gemm", "splitk_reduce_residual_norm");
+constexpr int64_t kResNormMaxN = 4096;  // splitk_reduce_residual_norm: 256 threads x 2 x 8
+constexpr int kResNormMaxSplits = 8;
+
+// Parts of a decode-sized projection whose output is wider than the fused kernels hold: the
+// tiled MFMA GEMM where it runs faster (tiledDecodeLinear), else the skinny partial kernel with
+// `splits` K ranges (at most 8 and k / 64, fewer if the workspace holds fewer). The parts go to
+// workspace [parts, m, n] fp32, summed by the caller's reduce in part order.
+bool decodeTiled(int64_t m, int64_t n) { return tiledDecodeLinear(m, n); }
+
+int64_t skinnyParts(int64_t k, int64_t splits) {
+  int64_t s = splits < 1 ? 1 : splits;
+  if (s > kMaxNormSplits) s = kMaxNormSplits;
+  if (s > k / 64) s = k / 64 > 0 ? k / 64 : 1;
+  return s;
+}
+
+// Workspace bytes of decodeParts: every part it would write, at most 8 (what the reduces sum;
+// the tiled path halves its split count until the parts fit).
+size_t decodePartsBytes(int64_t m, int64_t n, int64_t k, int64_t splits) {
+  int64_t parts = decodeTiled(m, n) ? bf16Splits(m, n, k) : skinnyParts(k, splits);
+  if (parts > kResNormMaxSplits) parts = kResNormMaxSplits;
+  return static_cast<size_t>(parts * m * n) * sizeof(float);
+}
+
+int decodeParts(const char* op, const void* x, const void* w, int64_t m, int64_t n, int64_t k,
+                int64_t splits, void* workspace, size_t workspace_bytes, void* stream,
+                int* parts_out) {
+  if (!aligned16(x) || !aligned16(w)) return bad(op, "x and w must be 16-byte aligned");
+  if (decodeTiled(m, n)) {
+    if (k <= 0 || k % 8 != 0) return bad(op, "reduction size must be a positive multiple of 8");
+    return tiledBf16Parts(x, w, m, n, k, workspace, workspace_bytes, stream, parts_out);
+  }
+  if (int rc = checkSkinny(op, m, k)) return rc;
+  int64_t parts = skinnyParts(k, splits);
+  const size_t part = static_cast<size_t>(m * n) * sizeof(float);
+  while (parts > 1 && workspace_bytes < part * parts) --parts;
+  if (workspace == nullptr || workspace_bytes < part) return bad(op, "workspace too small");
+  *parts_out = static_cast<int>(parts);
+  const unsigned tiles = static_cast<unsigned>((n + kRowTile - 1) / kRowTile);
+  return launch(*k_partial.pick(m), {tiles, static_cast<unsigned>(parts)}, {kThreads}, 0, stream,
+                x, w, static_cast<float*>(workspace), static_cast<int>(m), n, static_cast<int>(k),
+                static_cast<int>(parts));
+}
+
+// q|k|v parts for the skinny path: enough K ranges for about two workgroups per CU.
+int64_t qkvSkinnySplits(int64_t n, int64_t k) {
+  const int64_t tiles = (n + kRowTile - 1) / kRowTile;
+  return skinnyParts(k, (512 + tiles - 1) / tiles);
+}
+
+}  // namespace
 }  // namespace dli::hip
 
 using namespace dli::hip;
@@ -174,6 +235,64 @@ int dli_hip_qkv_rope_append(const void* hidden, const void* norm_weight, const v
                 norm_weight, eps, w_qkv, b_qkv, cos_table, sin_table, max_pos, positions, pos64,
                 q_out, key_pool, value_pool, block_table, block_size, max_blocks,
                 static_cast<int>(batch), static_cast<int>(hidden_size),
+                static_cast<int>(q_heads), static_cast<int>(kv_heads),
+                static_cast<int>(head_dim));
+}
+
+size_t dli_hip_qkv_rope_append_workspace(int64_t batch, int64_t hidden_size, int64_t q_heads,
+                                         int64_t kv_heads, int64_t head_dim) {
+  if (batch <= 0 || batch > 64 || hidden_size <= kMaxLmK || q_heads <= 0 || kv_heads <= 0 ||
+      head_dim <= 0)
+    return 0;
+  const int64_t n = (q_heads + 2 * kv_heads) * head_dim;
+  return decodePartsBytes(batch, n, hidden_size, qkvSkinnySplits(n, hidden_size));
+}
+
+int dli_hip_qkv_rope_append_ws(const void* hidden, const void* norm_weight, const void* w_qkv,
+                               const void* b_qkv, const float* cos_table, const float* sin_table,
+                               int64_t max_pos, const void* positions, int positions_dtype,
+                               void* q_out, void* key_pool, void* value_pool,
+                               const int32_t* block_table, int64_t block_size,
+                               int64_t max_blocks, int64_t batch, int64_t hidden_size,
+                               int64_t q_heads, int64_t kv_heads, int64_t head_dim, float eps,
+                               void* workspace, size_t workspace_bytes, void* stream) {
+  if (hidden_size <= kMaxLmK)
+    return dli_hip_qkv_rope_append(hidden, norm_weight, w_qkv, b_qkv, cos_table, sin_table,
+                                   max_pos, positions, positions_dtype, q_out, key_pool,
+                                   value_pool, block_table, block_size, max_blocks, batch,
+                                   hidden_size, q_heads, kv_heads, head_dim, eps, stream);
+  // a hidden size the fused kernel does not hold in registers: GEMM parts, then one reduce that
+  // adds the bias, rotates q and k and writes q and the cache
+  const char* op = "qkv_rope_append";
+  if (batch <= 0 || batch > 64) return bad(op, "batch rows must be in [1, 64]");
+  if (norm_weight != nullptr)
+    return bad(op, "the RMSNorm prologue needs hidden_size <= 1024 (normalize first)");
+  if (positions == nullptr || (positions_dtype != DLI_I64 && positions_dtype != DLI_I32))
+    return bad(op, "positions (int64/int32 [batch]) are required");
+  if (head_dim <= 0 || head_dim % 2 != 0) return bad(op, "head_dim must be even");
+  if (kv_heads <= 0 || q_heads <= 0 || q_heads > 4096 || kv_heads > 4096)
+    return bad(op, "head counts must be in [1, 4096]");
+  if (block_size <= 0 || max_blocks <= 0) return bad(op, "empty cache geometry");
+  if (max_pos < 0) return bad(op, "negative max_pos");
+  if (w_qkv == nullptr || cos_table == nullptr || sin_table == nullptr || q_out == nullptr ||
+      key_pool == nullptr || value_pool == nullptr || block_table == nullptr)
+    return bad(op, "NULL pointer");
+  if (!aligned16(q_out) || !aligned16(key_pool) || !aligned16(value_pool))
+    return bad(op, "q_out and the cache pools must be 16-byte aligned");
+  const int64_t n = (q_heads + 2 * kv_heads) * head_dim;
+  const size_t need = dli_hip_qkv_rope_append_workspace(batch, hidden_size, q_heads, kv_heads,
+                                                        head_dim);
+  if (workspace == nullptr || workspace_bytes < need) return bad(op, "workspace too small");
+  int parts = 0;
+  if (int rc = decodeParts(op, hidden, w_qkv, batch, n, hidden_size,
+                           qkvSkinnySplits(n, hidden_size), workspace, need, stream, &parts))
+    return rc;
+  const int64_t pairs = batch * n / 2;
+  const int64_t blocks = (pairs + 255) / 256;
+  return launch(k_reduce_qkv, {static_cast<unsigned>(blocks < 4096 ? blocks : 4096)}, {256}, 0,
+                stream, static_cast<const float*>(workspace), parts, b_qkv, cos_table, sin_table,
+                max_pos, positions, positions_dtype == DLI_I64 ? 1 : 0, q_out, key_pool,
+                value_pool, block_table, block_size, max_blocks, static_cast<int>(batch),
                 static_cast<int>(q_heads), static_cast<int>(kv_heads),
                 static_cast<int>(head_dim));
 }
@@ -226,8 +345,28 @@ int dli_hip_linear_residual_norm(const void* x, const void* w, const void* bias,
                                  int splits, void* workspace, size_t workspace_bytes,
                                  void* stream) {
   const char* op = "linear_residual_norm";
-  if (int rc = checkSkinny(op, m, k)) return rc;
   if (norm_weight == nullptr || xn_out == nullptr) return bad(op, "norm_weight and xn_out are required");
+  if (n > kMaxNormN) {
+    // wider than the fused residual kernel holds (a large hidden size): GEMM parts, then one
+    // workgroup per row sums them with the residual and normalizes
+    if (m <= 0 || m > 64) return bad(op, "batch rows must be in [1, 64]");
+    if (n > kResNormMaxN || n % 8 != 0) return bad(op, "n above 1024 must be a multiple of 8, at most 4096");
+    if (splits < 1) return bad(op, "splits must be positive");
+    if (residual == nullptr || h_out == nullptr) return bad(op, "residual and h_out are required");
+    if (!aligned16(residual) || !aligned16(norm_weight) || !aligned16(h_out) ||
+        !aligned16(xn_out) || (bias != nullptr && !aligned16(bias)))
+      return bad(op, "residual, bias, norm_weight, h_out and xn_out must be 16-byte aligned");
+    const size_t need = decodePartsBytes(m, n, k, splits);
+    int parts = 0;
+    if (int rc = decodeParts(op, x, w, m, n, k, splits, workspace,
+                             workspace_bytes < need ? workspace_bytes : need, stream, &parts))
+      return rc;
+    if (parts > kResNormMaxSplits) return bad(op, "too many K parts");
+    return launch(k_reduce_res_norm, {static_cast<unsigned>(m)}, {256}, 0, stream,
+                  static_cast<const float*>(workspace), parts, bias, residual, norm_weight, h_out,
+                  xn_out, static_cast<int>(m), static_cast<int>(n), eps);
+  }
+  if (int rc = checkSkinny(op, m, k)) return rc;
   return partialThenResidual(op, x, w, bias, residual, norm_weight, h_out, xn_out, m, n, k, eps,
                              splits, workspace, workspace_bytes, stream);
 }

@@ -60,6 +60,7 @@ DeviceKernel k_permute16("elementwise", "permute_0213_u128");
 DeviceKernel k_permute2("elementwise", "permute_0213_u16");
 FloatKernels k_rotary("elementwise", "rotary");
 FloatKernels k_argmax("elementwise", "argmax");
+DeviceKernel k_argmax_rows_v4("elementwise", "argmax_f32_rows_v4");
 FloatKernels k_rms_norm("norm", "rms_norm");
 DeviceKernel k_rms_norm_rows("norm", "rms_norm_rows_bf16_k");
 DeviceKernel k_kv_append_tiles("attention", "kv_append_tiles_bf16_k");
@@ -175,6 +176,25 @@ int tiledBf16(const void* x, const void* w, const void* bias,
   return launch(k_splitk_reduce_bf16, {strideBlocks(m * n)}, {256}, 0, stream,
                 static_cast<const float*>(workspace), bias, residual, out, m, n,
                 static_cast<int>(parts));
+}
+
+// The split GEMM of tiledBf16 alone: fp32 parts [parts, m, n] of x w^T in the workspace (K in
+// whole 128-wide slices over at most bf16Splits(m, n, k) parts, as many as the workspace holds,
+// at least one), for a caller's own reduce. *parts_out = the number of parts written.
+int tiledBf16Parts(const void* x, const void* w, int64_t m, int64_t n, int64_t k,
+                   void* workspace, size_t workspace_bytes, void* stream, int* parts_out) {
+  int64_t splits = bf16Splits(m, n, k);
+  const size_t part = static_cast<size_t>(m * n) * sizeof(float);
+  while (splits > 1 && workspace_bytes < part * splits) splits /= 2;
+  if (workspace == nullptr || workspace_bytes < part)
+    return fail(DLI_HIP_EINVAL, "tiled split GEMM: workspace too small");
+  const int64_t per = ((k + splits - 1) / splits + 127) / 128 * 128;
+  const int64_t parts = (k + per - 1) / per;
+  *parts_out = static_cast<int>(parts);
+  return launch(k_mfma_bf16_splitk,
+                {static_cast<unsigned>((n + 63) / 64), static_cast<unsigned>((m + 63) / 64),
+                 static_cast<unsigned>(parts)},
+                {256}, 0, stream, x, w, static_cast<float*>(workspace), m, n, k, per);
 }
 
 
@@ -654,6 +674,10 @@ int dli_hip_argmax(int dtype, const void* x, int64_t* ids, int64_t rows, int64_t
   if (rows < 0 || width <= 0) return badArg("argmax", "rows must be >= 0 and width > 0");
   if (rows == 0) return 0;
   const unsigned blocks = static_cast<unsigned>(rows < 65535 ? rows : 65535);
+  // wide fp32 rows (logits over a vocabulary): the 16-byte-load kernel
+  if (dtype == DLI_F32 && width % 4 == 0 && width >= 4096 &&
+      (reinterpret_cast<uintptr_t>(x) & 15u) == 0)
+    return launch(k_argmax_rows_v4, {blocks}, {1024}, 0, stream, x, ids, rows, width);
   return launch(*ka, {blocks}, {256}, 0, stream, x, ids, rows, width);
 }
 

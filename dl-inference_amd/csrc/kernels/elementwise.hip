@@ -300,6 +300,72 @@ DK_FLOAT_KERNELS(rotary, 256,
 DK_FLOAT_KERNELS(argmax, 256, (const void* x, int64_t* ids, int64_t rows, int64_t width),
                  (x, ids, rows, width))
 
+// argmax of fp32 rows whose width is a multiple of 4 on 16-byte aligned rows (vocabulary-wide
+// logits): one 1024-thread workgroup per row, 16-byte loads, four in flight per thread (64 KB
+// per workgroup, against 8 KB for the generic kernel, whose 152k-wide rows took 67 us for 64
+// rows). Each thread scans its elements in index order with the same rule as argmax_impl, and
+// the reductions keep the lower index of equal maxima: the first index of the maximum.
+extern "C" __global__ void __launch_bounds__(1024)
+    argmax_f32_rows_v4(const float* x, int64_t* ids, int64_t rows, int64_t width) {
+  typedef float f32x4_t __attribute__((ext_vector_type(4)));
+  constexpr int kThreads = 1024, kBatch = 4;
+  __shared__ float best_v[kThreads / kWave];
+  __shared__ int64_t best_i[kThreads / kWave];
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int64_t vecs = width / 4;
+  for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
+    const f32x4_t* row = reinterpret_cast<const f32x4_t*>(x + r * width);
+    float v = -INFINITY;
+    int64_t idx = width;  // sentinel larger than any index
+    for (int64_t j0 = threadIdx.x; j0 < vecs; j0 += kBatch * kThreads) {
+      f32x4_t e[kBatch];
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        const int64_t j = j0 + u * kThreads;
+        e[u] = j < vecs ? *gp(row + j) : f32x4_t{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+      }
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        const int64_t j = j0 + u * kThreads;
+        if (j >= vecs) break;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          if (e[u][c] > v || idx == width) {
+            v = e[u][c];
+            idx = 4 * j + c;
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) {
+      const float ov = __shfl_xor(v, off, kWave);
+      const int64_t oi = __shfl_xor(idx, off, kWave);
+      if (ov > v || (ov == v && oi < idx)) {
+        v = ov;
+        idx = oi;
+      }
+    }
+    __syncthreads();
+    if (lane == 0) {
+      best_v[wave] = v;
+      best_i[wave] = idx;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      float bv = best_v[0];
+      int64_t bi = best_i[0];
+      for (int w = 1; w < kThreads / kWave; ++w) {
+        if (best_v[w] > bv || (best_v[w] == bv && best_i[w] < bi)) {
+          bv = best_v[w];
+          bi = best_i[w];
+        }
+      }
+      ids[r] = bi < width ? bi : 0;
+    }
+  }
+}
+
 extern "C" __global__ void __launch_bounds__(256)
     permute_0213_u128(const void* x, void* out, int64_t n0, int64_t n1, int64_t n2, int64_t row) {
   typedef uint32_t Chunk16 __attribute__((ext_vector_type(4)));

@@ -317,7 +317,12 @@ __device__ __forceinline__ void gemmF32(ASrc A, BSrc B, int64_t R, int64_t Cn, i
 // to its first column, its own K and the full row stride).
 // BK: K columns per slice, 64 or 128 (128 doubles the bytes each workgroup has in flight: the
 // decode-sized kernels, whose few workgroups stream the weights).
-template <int BM, int BN, int BK = 64, class Epi>
+// kStreamB: b (the weights) is read with nontemporal loads, for the decode-sized kernels, whose
+// single row tile reads every weight once (many row tiles re-read them and keep cached loads).
+// Each load instruction covers whole 128-byte lines (16 lanes per 256-byte row slice of a
+// 128-wide slice); a streaming probe over 1 GiB read 6.5-6.9 TB/s that way against 5.8-6.0 with
+// cached loads.
+template <int BM, int BN, int BK = 64, bool kStreamB = false, class Epi>
 __device__ __forceinline__ void gemmBf16(const uint16_t* a, const uint16_t* b, int64_t R,
                                          int64_t Cn, int64_t K, int64_t ld, const Epi& epi) {
   static_assert(BK == 64 || BK == 128, "slice width");
@@ -358,25 +363,31 @@ __device__ __forceinline__ void gemmBf16(const uint16_t* a, const uint16_t* b, i
     const int64_t row = c0 + (t + i * kGemmThreads) / VPR;
     pb[i] = b + (row < Cn ? row : Cn - 1) * ld + kc;
   }
+  auto loadB = [](const uint16_t* p) {
+    if constexpr (kStreamB)
+      return __builtin_nontemporal_load(gp(reinterpret_cast<const U128*>(p)));
+    else
+      return gload16(p);
+  };
   auto fetch = [&](U128 (&xa)[AV], U128 (&xb)[BV], int64_t k0) {
     if (k0 + BK <= K) {
 #pragma unroll
       for (int i = 0; i < AV; ++i) xa[i] = gload16(pa[i] + k0);
 #pragma unroll
-      for (int i = 0; i < BV; ++i) xb[i] = gload16(pb[i] + k0);
+      for (int i = 0; i < BV; ++i) xb[i] = loadB(pb[i] + k0);
     } else {
       const bool in = k0 + kc < K;
 #pragma unroll
       for (int i = 0; i < AV; ++i) xa[i] = in ? gload16(pa[i] + k0) : zero16();
 #pragma unroll
-      for (int i = 0; i < BV; ++i) xb[i] = in ? gload16(pb[i] + k0) : zero16();
+      for (int i = 0; i < BV; ++i) xb[i] = in ? loadB(pb[i] + k0) : zero16();
     }
   };
   auto fetchWhole = [&](U128 (&xa)[AV], U128 (&xb)[BV], int64_t k0) {
 #pragma unroll
     for (int i = 0; i < AV; ++i) xa[i] = gload16(pa[i] + k0);
 #pragma unroll
-    for (int i = 0; i < BV; ++i) xb[i] = gload16(pb[i] + k0);
+    for (int i = 0; i < BV; ++i) xb[i] = loadB(pb[i] + k0);
   };
   auto stash = [&](const U128 (&xa)[AV], const U128 (&xb)[BV], uint16_t* as, uint16_t* bs) {
 #pragma unroll
@@ -1005,9 +1016,9 @@ extern "C" __global__ void __launch_bounds__(kGemmThreads) DK_BF16_OCCUPANCY
                                 int64_t N, int64_t K, int64_t per) {
   const int64_t k0 = static_cast<int64_t>(blockIdx.z) * per;
   const int64_t len = K - k0 < per ? K - k0 : per;
-  gemmBf16<64, 64, 128>(x + k0, w + k0, M, N, len, K,
-                        RowMajorOutBf16OrF32{part + static_cast<int64_t>(blockIdx.z) * M * N,
-                                             nullptr, N, 0, 1});
+  float* const out = part + static_cast<int64_t>(blockIdx.z) * M * N;
+  gemmBf16<64, 64, 128, true>(x + k0, w + k0, M, N, len, K,
+                              RowMajorOutBf16OrF32{out, nullptr, N, 0, 1});
 }
 
 // The same tile and slice shape without a split: decode-sized m (at most 64 rows), bias, bf16 or
@@ -1015,25 +1026,25 @@ extern "C" __global__ void __launch_bounds__(kGemmThreads) DK_BF16_OCCUPANCY
 extern "C" __global__ void __launch_bounds__(kGemmThreads) DK_BF16_OCCUPANCY
     mfma_linear_bf16_stream_t64(const uint16_t* x, const uint16_t* w, const uint16_t* bias,
                                 void* out, int64_t M, int64_t N, int64_t K, int out_f32) {
-  gemmBf16<64, 64, 128>(x, w, M, N, K, K,
-                        RowMajorOutBf16OrF32{out, reinterpret_cast<const bf16*>(bias), N, 0,
-                                             out_f32});
+  gemmBf16<64, 64, 128, true>(x, w, M, N, K, K,
+                              RowMajorOutBf16OrF32{out, reinterpret_cast<const bf16*>(bias), N, 0,
+                                                   out_f32});
 }
 extern "C" __global__ void __launch_bounds__(kGemmThreads) DK_BF16_OCCUPANCY
     mfma_linear_residual_bf16_stream_t64(const uint16_t* x, const uint16_t* w,
                                          const uint16_t* bias, const uint16_t* residual,
                                          uint16_t* out, int64_t M, int64_t N, int64_t K) {
-  gemmBf16<64, 64, 128>(x, w, M, N, K, K,
-                        ResidualOut{reinterpret_cast<bf16*>(out),
-                                    reinterpret_cast<const bf16*>(residual),
-                                    reinterpret_cast<const bf16*>(bias), N});
+  gemmBf16<64, 64, 128, true>(x, w, M, N, K, K,
+                              ResidualOut{reinterpret_cast<bf16*>(out),
+                                          reinterpret_cast<const bf16*>(residual),
+                                          reinterpret_cast<const bf16*>(bias), N});
 }
 
 extern "C" __global__ void __launch_bounds__(kGemmThreads) DK_BF16_OCCUPANCY
     mfma_gate_up_silu_bf16_stream_t64(const uint16_t* x, const uint16_t* w_gate_up, uint16_t* out,
                                       int64_t M, int64_t ffn, int64_t K) {
-  gemmBf16<64, 64, 128>(x, w_gate_up, M, 2 * ffn, K, K,
-                        SwiGluOut{reinterpret_cast<bf16*>(out), ffn});
+  gemmBf16<64, 64, 128, true>(x, w_gate_up, M, 2 * ffn, K, K,
+                              SwiGluOut{reinterpret_cast<bf16*>(out), ffn});
 }
 
 // out[m, n] = bf16(v + bias[n]), or with a residual bf16(residual[m, n] + bf16(v + bias[n])),
@@ -1050,5 +1061,162 @@ extern "C" __global__ void __launch_bounds__(256)
     if (bias != nullptr) v += bf16ToFloat(gp(bias)[e % N]);
     if (residual != nullptr) v = bf16ToFloat(gp(residual)[e]) + Num<bf16>::round(v);
     gp(out)[e] = floatToBf16(v);
+  }
+}
+
+// The split parts of the [q | k | v] projection of decode rows (one new token per row): each
+// value is the sum of its parts in split order plus the bias, rounded to bf16 (the linear
+// output); q and k columns are then rotated as interleaved pairs in fp32 and rounded again
+// (rotary/kernel.py:6-35; no rotation at positions >= max_pos); q goes to q_out [M, Hq, D], k and
+// v into the paged cache at the row's position (k_pool [block, Hkv, slot, D], v_pool [block, Hkv,
+// D, slot]; rows whose position is negative or past the cache write nothing). The arithmetic is
+// that of the qkv_rope_append decode kernels. One thread per (row, column pair): part reads and
+// q / k stores are coalesced along the row.
+extern "C" __global__ void __launch_bounds__(256)
+    splitk_reduce_qkv_rope_append(const float* part, int splits, const uint16_t* bias,
+                                  const float* cos_t, const float* sin_t, int64_t max_pos,
+                                  const void* positions, int pos64, uint16_t* q_out,
+                                  uint16_t* k_pool, uint16_t* v_pool, const int32_t* block_table,
+                                  int64_t block_size, int64_t max_blocks, int M, int Hq, int Hkv,
+                                  int D) {
+  FP_EXACT;
+  const int64_t N = static_cast<int64_t>(Hq + 2 * Hkv) * D;
+  const int64_t pairs = N / 2;
+  const int64_t total = static_cast<int64_t>(M) * pairs;
+  const int64_t plane = static_cast<int64_t>(M) * N;
+  const int64_t q_rows = static_cast<int64_t>(Hq) * D;
+  const int64_t k_rows = static_cast<int64_t>(Hkv) * D;
+  const int64_t capacity = max_blocks * block_size;
+  for (int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; e < total;
+       e += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int m = static_cast<int>(e / pairs);
+    const int64_t n = 2 * (e % pairs);
+    const int64_t pos = loadIndex(positions, pos64, m);
+    if (pos < 0) continue;
+    const int64_t at = static_cast<int64_t>(m) * N + n;
+    f32x2_t s = *gp(reinterpret_cast<const f32x2_t*>(part + at));
+    for (int z = 1; z < splits; ++z) {
+      const f32x2_t p = *gp(reinterpret_cast<const f32x2_t*>(part + z * plane + at));
+      s.x += p.x;
+      s.y += p.y;
+    }
+    if (bias != nullptr) {
+      s.x += bf16ToFloat(gp(bias)[n]);
+      s.y += bf16ToFloat(gp(bias)[n + 1]);
+    }
+    float v0 = Num<bf16>::round(s.x), v1 = Num<bf16>::round(s.y);
+    const bool is_q = n < q_rows;
+    const bool is_k = !is_q && n < q_rows + k_rows;
+    const int64_t local = is_q ? n : (is_k ? n - q_rows : n - q_rows - k_rows);
+    const int head = static_cast<int>(local / D);
+    const int d = static_cast<int>(local % D);
+    if ((is_q || is_k) && pos < max_pos) {
+      const int64_t c = pos * (D / 2) + d / 2;
+      const float cs = gp(cos_t)[c], sn = gp(sin_t)[c];
+      const float r0 = v0 * cs - v1 * sn;
+      const float r1 = v0 * sn + v1 * cs;
+      v0 = r0;
+      v1 = r1;
+    }
+    const uint32_t packed = packBf16x2(v0, v1);
+    if (is_q) {
+      *gp(reinterpret_cast<uint32_t*>(q_out + (static_cast<int64_t>(m) * Hq + head) * D + d)) =
+          packed;
+      continue;
+    }
+    if (pos >= capacity) continue;
+    const int64_t blk = gp(block_table)[m * max_blocks + pos / block_size];
+    const int64_t off = pos % block_size;
+    if (is_k) {
+      *gp(reinterpret_cast<uint32_t*>(k_pool + ((blk * Hkv + head) * block_size + off) * D + d)) =
+          packed;
+    } else {
+      uint16_t* dst = v_pool + ((blk * Hkv + head) * D + d) * block_size + off;
+      *gp(dst) = static_cast<uint16_t>(packed);
+      *gp(dst + block_size) = static_cast<uint16_t>(packed >> 16);
+    }
+  }
+}
+
+// Split parts of a residual projection (o_proj, down_proj) of decode rows, then the RMSNorm that
+// follows it: h = bf16(residual + bf16(sum of the parts in split order + bias)) (the values of
+// splitk_reduce_bf16) and xn = bf16(h * rsqrt(mean(h^2) + eps) * norm_w)
+// (rms_norm/kernel.py:6-14). One workgroup per row, h held in registers between the two; rows of
+// N <= kResNormMaxN columns (N % 8 == 0), at most kResNormMaxSplits parts. Every part of every
+// chunk is requested before the first is added (the index of parts past `splits` is clamped and
+// their sums discarded), so a row costs one memory round trip, not one per part.
+constexpr int kResNormChunks = 2;
+constexpr int kResNormMaxN = kResNormChunks * 256 * 8;
+constexpr int kResNormMaxSplits = 8;
+extern "C" __global__ void __launch_bounds__(256)
+    splitk_reduce_residual_norm(const float* part, int splits, const uint16_t* bias,
+                                const uint16_t* residual, const uint16_t* norm_w,
+                                uint16_t* h_out, uint16_t* xn_out, int M, int N, float eps) {
+  FP_EXACT;
+  __shared__ float wave_sq[256 / kWave];
+  const int m = blockIdx.x;
+  const int chunks = N / 8;
+  const int64_t plane = static_cast<int64_t>(M) * N;
+  uint32_t h[kResNormChunks][4];
+  float sq = 0.f;
+#pragma unroll
+  for (int c = 0; c < kResNormChunks; ++c) {
+    const int i = threadIdx.x + c * 256;
+    if (i >= chunks) break;
+    const int64_t at = static_cast<int64_t>(m) * N + i * 8;
+    f32x4 p[kResNormMaxSplits][2];
+#pragma unroll
+    for (int z = 0; z < kResNormMaxSplits; ++z) {
+      const int64_t zz = z < splits ? z : splits - 1;
+      p[z][0] = *gp(reinterpret_cast<const f32x4*>(part + zz * plane + at));
+      p[z][1] = *gp(reinterpret_cast<const f32x4*>(part + zz * plane + at + 4));
+    }
+    const U128 r = gload16(residual + at);
+    U128 b = U128{0u, 0u, 0u, 0u};
+    if (bias != nullptr) b = gload16(bias + i * 8);
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = p[0][e / 4][e % 4];
+#pragma unroll
+    for (int z = 1; z < kResNormMaxSplits; ++z)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = z < splits ? v[e] + p[z][e / 4][e % 4] : v[e];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      float lo = v[2 * k], hi = v[2 * k + 1];
+      if (bias != nullptr) {
+        lo += __uint_as_float(b[k] << 16);
+        hi += __uint_as_float(b[k] & 0xFFFF0000u);
+      }
+      lo = __uint_as_float(r[k] << 16) + Num<bf16>::round(lo);
+      hi = __uint_as_float(r[k] & 0xFFFF0000u) + Num<bf16>::round(hi);
+      h[c][k] = packBf16x2(lo, hi);
+      const float hl = __uint_as_float(h[c][k] << 16), hh = __uint_as_float(h[c][k] & 0xFFFF0000u);
+      sq += hl * hl;
+      sq += hh * hh;
+    }
+    *gp(reinterpret_cast<U128*>(h_out + at)) = U128{h[c][0], h[c][1], h[c][2], h[c][3]};
+  }
+  sq = waveSum(sq);
+  if (threadIdx.x % kWave == 0) wave_sq[threadIdx.x / kWave] = sq;
+  __syncthreads();
+  float total = 0.f;
+#pragma unroll
+  for (int w = 0; w < 256 / kWave; ++w) total += wave_sq[w];
+  const float inv = 1.0f / sqrtf(total / static_cast<float>(N) + eps);
+#pragma unroll
+  for (int c = 0; c < kResNormChunks; ++c) {
+    const int i = threadIdx.x + c * 256;
+    if (i >= chunks) break;
+    const U128 w = gload16(norm_w + i * 8);
+    uint32_t o[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float hl = __uint_as_float(h[c][k] << 16), hh = __uint_as_float(h[c][k] & 0xFFFF0000u);
+      o[k] = packBf16x2(hl * inv * __uint_as_float(w[k] << 16),
+                        hh * inv * __uint_as_float(w[k] & 0xFFFF0000u));
+    }
+    *gp(reinterpret_cast<U128*>(xn_out + static_cast<int64_t>(m) * N + i * 8)) =
+        U128{o[0], o[1], o[2], o[3]};
   }
 }

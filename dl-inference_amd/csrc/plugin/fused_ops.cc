@@ -64,14 +64,20 @@ class QkvRopeAppendOp final : public Operator {
     if (ctx.kv_cache == nullptr) throw std::invalid_argument("qkv_rope_append missing KV cache");
     KVCacheEntry& e = ctx.kv_cache->reserve(cache_name, DType::BFloat16, m, hkv, d, x.deviceId());
     *out[0] = Tensor::cuda(DType::BFloat16, {m, hq, 1, d}, x.deviceId());
-    check(dli_hip_qkv_rope_append(
+    // hidden sizes above 1024 project through a workspace (K-split parts and one reduce)
+    const std::size_t ws_bytes = dli_hip_qkv_rope_append_workspace(m, hidden, hq, hkv, d);
+    check(dli_hip_qkv_rope_append_ws(
               ptr(x), nw ? ptr(*nw) : nullptr, ptr(w), ptr(b), static_cast<const float*>(ptr(cos)),
               static_cast<const float*>(ptr(sin)), cos.dim(0), ptr(pos), hipDtype(pos.dtype()),
               ptr(*out[0]), ptr(e.key_pool), ptr(e.value_pool),
               static_cast<const std::int32_t*>(ptr(e.block_table)), e.block_size, e.max_blocks, m,
-              hidden, hq, hkv, d, eps, ctx.stream),
+              hidden, hq, hkv, d, eps,
+              ws_bytes ? workspace_.get(ws_bytes, x.deviceId()) : nullptr, ws_bytes, ctx.stream),
           type());
   }
+
+ private:
+  mutable PersistentWorkspace workspace_;
 };
 
 // inputs: x [B, S, H] (normalized), w_qkv [N, H], b_qkv [N], cos, sin [max_pos, D / 2];

@@ -89,6 +89,9 @@ _SIGNATURES = {
     "dli_hip_splitk_workspace": [_i64, _i64, _int],
     "dli_hip_qkv_rope_append": [_c_void_p] * 6 + [_i64, _c_void_p, _int] + [_c_void_p] * 4
     + [_i64] * 7 + [_float, _c_void_p],
+    "dli_hip_qkv_rope_append_workspace": [_i64] * 5,
+    "dli_hip_qkv_rope_append_ws": [_c_void_p] * 6 + [_i64, _c_void_p, _int] + [_c_void_p] * 4
+    + [_i64] * 7 + [_float, _c_void_p, _size, _c_void_p],
     "dli_hip_linear_residual": [_c_void_p] * 5 + [_i64] * 3 + [_int, _c_void_p, _size, _c_void_p],
     "dli_hip_linear_residual_norm": [_c_void_p] * 7 + [_i64] * 3
     + [_float, _int, _c_void_p, _size, _c_void_p],
@@ -119,6 +122,7 @@ _RESTYPES = {
     "dli_hip_conv2d_workspace": _size,
     "dli_hip_paged_attention_workspace": _size,
     "dli_hip_splitk_workspace": _size,
+    "dli_hip_qkv_rope_append_workspace": _size,
     "dli_hip_lm_head_argmax_workspace": _size,
     "dli_hip_decoder_stack_workspace": _size,
 }

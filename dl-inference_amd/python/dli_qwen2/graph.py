@@ -84,19 +84,55 @@ def _reference_nodes(cfg: Qwen2Config, batch: int, nodes: list):
     _node(nodes, "greedy", "argmax", ["logits"], ["next_ids"])
 
 
-def _large_nodes(cfg: Qwen2Config, batch: int, nodes: list, splits: dict,
-                 fused_mlp: bool = False):
+def _large_nodes(cfg: Qwen2Config, batch: int, nodes: list, splits: dict, fused: bool = False):
     """Decode step for hidden sizes the fused norm-prologue kernels do not hold in registers
-    (hidden > 1024, e.g. the Qwen2-7B shape): the reference node sequence with o_proj and
-    down_proj each fused with their residual add (linear_residual, split-K for down_proj).
-    Attention over the paged cache runs on the MFMA decode kernel for head_dim 64 or 128.
-    fused_mlp: gate_proj, up_proj, act_fn and mul as one gate_up_silu node over the interleaved
-    mlp.gate_up_proj.weight (pack_large_weights; the GPU plugin's operator, same rounding)."""
+    (hidden > 1024, e.g. the Qwen2-7B shape). Attention over the paged cache runs on the MFMA
+    decode kernel for head_dim 64 or 128.
+    fused=False: the reference node sequence with o_proj and down_proj each fused with their
+    residual add (linear_residual), which the ATen CPU plugin also runs.
+    fused=True (the GPU plugin's operators, same rounding points): per layer
+    qkv_rope_append (q|k|v projection over the packed self_attn.qkv_proj.{weight,bias}, bias,
+    RoPE, q out, k and v into the cache) -> paged_attention -> linear_residual_norm (o_proj +
+    residual + post_attention_layernorm) -> gate_up_silu (over the interleaved
+    mlp.gate_up_proj.weight) -> linear_residual_norm (down_proj + residual + the next layer's
+    input_layernorm, or model.norm after the last layer); the first layer's input_layernorm is
+    one rms_norm node (pack_large_weights packs the weights)."""
     h = "hidden_states"
     q_w = cfg.heads * cfg.head_dim
+    if fused:
+        _node(nodes, "model.layers.0.input_layernorm", "rms_norm",
+              [h, "model.layers.0.input_layernorm.weight"], ["layers_0_input_norm"],
+              {"eps": cfg.eps})
     for i in range(cfg.layers):
         p = f"model.layers.{i}"
         t = f"layers_{i}"
+        if fused:
+            last = i + 1 == cfg.layers
+            next_norm = "model.norm.weight" if last else \
+                f"model.layers.{i + 1}.input_layernorm.weight"
+            next_xn = "norm_hidden" if last else f"layers_{i + 1}_input_norm"
+            _node(nodes, f"{p}.self_attn.qkv_rope_append", "qkv_rope_append",
+                  [f"{t}_input_norm", f"{p}.self_attn.qkv_proj.weight",
+                   f"{p}.self_attn.qkv_proj.bias", "rotary_cos", "rotary_sin", "positions"],
+                  [f"{t}_q_rotary"],
+                  {"kv_cache": f"layer_{i}", "q_heads": cfg.heads, "kv_heads": cfg.kv_heads,
+                   "head_dim": cfg.head_dim, "eps": cfg.eps})
+            _node(nodes, f"{p}.self_attn.attention", "paged_attention",
+                  [f"{t}_q_rotary", "positions"], [f"{t}_attention"], {"kv_cache": f"layer_{i}"})
+            _node(nodes, f"{p}.self_attn.merge", "reshape", [f"{t}_attention"],
+                  [f"{t}_attention_merged"], {"shape": [batch, q_w]})
+            _node(nodes, f"{p}.self_attn.o_proj", "linear_residual_norm",
+                  [f"{t}_attention_merged", f"{p}.self_attn.o_proj.weight", h,
+                   f"{p}.post_attention_layernorm.weight"],
+                  [f"{t}_after_attention", f"{t}_post_attention_norm"],
+                  {"splits": splits.get("o", 1), "eps": cfg.eps})
+            _node(nodes, f"{p}.mlp.gate_up", "gate_up_silu",
+                  [f"{t}_post_attention_norm", f"{p}.mlp.gate_up_proj.weight"], [f"{t}_gated"])
+            _node(nodes, f"{p}.mlp.down_proj", "linear_residual_norm",
+                  [f"{t}_gated", f"{p}.mlp.down_proj.weight", f"{t}_after_attention", next_norm],
+                  [f"{t}_output", next_xn], {"splits": splits.get("down", 1), "eps": cfg.eps})
+            h = f"{t}_output"
+            continue
         _node(nodes, f"{p}.input_layernorm", "rms_norm", [h, f"{p}.input_layernorm.weight"],
               [f"{t}_input_norm"], {"eps": cfg.eps})
         for proj, heads in (("q", cfg.heads), ("k", cfg.kv_heads), ("v", cfg.kv_heads)):
@@ -119,22 +155,19 @@ def _large_nodes(cfg: Qwen2Config, batch: int, nodes: list, splits: dict,
         _node(nodes, f"{p}.post_attention_layernorm", "rms_norm",
               [f"{t}_after_attention", f"{p}.post_attention_layernorm.weight"],
               [f"{t}_post_attention_norm"], {"eps": cfg.eps})
-        if fused_mlp:
-            _node(nodes, f"{p}.mlp.gate_up", "gate_up_silu",
-                  [f"{t}_post_attention_norm", f"{p}.mlp.gate_up_proj.weight"], [f"{t}_gated"])
-        else:
-            _node(nodes, f"{p}.mlp.gate_proj", "linear",
-                  [f"{t}_post_attention_norm", f"{p}.mlp.gate_proj.weight"], [f"{t}_gate"])
-            _node(nodes, f"{p}.mlp.up_proj", "linear",
-                  [f"{t}_post_attention_norm", f"{p}.mlp.up_proj.weight"], [f"{t}_up"])
-            _node(nodes, f"{p}.mlp.act_fn", "silu", [f"{t}_gate"], [f"{t}_silu"])
-            _node(nodes, f"{p}.mlp.mul", "mul", [f"{t}_silu", f"{t}_up"], [f"{t}_gated"])
+        _node(nodes, f"{p}.mlp.gate_proj", "linear",
+              [f"{t}_post_attention_norm", f"{p}.mlp.gate_proj.weight"], [f"{t}_gate"])
+        _node(nodes, f"{p}.mlp.up_proj", "linear",
+              [f"{t}_post_attention_norm", f"{p}.mlp.up_proj.weight"], [f"{t}_up"])
+        _node(nodes, f"{p}.mlp.act_fn", "silu", [f"{t}_gate"], [f"{t}_silu"])
+        _node(nodes, f"{p}.mlp.mul", "mul", [f"{t}_silu", f"{t}_up"], [f"{t}_gated"])
         _node(nodes, f"{p}.mlp.down_proj", "linear_residual",
               [f"{t}_gated", f"{p}.mlp.down_proj.weight", f"{t}_after_attention"],
               [f"{t}_output"], {"splits": splits.get("down", 1)})
         h = f"{t}_output"
-    _node(nodes, "model.norm", "rms_norm", [h, "model.norm.weight"], ["norm_hidden"],
-          {"eps": cfg.eps})
+    if not fused:
+        _node(nodes, "model.norm", "rms_norm", [h, "model.norm.weight"], ["norm_hidden"],
+              {"eps": cfg.eps})
     _node(nodes, "lm_head", "linear", ["norm_hidden", "lm_head.weight"], ["logits"],
           {"out_dtype": "float32"})
     _node(nodes, "greedy", "argmax", ["logits"], ["next_ids"])
@@ -220,18 +253,17 @@ def uses_large_graph(cfg: Qwen2Config, fused: bool) -> bool:
 def build_decode_graph(cfg: Qwen2Config, batch: int, fused: bool = True,
                        splits: dict | None = None, logits_dtype: str = "float32",
                        stack: bool = False, check_status: bool = False,
-                       large_fused_mlp: bool = False) -> "dli.Graph":
+                       large_fused: bool = False) -> "dli.Graph":
     """fused=False: the reference's node sequence; fused=True: five launches per layer;
     stack=True (with fused): all layers in one decoder_stack node (check_status: the node waits
     for its launch and fails if a workgroup gave up waiting; for tests, not for capture). With
     fused=True and a hidden size above 1024 (the Qwen2-7B shape) the step is the large-hidden
-    graph instead (_large_nodes, with its MLP as one gate_up_silu node when large_fused_mlp),
-    whatever `stack` says."""
+    graph instead (_large_nodes; large_fused selects its GPU form), whatever `stack` says."""
     nodes: list = []
     _node(nodes, "model.embed_tokens", "embedding", ["input_ids", "model.embed_tokens.weight"],
           ["hidden_states"])
     if uses_large_graph(cfg, fused):
-        _large_nodes(cfg, batch, nodes, splits or large_splits(batch), large_fused_mlp)
+        _large_nodes(cfg, batch, nodes, splits or large_splits(batch), large_fused)
         graph = {"format": "dli.graph.v1", "model_type": "qwen2_decode_large",
                  "inputs": INPUTS, "outputs": OUTPUTS, "nodes": nodes}
         return dli.Graph.from_json(json.dumps(graph))
@@ -380,10 +412,16 @@ def interleave_gate_up(gate: torch.Tensor, up: torch.Tensor, block: int = 16) ->
 
 
 def pack_large_weights(cfg: Qwen2Config, weights: dict) -> dict:
-    """The large-hidden graph's fused MLP weight: mlp.gate_up_proj.weight (16-row interleave of
-    gate and up) in place of gate_proj and up_proj."""
+    """The packed tensors of the large-hidden graph's GPU form, in place of the ones they join:
+    self_attn.qkv_proj.{weight,bias} ([q|k|v] rows) and mlp.gate_up_proj.weight (16-row
+    interleave of gate and up)."""
     out = dict(weights)
     for i in range(cfg.layers):
+        a = f"model.layers.{i}.self_attn"
+        out[f"{a}.qkv_proj.weight"] = torch.cat(
+            [out.pop(f"{a}.{x}_proj.weight") for x in "qkv"], 0).contiguous()
+        out[f"{a}.qkv_proj.bias"] = torch.cat(
+            [out.pop(f"{a}.{x}_proj.bias") for x in "qkv"], 0).contiguous()
         p = f"model.layers.{i}.mlp"
         out[f"{p}.gate_up_proj.weight"] = interleave_gate_up(out.pop(f"{p}.gate_proj.weight"),
                                                               out.pop(f"{p}.up_proj.weight"))

@@ -27,19 +27,19 @@ class DecodeSession:
         self.stack = fused and stack and not uses_large_graph(cfg, fused)
         self.engine = engine or dli.Engine().load_plugin()
         self.engine.configure_kv_cache(block_size=block_size, max_seq_len=max_seq_len)
-        # the large-hidden graph's MLP as one gate_up_silu node on the GPU plugin (the ATen CPU
-        # plugin runs the reference's MLP nodes)
-        large_mlp = uses_large_graph(cfg, fused) and device != "cpu" and not prefill
+        # the large-hidden graph's GPU form (fused q|k|v, residual + RMSNorm and MLP nodes of
+        # the GPU plugin; the ATen CPU plugin runs the reference's nodes)
+        large_fused = uses_large_graph(cfg, fused) and device != "cpu" and not prefill
         self.graph = build_decode_graph(cfg, batch, fused=fused, splits=splits,
                                         logits_dtype=logits_dtype, stack=stack,
-                                        check_status=check_status, large_fused_mlp=large_mlp)
+                                        check_status=check_status, large_fused=large_fused)
         # prefill=True: generate() runs the prompt through one prefill graph (the layers over
         # [B, S] tokens at once), which reads the unpacked q/k/v and gate/up weights
         self.prefill = prefill
         self._prefill_graphs: dict = {}
         if fused and not uses_large_graph(cfg, fused):
             tensors = pack_fused_weights(cfg, weights, drop_unfused=not prefill)
-        elif large_mlp:
+        elif large_fused:
             tensors = pack_large_weights(cfg, weights)
         else:
             tensors = dict(weights)

@@ -300,6 +300,26 @@ int dli_hip_qkv_rope_append(const void* hidden, const void* norm_weight, const v
                             int64_t batch, int64_t hidden_size, int64_t q_heads, int64_t kv_heads,
                             int64_t head_dim, float eps, void* stream);
 
+/* dli_hip_qkv_rope_append for any hidden size, with a caller workspace of
+ * dli_hip_qkv_rope_append_workspace() bytes (0 when hidden <= 1024, where it is the call above).
+ * Above 1024 (a large hidden size such as the Qwen2-7B geometry's 3584) norm_weight must be
+ * NULL (the RMSNorm is a node of its own, or the previous dli_hip_linear_residual_norm), and the
+ * projection runs as K-split fp32 parts in the workspace (the tiled MFMA GEMM from 33 rows, the
+ * skinny kernels below) followed by one reduce that sums the parts in split order, adds the
+ * bias, rotates q and k, writes q and puts k and v into the cache: the same values as the call
+ * above and as the reference's q/k/v_proj, rotary_embedding and attention KV-append nodes
+ * (export.py:280-349; rotary/kernel.py:6-35). Calls sharing a workspace must be ordered. */
+size_t dli_hip_qkv_rope_append_workspace(int64_t batch, int64_t hidden_size, int64_t q_heads,
+                                         int64_t kv_heads, int64_t head_dim);
+int dli_hip_qkv_rope_append_ws(const void* hidden, const void* norm_weight, const void* w_qkv,
+                               const void* b_qkv, const float* cos_table, const float* sin_table,
+                               int64_t max_pos, const void* positions, int positions_dtype,
+                               void* q_out, void* key_pool, void* value_pool,
+                               const int32_t* block_table, int64_t block_size,
+                               int64_t max_blocks, int64_t batch, int64_t hidden_size,
+                               int64_t q_heads, int64_t kv_heads, int64_t head_dim, float eps,
+                               void* workspace, size_t workspace_bytes, void* stream);
+
 /* out = residual + (x W^T + b), the linear output rounded before the add. Replaces o_proj +
  * attention_residual and down_proj + mlp_residual (export.py:366-376, 416-424). splits in
  * [2, min(8, k / 64)] splits K over workgroups: each stores a partial tile in the workspace and
@@ -316,10 +336,14 @@ int dli_hip_linear_residual(const void* x, const void* w, const void* bias, cons
                             void* workspace, size_t workspace_bytes, void* stream);
 
 /* h_out = residual + (x W^T + b) as above, and xn_out = rms_norm(h_out) * norm_weight, both
- * [m, n] (n <= 1024). Replaces o_proj + attention_residual + post_attention_layernorm, and
- * down_proj + mlp_residual + the next layer's input_layernorm (or model.norm after the last
- * layer) (export.py:366-424; rms_norm/kernel.py:6-14). Always uses the workspace; splits in
- * [1, min(8, k / 64)]. */
+ * [m, n]. Replaces o_proj + attention_residual + post_attention_layernorm, and down_proj +
+ * mlp_residual + the next layer's input_layernorm (or model.norm after the last layer)
+ * (export.py:366-424; rms_norm/kernel.py:6-14). Always uses the workspace; splits in
+ * [1, min(8, k / 64)]. n <= 1024: the fused residual kernels. 1024 < n <= 4096 (n % 8 == 0; a
+ * large hidden size): K-split fp32 parts (the tiled MFMA GEMM from 33 rows, splitting K as far as
+ * the workspace of `splits` holds, up to its own choice; the skinny kernels with `splits` parts
+ * below), then one workgroup per row sums them in split order with the bias and the residual and
+ * normalizes; residual, bias, norm_weight and both outputs 16-byte aligned. */
 int dli_hip_linear_residual_norm(const void* x, const void* w, const void* bias,
                                  const void* residual, const void* norm_weight, void* h_out,
                                  void* xn_out, int64_t m, int64_t n, int64_t k, float eps,

@@ -45,7 +45,22 @@ def rope_tables(max_pos, d, theta=10000.0):
     (40, 256, 4, 2, None),    # 33..64 rows
 ])
 def test_qkv_rope_append(B, H, hq, hkv, positions, norm):
-    d = 64
+    _check_qkv_rope_append(B, H, hq, hkv, 64, positions, norm)
+
+
+@pytest.mark.parametrize("B,H,hq,hkv,d,positions", [
+    (64, 3584, 28, 4, 128, None),  # Qwen2-7B geometry at 64 rows: tiled GEMM parts + reduce
+    (8, 3584, 28, 4, 128, None),   # ... at 8 rows: skinny parts
+    (40, 1152, 9, 3, 128, None),   # 33..64 rows, 1920 q|k|v columns
+    (3, 2048, 4, 2, 64, [0, 191, 64]),
+])
+def test_qkv_rope_append_large_hidden(B, H, hq, hkv, d, positions):
+    """Hidden sizes above 1024 (no RMSNorm prologue: the norm is a node of its own): K-split
+    parts in the op's workspace, then the reduce that adds the bias, rotates and writes."""
+    _check_qkv_rope_append(B, H, hq, hkv, d, positions, False)
+
+
+def _check_qkv_rope_append(B, H, hq, hkv, d, positions, norm):
     n = (hq + 2 * hkv) * d
     if positions is None:
         positions = [(7 * b + 3) % 250 for b in range(B)]
@@ -100,7 +115,16 @@ CASES = [  # B, N, K, splits, bias
 ]
 
 
-@pytest.mark.parametrize("B,N,K,splits,bias", CASES)
+@pytest.mark.parametrize("B,N,K,splits,bias", CASES + [
+    # n > 1024 (a large hidden size): GEMM parts, then one workgroup per row adds the residual
+    # and normalizes; tiled parts from 33 rows, skinny parts below
+    (64, 3584, 3584, 4, False),
+    (64, 3584, 4864, 4, True),
+    (40, 1032, 1000, 4, True),
+    (8, 3584, 3584, 2, True),
+    (1, 2048, 512, 1, False),
+    (16, 4096, 1024, 3, True),
+])
 def test_linear_residual_norm(B, N, K, splits, bias):
     x, w, res = rand((B, K), 10), rand((N, K), 11, 0.03), rand((B, N), 12)
     nw = (1 + rand((N,), 13, 0.1).float()).to(torch.bfloat16)

@@ -80,14 +80,21 @@ def test_invalid_arguments_are_rejected_with_a_message():
 
 def test_fused_decode_entry_points_reject_invalid_arguments():
     lib = hip.load()
-    # residual + RMSNorm kernel holds a row of at most 1024 columns
+    # the fused residual + RMSNorm kernel holds rows of up to 1024 columns, the per-row reduce
+    # of the large-hidden path rows of up to 4096 (multiples of 8)
     assert lib.dli_hip_linear_residual_norm(None, None, None, None, None, None, None, 2, 64, 64,
                                             1e-6, 1, None, 0, None) == -1
     assert b"norm_weight and xn_out are required" in lib.dli_hip_last_error()
     fake = ctypes.c_void_p(256)  # never dereferenced: the size check comes first
+    assert lib.dli_hip_linear_residual_norm(None, None, None, None, fake, None, fake, 2, 5000, 64,
+                                            1e-6, 1, None, 0, None) == -1
+    assert b"at most 4096" in lib.dli_hip_last_error()
     assert lib.dli_hip_linear_residual_norm(None, None, None, None, fake, None, fake, 2, 2048, 64,
                                             1e-6, 1, None, 0, None) == -1
-    assert b"n must be in [1, 1024]" in lib.dli_hip_last_error()
+    assert b"residual and h_out are required" in lib.dli_hip_last_error()
+    assert lib.dli_hip_linear_residual_norm(None, None, None, None, fake, None, fake, 65, 2048, 64,
+                                            1e-6, 1, None, 0, None) == -1
+    assert b"batch rows" in lib.dli_hip_last_error()
     assert lib.dli_hip_linear_residual_norm(None, None, None, None, fake, None, fake, 2, 64, 128,
                                             1e-6, 3, None, 0, None) == -1  # 3 > k / 64
     assert b"splits must be in" in lib.dli_hip_last_error()
@@ -121,6 +128,20 @@ def test_fused_decode_entry_points_reject_invalid_arguments():
     assert lib.dli_hip_qkv_rope_append(None, None, None, None, None, None, 8, None, hip.I64, None,
                                        None, None, None, 64, 1, 2, 64, 2, 1, 16, 1e-6, None) == -1
     assert b"positions" in lib.dli_hip_last_error()
+    # hidden above 1024: no RMSNorm prologue, and the parts need a workspace
+    assert lib.dli_hip_qkv_rope_append_ws(fake, fake, fake, fake, fake, fake, 8, fake, hip.I64,
+                                          fake, fake, fake, fake, 64, 1, 2, 3584, 28, 4, 128,
+                                          1e-6, None, 0, None) == -1
+    assert b"normalize first" in lib.dli_hip_last_error()
+    assert lib.dli_hip_qkv_rope_append_ws(fake, None, fake, fake, fake, fake, 8, fake, hip.I64,
+                                          fake, fake, fake, fake, 64, 1, 2, 3584, 28, 4, 128,
+                                          1e-6, None, 0, None) == -1
+    assert b"workspace too small" in lib.dli_hip_last_error()
+    assert lib.dli_hip_qkv_rope_append_workspace(64, 896, 14, 2, 64) == 0  # the fused kernel
+    # 64 rows: the tiled GEMM's parts (2 K ranges over 72 column tiles of the 4608 q|k|v rows)
+    assert lib.dli_hip_qkv_rope_append_workspace(64, 3584, 28, 4, 128) == 2 * 64 * 4608 * 4
+    # 8 rows: two skinny K ranges over 288 row tiles
+    assert lib.dli_hip_qkv_rope_append_workspace(8, 3584, 28, 4, 128) == 2 * 8 * 4608 * 4
     # partials [splits, m, n] fp32 (256-byte aligned) + one arrival counter per 16-row tile
     assert lib.dli_hip_splitk_workspace(896, 32, 4) == 4 * 32 * 896 * 4 + 256
 

@@ -211,6 +211,25 @@ def test_attention_kv_cache_device_positions():
         assert_close(out[b:b + 1], ops.attention(to_np(q[b:b + 1]), kk, vv, causal=True), "bfloat16")
 
 
+@pytest.mark.parametrize("dtype,rows,width", [("float32", 3, 1000), ("bfloat16", 5, 4100),
+                                               ("float32", 64, 152064), ("float32", 7, 4096),
+                                               ("float32", 2, 4098)])
+def test_argmax_first_index_of_maximum(dtype, rows, width):
+    """torch.argmax's rule (first index of the maximum) on integer-valued rows with the maximum
+    planted several times per row: inside one 16-byte vector, across threads and at both ends.
+    Wide fp32 rows take the 16-byte-load kernel, the others the generic one."""
+    g = torch.Generator().manual_seed(rows * 7 + width)
+    x = torch.randint(-1000, 1000, (rows, width), generator=g).float()
+    for r in range(rows):
+        a = (r * 977) % (width - 1)
+        for p in (a, a + 1, (r * 4099 + 5) % width, width - 1 - r % 3):  # a, a + 1: one vector
+            x[r, p] = 5000.0
+    x[0, 0] = x[0, width - 1] = 6000.0
+    x = x.to(TORCH_DTYPES[dtype])
+    out = run_op("argmax", {"x": x.to(DEV)})["output"]
+    assert torch.equal(out.cpu(), torch.argmax(x.float(), dim=-1))
+
+
 def test_reshape_is_a_view():
     x = rand((4, 6), "float32", 30)
     out = run_op("reshape", {"x": x}, attrs={"shape": [3, -1]})["output"]
