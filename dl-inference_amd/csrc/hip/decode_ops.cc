@@ -574,13 +574,15 @@ std::atomic<int> forced_splits{[] {
 }()};
 }  // namespace
 
-int decodeAttentionSplits(int64_t pairs, int64_t max_blocks, int cus) {
+// Splits of `units` workgroup units whose blocks are dealt over `wph` waves per head: about one
+// workgroup per CU, no more splits than groups of wph blocks, never fewer than the per-lane
+// block ids of a wave (64) allow.
+int decodeAttentionSplits(int64_t units, int64_t max_blocks, int cus, int wph) {
   const int forced = forced_splits.load(std::memory_order_relaxed);
-  int64_t splits = forced > 0 ? forced : (pairs > 0 ? cus / pairs : 1);
-  // no more splits than wave groups of blocks, never fewer than the block ids allow
-  const int64_t useful = (max_blocks + kDecWaves - 1) / kDecWaves;
+  int64_t splits = forced > 0 ? forced : (units > 0 ? cus / units : 1);
+  const int64_t useful = (max_blocks + wph - 1) / wph;
   if (splits > useful) splits = useful;
-  const int64_t needed = (max_blocks + kDecWaves * 64 - 1) / (kDecWaves * 64);
+  const int64_t needed = (max_blocks + wph * 64 - 1) / (wph * 64);
   if (splits < needed) splits = needed;
   if (splits < 1) splits = 1;
   return static_cast<int>(splits);
@@ -598,7 +600,11 @@ int decodeAttentionFast(int dtype, const void* q, const void* key_pool, const vo
   if (batch * kv_heads > 65535) return 1;
   int cus = 0;
   if (int rc = computeUnits(&cus)) return rc;
-  const int splits = decodeAttentionSplits(batch * kv_heads, max_blocks, cus);
+  // head_dim 128: every kv head of a sequence in one workgroup when they divide its 8 waves (the
+  // workgroup then reads whole cache blocks of the pools)
+  const int hpw = head_dim == 128 && kDecWaves % kv_heads == 0 ? static_cast<int>(kv_heads) : 1;
+  const int splits =
+      decodeAttentionSplits(batch * kv_heads / hpw, max_blocks, cus, kDecWaves / hpw);
   if (splits > kMaxDecodeSplits) return 1;
   const int64_t rows = batch * q_heads;
   const size_t need = partialBytes(rows, head_dim) + static_cast<size_t>(rows) * sizeof(unsigned);
@@ -613,12 +619,12 @@ int decodeAttentionFast(int dtype, const void* q, const void* key_pool, const vo
   const float scale_log2 = scale * 1.4426950408889634f;
   if (head_dim == 128)
     return launch(k_dec_attn128,
-                  {static_cast<unsigned>(splits), static_cast<unsigned>(batch * kv_heads)},
+                  {static_cast<unsigned>(splits), static_cast<unsigned>(batch * kv_heads / hpw)},
                   {kDecWaves * 64}, 0, stream, static_cast<const uint16_t*>(q),
                   static_cast<const uint16_t*>(key_pool), static_cast<const uint16_t*>(value_pool),
                   block_table, positions, pos64, past, ws_ml, ws_o, counters,
                   static_cast<uint16_t*>(out), static_cast<int>(q_heads),
-                  static_cast<int>(kv_heads), max_blocks, splits, scale_log2);
+                  static_cast<int>(kv_heads), max_blocks, splits, scale_log2, hpw);
   return launch(k_dec_attn, {static_cast<unsigned>(splits), static_cast<unsigned>(batch * kv_heads)},
                 {kDecWaves * 64}, 0, stream, static_cast<const uint16_t*>(q),
                 static_cast<const uint16_t*>(key_pool), static_cast<const uint16_t*>(value_pool),

@@ -25,10 +25,11 @@ int check(int hip_status, const char* what);
 int requireRuntime();
 // Compute units of the current device (cached per device).
 int computeUnits(int* count);
-// Key-range splits per (sequence, kv head) of MFMA decode attention: about `cus` workgroups over
-// all pairs, no more splits than groups of 8 cache blocks, or the count set with
+// Key-range splits per workgroup unit of MFMA decode attention (a (sequence, kv head) pair, or a
+// group of kv heads of one sequence): about `cus` workgroups over all units, no more splits than
+// groups of wph cache blocks (wph: waves per kv head), or the count set with
 // dli_hip_set_decode_attention_splits (or DLI_ATTN_SPLITS) when one is set.
-int decodeAttentionSplits(int64_t pairs, int64_t max_blocks, int cus);
+int decodeAttentionSplits(int64_t units, int64_t max_blocks, int cus, int wph = 8);
 
 // A kernel by name inside one embedded code object; resolved once per device.
 class DeviceKernel {

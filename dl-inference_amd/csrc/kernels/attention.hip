@@ -259,7 +259,8 @@ extern "C" __global__ void __launch_bounds__(dk::kDecThreads)
 }
 
 // ---------------------------------------------------------------------------------------------
-// Decode attention for head_dim 128 (decode_attention_d128.h): grid (splits, batch * kv_heads).
+// Decode attention for head_dim 128 (decode_attention_d128.h): grid (splits, batch * kv_heads /
+// hpw), hpw kv heads per workgroup (1, or kv_heads when it divides 8).
 // ---------------------------------------------------------------------------------------------
 #include "decode_attention_d128.h"
 
@@ -268,10 +269,10 @@ extern "C" __global__ void __launch_bounds__(dk::kD128Threads)
                           const int32_t* block_table, const void* positions, int pos64,
                           int64_t past, float* ws_ml, float* ws_o, unsigned* counters,
                           uint16_t* out, int Hq, int Hkv, int64_t max_blocks, int splits,
-                          float scale_log2) {
+                          float scale_log2, int hpw) {
   __shared__ dk::DecodeAttn128Lds lds;
   const dk::DecodeAttn128Args a{q,     k_pool, v_pool,   block_table, positions, pos64,
                                 past,  ws_ml,  ws_o,     counters,    out,       Hq,
                                 Hkv,   max_blocks, splits, scale_log2};
-  dk::decodeAttention128Unit(a, blockIdx.x, blockIdx.y, lds);
+  dk::decodeAttention128Unit(a, blockIdx.x, blockIdx.y, hpw, lds);
 }

@@ -5,10 +5,15 @@
 // row per sequence at position positions[b] (keys [0, positions[b]] visible; the new token's
 // key and value are already in the cache).
 //
-// Same decomposition as the head_dim-64 kernel (decode_attention.h): one workgroup of 8 waves
-// per (sequence, kv head, split); the query heads of a GQA group form the 16 columns of the
-// MFMA; a sequence's 64-key cache blocks are dealt round-robin over the waves of all its
-// splits. A 64-key block of a 128-dim head is 32 KB of K and V, so a wave works through each
+// One workgroup of 8 waves per (sequence, group of kv heads, split): hpw kv heads per
+// workgroup, 8 / hpw waves per head (hpw = 1: all eight on one head, the head_dim-64 kernel's
+// decomposition). The query heads of a GQA group form the 16 columns of the MFMA; a sequence's
+// 64-key cache blocks are dealt round-robin over the waves of one head in all its splits.
+// With hpw = Hkv (the host's choice when Hkv divides 8) a workgroup reads every kv head of the
+// same cache blocks, which sit next to each other in the pools ([block, Hkv, ...]): contiguous
+// 4 x 16 KB per block at the Qwen2-7B geometry. A streaming probe read that order at 5.6 TB/s
+// against 4.9 TB/s for one head's 16 KB out of every 64 KB, the order of one head per
+// workgroup. A 64-key block of a 128-dim head is 32 KB of K and V, so a wave works through each
 // block as two 32-key halves (one half in registers while the next half's loads are in
 // flight) instead of whole blocks:
 //   S = K Q^T   four MFMAs per 16 keys (v_mfma_f32_16x16x32_bf16, 32 dims each); the A rows
@@ -123,7 +128,7 @@ struct DecodeAttn128Lds {
   float sm[kD128Waves][16];
   float sl[kD128Waves][16];
   float so[kD128Waves][kD128][17];
-  int is_last;
+  int is_last[kD128Waves];
 };
 
 struct DecodeAttn128Args {
@@ -144,19 +149,25 @@ struct DecodeAttn128Args {
   float scale_log2;
 };
 
-// Unit `split` of pair (b, kvh) = `pair`. Wave w of split s takes cache blocks s * 8 + w,
-// + splits * 8, ... of the sequence's L = positions[b] + 1 keys. Returns after writing the
-// output (one split) or its partial (and, in the last unit of the pair to arrive, the merge).
+// Unit `split` of kv heads [h0, h0 + hpw) of sequence b (unit = (b Hkv + h0) / hpw). Wave w
+// serves head h0 + w / wph (wph = 8 / hpw waves per head) and, as sub-wave u = w % wph of split
+// s, takes cache blocks s * wph + u, + splits * wph, ... of the sequence's L = positions[b] + 1
+// keys. Returns after writing each head's output (one split) or its partials (and, in the last
+// unit of a (sequence, kv head) pair to arrive, that pair's merge).
 __device__ __forceinline__ void decodeAttention128Unit(const DecodeAttn128Args& a, int split,
-                                                       int pair, DecodeAttn128Lds& s) {
+                                                       int unit, int hpw, DecodeAttn128Lds& s) {
   FP_EXACT;
   const int tid = freshThreadIdx();
   const int lane = tid % kWave, wave = tid / kWave;
   const int r = lane % 16, g = lane / 16;
-  const int b = pair / a.Hkv, kvh = pair % a.Hkv;
+  const int wph = kD128Waves / hpw;
+  const int b = (unit * hpw) / a.Hkv, h0 = (unit * hpw) % a.Hkv;
+  // uniform over the wave: the head's pool offsets and the block walk stay scalar
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  const int kvh = h0 + wave_u / wph;
   const int group = a.Hq / a.Hkv;
-  const int64_t stride = static_cast<int64_t>(a.splits) * kD128Waves;
-  const int64_t first = static_cast<int64_t>(split) * kD128Waves + wave;
+  const int64_t stride = static_cast<int64_t>(a.splits) * wph;
+  const int64_t first = static_cast<int64_t>(split) * wph + wave_u % wph;
   // The wave's cache block ids, one per lane (lane k holds the id of the wave's k-th block; the
   // split count keeps that below 64), loaded once: a block id read in the loop made every fetch
   // wait, in order, for the loads issued before it.
@@ -209,19 +220,19 @@ __device__ __forceinline__ void decodeAttention128Unit(const DecodeAttn128Args& 
 #pragma unroll
     for (int e = 0; e < 4; ++e) s.so[wave][d * 16 + 4 * g + e][r] = st.o[d][e];
   __syncthreads();
-  for (int idx = threadIdx.x; idx < group * kD128; idx += kD128Threads) {
-    const int hl = idx / kD128, d = idx % kD128;
+  // merge each head's wph waves in wave order
+  for (int idx = threadIdx.x; idx < hpw * group * kD128; idx += kD128Threads) {
+    const int hw = idx / (group * kD128), hl = idx / kD128 % group, d = idx % kD128;
+    const int w0 = hw * wph;
     float M = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < kD128Waves; ++w) M = fmaxf(M, s.sm[w][hl]);
+    for (int w = w0; w < w0 + wph; ++w) M = fmaxf(M, s.sm[w][hl]);
     float l = 0.f, acc = 0.f;
-#pragma unroll
-    for (int w = 0; w < kD128Waves; ++w) {
+    for (int w = w0; w < w0 + wph; ++w) {
       const float e = s.sm[w][hl] == -INFINITY ? 0.f : exp2f(s.sm[w][hl] - M);
       l += e * s.sl[w][hl];
       acc += e * s.so[w][d][hl];
     }
-    const int64_t row = static_cast<int64_t>(b) * a.Hq + kvh * group + hl;
+    const int64_t row = static_cast<int64_t>(b) * a.Hq + (h0 + hw) * group + hl;
     if (a.splits == 1) {
       *gp(a.out + row * kD128 + d) = l > 0.f ? floatToBf16(acc / l) : uint16_t{0};
       continue;
@@ -237,22 +248,26 @@ __device__ __forceinline__ void decodeAttention128Unit(const DecodeAttn128Args& 
   }
   if (a.splits == 1) return;
 
-  // arrive: every partial store of this workgroup has completed before the counter moves
+  // arrive: every partial store of this workgroup has completed before the counters move (one
+  // per (sequence, kv head) pair of the unit)
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
-  if (threadIdx.x == 0) {
+  if (threadIdx.x < hpw) {
+    const int pair = b * a.Hkv + h0 + threadIdx.x;
     const unsigned old = __hip_atomic_fetch_add(gp(a.counters) + pair, 1u, __ATOMIC_RELAXED,
                                                 __HIP_MEMORY_SCOPE_AGENT);
-    s.is_last = old + 1 == static_cast<unsigned>(a.splits);
-    if (s.is_last)
+    const bool last = old + 1 == static_cast<unsigned>(a.splits);
+    s.is_last[threadIdx.x] = last;
+    if (last)
       __hip_atomic_store(gp(a.counters) + pair, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   __syncthreads();
-  if (!s.is_last) return;
-  // merge every split's partial in split order (a split without keys left m = -inf, l = 0)
-  for (int idx = threadIdx.x; idx < group * kD128; idx += kD128Threads) {
-    const int hl = idx / kD128, d = idx % kD128;
-    const int64_t row = static_cast<int64_t>(b) * a.Hq + kvh * group + hl;
+  // merge every split's partial in split order (a split without keys left m = -inf, l = 0), for
+  // the pairs whose last unit this is
+  for (int idx = threadIdx.x; idx < hpw * group * kD128; idx += kD128Threads) {
+    const int hw = idx / (group * kD128), hl = idx / kD128 % group, d = idx % kD128;
+    if (!s.is_last[hw]) continue;
+    const int64_t row = static_cast<int64_t>(b) * a.Hq + (h0 + hw) * group + hl;
     float M = -INFINITY, l = 0.f, acc = 0.f;
     for (int sp = 0; sp < a.splits; ++sp) {
       const int64_t slot = row * a.splits + sp;
