@@ -214,7 +214,7 @@ def test_gate_up_silu_large_hidden(B, H, F):
 
 
 @pytest.mark.parametrize("B,H,V", [(1, 128, 1000), (5, 896, 4099), (32, 896, 151936 // 8),
-                                   (48, 256, 777)])
+                                   (48, 256, 777), (2, 512, 100), (3, 1024, 900)])
 @pytest.mark.parametrize("logits_dtype", ["float32", "bfloat16"])
 def test_lm_head_argmax(B, H, V, logits_dtype):
     g = torch.Generator().manual_seed(40 + B)
