@@ -58,10 +58,14 @@ __device__ __forceinline__ void loadKvBlock(KvBlockRegs& regs, const uint16_t* k
       regs.k[st][hf][0] = gload16(kbase + off * kDecD + g * 8);
       regs.k[st][hf][1] = gload16(kbase + off * kDecD + 32 + g * 8);
     }
-#pragma unroll
-    for (int d = 0; d < 4; ++d)
-      regs.v[st][d] = gload16(vbase + (d * 16 + r) * kDecBlock + 32 * st + 8 * g);
   }
+  // the two halves of each 128-byte V dim row next to each other: a line read by two loads far
+  // apart can be fetched from HBM twice
+#pragma unroll
+  for (int d = 0; d < 4; ++d)
+#pragma unroll
+    for (int st = 0; st < 2; ++st)
+      regs.v[st][d] = gload16(vbase + (d * 16 + r) * kDecBlock + 32 * st + 8 * g);
 }
 
 // One cache block of one kv head staged in LDS (the pools' layouts: K token-major, V dim-major).
