@@ -142,7 +142,9 @@ namespace {
 // Reduces of the large-hidden decode projections (mfma_gemm.hip): they read the fp32 parts
 // [parts, m, n] that decodeParts writes.
 DeviceKernel k_reduce_qkv("mfma_gemm", "splitk_reduce_qkv_rope_append");
-DeviceKernel k_reduce_res_norm("mfma_gemm", "splitk_reduce_residual_norm");
+DeviceKernel k_reduce_res_norm2("mfma_gemm", "splitk_reduce_residual_norm_p2");
+DeviceKernel k_reduce_res_norm4("mfma_gemm", "splitk_reduce_residual_norm_p4");
+DeviceKernel k_reduce_res_norm8("mfma_gemm", "splitk_reduce_residual_norm_p8");
 constexpr int64_t kResNormMaxN = 4096;  // splitk_reduce_residual_norm: 256 threads x 2 x 8
 constexpr int kResNormMaxSplits = 8;
 
@@ -150,8 +152,6 @@ constexpr int kResNormMaxSplits = 8;
 // tiled MFMA GEMM where it runs faster (tiledDecodeLinear), else the skinny partial kernel with
 // `splits` K ranges (at most 8 and k / 64, fewer if the workspace holds fewer). The parts go to
 // workspace [parts, m, n] fp32, summed by the caller's reduce in part order.
-bool decodeTiled(int64_t m, int64_t n) { return tiledDecodeLinear(m, n); }
-
 int64_t skinnyParts(int64_t k, int64_t splits) {
   int64_t s = splits < 1 ? 1 : splits;
   if (s > kMaxNormSplits) s = kMaxNormSplits;
@@ -162,7 +162,7 @@ int64_t skinnyParts(int64_t k, int64_t splits) {
 // Workspace bytes of decodeParts: every part it would write, at most 8 (what the reduces sum;
 // the tiled path halves its split count until the parts fit).
 size_t decodePartsBytes(int64_t m, int64_t n, int64_t k, int64_t splits) {
-  int64_t parts = decodeTiled(m, n) ? bf16Splits(m, n, k) : skinnyParts(k, splits);
+  int64_t parts = tiledDecodeLinear(m, n) ? bf16Splits(m, n, k) : skinnyParts(k, splits);
   if (parts > kResNormMaxSplits) parts = kResNormMaxSplits;
   return static_cast<size_t>(parts * m * n) * sizeof(float);
 }
@@ -171,7 +171,7 @@ int decodeParts(const char* op, const void* x, const void* w, int64_t m, int64_t
                 int64_t splits, void* workspace, size_t workspace_bytes, void* stream,
                 int* parts_out) {
   if (!aligned16(x) || !aligned16(w)) return bad(op, "x and w must be 16-byte aligned");
-  if (decodeTiled(m, n)) {
+  if (tiledDecodeLinear(m, n)) {
     if (k <= 0 || k % 8 != 0) return bad(op, "reduction size must be a positive multiple of 8");
     return tiledBf16Parts(x, w, m, n, k, workspace, workspace_bytes, stream, parts_out);
   }
@@ -362,7 +362,8 @@ int dli_hip_linear_residual_norm(const void* x, const void* w, const void* bias,
                              workspace_bytes < need ? workspace_bytes : need, stream, &parts))
       return rc;
     if (parts > kResNormMaxSplits) return bad(op, "too many K parts");
-    return launch(k_reduce_res_norm, {static_cast<unsigned>(m)}, {256}, 0, stream,
+    DeviceKernel& k = parts <= 2 ? k_reduce_res_norm2 : (parts <= 4 ? k_reduce_res_norm4 : k_reduce_res_norm8);
+    return launch(k, {static_cast<unsigned>(m)}, {256}, 0, stream,
                   static_cast<const float*>(workspace), parts, bias, residual, norm_weight, h_out,
                   xn_out, static_cast<int>(m), static_cast<int>(n), eps);
   }

@@ -1142,16 +1142,18 @@ extern "C" __global__ void __launch_bounds__(256)
 // follows it: h = bf16(residual + bf16(sum of the parts in split order + bias)) (the values of
 // splitk_reduce_bf16) and xn = bf16(h * rsqrt(mean(h^2) + eps) * norm_w)
 // (rms_norm/kernel.py:6-14). One workgroup per row, h held in registers between the two; rows of
-// N <= kResNormMaxN columns (N % 8 == 0), at most kResNormMaxSplits parts. Every part of every
-// chunk is requested before the first is added (the index of parts past `splits` is clamped and
-// their sums discarded), so a row costs one memory round trip, not one per part.
+// N <= 4096 columns (N % 8 == 0), at most kMaxParts parts (2, 4 or 8: the kernel suffix). Every
+// part of every chunk is requested before the first is added (the index of parts past `splits`
+// is clamped and their sums discarded), so a row costs one memory round trip, not one per part,
+// and the smallest kMaxParts that holds the parts keeps the surplus loads few.
 constexpr int kResNormChunks = 2;
-constexpr int kResNormMaxN = kResNormChunks * 256 * 8;
-constexpr int kResNormMaxSplits = 8;
-extern "C" __global__ void __launch_bounds__(256)
-    splitk_reduce_residual_norm(const float* part, int splits, const uint16_t* bias,
-                                const uint16_t* residual, const uint16_t* norm_w,
-                                uint16_t* h_out, uint16_t* xn_out, int M, int N, float eps) {
+template <int kMaxParts>
+__device__ __forceinline__ void splitkReduceResidualNorm(const float* part, int splits,
+                                                         const uint16_t* bias,
+                                                         const uint16_t* residual,
+                                                         const uint16_t* norm_w, uint16_t* h_out,
+                                                         uint16_t* xn_out, int M, int N,
+                                                         float eps) {
   FP_EXACT;
   __shared__ float wave_sq[256 / kWave];
   const int m = blockIdx.x;
@@ -1164,9 +1166,9 @@ extern "C" __global__ void __launch_bounds__(256)
     const int i = threadIdx.x + c * 256;
     if (i >= chunks) break;
     const int64_t at = static_cast<int64_t>(m) * N + i * 8;
-    f32x4 p[kResNormMaxSplits][2];
+    f32x4 p[kMaxParts][2];
 #pragma unroll
-    for (int z = 0; z < kResNormMaxSplits; ++z) {
+    for (int z = 0; z < kMaxParts; ++z) {
       const int64_t zz = z < splits ? z : splits - 1;
       p[z][0] = *gp(reinterpret_cast<const f32x4*>(part + zz * plane + at));
       p[z][1] = *gp(reinterpret_cast<const f32x4*>(part + zz * plane + at + 4));
@@ -1178,7 +1180,7 @@ extern "C" __global__ void __launch_bounds__(256)
 #pragma unroll
     for (int e = 0; e < 8; ++e) v[e] = p[0][e / 4][e % 4];
 #pragma unroll
-    for (int z = 1; z < kResNormMaxSplits; ++z)
+    for (int z = 1; z < kMaxParts; ++z)
 #pragma unroll
       for (int e = 0; e < 8; ++e) v[e] = z < splits ? v[e] + p[z][e / 4][e % 4] : v[e];
 #pragma unroll
@@ -1220,3 +1222,13 @@ extern "C" __global__ void __launch_bounds__(256)
         U128{o[0], o[1], o[2], o[3]};
   }
 }
+
+#define DK_RESNORM(P)                                                                            \
+  extern "C" __global__ void __launch_bounds__(256) splitk_reduce_residual_norm_p##P(           \
+      const float* part, int splits, const uint16_t* bias, const uint16_t* residual,             \
+      const uint16_t* norm_w, uint16_t* h_out, uint16_t* xn_out, int M, int N, float eps) {      \
+    splitkReduceResidualNorm<P>(part, splits, bias, residual, norm_w, h_out, xn_out, M, N, eps); \
+  }
+DK_RESNORM(2)
+DK_RESNORM(4)
+DK_RESNORM(8)
