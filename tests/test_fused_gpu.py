@@ -287,6 +287,11 @@ def test_lm_head_argmax_with_final_norm(B):
     (8, [-1, 0, 31, 32, 63, 64, 1000, 8191], 8256, (28, 4, 128)),
     (64, [8191] * 64, 8256, (28, 4, 128)),
     (3, [5, 130, 517], 600, (28, 4, 128)),
+    # every kv head of a sequence in one workgroup: 4 waves per head (2 kv heads), 1 wave per head
+    # (8 kv heads); 3 kv heads do not divide the 8 waves (one kv head per workgroup)
+    (4, [100, 4000, 8191, 0], 8256, (16, 2, 128)),
+    (2, [3000, 77], 4160, (8, 8, 128)),
+    (3, [50, 2000, 4100], 4160, (12, 3, 128)),
 ])
 def test_paged_attention_decode(B, positions, max_seq, geometry):
     """paged_attention (decode, 64-key blocks): every (sequence, kv head) is split over
