@@ -480,9 +480,10 @@ int dli_hip_lm_head_argmax_norm(const void* x, const void* norm_weight, float ep
                       xn, w, logits, logits_f32, part_val, part_idx, static_cast<int>(m), vocab,
                       static_cast<int>(hidden_size), norm_weight, eps))
     return rc;
+  // one partial per row from each lm_head workgroup (blocks <= tiles: the workspace holds them)
   return launch(k_argmax_final, {static_cast<unsigned>(m)}, {kThreads}, 0, stream,
                 static_cast<const float*>(part_val), static_cast<const int32_t*>(part_idx),
-                static_cast<int>(tiles), ids);
+                static_cast<int>(blocks), ids);
 }
 
 }  // extern "C"

@@ -17,7 +17,7 @@
 //                          bf16(bf16(silu(gate)) * up) (weights interleaved in 16-row blocks:
 //                          [gate 16 rows | up 16 rows] per output block of 16)
 //  lm_head_argmax          [optional final RMSNorm of x in registers] -> logits = xn W^T
-//                          (fp32) -> logits out + per-tile argmax partials; argmax_finalize
+//                          (fp32) -> logits out + per-workgroup argmax partials; argmax_finalize
 //                          reduces them (first index of the maximum)
 // qkv_rope_append, gate_up_silu and lm_head_argmax walk their weight tiles grid-strided
 // (tileLoop), sized by the host to the workgroups that are resident at once, so the weight
@@ -27,7 +27,7 @@
 
 using namespace dk;
 
-// Device scratch of dli_hip_lm_head_argmax_norm_noalloc (the per-tile argmax partials that the
+// Device scratch of dli_hip_lm_head_argmax_norm_noalloc (the argmax partials that the
 // other lm_head entry points keep in a caller's workspace), for callers that cannot allocate.
 // One copy per device that loads this module, zero at load, held until the process ends. Its
 // name stays in the code object's symbol table (no `static`), because the host finds it with
@@ -171,95 +171,176 @@ __device__ void gate_up_silu_impl(const uint16_t* x, const uint16_t* norm_w, flo
 
 constexpr int kLmTileN = 32;  // vocab rows per lm_head tile (NF = 2)
 constexpr int kLmQuarters = kLmTileN / 4;
+constexpr int kLmStageTiles = 12;  // tiles of logits a workgroup holds in LDS before writing them
 
-// Logits of vocab tiles of 32 rows (grid-strided over the workgroups) plus each tile's argmax
-// partial per row: part_*[m * tiles + t]. Requires K / 64 <= 4 * kWaves.
+// Writes `staged` tiles of logits staged in LDS (slot j: tile first + j * stride, batch row m at
+// m * kRow floats) to out [M, V] (float or bfloat16). A lane writes kPer consecutive logits of
+// one row with one 16-byte store when `wide` (16-byte aligned rows) and the chunk lies inside
+// the vocabulary; other chunks are written element by element.
+template <bool kF32, int kTileM, int kTileN, int kRow, typename T>
+__device__ __forceinline__ void flushStagedLogits(const float* stage, int staged, int64_t first,
+                                                  int64_t stride, T* out, int M, int64_t V,
+                                                  bool wide) {
+  constexpr int kPer = kF32 ? 4 : 8;
+  constexpr int kChunks = kTileN / kPer;  // per batch row of a tile
+  for (int idx = threadIdx.x; idx < staged * kTileM * kChunks; idx += kThreads) {
+    const int j = idx / (kTileM * kChunks), e = idx % (kTileM * kChunks);
+    const int c = e % kChunks, m = e / kChunks;  // a row's chunks on adjacent lanes
+    if (m >= M) continue;
+    const int64_t n = (first + j * stride) * kTileN + c * kPer;
+    const float* src = stage + j * kTileM * kRow + m * kRow + c * kPer;
+    T* dst = out + static_cast<int64_t>(m) * V + n;
+    if (wide && n + kPer <= V) {
+      U128 o;
+      if constexpr (kF32) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[i] = __builtin_bit_cast(uint32_t, src[i]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[i] = packBf16x2(src[2 * i], src[2 * i + 1]);
+      }
+      PlainMem::store16(dst, o);
+    } else {
+      for (int i = 0; i < kPer && n + i < V; ++i) {
+        if constexpr (kF32)
+          dst[i] = src[i];
+        else
+          dst[i] = floatToBf16(src[i]);
+      }
+    }
+  }
+}
+
+// Logits of vocab tiles of 32 rows (grid-strided over the workgroups) plus each workgroup's
+// argmax partial per row, part_*[m * gridDim.x + blockIdx.x]: the first index of the largest
+// logit among the workgroup's tiles. Requires K / 64 <= 4 * kWaves.
 // With norm_w non-NULL, xn is the un-normalized residual stream and its final RMSNorm
 // (model.norm, bf16 output) is applied in registers first (tileLoop's prologue).
+//
+// The tile loop issues no global store while its LDS staging has room: the tile logits are
+// staged in LDS (fp32, rows padded to kTileN + 1 floats against bank conflicts) and written
+// after the loop, or whenever kLmStageTiles tiles are staged, as 16-byte stores of 4 fp32 or
+// 8 bf16 logits; the argmax runs in registers, one (row, quarter of the tile rows) item per
+// thread, and is merged per workgroup once. At 32 rows, 896 columns and 151,936 vocabulary rows
+// this takes the launch from 64 to 56 us against one 2-byte logit store per thread and tile
+// plus per-tile argmax partials inside the loop.
 template <int MB>
 __device__ void lm_head_argmax_impl(const uint16_t* xn, const uint16_t* w, void* logits,
                                     int logits_f32, float* part_val, int32_t* part_idx, int M,
                                     int64_t V, int K, const uint16_t* norm_w, float eps) {
   using Core = SkinnyCore<2, MB, kWaves>;
   static_assert(Core::kTileN == kLmTileN, "lm_head tile");
-  // the tile reductions, then the argmax quarters (inside the reductions' area) or, during the
-  // prologue only, the RMSNorm row sums (after it)
-  static_assert(kNormLdsFloats<MB, kWaves> <= kLmQuarters * Core::kTileM, "lm_head lds");
-  __shared__ float lds[Core::kLdsFloats + kLmQuarters * Core::kTileM];
-  __shared__ int lds_arg[kLmQuarters * Core::kTileM];
-  const int64_t tiles = (V + Core::kTileN - 1) / Core::kTileN;
-  tileLoop<2, MB, kWaves, 4>(w, XGlobal{xn, K}, V, K, M, lds, norm_w, eps, blockIdx.x,
-                             gridDim.x, INT64_MAX, NoWait{}, [&](int64_t t) {
-    const int64_t n0 = t * Core::kTileN;
+  constexpr int kTileM = Core::kTileM, kTileN = Core::kTileN;
+  constexpr int kRow = kTileN + 1;             // staged floats per batch row of a tile
+  constexpr int kStageFloats = kTileM * kRow;  // per staged tile
+  constexpr int kItems = (kLmQuarters * kTileM + kThreads - 1) / kThreads;
+  // the tile reductions, then the staged logits (during the prologue only, the RMSNorm row sums)
+  static_assert(kNormLdsFloats<MB, kWaves> <= kLmStageTiles * kStageFloats, "lm_head lds");
+  static_assert(2 * kLmQuarters * kTileM <= Core::kLdsFloats, "lm_head quarter merge");
+  __shared__ float lds[Core::kLdsFloats + kLmStageTiles * kStageFloats];
+  float* const stage = lds + Core::kLdsFloats;
+  const int64_t stride = gridDim.x;
+  int64_t stage_first = blockIdx.x;  // tile of stage slot 0; slot j holds stage_first + j stride
+  int staged = 0;
+  // 16-byte stores (4 fp32 or 8 bf16 logits) wherever rows stay 16-byte aligned
+  const bool wide = (reinterpret_cast<uintptr_t>(logits) & 15) == 0 && V % (logits_f32 ? 4 : 8) == 0;
+  auto flush = [&]() {
+    if (logits_f32)
+      flushStagedLogits<true, kTileM, kTileN, kRow>(stage, staged, stage_first, stride,
+                                                    static_cast<float*>(logits), M, V, wide);
+    else
+      flushStagedLogits<false, kTileM, kTileN, kRow>(stage, staged, stage_first, stride,
+                                                     static_cast<uint16_t*>(logits), M, V, wide);
+  };
+  float best[kItems];
+  int32_t arg[kItems];
+#pragma unroll
+  for (int i = 0; i < kItems; ++i) {
+    best[i] = -INFINITY;
+    arg[i] = -1;
+  }
+  tileLoop<2, MB, kWaves, 4>(w, XGlobal{xn, K}, V, K, M, lds, norm_w, eps, blockIdx.x, stride,
+                             INT64_MAX, NoWait{}, [&](int64_t t) {
+    const int64_t n0 = t * kTileN;
     if (logits != nullptr) {
-      for (int idx = threadIdx.x; idx < Core::kTileN * Core::kTileM; idx += kThreads) {
-        const int nl = idx % Core::kTileN, m = idx / Core::kTileN;  // n fastest: coalesced stores
-        const int64_t n = n0 + nl;
-        if (m >= M || n >= V) continue;
-        const float v = lds[nl * Core::kTileM + m];
-        if (logits_f32)
-          static_cast<float*>(logits)[m * V + n] = v;
-        else
-          static_cast<uint16_t*>(logits)[m * V + n] = floatToBf16(v);
+      if (staged == kLmStageTiles) {
+        flush();
+        __syncthreads();  // every slot read before slot 0 is written again
+        stage_first = t;
+        staged = 0;
       }
+      float* const slot = stage + staged * kStageFloats;
+      for (int idx = threadIdx.x; idx < kTileN * kTileM; idx += kThreads) {
+        const int m = idx % kTileM, nl = idx / kTileM;
+        slot[m * kRow + nl] = lds[nl * kTileM + m];
+      }
+      ++staged;
     }
-    // argmax: thread (m, q) scans rows 4q..4q+3 of the tile, then one thread per m merges the
-    // quarters in order (first index among equal maxima).
-    float* qv = lds + Core::kTileN * Core::kTileM;
-    for (int idx = threadIdx.x; idx < kLmQuarters * Core::kTileM; idx += kThreads) {
-      const int m = idx % Core::kTileM, q = idx / Core::kTileM;
-      float best = -INFINITY;
-      int arg = -1;
+    // thread item (m, q) scans rows 4q..4q+3 of each tile in order: first index of the maximum
+#pragma unroll
+    for (int i = 0; i < kItems; ++i) {
+      const int idx = threadIdx.x + i * kThreads;
+      if (idx >= kLmQuarters * kTileM) break;
+      const int m = idx % kTileM, q = idx / kTileM;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int nl = q * 4 + j;
-        const float v = lds[nl * Core::kTileM + m];
-        if (n0 + nl < V && (arg < 0 || v > best)) {
-          best = v;
-          arg = nl;
+        const float v = lds[nl * kTileM + m];
+        if (n0 + nl < V && (arg[i] < 0 || v > best[i])) {
+          best[i] = v;
+          arg[i] = static_cast<int32_t>(n0 + nl);
         }
       }
-      qv[q * Core::kTileM + m] = best;
-      lds_arg[q * Core::kTileM + m] = arg;
-    }
-    __syncthreads();
-    for (int m = threadIdx.x; m < M; m += kThreads) {
-      float best = -INFINITY;
-      int arg = -1;
-      for (int q = 0; q < kLmQuarters; ++q) {
-        const float v = qv[q * Core::kTileM + m];
-        const int a = lds_arg[q * Core::kTileM + m];
-        if (a >= 0 && (arg < 0 || v > best)) {
-          best = v;
-          arg = a;
-        }
-      }
-      part_val[m * tiles + t] = best;
-      part_idx[m * tiles + t] = static_cast<int32_t>(n0 + (arg < 0 ? 0 : arg));
     }
   });
+  // tileLoop ends every tile with a barrier: the staging is complete and the reduction area free
+  if (logits != nullptr) flush();
+  float* const qv = lds;
+  int32_t* const qa = reinterpret_cast<int32_t*>(lds + kLmQuarters * kTileM);
+#pragma unroll
+  for (int i = 0; i < kItems; ++i) {
+    const int idx = threadIdx.x + i * kThreads;
+    if (idx >= kLmQuarters * kTileM) break;
+    qv[idx] = best[i];  // idx = q * kTileM + m
+    qa[idx] = arg[i];
+  }
+  __syncthreads();
+  for (int m = threadIdx.x; m < M; m += kThreads) {
+    float b = -INFINITY;
+    int32_t a = -1;
+    for (int q = 0; q < kLmQuarters; ++q) {  // the quarters interleave: ties go to the lower index
+      const float v = qv[q * kTileM + m];
+      const int32_t i = qa[q * kTileM + m];
+      if (i >= 0 && (a < 0 || v > b || (v == b && i < a))) {
+        b = v;
+        a = i;
+      }
+    }
+    part_val[static_cast<int64_t>(m) * stride + blockIdx.x] = b;
+    part_idx[static_cast<int64_t>(m) * stride + blockIdx.x] = a < 0 ? 0x7fffffff : a;
+  }
 }
 
-// One workgroup per row: reduce that row's tile partials (contiguous) in tile order; ties keep
-// the lower index.
-__device__ void argmax_finalize_impl(const float* part_val, const int32_t* part_idx, int tiles,
+// One workgroup per row: reduce that row's partials (contiguous, one per lm_head workgroup);
+// ties keep the lower index.
+__device__ void argmax_finalize_impl(const float* part_val, const int32_t* part_idx, int parts,
                                      int64_t* ids) {
   __shared__ float sv[kWaves];
   __shared__ int32_t si[kWaves];
   const int m = blockIdx.x;
-  const float* vals = part_val + static_cast<int64_t>(m) * tiles;
-  const int32_t* idxs = part_idx + static_cast<int64_t>(m) * tiles;
+  const float* vals = part_val + static_cast<int64_t>(m) * parts;
+  const int32_t* idxs = part_idx + static_cast<int64_t>(m) * parts;
   float best = -INFINITY;
   int32_t arg = 0x7fffffff;
   constexpr int kBatch = 8;  // loads of kBatch partials in flight per thread
-  for (int t0 = threadIdx.x; t0 < tiles; t0 += kBatch * kThreads) {
+  for (int t0 = threadIdx.x; t0 < parts; t0 += kBatch * kThreads) {
     float v[kBatch];
     int32_t ix[kBatch];
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
       const int t = t0 + u * kThreads;
-      v[u] = t < tiles ? vals[t] : -INFINITY;
-      ix[u] = t < tiles ? idxs[t] : 0x7fffffff;
+      v[u] = t < parts ? vals[t] : -INFINITY;
+      ix[u] = t < parts ? idxs[t] : 0x7fffffff;
     }
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
@@ -330,7 +411,7 @@ __device__ void argmax_finalize_impl(const float* part_val, const int32_t* part_
       int M, int64_t F, int K) {                                                                  \
     gate_up_silu_impl<MB>(x, norm_w, eps, w_gu, out, M, F, K);                                    \
   }                                                                                               \
-  extern "C" __global__ void __launch_bounds__(kThreads, 2) lm_head_argmax_m##MB(                  \
+  extern "C" __global__ void __launch_bounds__(kThreads, MB >= 4 ? 1 : 2) lm_head_argmax_m##MB(    \
       const uint16_t* xn, const uint16_t* w, void* logits, int logits_f32, float* part_val,       \
       int32_t* part_idx, int M, int64_t V, int K, const uint16_t* norm_w, float eps) {            \
     lm_head_argmax_impl<MB>(xn, w, logits, logits_f32, part_val, part_idx, M, V, K, norm_w, eps); \
