@@ -393,8 +393,8 @@ int dli_hip_lm_head_argmax_norm(const void* x, const void* norm_weight, float ep
                                 void* logits, int logits_dtype, int64_t* ids, int64_t m,
                                 int64_t vocab, int64_t hidden_size, void* workspace,
                                 size_t workspace_bytes, void* stream);
-/* dli_hip_lm_head_argmax_norm without a workspace argument and without allocating: the per-tile
- * argmax partials go to a static 4 MiB device array of the library (one per device, set up on
+/* dli_hip_lm_head_argmax_norm without a workspace argument and without allocating: the argmax
+ * partials (one per row and lm_head workgroup) go to a static 4 MiB device array of the library (one per device, set up on
  * the first call on that device, which also loads the kernels there; held until the process
  * ends). No counterpart in the reference: it is for callers that cannot allocate device memory
  * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). Same
