@@ -180,7 +180,8 @@ def time_decode_attention(session, cfg, B, ctx, pos, g, stream, hip, reps=200):
         hip.call("dli_hip_paged_attention", hip.BF16, q.data_ptr(), e["key_pool"].data_ptr(),
                  e["value_pool"].data_ptr(), e["block_table"].data_ptr(), out.data_ptr(), B, cfg.heads,
                  cfg.kv_heads, 1, cfg.head_dim, e["block_size"], e["max_blocks"], 0,
-                 pos.data_ptr(), hip.I64, 1, cfg.head_dim ** -0.5, ws.data_ptr(), ws_bytes, s_ptr)
+                 pos.data_ptr(), hip.I64, 1, cfg.head_dim ** -0.5, 0, ws.data_ptr(), ws_bytes,
+                 s_ptr)
 
     us = _time_launches(attn, stream, reps)
     nbytes = B * ctx * cfg.kv_heads * cfg.head_dim * 2 * 2 + 2 * B * cfg.heads * cfg.head_dim * 2
@@ -212,7 +213,7 @@ def time_decoder_stack(session, cfg, B, ctx, pos, g, stream, hip, down_splits, r
     e0 = session.engine.kv_cache_entry("layer_0")
     ws_bytes = hip.lib().dli_hip_decoder_stack_workspace(L, B, cfg.hidden, cfg.heads,
                                                           cfg.kv_heads, cfg.head_dim, cfg.ffn,
-                                                          e0["max_blocks"], down_splits)
+                                                          e0["max_blocks"], down_splits, 0)
     ws = torch.zeros((ws_bytes + 3) // 4, dtype=torch.int32, device="cuda")
     x = (torch.randn(B, cfg.hidden, generator=g, device="cuda") * 0.5).to(torch.bfloat16)
     out = torch.empty_like(x)
@@ -224,7 +225,7 @@ def time_decoder_stack(session, cfg, B, ctx, pos, g, stream, hip, down_splits, r
                  pos.data_ptr(), hip.I64, cos.data_ptr(), sin.data_ptr(), cos.shape[0],
                  e0["block_size"], e0["max_blocks"], B, cfg.hidden, cfg.heads, cfg.kv_heads,
                  cfg.head_dim, cfg.ffn, cfg.eps, down_splits, ws.data_ptr(), ws_bytes, None,
-                 s_ptr)
+                 None, s_ptr)
 
     us = _time_launches(stack, stream, reps)
     aborted = ctypes.c_int()
@@ -644,6 +645,7 @@ def main():
     for _ in range(args.warmup):
         one_step()
     torch.cuda.synchronize()
+    session.check_status()  # a decoder_stack wait that gave up invalidates the steps: exit non-zero
     stream = torch.cuda.current_stream()
     start_ev, stop_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
@@ -653,6 +655,7 @@ def main():
     stop_ev.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    session.check_status()
     ms_per_step = start_ev.elapsed_time(stop_ev) / args.steps
     tok_s = B * 1000.0 / ms_per_step
     total, w_bytes, kv_read, kv_write, logit_bytes = step_bytes(cfg, B, ctx)

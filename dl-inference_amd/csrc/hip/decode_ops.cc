@@ -19,7 +19,6 @@ constexpr int kResWaves = 8;         // waves per linear_residual workgroup
 constexpr int64_t kMaxNormN = 1024;  // residual_rms_norm: 256 threads x 4 columns
 constexpr int kMaxNormSplits = 8;    // residual_rms_norm sums at most 8 split-K partials
 constexpr int64_t kMaxLmK = 1024;    // tile loops keep x for K / 64 <= 16 steps in registers
-constexpr int kMaxDecodeSplits = 32; // splits a decode-attention call may use
 
 struct MbKernels {
   DeviceKernel m1, m2, m4;
@@ -552,36 +551,31 @@ namespace dli::hip {
 // grid runs in one round (the kernel fits one 8-wave workgroup per CU); the blocks of a
 // sequence are dealt round-robin over all waves of its splits. The last split of a (sequence,
 // kv head) to finish merges the partials (agent-scope stores and loads plus a per-(sequence,
-// kv head) counter in the workspace, which it leaves at zero). DLI_ATTN_SPLITS=<n> overrides
-// the split count (tuning).
+// kv head) counter in the workspace, which it leaves at zero). A caller's split count
+// (`requested` > 0) replaces the per-CU choice.
 namespace {
 constexpr int kDecWaves = 8;
 constexpr int kDecBlock = 64;
 
 // Workspace: partials [ml: rows x splits x 2][o: rows x splits x head_dim] fp32 inside a region
-// sized for kMaxDecodeSplits, then per-(sequence, kv head) arrival counters (rows of them, which
-// is at least batch * kv_heads), 256-B aligned.
-size_t partialBytes(int64_t rows, int64_t head_dim = 64) {
-  return alignUp(static_cast<size_t>(rows) * kMaxDecodeSplits * (2 + head_dim) * sizeof(float),
+// sized for kMaxDecodeSplits and the largest head_dim (128), then per-(sequence, kv head)
+// arrival counters (rows of them, which is at least batch * kv_heads), 256-B aligned. The
+// counters sit at the same offset for every head_dim, so one workspace may serve calls of both
+// head sizes: no call's partials overlap another's counters.
+constexpr int64_t kMaxDecodeHeadDim = 128;
+size_t partialBytes(int64_t rows) {
+  return alignUp(static_cast<size_t>(rows) * kMaxDecodeSplits * (2 + kMaxDecodeHeadDim) *
+                     sizeof(float),
                  256);
 }
 
 }  // namespace
 
-namespace {
-// 0 = choose per call; set by dli_hip_set_decode_attention_splits or DLI_ATTN_SPLITS=<n>.
-std::atomic<int> forced_splits{[] {
-  const char* v = std::getenv("DLI_ATTN_SPLITS");
-  return v ? std::atoi(v) : 0;
-}()};
-}  // namespace
-
 // Splits of `units` workgroup units whose blocks are dealt over `wph` waves per head: about one
 // workgroup per CU, no more splits than groups of wph blocks, never fewer than the per-lane
 // block ids of a wave (64) allow.
-int decodeAttentionSplits(int64_t units, int64_t max_blocks, int cus, int wph) {
-  const int forced = forced_splits.load(std::memory_order_relaxed);
-  int64_t splits = forced > 0 ? forced : (units > 0 ? cus / units : 1);
+int decodeAttentionSplits(int64_t units, int64_t max_blocks, int cus, int wph, int requested) {
+  int64_t splits = requested > 0 ? requested : (units > 0 ? cus / units : 1);
   const int64_t useful = (max_blocks + wph - 1) / wph;
   if (splits > useful) splits = useful;
   const int64_t needed = (max_blocks + wph * 64 - 1) / (wph * 64);
@@ -594,8 +588,8 @@ int decodeAttentionFast(int dtype, const void* q, const void* key_pool, const vo
                         const int32_t* block_table, void* out, int64_t batch, int64_t q_heads,
                         int64_t kv_heads, int64_t seq_q, int64_t head_dim, int64_t block_size,
                         int64_t max_blocks, int64_t past, const void* positions,
-                        int positions_dtype, float scale, void* workspace, size_t workspace_bytes,
-                        void* stream) {
+                        int positions_dtype, float scale, int requested_splits, void* workspace,
+                        size_t workspace_bytes, void* stream) {
   if (dtype != DLI_BF16 || seq_q != 1 || (head_dim != 64 && head_dim != 128) ||
       q_heads / kv_heads > 16 || block_size != kDecBlock || !aligned16(q))
     return 1;
@@ -606,16 +600,17 @@ int decodeAttentionFast(int dtype, const void* q, const void* key_pool, const vo
   // workgroup then reads whole cache blocks of the pools)
   const int hpw = head_dim == 128 && kDecWaves % kv_heads == 0 ? static_cast<int>(kv_heads) : 1;
   const int splits =
-      decodeAttentionSplits(batch * kv_heads / hpw, max_blocks, cus, kDecWaves / hpw);
+      decodeAttentionSplits(batch * kv_heads / hpw, max_blocks, cus, kDecWaves / hpw,
+                            requested_splits);
   if (splits > kMaxDecodeSplits) return 1;
   const int64_t rows = batch * q_heads;
-  const size_t need = partialBytes(rows, head_dim) + static_cast<size_t>(rows) * sizeof(unsigned);
+  const size_t need = partialBytes(rows) + static_cast<size_t>(rows) * sizeof(unsigned);
   if (splits > 1 && (workspace == nullptr || workspace_bytes < need)) return 1;
   float* ws_ml = static_cast<float*>(workspace);
   float* ws_o = splits > 1 ? ws_ml + rows * splits * 2 : nullptr;
   unsigned* counters =
       splits > 1 ? reinterpret_cast<unsigned*>(static_cast<char*>(workspace) +
-                                               partialBytes(rows, head_dim))
+                                               partialBytes(rows))
                  : nullptr;
   const int pos64 = positions_dtype == DLI_I64 ? 1 : 0;
   const float scale_log2 = scale * 1.4426950408889634f;
@@ -639,14 +634,7 @@ size_t decodeAttentionWorkspace(int64_t batch, int64_t q_heads, int64_t seq_q, i
                                 int64_t max_tokens) {
   if (seq_q != 1 || (head_dim != 64 && head_dim != 128)) return 0;
   const int64_t rows = batch * q_heads;
-  return partialBytes(rows, head_dim) + static_cast<size_t>(rows) * sizeof(unsigned);
+  return partialBytes(rows) + static_cast<size_t>(rows) * sizeof(unsigned);
 }
 
 }  // namespace dli::hip
-
-extern "C" int dli_hip_set_decode_attention_splits(int splits) {
-  if (splits < 0 || splits > dli::hip::kMaxDecodeSplits)
-    return dli::hip::fail(DLI_HIP_EINVAL, "decode attention splits must be in [0, 32]");
-  dli::hip::forced_splits.store(splits, std::memory_order_relaxed);
-  return 0;
-}

@@ -202,8 +202,8 @@ int decodeAttentionFast(int dtype, const void* q, const void* key_pool, const vo
                         const int32_t* block_table, void* out, int64_t batch, int64_t q_heads,
                         int64_t kv_heads, int64_t seq_q, int64_t head_dim, int64_t block_size,
                         int64_t max_blocks, int64_t past, const void* positions,
-                        int positions_dtype, float scale, void* workspace, size_t workspace_bytes,
-                        void* stream);
+                        int positions_dtype, float scale, int requested_splits, void* workspace,
+                        size_t workspace_bytes, void* stream);
 size_t decodeAttentionWorkspace(int64_t batch, int64_t q_heads, int64_t seq_q, int64_t head_dim,
                                 int64_t max_tokens);
 }  // namespace dli::hip
@@ -641,7 +641,7 @@ int dli_hip_paged_attention(int dtype, const void* q, const void* key_pool,
                             int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t seq_q,
                             int64_t head_dim, int64_t block_size, int64_t max_blocks, int64_t past,
                             const void* positions, int positions_dtype, int causal, float scale,
-                            void* workspace, size_t workspace_bytes, void* stream) {
+                            int splits, void* workspace, size_t workspace_bytes, void* stream) {
   DeviceKernel* ka = k_paged_attention.pick(dtype);
   if (ka == nullptr) return badDtype("paged_attention", dtype);
   if (head_dim <= 0 || head_dim > 256) return badArg("paged_attention", "head_dim must be in [1, 256]");
@@ -651,13 +651,15 @@ int dli_hip_paged_attention(int dtype, const void* q, const void* key_pool,
   if (positions != nullptr && !validIndexDtype(positions_dtype))
     return badArg("paged_attention", "positions must be int64 or int32");
   if (batch < 0 || seq_q < 0) return badArg("paged_attention", "negative size");
+  if (splits < 0 || splits > kMaxDecodeSplits)
+    return badArg("paged_attention", "splits must be in [0, 32]");
   const int64_t rows = batch * q_heads * seq_q;
   if (rows == 0) return 0;
   if (rows > 0x7fffffff) return badArg("paged_attention", "too many query rows");
   if (causal || seq_q == 1) {
     const int rc = decodeAttentionFast(dtype, q, key_pool, value_pool, block_table, out, batch,
                                        q_heads, kv_heads, seq_q, head_dim, block_size, max_blocks,
-                                       past, positions, positions_dtype, scale, workspace,
+                                       past, positions, positions_dtype, scale, splits, workspace,
                                        workspace_bytes, stream);
     if (rc != 1) return rc;
   }

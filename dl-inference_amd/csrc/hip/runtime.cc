@@ -51,8 +51,6 @@ struct Runtime {
   Status (*deviceGetAttribute)(int*, int, int) = nullptr;
   Status (*streamIsCapturing)(StreamT, int*) = nullptr;
   Status (*moduleGetGlobal)(void**, size_t*, ModuleT, const char*) = nullptr;
-  Status (*moduleLaunchCooperativeKernel)(FunctionT, unsigned, unsigned, unsigned, unsigned,
-                                          unsigned, unsigned, unsigned, StreamT, void**) = nullptr;
   Status (*moduleOccupancy)(int*, FunctionT, int, size_t) = nullptr;
 
   template <typename F>
@@ -91,7 +89,6 @@ struct Runtime {
                     bind(deviceGetAttribute, "hipDeviceGetAttribute") &&
                     bind(streamIsCapturing, "hipStreamIsCapturing") &&
                     bind(moduleGetGlobal, "hipModuleGetGlobal") &&
-                    bind(moduleLaunchCooperativeKernel, "hipModuleLaunchCooperativeKernel") &&
                     bind(moduleOccupancy, "hipModuleOccupancyMaxActiveBlocksPerMultiprocessor");
     if (!ok) {
       dlclose(handle);
@@ -251,15 +248,14 @@ int launchResidentRaw(DeviceKernel& kernel, Dim3 grid, Dim3 block, unsigned lds_
                                     " workgroups cannot all be resident (" +
                                     std::to_string(per_cu) + " per CU, " + std::to_string(cus) +
                                     " CUs)");
-  int capturing = 0;
-  if (int rc = check(runtime().streamIsCapturing(stream, &capturing), "hipStreamIsCapturing"))
-    return rc;
-  if (capturing != 0)  // a graph node: residency is checked above, the replay launches it
-    return check(runtime().moduleLaunchKernel(fn, grid.x, grid.y, grid.z, block.x, block.y,
-                                              block.z, lds_bytes, stream, args, nullptr),
-                 kernel.name());
-  return check(runtime().moduleLaunchCooperativeKernel(fn, grid.x, grid.y, grid.z, block.x,
-                                                       block.y, block.z, lds_bytes, stream, args),
+  // A plain launch, eager or captured alike. The grid fits the device at once (checked above),
+  // so on a device that runs nothing else every workgroup is resident together; work on other
+  // streams can only delay some workgroups, and the kernel's bounded waits turn a wait that
+  // outlasts that into a reported give-up, never a hang. (hipModuleLaunchCooperativeKernel
+  // was used for eager launches before: under rocprofv3 its runtime path made every profiled
+  // process end with a SIGSEGV in the profiler's teardown.)
+  return check(runtime().moduleLaunchKernel(fn, grid.x, grid.y, grid.z, block.x, block.y, block.z,
+                                            lds_bytes, stream, args, nullptr),
                kernel.name());
 }
 
@@ -309,6 +305,18 @@ int dli_hip_compute_units(int* count) {
 int dli_hip_set_device(int device) {
   if (int rc = requireRuntime()) return rc;
   return check(runtime().setDevice(device), "hipSetDevice");
+}
+
+int dli_hip_code_object(const char* name, const void** image, size_t* image_bytes) {
+  if (name == nullptr || image == nullptr || image_bytes == nullptr)
+    return fail(DLI_HIP_EINVAL, "name, image and image_bytes must be non-NULL");
+  for (const dli::hip::CodeObject& co : dli::hip::kCodeObjects) {
+    if (std::strcmp(co.name, name) != 0) continue;
+    *image = co.begin;
+    *image_bytes = static_cast<size_t>(co.end - co.begin);
+    return 0;
+  }
+  return fail(DLI_HIP_EINVAL, std::string("no embedded code object named ") + name);
 }
 
 int dli_hip_module_load(const void* image, size_t image_bytes, void** module) {

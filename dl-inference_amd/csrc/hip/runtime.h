@@ -27,9 +27,10 @@ int requireRuntime();
 int computeUnits(int* count);
 // Key-range splits per workgroup unit of MFMA decode attention (a (sequence, kv head) pair, or a
 // group of kv heads of one sequence): about `cus` workgroups over all units, no more splits than
-// groups of wph cache blocks (wph: waves per kv head), or the count set with
-// dli_hip_set_decode_attention_splits (or DLI_ATTN_SPLITS) when one is set.
-int decodeAttentionSplits(int64_t units, int64_t max_blocks, int cus, int wph = 8);
+// groups of wph cache blocks (wph: waves per kv head); `requested` > 0 (the caller's count)
+// replaces the per-CU choice. Never fewer splits than the per-lane block ids of a wave allow.
+int decodeAttentionSplits(int64_t units, int64_t max_blocks, int cus, int wph, int requested);
+constexpr int kMaxDecodeSplits = 32;  // key-range splits a decode-attention call may use
 
 // A kernel by name inside one embedded code object; resolved once per device.
 class DeviceKernel {
@@ -51,9 +52,8 @@ int launchRaw(DeviceKernel& kernel, Dim3 grid, Dim3 block, unsigned lds_bytes, v
               void** args);
 
 // launchRaw for a kernel whose workgroups wait on each other (a persistent launch): refuses a
-// grid larger than the device can hold resident at once (occupancy query), and launches
-// cooperatively (hipModuleLaunchCooperativeKernel, which waits until the whole grid can be
-// resident) unless the stream is being captured, where a plain kernel node is recorded.
+// grid larger than the device can hold resident at once (occupancy query against the compute
+// unit count), then launches it as a plain kernel (a plain kernel node under stream capture).
 int launchResidentRaw(DeviceKernel& kernel, Dim3 grid, Dim3 block, unsigned lds_bytes,
                       void* stream, void** args);
 

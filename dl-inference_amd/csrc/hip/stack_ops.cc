@@ -25,10 +25,6 @@ int bad(const std::string& what) {
   return fail(DLI_HIP_EINVAL, "decoder_stack: " + what);
 }
 
-// Stage timeline buffer of the next launches (dli_hip_decoder_stack_trace), NULL when off.
-unsigned long long* g_trace = nullptr;
-int g_trace_layers = 0;
-
 size_t alignUp(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 int tileRows(int64_t m) { return m <= 16 ? 16 : (m <= 32 ? 32 : 64); }
@@ -90,16 +86,17 @@ int stackGrid(unsigned* grid) {
 }
 
 // Attention units go to the workgroups that do no q|k|v work (dli_stack::qkvWorkgroups, the
-// last ones of the grid), so splits ~ (grid - those) / pairs.
+// last ones of the grid), so splits ~ (grid - those) / pairs, unless the caller requests a count.
 int attnSplits(int64_t pairs, int64_t max_blocks, int64_t q_tiles, int64_t kv_tiles,
-               int* splits) {
+               int requested, int* splits) {
   unsigned grid = 0;
   if (int rc = stackGrid(&grid)) return rc;
   const int64_t qkv_wgs = dli_stack::qkvWorkgroups(static_cast<int>(q_tiles),
                                                    static_cast<int>(kv_tiles),
                                                    static_cast<int>(grid));
   const int64_t free_wgs = static_cast<int64_t>(grid) > qkv_wgs ? grid - qkv_wgs : grid;
-  *splits = decodeAttentionSplits(pairs, max_blocks, static_cast<int>(free_wgs));
+  *splits = decodeAttentionSplits(pairs, max_blocks, static_cast<int>(free_wgs), kDecWaves,
+                                  requested);
   return 0;
 }
 
@@ -112,13 +109,15 @@ extern "C" {
 
 size_t dli_hip_decoder_stack_workspace(int num_layers, int64_t batch, int64_t hidden_size,
                                        int64_t q_heads, int64_t kv_heads, int64_t head_dim,
-                                       int64_t ffn, int64_t max_blocks, int down_splits) {
+                                       int64_t ffn, int64_t max_blocks, int down_splits,
+                                       int attention_splits) {
   if (num_layers <= 0 || batch <= 0 || hidden_size <= 0 || q_heads <= 0 || kv_heads <= 0 ||
-      head_dim <= 0 || ffn <= 0 || max_blocks <= 0 || down_splits < 1)
+      head_dim <= 0 || ffn <= 0 || max_blocks <= 0 || down_splits < 1 || attention_splits < 0 ||
+      attention_splits > kMaxDecodeSplits)
     return 0;
   int splits = 0;
   if (attnSplits(batch * kv_heads, max_blocks, q_heads * head_dim / 16,
-                 2 * kv_heads * head_dim / 16, &splits) != 0)
+                 2 * kv_heads * head_dim / 16, attention_splits, &splits) != 0)
     return 0;
   return layoutFor(batch, hidden_size, q_heads, kv_heads, head_dim, ffn, splits, down_splits,
                    num_layers)
@@ -132,9 +131,14 @@ int dli_hip_decoder_stack(const DliDecoderLayer* layers, int num_layers, const v
                           int64_t hidden_size, int64_t q_heads, int64_t kv_heads,
                           int64_t head_dim, int64_t ffn, float eps, int down_splits,
                           void* workspace, size_t workspace_bytes, unsigned* status,
-                          void* stream) {
+                          const DliStackOptions* options, void* stream) {
   if (layers == nullptr || num_layers < 0) return bad("layers is NULL");
   if (num_layers == 0) return 0;
+  const DliStackOptions opt = options != nullptr ? *options : DliStackOptions{0, nullptr, 0};
+  if (opt.attention_splits < 0 || opt.attention_splits > kMaxDecodeSplits)
+    return bad("attention_splits must be in [0, 32]");
+  if (opt.trace != nullptr && opt.trace_layers <= 0)
+    return bad("trace_layers must be positive with a trace buffer");
   if (batch <= 0 || batch > 64) return bad("batch must be in [1, 64]");
   if (hidden_size <= 0 || hidden_size % 64 != 0 || hidden_size > kMaxHidden)
     return bad("hidden_size must be a multiple of 64 in [64, 1024]");
@@ -166,7 +170,7 @@ int dli_hip_decoder_stack(const DliDecoderLayer* layers, int num_layers, const v
   }
   int splits = 0;
   if (int rc = attnSplits(batch * kv_heads, max_blocks, q_heads * head_dim / 16,
-                          2 * kv_heads * head_dim / 16, &splits))
+                          2 * kv_heads * head_dim / 16, opt.attention_splits, &splits))
     return rc;
   if (max_blocks > static_cast<int64_t>(splits) * kDecWaves * 64)
     return bad("max_blocks exceeds what the attention splits can index");
@@ -210,8 +214,8 @@ int dli_hip_decoder_stack(const DliDecoderLayer* layers, int num_layers, const v
   a.down_splits = down_splits;
   a.eps = eps;
   a.scale_log2 = static_cast<float>(1.4426950408889634 / 8.0);  // log2(e) / sqrt(64)
-  a.trace = g_trace;
-  a.trace_layers = g_trace_layers;
+  a.trace = opt.trace;
+  a.trace_layers = opt.trace != nullptr ? opt.trace_layers : 0;
   // Layers run in launches of at most kMaxLayers; later launches continue from hidden_out.
   for (int first = 0; first < num_layers; first += dli_stack::kMaxLayers) {
     const int count = num_layers - first < dli_stack::kMaxLayers ? num_layers - first
@@ -239,13 +243,6 @@ int dli_hip_decoder_stack(const DliDecoderLayer* layers, int num_layers, const v
     }
     if (int rc = launchResident(*kernel, {grid}, {kStackThreads}, 0, stream, a)) return rc;
   }
-  return 0;
-}
-
-int dli_hip_decoder_stack_trace(unsigned long long* trace, int trace_layers) {
-  if (trace != nullptr && trace_layers <= 0) return bad("trace_layers must be positive");
-  g_trace = trace;
-  g_trace_layers = trace != nullptr ? trace_layers : 0;
   return 0;
 }
 

@@ -62,10 +62,23 @@ inline std::vector<std::int64_t> withLast(std::vector<std::int64_t> shape, std::
 // zero fill, which runs on torch's current stream, before any kernel on another stream uses it.
 class PersistentWorkspace {
  public:
-  void* get(std::size_t bytes, int device_id) {
+  // The node's buffer of at least `bytes`, zero-filled when first made (or grown). Making it
+  // allocates and synchronizes the device, which a stream under capture cannot do: such a call
+  // is refused with std::runtime_error (run the graph once eagerly before capturing it, as
+  // DecodeSession and GreedyDecoder do, so every node has its buffer).
+  void* get(std::size_t bytes, int device_id, void* stream) {
     if (bytes == 0) return nullptr;
     std::lock_guard<std::mutex> lock(mutex_);
     if (!buffer_.defined() || buffer_.nbytes() < bytes || buffer_.deviceId() != device_id) {
+      int capturing = 0;
+      if (int rc = dli_hip_stream_is_capturing(stream, &capturing))
+        throw std::runtime_error(std::string("workspace: ") + dli_hip_last_error() + " (" +
+                                 std::to_string(rc) + ")");
+      if (capturing != 0)
+        throw std::runtime_error(
+            "workspace: the first use of this node's scratch buffer is inside a stream capture; "
+            "run the graph once without capture first (the buffer is allocated and zero-filled "
+            "then, and reused by the captured graph)");
       const auto words = static_cast<std::int64_t>((bytes + 3) / 4);
       if (buffer_.defined()) retired_.push_back(buffer_);
       buffer_ = Tensor(at::zeros({words}, at::TensorOptions().dtype(at::kInt).device(at::kCUDA, device_id)));

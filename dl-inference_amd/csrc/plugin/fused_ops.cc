@@ -72,7 +72,7 @@ class QkvRopeAppendOp final : public Operator {
               ptr(*out[0]), ptr(e.key_pool), ptr(e.value_pool),
               static_cast<const std::int32_t*>(ptr(e.block_table)), e.block_size, e.max_blocks, m,
               hidden, hq, hkv, d, eps,
-              ws_bytes ? workspace_.get(ws_bytes, x.deviceId()) : nullptr, ws_bytes, ctx.stream),
+              ws_bytes ? workspace_.get(ws_bytes, x.deviceId(), ctx.stream) : nullptr, ws_bytes, ctx.stream),
           type());
   }
 
@@ -136,13 +136,15 @@ class PagedAttentionOp final : public Operator {
       throw std::invalid_argument("paged_attention: q does not match the cache entry");
     const std::int64_t B = q.dim(0), Hq = q.dim(1), D = q.dim(3);
     const float scale = static_cast<float>(attrDouble(attrs, "scale", 1.0 / std::sqrt(static_cast<double>(D))));
+    // key-range splits per (sequence, kv head); 0 = about one workgroup per CU
+    const auto splits = static_cast<int>(attrs.value_or<std::int64_t>("attention_splits", 0));
     *out[0] = Tensor::cuda(q.dtype(), q.shape(), q.deviceId());
     const std::size_t ws_bytes = dli_hip_paged_attention_workspace(B, Hq, 1, D, e->capacity());
     check(dli_hip_paged_attention(hipDtype(q.dtype()), ptr(q), ptr(e->key_pool), ptr(e->value_pool),
                                   static_cast<const std::int32_t*>(ptr(e->block_table)), ptr(*out[0]),
                                   B, Hq, e->heads, 1, D, e->block_size, e->max_blocks, 0, ptr(pos),
-                                  hipDtype(pos.dtype()), 1, scale,
-                                  workspace_.get(ws_bytes, q.deviceId()), ws_bytes, ctx.stream),
+                                  hipDtype(pos.dtype()), 1, scale, splits,
+                                  workspace_.get(ws_bytes, q.deviceId(), ctx.stream), ws_bytes, ctx.stream),
           type());
   }
 
@@ -172,7 +174,7 @@ class LinearResidualOp final : public Operator {
     const std::size_t ws_bytes = dli_hip_splitk_workspace(n, m, splits);
     check(dli_hip_linear_residual(ptr(x), ptr(w), in.size() == 4 ? ptr(*in[3]) : nullptr, ptr(res),
                                   ptr(*out[0]), m, n, k, splits,
-                                  workspace_.get(ws_bytes, x.deviceId()), ws_bytes, ctx.stream),
+                                  workspace_.get(ws_bytes, x.deviceId(), ctx.stream), ws_bytes, ctx.stream),
           type());
   }
 
@@ -207,7 +209,7 @@ class LinearResidualNormOp final : public Operator {
     const std::size_t ws_bytes = dli_hip_splitk_workspace(n, m, splits);
     check(dli_hip_linear_residual_norm(ptr(x), ptr(w), in.size() == 5 ? ptr(*in[4]) : nullptr,
                                        ptr(res), ptr(nw), ptr(*out[0]), ptr(*out[1]), m, n, k, eps,
-                                       splits, workspace_.get(ws_bytes, x.deviceId()), ws_bytes,
+                                       splits, workspace_.get(ws_bytes, x.deviceId(), ctx.stream), ws_bytes,
                                        ctx.stream),
           type());
   }
@@ -282,7 +284,10 @@ class LmHeadArgmaxOp final : public Operator {
 
 // All decoder layers in one launch (dli_hip_decoder_stack). inputs: hidden [B, H], positions
 // [B], cos, sin, then per layer: input_layernorm.weight, qkv_proj.weight, qkv_proj.bias,
-// o_proj.weight, post_attention_layernorm.weight, gate_up_proj.weight, down_proj.weight.
+// o_proj.weight, post_attention_layernorm.weight, gate_up_proj.weight, down_proj.weight; then,
+// optionally, a stage-timeline buffer (int64, layers x CUs x 24 entries: DliStackOptions.trace).
+// Attributes: attention_splits (0 = the launch's choice; the paged_attention node's count makes
+// the two bit-identical), down_splits, eps, kv_cache_prefix, check_status.
 // Layer i appends to and attends over cache entry kv_cache_prefix + i. Computes what the
 // five-launch layer (qkv_rope_append, paged_attention, linear_residual, gate_up_silu,
 // linear_residual with down_splits) computes, bit for bit.
@@ -293,8 +298,9 @@ class DecoderStackOp final : public Operator {
                const Attributes& attrs, ExecutionContext& ctx) const override {
     constexpr std::size_t kPerLayer = 7, kHead = 4;
     const auto layers = attrs.require<std::int64_t>("layers");
-    if (layers < 1 || in.size() != kHead + kPerLayer * static_cast<std::size_t>(layers))
-      throw std::invalid_argument("decoder_stack expects 4 + 7 * layers inputs");
+    const std::size_t n_in = kHead + kPerLayer * static_cast<std::size_t>(layers);
+    if (layers < 1 || (in.size() != n_in && in.size() != n_in + 1))
+      throw std::invalid_argument("decoder_stack expects 4 + 7 * layers inputs (+ a trace buffer)");
     if (out.size() != 1 && out.size() != 2)
       throw std::invalid_argument("decoder_stack outputs: hidden (, status)");
     requireArity(in, out, in.size(), in.size(), out.size(), type());
@@ -309,6 +315,21 @@ class DecoderStackOp final : public Operator {
     const auto d = attrs.require<std::int64_t>("head_dim");
     const auto eps = static_cast<float>(attrDouble(attrs, "eps", 1e-6));
     const auto down_splits = attrs.value_or<std::int64_t>("down_splits", 4);
+    DliStackOptions options{};
+    options.attention_splits =
+        static_cast<int>(attrs.value_or<std::int64_t>("attention_splits", 0));
+    if (in.size() == n_in + 1) {
+      const Tensor& trace = *in[n_in];
+      if (trace.dtype() != DType::Int64)
+        throw std::invalid_argument("decoder_stack trace buffer must be int64");
+      int cus = 0;
+      check(dli_hip_compute_units(&cus), type());
+      const auto per_layer = static_cast<std::int64_t>(cus) * 24;
+      options.trace_layers = static_cast<int>(static_cast<std::int64_t>(trace.numel()) / per_layer);
+      if (options.trace_layers < 1)
+        throw std::invalid_argument("decoder_stack trace buffer holds less than one layer");
+      options.trace = static_cast<unsigned long long*>(ptr(trace));
+    }
     const std::string prefix = attrs.value_or<std::string>("kv_cache_prefix", "layer_");
     const std::int64_t hidden = x.shape().back(), m = rowsOf(x);
     const std::int64_t n_qkv = (hq + 2 * hkv) * d;
@@ -349,20 +370,21 @@ class DecoderStackOp final : public Operator {
     *out[0] = Tensor::cuda(DType::BFloat16, x.shape(), x.deviceId());
     const std::size_t ws_bytes = dli_hip_decoder_stack_workspace(
         static_cast<int>(layers), m, hidden, hq, hkv, d, ffn, max_blocks,
-        static_cast<int>(down_splits));
+        static_cast<int>(down_splits), options.attention_splits);
+    if (ws_bytes == 0) throw std::invalid_argument("decoder_stack: unsupported geometry or splits");
     // The launch status accumulates in one persistent word per operator instance (the same
     // buffer every run, so a captured graph keeps reporting into it); the second output, when
     // the node lists one, is that word. A driver reads it after a synchronization it makes anyway
     // and zeroes it.
-    void* status = status_.get(sizeof(unsigned), x.deviceId());
+    void* status = status_.get(sizeof(unsigned), x.deviceId(), ctx.stream);
     check(dli_hip_decoder_stack(table.data(), static_cast<int>(layers), ptr(x), ptr(*out[0]),
                                 ptr(pos), hipDtype(pos.dtype()),
                                 static_cast<const float*>(ptr(cos)),
                                 static_cast<const float*>(ptr(sin)), cos.dim(0), block_size,
                                 max_blocks, m, hidden, hq, hkv, d, ffn, eps,
                                 static_cast<int>(down_splits),
-                                workspace_.get(ws_bytes, x.deviceId()), ws_bytes,
-                                static_cast<unsigned*>(status), ctx.stream),
+                                workspace_.get(ws_bytes, x.deviceId(), ctx.stream), ws_bytes,
+                                static_cast<unsigned*>(status), &options, ctx.stream),
           type());
     if (out.size() == 2) *out[1] = status_.tensor().withShape({1});
     // check_status (tests): wait for the launch and fail if a wait in it gave up

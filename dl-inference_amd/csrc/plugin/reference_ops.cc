@@ -286,8 +286,8 @@ class AttentionOp final : public Operator {
               dt, ptr(q), ptr(e.key_pool), ptr(e.value_pool),
               static_cast<const std::int32_t*>(ptr(e.block_table)), ptr(*out[0]), B, Hq, Hkv, Sq,
               D, e.block_size, e.max_blocks, past, positions ? ptr(*positions) : nullptr,
-              positions ? hipDtype(positions->dtype()) : DLI_I64, causal ? 1 : 0, scale,
-              workspace_.get(ws_bytes, q.deviceId()), ws_bytes, ctx.stream),
+              positions ? hipDtype(positions->dtype()) : DLI_I64, causal ? 1 : 0, scale, 0,
+              workspace_.get(ws_bytes, q.deviceId(), ctx.stream), ws_bytes, ctx.stream),
           type());
   }
 

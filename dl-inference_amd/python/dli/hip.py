@@ -34,6 +34,7 @@ _SIGNATURES = {
     "dli_hip_set_device": [_int],
     "dli_hip_compute_units": [ctypes.POINTER(_int)],
     "dli_hip_module_load": [_c_void_p, _size, ctypes.POINTER(_c_void_p)],
+    "dli_hip_code_object": [ctypes.c_char_p, ctypes.POINTER(_c_void_p), ctypes.POINTER(_size)],
     "dli_hip_module_get_function": [_c_void_p, ctypes.c_char_p, ctypes.POINTER(_c_void_p)],
     "dli_hip_module_unload": [_c_void_p],
     "dli_hip_launch": [_c_void_p, ctypes.c_uint, ctypes.c_uint, ctypes.c_uint, ctypes.c_uint,
@@ -84,7 +85,7 @@ _SIGNATURES = {
     "dli_hip_linear_workspace": [_int, _i64, _i64, _i64],
     "dli_hip_paged_attention_workspace": [_i64] * 5,
     "dli_hip_paged_attention": [_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p]
-    + [_i64] * 8 + [_c_void_p, _int, _int, _float, _c_void_p, _size, _c_void_p],
+    + [_i64] * 8 + [_c_void_p, _int, _int, _float, _int, _c_void_p, _size, _c_void_p],
     "dli_hip_argmax": [_int, _c_void_p, _c_void_p, _i64, _i64, _c_void_p],
     "dli_hip_splitk_workspace": [_i64, _i64, _int],
     "dli_hip_qkv_rope_append": [_c_void_p] * 6 + [_i64, _c_void_p, _int] + [_c_void_p] * 4
@@ -105,14 +106,12 @@ _SIGNATURES = {
                                     _c_void_p, _i64, _i64, _i64, _c_void_p, _size, _c_void_p],
     "dli_hip_lm_head_argmax_norm_noalloc": [_c_void_p, _c_void_p, _float, _c_void_p, _c_void_p,
                                             _int, _c_void_p, _i64, _i64, _i64, _c_void_p],
-    "dli_hip_decoder_stack_workspace": [_int] + [_i64] * 7 + [_int],
+    "dli_hip_decoder_stack_workspace": [_int] + [_i64] * 7 + [_int, _int],
     "dli_hip_decoder_stack": [_c_void_p, _int, _c_void_p, _c_void_p, _c_void_p, _int, _c_void_p,
                               _c_void_p] + [_i64] * 9 + [_float, _int, _c_void_p, _size,
-                                                         _c_void_p, _c_void_p],
+                                                         _c_void_p, _c_void_p, _c_void_p],
     "dli_hip_decoder_stack_status": [_c_void_p, ctypes.POINTER(_int), _c_void_p],
-    "dli_hip_decoder_stack_trace": [_c_void_p, _int],
     "dli_hip_stream_is_capturing": [_c_void_p, ctypes.POINTER(_int)],
-    "dli_hip_set_decode_attention_splits": [_int],
 }
 _RESTYPES = {
     "dli_hip_load_error": ctypes.c_char_p,
@@ -133,6 +132,11 @@ class DecoderLayer(ctypes.Structure):
     _fields_ = [(name, _c_void_p) for name in (
         "input_norm", "w_qkv", "b_qkv", "w_o", "post_norm", "w_gate_up", "w_down", "key_pool",
         "value_pool", "block_table")]
+
+
+class StackOptions(ctypes.Structure):
+    """DliStackOptions: per-call options of dli_hip_decoder_stack (include/dli_hip.h)."""
+    _fields_ = [("attention_splits", _int), ("trace", _c_void_p), ("trace_layers", _int)]
 
 
 class HipError(RuntimeError):

@@ -118,7 +118,8 @@ def _large_nodes(cfg: Qwen2Config, batch: int, nodes: list, splits: dict, fused:
                   {"kv_cache": f"layer_{i}", "q_heads": cfg.heads, "kv_heads": cfg.kv_heads,
                    "head_dim": cfg.head_dim, "eps": cfg.eps})
             _node(nodes, f"{p}.self_attn.attention", "paged_attention",
-                  [f"{t}_q_rotary", "positions"], [f"{t}_attention"], {"kv_cache": f"layer_{i}"})
+                  [f"{t}_q_rotary", "positions"], [f"{t}_attention"],
+                  {"kv_cache": f"layer_{i}", "attention_splits": splits.get("attn", 0)})
             _node(nodes, f"{p}.self_attn.merge", "reshape", [f"{t}_attention"],
                   [f"{t}_attention_merged"], {"shape": [batch, q_w]})
             _node(nodes, f"{p}.self_attn.o_proj", "linear_residual_norm",
@@ -185,7 +186,8 @@ def _fused_nodes(cfg: Qwen2Config, batch: int, nodes: list, splits: dict, logits
               {"kv_cache": f"layer_{i}", "q_heads": cfg.heads, "kv_heads": cfg.kv_heads,
                "head_dim": cfg.head_dim, "eps": cfg.eps})
         _node(nodes, f"{p}.self_attn.attention", "paged_attention", [f"{t}_q_rotary", "positions"],
-              [f"{t}_attention"], {"kv_cache": f"layer_{i}"})
+              [f"{t}_attention"],
+              {"kv_cache": f"layer_{i}", "attention_splits": splits.get("attn", 0)})
         _node(nodes, f"{p}.self_attn.merge", "reshape", [f"{t}_attention"], [f"{t}_attention_merged"],
               {"shape": [batch, cfg.heads * cfg.head_dim]})
         _node(nodes, f"{p}.self_attn.o_proj", "linear_residual",
@@ -209,10 +211,12 @@ def _head_nodes(cfg: Qwen2Config, nodes: list, h: str, logits_dtype: str):
 
 
 def _stack_nodes(cfg: Qwen2Config, nodes: list, splits: dict, logits_dtype: str,
-                 check_status: bool = False):
+                 check_status: bool = False, stack_trace: bool = False):
     """Every decoder layer in one decoder_stack node (one persistent launch), then the head
-    (model.norm inside lm_head_argmax) as in the fused graph. Same rounding points and values as the fused
-    graph with o split 1."""
+    (model.norm inside lm_head_argmax) as in the fused graph. Same rounding points and values as
+    the fused graph with o split 1 and the same attention split count (splits["attn"], 0 = each
+    path's own choice). stack_trace: the node also reads graph input "stack_trace", an int64
+    buffer that receives the launch's stage timeline."""
     inputs = ["hidden_states", "positions", "rotary_cos", "rotary_sin"]
     for i in range(cfg.layers):
         p = f"model.layers.{i}"
@@ -220,10 +224,13 @@ def _stack_nodes(cfg: Qwen2Config, nodes: list, splits: dict, logits_dtype: str,
                    f"{p}.self_attn.qkv_proj.bias", f"{p}.self_attn.o_proj.weight",
                    f"{p}.post_attention_layernorm.weight", f"{p}.mlp.gate_up_proj.weight",
                    f"{p}.mlp.down_proj.weight"]
+    if stack_trace:
+        inputs.append("stack_trace")
     _node(nodes, "model.layers", "decoder_stack", inputs, ["layers_output", "status"],
           {"layers": cfg.layers, "q_heads": cfg.heads, "kv_heads": cfg.kv_heads,
            "head_dim": cfg.head_dim, "eps": cfg.eps,
            "down_splits": splits.get("down", STACK_SPLITS["down"]),
+           "attention_splits": splits.get("attn", 0),
            "kv_cache_prefix": "layer_", "check_status": int(check_status)})
     _head_nodes(cfg, nodes, "layers_output", logits_dtype)
 
@@ -253,12 +260,15 @@ def uses_large_graph(cfg: Qwen2Config, fused: bool) -> bool:
 def build_decode_graph(cfg: Qwen2Config, batch: int, fused: bool = True,
                        splits: dict | None = None, logits_dtype: str = "float32",
                        stack: bool = False, check_status: bool = False,
-                       large_fused: bool = False) -> "dli.Graph":
+                       large_fused: bool = False, stack_trace: bool = False) -> "dli.Graph":
     """fused=False: the reference's node sequence; fused=True: five launches per layer;
     stack=True (with fused): all layers in one decoder_stack node (check_status: the node waits
     for its launch and fails if a workgroup gave up waiting; for tests, not for capture). With
     fused=True and a hidden size above 1024 (the Qwen2-7B shape) the step is the large-hidden
-    graph instead (_large_nodes; large_fused selects its GPU form), whatever `stack` says."""
+    graph instead (_large_nodes; large_fused selects its GPU form), whatever `stack` says.
+    splits: {"o", "down": K splits, "attn": attention key-range splits, 0 = each call's own
+    choice}; stack_trace: the decoder_stack node records its stage timeline into graph input
+    "stack_trace" (int64, layers x CUs x 24)."""
     nodes: list = []
     _node(nodes, "model.embed_tokens", "embedding", ["input_ids", "model.embed_tokens.weight"],
           ["hidden_states"])
@@ -268,15 +278,16 @@ def build_decode_graph(cfg: Qwen2Config, batch: int, fused: bool = True,
                  "inputs": INPUTS, "outputs": OUTPUTS, "nodes": nodes}
         return dli.Graph.from_json(json.dumps(graph))
     if fused and stack:
-        _stack_nodes(cfg, nodes, splits or STACK_SPLITS, logits_dtype, check_status)
+        _stack_nodes(cfg, nodes, splits or STACK_SPLITS, logits_dtype, check_status, stack_trace)
     elif fused:
         _fused_nodes(cfg, batch, nodes, splits or DEFAULT_SPLITS, logits_dtype)
     else:
         _reference_nodes(cfg, batch, nodes)
     model_type = "qwen2_decode" if not fused else ("qwen2_decode_stack" if stack else "qwen2_decode_fused")
     outputs = OUTPUTS + ["status"] if fused and stack else OUTPUTS
+    inputs = INPUTS + ["stack_trace"] if fused and stack and stack_trace else INPUTS
     graph = {"format": "dli.graph.v1", "model_type": model_type,
-             "inputs": INPUTS, "outputs": outputs, "nodes": nodes}
+             "inputs": inputs, "outputs": outputs, "nodes": nodes}
     return dli.Graph.from_json(json.dumps(graph))
 
 

@@ -20,7 +20,8 @@ class DecodeSession:
     def __init__(self, cfg: Qwen2Config, weights: dict, batch: int, max_seq_len: int,
                  fused: bool = True, engine: "dli.Engine | None" = None, splits: dict | None = None,
                  block_size: int = 64, logits_dtype: str = "float32", device: str = "cuda",
-                 stack: bool = False, check_status: bool = False, prefill: bool = False):
+                 stack: bool = False, check_status: bool = False, prefill: bool = False,
+                 stack_trace: "torch.Tensor | None" = None):
         self.cfg = cfg
         self.batch = batch
         self.fused = fused
@@ -30,9 +31,14 @@ class DecodeSession:
         # the large-hidden graph's GPU form (fused q|k|v, residual + RMSNorm and MLP nodes of
         # the GPU plugin; the ATen CPU plugin runs the reference's nodes)
         large_fused = uses_large_graph(cfg, fused) and device != "cpu" and not prefill
+        # stack_trace: int64 device buffer (layers x CUs x 24) for the decoder stack's stage
+        # timeline, written by every step
+        if stack_trace is not None and not self.stack:
+            raise ValueError("stack_trace needs the decoder stack graph")
         self.graph = build_decode_graph(cfg, batch, fused=fused, splits=splits,
                                         logits_dtype=logits_dtype, stack=stack,
-                                        check_status=check_status, large_fused=large_fused)
+                                        check_status=check_status, large_fused=large_fused,
+                                        stack_trace=stack_trace is not None)
         # prefill=True: generate() runs the prompt through one prefill graph (the layers over
         # [B, S] tokens at once), which reads the unpacked q/k/v and gate/up weights
         self.prefill = prefill
@@ -47,6 +53,8 @@ class DecodeSession:
         self.positions = torch.zeros(batch, dtype=torch.int64, device=device)
         tensors["input_ids"] = self.ids
         tensors["positions"] = self.positions
+        if stack_trace is not None:
+            tensors["stack_trace"] = stack_trace
         self.inputs = tensors
         self.max_seq_len = max_seq_len
         self._graph = None
@@ -124,7 +132,10 @@ class DecodeSession:
         graph = self._prefill_graphs.get(s)
         if graph is None:
             on_gpu = prompt.is_cuda and self.fused and not uses_large_graph(self.cfg, self.fused)
-            graph = build_prefill_graph(self.cfg, b, s, fused_head=prompt.is_cuda, fused=on_gpu)
+            # lm_head_argmax holds a tile's rows in registers (hidden <= 1024): larger hiddens
+            # take rms_norm + linear + argmax
+            fused_head = prompt.is_cuda and not uses_large_graph(self.cfg, True)
+            graph = build_prefill_graph(self.cfg, b, s, fused_head=fused_head, fused=on_gpu)
             self._prefill_graphs[s] = graph
         self.engine.set_kv_cache_length(0)  # the prompt starts every sequence at position 0
         inputs = dict(self.inputs)

@@ -87,6 +87,12 @@ int dli_hip_set_device(int device);
 /* Module load + launch (CudaAotKernel::load / launch, cuda_driver.cc:107-129). A launch with
  * any grid dimension 0 returns 0 without touching the runtime (cuda_driver.cc:123). */
 int dli_hip_module_load(const void* image, size_t image_bytes, void** module);
+/* Image of the library's embedded gfx950 code object `name` ("attention", "conv", "decode",
+ * "elementwise", "flash_attention", "gemm", "mfma_gemm", "norm", "stack"), for
+ * dli_hip_module_load. The reference's counterpart is the cubin file its plugin reads next to
+ * itself (CudaAotKernel::load, cuda_driver.cc:107-117); here the images live inside the library.
+ * The image stays valid while the library is loaded. */
+int dli_hip_code_object(const char* name, const void** image, size_t* image_bytes);
 int dli_hip_module_get_function(void* module, const char* name, void** function);
 int dli_hip_module_unload(void* module);
 int dli_hip_launch(void* function, unsigned grid_x, unsigned grid_y, unsigned grid_z,
@@ -256,9 +262,11 @@ int dli_hip_kv_append(int dtype, const void* key, const void* value, void* key_p
  * `past`); the query at index i sits at position past_len + i and, when causal, sees keys
  * at positions <= past_len + i. Split along the keys across workgroups ("flash decoding");
  * partial results and per-(sequence, kv head) arrival counters go to `workspace` (size from
- * dli_hip_paged_attention_workspace). The workspace must be zero-filled before its first use;
- * every call leaves the counters at zero again. Calls sharing a workspace must be ordered
- * (same stream). */
+ * dli_hip_paged_attention_workspace, the same offsets for every head_dim). The workspace must be
+ * zero-filled before its first use; every call leaves the counters at zero again. Calls sharing
+ * a workspace must be ordered (same stream). splits: the key-range split count of the MFMA
+ * decode kernel (bf16, one query per sequence), 0 = about one workgroup per CU, else in [1, 32];
+ * dli_hip_decoder_stack with the same attention_splits gives bit-identical results. */
 size_t dli_hip_paged_attention_workspace(int64_t batch, int64_t q_heads, int64_t seq_q,
                                          int64_t head_dim, int64_t max_tokens);
 int dli_hip_paged_attention(int dtype, const void* q, const void* key_pool,
@@ -266,8 +274,8 @@ int dli_hip_paged_attention(int dtype, const void* q, const void* key_pool,
                             int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t seq_q,
                             int64_t head_dim, int64_t block_size, int64_t max_blocks,
                             int64_t past, const void* positions, int positions_dtype,
-                            int causal, float scale, void* workspace, size_t workspace_bytes,
-                            void* stream);
+                            int causal, float scale, int splits, void* workspace,
+                            size_t workspace_bytes, void* stream);
 
 /* ids[r] = first index of the maximum of row r of x [rows, width] (torch.argmax rule). */
 int dli_hip_argmax(int dtype, const void* x, int64_t* ids, int64_t rows, int64_t width,
@@ -433,20 +441,40 @@ typedef struct DliDecoderLayer {
   const int32_t* block_table;  /* [batch, max_blocks] */
 } DliDecoderLayer;
 
+/* Per-call options of dli_hip_decoder_stack (NULL = all zero).
+ * attention_splits: key-range splits per (sequence, kv head) attention pair, 0 = spread the
+ *   pairs over the CUs the q|k|v stage leaves free, else in [1, 32] (the same count as
+ *   dli_hip_paged_attention's splits gives bit-identical results).
+ * trace, trace_layers: stage timeline (no counterpart in the reference; its profiler exists only
+ *   as a design, .codex/profiling_design.md). With trace non-NULL the launch stamps the 100 MHz
+ *   real-time counter (s_memrealtime) at the stage boundaries of each workgroup:
+ *   trace[(layer * grid + workgroup) * 24 + event] for layer < trace_layers, where grid is the
+ *   launch's workgroup count (one per CU) and the events are those of dli_stack::kTr* in
+ *   csrc/kernels/stack_args.h (0 = layer entry ... 12 = down_proj done). The buffer holds
+ *   trace_layers * grid * 24 uint64 of device memory; events a workgroup does not reach are left
+ *   as they were. */
+typedef struct DliStackOptions {
+  int attention_splits;
+  unsigned long long* trace;
+  int trace_layers;
+} DliStackOptions;
+
 /* Workspace bytes for dli_hip_decoder_stack with num_layers layers (arrival counters, partials
  * and one activation slab per layer of a launch, so no activation buffer is reused within a
- * launch). */
+ * launch), for the given down_splits and attention_splits (0 = the launch's own choice). */
 size_t dli_hip_decoder_stack_workspace(int num_layers, int64_t batch, int64_t hidden_size,
                                        int64_t q_heads, int64_t kv_heads, int64_t head_dim,
-                                       int64_t ffn, int64_t max_blocks, int down_splits);
+                                       int64_t ffn, int64_t max_blocks, int down_splits,
+                                       int attention_splits);
 
 /* hidden_out = the residual stream after `num_layers` layers applied to hidden_in [batch,
  * hidden_size] (hidden_out may equal hidden_in). Each layer appends its new k/v at
  * positions[b] and attends over keys [0, positions[b]]. The workspace must be zero-filled
  * before its first use; every call leaves it ready for the next one on the same stream. Calls
  * that share a workspace must not overlap.
- * The launch is refused when the device cannot hold every workgroup resident at once, and runs
- * as a cooperative launch outside stream capture. status (device memory, may be NULL): when
+ * The launch is refused when the device cannot hold every workgroup resident at once; it is a
+ * plain kernel launch (or graph node), so work running on other streams at the same time can hold
+ * workgroups back and make a wait give up (reported through status). status (device memory, may be NULL): when
  * non-NULL, a launch in which a wait gave up ORs a non-zero value into *status and clears the
  * workspace's abort word, so later launches run normally; the caller reads *status after a
  * synchronization it already makes and zeroes it. With status NULL the abort word stays set for
@@ -458,24 +486,7 @@ int dli_hip_decoder_stack(const DliDecoderLayer* layers, int num_layers, const v
                           int64_t hidden_size, int64_t q_heads, int64_t kv_heads,
                           int64_t head_dim, int64_t ffn, float eps, int down_splits,
                           void* workspace, size_t workspace_bytes, unsigned* status,
-                          void* stream);
-
-/* Sets the key-range split count of MFMA decode attention for every later call of
- * dli_hip_paged_attention and dli_hip_decoder_stack in the process (0 = choose per call: the
- * stand-alone kernel spreads over all CUs, the decoder stack over the CUs its q|k|v stage leaves
- * free). Equal counts make the two paths bit-identical. splits in [0, 32]. */
-int dli_hip_set_decode_attention_splits(int splits);
-
-/* Stage timeline of the decoder stack (no counterpart in the reference; its profiler exists only
- * as a design, .codex/profiling_design.md). With trace non-NULL, every later
- * dli_hip_decoder_stack launch in the process stamps the 100 MHz real-time counter
- * (s_memrealtime) at the stage boundaries of each workgroup:
- * trace[(layer * grid + workgroup) * 24 + event] for layer < trace_layers, where grid is the
- * launch's workgroup count (one per CU) and the events are those of dli_stack::kTr* in
- * csrc/kernels/stack_args.h (0 = layer entry ... 12 = down_proj done). The buffer holds
- * trace_layers * grid * 24 uint64 of device memory and must stay valid while such launches run;
- * events a workgroup does not reach are left as they were. NULL turns it off. */
-int dli_hip_decoder_stack_trace(unsigned long long* trace, int trace_layers);
+                          const DliStackOptions* options, void* stream);
 
 /* Synchronizes `stream`, then *aborted = 1 when a launch since the last query gave up waiting
  * for another workgroup (its outputs are invalid; this can only happen when the workgroups

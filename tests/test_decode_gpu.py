@@ -258,20 +258,24 @@ def test_qwen2_0_5b_shape_step_at_context_4096_matches_oracle(batch):
 
 
 @pytest.mark.slow
-def test_qwen2_0_5b_shape_fp32_reference_graph_identical_greedy_ids():
+@pytest.mark.parametrize("batch", [1, 4, 8, 32])
+def test_qwen2_0_5b_shape_fp32_reference_graph_identical_greedy_ids(batch):
     """The reference's own precision: the reference-style graph (the exporter's 19 nodes per
-    layer) in fp32 at the Qwen2-0.5B shape, batch 4, 512 random prompt tokens fed through the
-    decode step, then 64 greedy tokens. They must equal the fp32 oracle's free-running greedy
-    tokens exactly (prefill as one batched pass, then one step per token)."""
+    layer) in fp32 at the Qwen2-0.5B shape, 512 random prompt tokens fed through the decode step,
+    then 64 greedy tokens, at the config's batches 1, 8 and 32 (and 4). Every row must equal the
+    fp32 oracle's free-running greedy tokens exactly (prefill as one batched pass, then one step
+    per token): the bar of the reference's end-to-end test (tests/e2e/test_models.py:61-71)."""
     cfg = QWEN2_0_5B
     w = random_weights(cfg, seed=47, device="cuda", dtype=torch.float32)
-    prompt = _prompt(cfg, 4, 512, 48)
-    session = DecodeSession(cfg, w, 4, max_seq_len=512 + 64 + 8, fused=False).capture()
+    prompt = _prompt(cfg, batch, 512, 48)
+    session = DecodeSession(cfg, w, batch, max_seq_len=512 + 64 + 8, fused=False).capture()
     got = session.generate(prompt.cuda(), 64).cpu()
     expect, margins = Qwen2Oracle(cfg, w, round_bf16=False).generate(prompt, 64)
-    first = [(got[r] != expect[r]).nonzero()[:1].tolist() for r in range(4)]
-    print(f"\nfp32 greedy over 64 steps: smallest top-1/top-2 oracle margin "
-          f"{float(margins.min()):.3e}; first differing step per row {first}", flush=True)
+    differ = [r for r in range(batch) if not torch.equal(got[r], expect[r])]
+    first = {r: int((got[r] != expect[r]).nonzero()[0]) for r in differ}
+    print(f"\nfp32 greedy, batch {batch}, 64 steps: smallest top-1/top-2 oracle margin "
+          f"{float(margins.min()):.3e}; rows differing {len(differ)} of {batch}, first differing "
+          f"step per such row {first}", flush=True)
     assert torch.equal(got, expect)
 
 
@@ -330,3 +334,97 @@ def test_qwen2_7b_shape_step_at_context_8192_matches_oracle():
     assert float(err_bf16.max()) <= 1.5 * float(noise.max())
     flips = _flip_report(logits, ref, exact, nxt, torch.argmax(ref, -1))
     print(f"tokens: {batch - len(flips)}/{batch} equal to the oracle's argmax", flush=True)
+
+
+def _new_kv(engine, layer, batch, pos):
+    """The key and value the step wrote at position pos of every row, from the paged pools of
+    cache entry layer_<layer> (key [blocks, Hkv, 64, D], value [blocks, Hkv, D, 64]):
+    [B, Hkv, D] each, float32 on the host."""
+    e = engine.kv_cache_entry(f"layer_{layer}")
+    bs = e["block_size"]
+    blocks = e["block_table"].long()[:, pos // bs]
+    slot = pos % bs
+    k = e["key_pool"][blocks][:, :, slot, :]
+    v = e["value_pool"][blocks][:, :, :, slot]
+    return k.float().cpu(), v.float().cpu()
+
+
+@pytest.mark.slow
+def test_qwen2_7b_shape_full_model_step_at_context_8192():
+    """Config 5 at full size: all 28 Qwen2-7B-shape layers, batch 64, every row at position 8191
+    over an 8191-key context in every layer (15 GB of weights, 30 GB of paged cache), through the
+    large-hidden decode graph. The whole model is too large for the oracle, so the run is held to
+    properties: next_ids == argmax(logits); a HIP-graph replay of the step equals the eager step
+    bit for bit (logits, ids and the K/V it appended in every layer); and the K/V that layers 0
+    and 1 appended equal, at the bf16 bar, those of the oracle's 2-layer slice of the same model
+    on the same context (layer 1's input is layer 0's whole output, attention over 8192 keys
+    included)."""
+    from dataclasses import replace
+
+    from dli_qwen2 import QWEN2_7B
+
+    cfg, ctx, batch = QWEN2_7B, 8192, 64
+    pos_i = ctx - 1
+    w = random_weights(cfg, seed=97, device="cuda")
+    ids = torch.randint(0, cfg.vocab, (batch,), generator=torch.Generator().manual_seed(98))
+    session = DecodeSession(cfg, w, batch, max_seq_len=ctx + 8)
+    pos = torch.full((batch,), pos_i, dtype=torch.int64, device="cuda")
+    session.step(ids.cuda(), pos)  # creates the cache entries (the context is written next)
+    torch.cuda.synchronize()
+    sliced = {k: v.cpu() for k, v in w.items()
+              if not k.startswith("model.layers.") or int(k.split(".")[2]) < 2}
+    oracle = Qwen2Oracle(replace(cfg, layers=2), sliced)
+    oracle.reset_static(batch, ctx, seed=99, fill=pos_i)
+    _fill_paged_cache(session.engine, oracle, 2, batch, pos_i)
+    g = torch.Generator(device="cuda").manual_seed(100)
+    for i in range(2, cfg.layers):  # the other layers' context: seeded N(0, 1) bf16
+        e = session.engine.kv_cache_entry(f"layer_{i}")
+        for pool in (e["key_pool"], e["value_pool"]):
+            pool.copy_(torch.randn(pool.shape, generator=g, device="cuda").to(pool.dtype))
+    torch.cuda.synchronize()
+    del sliced
+
+    logits, nxt = session.step(ids.cuda(), pos)
+    logits, nxt = logits.clone(), nxt.clone()
+    torch.cuda.synchronize()
+    eager_kv = [_new_kv(session.engine, i, batch, pos_i) for i in range(cfg.layers)]
+    assert bool(torch.isfinite(logits).all())
+    assert torch.equal(nxt, torch.argmax(logits, -1)), "next_ids != argmax(logits)"
+
+    session.capture()  # its warm-up step rewrites position 8191 with the same values
+    session.ids.copy_(ids.cuda())
+    session.positions.copy_(pos)
+    out = session.replay()
+    torch.cuda.synchronize()
+    session.check_status()
+    assert torch.equal(out["logits"], logits), "graph replay logits differ from the eager step"
+    assert torch.equal(out["next_ids"], nxt)
+    for i in range(cfg.layers):
+        k, v = _new_kv(session.engine, i, batch, pos_i)
+        assert torch.equal(k, eager_kv[i][0]) and torch.equal(v, eager_kv[i][1]), f"layer {i}"
+
+    oracle.step_static(ids, pos_i)  # writes the slice's new K/V at position 8191
+    for i in range(2):
+        ref_k = oracle.k_static[i][:, :, pos_i]
+        ref_v = oracle.v_static[i][:, :, pos_i]
+        k, v = eager_kv[i]
+        for name, a, b in (("key", k, ref_k), ("value", v, ref_v)):
+            rel = float((a - b).norm() / b.norm())
+            print(f"\nlayer {i} {name} appended at {pos_i}: relative L2 error {rel:.3e}",
+                  flush=True)
+            assert rel <= 1e-2, f"layer {i} {name}: relative error {rel:.3e}"
+            torch.testing.assert_close(a, b, rtol=2e-2, atol=2e-2)
+
+
+def test_large_hidden_prefill_graph_then_decode_teacher_forced_parity():
+    """A large-hidden model (the Qwen2-7B geometry, one layer) with its prompt through the
+    prefill graph: the head is rms_norm + linear + argmax there (lm_head_argmax holds at most
+    1024 columns), then greedy steps; every row scored by the oracle."""
+    from dataclasses import replace
+
+    from dli_qwen2 import QWEN2_7B
+
+    cfg = replace(QWEN2_7B, layers=1)
+    w = random_weights(cfg, seed=101, device="cuda")
+    _teacher_forced_parity(cfg, w, batch=2, prompt_len=8, steps=4, seed=102, agree_min=0.75,
+                           prefill=True)

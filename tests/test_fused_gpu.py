@@ -330,3 +330,32 @@ def test_paged_attention_decode(B, positions, max_seq, geometry):
         v = np.concatenate([vp[blk].transpose(0, 2, 1) for blk in blocks], axis=1)[:, :n]  # [Hkv, n, D]
         ref = ops.attention(to_np(q[i:i + 1]), k[None], v[None], causal=True)
         assert_close(out[i:i + 1], ref, "bfloat16")
+
+
+def test_workspace_first_use_inside_a_capture_is_refused():
+    """A node whose scratch buffer would be allocated and zero-filled inside a stream capture is
+    refused with a clear error (the allocation and its device synchronization cannot be
+    captured); after one eager run the same node captures and replays, equal to eager."""
+    from support import one_node_graph
+
+    x, w, res = rand((8, 896), 24), rand((896, 896), 25, 0.03), rand((8, 896), 26)
+    inputs = {"x": x, "w": w, "res": res}
+    graph = one_node_graph("linear_residual", inputs, attrs={"splits": 3})
+    e = dli.Engine().load_plugin()  # its linear_residual node has no buffer yet
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with pytest.raises(RuntimeError, match="inside a stream capture"):
+        with torch.cuda.graph(g):
+            e.run(graph, inputs)
+    del g
+    torch.cuda.synchronize()
+    eager = e.run(graph, inputs)["output"].clone()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = e.run(graph, inputs)["output"]
+    for _ in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+    assert_close(eager, _residual_oracle(x, w, res, None), "bfloat16")

@@ -54,6 +54,20 @@ def test_no_device_behaviour():
     assert b"unavailable" in lib.dli_hip_last_error()
 
 
+def test_embedded_code_objects_are_gfx950_elf_images():
+    """dli_hip_code_object hands out the embedded code objects (the images dli_hip_module_load
+    takes): AMDGPU ELF files; an unknown name is an error."""
+    lib = hip.load()
+    image, size = ctypes.c_void_p(), ctypes.c_size_t()
+    for name in (b"elementwise", b"decode", b"stack", b"mfma_gemm"):
+        assert lib.dli_hip_code_object(name, ctypes.byref(image), ctypes.byref(size)) == 0
+        head = ctypes.string_at(image.value, 20)
+        assert size.value > 1024 and head[:4] == b"\x7fELF"
+        assert int.from_bytes(head[18:20], "little") == 224  # e_machine EM_AMDGPU
+    assert lib.dli_hip_code_object(b"nope", ctypes.byref(image), ctypes.byref(size)) == -1
+    assert b"no embedded code object named nope" in lib.dli_hip_last_error()
+
+
 def test_grid_zero_launch_and_empty_work_are_noops():
     lib = hip.load()
     assert lib.dli_hip_launch(None, 0, 1, 1, 64, 1, 1, 0, None, None) == 0
@@ -165,10 +179,10 @@ def test_decoder_stack_rejects_invalid_arguments():
     fake = ctypes.c_void_p(256)
 
     def call(layers=ctypes.byref(layer), n=1, positions=fake, pos_dtype=hip.I64, block_size=64,
-             batch=32, hidden=896, hq=14, hkv=2, d=64, ffn=4864, splits=4):
+             batch=32, hidden=896, hq=14, hkv=2, d=64, ffn=4864, splits=4, options=None):
         return lib.dli_hip_decoder_stack(layers, n, fake, fake, positions, pos_dtype, fake, fake,
                                          1024, block_size, 64, batch, hidden, hq, hkv, d, ffn,
-                                         1e-6, splits, fake, 1 << 20, None, None)
+                                         1e-6, splits, fake, 1 << 20, None, options, None)
 
     assert call(n=0) == 0  # no layers: nothing to do
     assert call(layers=None) == -1
@@ -191,3 +205,9 @@ def test_decoder_stack_rejects_invalid_arguments():
     assert call(layers=ctypes.byref(missing)) == -1
     assert b"layer 0 has a NULL pointer" in lib.dli_hip_last_error()
     assert lib.dli_hip_decoder_stack_status(None, None, None) == -1
+    # per-call options: the attention split count and the trace buffer travel with the call
+    assert call(options=ctypes.byref(hip.StackOptions(33, None, 0))) == -1
+    assert b"attention_splits must be in [0, 32]" in lib.dli_hip_last_error()
+    assert call(options=ctypes.byref(hip.StackOptions(0, 256, 0))) == -1
+    assert b"trace_layers must be positive" in lib.dli_hip_last_error()
+    assert lib.dli_hip_decoder_stack_workspace(24, 32, 896, 14, 2, 64, 4864, 65, 3, 33) == 0

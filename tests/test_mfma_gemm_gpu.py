@@ -215,16 +215,18 @@ def test_reference_tiny_alexnet_end_to_end(fused):
     close_f32(out, expect)  # the reference test allows rtol 5e-3, atol 2e-2
 
 
+@pytest.mark.parametrize("batch", [2, 64])
 @pytest.mark.parametrize("fused", [False, True], ids=["relu_nodes", "fused_relu"])
-def test_alexnet_cifar_graph(fused):
-    """The AlexNet-style fp32 benchmark network (dli_alexnet) at batch 2 against ATen on the
-    CPU (fp32; relative L2 error of the logits, and per element at the fp32 tolerance)."""
+def test_alexnet_cifar_graph(fused, batch):
+    """The AlexNet-style fp32 benchmark network (dli_alexnet) against ATen in float64 on the CPU
+    (per element at the fp32 tolerance). Batch 64 is the benchmark's batch: the split-K and
+    tile choices it makes (conv splits over the patch, FC splits over K) run here."""
     import dli_alexnet as net
 
     w = net.random_weights(seed=3)
-    x = torch.randn((2,) + net.IMAGE, generator=torch.Generator().manual_seed(4))
+    x = torch.randn((batch,) + net.IMAGE, generator=torch.Generator().manual_seed(4))
     ref = net.torch_forward(x.double(), {k: v.double() for k, v in w.items()}).numpy()
-    out = plugin_engine().run(net.build_graph(2, fused=fused),
+    out = plugin_engine().run(net.build_graph(batch, fused=fused),
                               {"x": x.cuda(), **{k: v.cuda() for k, v in w.items()}})["logits"]
     torch.cuda.synchronize()
     close_f32(out, ref)

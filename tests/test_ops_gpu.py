@@ -245,3 +245,44 @@ def test_plugin_uses_native_library():
     from dli import hip
 
     assert hip.lib().dli_hip_available() == 1, hip.lib().dli_hip_load_error()
+
+
+def test_public_launch_and_allocator_abi_runs_a_kernel():
+    """The CudaAotKernel / cuda_runtime replacement from the C ABI alone (the reference's
+    tests/cpp/test_cuda_aot_kernel.cc and cuda_driver.cc:107-129): the embedded elementwise code
+    object through dli_hip_module_load, its add_f32 kernel through dli_hip_module_get_function,
+    buffers through dli_hip_malloc and dli_hip_memcpy, one dli_hip_launch, results against the
+    oracle's add (add/kernel.py:6-11: out[i] = a[i] + b[i % width]), then unload and free."""
+    import ctypes
+
+    from dli import hip
+
+    lib = hip.load()
+    image, size = ctypes.c_void_p(), ctypes.c_size_t()
+    assert lib.dli_hip_code_object(b"elementwise", ctypes.byref(image), ctypes.byref(size)) == 0
+    module, fn = ctypes.c_void_p(), ctypes.c_void_p()
+    hip.call("dli_hip_module_load", image, size.value, ctypes.byref(module))
+    hip.call("dli_hip_module_get_function", module, b"add_f32", ctypes.byref(fn))
+    total, width = 3000, 7
+    rng = np.random.default_rng(5)
+    a = rng.standard_normal(total).astype(np.float32)
+    b = rng.standard_normal(width).astype(np.float32)
+    dev = [ctypes.c_void_p() for _ in range(3)]
+    for buf, n in zip(dev, (total, width, total)):
+        hip.call("dli_hip_malloc", n * 4, ctypes.byref(buf))
+    try:
+        hip.call("dli_hip_memcpy", dev[0], a.ctypes.data, total * 4, 1)  # host to device
+        hip.call("dli_hip_memcpy", dev[1], b.ctypes.data, width * 4, 1)
+        n_total, n_width = ctypes.c_int64(total), ctypes.c_int64(width)
+        args = (ctypes.c_void_p * 5)(*[ctypes.addressof(x) for x in
+                                       (dev[0], dev[1], dev[2], n_total, n_width)])
+        # the kernel is grid-strided with 256 threads per workgroup
+        hip.call("dli_hip_launch", fn, 4, 1, 1, 256, 1, 1, 0, None, args)
+        hip.call("dli_hip_device_synchronize")
+        out = np.empty(total, dtype=np.float32)
+        hip.call("dli_hip_memcpy", out.ctypes.data, dev[2], total * 4, 2)  # device to host
+    finally:
+        for buf in dev:
+            hip.call("dli_hip_free", buf)
+        hip.call("dli_hip_module_unload", module)
+    np.testing.assert_array_equal(out, ops.add(a, b).astype(np.float32))

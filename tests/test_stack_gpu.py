@@ -11,19 +11,9 @@ from __future__ import annotations
 import pytest
 import torch
 
-from dli import hip
 from dli_qwen2 import QWEN2_0_5B, DecodeSession, random_weights, tiny_config
 
 pytestmark = pytest.mark.gpu
-
-
-@pytest.fixture(autouse=True)
-def same_attention_splits():
-    """Both paths split each attention pair's keys the same way (by default the stack spreads
-    attention over the CUs its q|k|v stage leaves free, the stand-alone kernel over all CUs)."""
-    hip.call("dli_hip_set_decode_attention_splits", 3)
-    yield
-    hip.call("dli_hip_set_decode_attention_splits", 0)
 
 
 def _prompt(cfg, batch, length, seed):
@@ -56,10 +46,12 @@ def _assert_same(fused, stack, a, b, layers):
         assert torch.equal(ea["value_pool"], eb["value_pool"]), f"value cache of layer {i} differs"
 
 
-def _pair(cfg, w, batch, max_seq_len, down=1, **kw):
+def _pair(cfg, w, batch, max_seq_len, down=1, attn=3, **kw):
     """A fused and a stack session with the same down_proj split-K (1: one workgroup reduces a
-    tile over the full K; more: the last split to finish merges the partials)."""
-    splits = {"o": 1, "down": down}
+    tile over the full K; more: the last split to finish merges the partials) and the same
+    attention split count per (sequence, kv head) pair (by default the stack spreads attention
+    over the CUs its q|k|v stage leaves free, the stand-alone kernel over all CUs)."""
+    splits = {"o": 1, "down": down, "attn": attn}
     fused = DecodeSession(cfg, w, batch, max_seq_len=max_seq_len, fused=True, splits=splits)
     stack = DecodeSession(cfg, w, batch, max_seq_len=max_seq_len, fused=True, stack=True,
                           splits=splits, check_status=True, **kw)
@@ -105,7 +97,7 @@ def test_stack_graph_replay_equals_fused_eager():
     cfg = tiny_config(layers=2)
     w = random_weights(cfg, seed=51, device="cuda")
     prompt = _prompt(cfg, 8, 4, 52)
-    splits = {"o": 1, "down": 1}
+    splits = {"o": 1, "down": 1, "attn": 3}
     fused = DecodeSession(cfg, w, 8, max_seq_len=64, splits=splits)
     stack = DecodeSession(cfg, w, 8, max_seq_len=64, stack=True, splits=splits).capture()
     _assert_same(fused, stack, _run_steps(fused, prompt, 5), _run_steps(stack, prompt, 5),
@@ -147,11 +139,10 @@ def _fill_caches(sessions, cfg, seed):
 def test_stack_long_context_split_merge_bitwise(splits):
     """Context up to 4096 keys: every pair's keys are split over several workgroups and merged
     by the last to finish, in both paths."""
-    hip.call("dli_hip_set_decode_attention_splits", splits)
     cfg = tiny_config(layers=2)
     w = random_weights(cfg, seed=81, device="cuda")
     batch = 32
-    fused, stack = _pair(cfg, w, batch, 4096 + 64)
+    fused, stack = _pair(cfg, w, batch, 4096 + 64, attn=splits)
     start = torch.tensor([4000 - 37 * b for b in range(batch)], device="cuda")
     ids0 = torch.randint(0, cfg.vocab, (batch,), generator=torch.Generator().manual_seed(82))
     outs = []
@@ -171,22 +162,20 @@ def test_stack_long_context_split_merge_bitwise(splits):
 
 
 def test_stack_trace_timeline():
-    """dli_hip_decoder_stack_trace: every workgroup stamps its layer entries in order, each
-    layer's stage stamps after its entry, and the stamps do not change the results (the traced
-    run matches the fused graph bit for bit). Off again, the buffer is left alone."""
+    """The stage timeline (a trace buffer input of the decoder_stack node, DliStackOptions.trace):
+    every workgroup stamps its layer entries in order, each layer's stage stamps after its entry,
+    and the stamps do not change the results (the traced run matches the fused graph bit for
+    bit). A session without the buffer, running at the same time, leaves it alone."""
     cfg = tiny_config(layers=3)
     w = random_weights(cfg, seed=71, device="cuda")
     prompt = _prompt(cfg, 8, 3, 72)
-    fused, stack = _pair(cfg, w, 8, 128, down=3)
     grid = torch.cuda.get_device_properties(0).multi_processor_count
     events = 24  # dli_stack::kTraceEvents
     trace = torch.zeros(cfg.layers * grid * events, dtype=torch.int64, device="cuda")
-    hip.call("dli_hip_decoder_stack_trace", trace.data_ptr(), cfg.layers)
-    try:
-        traced = _run_steps(stack, prompt, 1)
-        torch.cuda.synchronize()
-    finally:
-        hip.call("dli_hip_decoder_stack_trace", None, 0)
+    fused, stack = _pair(cfg, w, 8, 128, down=3, stack_trace=trace)
+    _, untraced = _pair(cfg, w, 8, 128, down=3)
+    traced = _run_steps(stack, prompt, 1)
+    torch.cuda.synchronize()
     _assert_same(fused, stack, _run_steps(fused, prompt, 1), traced, cfg.layers)
     t = trace.view(cfg.layers, grid, events).cpu()
     start = t[:, :, 0]  # kTrLayerStart: written by every workgroup in every layer
@@ -199,13 +188,16 @@ def test_stack_trace_timeline():
     # the stamps of one layer end before the next layer's entries of the same workgroup
     assert bool((later[:-1].amax(dim=2) <= start[1:]).all())
     before = trace.clone()
-    _run_steps(stack, prompt[:, :1], 0, start=3)
+    _run_steps(untraced, prompt[:, :1], 0, start=3)
     torch.cuda.synchronize()
-    assert torch.equal(trace, before), "the trace buffer changed after tracing was turned off"
+    assert torch.equal(trace, before), "a session without the trace buffer wrote to it"
 
 
-def test_stack_trace_rejects_bad_arguments():
-    buf = torch.zeros(16, dtype=torch.int64, device="cuda")
-    with pytest.raises(hip.HipError):
-        hip.call("dli_hip_decoder_stack_trace", buf.data_ptr(), 0)
-    hip.call("dli_hip_decoder_stack_trace", None, 0)
+def test_stack_trace_buffer_too_small_is_rejected():
+    cfg = tiny_config(layers=2)
+    w = random_weights(cfg, seed=73, device="cuda")
+    buf = torch.zeros(16, dtype=torch.int64, device="cuda")  # less than one layer
+    _, stack = _pair(cfg, w, 4, 64, stack_trace=buf)
+    with pytest.raises(ValueError, match="trace buffer"):
+        stack.step(torch.zeros(4, dtype=torch.int64, device="cuda"),
+                   torch.zeros(4, dtype=torch.int64, device="cuda"))
