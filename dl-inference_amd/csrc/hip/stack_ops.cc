@@ -7,6 +7,8 @@
 #include "../kernels/stack_args.h"
 #include "runtime.h"
 
+static_assert(dli_stack::kTraceEvents == DLI_STACK_TRACE_EVENTS, "trace layout of include/dli_hip.h");
+
 namespace dli::hip {
 namespace {
 
@@ -32,10 +34,11 @@ int tileRows(int64_t m) { return m <= 16 ? 16 : (m <= 32 ? 32 : 64); }
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 // Workspace regions, each 256-byte aligned: arrival counters, attention partials, down_proj
-// partials, then one activation slab per layer of a launch (q, attn, h_mid, act, h; bf16
-// elements, offsets relative to the slab).
+// partials, x0 (the launch input in fragment order), then one activation slab per layer of a
+// launch (q, attn, h_mid, act, h; bf16 elements, offsets relative to the slab). attn, h_mid, act and h are in MFMA fragment order
+// with rows padded to the kernel's tile (tileRows).
 struct StackLayout {
-  size_t sync, attn_tag, down_tag, slabs, total;
+  size_t sync, attn_tag, down_tag, x0, slabs, total;
   int64_t slab_elems, off_attn, off_h_mid, off_act, off_h;
 };
 
@@ -55,17 +58,19 @@ StackLayout layoutFor(int64_t m, int64_t hidden, int64_t q_heads, int64_t kv_hea
   l.attn_tag = take(static_cast<size_t>(rows) * attn_splits * (head_dim + 2) * sizeof(uint64_t));
   l.down_tag =
       take(static_cast<size_t>(down_tiles) * down_splits * 16 * tileRows(m) * sizeof(uint64_t));
+  const int64_t mp = tileRows(m);  // fragment-order activations hold whole 16-row blocks
+  l.x0 = take(static_cast<size_t>(mp * hidden) * 2);  // x_in in fragment order
   int64_t e = 0;  // slab elements, each part 256-byte aligned (128 bf16)
   auto part = [&](int64_t elems) {
     const int64_t here = e;
     e += (elems + 127) / 128 * 128;
     return here;
   };
-  part(rows * head_dim);  // q at 0
-  l.off_attn = part(rows * head_dim);
-  l.off_h_mid = part(m * hidden);
-  l.off_act = part(m * ffn);
-  l.off_h = part(m * hidden);
+  part(rows * head_dim);  // q at 0 (row-major)
+  l.off_attn = part(mp * q_heads * head_dim);
+  l.off_h_mid = part(mp * hidden);
+  l.off_act = part(mp * ffn);
+  l.off_h = part(mp * hidden);
   l.slab_elems = e;
   const int per_launch = num_layers < dli_stack::kMaxLayers ? num_layers : dli_stack::kMaxLayers;
   l.slabs = take(static_cast<size_t>(e) * 2 * static_cast<size_t>(per_launch));
@@ -188,6 +193,7 @@ int dli_hip_decoder_stack(const DliDecoderLayer* layers, int num_layers, const v
   std::memset(&a, 0, sizeof(a));
   a.h_out = static_cast<uint16_t*>(hidden_out);
   a.slabs = reinterpret_cast<uint16_t*>(ws + lay.slabs);
+  a.x0 = reinterpret_cast<uint16_t*>(ws + lay.x0);
   a.slab_elems = lay.slab_elems;
   a.off_attn = lay.off_attn;
   a.off_h_mid = lay.off_h_mid;

@@ -215,7 +215,7 @@ struct DecodeAttnArgs {
   float* ws_ml;  // [B Hq][max_splits][2]   (m, l) per unit
   float* ws_o;   // [B Hq][max_splits][64]  unnormalized O per unit
   unsigned* counters;  // [B Hkv] arrivals per pair
-  uint16_t* out;       // [B, Hq, D]
+  uint16_t* out;       // [B, Hq, D] (row-major, or fragment order: out_frag_steps)
   int Hq, Hkv;
   int64_t max_blocks;
   int max_splits;
@@ -225,7 +225,17 @@ struct DecodeAttnArgs {
   uint64_t* ws_tag = nullptr;
   unsigned tag = 0;
   unsigned* abort_word = nullptr;
+  // > 0: out is [B, Hq * D] in fragment order (fragOffset) with Hq * D / 64 steps
+  int out_frag_steps = 0;
 };
+
+// Address of output element (sequence b, query head `head`, dim d).
+__device__ __forceinline__ uint16_t* attnOut(const DecodeAttnArgs& a, int64_t b, int64_t head,
+                                             int d) {
+  const int64_t k = head * kDecD + d;
+  return a.out + (a.out_frag_steps > 0 ? fragOffset(static_cast<int>(b), k, a.out_frag_steps)
+                                       : b * a.Hq * kDecD + k);
+}
 
 constexpr int kTagSlot = kDecD + 2;  // tagged words per (row, split): O, then m and l
 
@@ -333,9 +343,7 @@ __device__ __forceinline__ bool decodeAttentionUnit(const DecodeAttnArgs& a, int
   const int merger = n_active > 0 ? n_active - 1 : 0;
   if (!active && (max_splits == 1 || (tagged && split == merger))) {  // empty sequence: zeros
     for (int idx = threadIdx.x; idx < group * kDecD; idx += kDecThreads)
-      Mem::storeU16(a.out + (static_cast<int64_t>(b) * a.Hq + kvh * group + idx / kDecD) * kDecD +
-                        idx % kDecD,
-                    uint16_t{0});
+      Mem::storeU16(attnOut(a, b, kvh * group + idx / kDecD, idx % kDecD), uint16_t{0});
     return true;
   }
 
@@ -465,7 +473,7 @@ __device__ __forceinline__ bool decodeAttentionUnit(const DecodeAttnArgs& a, int
       }
       const int64_t row = static_cast<int64_t>(b) * a.Hq + kvh * group + hl;
       if (max_splits == 1) {
-        Mem::storeU16(a.out + row * kDecD + d, floatToBf16(acc / l));
+        Mem::storeU16(attnOut(a, b, row - static_cast<int64_t>(b) * a.Hq, d), floatToBf16(acc / l));
         continue;
       }
       if (tagged) {
@@ -502,7 +510,7 @@ __device__ __forceinline__ bool decodeAttentionUnit(const DecodeAttnArgs& a, int
             if (c < live) combineSplit(Mt, lt, at, v[c], v[kChunk + c], v[2 * kChunk + c]);
         }
         combineSplit(Mt, lt, at, M, l, acc);
-        Mem::storeU16(a.out + row * kDecD + d, floatToBf16(at / lt));
+        Mem::storeU16(attnOut(a, b, row - static_cast<int64_t>(b) * a.Hq, d), floatToBf16(at / lt));
         continue;
       }
       const int64_t slot = row * max_splits + split;
@@ -558,7 +566,7 @@ __device__ __forceinline__ bool decodeAttentionUnit(const DecodeAttnArgs& a, int
         combineSplit(M, l, acc, ms[c], ls[c], os[c]);
       }
     }
-    Mem::storeU16(a.out + row * kDecD + d, n > 0 ? floatToBf16(acc / l) : uint16_t{0});  // no keys: zeros
+    Mem::storeU16(attnOut(a, b, row - static_cast<int64_t>(b) * a.Hq, d), n > 0 ? floatToBf16(acc / l) : uint16_t{0});  // no keys: zeros
   }
   return true;
 }

@@ -143,11 +143,12 @@ __device__ __forceinline__ void normalizeFragments(
 // requested, then gate() waits until another workgroup has produced x, and x is loaded with
 // Mem. The arithmetic is the same either way.
 //
-// mark(p) (every thread calls it) marks points for a timeline: 0 once x is loaded (and
-// normalized), 1 when the first tile is reduced.
+// mark(p) (every thread calls it) marks points for a timeline: 2 once x is requested, 0 once x
+// is loaded (and normalized), 1 when the first tile is reduced. xs: XGlobal (row-major) or XFrag
+// (fragment order).
 template <int NF, int MB, int kW, int kU, class Mem = PlainMem, bool kGated = false,
-          class Gate = NoWait, typename Epi, class Mark = NoMark>
-__device__ __forceinline__ void tileLoop(const uint16_t* w, const XGlobal& xs, int64_t N, int K,
+          class Gate = NoWait, typename Epi, class Mark = NoMark, class XS = XGlobal>
+__device__ __forceinline__ void tileLoop(const uint16_t* w, const XS& xs, int64_t N, int K,
                                          int M, float* lds, const uint16_t* norm_w, float eps,
                                          int64_t t_first, int64_t t_stride, int64_t t_end,
                                          Gate&& gate, Epi&& epi, Mark mark = Mark{}) {
@@ -177,6 +178,7 @@ __device__ __forceinline__ void tileLoop(const uint16_t* w, const XGlobal& xs, i
     Core::template issueX<Mem>(xb, Core::xrows(xs, M, r, g), wave, steps);
   }
   float* const norm_lds = lds + Core::kLdsFloats;
+  mark(2);  // x issued (a tracing caller may wait for it here)
   if (norm_w != nullptr)
     normalizeFragments<NF, MB, kW, kU>(xb, wv, K, eps, norm_lds, wave, steps, r, g);
   mark(0);
@@ -319,9 +321,10 @@ struct QkvEpilogue {
 
 // Tile t of the interleaved gate/up weight = gate rows [16t, 16t+16) then up rows [16t, 16t+16);
 // lds holds the reduced [32][16 MB] tile. out[m, f] = bf16(bf16(silu(bf16 gate)) * bf16 up).
+// frag_steps > 0: out is in fragment order (fragOffset) with F / 64 steps.
 template <int MB, class Mem>
 __device__ __forceinline__ void gateUpEpilogue(const float* lds, uint16_t* out, int M, int64_t F,
-                                               int64_t t) {
+                                               int64_t t, int frag_steps = 0) {
   FP_EXACT;
   constexpr int kTileM = 16 * MB;
   const int64_t f0 = t * 16;
@@ -332,7 +335,7 @@ __device__ __forceinline__ void gateUpEpilogue(const float* lds, uint16_t* out, 
     const float g = roundBf16(lds[j * kTileM + m]);
     const float u = roundBf16(lds[(16 + j) * kTileM + m]);
     const float s = roundBf16(g / (1.0f + expf(-g)));
-    Mem::storeU16(out + m * F + f, floatToBf16(s * u));
+    Mem::storeU16(out + actOffset(m, f, F, frag_steps), floatToBf16(s * u));
   }
 }
 
@@ -343,7 +346,8 @@ __device__ __forceinline__ void gateUpEpilogue(const float* lds, uint16_t* out, 
 // Thread item (m, half) owns the 8 consecutive outputs n0 + 8 half, ..., + 7 of row m, so a row
 // segment is read and written with one 16-byte access when N is a multiple of 8 and the
 // pointers are 16-byte aligned (element by element otherwise); the values are the same either
-// way.
+// way. frag_steps > 0: residual / out are in fragment order (fragOffset, N / 64 steps), where a
+// row segment of 8 outputs is contiguous too.
 template <int MB, int kThreadsT, class Mem>
 struct ResidualTile {
   static constexpr int kTileN = 16;
@@ -358,13 +362,13 @@ struct ResidualTile {
   }
 
   __device__ __forceinline__ void load(const uint16_t* residual, const uint16_t* bias, int64_t n0,
-                                       int M, int64_t N) {
+                                       int M, int64_t N, int frag_steps = 0) {
     const int idx = threadIdx.x;
     const int m = idx / 2;
     const int64_t n = n0 + 8 * (idx % 2);
     const bool live = idx < kItems && m < M;
     if (live && n + 8 <= N && vectorOk(residual, N)) {
-      const U128 r = Mem::load16(residual + m * N + n);
+      const U128 r = Mem::load16(residual + actOffset(m, n, N, frag_steps));
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         res[2 * e] = bf16ToFloat(static_cast<uint16_t>(r[e]));
@@ -373,7 +377,9 @@ struct ResidualTile {
     } else {
 #pragma unroll
       for (int j = 0; j < 8; ++j)
-        res[j] = live && n + j < N ? bf16ToFloat(Mem::loadU16(residual + m * N + n + j)) : 0.f;
+        res[j] = live && n + j < N
+                     ? bf16ToFloat(Mem::loadU16(residual + actOffset(m, n + j, N, frag_steps)))
+                     : 0.f;
     }
 #pragma unroll
     for (int j = 0; j < 8; ++j)
@@ -382,7 +388,8 @@ struct ResidualTile {
 
   // y(e) returns the fp32 GEMM result of tile element e = nl * kTileM + m (row nl, column m).
   template <class Y>
-  __device__ __forceinline__ void store(uint16_t* out, int64_t n0, int M, int64_t N, Y&& y) const {
+  __device__ __forceinline__ void store(uint16_t* out, int64_t n0, int M, int64_t N, Y&& y,
+                                        int frag_steps = 0) const {
     FP_EXACT;
     const int idx = threadIdx.x;
     const int m = idx / 2, half = idx % 2;
@@ -395,12 +402,12 @@ struct ResidualTile {
       U128 o;
 #pragma unroll
       for (int e = 0; e < 4; ++e) o[e] = packBf16x2(v[2 * e], v[2 * e + 1]);
-      Mem::store16(out + m * N + n, o);
+      Mem::store16(out + actOffset(m, n, N, frag_steps), o);
       return;
     }
 #pragma unroll
     for (int j = 0; j < 8; ++j)
-      if (n + j < N) Mem::storeU16(out + m * N + n + j, floatToBf16(v[j]));
+      if (n + j < N) Mem::storeU16(out + actOffset(m, n + j, N, frag_steps), floatToBf16(v[j]));
   }
 };
 
@@ -458,11 +465,13 @@ __device__ __forceinline__ bool splitKArrive(const float* lds, float* partials, 
 // adds the other splits' words to its own partial in split order as they arrive (loadTagged),
 // writes out = residual + bf16(sum + b) through rt and returns true. The sums are those of
 // splitKArrive, bit for bit. partials: this tile's [splits][16 x 16 MB] tagged words.
+// out_frag_steps: out's layout (ResidualTile::store).
 template <int MB, int kThreadsT, class Mem>
 __device__ __forceinline__ bool splitKTagged(float* lds, uint64_t* partials, int split,
                                              int splits, unsigned tag, unsigned* abort_word,
                                              const ResidualTile<MB, kThreadsT, Mem>& rt,
-                                             uint16_t* out, int64_t n0, int M, int64_t N) {
+                                             uint16_t* out, int64_t n0, int M, int64_t N,
+                                             int out_frag_steps = 0) {
   FP_EXACT;
   constexpr int kElems = 16 * 16 * MB;
   if (split != 0) {
@@ -483,7 +492,7 @@ __device__ __forceinline__ bool splitKTagged(float* lds, uint64_t* partials, int
     lds[idx] = y;
   }
   __syncthreads();
-  rt.store(out, n0, M, N, [&](int e) { return lds[e]; });
+  rt.store(out, n0, M, N, [&](int e) { return lds[e]; }, out_frag_steps);
   return true;
 }
 

@@ -79,10 +79,34 @@ struct WriteThroughMem {
   }
 };
 
+// Element (m, k) of an activation [rows, 64 * steps] stored in MFMA fragment order: blocks of
+// [16 rows x 32 columns], one per (row block b, 64-column step s, half h), each laid out as
+// [column group g = 8 columns][row r][8 columns]. A fragment load of (b, s, h), where lane
+// g * 16 + r reads row 16 b + r, columns 64 s + 32 h + 8 g .. + 7, is then one contiguous 1 KB
+// read (the row-major [rows, K] layout spreads it over 16 rows: 64 bytes of each of 16 lines,
+// measured 2.7 times slower for a 57 KB activation). Rows are padded to whole 16-row blocks.
+__device__ __forceinline__ int64_t fragOffset(int m, int64_t k, int steps) {
+  const int64_t b = m >> 4, r = m & 15, s = k >> 6, h = (k >> 5) & 1, g = (k >> 3) & 3;
+  return ((((b * steps + s) * 2 + h) * 4 + g) * 16 + r) * 8 + (k & 7);
+}
+
+// Offset of element (m, k) of an activation with `ld` columns: row-major when frag_steps is 0,
+// else fragment order with frag_steps = ld / 64 (fragOffset).
+__device__ __forceinline__ int64_t actOffset(int m, int64_t k, int64_t ld, int frag_steps) {
+  return frag_steps > 0 ? fragOffset(m, k, frag_steps) : m * ld + k;
+}
+
 // The B operand (the skinny activation x): [M, K] row-major with `stride` elements per row.
 struct XGlobal {
   const uint16_t* x;
   int64_t stride;
+};
+
+// The B operand in fragment order (fragOffset) with `steps` = K / 64, rows padded to 16-row
+// blocks. A separate type, so the layout is fixed at compile time in each GEMM.
+struct XFrag {
+  const uint16_t* x;
+  int steps;
 };
 
 // kUnroll: 64-column steps per batch and wave (two batches are in flight).
@@ -119,9 +143,15 @@ struct SkinnyCore {
     return rw;
   }
 
-  struct XRows {
+  // Lane pointers of each row block; kStep and kHalf are the element distances of a 64-column
+  // step and of the second 32-column half of a step in the layout.
+  template <bool kFrag>
+  struct XRowsT {
+    static constexpr int64_t kStep = kFrag ? 1024 : 64;
+    static constexpr int64_t kHalf = kFrag ? 512 : 32;
     const uint16_t* x[MB];
   };
+  using XRows = XRowsT<false>;
 
   __device__ __forceinline__ static XRows xrows(const XGlobal& xs, int M, int r, int g) {
     XRows xr;
@@ -130,6 +160,15 @@ struct SkinnyCore {
       const int m = b * 16 + r;
       xr.x[b] = xs.x + static_cast<int64_t>(m < M ? m : M - 1) * xs.stride + g * 8;
     }
+    return xr;
+  }
+
+  // Fragment order: padded rows are read as they are (they feed discarded outputs only).
+  __device__ __forceinline__ static XRowsT<true> xrows(const XFrag& xs, int, int r, int g) {
+    XRowsT<true> xr;
+#pragma unroll
+    for (int b = 0; b < MB; ++b)
+      xr.x[b] = xs.x + (static_cast<int64_t>(b) * xs.steps * 128 + g * 16 + r) * 8;
     return xr;
   }
 
@@ -151,17 +190,18 @@ struct SkinnyCore {
   }
 
   // x loads of the same batch.
-  template <class Mem = PlainMem>
-  __device__ __forceinline__ static void issueX(XBatch& bt, const XRows& xr, int s0, int step_end) {
+  template <class Mem = PlainMem, bool kFrag = false>
+  __device__ __forceinline__ static void issueX(XBatch& bt, const XRowsT<kFrag>& xr, int s0,
+                                                int step_end) {
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       const int s = s0 + u * kWaves;
       if (s >= step_end) break;
-      const int64_t k0 = static_cast<int64_t>(s) * 64;
+      const int64_t k0 = static_cast<int64_t>(s) * XRowsT<kFrag>::kStep;
 #pragma unroll
       for (int b = 0; b < MB; ++b) {
         bt.x[u][b][0] = Mem::load16(xr.x[b] + k0);
-        bt.x[u][b][1] = Mem::load16(xr.x[b] + k0 + 32);
+        bt.x[u][b][1] = Mem::load16(xr.x[b] + k0 + XRowsT<kFrag>::kHalf);
       }
     }
   }
@@ -231,9 +271,10 @@ struct SkinnyCore {
   // batches are requested, then gate() (called by every thread) waits until x is ready, and only
   // then are the x batches loaded (with Mem). The batches are accumulated in the order run()
   // uses, so both give bit-identical tiles.
-  // mark(0) (every thread calls it) marks the point where the tile is reduced.
-  template <class Mem, class Gate, class Mark = NoMark>
-  __device__ __forceinline__ static void runGated(const uint16_t* __restrict__ w, const XGlobal& xs,
+  // mark(0) (every thread calls it) marks the point where the tile is reduced, mark(1) the point
+  // where the first x batches are requested. xs: XGlobal (row-major) or XFrag (fragment order).
+  template <class Mem, class Gate, class Mark = NoMark, class XS = XGlobal>
+  __device__ __forceinline__ static void runGated(const uint16_t* __restrict__ w, const XS& xs,
                                                   int64_t N, int64_t K, int M, int64_t n0,
                                                   int step_begin, int step_end, float* lds,
                                                   Gate&& gate, Mark mark = Mark{}) {
@@ -243,7 +284,7 @@ struct SkinnyCore {
     f32x4 acc[NF][MB];
     zero(acc);
     const Rows rw = rows(w, N, K, n0, r, g);
-    const XRows xr = xrows(xs, M, r, g);
+    const auto xr = xrows(xs, M, r, g);
     constexpr int kStride = kUnroll * kWaves;
     WBatch w0, w1;
     XBatch x0, x1;
@@ -253,6 +294,7 @@ struct SkinnyCore {
     gate();
     issueX<Mem>(x0, xr, s0, step_end);
     if (s0 + kStride < step_end) issueX<Mem>(x1, xr, s0 + kStride, step_end);
+    mark(1);  // loads of the first batches issued (a tracing caller may wait for them here)
     for (; s0 < step_end; s0 += 2 * kStride) {
       const int s1 = s0 + kStride;
       compute(acc, w0, x0, s0, step_end);

@@ -110,6 +110,15 @@ __device__ __forceinline__ void stamp(const Args& a, int l, int e, unsigned long
   if (threadIdx.x == 0) lds[e] = __builtin_amdgcn_s_memrealtime();
 }
 
+// Stamps event e once every wave's outstanding loads have arrived (only while tracing: the
+// stage waits for them soon after anyway, but the wait and barrier stay off the untraced path).
+__device__ __forceinline__ void stampLoaded(const Args& a, int l, int e, unsigned long long* lds) {
+  if (a.trace == nullptr || a.trace_base + l >= a.trace_layers) return;
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();  // every wave's loads
+  if (threadIdx.x == 0) lds[e] = __builtin_amdgcn_s_memrealtime();
+}
+
 __device__ __forceinline__ void flushStamps(const Args& a, int l, unsigned long long* lds) {
   unsigned long long* const t = a.trace;
   if (t == nullptr || a.trace_base + l >= a.trace_layers) return;
@@ -148,7 +157,7 @@ struct StackLds {
   };
   // as many early slots as fit in 160 KB beside the union (7 up to 32 rows, 5 at 64)
   static constexpr int kEarlyFit =
-      static_cast<int>((163840 - 256 - sizeof(Shared)) / sizeof(KvBlockLds));
+      static_cast<int>((163840 - 512 - sizeof(Shared)) / sizeof(KvBlockLds));
   static constexpr int kEarly = kEarlyFit < kDecWaves - 1 ? kEarlyFit : kDecWaves - 1;
   union {
     KvBlockLds kv[kDecWaves];
@@ -191,6 +200,16 @@ __device__ void decoderStack(const Args& a) {
     for (int e = 0; e < dli_stack::kTraceEvents; ++e) smem.trace[e] = 0;
   // launch epoch (advanced only by the last workgroup out, after every workgroup has read it)
   const unsigned epoch = __builtin_amdgcn_readfirstlane(loadAgent(a.sync + dli_stack::kEpochWord));
+  // Prologue: x_in (row-major) into x0 in fragment order, one 16-column tile per workgroup like
+  // a down_proj tile, counted on kDownDone as the output of "layer -1" (so every layer's q|k|v
+  // waits for (l + 1) x down_tiles arrivals and reads its x in fragment order).
+  for (int t = bid; t < down_tiles; t += G) {
+    const int m = threadIdx.x / 2;  // thread item: 8 columns of one row
+    const int64_t n = static_cast<int64_t>(t) * 16 + 8 * (threadIdx.x % 2);
+    if (m < a.M)  // the host checks 16-byte alignment and H % 64 == 0
+      Mem::store16(a.x0 + fragOffset(m, n, a.H / 64), gload16(a.x_in + m * a.H + n));
+    arrive(a.sync + dli_stack::stageWord(dli_stack::kDownDone), 1);
+  }
   for (int l = 0; l < a.layers; ++l) {
     if (l > 0) flushStamps(a, l - 1, smem.trace);
     const Layer& L = a.layer[l];
@@ -205,7 +224,7 @@ __device__ void decoderStack(const Args& a) {
     uint16_t* const act = slab + a.off_act;
     uint16_t* const h = l == a.layers - 1 ? fresh(a.h_out) : slab + a.off_h;
     const uint16_t* const h_prev =
-        l == 0 ? fresh(a.x_in) : static_cast<const uint16_t*>(slab - a.slab_elems + a.off_h);
+        l == 0 ? fresh(a.x0) : static_cast<const uint16_t*>(slab - a.slab_elems + a.off_h);
     unsigned* const sync = fresh(a.sync);
     unsigned* const abort_word = sync + dli_stack::kAbortWord;
     stamp(a, l, dli_stack::kTrLayerStart, smem.trace);
@@ -257,12 +276,12 @@ __device__ void decoderStack(const Args& a) {
         }
       };
       tileLoop<1, MB, kNormWaves, kNormUnroll, Mem, true>(
-          L.w_qkv, XGlobal{h_prev, H}, qkv_tiles * 16, H, M, lds, L.input_norm, a.eps, t0,
+          L.w_qkv, XFrag{h_prev, H / 64}, qkv_tiles * 16, H, M, lds, L.input_norm, a.eps, t0,
           t_stride, t_end,
           [&] {
-            if (l > 0)
-              waitAtLeast(sync + dli_stack::stageWord(dli_stack::kDownDone), l * down_tiles,
-                          abort_word);
+            // h of the previous layer (for the first layer: the prologue's copy of x_in)
+            waitAtLeast(sync + dli_stack::stageWord(dli_stack::kDownDone), gen * down_tiles,
+                        abort_word);
             stamp(a, l, dli_stack::kTrQkvWait, smem.trace);
           },
           [&](int64_t t) {
@@ -271,7 +290,12 @@ __device__ void decoderStack(const Args& a) {
             else
               finish(epi1, t);
           },
-          [&](int p) { stamp(a, l, dli_stack::kTrQkvNorm + p, smem.trace); });
+          [&](int p) {
+            if (p == 2)
+              stampLoaded(a, l, dli_stack::kTrQkvX, smem.trace);
+            else
+              stamp(a, l, dli_stack::kTrQkvNorm + p, smem.trace);
+          });
       if (kv_written > 0) {
         arrive(sync + dli_stack::stageWord(dli_stack::kKvDone), kv_written);
         stamp(a, l, dli_stack::kTrKvPublished, smem.trace);
@@ -322,7 +346,8 @@ __device__ void decoderStack(const Args& a) {
                               a.scale_log2,
                               fresh(a.attn_tag),
                               tag,
-                              abort_word};
+                              abort_word,
+                              a.Hq * a.D / 64};
       for (int u = bid; u < attn_units; u += G) {
         const bool merged = decodeAttentionUnit<Mem, true>(
             da, u % splits, u / splits, gen * splits, false, smem.p.u.attn, smem.kv,
@@ -355,12 +380,18 @@ __device__ void decoderStack(const Args& a) {
       const int H = fresh(a.H), M = fresh(a.M), qd = fresh(a.Hq * a.D);
       const int64_t n0 = static_cast<int64_t>(t) * 16;
       ResidualTile<MB, kResThreads, Mem> rt;
-      OCore::template runGated<Mem>(L.w_o, XGlobal{attn, qd}, H, qd, M, n0, 0, qd / 64, lds, [&] {
-        waitAtLeast(sync + dli_stack::stageWord(dli_stack::kAttnDone), gen * pairs, abort_word);
-        stamp(a, l, dli_stack::kTrOWait, smem.trace);
-        rt.load(h_prev, nullptr, n0, M, H);
-      });
-      rt.store(h_mid, n0, M, H, [&](int e) { return lds[e]; });
+      OCore::template runGated<Mem>(
+          L.w_o, XFrag{attn, qd / 64}, H, qd, M, n0, 0, qd / 64, lds,
+          [&] {
+            waitAtLeast(sync + dli_stack::stageWord(dli_stack::kAttnDone), gen * pairs,
+                        abort_word);
+            stamp(a, l, dli_stack::kTrOWait, smem.trace);
+            rt.load(h_prev, nullptr, n0, M, H, H / 64);
+          },
+          [&](int p) {
+            if (p == 1) stampLoaded(a, l, dli_stack::kTrOX, smem.trace);
+          });
+      rt.store(h_mid, n0, M, H, [&](int e) { return lds[e]; }, H / 64);
       arrive(sync + dli_stack::stageWord(dli_stack::kODone), 1);
       stamp(a, l, dli_stack::kTrODone, smem.trace);
     }
@@ -385,15 +416,21 @@ __device__ void decoderStack(const Args& a) {
     if (gu_first < gu_end) {
       const int H = fresh(a.H), M = fresh(a.M), F = fresh(a.F);
       tileLoop<2, MB, kNormWaves, kNormUnroll, Mem, true>(
-          L.w_gate_up, XGlobal{h_mid, H}, 2 * static_cast<int64_t>(F), H, M, lds, L.post_norm,
+          L.w_gate_up, XFrag{h_mid, H / 64}, 2 * static_cast<int64_t>(F), H, M, lds,
+          L.post_norm,
           a.eps, gu_first, gu_stride, gu_end,
           [&] {
             waitAtLeast(sync + dli_stack::stageWord(dli_stack::kODone), gen * o_tiles,
                         abort_word);
             stamp(a, l, dli_stack::kTrGuWait, smem.trace);
           },
-          [&](int64_t t) { gateUpEpilogue<MB, Mem>(lds, act, M, F, t); },
-          [&](int p) { stamp(a, l, dli_stack::kTrGuNorm + p, smem.trace); });
+          [&](int64_t t) { gateUpEpilogue<MB, Mem>(lds, act, M, F, t, F / 64); },
+          [&](int p) {
+            if (p == 2)
+              stampLoaded(a, l, dli_stack::kTrGuX, smem.trace);
+            else
+              stamp(a, l, dli_stack::kTrGuNorm + p, smem.trace);
+          });
       arrive(sync + dli_stack::stageWord(dli_stack::kGateUpDone),
              static_cast<unsigned>((gu_end - gu_first + gu_stride - 1) / gu_stride));
       stamp(a, l, dli_stack::kTrGuDone, smem.trace);
@@ -410,14 +447,19 @@ __device__ void decoderStack(const Args& a) {
         waitAtLeast(sync + dli_stack::stageWord(dli_stack::kGateUpDone), gen * gu_tiles,
                     abort_word);
         stamp(a, l, dli_stack::kTrDownWait, smem.trace);
-        rt.load(h_mid, nullptr, n0, M, H);
+        rt.load(h_mid, nullptr, n0, M, H, H / 64);
       };
+      const int h_frag = l == a.layers - 1 ? 0 : H / 64;  // the last layer writes h_out
       if (down_splits == 1) {
-        OCore::template runGated<Mem>(L.w_down, XGlobal{act, F}, H, F, M, n0, 0, F / 64, lds,
-                                      gate, [&](int) {
-                                        stamp(a, l, dli_stack::kTrDownReduced, smem.trace);
+        OCore::template runGated<Mem>(L.w_down, XFrag{act, F / 64}, H, F, M, n0, 0, F / 64,
+                                      lds,
+                                      gate, [&](int p) {
+                                        if (p == 1)
+                                          stampLoaded(a, l, dli_stack::kTrDownX, smem.trace);
+                                        else
+                                          stamp(a, l, dli_stack::kTrDownReduced, smem.trace);
                                       });
-        rt.store(h, n0, M, H, [&](int e) { return lds[e]; });
+        rt.store(h, n0, M, H, [&](int e) { return lds[e]; }, h_frag);
         arrive(sync + dli_stack::stageWord(dli_stack::kDownDone), 1);
         stamp(a, l, dli_stack::kTrDownDone, smem.trace);
         continue;
@@ -425,11 +467,15 @@ __device__ void decoderStack(const Args& a) {
       int sb, se;
       splitRange(F / 64, split, down_splits, sb, se);
       DownCore::template runGated<Mem>(
-          L.w_down, XGlobal{act, F}, H, F, M, n0, sb, se, lds, gate,
-          [&](int) { stamp(a, l, dli_stack::kTrDownReduced, smem.trace); });
+          L.w_down, XFrag{act, F / 64}, H, F, M, n0, sb, se, lds, gate, [&](int p) {
+            if (p == 1)
+              stampLoaded(a, l, dli_stack::kTrDownX, smem.trace);
+            else
+              stamp(a, l, dli_stack::kTrDownReduced, smem.trace);
+          });
       if (splitKTagged<MB, kResThreads, Mem>(
               lds, fresh(a.down_tag) + static_cast<int64_t>(tile) * down_splits * kTileElems,
-              split, down_splits, tag, abort_word, rt, h, n0, M, H))
+              split, down_splits, tag, abort_word, rt, h, n0, M, H, h_frag))
         arrive(sync + dli_stack::stageWord(dli_stack::kDownDone), 1);
       stamp(a, l, dli_stack::kTrDownDone, smem.trace);
     }

@@ -27,10 +27,13 @@ struct Args {
   Layer layer[kMaxLayers];
   const uint16_t* x_in;  // [M, H] residual stream entering the first layer
   uint16_t* h_out;       // [M, H] residual stream after the last layer
+  uint16_t* x0;          // x_in in fragment order (written by the launch's prologue)
   // Activations of layer l live in their own slab at slabs + l * slab_elems (never reused within
-  // a launch): q [M, Hq, D] at offset 0, attn [M, Hq, D] at off_attn, h_mid [M, H] (residual
-  // stream after attention) at off_h_mid, act [M, F] at off_act, h [M, H] (after the layer) at
-  // off_h; the last layer writes h_out instead.
+  // a launch): q [M, Hq, D] (row-major) at offset 0; in MFMA fragment order (fragOffset in
+  // skinny.h, rows padded to the tile's 16 MB) attn [M, Hq D] at off_attn, h_mid [M, H]
+  // (residual stream after attention) at off_h_mid, act [M, F] at off_act and h [M, H] (after
+  // the layer) at off_h; the last layer writes h_out (row-major) instead, and the first reads
+  // x0, the prologue's fragment-order copy of x_in.
   uint16_t* slabs;
   int64_t slab_elems, off_attn, off_h_mid, off_act, off_h;
   const float* cos_t;  // [max_pos, D / 2]
@@ -80,7 +83,11 @@ enum : int {
   kTrGuNorm,          // S4: h_mid loaded and normalized
   kTrGuReduced,       // S4: first tile reduced
   kTrDownReduced,     // S5: tile (or split partial) reduced
-  kTraceEvents = 24
+  kTrQkvX,            // S1: x (and every load issued before it) arrived
+  kTrGuX,             // S4: h_mid arrived
+  kTrOX,              // S3: the attention rows arrived
+  kTrDownX,           // S5: act arrived
+  kTraceEvents = 32
 };
 
 // Layout of `sync` in 32-bit words. A stage counter is split into kShards sub-counters, each on

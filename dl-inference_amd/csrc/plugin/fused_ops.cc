@@ -285,7 +285,7 @@ class LmHeadArgmaxOp final : public Operator {
 // All decoder layers in one launch (dli_hip_decoder_stack). inputs: hidden [B, H], positions
 // [B], cos, sin, then per layer: input_layernorm.weight, qkv_proj.weight, qkv_proj.bias,
 // o_proj.weight, post_attention_layernorm.weight, gate_up_proj.weight, down_proj.weight; then,
-// optionally, a stage-timeline buffer (int64, layers x CUs x 24 entries: DliStackOptions.trace).
+// optionally, a stage-timeline buffer (int64, layers x CUs x DLI_STACK_TRACE_EVENTS entries: DliStackOptions.trace).
 // Attributes: attention_splits (0 = the launch's choice; the paged_attention node's count makes
 // the two bit-identical), down_splits, eps, kv_cache_prefix, check_status.
 // Layer i appends to and attends over cache entry kv_cache_prefix + i. Computes what the
@@ -324,7 +324,7 @@ class DecoderStackOp final : public Operator {
         throw std::invalid_argument("decoder_stack trace buffer must be int64");
       int cus = 0;
       check(dli_hip_compute_units(&cus), type());
-      const auto per_layer = static_cast<std::int64_t>(cus) * 24;
+      const auto per_layer = static_cast<std::int64_t>(cus) * DLI_STACK_TRACE_EVENTS;
       options.trace_layers = static_cast<int>(static_cast<std::int64_t>(trace.numel()) / per_layer);
       if (options.trace_layers < 1)
         throw std::invalid_argument("decoder_stack trace buffer holds less than one layer");

@@ -448,11 +448,14 @@ typedef struct DliDecoderLayer {
  * trace, trace_layers: stage timeline (no counterpart in the reference; its profiler exists only
  *   as a design, .codex/profiling_design.md). With trace non-NULL the launch stamps the 100 MHz
  *   real-time counter (s_memrealtime) at the stage boundaries of each workgroup:
- *   trace[(layer * grid + workgroup) * 24 + event] for layer < trace_layers, where grid is the
+ *   trace[(layer * grid + workgroup) * DLI_STACK_TRACE_EVENTS + event] for layer < trace_layers,
+ *   where grid is the
  *   launch's workgroup count (one per CU) and the events are those of dli_stack::kTr* in
  *   csrc/kernels/stack_args.h (0 = layer entry ... 12 = down_proj done). The buffer holds
- *   trace_layers * grid * 24 uint64 of device memory; events a workgroup does not reach are left
+ *   trace_layers * grid * DLI_STACK_TRACE_EVENTS uint64 of device memory; events a workgroup
+ *   does not reach are left
  *   as they were. */
+#define DLI_STACK_TRACE_EVENTS 32
 typedef struct DliStackOptions {
   int attention_splits;
   unsigned long long* trace;

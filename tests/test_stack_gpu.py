@@ -170,7 +170,7 @@ def test_stack_trace_timeline():
     w = random_weights(cfg, seed=71, device="cuda")
     prompt = _prompt(cfg, 8, 3, 72)
     grid = torch.cuda.get_device_properties(0).multi_processor_count
-    events = 24  # dli_stack::kTraceEvents
+    events = 32  # DLI_STACK_TRACE_EVENTS
     trace = torch.zeros(cfg.layers * grid * events, dtype=torch.int64, device="cuda")
     fused, stack = _pair(cfg, w, 8, 128, down=3, stack_trace=trace)
     _, untraced = _pair(cfg, w, 8, 128, down=3)
