@@ -83,7 +83,7 @@ __device__ void linear_residual_splitk_impl(const uint16_t* x, const uint16_t* w
                                             const uint16_t* bias, const uint16_t* residual,
                                             uint16_t* out, int M, int64_t N, int K, int splits,
                                             float* partials, unsigned* counters) {
-  using Core = SkinnyCore<1, MB, kResWaves, 2>;
+  using Core = SkinnyCore<1, MB, kResWaves, 2, kDownIdle>;  // the decoder stack's down_proj core
   constexpr int kElems = Core::kTileN * Core::kTileM;
   __shared__ float lds[Core::kLdsFloats];
   __shared__ int is_last;

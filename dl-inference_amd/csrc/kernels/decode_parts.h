@@ -30,6 +30,10 @@ constexpr int kNormUnroll = 2;
 constexpr int kResWaves = 8;
 constexpr int kResThreads = kResWaves * kWave;
 constexpr int kMaxSplits = 8;  // split-K partials summed by the last arriver
+// Split-K linear_residual (down_proj): waves without K steps. The decoder stack's down_proj
+// units poll the gate_up counter from wave 0, whose poll then does not queue behind weight
+// loads; the one-stage kernel uses the same split of K over waves, so both sum alike.
+constexpr int kDownIdle = 1;
 
 __device__ __forceinline__ float roundBf16(float v) { return bf16ToFloat(floatToBf16(v)); }
 

@@ -8,7 +8,10 @@
 //     caller may split K over grid.y and reduce the partial tiles itself).
 //   - Its kWaves waves take steps begin + wave, + kWaves, ...: per step a lane loads two 16-byte
 //     runs of one weight row, so every wave-wide load pair covers 16 rows x 128 contiguous bytes
-//     (whole cache lines, each byte fetched once).
+//     (whole cache lines, each byte fetched once). With kIdle > 0 the first kIdle waves take no
+//     step (waves kIdle.. take begin + wave - kIdle, + kWaves - kIdle, ...): a gated caller's
+//     polling wave then has no weight loads in flight, so its poll does not complete behind them
+//     (a wave's loads complete in issue order).
 //   - x fragments are loaded from global memory with the weights (x is small and stays in L2).
 //   - MFMA v_mfma_f32_16x16x32_bf16: A = 16 weight rows x 32 k, B = 32 k x 16 batch rows.
 //     Lane l holds A[l % 16][(l / 16) * 8 + j] and B[(l / 16) * 8 + j][l % 16], j < 8, and
@@ -109,9 +112,12 @@ struct XFrag {
   int steps;
 };
 
-// kUnroll: 64-column steps per batch and wave (two batches are in flight).
-template <int NF, int MB, int kWaves, int kUnroll = 4>
+// kUnroll: 64-column steps per batch and wave (two batches are in flight); kIdle: leading waves
+// without steps (their partial tiles are zero).
+template <int NF, int MB, int kWaves, int kUnroll = 4, int kIdle = 0>
 struct SkinnyCore {
+  static_assert(kIdle >= 0 && kIdle < kWaves, "at least one wave takes steps");
+  static constexpr int kCW = kWaves - kIdle;  // waves that take steps
   static constexpr int kTileN = 16 * NF;
   static constexpr int kTileM = 16 * MB;
   // LDS floats needed by reduce(): one partial tile per wave.
@@ -172,13 +178,13 @@ struct SkinnyCore {
     return xr;
   }
 
-  // Weight loads of the batch whose first step is s0 (steps s0 + u * kWaves). s0 is uniform
+  // Weight loads of the batch whose first step is s0 (steps s0 + u * kCW). s0 is uniform
   // over the wave, so steps past step_end are skipped with a scalar branch; their registers are
   // never read (compute stops at step_end).
   __device__ __forceinline__ static void issueW(WBatch& bt, const Rows& rw, int s0, int step_end) {
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
-      const int s = s0 + u * kWaves;
+      const int s = s0 + u * kCW;
       if (s >= step_end) break;
       const int64_t k0 = static_cast<int64_t>(s) * 64;
 #pragma unroll
@@ -195,7 +201,7 @@ struct SkinnyCore {
                                                 int step_end) {
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
-      const int s = s0 + u * kWaves;
+      const int s = s0 + u * kCW;
       if (s >= step_end) break;
       const int64_t k0 = static_cast<int64_t>(s) * XRowsT<kFrag>::kStep;
 #pragma unroll
@@ -210,7 +216,7 @@ struct SkinnyCore {
                                                  const XBatch& xb, int s0, int step_end) {
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
-      if (s0 + u * kWaves >= step_end) break;  // uniform per wave
+      if (s0 + u * kCW >= step_end) break;  // uniform per wave
 #pragma unroll
       for (int h = 0; h < 2; ++h)
 #pragma unroll
@@ -243,10 +249,10 @@ struct SkinnyCore {
     zero(acc);
     const Rows rw = rows(w, N, K, n0, r, g);
     const XRows xr = xrows(xs, M, r, g);
-    constexpr int kStride = kUnroll * kWaves;
+    constexpr int kStride = kUnroll * kCW;
     WBatch w0, w1;
     XBatch x0, x1;
-    int s0 = step_begin + wave;
+    int s0 = wave < kIdle ? step_end : step_begin + wave - kIdle;  // uniform
     issueW(w0, rw, s0, step_end);
     issueX(x0, xr, s0, step_end);
     for (; s0 < step_end; s0 += 2 * kStride) {
@@ -285,10 +291,10 @@ struct SkinnyCore {
     zero(acc);
     const Rows rw = rows(w, N, K, n0, r, g);
     const auto xr = xrows(xs, M, r, g);
-    constexpr int kStride = kUnroll * kWaves;
+    constexpr int kStride = kUnroll * kCW;
     WBatch w0, w1;
     XBatch x0, x1;
-    int s0 = step_begin + wave;
+    int s0 = wave < kIdle ? step_end : step_begin + wave - kIdle;  // uniform
     issueW(w0, rw, s0, step_end);
     if (s0 + kStride < step_end) issueW(w1, rw, s0 + kStride, step_end);
     gate();

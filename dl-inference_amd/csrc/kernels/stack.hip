@@ -76,13 +76,17 @@ __device__ __forceinline__ void arrive(unsigned* stage, unsigned n) {
 // Polls a stage counter from one wave (lane i < kShards loads shard i with an agent-scope
 // vector load) until the shards sum to at least target, the abort word is set, or kSpinLimit
 // polls have passed (which sets the abort word). The loop condition is uniform over the wave.
+// first (tracing, or NULL): receives the time the first poll returned (the wave's loads complete
+// in issue order, so that is also when the loads it issued before the wait had arrived).
 __device__ __forceinline__ void pollStage(const unsigned* stage, unsigned target,
-                                          unsigned* abort_word) {
+                                          unsigned* abort_word,
+                                          unsigned long long* first = nullptr) {
   const int lane = freshThreadIdx() % kWave;
   for (int spins = 0;; ++spins) {
     unsigned v = lane < dli_stack::kShards ? loadAgent(stage + lane * dli_stack::kLineWords) : 0u;
 #pragma unroll
     for (int o = 1; o < dli_stack::kShards; o *= 2) v += __shfl_xor(v, o, kWave);
+    if (first != nullptr && spins == 0 && lane == 0) *first = __builtin_amdgcn_s_memrealtime();
     if (__builtin_amdgcn_readfirstlane(v) >= target) break;
     if (spins % kAbortPollEvery == 0 &&
         __builtin_amdgcn_readfirstlane(loadAgent(abort_word)) != 0u)
@@ -97,8 +101,9 @@ __device__ __forceinline__ void pollStage(const unsigned* stage, unsigned target
 
 // Returns in every thread of the workgroup once the stage counter reaches target (wave 0 polls).
 __device__ __forceinline__ void waitAtLeast(const unsigned* stage, unsigned target,
-                                            unsigned* abort_word) {
-  if (threadIdx.x < kWave) pollStage(stage, target, abort_word);
+                                            unsigned* abort_word,
+                                            unsigned long long* first = nullptr) {
+  if (threadIdx.x < kWave) pollStage(stage, target, abort_word, first);
   __syncthreads();
 }
 
@@ -117,6 +122,12 @@ __device__ __forceinline__ void stampLoaded(const Args& a, int l, int e, unsigne
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();  // every wave's loads
   if (threadIdx.x == 0) lds[e] = __builtin_amdgcn_s_memrealtime();
+}
+
+// The LDS stamp slot of event e while tracing layer l, else NULL.
+__device__ __forceinline__ unsigned long long* traceSlot(const Args& a, int l, int e,
+                                                         unsigned long long* lds) {
+  return a.trace == nullptr || a.trace_base + l >= a.trace_layers ? nullptr : lds + e;
 }
 
 __device__ __forceinline__ void flushStamps(const Args& a, int l, unsigned long long* lds) {
@@ -173,7 +184,8 @@ struct StackLds {
 template <int MB>
 __device__ void decoderStack(const Args& a) {
   using OCore = SkinnyCore<1, MB, kResWaves, (MB >= 4 ? 2 : 4)>;
-  using DownCore = SkinnyCore<1, MB, kResWaves, 2>;
+  // down_proj splits: wave 0 (the poller of the act wait) takes no K step (kDownIdle)
+  using DownCore = SkinnyCore<1, MB, kResWaves, 2, kDownIdle>;
   using Mem = WriteThroughMem;
   constexpr int kTileElems = 16 * 16 * MB;
   static_assert(SkinnyCore<1, MB, kNormWaves, kNormUnroll>::kLdsFloats <=
@@ -281,7 +293,7 @@ __device__ void decoderStack(const Args& a) {
           [&] {
             // h of the previous layer (for the first layer: the prologue's copy of x_in)
             waitAtLeast(sync + dli_stack::stageWord(dli_stack::kDownDone), gen * down_tiles,
-                        abort_word);
+                        abort_word, traceSlot(a, l, dli_stack::kTrQkvPoll, smem.trace));
             stamp(a, l, dli_stack::kTrQkvWait, smem.trace);
           },
           [&](int64_t t) {
@@ -384,7 +396,7 @@ __device__ void decoderStack(const Args& a) {
           L.w_o, XFrag{attn, qd / 64}, H, qd, M, n0, 0, qd / 64, lds,
           [&] {
             waitAtLeast(sync + dli_stack::stageWord(dli_stack::kAttnDone), gen * pairs,
-                        abort_word);
+                        abort_word, traceSlot(a, l, dli_stack::kTrOPoll, smem.trace));
             stamp(a, l, dli_stack::kTrOWait, smem.trace);
             rt.load(h_prev, nullptr, n0, M, H, H / 64);
           },
@@ -421,7 +433,7 @@ __device__ void decoderStack(const Args& a) {
           a.eps, gu_first, gu_stride, gu_end,
           [&] {
             waitAtLeast(sync + dli_stack::stageWord(dli_stack::kODone), gen * o_tiles,
-                        abort_word);
+                        abort_word, traceSlot(a, l, dli_stack::kTrGuPoll, smem.trace));
             stamp(a, l, dli_stack::kTrGuWait, smem.trace);
           },
           [&](int64_t t) { gateUpEpilogue<MB, Mem>(lds, act, M, F, t, F / 64); },
@@ -445,7 +457,7 @@ __device__ void decoderStack(const Args& a) {
       ResidualTile<MB, kResThreads, Mem> rt;
       auto gate = [&] {
         waitAtLeast(sync + dli_stack::stageWord(dli_stack::kGateUpDone), gen * gu_tiles,
-                    abort_word);
+                    abort_word, traceSlot(a, l, dli_stack::kTrDownPoll, smem.trace));
         stamp(a, l, dli_stack::kTrDownWait, smem.trace);
         rt.load(h_mid, nullptr, n0, M, H, H / 64);
       };

@@ -87,6 +87,10 @@ enum : int {
   kTrGuX,             // S4: h_mid arrived
   kTrOX,              // S3: the attention rows arrived
   kTrDownX,           // S5: act arrived
+  kTrQkvPoll,         // S1: the first poll of the wait returned
+  kTrOPoll,           // S3: the first poll of the wait returned
+  kTrGuPoll,          // S4: the first poll of the wait returned
+  kTrDownPoll,        // S5: the first poll of the wait returned
   kTraceEvents = 32
 };
 
