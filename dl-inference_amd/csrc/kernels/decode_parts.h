@@ -343,34 +343,6 @@ __device__ __forceinline__ void gateUpEpilogue(const float* lds, uint16_t* out, 
   }
 }
 
-// gateUpEpilogue for an output in fragment order with F a multiple of 64 (the decoder stack's
-// act): thread item (m, half) computes outputs f0 + 8 half .. + 7 of row m, contiguous in that
-// layout, and stores them as one 16-byte run (the same values as gateUpEpilogue).
-template <int MB, class Mem>
-__device__ __forceinline__ void gateUpEpilogueFrag(const float* lds, uint16_t* out, int M,
-                                                   int64_t t, int frag_steps) {
-  FP_EXACT;
-  constexpr int kTileM = 16 * MB;
-  const int64_t f0 = t * 16;
-  for (int idx = threadIdx.x; idx < 2 * kTileM; idx += kNormThreads) {
-    const int m = idx % kTileM, half = idx / kTileM;
-    if (m >= M) continue;
-    float v[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int jj = 8 * half + j;
-      const float g = roundBf16(lds[jj * kTileM + m]);
-      const float u = roundBf16(lds[(16 + jj) * kTileM + m]);
-      const float s = roundBf16(g / (1.0f + expf(-g)));
-      v[j] = s * u;
-    }
-    U128 o;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) o[e] = packBf16x2(v[2 * e], v[2 * e + 1]);
-    Mem::store16(out + fragOffset(m, f0 + 8 * half, frag_steps), o);
-  }
-}
-
 // ---- residual update of one 16-row tile ---------------------------------------------------
 
 // out[m, n] = bf16(residual[m, n] + bf16(y[n][m] + b[n])) for the tile at weight row n0, with

@@ -436,7 +436,7 @@ __device__ void decoderStack(const Args& a) {
                         abort_word, traceSlot(a, l, dli_stack::kTrGuPoll, smem.trace));
             stamp(a, l, dli_stack::kTrGuWait, smem.trace);
           },
-          [&](int64_t t) { gateUpEpilogueFrag<MB, Mem>(lds, act, M, t, F / 64); },
+          [&](int64_t t) { gateUpEpilogue<MB, Mem>(lds, act, M, F, t, F / 64); },
           [&](int p) {
             if (p == 2)
               stampLoaded(a, l, dli_stack::kTrGuX, smem.trace);
