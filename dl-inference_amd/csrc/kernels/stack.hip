@@ -181,8 +181,30 @@ struct StackLds {
   unsigned long long trace[dli_stack::kTraceEvents];  // stamps of the current layer
 };
 
+// Layout of the stack's activation slabs: MFMA fragment order (fragOffset) for the 32- and
+// 64-row kernels, where every fragment load is one contiguous 1 KB read; row-major for the
+// 16-row kernel, whose loads of rows past M fold onto row M - 1 (a batch of 1 would otherwise
+// read 16 rows per fragment).
+template <bool kFrag>
+struct ActX;
+template <>
+struct ActX<true> {
+  __device__ __forceinline__ static XFrag make(const uint16_t* p, int ld) {
+    return XFrag{p, ld / 64};
+  }
+  __device__ __forceinline__ static int steps(int ld) { return ld / 64; }
+};
+template <>
+struct ActX<false> {
+  __device__ __forceinline__ static XGlobal make(const uint16_t* p, int ld) {
+    return XGlobal{p, ld};
+  }
+  __device__ __forceinline__ static int steps(int) { return 0; }
+};
+
 template <int MB>
 __device__ void decoderStack(const Args& a) {
+  using AX = ActX<(MB >= 2)>;
   using OCore = SkinnyCore<1, MB, kResWaves, (MB >= 4 ? 2 : 4)>;
   // down_proj splits: wave 0 (the poller of the act wait) takes no K step (kDownIdle)
   using DownCore = SkinnyCore<1, MB, kResWaves, 2, kDownIdle>;
@@ -219,7 +241,7 @@ __device__ void decoderStack(const Args& a) {
     const int m = threadIdx.x / 2;  // thread item: 8 columns of one row
     const int64_t n = static_cast<int64_t>(t) * 16 + 8 * (threadIdx.x % 2);
     if (m < a.M)  // the host checks 16-byte alignment and H % 64 == 0
-      Mem::store16(a.x0 + fragOffset(m, n, a.H / 64), gload16(a.x_in + m * a.H + n));
+      Mem::store16(a.x0 + actOffset(m, n, a.H, AX::steps(a.H)), gload16(a.x_in + m * a.H + n));
     arrive(a.sync + dli_stack::stageWord(dli_stack::kDownDone), 1);
   }
   for (int l = 0; l < a.layers; ++l) {
@@ -288,7 +310,7 @@ __device__ void decoderStack(const Args& a) {
         }
       };
       tileLoop<1, MB, kNormWaves, kNormUnroll, Mem, true>(
-          L.w_qkv, XFrag{h_prev, H / 64}, qkv_tiles * 16, H, M, lds, L.input_norm, a.eps, t0,
+          L.w_qkv, AX::make(h_prev, H), qkv_tiles * 16, H, M, lds, L.input_norm, a.eps, t0,
           t_stride, t_end,
           [&] {
             // h of the previous layer (for the first layer: the prologue's copy of x_in)
@@ -359,7 +381,7 @@ __device__ void decoderStack(const Args& a) {
                               fresh(a.attn_tag),
                               tag,
                               abort_word,
-                              a.Hq * a.D / 64};
+                              AX::steps(a.Hq * a.D)};
       for (int u = bid; u < attn_units; u += G) {
         const bool merged = decodeAttentionUnit<Mem, true>(
             da, u % splits, u / splits, gen * splits, false, smem.p.u.attn, smem.kv,
@@ -393,17 +415,17 @@ __device__ void decoderStack(const Args& a) {
       const int64_t n0 = static_cast<int64_t>(t) * 16;
       ResidualTile<MB, kResThreads, Mem> rt;
       OCore::template runGated<Mem>(
-          L.w_o, XFrag{attn, qd / 64}, H, qd, M, n0, 0, qd / 64, lds,
+          L.w_o, AX::make(attn, qd), H, qd, M, n0, 0, qd / 64, lds,
           [&] {
             waitAtLeast(sync + dli_stack::stageWord(dli_stack::kAttnDone), gen * pairs,
                         abort_word, traceSlot(a, l, dli_stack::kTrOPoll, smem.trace));
             stamp(a, l, dli_stack::kTrOWait, smem.trace);
-            rt.load(h_prev, nullptr, n0, M, H, H / 64);
+            rt.load(h_prev, nullptr, n0, M, H, AX::steps(H));
           },
           [&](int p) {
             if (p == 1) stampLoaded(a, l, dli_stack::kTrOX, smem.trace);
           });
-      rt.store(h_mid, n0, M, H, [&](int e) { return lds[e]; }, H / 64);
+      rt.store(h_mid, n0, M, H, [&](int e) { return lds[e]; }, AX::steps(H));
       arrive(sync + dli_stack::stageWord(dli_stack::kODone), 1);
       stamp(a, l, dli_stack::kTrODone, smem.trace);
     }
@@ -428,7 +450,7 @@ __device__ void decoderStack(const Args& a) {
     if (gu_first < gu_end) {
       const int H = fresh(a.H), M = fresh(a.M), F = fresh(a.F);
       tileLoop<2, MB, kNormWaves, kNormUnroll, Mem, true>(
-          L.w_gate_up, XFrag{h_mid, H / 64}, 2 * static_cast<int64_t>(F), H, M, lds,
+          L.w_gate_up, AX::make(h_mid, H), 2 * static_cast<int64_t>(F), H, M, lds,
           L.post_norm,
           a.eps, gu_first, gu_stride, gu_end,
           [&] {
@@ -436,7 +458,7 @@ __device__ void decoderStack(const Args& a) {
                         abort_word, traceSlot(a, l, dli_stack::kTrGuPoll, smem.trace));
             stamp(a, l, dli_stack::kTrGuWait, smem.trace);
           },
-          [&](int64_t t) { gateUpEpilogue<MB, Mem>(lds, act, M, F, t, F / 64); },
+          [&](int64_t t) { gateUpEpilogue<MB, Mem>(lds, act, M, F, t, AX::steps(F)); },
           [&](int p) {
             if (p == 2)
               stampLoaded(a, l, dli_stack::kTrGuX, smem.trace);
@@ -459,11 +481,11 @@ __device__ void decoderStack(const Args& a) {
         waitAtLeast(sync + dli_stack::stageWord(dli_stack::kGateUpDone), gen * gu_tiles,
                     abort_word, traceSlot(a, l, dli_stack::kTrDownPoll, smem.trace));
         stamp(a, l, dli_stack::kTrDownWait, smem.trace);
-        rt.load(h_mid, nullptr, n0, M, H, H / 64);
+        rt.load(h_mid, nullptr, n0, M, H, AX::steps(H));
       };
-      const int h_frag = l == a.layers - 1 ? 0 : H / 64;  // the last layer writes h_out
+      const int h_frag = l == a.layers - 1 ? 0 : AX::steps(H);  // the last layer writes h_out
       if (down_splits == 1) {
-        OCore::template runGated<Mem>(L.w_down, XFrag{act, F / 64}, H, F, M, n0, 0, F / 64,
+        OCore::template runGated<Mem>(L.w_down, AX::make(act, F), H, F, M, n0, 0, F / 64,
                                       lds,
                                       gate, [&](int p) {
                                         if (p == 1)
@@ -479,7 +501,7 @@ __device__ void decoderStack(const Args& a) {
       int sb, se;
       splitRange(F / 64, split, down_splits, sb, se);
       DownCore::template runGated<Mem>(
-          L.w_down, XFrag{act, F / 64}, H, F, M, n0, sb, se, lds, gate, [&](int p) {
+          L.w_down, AX::make(act, F), H, F, M, n0, sb, se, lds, gate, [&](int p) {
             if (p == 1)
               stampLoaded(a, l, dli_stack::kTrDownX, smem.trace);
             else
