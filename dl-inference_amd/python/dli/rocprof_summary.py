@@ -51,15 +51,25 @@ def counter_means(path: str, counter: str) -> "OrderedDict[str, tuple[int, float
     return OrderedDict((k, (n, v / n)) for k, (n, v) in sums.items())
 
 
+COPY_LAST = 0  # > 0: calibrate on the last COPY_LAST copy dispatches (--copy-last)
+
+
 def copy_mean(path: str, counter: str, pattern: str) -> float:
     """Mean counter value over the dispatches matching `pattern` that read within 2% of the
     largest value (the calibration copy is the largest copy in the run; copy kernels use a fixed
-    grid, so the grid size does not tell copies of different sizes apart)."""
+    grid, so the grid size does not tell copies of different sizes apart). With COPY_LAST set,
+    the last COPY_LAST matching dispatches instead (for runs that also copy larger tensors
+    before the calibration copies at their end)."""
     rx = re.compile(pattern)
-    vals = [float(r["Counter_Value"]) for r in csv.DictReader(open(path))
+    rows = [r for r in csv.DictReader(open(path))
             if r["Counter_Name"] == counter and rx.search(r["Kernel_Name"])]
-    if not vals:
+    if not rows:
         raise SystemExit(f"no dispatch matches {pattern!r}")
+    if COPY_LAST > 0:
+        rows.sort(key=lambda r: int(r["Dispatch_Id"]))
+        top = [float(r["Counter_Value"]) for r in rows[-COPY_LAST:]]
+        return sum(top) / len(top)
+    vals = [float(r["Counter_Value"]) for r in rows]
     top = [v for v in vals if v >= 0.98 * max(vals)]
     return sum(top) / len(top)
 
@@ -148,6 +158,8 @@ def main(argv=None):
     pm.add_argument("--kernel", action="append", required=True)
     pm.add_argument("--copy-kernel", required=True)
     pm.add_argument("--copy-bytes", type=int, required=True)
+    pm.add_argument("--copy-last", type=int, default=0,
+                    help="calibrate on the last N copy dispatches (bench.py makes 3)")
     mf = sub.add_parser("mfma")
     mf.add_argument("--counters", required=True)
     mf.add_argument("--stats", required=True)
@@ -160,6 +172,8 @@ def main(argv=None):
     elif args.cmd == "mfma":
         print(mfma(args.counters, args.stats, args.kernel, args.simds, args.xcds))
     else:
+        global COPY_LAST
+        COPY_LAST = args.copy_last
         print(pmc(args.fetch, args.write, args.kernel, args.copy_kernel, args.copy_bytes))
 
 
