@@ -66,7 +66,7 @@ StackLayout layoutFor(int64_t m, int64_t hidden, int64_t q_heads, int64_t kv_hea
     e += (elems + 127) / 128 * 128;
     return here;
   };
-  part(rows * head_dim);  // q at 0 (row-major)
+  part(rows * head_dim * 2);  // q at 0: [rows, head_dim / 2] tagged 8-byte words
   l.off_attn = part(mp * q_heads * head_dim);
   l.off_h_mid = part(mp * hidden);
   l.off_act = part(mp * ffn);

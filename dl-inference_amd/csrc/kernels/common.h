@@ -42,16 +42,24 @@ __device__ __forceinline__ const DK_GLOBAL T* gp(const T* p) {
 // tag value.
 constexpr int kTagSpinLimit = 1 << 20;
 
-__device__ __forceinline__ void storeTagged(uint64_t* p, float v, unsigned tag) {
-  __hip_atomic_store(gp(p), (static_cast<uint64_t>(tag) << 32) | __float_as_uint(v),
-                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ void storeTaggedBits(uint64_t* p, uint32_t bits, unsigned tag) {
+  __hip_atomic_store(gp(p), (static_cast<uint64_t>(tag) << 32) | bits, __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
 }
+
+__device__ __forceinline__ void storeTagged(uint64_t* p, float v, unsigned tag) {
+  storeTaggedBits(p, __float_as_uint(v), tag);
+}
+
+__device__ __forceinline__ void fromBits(float& v, uint32_t bits) { v = __uint_as_float(bits); }
+__device__ __forceinline__ void fromBits(uint32_t& v, uint32_t bits) { v = bits; }
 
 // v[i] = the value at p[i] once its tag is `tag`, for i < n (all n loads in flight at once, the
 // set reread until every tag matches). Gives up after kTagSpinLimit rounds, or once *abort_word
-// is non-zero, and then sets *abort_word (the values are then invalid).
-template <int N>
-__device__ __forceinline__ void loadTagged(float (&v)[N], const uint64_t* const (&p)[N], int n,
+// is non-zero, and then sets *abort_word (the values are then invalid). T: float, or uint32_t
+// for the raw 32 bits (two packed bf16).
+template <int N, class T>
+__device__ __forceinline__ void loadTagged(T (&v)[N], const uint64_t* const (&p)[N], int n,
                                            unsigned tag, unsigned* abort_word) {
   for (int spins = 0;; ++spins) {
     uint64_t w[N];
@@ -63,7 +71,7 @@ __device__ __forceinline__ void loadTagged(float (&v)[N], const uint64_t* const 
 #pragma unroll
     for (int i = 0; i < N; ++i) {
       ok = ok && static_cast<unsigned>(w[i] >> 32) == tag;
-      v[i] = __uint_as_float(static_cast<unsigned>(w[i]));
+      fromBits(v[i], static_cast<uint32_t>(w[i]));
     }
     if (ok) return;
     if (spins >= kTagSpinLimit ||

@@ -227,6 +227,9 @@ struct DecodeAttnArgs {
   unsigned* abort_word = nullptr;
   // > 0: out is [B, Hq * D] in fragment order (fragOffset) with Hq * D / 64 steps
   int out_frag_steps = 0;
+  // When set, q is read from here instead: [B, Hq, D / 2] tagged words (the bf16 pair (d, d + 1)
+  // and tag `tag`, QkvParams::q_tagged), polled by wave 0 until every word carries the tag.
+  const uint64_t* q_tagged = nullptr;
 };
 
 // Address of output element (sequence b, query head `head`, dim d).
@@ -244,6 +247,9 @@ struct DecodeAttnLds {
   float sm[kDecWaves][16];
   float sl[kDecWaves][16];
   float so[kDecWaves][kDecD][17];
+  // q of the unit, handed from wave 0 to the others (tagged q). Kept clear of the first 4 KB,
+  // which a caller may overlay with the last wave's staged cache block.
+  U128 q[2 * kWave];
   int is_last;
 };
 
@@ -301,7 +307,8 @@ __device__ __forceinline__ void stageThirdKvBlocks(const DecodeAttnArgs& a, int 
 //
 // mark(p) (every thread calls it) marks internal points for a timeline: 0 when this wave's
 // blocks are attended, 1 when every wave's are (after the barrier), 2 after the unit's arrival,
-// 3 and 4 when this wave has attended its first and second block.
+// 3 and 4 when this wave has attended its first and second block, 5 when this wave has q.
+static_assert(offsetof(DecodeAttnLds, q) >= sizeof(KvBlockLds), "q clear of a staged block");
 template <class Mem, bool kPreload, class Gate, class KvReady, class Mark = NoMark>
 __device__ __forceinline__ bool decodeAttentionUnit(const DecodeAttnArgs& a, int split, int pair,
                                                     unsigned arrivals, bool reset,
@@ -375,14 +382,33 @@ __device__ __forceinline__ bool decodeAttentionUnit(const DecodeAttnArgs& a, int
 
   if (active) {
     U128 qf[2];
-    if (r < group) {
-      const uint16_t* qp = a.q + (static_cast<int64_t>(b) * a.Hq + kvh * group + r) * kDecD + g * 8;
-      qf[0] = Mem::load16(qp);
-      qf[1] = Mem::load16(qp + 32);
+    const int64_t q_at = (static_cast<int64_t>(b) * a.Hq + kvh * group + r) * kDecD + g * 8;
+    if (a.q_tagged != nullptr) {
+      // Wave 0 polls the unit's q words (one request per 128-byte line and lane group, as few as
+      // one counter poll would make) and hands q to the other waves through LDS (every wave of
+      // an earlier unit has read s.q before that unit's merge barrier).
+      U128* const q_lds = s.q;
+      if (wave == 0 && r < group) {
+        // dims g*8 .. g*8+7 and 32+g*8 .. 32+g*8+7: words q_at/2 .. +3 and q_at/2+16 .. +19
+        const uint64_t* const qw = a.q_tagged + q_at / 2;
+        const uint64_t* const ptr[8] = {qw,      qw + 1,  qw + 2,  qw + 3,
+                                        qw + 16, qw + 17, qw + 18, qw + 19};
+        uint32_t bits[8];
+        loadTagged<8>(bits, ptr, 8, a.tag, a.abort_word);
+        q_lds[lane] = U128{bits[0], bits[1], bits[2], bits[3]};
+        q_lds[kWave + lane] = U128{bits[4], bits[5], bits[6], bits[7]};
+      }
+      __syncthreads();
+      qf[0] = r < group ? q_lds[lane] : zero16();
+      qf[1] = r < group ? q_lds[kWave + lane] : zero16();
+    } else if (r < group) {
+      qf[0] = Mem::load16(a.q + q_at);
+      qf[1] = Mem::load16(a.q + q_at + 32);
     } else {
       qf[0] = zero16();
       qf[1] = zero16();
     }
+    mark(5);
     int k = 0;  // ordinal of the wave's block
     for (int64_t i = first; i < n_live; i += 2 * stride, k += 2) {
       if (!a_ready) fetch(bufA, k);

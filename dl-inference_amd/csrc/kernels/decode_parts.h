@@ -218,15 +218,30 @@ struct QkvParams {
   uint16_t* q_out;  // [M, Hq, D]
   KvCacheArgs kv;
   int M, Hq, Hkv, D;
+  // When set, q goes here instead of q_out: [M, Hq, D / 2] tagged words (storeTaggedBits), each
+  // the bf16 pair (d, d + 1) with tag q_tag, for a reader that polls the words themselves.
+  uint64_t* q_tagged = nullptr;
+  unsigned q_tag = 0;
 };
 
 enum : int { kQkvAll = 0, kQkvQ = 1, kQkvCache = 2 };
+
+// Operands of one QkvEpilogue thread item, parked in LDS (QkvEpilogue<..., true>).
+struct QkvParked {
+  int64_t pos;
+  float c, s, b0, b1;
+  int32_t blk;  // a block_table entry, or -1
+  int32_t unused;
+};
 
 // Epilogue of one 16-row tile of the [q | k | v] projection (kNormThreads threads). Thread item
 // (pair, m) owns output columns n0 + 2 pair, n0 + 2 pair + 1 of row m: a RoPE pair
 // (rotary/kernel.py:6-35 rotates interleaved pairs). The operands that do not depend on the GEMM
 // (position, rotary coefficients, bias, cache block) are fetched by prefetch() before it.
-template <int MB, class Mem>
+// kParked: prefetch() waits for them and parks them in LDS at park[0, kPairs) (each thread its
+// own slots, so no barrier), instead of holding them in registers across the tile's GEMM, where
+// a kernel short of registers spills them and reloads each from scratch with a full wait.
+template <int MB, class Mem, bool kParked = false>
 struct QkvEpilogue {
   static constexpr int kTileN = 16;
   static constexpr int kTileM = 16 * MB;
@@ -235,6 +250,7 @@ struct QkvEpilogue {
   int64_t pos[kItems];
   float cs[kItems][2], bs[kItems][2];
   int64_t blk[kItems];
+  QkvParked* park = nullptr;  // kParked: kPairs slots
 
   __device__ __forceinline__ void prefetch(const QkvParams& p, int64_t n0) {
     FP_EXACT;
@@ -245,19 +261,20 @@ struct QkvEpilogue {
     const int64_t capacity = p.kv.max_blocks * p.kv.block_size;
 #pragma unroll
     for (int it = 0; it < kItems; ++it) {
-      const int idx = threadIdx.x + it * kNormThreads;
+      const int idx = freshThreadIdx() + it * kNormThreads;
       const int m = idx % kTileM;
       pos[it] = (idx < kPairs && m < p.M) ? loadIndex(p.positions, p.pos64, m) : -1;
     }
 #pragma unroll
     for (int it = 0; it < kItems; ++it) {
-      const int idx = threadIdx.x + it * kNormThreads;
+      const int idx = freshThreadIdx() + it * kNormThreads;
       const int pair = idx / kTileM, m = idx % kTileM;
       const int64_t n = n0 + 2 * pair;
       const bool live = pos[it] >= 0 && n < N;
-      const int64_t local =
-          n < q_rows ? n : (n < q_rows + k_rows ? n - q_rows : n - q_rows - k_rows);
-      const int d = static_cast<int>(local % p.D);
+      // column within the q, k or v block: below (Hq + 2 Hkv) D, so 32-bit arithmetic is exact
+      const int local = static_cast<int>(
+          n < q_rows ? n : (n < q_rows + k_rows ? n - q_rows : n - q_rows - k_rows));
+      const int d = local % p.D;
       const bool rot = live && n < q_rows + k_rows && pos[it] < p.max_pos;
       cs[it][0] = rot ? gp(p.cos_t)[pos[it] * half + d / 2] : 1.f;
       cs[it][1] = rot ? gp(p.sin_t)[pos[it] * half + d / 2] : 0.f;
@@ -266,6 +283,11 @@ struct QkvEpilogue {
       blk[it] = (live && n >= q_rows && pos[it] < capacity)
                     ? gp(p.kv.block_table)[m * p.kv.max_blocks + pos[it] / p.kv.block_size]
                     : -1;
+      if constexpr (kParked) {
+        if (idx < kPairs)
+          park[idx] = QkvParked{pos[it],   cs[it][0], cs[it][1], bs[it][0],
+                                bs[it][1], static_cast<int32_t>(blk[it]), 0};
+      }
     }
   }
 
@@ -279,41 +301,52 @@ struct QkvEpilogue {
     const int64_t k_rows = static_cast<int64_t>(p.Hkv) * p.D;
 #pragma unroll
     for (int it = 0; it < kItems; ++it) {
-      const int idx = threadIdx.x + it * kNormThreads;
+      const int idx = freshThreadIdx() + it * kNormThreads;
       const int pair = idx / kTileM;
       const int m = idx % kTileM;
       const int64_t n = n0 + 2 * pair;
-      if (pos[it] < 0 || n >= N) continue;
+      QkvParked o;
+      if constexpr (kParked) {
+        if (idx >= kPairs) continue;
+        o = park[idx];
+      } else {
+        o = QkvParked{pos[it], cs[it][0], cs[it][1], bs[it][0], bs[it][1], 0, 0};
+      }
+      const int64_t blk_it = kParked ? static_cast<int64_t>(o.blk) : blk[it];
+      if (o.pos < 0 || n >= N) continue;
       // linear output (bias added, rounded), then the rotation in fp32, rounded again
-      float v0 = roundBf16(lds[(2 * pair) * kTileM + m] + bs[it][0]);
-      float v1 = roundBf16(lds[(2 * pair + 1) * kTileM + m] + bs[it][1]);
+      float v0 = roundBf16(lds[(2 * pair) * kTileM + m] + o.b0);
+      float v1 = roundBf16(lds[(2 * pair + 1) * kTileM + m] + o.b1);
       const bool is_q = n < q_rows;
       const bool is_k = !is_q && n < q_rows + k_rows;
       if ((kOutputs == kQkvQ && !is_q) || (kOutputs == kQkvCache && is_q)) continue;
-      const int64_t local = is_q ? n : (is_k ? n - q_rows : n - q_rows - k_rows);
-      const int head = static_cast<int>(local / p.D);
-      const int d = static_cast<int>(local % p.D);
+      const int local = static_cast<int>(is_q ? n : (is_k ? n - q_rows : n - q_rows - k_rows));
+      const int head = local / p.D;
+      const int d = local % p.D;
       if (is_q || is_k) {
-        const float r0 = v0 * cs[it][0] - v1 * cs[it][1];
-        const float r1 = v0 * cs[it][1] + v1 * cs[it][0];
+        const float r0 = v0 * o.c - v1 * o.s;
+        const float r1 = v0 * o.s + v1 * o.c;
         v0 = r0;
         v1 = r1;
       }
       const uint32_t packed = packBf16x2(v0, v1);
       if (is_q) {
-        uint16_t* dst = p.q_out + (static_cast<int64_t>(m) * p.Hq + head) * p.D + d;
-        Mem::storeU32(reinterpret_cast<uint32_t*>(dst), packed);
+        const int64_t at = (static_cast<int64_t>(m) * p.Hq + head) * p.D + d;
+        if (p.q_tagged != nullptr)
+          storeTaggedBits(p.q_tagged + at / 2, packed, p.q_tag);
+        else
+          Mem::storeU32(reinterpret_cast<uint32_t*>(p.q_out + at), packed);
         continue;
       }
-      if (blk[it] < 0) continue;
-      const int64_t off = pos[it] % p.kv.block_size;
+      if (blk_it < 0) continue;
+      const int64_t off = o.pos % p.kv.block_size;
       if (is_k) {
         uint16_t* dst =
-            p.kv.k_pool + ((blk[it] * p.Hkv + head) * p.kv.block_size + off) * p.D + d;
+            p.kv.k_pool + ((blk_it * p.Hkv + head) * p.kv.block_size + off) * p.D + d;
         Mem::storeU32(reinterpret_cast<uint32_t*>(dst), packed);
       } else {
         uint16_t* dst =
-            p.kv.v_pool + ((blk[it] * p.Hkv + head) * p.D + d) * p.kv.block_size + off;
+            p.kv.v_pool + ((blk_it * p.Hkv + head) * p.D + d) * p.kv.block_size + off;
         Mem::storeU16(dst, static_cast<uint16_t>(packed));
         Mem::storeU16(dst + p.kv.block_size, static_cast<uint16_t>(packed >> 16));
       }

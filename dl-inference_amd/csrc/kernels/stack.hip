@@ -18,7 +18,8 @@
 // coherent memory side; the L2 caches of the 8 XCDs are not coherent with each other), waits
 // for them (s_waitcnt vmcnt(0)) and adds to its shard of the stage counter; a consumer polls the
 // shards until they sum to (layer + 1) x the producers of that stage. Consumers then read with
-// plain loads, so each XCD's L2 serves the repeated reads of an activation row. That is correct
+// plain loads, so each XCD's L2 serves the repeated reads of an activation row (q, read by few
+// units per row, is the exception: see Work placement). That is correct
 // because every layer has its own activation buffers (slabs): no line a consumer reads can have
 // been read, and cached stale, earlier in the launch. Before waiting, a workgroup requests the
 // weights of its next tile (attention units: their first cache blocks), which do not depend on
@@ -29,8 +30,10 @@
 // attention units go to the other workgroups; o_proj tiles to the q|k|v workgroups (idle
 // through attention, so they request the o_proj weights meanwhile); gate_up tiles bid,
 // bid + a_wgs, ... to the a_wgs other workgroups; down_proj units to the first ones. q and the
-// new k/v are signalled on separate counters: attention needs q at once, but the new k/v only
-// for the block holding the newest token. A wave with a third cache block stages it in LDS
+// new k/v are signalled apart: attention needs q at once, and q goes out as tagged words
+// (common.h) that each attention wave polls directly, with no store acknowledgement and no
+// counter between the q|k|v tile and the unit; the new k/v is needed only for the block holding
+// the newest token and has its own counter. A wave with a third cache block stages it in LDS
 // (direct global-to-LDS loads) next to the two it requests into registers, so nothing streams
 // after the wait; waves 0..kEarly-1 stage it during the previous layer, right after their
 // attention unit, so that part of the K/V stream overlaps o_proj, gate_up and down_proj, when
@@ -73,19 +76,46 @@ __device__ __forceinline__ void arrive(unsigned* stage, unsigned n) {
                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Sum of v over the 64 lanes of a full wave, in a scalar: DPP adds within each 16-lane row
+// (quad swaps, then the half-row and row mirrors), then the four row sums. Every lane must be
+// active.
+template <int kCtrl>
+__device__ __forceinline__ unsigned dppMove(unsigned x) {
+  return static_cast<unsigned>(
+      __builtin_amdgcn_update_dpp(0, static_cast<int>(x), kCtrl, 0xF, 0xF, false));
+}
+
+__device__ __forceinline__ unsigned waveSum(unsigned v) {
+  v += dppMove<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+  v += dppMove<0x4E>(v);   // quad_perm [2, 3, 0, 1]
+  v += dppMove<0x141>(v);  // row_half_mirror
+  v += dppMove<0x140>(v);  // row_mirror
+  return __builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16) +
+         __builtin_amdgcn_readlane(v, 32) + __builtin_amdgcn_readlane(v, 48);
+}
+
 // Polls a stage counter from one wave (lane i < kShards loads shard i with an agent-scope
 // vector load) until the shards sum to at least target, the abort word is set, or kSpinLimit
 // polls have passed (which sets the abort word). The loop condition is uniform over the wave.
 // first (tracing, or NULL): receives the time the first poll returned (the wave's loads complete
 // in issue order, so that is also when the loads it issued before the wait had arrived).
+// kDpp: sum the shards with waveSum (DPP, a few cycles) instead of cross-lane shuffles (six
+// LDS-crossbar round trips, ~0.3 us); the 16-row kernel uses it (10-15 us per launch less at
+// batches 1 and 8), the larger ones keep the shuffles, with which the compiler spills less in
+// them (the 32-row kernel measured 5 us per launch slower with waveSum).
+template <bool kDpp>
 __device__ __forceinline__ void pollStage(const unsigned* stage, unsigned target,
                                           unsigned* abort_word,
                                           unsigned long long* first = nullptr) {
   const int lane = freshThreadIdx() % kWave;
   for (int spins = 0;; ++spins) {
     unsigned v = lane < dli_stack::kShards ? loadAgent(stage + lane * dli_stack::kLineWords) : 0u;
+    if constexpr (kDpp) {
+      v = waveSum(v);
+    } else {
 #pragma unroll
-    for (int o = 1; o < dli_stack::kShards; o *= 2) v += __shfl_xor(v, o, kWave);
+      for (int o = 1; o < dli_stack::kShards; o *= 2) v += __shfl_xor(v, o, kWave);
+    }
     if (first != nullptr && spins == 0 && lane == 0) *first = __builtin_amdgcn_s_memrealtime();
     if (__builtin_amdgcn_readfirstlane(v) >= target) break;
     if (spins % kAbortPollEvery == 0 &&
@@ -100,10 +130,11 @@ __device__ __forceinline__ void pollStage(const unsigned* stage, unsigned target
 }
 
 // Returns in every thread of the workgroup once the stage counter reaches target (wave 0 polls).
+template <bool kDpp>
 __device__ __forceinline__ void waitAtLeast(const unsigned* stage, unsigned target,
                                             unsigned* abort_word,
                                             unsigned long long* first = nullptr) {
-  if (threadIdx.x < kWave) pollStage(stage, target, abort_word, first);
+  if (threadIdx.x < kWave) pollStage<kDpp>(stage, target, abort_word, first);
   __syncthreads();
 }
 
@@ -157,15 +188,23 @@ __device__ __forceinline__ T fresh(T v) {
 // of their next-layer unit in kv_early while o_proj, gate_up and down_proj run (those use only
 // the union beside it); the rest of the stages use the union one at a time (each ends with a
 // barrier): the tile reductions and RMSNorm row sums, the attention merge, and the last wave's
-// staged block, which kv[kDecWaves - 1] overlays.
+// staged block, which kv[kDecWaves - 1] overlays. The q|k|v stage parks its epilogue operands
+// (two tiles' worth) in the union after its own tile reduction and row sums (qkvPark).
 template <int MB>
 struct StackLds {
   using GuCore = SkinnyCore<2, MB, kNormWaves, kNormUnroll>;
+  using QkvCore = SkinnyCore<1, MB, kNormWaves, kNormUnroll>;
+  using Epi = QkvEpilogue<MB, WriteThroughMem, true>;
+  static constexpr int kQkvParkFloat = QkvCore::kLdsFloats + kNormLdsFloats<MB, kNormWaves>;
   union Shared {
     // the largest stage tile reduction (gate_up), then the RMSNorm row sums
     float gemm[GuCore::kLdsFloats + kNormLdsFloats<MB, kNormWaves>];
     DecodeAttnLds attn;
   };
+  static_assert(kQkvParkFloat % 2 == 0 &&
+                    kQkvParkFloat * sizeof(float) + 2 * Epi::kPairs * sizeof(QkvParked) <=
+                        sizeof(Shared),
+                "the q|k|v epilogue operands fit the union after the stage's own use");
   // as many early slots as fit in 160 KB beside the union (7 up to 32 rows, 5 at 64)
   static constexpr int kEarlyFit =
       static_cast<int>((163840 - 512 - sizeof(Shared)) / sizeof(KvBlockLds));
@@ -179,6 +218,10 @@ struct StackLds {
   };
   int is_last;
   unsigned long long trace[dli_stack::kTraceEvents];  // stamps of the current layer
+
+  __device__ __forceinline__ QkvParked* qkvPark() {
+    return reinterpret_cast<QkvParked*>(p.u.gemm + kQkvParkFloat);
+  }
 };
 
 // Layout of the stack's activation slabs: MFMA fragment order (fragOffset) for the 32- and
@@ -205,6 +248,7 @@ struct ActX<false> {
 template <int MB>
 __device__ void decoderStack(const Args& a) {
   using AX = ActX<(MB >= 2)>;
+  constexpr bool kDppSum = MB == 1;  // see pollStage
   using OCore = SkinnyCore<1, MB, kResWaves, (MB >= 4 ? 2 : 4)>;
   // down_proj splits: wave 0 (the poller of the act wait) takes no K step (kDownIdle)
   using DownCore = SkinnyCore<1, MB, kResWaves, 2, kDownIdle>;
@@ -269,19 +313,27 @@ __device__ void decoderStack(const Args& a) {
     // so q, which attention needs first, is ready after one tile.
     if (jb >= 0) {
       const int H = fresh(a.H), M = fresh(a.M);
-      const QkvParams qp{L.b_qkv,
+      // built where used (prefetch, then each tile's epilogue) from fresh copies, so that none
+      // of it is held, or spilled, across the tile's GEMM
+      auto qkvParams = [&] {
+        const Layer& Lf = a.layer[l];
+        uint16_t* const qs = fresh(a.slabs) + l * fresh(a.slab_elems);
+        return QkvParams{fresh(Lf.b_qkv),
                          fresh(a.cos_t),
                          fresh(a.sin_t),
-                         a.max_pos,
+                         fresh(a.max_pos),
                          fresh(a.positions),
-                         a.pos64,
-                         q,
-                         KvCacheArgs{L.k_pool, L.v_pool, L.block_table, a.block_size,
-                                     a.max_blocks},
-                         M,
-                         a.Hq,
-                         a.Hkv,
-                         a.D};
+                         fresh(a.pos64),
+                         qs,
+                         KvCacheArgs{fresh(Lf.k_pool), fresh(Lf.v_pool), fresh(Lf.block_table),
+                                     fresh(a.block_size), fresh(a.max_blocks)},
+                         fresh(a.M),
+                         fresh(a.Hq),
+                         fresh(a.Hkv),
+                         fresh(a.D),
+                         reinterpret_cast<uint64_t*>(qs),
+                         fresh(tag)};
+      };
       const int j = jb;
       // this workgroup's tiles: t0, then t0 + t_stride while below t_end
       int t0, t_stride, t_end;
@@ -295,17 +347,23 @@ __device__ void decoderStack(const Args& a) {
         t_stride = qkv_wgs;
         t_end = qkv_tiles;
       }
-      QkvEpilogue<MB, Mem> epi0, epi1;  // operands of this workgroup's (at most) two tiles
-      epi0.prefetch(qp, static_cast<int64_t>(t0) * 16);
-      if (t0 + t_stride < t_end) epi1.prefetch(qp, static_cast<int64_t>(t0 + t_stride) * 16);
+      // operands of this workgroup's (at most) two tiles, parked in LDS
+      using Epi = QkvEpilogue<MB, Mem, true>;
+      Epi epi0, epi1;
+      epi0.park = smem.qkvPark();
+      epi1.park = epi0.park + Epi::kPairs;
+      epi0.prefetch(qkvParams(), static_cast<int64_t>(t0) * 16);
+      if (t0 + t_stride < t_end)
+        epi1.prefetch(qkvParams(), static_cast<int64_t>(t0 + t_stride) * 16);
       unsigned kv_written = 0;
-      auto finish = [&](const QkvEpilogue<MB, Mem>& e, int64_t t) {
-        if (t < q_tiles) {  // q: published at once, attention waits for it
-          e.template apply<kQkvQ>(qp, t * 16, lds);
-          arrive(sync + dli_stack::stageWord(dli_stack::kQkvDone), 1);
+      auto finish = [&](int64_t t) {
+        Epi e;  // the operands parked for tile t
+        e.park = smem.qkvPark() + (t == t0 ? 0 : Epi::kPairs);
+        if (t < q_tiles) {  // q: tagged words, which attention polls directly
+          e.template apply<kQkvQ>(qkvParams(), t * 16, lds);
           stamp(a, l, dli_stack::kTrQPublished, smem.trace);
         } else {  // k/v into the cache: attention needs it only for the newest-token block
-          e.template apply<kQkvCache>(qp, t * 16, lds);
+          e.template apply<kQkvCache>(qkvParams(), t * 16, lds);
           ++kv_written;
         }
       };
@@ -314,16 +372,12 @@ __device__ void decoderStack(const Args& a) {
           t_stride, t_end,
           [&] {
             // h of the previous layer (for the first layer: the prologue's copy of x_in)
-            waitAtLeast(sync + dli_stack::stageWord(dli_stack::kDownDone), gen * down_tiles,
-                        abort_word, traceSlot(a, l, dli_stack::kTrQkvPoll, smem.trace));
+            waitAtLeast<kDppSum>(sync + dli_stack::stageWord(dli_stack::kDownDone),
+                                 gen * down_tiles, abort_word,
+                                 traceSlot(a, l, dli_stack::kTrQkvPoll, smem.trace));
             stamp(a, l, dli_stack::kTrQkvWait, smem.trace);
           },
-          [&](int64_t t) {
-            if (t == t0)
-              finish(epi0, t);
-            else
-              finish(epi1, t);
-          },
+          [&](int64_t t) { finish(t); },
           [&](int p) {
             if (p == 2)
               stampLoaded(a, l, dli_stack::kTrQkvX, smem.trace);
@@ -381,21 +435,22 @@ __device__ void decoderStack(const Args& a) {
                               fresh(a.attn_tag),
                               tag,
                               abort_word,
-                              AX::steps(a.Hq * a.D)};
+                              AX::steps(a.Hq * a.D),
+                              reinterpret_cast<const uint64_t*>(q)};
       for (int u = bid; u < attn_units; u += G) {
         const bool merged = decodeAttentionUnit<Mem, true>(
             da, u % splits, u / splits, gen * splits, false, smem.p.u.attn, smem.kv,
             early && l > 0 ? StackLds<MB>::kEarly : 0,
+            [] {},  // q is polled as tagged words
+
             [&] {
-              waitAtLeast(sync + dli_stack::stageWord(dli_stack::kQkvDone), gen * q_tiles,
-                          abort_word);
-              stamp(a, l, dli_stack::kTrAttnWait, smem.trace);
+              pollStage<kDppSum>(sync + dli_stack::stageWord(dli_stack::kKvDone), gen * kv_tiles,
+                                 abort_word);
             },
-            [&] {
-              pollStage(sync + dli_stack::stageWord(dli_stack::kKvDone), gen * kv_tiles,
-                        abort_word);
-            },
-            [&](int point) { stamp(a, l, dli_stack::kTrAttnWave0 + point, smem.trace); });
+            [&](int point) {
+              stamp(a, l, point == 5 ? dli_stack::kTrAttnWait : dli_stack::kTrAttnWave0 + point,
+                    smem.trace);
+            });
         stamp(a, l, dli_stack::kTrAttnUnit, smem.trace);
         if (merged) {
           arrive(sync + dli_stack::stageWord(dli_stack::kAttnDone), 1);
@@ -417,8 +472,8 @@ __device__ void decoderStack(const Args& a) {
       OCore::template runGated<Mem>(
           L.w_o, AX::make(attn, qd), H, qd, M, n0, 0, qd / 64, lds,
           [&] {
-            waitAtLeast(sync + dli_stack::stageWord(dli_stack::kAttnDone), gen * pairs,
-                        abort_word, traceSlot(a, l, dli_stack::kTrOPoll, smem.trace));
+            waitAtLeast<kDppSum>(sync + dli_stack::stageWord(dli_stack::kAttnDone), gen * pairs,
+                                 abort_word, traceSlot(a, l, dli_stack::kTrOPoll, smem.trace));
             stamp(a, l, dli_stack::kTrOWait, smem.trace);
             rt.load(h_prev, nullptr, n0, M, H, AX::steps(H));
           },
@@ -454,8 +509,8 @@ __device__ void decoderStack(const Args& a) {
           L.post_norm,
           a.eps, gu_first, gu_stride, gu_end,
           [&] {
-            waitAtLeast(sync + dli_stack::stageWord(dli_stack::kODone), gen * o_tiles,
-                        abort_word, traceSlot(a, l, dli_stack::kTrGuPoll, smem.trace));
+            waitAtLeast<kDppSum>(sync + dli_stack::stageWord(dli_stack::kODone), gen * o_tiles,
+                                 abort_word, traceSlot(a, l, dli_stack::kTrGuPoll, smem.trace));
             stamp(a, l, dli_stack::kTrGuWait, smem.trace);
           },
           [&](int64_t t) { gateUpEpilogue<MB, Mem>(lds, act, M, F, t, AX::steps(F)); },
@@ -478,8 +533,8 @@ __device__ void decoderStack(const Args& a) {
       const int64_t n0 = static_cast<int64_t>(tile) * 16;
       ResidualTile<MB, kResThreads, Mem> rt;
       auto gate = [&] {
-        waitAtLeast(sync + dli_stack::stageWord(dli_stack::kGateUpDone), gen * gu_tiles,
-                    abort_word, traceSlot(a, l, dli_stack::kTrDownPoll, smem.trace));
+        waitAtLeast<kDppSum>(sync + dli_stack::stageWord(dli_stack::kGateUpDone), gen * gu_tiles,
+                             abort_word, traceSlot(a, l, dli_stack::kTrDownPoll, smem.trace));
         stamp(a, l, dli_stack::kTrDownWait, smem.trace);
         rt.load(h_mid, nullptr, n0, M, H, AX::steps(H));
       };

@@ -29,7 +29,8 @@ struct Args {
   uint16_t* h_out;       // [M, H] residual stream after the last layer
   uint16_t* x0;          // x_in in fragment order (written by the launch's prologue)
   // Activations of layer l live in their own slab at slabs + l * slab_elems (never reused within
-  // a launch): q [M, Hq, D] (row-major) at offset 0; in MFMA fragment order (fragOffset in
+  // a launch): q as [M, Hq, D / 2] tagged 8-byte words (bf16 pair, tag) at offset 0; in MFMA
+  // fragment order (fragOffset in
   // skinny.h, rows padded to the tile's 16 MB) attn [M, Hq D] at off_attn, h_mid [M, H]
   // (residual stream after attention) at off_h_mid, act [M, F] at off_act and h [M, H] (after
   // the layer) at off_h; the last layer writes h_out (row-major) instead, and the first reads
@@ -63,7 +64,7 @@ enum : int {
   kTrQkvWait,         // S1: the previous layer's h is complete
   kTrQPublished,      // S1: this workgroup's q tile is published
   kTrKvPublished,     // S1: this workgroup's k/v tiles are in the cache
-  kTrAttnWait,        // S2: q complete
+  kTrAttnWait,        // S2: every wave has q (tagged words polled by wave 0)
   kTrAttnUnit,        // S2: the unit's partial (or output) is written
   kTrAttnMerged,      // S2: this workgroup merged a pair and published it
   kTrOWait,           // S3: attention complete
@@ -101,8 +102,7 @@ enum : int {
 // at the start and advanced by the last one out, goes into the tags of the tagged partials, so
 // a word left by an earlier launch or layer never carries the tag a reader expects.
 enum : int {
-  kQkvDone = 0,  // every q tile written
-  kKvDone,       // every k/v tile written into the cache
+  kKvDone = 0,   // every k/v tile written into the cache (q travels as tagged words)
   kAttnDone,     // attention output of every pair written
   kODone,        // every o_proj tile (h_mid) written
   kGateUpDone,   // every gate_up tile (act) written
