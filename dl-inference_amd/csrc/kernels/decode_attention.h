@@ -349,7 +349,7 @@ __device__ __forceinline__ bool decodeAttentionUnit(const DecodeAttnArgs& a, int
   // the fewest blocks
   const int merger = n_active > 0 ? n_active - 1 : 0;
   if (!active && (max_splits == 1 || (tagged && split == merger))) {  // empty sequence: zeros
-    for (int idx = threadIdx.x; idx < group * kDecD; idx += kDecThreads)
+    for (int idx = freshThreadIdx(); idx < group * kDecD; idx += kDecThreads)
       Mem::storeU16(attnOut(a, b, kvh * group + idx / kDecD, idx % kDecD), uint16_t{0});
     return true;
   }
@@ -485,7 +485,7 @@ __device__ __forceinline__ bool decodeAttentionUnit(const DecodeAttnArgs& a, int
 #pragma unroll
       for (int e = 0; e < 4; ++e) s.so[wave][d * 16 + 4 * g + e][r] = st8.o[d][e];
     __syncthreads();
-    for (int idx = threadIdx.x; idx < group * kDecD; idx += kDecThreads) {
+    for (int idx = freshThreadIdx(); idx < group * kDecD; idx += kDecThreads) {
       const int hl = idx / kDecD, d = idx % kDecD;
       float M = -INFINITY;
 #pragma unroll
@@ -569,7 +569,7 @@ __device__ __forceinline__ bool decodeAttentionUnit(const DecodeAttnArgs& a, int
   // memory round trips overlap.
   constexpr int kCombineChunk = 8;
   const int n = n_active;
-  for (int idx = threadIdx.x; idx < group * kDecD; idx += kDecThreads) {
+  for (int idx = freshThreadIdx(); idx < group * kDecD; idx += kDecThreads) {
     const int hl = idx / kDecD, d = idx % kDecD;
     const int64_t row = static_cast<int64_t>(b) * a.Hq + kvh * group + hl;
     float M = -INFINITY, l = 0.f, acc = 0.f;

@@ -365,7 +365,7 @@ __device__ __forceinline__ void gateUpEpilogue(const float* lds, uint16_t* out, 
   FP_EXACT;
   constexpr int kTileM = 16 * MB;
   const int64_t f0 = t * 16;
-  for (int idx = threadIdx.x; idx < 16 * kTileM; idx += kNormThreads) {
+  for (int idx = freshThreadIdx(); idx < 16 * kTileM; idx += kNormThreads) {
     const int j = idx % 16, m = idx / 16;
     const int64_t f = f0 + j;
     if (m >= M || f >= F) continue;
@@ -400,7 +400,7 @@ struct ResidualTile {
 
   __device__ __forceinline__ void load(const uint16_t* residual, const uint16_t* bias, int64_t n0,
                                        int M, int64_t N, int frag_steps = 0) {
-    const int idx = threadIdx.x;
+    const int idx = freshThreadIdx();
     const int m = idx / 2;
     const int64_t n = n0 + 8 * (idx % 2);
     const bool live = idx < kItems && m < M;
@@ -428,7 +428,7 @@ struct ResidualTile {
   __device__ __forceinline__ void store(uint16_t* out, int64_t n0, int M, int64_t N, Y&& y,
                                         int frag_steps = 0) const {
     FP_EXACT;
-    const int idx = threadIdx.x;
+    const int idx = freshThreadIdx();
     const int m = idx / 2, half = idx % 2;
     const int64_t n = n0 + 8 * half;
     if (idx >= kItems || m >= M) return;
@@ -464,7 +464,7 @@ __device__ __forceinline__ bool splitKArrive(const float* lds, float* partials, 
                                              int* is_last) {
   FP_EXACT;
   constexpr int kElems = 16 * 16 * MB;
-  for (int idx = threadIdx.x; idx < kElems; idx += kThreadsT)
+  for (int idx = freshThreadIdx(); idx < kElems; idx += kThreadsT)
     __hip_atomic_store(gp(partials) + static_cast<int64_t>(split) * kElems + idx, lds[idx],
                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -480,7 +480,7 @@ __device__ __forceinline__ bool splitKArrive(const float* lds, float* partials, 
   if (!*is_last) return false;
   // The sums replace this workgroup's own partial in lds (every thread has stored it above).
   float* const sums = const_cast<float*>(lds);
-  for (int idx = threadIdx.x; idx < kElems; idx += kThreadsT) {
+  for (int idx = freshThreadIdx(); idx < kElems; idx += kThreadsT) {
     float part[kMaxSplits];
 #pragma unroll
     for (int sp = 0; sp < kMaxSplits; ++sp)
@@ -512,11 +512,11 @@ __device__ __forceinline__ bool splitKTagged(float* lds, uint64_t* partials, int
   FP_EXACT;
   constexpr int kElems = 16 * 16 * MB;
   if (split != 0) {
-    for (int idx = threadIdx.x; idx < kElems; idx += kThreadsT)
+    for (int idx = freshThreadIdx(); idx < kElems; idx += kThreadsT)
       storeTagged(partials + static_cast<int64_t>(split) * kElems + idx, lds[idx], tag);
     return false;
   }
-  for (int idx = threadIdx.x; idx < kElems; idx += kThreadsT) {
+  for (int idx = freshThreadIdx(); idx < kElems; idx += kThreadsT) {
     const uint64_t* ptr[kMaxSplits - 1];
 #pragma unroll
     for (int sp = 1; sp < kMaxSplits; ++sp)

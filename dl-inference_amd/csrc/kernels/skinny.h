@@ -332,7 +332,7 @@ struct SkinnyCore {
 #pragma unroll
         for (int i = 0; i < 4; ++i) mine[(f * 16 + g * 4 + i) * kTileM + b * 16 + r] = acc[f][b][i];
     __syncthreads();
-    for (int idx = threadIdx.x; idx < kTileN * kTileM; idx += kWaves * kWave) {
+    for (int idx = freshThreadIdx(); idx < kTileN * kTileM; idx += kWaves * kWave) {
       float sum = lds[idx];
       for (int v = 1; v < kWaves; ++v) sum += lds[v * kTileN * kTileM + idx];
       lds[idx] = sum;

@@ -99,23 +99,15 @@ __device__ __forceinline__ unsigned waveSum(unsigned v) {
 // polls have passed (which sets the abort word). The loop condition is uniform over the wave.
 // first (tracing, or NULL): receives the time the first poll returned (the wave's loads complete
 // in issue order, so that is also when the loads it issued before the wait had arrived).
-// kDpp: sum the shards with waveSum (DPP, a few cycles) instead of cross-lane shuffles (six
-// LDS-crossbar round trips, ~0.3 us); the 16-row kernel uses it (10-15 us per launch less at
-// batches 1 and 8), the larger ones keep the shuffles, with which the compiler spills less in
-// them (the 32-row kernel measured 5 us per launch slower with waveSum).
-template <bool kDpp>
+// The shards are summed with waveSum (DPP, a few cycles; cross-lane shuffles took six
+// LDS-crossbar round trips, ~0.3 us per poll).
 __device__ __forceinline__ void pollStage(const unsigned* stage, unsigned target,
                                           unsigned* abort_word,
                                           unsigned long long* first = nullptr) {
   const int lane = freshThreadIdx() % kWave;
   for (int spins = 0;; ++spins) {
     unsigned v = lane < dli_stack::kShards ? loadAgent(stage + lane * dli_stack::kLineWords) : 0u;
-    if constexpr (kDpp) {
-      v = waveSum(v);
-    } else {
-#pragma unroll
-      for (int o = 1; o < dli_stack::kShards; o *= 2) v += __shfl_xor(v, o, kWave);
-    }
+    v = waveSum(v);
     if (first != nullptr && spins == 0 && lane == 0) *first = __builtin_amdgcn_s_memrealtime();
     if (__builtin_amdgcn_readfirstlane(v) >= target) break;
     if (spins % kAbortPollEvery == 0 &&
@@ -130,11 +122,10 @@ __device__ __forceinline__ void pollStage(const unsigned* stage, unsigned target
 }
 
 // Returns in every thread of the workgroup once the stage counter reaches target (wave 0 polls).
-template <bool kDpp>
 __device__ __forceinline__ void waitAtLeast(const unsigned* stage, unsigned target,
                                             unsigned* abort_word,
                                             unsigned long long* first = nullptr) {
-  if (threadIdx.x < kWave) pollStage<kDpp>(stage, target, abort_word, first);
+  if (threadIdx.x < kWave) pollStage(stage, target, abort_word, first);
   __syncthreads();
 }
 
@@ -248,7 +239,6 @@ struct ActX<false> {
 template <int MB>
 __device__ void decoderStack(const Args& a) {
   using AX = ActX<(MB >= 2)>;
-  constexpr bool kDppSum = MB == 1;  // see pollStage
   using OCore = SkinnyCore<1, MB, kResWaves, (MB >= 4 ? 2 : 4)>;
   // down_proj splits: wave 0 (the poller of the act wait) takes no K step (kDownIdle)
   using DownCore = SkinnyCore<1, MB, kResWaves, 2, kDownIdle>;
@@ -372,9 +362,8 @@ __device__ void decoderStack(const Args& a) {
           t_stride, t_end,
           [&] {
             // h of the previous layer (for the first layer: the prologue's copy of x_in)
-            waitAtLeast<kDppSum>(sync + dli_stack::stageWord(dli_stack::kDownDone),
-                                 gen * down_tiles, abort_word,
-                                 traceSlot(a, l, dli_stack::kTrQkvPoll, smem.trace));
+            waitAtLeast(sync + dli_stack::stageWord(dli_stack::kDownDone), gen * down_tiles,
+                        abort_word, traceSlot(a, l, dli_stack::kTrQkvPoll, smem.trace));
             stamp(a, l, dli_stack::kTrQkvWait, smem.trace);
           },
           [&](int64_t t) { finish(t); },
@@ -444,8 +433,8 @@ __device__ void decoderStack(const Args& a) {
             [] {},  // q is polled as tagged words
 
             [&] {
-              pollStage<kDppSum>(sync + dli_stack::stageWord(dli_stack::kKvDone), gen * kv_tiles,
-                                 abort_word);
+              pollStage(sync + dli_stack::stageWord(dli_stack::kKvDone), gen * kv_tiles,
+                        abort_word);
             },
             [&](int point) {
               stamp(a, l, point == 5 ? dli_stack::kTrAttnWait : dli_stack::kTrAttnWave0 + point,
@@ -472,8 +461,8 @@ __device__ void decoderStack(const Args& a) {
       OCore::template runGated<Mem>(
           L.w_o, AX::make(attn, qd), H, qd, M, n0, 0, qd / 64, lds,
           [&] {
-            waitAtLeast<kDppSum>(sync + dli_stack::stageWord(dli_stack::kAttnDone), gen * pairs,
-                                 abort_word, traceSlot(a, l, dli_stack::kTrOPoll, smem.trace));
+            waitAtLeast(sync + dli_stack::stageWord(dli_stack::kAttnDone), gen * pairs,
+                        abort_word, traceSlot(a, l, dli_stack::kTrOPoll, smem.trace));
             stamp(a, l, dli_stack::kTrOWait, smem.trace);
             rt.load(h_prev, nullptr, n0, M, H, AX::steps(H));
           },
@@ -509,8 +498,8 @@ __device__ void decoderStack(const Args& a) {
           L.post_norm,
           a.eps, gu_first, gu_stride, gu_end,
           [&] {
-            waitAtLeast<kDppSum>(sync + dli_stack::stageWord(dli_stack::kODone), gen * o_tiles,
-                                 abort_word, traceSlot(a, l, dli_stack::kTrGuPoll, smem.trace));
+            waitAtLeast(sync + dli_stack::stageWord(dli_stack::kODone), gen * o_tiles,
+                        abort_word, traceSlot(a, l, dli_stack::kTrGuPoll, smem.trace));
             stamp(a, l, dli_stack::kTrGuWait, smem.trace);
           },
           [&](int64_t t) { gateUpEpilogue<MB, Mem>(lds, act, M, F, t, AX::steps(F)); },
@@ -533,8 +522,8 @@ __device__ void decoderStack(const Args& a) {
       const int64_t n0 = static_cast<int64_t>(tile) * 16;
       ResidualTile<MB, kResThreads, Mem> rt;
       auto gate = [&] {
-        waitAtLeast<kDppSum>(sync + dli_stack::stageWord(dli_stack::kGateUpDone), gen * gu_tiles,
-                             abort_word, traceSlot(a, l, dli_stack::kTrDownPoll, smem.trace));
+        waitAtLeast(sync + dli_stack::stageWord(dli_stack::kGateUpDone), gen * gu_tiles,
+                    abort_word, traceSlot(a, l, dli_stack::kTrDownPoll, smem.trace));
         stamp(a, l, dli_stack::kTrDownWait, smem.trace);
         rt.load(h_mid, nullptr, n0, M, H, AX::steps(H));
       };
