@@ -401,7 +401,7 @@ __device__ void argmax_finalize_impl(const float* part_val, const int32_t* part_
     linear_residual_splitk_impl<MB>(x, w, bias, residual, out, M, N, K, splits, partials,         \
                                     counters);                                                    \
   }                                                                                               \
-  extern "C" __global__ void __launch_bounds__(kThreads, 2) linear_partial_m##MB(                 \
+  extern "C" __global__ void __launch_bounds__(kThreads, MB >= 4 ? 1 : 2) linear_partial_m##MB(   \
       const uint16_t* x, const uint16_t* w, float* partials, int M, int64_t N, int K,             \
       int splits) {                                                                               \
     linear_partial_impl<MB>(x, w, partials, M, N, K, splits);                                     \
