@@ -516,7 +516,13 @@ __device__ void decoderStack(const Args& a) {
 
     // S5: down_proj + MLP residual. With one split a tile is reduced over the full K; with
     // several the last split of a tile to finish sums the partials and writes h.
-    for (int u = bid; u < down_units; u += G) {
+    // Unit of workgroup w < down_units: with the units a multiple of the 8 XCDs (workgroups
+    // are dealt to them round-robin, w on XCD w % 8), unit (w % 8) * (down_units / 8) + w / 8,
+    // so that each XCD holds the units of one or two splits and its L2 fetches those splits'
+    // share of act rather than all of it.
+    const bool xcd_order = down_units % 8 == 0 && down_units <= G;
+    for (int w = bid; w < down_units; w += G) {
+      const int u = xcd_order ? (w % 8) * (down_units / 8) + w / 8 : w;
       const int H = fresh(a.H), M = fresh(a.M), F = fresh(a.F);
       const int tile = u % down_tiles, split = u / down_tiles;
       const int64_t n0 = static_cast<int64_t>(tile) * 16;
