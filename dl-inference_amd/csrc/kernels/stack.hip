@@ -404,7 +404,8 @@ __device__ void decoderStack(const Args& a) {
       stageThirdKvBlocks(dn, bid % splits, bid / splits, smem.kv, StackLds<MB>::kEarly);
     };
     if (bid < attn_units) {
-      // split partials as tagged words: split 0 merges as they arrive, no pair counter
+      // split partials as tagged words: the last active split merges them as they arrive, no
+      // pair counter
       const DecodeAttnArgs da{q,
                               L.k_pool,
                               L.v_pool,
@@ -431,7 +432,6 @@ __device__ void decoderStack(const Args& a) {
             da, u % splits, u / splits, gen * splits, false, smem.p.u.attn, smem.kv,
             early && l > 0 ? StackLds<MB>::kEarly : 0,
             [] {},  // q is polled as tagged words
-
             [&] {
               pollStage(sync + dli_stack::stageWord(dli_stack::kKvDone), gen * kv_tiles,
                         abort_word);
