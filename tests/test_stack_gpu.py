@@ -135,13 +135,12 @@ def _fill_caches(sessions, cfg, seed):
                 p[name].copy_(val)
 
 
-@pytest.mark.parametrize("splits", [3, 4])
-def test_stack_long_context_split_merge_bitwise(splits):
+@pytest.mark.parametrize("batch,splits", [(32, 3), (32, 4), (4, 6), (2, 9)])
+def test_stack_long_context_split_merge_bitwise(batch, splits):
     """Context up to 4096 keys: every pair's keys are split over several workgroups and merged
-    by the last to finish, in both paths."""
+    by the last to finish, in both paths (up to 9 splits, the most a 65-block context uses)."""
     cfg = tiny_config(layers=2)
     w = random_weights(cfg, seed=81, device="cuda")
-    batch = 32
     fused, stack = _pair(cfg, w, batch, 4096 + 64, attn=splits)
     start = torch.tensor([4000 - 37 * b for b in range(batch)], device="cuda")
     ids0 = torch.randint(0, cfg.vocab, (batch,), generator=torch.Generator().manual_seed(82))
