@@ -31,9 +31,10 @@
 // through attention, so they request the o_proj weights meanwhile); gate_up tiles bid,
 // bid + a_wgs, ... to the a_wgs other workgroups; down_proj units to the first ones. q and the
 // new k/v are signalled apart: attention needs q at once, and q goes out as tagged words
-// (common.h) that each attention wave polls directly, with no store acknowledgement and no
-// counter between the q|k|v tile and the unit; the new k/v is needed only for the block holding
-// the newest token and has its own counter. A wave with a third cache block stages it in LDS
+// (common.h) that wave 0 of each attention unit polls directly and hands to the other waves
+// through LDS, with no store acknowledgement and no counter between the q|k|v tile and the
+// unit; the new k/v is needed only for the block holding the newest token and has its own
+// counter. A wave with a third cache block stages it in LDS
 // (direct global-to-LDS loads) next to the two it requests into registers, so nothing streams
 // after the wait; waves 0..kEarly-1 stage it during the previous layer, right after their
 // attention unit, so that part of the K/V stream overlaps o_proj, gate_up and down_proj, when
@@ -515,7 +516,8 @@ __device__ void decoderStack(const Args& a) {
     }
 
     // S5: down_proj + MLP residual. With one split a tile is reduced over the full K; with
-    // several the last split of a tile to finish sums the partials and writes h.
+    // several, split 0 of a tile adds the other splits' tagged partials as they arrive and
+    // writes h.
     // Unit of workgroup w < down_units: with the units a multiple of the 8 XCDs (workgroups
     // are dealt to them round-robin, w on XCD w % 8), unit (w % 8) * (down_units / 8) + w / 8,
     // so that each XCD holds the units of one or two splits and its L2 fetches those splits'
