@@ -247,8 +247,8 @@ struct DecodeAttnLds {
   float sm[kDecWaves][16];
   float sl[kDecWaves][16];
   float so[kDecWaves][kDecD][17];
-  // q of the unit, handed from wave 0 to the others (tagged q). Kept clear of the first 4 KB,
-  // which a caller may overlay with the last wave's staged cache block.
+  // q of the unit, handed from wave 0 to the others (tagged q). Kept clear of the first
+  // sizeof(KvBlockLds) bytes, which a caller may overlay with the last wave's staged cache block.
   U128 q[2 * kWave];
   int is_last;
 };
