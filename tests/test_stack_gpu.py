@@ -104,6 +104,42 @@ def test_stack_graph_replay_equals_fused_eager():
                  cfg.layers)
 
 
+@pytest.mark.parametrize("stack", [True, False])
+def test_multi_step_graph_equals_single_steps(stack):
+    """capture(chain_ids=True, steps=3): one graph launch runs three greedy steps, each reading
+    the previous step's next_ids and its own row of step_positions. The last step's logits and
+    ids, the chained input ids and every layer's KV cache (which holds the keys and values of
+    all three new tokens) equal three one-step replays, bit for bit."""
+    cfg = tiny_config(layers=2)
+    w = random_weights(cfg, seed=53, device="cuda")
+    prompt = _prompt(cfg, 4, 4, 54)
+    single = DecodeSession(cfg, w, 4, max_seq_len=64, stack=stack).capture()
+    multi = DecodeSession(cfg, w, 4, max_seq_len=64, stack=stack)
+    ids = _run_steps(single, prompt, 0)[-1][1].cuda()
+    assert torch.equal(_run_steps(multi, prompt, 0)[-1][1].cuda(), ids)
+    pos = torch.full((4,), prompt.shape[1], dtype=torch.int64, device="cuda")
+    expect = []
+    for t in range(3):
+        logits, nxt = single.step(ids if t == 0 else expect[-1][1].cuda(), pos + t)
+        expect.append((logits.float().cpu().clone(), nxt.cpu().clone()))
+    multi.capture(chain_ids=True, steps=3)
+    with pytest.raises(ValueError):
+        multi.step(ids, pos)
+    multi.ids.copy_(ids)
+    for t in range(3):
+        multi.step_positions[t].copy_(pos + t)
+    out = multi.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(out["logits"].float().cpu(), expect[-1][0]), "last step's logits differ"
+    assert torch.equal(out["next_ids"].cpu(), expect[-1][1]), "last step's ids differ"
+    assert torch.equal(multi.ids.cpu(), expect[-1][1]), "chained input ids differ"
+    for i in range(cfg.layers):
+        ea = single.engine.kv_cache_entry(f"layer_{i}")
+        eb = multi.engine.kv_cache_entry(f"layer_{i}")
+        assert torch.equal(ea["key_pool"], eb["key_pool"]), f"key cache of layer {i} differs"
+        assert torch.equal(ea["value_pool"], eb["value_pool"]), f"value cache of layer {i} differs"
+
+
 def test_stack_qwen2_0_5b_shape_batch32_bitwise():
     """All 24 layers of the Qwen2-0.5B shape at batch 32 (one launch)."""
     cfg = QWEN2_0_5B
