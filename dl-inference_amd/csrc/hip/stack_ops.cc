@@ -139,7 +139,7 @@ int dli_hip_decoder_stack(const DliDecoderLayer* layers, int num_layers, const v
                           const DliStackOptions* options, void* stream) {
   if (layers == nullptr || num_layers < 0) return bad("layers is NULL");
   if (num_layers == 0) return 0;
-  const DliStackOptions opt = options != nullptr ? *options : DliStackOptions{0, nullptr, 0};
+  const DliStackOptions opt = options != nullptr ? *options : DliStackOptions{};
   if (opt.attention_splits < 0 || opt.attention_splits > kMaxDecodeSplits)
     return bad("attention_splits must be in [0, 32]");
   if (opt.trace != nullptr && opt.trace_layers <= 0)
@@ -160,9 +160,17 @@ int dli_hip_decoder_stack(const DliDecoderLayer* layers, int num_layers, const v
   if (cos_table == nullptr || sin_table == nullptr || max_pos <= 0)
     return bad("rotary tables are required");
   if (max_blocks <= 0) return bad("empty cache geometry");
-  if (hidden_in == nullptr || hidden_out == nullptr) return bad("hidden_in/hidden_out are NULL");
-  if (!aligned16(hidden_in) || !aligned16(hidden_out))
-    return bad("hidden_in and hidden_out must be 16-byte aligned");
+  const bool from_ids = opt.token_ids != nullptr;
+  if (from_ids) {
+    if (opt.token_ids_dtype != DLI_I64 && opt.token_ids_dtype != DLI_I32)
+      return bad("token_ids must be int64 or int32");
+    if (opt.embedding == nullptr || !aligned16(opt.embedding) || opt.vocab <= 0)
+      return bad("token_ids need a 16-byte aligned embedding table and vocab > 0");
+  } else if (hidden_in == nullptr || !aligned16(hidden_in)) {
+    return bad("hidden_in is NULL or not 16-byte aligned");
+  }
+  if (hidden_out == nullptr || !aligned16(hidden_out))
+    return bad("hidden_out is NULL or not 16-byte aligned");
   for (int i = 0; i < num_layers; ++i) {
     const DliDecoderLayer& L = layers[i];
     if (L.input_norm == nullptr || L.w_qkv == nullptr || L.w_o == nullptr ||
@@ -229,6 +237,11 @@ int dli_hip_decoder_stack(const DliDecoderLayer* layers, int num_layers, const v
     a.layers = count;
     a.trace_base = first;
     a.x_in = static_cast<const uint16_t*>(first == 0 ? hidden_in : hidden_out);
+    // the first launch gathers the embedding rows of token_ids; later ones continue from h_out
+    a.token_ids = first == 0 && from_ids ? opt.token_ids : nullptr;
+    a.ids64 = opt.token_ids_dtype == DLI_I64 ? 1 : 0;
+    a.embed = static_cast<const uint16_t*>(opt.embedding);
+    a.vocab = opt.vocab;
     for (int i = 0; i < dli_stack::kMaxLayers; ++i) {
       dli_stack::Layer& d = a.layer[i];
       if (i >= count) {

@@ -269,14 +269,24 @@ __device__ void decoderStack(const Args& a) {
     for (int e = 0; e < dli_stack::kTraceEvents; ++e) smem.trace[e] = 0;
   // launch epoch (advanced only by the last workgroup out, after every workgroup has read it)
   const unsigned epoch = __builtin_amdgcn_readfirstlane(loadAgent(a.sync + dli_stack::kEpochWord));
-  // Prologue: x_in (row-major) into x0 in fragment order, one 16-column tile per workgroup like
-  // a down_proj tile, counted on kDownDone as the output of "layer -1" (so every layer's q|k|v
-  // waits for (l + 1) x down_tiles arrivals and reads its x in fragment order).
+  // Prologue: x_in (row-major), or the embedding rows of token_ids (embedding/kernel.py:6-23:
+  // a zero row for an id out of range), into x0 in fragment order, one 16-column tile per
+  // workgroup like a down_proj tile, counted on kDownDone as the output of "layer -1" (so every
+  // layer's q|k|v waits for (l + 1) x down_tiles arrivals and reads its x in fragment order).
   for (int t = bid; t < down_tiles; t += G) {
     const int m = threadIdx.x / 2;  // thread item: 8 columns of one row
     const int64_t n = static_cast<int64_t>(t) * 16 + 8 * (threadIdx.x % 2);
-    if (m < a.M)  // the host checks 16-byte alignment and H % 64 == 0
-      Mem::store16(a.x0 + actOffset(m, n, a.H, AX::steps(a.H)), gload16(a.x_in + m * a.H + n));
+    if (m < a.M) {  // the host checks 16-byte alignment and H % 64 == 0
+      U128 v;
+      if (a.token_ids != nullptr) {
+        const int64_t id = a.ids64 ? static_cast<const int64_t*>(a.token_ids)[m]
+                                   : static_cast<const int32_t*>(a.token_ids)[m];
+        v = id >= 0 && id < a.vocab ? gload16(a.embed + id * a.H + n) : zero16();
+      } else {
+        v = gload16(a.x_in + m * a.H + n);
+      }
+      Mem::store16(a.x0 + actOffset(m, n, a.H, AX::steps(a.H)), v);
+    }
     arrive(a.sync + dli_stack::stageWord(dli_stack::kDownDone), 1);
   }
   for (int l = 0; l < a.layers; ++l) {

@@ -26,6 +26,13 @@ struct Layer {
 struct Args {
   Layer layer[kMaxLayers];
   const uint16_t* x_in;  // [M, H] residual stream entering the first layer
+  // When non-NULL, the first layer's input rows are instead rows token_ids[m] of embed
+  // ([vocab, H]; a zero row for an id outside [0, vocab)), gathered by the prologue; x_in is
+  // then not read.
+  const void* token_ids;  // [M] int32/int64 (ids64)
+  const uint16_t* embed;
+  int64_t vocab;
+  int ids64;
   uint16_t* h_out;       // [M, H] residual stream after the last layer
   uint16_t* x0;          // x_in in fragment order (written by the launch's prologue)
   // Activations of layer l live in their own slab at slabs + l * slab_elems (never reused within
@@ -34,7 +41,7 @@ struct Args {
   // skinny.h, rows padded to the tile's 16 MB) attn [M, Hq D] at off_attn, h_mid [M, H]
   // (residual stream after attention) at off_h_mid, act [M, F] at off_act and h [M, H] (after
   // the layer) at off_h; the last layer writes h_out (row-major) instead, and the first reads
-  // x0, the prologue's fragment-order copy of x_in.
+  // x0, the prologue's fragment-order copy of x_in (or of the embedding rows).
   uint16_t* slabs;
   int64_t slab_elems, off_attn, off_h_mid, off_act, off_h;
   const float* cos_t;  // [max_pos, D / 2]

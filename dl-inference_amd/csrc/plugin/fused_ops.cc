@@ -286,6 +286,9 @@ class LmHeadArgmaxOp final : public Operator {
 // [B], cos, sin, then per layer: input_layernorm.weight, qkv_proj.weight, qkv_proj.bias,
 // o_proj.weight, post_attention_layernorm.weight, gate_up_proj.weight, down_proj.weight; then,
 // optionally, a stage-timeline buffer (int64, layers x CUs x DLI_STACK_TRACE_EVENTS entries: DliStackOptions.trace).
+// With token ids instead of hidden (int64/int32 [B]) the embedding table [vocab, H] follows the
+// layer weights (before the timeline buffer) and the launch gathers the first layer's input
+// rows itself (the model.embed_tokens node folded in: DliStackOptions.token_ids).
 // Attributes: attention_splits (0 = the launch's choice; the paged_attention node's count makes
 // the two bit-identical), down_splits, eps, kv_cache_prefix, check_status.
 // Layer i appends to and attends over cache entry kv_cache_prefix + i. Computes what the
@@ -298,15 +301,29 @@ class DecoderStackOp final : public Operator {
                const Attributes& attrs, ExecutionContext& ctx) const override {
     constexpr std::size_t kPerLayer = 7, kHead = 4;
     const auto layers = attrs.require<std::int64_t>("layers");
-    const std::size_t n_in = kHead + kPerLayer * static_cast<std::size_t>(layers);
-    if (layers < 1 || (in.size() != n_in && in.size() != n_in + 1))
+    const std::size_t n_layer_in = kHead + kPerLayer * static_cast<std::size_t>(layers);
+    if (layers < 1 || in.empty())
       throw std::invalid_argument("decoder_stack expects 4 + 7 * layers inputs (+ a trace buffer)");
+    const bool from_ids = in[0]->dtype() == DType::Int64 || in[0]->dtype() == DType::Int32;
+    const std::size_t n_in = n_layer_in + (from_ids ? 1 : 0);  // + the embedding table
+    if (in.size() != n_in && in.size() != n_in + 1)
+      throw std::invalid_argument(from_ids ? "decoder_stack expects token ids, 3 + 7 * layers "
+                                             "inputs, the embedding table (+ a trace buffer)"
+                                           : "decoder_stack expects 4 + 7 * layers inputs (+ a "
+                                             "trace buffer)");
     if (out.size() != 1 && out.size() != 2)
       throw std::invalid_argument("decoder_stack outputs: hidden (, status)");
     requireArity(in, out, in.size(), in.size(), out.size(), type());
     requireCudaInputs(in, type());
     const Tensor &x = *in[0], &pos = *in[1], &cos = *in[2], &sin = *in[3];
-    requireBf16(x, type(), "hidden");
+    const Tensor* embed = from_ids ? in[n_layer_in] : nullptr;
+    if (from_ids) {
+      requireBf16(*embed, type(), "embedding table");
+      if (embed->rank() != 2 || x.rank() != 1)
+        throw std::invalid_argument("decoder_stack token ids must be [B], the table [vocab, H]");
+    } else {
+      requireBf16(x, type(), "hidden");
+    }
     requireIndex(pos, type(), "positions");
     requireFloat(cos, type());
     requireFloat(sin, type());
@@ -331,7 +348,14 @@ class DecoderStackOp final : public Operator {
       options.trace = static_cast<unsigned long long*>(ptr(trace));
     }
     const std::string prefix = attrs.value_or<std::string>("kv_cache_prefix", "layer_");
-    const std::int64_t hidden = x.shape().back(), m = rowsOf(x);
+    const std::int64_t hidden = from_ids ? embed->dim(1) : x.shape().back();
+    const std::int64_t m = from_ids ? static_cast<std::int64_t>(x.numel()) : rowsOf(x);
+    if (from_ids) {
+      options.token_ids = ptr(x);
+      options.token_ids_dtype = hipDtype(x.dtype());
+      options.embedding = ptr(*embed);
+      options.vocab = embed->dim(0);
+    }
     const std::int64_t n_qkv = (hq + 2 * hkv) * d;
     if (static_cast<std::int64_t>(pos.numel()) != m)
       throw std::invalid_argument("decoder_stack positions must have one entry per row");
@@ -367,7 +391,9 @@ class DecoderStackOp final : public Operator {
                           ptr(e.key_pool), ptr(e.value_pool),
                           static_cast<const std::int32_t*>(ptr(e.block_table))};
     }
-    *out[0] = Tensor::cuda(DType::BFloat16, x.shape(), x.deviceId());
+    *out[0] = Tensor::cuda(DType::BFloat16,
+                           from_ids ? std::vector<std::int64_t>{m, hidden} : x.shape(),
+                           x.deviceId());
     const std::size_t ws_bytes = dli_hip_decoder_stack_workspace(
         static_cast<int>(layers), m, hidden, hq, hkv, d, ffn, max_blocks,
         static_cast<int>(down_splits), options.attention_splits);
@@ -377,7 +403,8 @@ class DecoderStackOp final : public Operator {
     // the node lists one, is that word. A driver reads it after a synchronization it makes anyway
     // and zeroes it.
     void* status = status_.get(sizeof(unsigned), x.deviceId(), ctx.stream);
-    check(dli_hip_decoder_stack(table.data(), static_cast<int>(layers), ptr(x), ptr(*out[0]),
+    check(dli_hip_decoder_stack(table.data(), static_cast<int>(layers),
+                                from_ids ? nullptr : ptr(x), ptr(*out[0]),
                                 ptr(pos), hipDtype(pos.dtype()),
                                 static_cast<const float*>(ptr(cos)),
                                 static_cast<const float*>(ptr(sin)), cos.dim(0), block_size,

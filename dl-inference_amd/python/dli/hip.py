@@ -136,7 +136,9 @@ class DecoderLayer(ctypes.Structure):
 
 class StackOptions(ctypes.Structure):
     """DliStackOptions: per-call options of dli_hip_decoder_stack (include/dli_hip.h)."""
-    _fields_ = [("attention_splits", _int), ("trace", _c_void_p), ("trace_layers", _int)]
+    _fields_ = [("attention_splits", _int), ("trace", _c_void_p), ("trace_layers", _int),
+                ("token_ids", _c_void_p), ("token_ids_dtype", _int), ("embedding", _c_void_p),
+                ("vocab", ctypes.c_int64)]
 
 
 class HipError(RuntimeError):

@@ -11,8 +11,9 @@ linear_residual for o_proj and for down_proj), then one lm_head_argmax node that
 model.norm.
 Same rounding points, same tensor names for inputs and outputs.
 
-stack graph (fused=True, stack=True): the decoder layers of the fused graph as one
-decoder_stack node (one persistent launch for all layers), bit-identical to the fused graph. It
+stack graph (fused=True, stack=True): the embedding and the decoder layers of the fused graph
+as one decoder_stack node (one persistent launch for all layers, which gathers the token rows of
+the embedding table itself), bit-identical to the fused graph. It
 has a third output, `status` (int32 [1], the launch status the decoder_stack node accumulates:
 non-zero when a wait in the persistent launch gave up and the step's outputs are invalid), which
 the decode drivers check where they synchronize anyway.
@@ -216,14 +217,16 @@ def _stack_nodes(cfg: Qwen2Config, nodes: list, splits: dict, logits_dtype: str,
     (model.norm inside lm_head_argmax) as in the fused graph. Same rounding points and values as
     the fused graph with o split 1 and the same attention split count (splits["attn"], 0 = each
     path's own choice). stack_trace: the node also reads graph input "stack_trace", an int64
-    buffer that receives the launch's stage timeline."""
-    inputs = ["hidden_states", "positions", "rotary_cos", "rotary_sin"]
+    buffer that receives the launch's stage timeline. The node takes the token ids and the
+    embedding table itself (model.embed_tokens folded into the launch: no embedding node)."""
+    inputs = ["input_ids", "positions", "rotary_cos", "rotary_sin"]
     for i in range(cfg.layers):
         p = f"model.layers.{i}"
         inputs += [f"{p}.input_layernorm.weight", f"{p}.self_attn.qkv_proj.weight",
                    f"{p}.self_attn.qkv_proj.bias", f"{p}.self_attn.o_proj.weight",
                    f"{p}.post_attention_layernorm.weight", f"{p}.mlp.gate_up_proj.weight",
                    f"{p}.mlp.down_proj.weight"]
+    inputs.append("model.embed_tokens.weight")
     if stack_trace:
         inputs.append("stack_trace")
     _node(nodes, "model.layers", "decoder_stack", inputs, ["layers_output", "status"],
@@ -270,8 +273,9 @@ def build_decode_graph(cfg: Qwen2Config, batch: int, fused: bool = True,
     choice}; stack_trace: the decoder_stack node records its stage timeline into graph input
     "stack_trace" (int64, layers x CUs x 24)."""
     nodes: list = []
-    _node(nodes, "model.embed_tokens", "embedding", ["input_ids", "model.embed_tokens.weight"],
-          ["hidden_states"])
+    if not (fused and stack) or uses_large_graph(cfg, fused):  # the stack gathers it itself
+        _node(nodes, "model.embed_tokens", "embedding", ["input_ids", "model.embed_tokens.weight"],
+              ["hidden_states"])
     if uses_large_graph(cfg, fused):
         _large_nodes(cfg, batch, nodes, splits or large_splits(batch), large_fused)
         graph = {"format": "dli.graph.v1", "model_type": "qwen2_decode_large",

@@ -454,12 +454,22 @@ typedef struct DliDecoderLayer {
  *   csrc/kernels/stack_args.h (0 = layer entry ... 12 = down_proj done). The buffer holds
  *   trace_layers * grid * DLI_STACK_TRACE_EVENTS uint64 of device memory; events a workgroup
  *   does not reach are left
- *   as they were. */
+ *   as they were.
+ * token_ids, token_ids_dtype, embedding, vocab: with token_ids non-NULL (device [batch],
+ *   token_ids_dtype DLI_I64 or DLI_I32) the first layer's input is row token_ids[b] of
+ *   embedding (device bf16 [vocab, hidden_size], 16-byte aligned; a zero row for an id outside
+ *   [0, vocab)), which is what dli_hip_embedding writes, gathered by the launch itself, and
+ *   hidden_in is not read (it may be NULL). This folds the model.embed_tokens node
+ *   (export.py:273-279) into the launch and saves its kernel launch per step. */
 #define DLI_STACK_TRACE_EVENTS 32
 typedef struct DliStackOptions {
   int attention_splits;
   unsigned long long* trace;
   int trace_layers;
+  const void* token_ids;
+  int token_ids_dtype;
+  const void* embedding;
+  int64_t vocab;
 } DliStackOptions;
 
 /* Workspace bytes for dli_hip_decoder_stack with num_layers layers (arrival counters, partials
@@ -471,7 +481,7 @@ size_t dli_hip_decoder_stack_workspace(int num_layers, int64_t batch, int64_t hi
                                        int attention_splits);
 
 /* hidden_out = the residual stream after `num_layers` layers applied to hidden_in [batch,
- * hidden_size] (hidden_out may equal hidden_in). Each layer appends its new k/v at
+ * hidden_size] (hidden_out may equal hidden_in; or to the embedding rows of options->token_ids). Each layer appends its new k/v at
  * positions[b] and attends over keys [0, positions[b]]. The workspace must be zero-filled
  * before its first use; every call leaves it ready for the next one on the same stream. Calls
  * that share a workspace must not overlap.

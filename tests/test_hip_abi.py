@@ -210,4 +210,16 @@ def test_decoder_stack_rejects_invalid_arguments():
     assert b"attention_splits must be in [0, 32]" in lib.dli_hip_last_error()
     assert call(options=ctypes.byref(hip.StackOptions(0, 256, 0))) == -1
     assert b"trace_layers must be positive" in lib.dli_hip_last_error()
+    # token ids in place of hidden_in (the embedding gathered by the launch)
+    assert lib.dli_hip_decoder_stack(ctypes.byref(layer), 1, None, fake, fake, hip.I64, fake,
+                                     fake, 1024, 64, 64, 32, 896, 14, 2, 64, 4864, 1e-6, 3, fake,
+                                     1 << 20, None, None, None) == -1
+    assert b"hidden_in is NULL" in lib.dli_hip_last_error()
+    for dtype, table, vocab, msg in ((hip.F32, 256, 1000, b"token_ids must be int64 or int32"),
+                                     (hip.I64, None, 1000, b"embedding table"),
+                                     (hip.I32, 258, 1000, b"embedding table"),
+                                     (hip.I64, 256, 0, b"vocab > 0")):
+        opts = hip.StackOptions(0, None, 0, 256, dtype, table, vocab)
+        assert call(options=ctypes.byref(opts)) == -1
+        assert msg in lib.dli_hip_last_error()
     assert lib.dli_hip_decoder_stack_workspace(24, 32, 896, 14, 2, 64, 4864, 65, 3, 33) == 0
