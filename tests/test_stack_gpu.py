@@ -150,6 +150,43 @@ def test_stack_qwen2_0_5b_shape_batch32_bitwise():
                  _run_steps(stack, prompt, 3, start=60), cfg.layers)
 
 
+def test_bench_step_matches_the_fp32_logit_session():
+    """The benchmark's own step: Qwen2-0.5B shape, batch 32, every sequence at position 4095 of
+    a seeded 4095-key context, the stack graph with bf16 logits, captured as 5 chained greedy
+    steps in one graph. Against a stack session with fp32 logits stepped one replay at a time:
+    lm_head_argmax picks the ids from the fp32 logits before it rounds them, so after 5 steps
+    the ids are equal and the bf16 logits are the fp32 logits rounded, bit for bit."""
+    cfg, b, ctx = QWEN2_0_5B, 32, 4096
+    w = random_weights(cfg, seed=81, device="cuda")
+    ref = DecodeSession(cfg, w, b, max_seq_len=ctx + 64, stack=True)
+    bench = DecodeSession(cfg, w, b, max_seq_len=ctx + 64, stack=True,
+                          logits_dtype="bfloat16")
+    g = torch.Generator(device="cuda").manual_seed(82)
+    ids = torch.randint(0, cfg.vocab, (b,), generator=g, device="cuda")
+    pos = torch.full((b,), ctx - 1, dtype=torch.int64, device="cuda")
+    for sess in (ref, bench):
+        sess.ids.copy_(ids)
+        sess.positions.copy_(pos)
+        sess.run_eager()  # reserves the caches
+    _fill_caches([ref, bench], cfg, 83)
+    ref.capture()
+    nxt = ids
+    for _ in range(5):
+        logits, nxt = ref.step(nxt, pos)
+        nxt = nxt.clone()
+    bench.ids.copy_(ids)
+    bench.positions.copy_(pos)
+    bench.capture(chain_ids=True, steps=5)
+    bench.ids.copy_(ids)
+    out = bench.replay()
+    torch.cuda.synchronize()
+    bench.check_status()
+    assert torch.equal(out["next_ids"], nxt), "ids differ after 5 steps"
+    assert torch.equal(bench.ids, nxt), "chained input ids differ"
+    assert out["logits"].dtype == torch.bfloat16
+    assert torch.equal(out["logits"], logits.to(torch.bfloat16)), "bf16 logits != rounded fp32"
+
+
 def test_stack_more_layers_than_one_launch():
     """40 layers run as two launches (32 + 8) that continue from the same output buffer."""
     cfg = tiny_config(layers=40)
