@@ -243,10 +243,17 @@ __device__ __forceinline__ uint16_t* attnOut(const DecodeAttnArgs& a, int64_t b,
 constexpr int kTagSlot = kDecD + 2;  // tagged words per (row, split): O, then m and l
 
 // LDS of one unit (kDecWaves waves).
+// Splits whose words the merger polls per round (decodeAttentionUnit): kMergeChunk in the
+// general loop; up to kOneRoundSplits in one round when it would take more than one.
+constexpr int kMergeChunk = 4;
+constexpr int kOneRoundSplits = 8;
+
 struct DecodeAttnLds {
   float sm[kDecWaves][16];
   float sl[kDecWaves][16];
   float so[kDecWaves][kDecD][17];
+  float pm[kOneRoundSplits][16];  // the other splits' (m, l) of each head, for the merger
+  float pl[kOneRoundSplits][16];
   // q of the unit, handed from wave 0 to the others (tagged q). Kept clear of the first
   // sizeof(KvBlockLds) bytes, which a caller may overlay with the last wave's staged cache block.
   U128 q[2 * kWave];
@@ -309,7 +316,8 @@ __device__ __forceinline__ void stageThirdKvBlocks(const DecodeAttnArgs& a, int 
 // blocks are attended, 1 when every wave's are (after the barrier), 2 after the unit's arrival,
 // 3 and 4 when this wave has attended its first and second block, 5 when this wave has q.
 static_assert(offsetof(DecodeAttnLds, q) >= sizeof(KvBlockLds), "q clear of a staged block");
-template <class Mem, bool kPreload, class Gate, class KvReady, class Mark = NoMark>
+template <class Mem, bool kPreload, bool kOneRound = false, class Gate, class KvReady,
+          class Mark = NoMark>
 __device__ __forceinline__ bool decodeAttentionUnit(const DecodeAttnArgs& a, int split, int pair,
                                                     unsigned arrivals, bool reset,
                                                     DecodeAttnLds& s, KvBlockLds* stage,
@@ -485,6 +493,59 @@ __device__ __forceinline__ bool decodeAttentionUnit(const DecodeAttnArgs& a, int
 #pragma unroll
       for (int e = 0; e < 4; ++e) s.so[wave][d * 16 + 4 * g + e][r] = st8.o[d][e];
     __syncthreads();
+    // The merger in one polling round where the loop below would take several (more than
+    // kMergeChunk other splits, at most kOneRoundSplits) and the unit's (head, d) items leave
+    // its last wave free: that wave polls the splits' (m, l) words into LDS while each item
+    // thread polls its O[d] words, so the merge waits one round trip after the last partial
+    // lands rather than one per chunk. The arithmetic and the split order are the loop's.
+    // (With one chunk the loop is faster: no barrier between the polls and the combine.)
+    // kOneRound compiles this path in: the 16-row stack kernel (small batches, up to 9 splits
+    // per pair); the others keep the code they had, which measured faster at batch 32.
+    if (kOneRound && tagged && split == merger && merger > kMergeChunk &&
+        merger <= kOneRoundSplits && group * kDecD <= kDecThreads - kWave) {
+      const int t = freshThreadIdx();
+      const int hl = t / kDecD, d = t % kDecD;
+      const bool item = t < group * kDecD;
+      float M = -INFINITY, l = 0.f, acc = 0.f, o[kOneRoundSplits];
+      if (t >= kDecThreads - kWave) {
+        const int j = t - (kDecThreads - kWave);
+        if (j < group * merger) {
+          const int h = j / merger, sp = j % merger;
+          const int64_t row = static_cast<int64_t>(b) * a.Hq + kvh * group + h;
+          const uint64_t* const slot = a.ws_tag + (row * max_splits + sp) * kTagSlot;
+          const uint64_t* const p[2] = {slot + kDecD, slot + kDecD + 1};
+          float v[2];
+          loadTagged<2>(v, p, 2, a.tag, a.abort_word);
+          s.pm[sp][h] = v[0];
+          s.pl[sp][h] = v[1];
+        }
+      } else if (item) {
+#pragma unroll
+        for (int w = 0; w < kDecWaves; ++w) M = fmaxf(M, s.sm[w][hl]);
+#pragma unroll
+        for (int w = 0; w < kDecWaves; ++w) {
+          const float e = s.sm[w][hl] == -INFINITY ? 0.f : exp2f(s.sm[w][hl] - M);
+          l += e * s.sl[w][hl];
+          acc += e * s.so[w][d][hl];
+        }
+        const int64_t row = static_cast<int64_t>(b) * a.Hq + kvh * group + hl;
+        const uint64_t* ptr[kOneRoundSplits];
+#pragma unroll
+        for (int c = 0; c < kOneRoundSplits; ++c)  // dead slots repeat split 0
+          ptr[c] = a.ws_tag + (row * max_splits + (c < merger ? c : 0)) * kTagSlot + d;
+        loadTagged<kOneRoundSplits>(o, ptr, kOneRoundSplits, a.tag, a.abort_word);
+      }
+      __syncthreads();
+      if (item) {
+        float Mt = -INFINITY, lt = 0.f, at = 0.f;
+#pragma unroll
+        for (int c = 0; c < kOneRoundSplits; ++c)
+          if (c < merger) combineSplit(Mt, lt, at, s.pm[c][hl], s.pl[c][hl], o[c]);
+        combineSplit(Mt, lt, at, M, l, acc);
+        Mem::storeU16(attnOut(a, b, kvh * group + hl, d), floatToBf16(at / lt));
+      }
+      return true;
+    }
     for (int idx = freshThreadIdx(); idx < group * kDecD; idx += kDecThreads) {
       const int hl = idx / kDecD, d = idx % kDecD;
       float M = -INFINITY;
@@ -515,7 +576,7 @@ __device__ __forceinline__ bool decodeAttentionUnit(const DecodeAttnArgs& a, int
         // the merger (last active split): splits 0.. in order as their words arrive, then its
         // own partial
         float Mt = -INFINITY, lt = 0.f, at = 0.f;
-        constexpr int kChunk = 4;
+        constexpr int kChunk = kMergeChunk;
         for (int s0 = 0; s0 < merger; s0 += kChunk) {
           const uint64_t* ptr[3 * kChunk];
           const int live = merger - s0 < kChunk ? merger - s0 : kChunk;

@@ -439,7 +439,7 @@ __device__ void decoderStack(const Args& a) {
                               AX::steps(a.Hq * a.D),
                               reinterpret_cast<const uint64_t*>(q)};
       for (int u = bid; u < attn_units; u += G) {
-        const bool merged = decodeAttentionUnit<Mem, true>(
+        const bool merged = decodeAttentionUnit<Mem, true, MB == 1>(
             da, u % splits, u / splits, gen * splits, false, smem.p.u.attn, smem.kv,
             early && l > 0 ? StackLds<MB>::kEarly : 0,
             [] {},  // q is polled as tagged words
