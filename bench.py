@@ -705,7 +705,8 @@ def main():
         cpu = cpu_engine_decode_baseline(cfg, weights, B, ctx, ids, args.cpu_baseline_steps,
                                          args.cpu_baseline_warmup)
 
-    graph_desc = {"stack": "decoder_stack (one persistent launch for all layers)",
+    graph_desc = {"stack": "decoder_stack (one persistent launch for the embedding gather and "
+                           "all layers) + lm_head_argmax + argmax_finalize",
                   "fused": "fused (five launches per layer)",
                   "large": "large-hidden graph (per layer: q|k|v + RoPE + KV append, "
                            "head_dim-128 MFMA decode attention, o_proj and down_proj each with "
