@@ -151,7 +151,12 @@ __device__ __forceinline__ void attendBlock(SoftmaxState& st8, const KvBlockRegs
       }
   mx = rowsMax(mx);
   const float m_new = fmaxf(st8.m, mx);
-  const float alpha = exp2f(st8.m - m_new);
+  // The raw v_exp_f32 (2^x without subnormal results): the library exp2f adds five instructions
+  // per call to produce subnormal results, 80 of the block's VALU instructions, and this loop is
+  // VALU-bound (8 waves, 2 per SIMD). A subnormal p only ever meets a sum l >= 1 (the running
+  // maximum contributes 2^0) and P*V terms far below O's last bit, and every path that attends
+  // blocks uses this code, so they stay bit-identical to each other.
+  const float alpha = __builtin_amdgcn_exp2f(st8.m - m_new);
   float p[2][2][4];
   float sum = 0.f;
 #pragma unroll
@@ -160,7 +165,7 @@ __device__ __forceinline__ void attendBlock(SoftmaxState& st8, const KvBlockRegs
     for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        p[st][hf][e] = exp2f(sc[st][hf][e] - m_new);
+        p[st][hf][e] = __builtin_amdgcn_exp2f(sc[st][hf][e] - m_new);
         sum += p[st][hf][e];
       }
   st8.l = st8.l * alpha + sum;
