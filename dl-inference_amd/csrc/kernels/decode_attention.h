@@ -202,8 +202,8 @@ __device__ __forceinline__ void combineSplit(float& M, float& l, float& acc, flo
                                              float oc) {
   FP_EXACT;
   const float m_new = fmaxf(M, mc);
-  const float al = M == -INFINITY ? 0.f : exp2f(M - m_new);
-  const float e = mc == -INFINITY ? 0.f : exp2f(mc - m_new);
+  const float al = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(M - m_new);
+  const float e = mc == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mc - m_new);
   l = l * al + lc * e;
   acc = acc * al + oc * e;
   M = m_new;
@@ -529,7 +529,7 @@ __device__ __forceinline__ bool decodeAttentionUnit(const DecodeAttnArgs& a, int
         for (int w = 0; w < kDecWaves; ++w) M = fmaxf(M, s.sm[w][hl]);
 #pragma unroll
         for (int w = 0; w < kDecWaves; ++w) {
-          const float e = s.sm[w][hl] == -INFINITY ? 0.f : exp2f(s.sm[w][hl] - M);
+          const float e = s.sm[w][hl] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(s.sm[w][hl] - M);
           l += e * s.sl[w][hl];
           acc += e * s.so[w][d][hl];
         }
@@ -559,7 +559,7 @@ __device__ __forceinline__ bool decodeAttentionUnit(const DecodeAttnArgs& a, int
       float l = 0.f, acc = 0.f;
 #pragma unroll
       for (int w = 0; w < kDecWaves; ++w) {
-        const float e = s.sm[w][hl] == -INFINITY ? 0.f : exp2f(s.sm[w][hl] - M);
+        const float e = s.sm[w][hl] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(s.sm[w][hl] - M);
         l += e * s.sl[w][hl];
         acc += e * s.so[w][d][hl];
       }
