@@ -114,3 +114,23 @@ def test_decoder_raises_on_a_reported_launch_failure():
     bad.check_status()  # the word was cleared when it was reported
     with pytest.raises(RuntimeError, match="gave up waiting"):
         bad.generate(torch.zeros(2, 1, dtype=torch.int64), 2)
+
+
+def test_stack_graph_folds_the_embedding_into_the_decoder_stack_node():
+    """The stack graph has no embedding node: its decoder_stack node reads the token ids and,
+    after the layer weights, the embedding table (the launch gathers the rows itself). The
+    fused graph keeps the embedding node."""
+    from dli_qwen2 import tiny_config
+    from dli_qwen2.graph import build_decode_graph
+
+    cfg = tiny_config(layers=2)
+    stack = json.loads(build_decode_graph(cfg, 4, fused=True, stack=True,
+                                          stack_trace=True).to_json())
+    ops = [n["op"] for n in stack["nodes"]]
+    assert ops == ["decoder_stack", "lm_head_argmax"]
+    node = stack["nodes"][0]
+    assert node["inputs"][:4] == ["input_ids", "positions", "rotary_cos", "rotary_sin"]
+    assert node["inputs"][-2:] == ["model.embed_tokens.weight", "stack_trace"]
+    assert len(node["inputs"]) == 4 + 7 * cfg.layers + 2
+    fused = json.loads(build_decode_graph(cfg, 4, fused=True).to_json())
+    assert fused["nodes"][0]["op"] == "embedding"
