@@ -164,9 +164,9 @@ __device__ void gate_up_silu_impl(const uint16_t* x, const uint16_t* norm_w, flo
                                   const uint16_t* w_gu, uint16_t* out, int M, int64_t F, int K) {
   using Core = SkinnyCore<2, MB, kNormWaves, kNormUnroll>;
   __shared__ float lds[Core::kLdsFloats + kNormLdsFloats<MB, kNormWaves>];
-  tileLoop<2, MB, kNormWaves, kNormUnroll>(
+  tileLoop<2, MB, kNormWaves, kNormUnroll, PlainMem, false, (MB >= 2)>(
       w_gu, XGlobal{x, K}, 2 * F, K, M, lds, norm_w, eps, blockIdx.x, gridDim.x, INT64_MAX, NoWait{},
-      [&](int64_t t) { gateUpEpilogue<MB, PlainMem>(lds, out, M, F, t); });
+      [&](int64_t t) { gateUpEpilogue<MB, PlainMem, (MB >= 2)>(lds, out, M, F, t); });
 }
 
 constexpr int kLmTileN = 32;  // vocab rows per lm_head tile (NF = 2)

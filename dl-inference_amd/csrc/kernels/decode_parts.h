@@ -151,7 +151,8 @@ __device__ __forceinline__ void normalizeFragments(
 // is loaded (and normalized), 1 when the first tile is reduced. xs: XGlobal (row-major) or XFrag
 // (fragment order).
 template <int NF, int MB, int kW, int kU, class Mem = PlainMem, bool kGated = false,
-          class Gate = NoWait, typename Epi, class Mark = NoMark, class XS = XGlobal>
+          bool kLazySum = false, class Gate = NoWait, typename Epi, class Mark = NoMark,
+          class XS = XGlobal>
 __device__ __forceinline__ void tileLoop(const uint16_t* w, const XS& xs, int64_t N, int K,
                                          int M, float* lds, const uint16_t* norm_w, float eps,
                                          int64_t t_first, int64_t t_stride, int64_t t_end,
@@ -190,7 +191,10 @@ __device__ __forceinline__ void tileLoop(const uint16_t* w, const XS& xs, int64_
     f32x4 acc[NF][MB];
     Core::zero(acc);
     Core::compute(acc, wb, xb, wave, steps);
-    Core::reduce(acc, lds, r, g, wave);
+    if constexpr (kLazySum)
+      Core::storePartials(acc, lds, r, g, wave);  // epi adds the wave slices (partialSum)
+    else
+      Core::reduce(acc, lds, r, g, wave);
     if (tt == t_first) mark(1);
     epi(tt);
     __syncthreads();  // lds is reused by the next tile
@@ -357,20 +361,24 @@ struct QkvEpilogue {
 // ---- gate_up: SwiGLU of one 16-output block ----------------------------------------------
 
 // Tile t of the interleaved gate/up weight = gate rows [16t, 16t+16) then up rows [16t, 16t+16);
-// lds holds the reduced [32][16 MB] tile. out[m, f] = bf16(bf16(silu(bf16 gate)) * bf16 up).
+// lds holds the reduced [32][16 MB] tile, or with kLazySum the waves' partial tiles, which are
+// added here (SkinnyCore::partialSum: the sum reduce() forms, in its order).
+// out[m, f] = bf16(bf16(silu(bf16 gate)) * bf16 up).
 // frag_steps > 0: out is in fragment order (fragOffset) with F / 64 steps.
-template <int MB, class Mem>
+template <int MB, class Mem, bool kLazySum = false>
 __device__ __forceinline__ void gateUpEpilogue(const float* lds, uint16_t* out, int M, int64_t F,
                                                int64_t t, int frag_steps = 0) {
   FP_EXACT;
+  using Core = SkinnyCore<2, MB, kNormWaves, kNormUnroll>;
   constexpr int kTileM = 16 * MB;
   const int64_t f0 = t * 16;
+  auto at = [&](int n, int m) { return kLazySum ? Core::partialSum(lds, n, m) : lds[n * kTileM + m]; };
   for (int idx = freshThreadIdx(); idx < 16 * kTileM; idx += kNormThreads) {
     const int j = idx % 16, m = idx / 16;
     const int64_t f = f0 + j;
     if (m >= M || f >= F) continue;
-    const float g = roundBf16(lds[j * kTileM + m]);
-    const float u = roundBf16(lds[(16 + j) * kTileM + m]);
+    const float g = roundBf16(at(j, m));
+    const float u = roundBf16(at(16 + j, m));
     const float s = roundBf16(g / (1.0f + expf(-g)));
     Mem::storeU16(out + actOffset(m, f, F, frag_steps), floatToBf16(s * u));
   }

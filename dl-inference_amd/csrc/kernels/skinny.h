@@ -120,8 +120,10 @@ struct SkinnyCore {
   static constexpr int kCW = kWaves - kIdle;  // waves that take steps
   static constexpr int kTileN = 16 * NF;
   static constexpr int kTileM = 16 * MB;
-  // LDS floats needed by reduce(): one partial tile per wave.
-  static constexpr int kLdsFloats = kWaves * kTileN * kTileM;
+  // LDS floats needed by reduce() or storePartials(): one partial tile per wave (rows padded to
+  // kTileM + 1 floats by storePartials).
+  static constexpr int kPadM = kTileM + 1;
+  static constexpr int kLdsFloats = kWaves * kTileN * kPadM;
 
   struct WBatch {
     U128 a[kUnroll][NF][2];
@@ -322,6 +324,30 @@ struct SkinnyCore {
   }
 
   // Partial tiles -> LDS [wave][n][m], then a fixed-order sum over waves into lds[0..tile).
+  // reduce() without its sum: each wave's partial tile stays in its slice of lds (wave w at
+  // lds + w * kTileN * kPadM, row n at n * kPadM: rows padded so that an epilogue walking n
+  // across lanes spreads over the LDS banks), for an epilogue that reads every element once and
+  // adds the slices itself (partialSum, in reduce()'s order), which saves reduce()'s second
+  // pass over LDS and its second barrier.
+  __device__ __forceinline__ static void storePartials(f32x4 (&acc)[NF][MB], float* lds, int r,
+                                                       int g, int wave) {
+    float* mine = lds + wave * kTileN * kPadM;
+#pragma unroll
+    for (int f = 0; f < NF; ++f)
+#pragma unroll
+      for (int b = 0; b < MB; ++b)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) mine[(f * 16 + g * 4 + i) * kPadM + b * 16 + r] = acc[f][b][i];
+    __syncthreads();
+  }
+  // element (n, m) of the tile: row n (weight row), column m (batch row)
+  __device__ __forceinline__ static float partialSum(const float* lds, int n, int m) {
+    float sum = lds[n * kPadM + m];
+#pragma unroll
+    for (int v = 1; v < kWaves; ++v) sum += lds[(v * kTileN + n) * kPadM + m];
+    return sum;
+  }
+
   __device__ __forceinline__ static void reduce(f32x4 (&acc)[NF][MB], float* lds, int r, int g,
                                                 int wave) {
     float* mine = lds + wave * kTileN * kTileM;

@@ -504,7 +504,7 @@ __device__ void decoderStack(const Args& a) {
     if (gu_end > gu_tiles) gu_end = gu_tiles;
     if (gu_first < gu_end) {
       const int H = fresh(a.H), M = fresh(a.M), F = fresh(a.F);
-      tileLoop<2, MB, kNormWaves, kNormUnroll, Mem, true>(
+      tileLoop<2, MB, kNormWaves, kNormUnroll, Mem, true, (MB >= 2)>(
           L.w_gate_up, AX::make(h_mid, H), 2 * static_cast<int64_t>(F), H, M, lds,
           L.post_norm,
           a.eps, gu_first, gu_stride, gu_end,
@@ -513,7 +513,7 @@ __device__ void decoderStack(const Args& a) {
                         abort_word, traceSlot(a, l, dli_stack::kTrGuPoll, smem.trace));
             stamp(a, l, dli_stack::kTrGuWait, smem.trace);
           },
-          [&](int64_t t) { gateUpEpilogue<MB, Mem>(lds, act, M, F, t, AX::steps(F)); },
+          [&](int64_t t) { gateUpEpilogue<MB, Mem, (MB >= 2)>(lds, act, M, F, t, AX::steps(F)); },
           [&](int p) {
             if (p == 2)
               stampLoaded(a, l, dli_stack::kTrGuX, smem.trace);
